@@ -1,0 +1,236 @@
+"""The stock PyTorch statements of the pair-stack hot path, restated on the CPU -- TEST INFRASTRUCTURE ONLY.
+
+Every function evaluates in ``dtype`` (float64 by default; float32 for the fp32 yardstick the BASELINE tolerances are stated
+against) on CPU tensors and returns a tensor of that dtype.  They are the checker of the HIP path and the timed CPU baseline of
+``bench.py``; nothing in the product imports them.
+
+Reference statements followed (paths under the reference tree):
+    layer_norm            torch.nn.LayerNorm as used by every module below (biased variance, eps inside the sqrt)
+    triangle_attention_op common/opt_core/opt_core/kernels/triattn/__init__.py:3-8 (op contract), :1202-1220 (``reference``:
+                          -inf at masked keys, a fully-masked row is uniform over all keys)
+    tri_attn              boltz2/stock/src/boltz/model/layers/triangular_attention/attention.py:108-179 and
+                          primitives.py:126-156 (LayerNorm), :159-196 (softmax, _attention), :265-366 (Attention: q/sqrt(c),
+                          sigmoid gate, linear_o); the 1e9*(mask-1) additive mask of attention.py:149
+    trimul                boltz2/stock/src/boltz/model/layers/triangular_mult.py:73-124 (outgoing), :161-212 (incoming);
+                          ten-tensor vocabulary of common/opt_core/opt_core/kernels/trimul/__init__.py:3-11, :1946-1979
+    transition            boltz2/stock/src/boltz/model/layers/transition.py:47-78;
+                          common/opt_core/opt_core/kernels/transition/__init__.py:5-10, :1022-1032 (mask, residual)
+    pair_block            boltz2/stock/src/boltz/model/layers/pairformer.py:75-102 (order and residual adds; dropout = 1 in eval)
+    triatt_prologue /     common/opt_core/opt_core/attn/pair_fused.py:1136-1233 (q,k,v [B,I,H,J,D], g [B,I,J,HD] pre-sigmoid,
+    triatt_epilogue       bias [B,1,H,I,J] in the attention frame) and :1416-1498 (u = (sigmoid(g) o) W_o^T, residual into z,
+                          transposed scatter for the ending node)
+"""
+import math
+
+import torch
+
+__all__ = ["layer_norm", "triangle_attention_op", "tri_attn", "triatt_prologue", "triatt_epilogue", "trimul", "transition",
+           "pair_block", "make_block_params", "block_flops"]
+
+
+def layer_norm(x, w=None, b=None, eps=1e-5):
+    """(x - mean) / sqrt(var + eps) * w + b over the last axis, biased variance, evaluated in x's dtype.
+    Pinned by: torch.nn.functional.layer_norm (library routine), constant rows -> b (tests/test_oracle.py)."""
+    mu = x.mean(dim=-1, keepdim=True)
+    xc = x - mu
+    var = (xc * xc).mean(dim=-1, keepdim=True)
+    y = xc / torch.sqrt(var + eps)
+    if w is not None:
+        y = y * w.to(x.dtype)
+    if b is not None:
+        y = y + b.to(x.dtype)
+    return y
+
+
+def triangle_attention_op(q, k, v, bias, mask=None, scale=None, dtype=torch.float64, rows_per_step=32):
+    """out[b,n,h,i,:] = softmax_j(scale q.k + bias[b,0,h,i,j], -inf where mask[b,n,0,0,j] is False) @ v[b,n,h,j,:].
+    q/k/v [B,N,H,S,D], bias [B,1,H,S,S], mask [B,N,1,1,S] bool (or None).  A fully-masked row is the uniform mean of v over all
+    keys (triattn/__init__.py:1202-1220).
+    Pinned by: the reference's fp64 rows (tests/golden/triattn_*), S = 1 -> v, key-permutation equivariance, bias row-shift
+    invariance, brute force (tests/test_oracle.py)."""
+    B, N, H, S, D = q.shape
+    sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
+    out = torch.empty(B, N, H, S, D, dtype=dtype)
+    bias_ = bias.to(dtype)
+    for n0 in range(0, N, rows_per_step):
+        n1 = min(N, n0 + rows_per_step)
+        s = torch.matmul(q[:, n0:n1].to(dtype), k[:, n0:n1].to(dtype).transpose(-1, -2)) * sc + bias_
+        if mask is not None:
+            keep = mask[:, n0:n1].reshape(B, n1 - n0, 1, 1, S).to(torch.bool)
+            dead = ~keep.any(dim=-1, keepdim=True)
+            s = torch.where(keep | dead, s, torch.full_like(s, float("-inf")))
+            s = torch.where(dead.expand_as(s), torch.zeros_like(s), s)
+        out[:, n0:n1] = torch.matmul(torch.softmax(s, dim=-1), v[:, n0:n1].to(dtype))
+    return out
+
+
+def _as4(z):
+    return (z, False) if z.dim() == 4 else (z.unsqueeze(0), True)
+
+
+def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_step=64, inf=1e9):
+    """Stock TriangleAttention{Starting,Ending}Node forward -> the update in z's frame ([B,N,N,C] or [N,N,C]).
+    P: dict ln_w, ln_b [C], w_q, w_k, w_v, w_g [H*D, C], w_b [H, C], w_o [C, H*D], plus ints H, D.
+    The ending node transposes z (and the mask) in and the update out (attention.py:140-142, :175-176).
+    Pinned by: ending(z) == starting(z^T)^T, the op form (triangle_attention_op) on the same projections, and the BASELINE
+    config-1 block (tests/test_oracle.py)."""
+    z4, sq = _as4(z)
+    B, N, _, C = z4.shape
+    H, D = int(P["H"]), int(P["D"])
+    x = z4.to(dtype)
+    m = torch.ones(B, N, N, dtype=dtype) if mask is None else (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(dtype)
+    if ending:
+        x = x.transpose(1, 2)
+        m = m.transpose(1, 2)
+    x = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
+    wq, wk, wv, wg = (P[n].to(dtype) for n in ("w_q", "w_k", "w_v", "w_g"))
+    wb, wo = P["w_b"].to(dtype), P["w_o"].to(dtype)
+    tri_bias = torch.matmul(x, wb.t()).permute(0, 3, 1, 2).unsqueeze(1)          # [B, 1, H, I, J]
+    out = torch.empty(B, N, N, wo.shape[0], dtype=dtype)
+    for i0 in range(0, N, rows_per_step):
+        i1 = min(N, i0 + rows_per_step)
+        xi = x[:, i0:i1]                                                            # [B, r, J, C]
+        mask_bias = (inf * (m[:, i0:i1] - 1.0))[:, :, None, None, :]                # [B, r, 1, 1, J]
+        q = torch.matmul(xi, wq.t()).view(B, i1 - i0, N, H, D).transpose(-2, -3) / math.sqrt(D)
+        kk = torch.matmul(xi, wk.t()).view(B, i1 - i0, N, H, D).transpose(-2, -3)
+        vv = torch.matmul(xi, wv.t()).view(B, i1 - i0, N, H, D).transpose(-2, -3)
+        a = torch.matmul(q, kk.transpose(-1, -2)) + mask_bias + tri_bias            # [B, r, H, J, J]
+        a = torch.softmax(a, dim=-1)
+        o = torch.matmul(a, vv).transpose(-2, -3)                                   # [B, r, J, H, D]
+        g = torch.sigmoid(torch.matmul(xi, wg.t())).view(B, i1 - i0, N, H, D)
+        out[:, i0:i1] = torch.matmul((o * g).reshape(B, i1 - i0, N, H * D), wo.t())
+    if ending:
+        out = out.transpose(1, 2)
+    return out[0] if sq else out
+
+
+def triatt_prologue(z, P, *, ending=False, dtype=torch.float64):
+    """The block prologue's tensors in the attention frame x = z (or z^T): q, k, v [B,I,H,J,D], g [B,I,J,H*D] (pre-sigmoid),
+    bias [B,1,H,I,J] -- unrounded (pair_fused.py:1136-1233 states the same tensors with bf16 rounding points).
+    Pinned by: tri_attn == epilogue(op(prologue)) (tests/test_oracle.py)."""
+    z4, _ = _as4(z)
+    B, N, _, C = z4.shape
+    H, D = int(P["H"]), int(P["D"])
+    x = z4.to(dtype)
+    if ending:
+        x = x.transpose(1, 2)
+    x = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
+
+    def heads(w):
+        return torch.matmul(x, w.to(dtype).t()).view(B, N, N, H, D).permute(0, 1, 3, 2, 4)
+    q, k, v = heads(P["w_q"]), heads(P["w_k"]), heads(P["w_v"])
+    g = torch.matmul(x, P["w_g"].to(dtype).t())
+    bias = torch.matmul(x, P["w_b"].to(dtype).t()).permute(0, 3, 1, 2).unsqueeze(1)
+    return q, k, v, g, bias
+
+
+def triatt_epilogue(o, g, P, *, dtype=torch.float64):
+    """u [B,I,J,C_out] = (sigmoid(g) * o) @ w_o^T in the attention frame; o [B,I,H,J,D], g [B,I,J,H*D]."""
+    B, I, H, J, D = o.shape
+    ot = o.to(dtype).permute(0, 1, 3, 2, 4).reshape(B, I, J, H * D)
+    return torch.matmul(torch.sigmoid(g.to(dtype)) * ot, P["w_o"].to(dtype).t())
+
+
+def trimul(z, mask=None, *, direction, weights, residual=False, dtype=torch.float64, eps=1e-5):
+    """Stock TriangleMultiplication{Outgoing,Incoming} in the ten-tensor vocabulary:
+        x = LN_in(z); a = mask * sigmoid(x W_ag^T) * (x W_ap^T); b likewise;
+        X[i,j] = sum_k a[i,k] b[j,k] (outgoing) | sum_k a[k,i] b[k,j] (incoming);
+        update = sigmoid(x W_og^T) * (LN_out(X) W_o^T); z + update when residual.
+    z [B,N,N,c_z] or [N,N,c_z]; mask [B,N,N] / [N,N] 0/1 or None.
+    Pinned by: the reference's closed-form vectors (input SHA-256 + H100 witness outputs within their recorded fp64 error),
+    incoming(z) == outgoing(z^T)^T, all-zero mask -> update = sigmoid(x W_og^T) (ln_out_b W_o^T) (tests/test_oracle.py)."""
+    z4, sq = _as4(z)
+    w = {k_: v_.to(dtype) for k_, v_ in weights.items() if hasattr(v_, "to")}
+    x = layer_norm(z4.to(dtype), w["ln_in_w"], w["ln_in_b"], eps)
+    m = None
+    if mask is not None:
+        m = (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(dtype).unsqueeze(-1)
+    a = torch.sigmoid(torch.matmul(x, w["w_ag"].t())) * torch.matmul(x, w["w_ap"].t())
+    b = torch.sigmoid(torch.matmul(x, w["w_bg"].t())) * torch.matmul(x, w["w_bp"].t())
+    if m is not None:
+        a = a * m
+        b = b * m
+    if direction in ("outgoing", "out"):
+        X = torch.einsum("bikd,bjkd->bijd", a, b)
+    elif direction in ("incoming", "in"):
+        X = torch.einsum("bkid,bkjd->bijd", a, b)
+    else:
+        raise ValueError(direction)
+    upd = torch.sigmoid(torch.matmul(x, w["w_og"].t())) * torch.matmul(layer_norm(X, w["ln_out_w"], w["ln_out_b"], eps), w["w_o"].t())
+    out = z4.to(dtype) + upd if residual else upd
+    return out[0] if sq else out
+
+
+def transition(x, w_a, w_b, w_o, ln_w=None, ln_b=None, *, eps=1e-5, mask=None, residual=False, dtype=torch.float64):
+    """y = W_o(silu(W_a n) * (W_b n)), n = LayerNorm(x); optional row mask (y * mask) and residual (x + y).
+    Pinned by: the reference's H100 stock bytes at c = 256 (tests/golden/transition_*), W_o = 0 -> identity residual, row
+    independence (tests/test_oracle.py)."""
+    xx = x.to(dtype)
+    n = layer_norm(xx, ln_w, ln_b, eps)
+    a = torch.matmul(n, w_a.to(dtype).t())
+    h = a * torch.sigmoid(a) * torch.matmul(n, w_b.to(dtype).t())
+    y = torch.matmul(h, w_o.to(dtype).t())
+    if mask is not None:
+        y = y * mask.reshape(y.shape[:-1]).to(dtype)[..., None]
+    return xx + y if residual else y
+
+
+def pair_block(z, mask, params, *, dtype=torch.float64):
+    """One Pairformer layer's pair stack (pairformer.py:75-102, eval): z += trimul_out; z += trimul_in; z += tri_att_start;
+    z += tri_att_end; z += transition_z.  ``params`` from :func:`make_block_params`."""
+    z = z.to(dtype)
+    z = z + trimul(z, mask, direction="outgoing", weights=params["tmo"], dtype=dtype)
+    z = z + trimul(z, mask, direction="incoming", weights=params["tmi"], dtype=dtype)
+    z = z + tri_attn(z, params["tas"], mask, ending=False, dtype=dtype)
+    z = z + tri_attn(z, params["tae"], mask, ending=True, dtype=dtype)
+    t = params["tr"]
+    z = z + transition(z, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"], dtype=dtype)
+    return z
+
+
+def make_block_params(c_z=128, heads=4, head_dim=32, factor=4, seed=0):
+    """BASELINE config-1 weights: N(0, 1/fan_in) from torch.Generator('cpu').manual_seed(seed), drawn in module order
+    (trimul out, trimul in, tri-att start, tri-att end, transition) and parameter order within a module; LayerNorm weight 1,
+    bias 0.  fp32 CPU tensors.  The boltz p_in / g_in halves map onto the ten-tensor vocabulary as
+    boltz2/opt/boltz2_opt/trimul.py:64-68 does (first half -> a, second half -> b)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    C, H, D = c_z, heads, head_dim
+    HD = H * D
+
+    def lin(o, i):
+        return torch.randn(o, i, generator=g, dtype=torch.float32) / math.sqrt(i)
+
+    def tm():
+        p_in, g_in = lin(2 * C, C), lin(2 * C, C)
+        p_out, g_out = lin(C, C), lin(C, C)
+        return {"ln_in_w": torch.ones(C), "ln_in_b": torch.zeros(C), "w_ap": p_in[:C].contiguous(), "w_bp": p_in[C:].contiguous(),
+                "w_ag": g_in[:C].contiguous(), "w_bg": g_in[C:].contiguous(), "ln_out_w": torch.ones(C), "ln_out_b": torch.zeros(C),
+                "w_o": p_out, "w_og": g_out}
+
+    def ta():
+        w_b = lin(H, C)                                             # TriangleAttention.linear (c_in -> heads), then mha q, k, v, o, g
+        w_q, w_k, w_v = lin(HD, C), lin(HD, C), lin(HD, C)
+        w_o = lin(C, HD)
+        w_g = lin(HD, C)
+        return {"ln_w": torch.ones(C), "ln_b": torch.zeros(C), "w_q": w_q, "w_k": w_k, "w_v": w_v, "w_g": w_g, "w_b": w_b,
+                "w_o": w_o, "H": H, "D": D}
+
+    params = {"tmo": tm(), "tmi": tm(), "tas": ta(), "tae": ta()}
+    hid = factor * C
+    params["tr"] = {"ln_w": torch.ones(C), "ln_b": torch.zeros(C), "w_a": lin(hid, C), "w_b": lin(hid, C), "w_o": lin(C, hid)}
+    return params
+
+
+def block_flops(n, c_z=128, c_h=128, heads=4, head_dim=32, factor=4):
+    """Algorithmic FLOPs (2 per multiply-add) of one pair block, per op:
+    trimul (one direction) 2N^2(4 c_z c_h + c_z^2 + c_h c_z) + 2N^3 c_h; tri-att (one node) 2N^2 c_z(4HD + H) + 4N^3 HD
+    + 2N^2 HD c_z; transition 2N^2 (3 factor c_z^2)."""
+    N = n
+    HD = heads * head_dim
+    tm = 2 * N * N * (4 * c_z * c_h + c_z * c_z + c_h * c_z) + 2 * N ** 3 * c_h
+    ta_pro = 2 * N * N * c_z * (4 * HD + heads)
+    ta_core = 4 * N ** 3 * HD
+    ta_epi = 2 * N * N * HD * c_z
+    tr = 2 * N * N * 3 * factor * c_z * c_z
+    return {"trimul": tm, "triatt": ta_pro + ta_core + ta_epi, "triatt_core": ta_core, "triatt_prologue": ta_pro,
+            "triatt_epilogue": ta_epi, "transition": tr, "block": 2 * tm + 2 * (ta_pro + ta_core + ta_epi) + tr}
