@@ -1,0 +1,183 @@
+/* fpf_hip.h -- the C ABI of libfpf_hip.so: the FlashPairformer pair-stack hot path (triangle attention, triangle
+ * multiplication, LayerNorm + SwiGLU transition, standalone LayerNorm) as hand-written gfx950 (MI355X) HIP kernels.
+ *
+ * Every entry point takes one POD argument block whose first field is abi_version (= FPF_ABI_VERSION), a HIP stream
+ * (hipStream_t passed as void*, NULL = the null stream) and an error buffer.  Rules shared by all entry points:
+ *   - return FPF_OK (0) once the kernels are enqueued; any other value means NOTHING was launched and err holds one line
+ *     (the caller's face maps it to a refusal by name);
+ *   - every pointer is a caller-owned device pointer (workspaces included); the library allocates and frees nothing and
+ *     never synchronises the host, so calls are capture-safe and reentrant across host threads and streams;
+ *   - shapes are 64-bit; strides are in ELEMENTS;
+ *   - dtype codes: FPF_DT_BF16 = bf16 storage with fp32 accumulation and softmax (the "fast" tier), FPF_DT_F32 = fp32
+ *     storage and fp32 arithmetic throughout (the "exact" tier).
+ *
+ * The reference interface each entry point replaces is cited on its declaration (paths under the reference tree).
+ */
+#ifndef FPF_HIP_H
+#define FPF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FPF_ABI_VERSION 1
+
+enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
+enum {
+  FPF_OK = 0,
+  FPF_E_VERSION = 1,   /* abi_version mismatch */
+  FPF_E_ARGS = 2,      /* NULL pointer / bad flag */
+  FPF_E_SHAPE = 3,     /* a shape this entry point does not serve (e.g. head_dim != 32 on the bf16 core) */
+  FPF_E_DTYPE = 4,     /* a dtype code this entry point does not serve */
+  FPF_E_ALIGN = 5,     /* a pointer or stride that breaks the 16-byte vector access the kernels use */
+  FPF_E_WORKSPACE = 6, /* workspace missing or smaller than the *_workspace_bytes query */
+  FPF_E_LAUNCH = 7     /* hipLaunchKernel reported an error (the message carries hipGetErrorString) */
+};
+
+/* Library identity.  No counterpart in the reference (its sealed packages carry the same facts in manifests). */
+int fpf_abi_version(void);
+const char* fpf_describe(void);
+
+/* ---------------------------------------------------------------------------------------------------------------- LayerNorm
+ * y[r, :] = (x[r, :] - mean) * rsqrt(var + eps) * gamma + beta, biased variance, fp32 statistics.
+ * Replaces: common/opt_core/opt_core/kernels/ln/__init__.py:836 layer_norm (the standalone LN face; forms fp32 / bf16 /
+ * bf16 out of ln/DESIGN.md:5-9 are the dtype_in / dtype_out pairs). */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype_in;        /* FPF_DT_BF16 | FPF_DT_F32 */
+  int32_t dtype_out;       /* FPF_DT_BF16 | FPF_DT_F32 */
+  int32_t cols;            /* normalised width, <= 1024, a multiple of 8 (bf16) / 4 (fp32) */
+  int64_t rows;
+  const void* x;
+  int64_t x_row_stride;    /* elements between rows (>= cols) */
+  void* y;
+  int64_t y_row_stride;
+  const float* gamma;      /* [cols] or NULL (= 1) */
+  const float* beta;       /* [cols] or NULL (= 0) */
+  float eps;
+} FpfLnArgs;
+int fpf_layernorm_fwd(const FpfLnArgs* a, void* stream, char* err, size_t errlen);
+
+/* ---------------------------------------------------------------------------------------------------------------- transition
+ * out = [x +] mask_r * W_o( silu(W_a n) * (W_b n) ),  n = LayerNorm(x) over c; hidden never leaves the chip.
+ * Replaces: common/opt_core/opt_core/kernels/transition/__init__.py:1074 transition (row v2 semantics: mask and residual
+ * folded, out may alias x) and common/opt_core/opt_core/attn/pair_fused.py:1519 transition. */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* FPF_DT_BF16 (x, out, w_* bf16) | FPF_DT_F32 (all fp32) */
+  int32_t c;               /* bf16: 128; fp32: any multiple of 4 <= 256 */
+  int32_t hidden;          /* bf16: multiple of 32; fp32: any */
+  int64_t rows;
+  const void* x;           /* [rows, c] contiguous */
+  void* out;               /* [rows, c] contiguous; may equal x (each row is read before it is written) */
+  const float* ln_w;       /* [c] or NULL */
+  const float* ln_b;       /* [c] or NULL */
+  float eps;
+  const void* w_a;         /* [hidden, c] (silu branch) */
+  const void* w_b;         /* [hidden, c] */
+  const void* w_o;         /* [c, hidden] */
+  const float* row_mask;   /* [rows] or NULL: the update is multiplied by it before the residual add */
+  int32_t residual;        /* 1: out = x + update */
+} FpfTransitionArgs;
+int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char* err, size_t errlen);
+
+/* ---------------------------------------------------------------------------------------------------------------- triangle multiplication
+ * x = LN_in(z); a = mask * sigmoid(x W_ag^T) * (x W_ap^T); b likewise;
+ * X[i,j] = sum_k a[i,k] b[j,k] (outgoing) | sum_k a[k,i] b[k,j] (incoming);
+ * update = sigmoid(x W_og^T) * (LN_out(X) W_o^T); out = [z +] update.
+ * Replaces: common/opt_core/opt_core/kernels/trimul/__init__.py:1982 triangle_multiplication (op :3-11, the ten tensors of
+ * WEIGHT_KEYS :171); the row `native` structure K1 -> batched contraction -> K3 (trimul/native/DESIGN.md:1-40).
+ * Launches: K1 (LN_in + four gated projections + mask -> bf16 channel-major planes; the incoming variant writes them
+ * transposed), the batched contraction over k, K3 (LN_out + W_o + output gate + residual). */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* FPF_DT_BF16 (z, out, w_* bf16) | FPF_DT_F32 */
+  int32_t c_z;             /* bf16: 128 */
+  int32_t c_h;             /* bf16: 128 */
+  int64_t batch;
+  int64_t n;
+  const void* z;           /* [B, N, N, c_z] contiguous */
+  void* out;               /* [B, N, N, c_z]; may equal z */
+  const float* mask;       /* [B, N, N] (0 / 1) or NULL */
+  const float* ln_in_w;    /* [c_z] */
+  const float* ln_in_b;
+  const float* ln_out_w;   /* [c_h] */
+  const float* ln_out_b;
+  const void* w_ag;        /* [c_h, c_z] */
+  const void* w_ap;
+  const void* w_bg;
+  const void* w_bp;
+  const void* w_o;         /* [c_z, c_h] */
+  const void* w_og;        /* [c_z, c_z] */
+  int32_t outgoing;        /* 1 outgoing, 0 incoming */
+  int32_t residual;
+  float eps;
+  void* workspace;
+  size_t workspace_bytes;
+} FpfTrimulArgs;
+size_t fpf_trimul_workspace_bytes(int64_t batch, int64_t n, int32_t c_z, int32_t c_h, int32_t dtype);
+int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, size_t errlen);
+
+/* ---------------------------------------------------------------------------------------------------------------- triangle attention (op)
+ * out[b,n,h,i,:] = softmax_j(scale q.k + bias[b,h,i,j], -inf where mask[b,n,j] == 0) @ v[b,n,h,j,:];
+ * a row whose keys are all masked is the uniform mean of v over all keys.
+ * Replaces: common/opt_core/opt_core/kernels/triattn/__init__.py:1094 triangle_attention (op :3-8); the reference's plain-C
+ * call struct model is kernels/triattn_xla/csrc/triattn_cuda_abi.h:13-40. */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* q / k / v / out: FPF_DT_BF16 (head_dim 32) | FPF_DT_F32 (head_dim <= 64) */
+  int64_t B, N, H, S, D;
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t q_stride[5];     /* [B, N, H, S, D] element strides; stride[4] must be 1 */
+  int64_t k_stride[5];
+  int64_t v_stride[5];
+  const void* bias;        /* [B, H, S, S] (the [B,1,H,S,S] operand without its unit axis) */
+  int32_t bias_dtype;      /* FPF_DT_F32 | FPF_DT_BF16 */
+  int64_t bias_stride[4];  /* stride[3] must be 1 */
+  const void* mask;        /* [B, N, S] or NULL, nonzero = attend */
+  int32_t mask_dtype;      /* FPF_DT_U8 | FPF_DT_F32 */
+  int64_t mask_stride[3];
+  void* out;
+  int64_t out_stride[5];   /* stride[4] must be 1 */
+  float scale;
+} FpfTriattnArgs;
+int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err, size_t errlen);
+
+/* ---------------------------------------------------------------------------------------------------------------- triangle attention (block)
+ * The fused block: prologue (LN -> q|k|v|g and the pair-bias projection, reading z or z^T by address) -> core -> epilogue
+ * (sigmoid(g) * o @ W_o^T, written as an update in z's frame or added to z in place, transposed scatter for the ending node).
+ * Replaces: common/opt_core/opt_core/attn/pair_fused.py:1500 tri_attn_block (prologue :1136, core_attention :1391,
+ * epilogue :1416; weights as pack_triattn_weights :679 packs them: w_qkvg [4HD, C] rows q|k|v|g, w_b [H, C], w_o [C, HD]). */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* FPF_DT_BF16 (C = 128, H*D = 128, D = 32) | FPF_DT_F32 */
+  int64_t B, N;
+  int32_t C, H, D;
+  const void* z;           /* [B, N, N, C] contiguous, z's own frame */
+  const void* mask;        /* [B, N, N] pair mask in z's frame or NULL, nonzero = keep */
+  int32_t mask_dtype;      /* FPF_DT_U8 | FPF_DT_F32 */
+  const float* ln_w;       /* [C] or NULL */
+  const float* ln_b;
+  float eps;
+  const void* w_qkvg;      /* [4*H*D, C] */
+  const void* w_b;         /* [H, C] */
+  const void* w_o;         /* [C, H*D] */
+  int32_t ending;          /* 0 starting node, 1 ending node (attention over z^T) */
+  int32_t residual;        /* 1: z += update in place (z must then be writable: out == z) */
+  void* out;               /* residual: == z; else the update [B, N, N, C] in z's frame */
+  float scale;             /* <= 0: 1/sqrt(D) */
+  void* workspace;
+  size_t workspace_bytes;
+} FpfTriattnBlockArgs;
+size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int32_t C, int32_t H, int32_t D, int32_t dtype);
+int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FPF_HIP_H */

@@ -1,0 +1,41 @@
+"""Shared helpers of the parity tests (error metrics with the BASELINE tolerances)."""
+import torch
+
+BF16_MAX_ABS = 2e-2      # bf16 fast tier vs the fp32 reference
+BF16_REL_L2 = 5e-3
+F32_REL = 1e-5           # fp32 exact tier vs the fp32 reference
+
+
+def rel_l2(out, ref):
+    o, r = out.double().cpu(), ref.double().cpu()
+    return ((o - r).norm() / r.norm().clamp_min(1e-30)).item()
+
+
+def max_abs(out, ref):
+    return (out.double().cpu() - ref.double().cpu()).abs().max().item()
+
+
+def assert_bf16_close(out, ref, what=""):
+    ma, rl = max_abs(out, ref), rel_l2(out, ref)
+    print("[parity] %s max_abs=%.3e rel_l2=%.3e" % (what, ma, rl))
+    assert ma <= BF16_MAX_ABS and rl <= BF16_REL_L2, "%s max_abs=%.3e rel_l2=%.3e" % (what, ma, rl)
+    return ma, rl
+
+
+def assert_f32_close(out, ref, what=""):
+    rl = rel_l2(out, ref)
+    print("[parity] %s rel_l2=%.3e" % (what, rl))
+    assert rl <= F32_REL, "%s rel_l2=%.3e" % (what, rl)
+    return rl
+
+
+def assert_bf16_residual_close(out, ref, what=""):
+    """Residual-form outputs (z + update stored in bf16): the update bars plus the half-ulp of the bf16 output itself, which no
+    kernel can avoid once |z + update| >= 4 (half-ulp 2^-7 there, 2^-6 from 8)."""
+    o, r = out.double().cpu(), ref.double().cpu()
+    ulp = torch.pow(2.0, torch.floor(torch.log2(r.abs().clamp_min(2.0 ** -126))) - 7)
+    excess = ((o - r).abs() - 0.5 * ulp).max().item()
+    rl = rel_l2(o, r)
+    print("[parity] %s max(|err| - ulp/2)=%.3e rel_l2=%.3e" % (what, excess, rl))
+    assert excess <= BF16_MAX_ABS and rl <= BF16_REL_L2, "%s excess=%.3e rel_l2=%.3e" % (what, excess, rl)
+    return excess, rl

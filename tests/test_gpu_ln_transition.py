@@ -1,0 +1,91 @@
+"""GPU parity of the LayerNorm and transition kernels against the CPU oracle (same seeded inputs)."""
+import pytest
+import torch
+
+from _util import assert_bf16_close, assert_bf16_residual_close, assert_f32_close
+from oracle import stock as S
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.mark.parametrize("din,dout", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32), (torch.bfloat16, torch.float32),
+                                      (torch.float32, torch.bfloat16)])
+@pytest.mark.parametrize("rows,cols", [(1000, 128), (37, 256), (5, 384)])
+def test_layer_norm(din, dout, rows, cols):
+    from fpf_hip.kernels import ln
+    g = _g(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * 3 + 0.5).to(din)
+    w = 1 + 0.1 * torch.randn(cols, generator=g)
+    b = 0.1 * torch.randn(cols, generator=g)
+    word = "fast" if din == torch.bfloat16 else "exact"
+    y, sel = ln.layer_norm(x.to(DEV), (cols,), w.to(DEV), b.to(DEV), 1e-5, word=word, out_dtype=dout)
+    torch.cuda.synchronize()
+    ref = S.layer_norm(x.double(), w.double(), b.double(), 1e-5)
+    if dout == torch.float32 and din == torch.float32:
+        assert_f32_close(y, ref, "ln fp32")
+    else:
+        assert_bf16_close(y, ref, "ln")
+    assert sel.row in ("hip_gfx950", "hip_gfx950_f32")
+
+
+def _tr_weights(c, hidden, seed, dtype):
+    g = _g(seed)
+    wa = torch.randn(hidden, c, generator=g) / c ** 0.5
+    wb = torch.randn(hidden, c, generator=g) / c ** 0.5
+    wo = torch.randn(c, hidden, generator=g) / hidden ** 0.5
+    lw = 1 + 0.1 * torch.randn(c, generator=g)
+    lb = 0.1 * torch.randn(c, generator=g)
+    return [t.to(dtype) for t in (wa, wb, wo)] + [lw, lb]
+
+
+@pytest.mark.parametrize("rows", [4096, 1000, 1])
+@pytest.mark.parametrize("residual,masked", [(False, False), (True, True)])
+def test_transition_bf16(rows, residual, masked):
+    from fpf_hip.kernels import transition as T
+    c, hidden = 128, 512
+    wa, wb, wo, lw, lb = _tr_weights(c, hidden, 11, torch.bfloat16)
+    x = torch.randn(rows, c, generator=_g(rows)).to(torch.bfloat16)
+    mask = (torch.rand(rows, generator=_g(3)) > 0.2).float() if masked else None
+    W = T.pack(w_a=wa.to(DEV), w_b=wb.to(DEV), w_o=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV))
+    y, sel = T.transition(x.to(DEV), W, word="fast", residual=residual, mask=None if mask is None else mask.to(DEV))
+    torch.cuda.synchronize()
+    assert sel.row == "hip_gfx950"
+    ref = S.transition(x.float(), wa.float(), wb.float(), wo.float(), lw, lb, residual=residual, mask=mask, dtype=torch.float32)
+    if residual:
+        assert_bf16_residual_close(y, ref, "transition residual")
+    else:
+        assert_bf16_close(y, ref, "transition update")
+    if masked:
+        assert torch.equal(y.cpu()[mask == 0], x[mask == 0]), "masked rows must equal x bit for bit"
+
+
+def test_transition_bf16_in_place_equals_out_of_place():
+    from fpf_hip.kernels import transition as T
+    wa, wb, wo, lw, lb = _tr_weights(128, 512, 12, torch.bfloat16)
+    x = torch.randn(3000, 128, generator=_g(5)).to(torch.bfloat16).to(DEV)
+    W = T.pack(w_a=wa.to(DEV), w_b=wb.to(DEV), w_o=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV))
+    y1, _ = T.transition(x, W, word="fast", residual=True)
+    x2 = x.clone()
+    y2, _ = T.transition(x2, W, word="fast", residual=True, out=x2)
+    torch.cuda.synchronize()
+    assert y2.data_ptr() == x2.data_ptr()
+    assert torch.equal(y1, x2)
+
+
+@pytest.mark.parametrize("rows", [777, 4096])
+def test_transition_fp32_exact(rows):
+    from fpf_hip.kernels import transition as T
+    c, hidden = 128, 512
+    wa, wb, wo, lw, lb = _tr_weights(c, hidden, 13, torch.float32)
+    x = torch.randn(rows, c, generator=_g(rows + 1))
+    W = T.pack(w_a=wa.to(DEV), w_b=wb.to(DEV), w_o=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV))
+    y, sel = T.transition(x.to(DEV), W, word="exact", residual=False)
+    torch.cuda.synchronize()
+    assert sel.row == "hip_gfx950_f32"
+    ref = S.transition(x, wa, wb, wo, lw, lb, dtype=torch.float64)
+    assert_f32_close(y, ref, "transition fp32")

@@ -1,0 +1,119 @@
+"""GPU parity of the triangle-multiplication kernels (K1 -> contraction -> K3) against the CPU oracle."""
+import json
+import os
+
+import pytest
+import torch
+
+from _util import assert_bf16_close, assert_bf16_residual_close, assert_f32_close, max_abs, rel_l2
+from conftest import GOLDEN
+from oracle import stock as S
+from oracle import vectors as V
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _weights(c, seed, dtype, ln_affine=True):
+    g = torch.Generator().manual_seed(seed)
+    w = {k: torch.randn(c, c, generator=g) / c ** 0.5 for k in ("w_ag", "w_ap", "w_bg", "w_bp", "w_o", "w_og")}
+    if ln_affine:
+        w.update(ln_in_w=1 + 0.1 * torch.randn(c, generator=g), ln_in_b=0.1 * torch.randn(c, generator=g),
+                 ln_out_w=1 + 0.1 * torch.randn(c, generator=g), ln_out_b=0.1 * torch.randn(c, generator=g))
+    else:
+        w.update(ln_in_w=torch.ones(c), ln_in_b=torch.zeros(c), ln_out_w=torch.ones(c), ln_out_b=torch.zeros(c))
+    return {k: (v.to(dtype) if k.startswith("w_") else v) for k, v in w.items()}
+
+
+def _dev(w):
+    return {k: v.to(DEV) for k, v in w.items()}
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("B,N,masked", [(1, 64, False), (1, 100, True), (2, 37, True)])
+def test_trimul_bf16(direction, B, N, masked):
+    from fpf_hip.kernels import trimul as TM
+    w = _weights(128, 1, torch.bfloat16)
+    g = torch.Generator().manual_seed(N)
+    z = torch.randn(B, N, N, 128, generator=g).to(torch.bfloat16)
+    mask = None
+    if masked:
+        mask = torch.ones(B, N, N)
+        mask[:, N - 5:, :] = 0
+        mask[:, :, N - 5:] = 0
+    out = TM.triangle_multiplication(z.to(DEV), None if mask is None else mask.to(DEV), direction=direction, weights=_dev(w), word="fast")
+    torch.cuda.synchronize()
+    ref = S.trimul(z.float(), mask, direction=direction, weights={k: v.float() for k, v in w.items()}, dtype=torch.float32)
+    assert_bf16_close(out, ref, "trimul %s B%d N%d" % (direction, B, N))
+
+
+def test_trimul_bf16_residual_in_place_equals_out_of_place():
+    from fpf_hip.kernels import trimul as TM
+    w = _dev(_weights(128, 2, torch.bfloat16))
+    z = torch.randn(1, 96, 96, 128, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    y1 = TM.triangle_multiplication(z, None, direction="incoming", weights=w, word="fast", residual=True)
+    z2 = z.clone()
+    y2 = TM.triangle_multiplication(z2, None, direction="incoming", weights=w, word="fast", residual=True, out=z2)
+    torch.cuda.synchronize()
+    assert y2.data_ptr() == z2.data_ptr() and torch.equal(y1, z2)
+
+
+def test_trimul_bf16_zero_mask_zero_ln_out_bias_gives_exact_zero():
+    from fpf_hip.kernels import trimul as TM
+    w = _weights(128, 4, torch.bfloat16)
+    w["ln_out_b"] = torch.zeros(128)
+    z = torch.randn(50, 50, 128, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    out = TM.triangle_multiplication(z.to(DEV), torch.zeros(50, 50, device=DEV), direction="outgoing", weights=_dev(w), word="fast")
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out) == 0
+
+
+def test_trimul_bf16_masked_rows_update_is_gate_times_bias_projection():
+    """A pixel whose row AND column are masked sees X = 0 for every k, so its update is sigmoid(x W_og) (ln_out_b W_o^T)."""
+    from fpf_hip.kernels import trimul as TM
+    w = _weights(128, 6, torch.bfloat16)
+    w["ln_out_b"] = torch.zeros(128)
+    N = 40
+    z = torch.randn(N, N, 128, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16)
+    mask = torch.ones(N, N)
+    mask[N - 3:, :] = 0
+    mask[:, N - 3:] = 0
+    out = TM.triangle_multiplication(z.to(DEV), mask.to(DEV), direction="outgoing", weights=_dev(w), word="fast").cpu()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out[N - 3:, N - 3:]) == 0          # X = 0 there and beta_out = 0 -> exactly 0
+
+
+TRIMUL = json.load(open(os.path.join(GOLDEN, "trimul_cases.json")))["cases"]
+CF = [c for c in TRIMUL if c["form"] == "bf16" and c["c_z"] == 128 and c["n"] <= 256]
+
+
+@pytest.mark.parametrize("case", CF, ids=[c["id"] for c in CF])
+def test_trimul_closed_form_vectors(case):
+    """The reference's closed-form cases: error vs the fp64 statement within the BASELINE bars, reported beside the H100
+    kernel's recorded error for the same inputs."""
+    from fpf_hip.kernels import trimul as TM
+    z, mask, w = V.trimul_inputs(case)
+    out = TM.triangle_multiplication(z.to(DEV), None if mask is None else mask.to(DEV), direction=case["direction"], weights=_dev(w),
+                                     word="fast", residual=case["residual"])
+    torch.cuda.synchronize()
+    ref = S.trimul(z, mask, direction=case["direction"], weights=w, residual=case["residual"], dtype=torch.float64)
+    (assert_bf16_residual_close if case["residual"] else assert_bf16_close)(out, ref, case["id"])
+    h100 = case["expected"].get("sm90", {}).get("numerics", {})
+    print("[parity] %s ours max_abs=%.3e rel_rms=%.3e | H100 native max_abs=%s rel_rms=%s" % (
+        case["id"], max_abs(out, ref), rel_l2(out, ref), h100.get("max_abs_fp64"), h100.get("rel_rms_fp64")))
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("N,masked", [(48, False), (70, True)])
+def test_trimul_fp32_exact(direction, N, masked):
+    from fpf_hip.kernels import trimul as TM
+    w = _weights(128, 8, torch.float32)
+    z = torch.randn(N, N, 128, generator=torch.Generator().manual_seed(N))
+    mask = None
+    if masked:
+        mask = torch.ones(N, N)
+        mask[N - 4:, :] = 0
+    out = TM.triangle_multiplication(z.to(DEV), None if mask is None else mask.to(DEV), direction=direction, weights=_dev(w), word="exact")
+    torch.cuda.synchronize()
+    ref = S.trimul(z, mask, direction=direction, weights=w, dtype=torch.float64)
+    assert_f32_close(out, ref, "trimul fp32 %s N%d" % (direction, N))

@@ -1,0 +1,501 @@
+// Triangle multiplication (outgoing / incoming), three launches on the caller's stream:
+//   K1        LN_in(z) -> four gated projections -> mask -> channel-major planes A[c][P][Q], B[c][P][Q] (bf16)
+//             outgoing: plane (P, Q) = z pixel (P, Q);  incoming: plane (P, Q) = z pixel (Q, P) (the transposed load: a wave's
+//             32 plane columns are 32 z rows of one column, each a contiguous 256-byte pixel row)
+//   contract  X[c][i][j] = sum_k A[c][i][k] B[c][j][k] -- a batched "NT" bf16 MFMA GEMM, fp32 accumulation, bf16 X
+//   K3        LN_out(X) W_o^T * sigmoid(LN_in(z) W_og^T) [+ z] -> out (LN_in recomputed from z instead of storing the gate)
+// Replaces common/opt_core/opt_core/kernels/trimul/__init__.py:1982 (triangle_multiplication), row `native`'s K1 | bmm | K3
+// structure (kernels/trimul/native/DESIGN.md:1-40).  Planes are padded to Np = ceil(N / 128) * 128 with zeros so the
+// contraction needs no bounds checks.  The fp32 path (exact tier) has the same three launches in fp32 scalar FMA.
+#include "fpf_common.h"
+
+namespace fpf {
+
+constexpr int TM_C = 128;            // c_z = c_h for the bf16 path
+constexpr int TM_WLD = TM_C + 8;     // LDS pitch (bf16) of a 128-wide weight row
+constexpr int TM_TILE = 128;         // contraction tile and plane padding
+
+__device__ __forceinline__ void ln128_from_regs(float (&xv)[64], int g, const float* __restrict__ w, const float* __restrict__ b, float eps,
+                                                bf16x8 (&xb)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) s += xv[i];
+  s += xor32(s);
+  const float mean = s * (1.0f / 128.0f);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const float d = xv[i] - mean;
+    q += d * d;
+  }
+  q += xor32(q);
+  const float rstd = 1.0f / sqrtf(q * (1.0f / 128.0f) + eps);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int c0 = 64 * g + 8 * t;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (xv[8 * t + e] - mean) * rstd * (w ? w[c0 + e] : 1.f) + (b ? b[c0 + e] : 0.f);
+    xb[t] = as_bf8(u32x4{pack2(y[0], y[1]), pack2(y[2], y[3]), pack2(y[4], y[5]), pack2(y[6], y[7])});
+  }
+}
+
+__device__ __forceinline__ void load_row128(const uint16_t* __restrict__ row, bool live, int g, float (&xv)[64]) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const u32x4 r = live ? *reinterpret_cast<const u32x4*>(row + 64 * g + 8 * t) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xv[8 * t + 2 * e] = lo_bf(r[e]);
+      xv[8 * t + 2 * e + 1] = hi_bf(r[e]);
+    }
+  }
+}
+
+// Cooperative copy of 32 rows (r0 ..) of a [128 x 128] bf16 weight into LDS with pitch TM_WLD.
+__device__ __forceinline__ void stage_w32(uint16_t* __restrict__ s, const uint16_t* __restrict__ w, int r0, int tid) {
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int i = tid + 256 * it;
+    const int r = i >> 4, ch = i & 15;
+    *reinterpret_cast<u32x4*>(&s[r * TM_WLD + ch * 8]) = *reinterpret_cast<const u32x4*>(w + (int64_t)(r0 + r) * TM_C + ch * 8);
+  }
+}
+
+__device__ __forceinline__ f32x16 gemm_rows32(const uint16_t* __restrict__ s, int n, int g, const bf16x8 (&xb)[8]) {
+  f32x16 acc = {};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&s[n * TM_WLD + 64 * g + 8 * t])), xb[t], acc);
+  return acc;
+}
+
+// ---------------------------------------------------------------------------------------------------------------- K1 (bf16)
+__global__ void __launch_bounds__(256) trimul_k1_bf16(const uint16_t* __restrict__ z, const float* __restrict__ mask,
+                                                      const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
+                                                      const uint16_t* __restrict__ w_ap, const uint16_t* __restrict__ w_ag,
+                                                      const uint16_t* __restrict__ w_bp, const uint16_t* __restrict__ w_bg,
+                                                      uint16_t* __restrict__ pa, uint16_t* __restrict__ pb, int64_t N, int64_t Np, int outgoing) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[4][32 * TM_WLD];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t tiles_per_row = Np / 32;
+  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;           // wave tile: plane row P, columns Q0 .. Q0 + 31
+  const int64_t b = blockIdx.y;
+  const int64_t P = wt / tiles_per_row, Q = (wt % tiles_per_row) * 32 + n;
+  const bool live = P < N && Q < N;
+  const int64_t zi = outgoing ? P : Q, zj = outgoing ? Q : P;
+  const int64_t pix = (b * N + zi) * N + zj;
+  float xv[64];
+  load_row128(z + pix * TM_C, live, g, xv);
+  bf16x8 xb[8];
+  ln128_from_regs(xv, g, ln_w, ln_b, eps, xb);
+  const float m = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
+  const int64_t plane = Np * Np;
+  uint16_t* oa = pa + b * TM_C * plane + P * Np + Q;
+  uint16_t* ob = pb + b * TM_C * plane + P * Np + Q;
+  for (int cb = 0; cb < 4; ++cb) {
+    __syncthreads();
+    stage_w32(sW[0], w_ap, cb * 32, tid);
+    stage_w32(sW[1], w_ag, cb * 32, tid);
+    stage_w32(sW[2], w_bp, cb * 32, tid);
+    stage_w32(sW[3], w_bg, cb * 32, tid);
+    __syncthreads();
+    if (P >= Np) continue;
+    const f32x16 ap = gemm_rows32(sW[0], n, g, xb), ag = gemm_rows32(sW[1], n, g, xb);
+    const f32x16 bp = gemm_rows32(sW[2], n, g, xb), bg = gemm_rows32(sW[3], n, g, xb);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int c = cb * 32 + c_row(v, g);
+      oa[c * plane] = f2bf(m * sigmoidf_(ag[v]) * ap[v]);
+      ob[c * plane] = f2bf(m * sigmoidf_(bg[v]) * bp[v]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- contraction (bf16)
+constexpr int CT_BK = 64;
+constexpr int CT_LD = CT_BK + 8;     // 144-byte LDS rows: conflict-free 16-byte fragment reads
+
+__global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X,
+                                                            int64_t Np, int64_t N, int64_t nbatch) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[TM_TILE * CT_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[TM_TILE * CT_LD];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  // XCD-aware order: the hardware deals workgroups round-robin over 8 XCDs; give each XCD a contiguous run of (plane, tile)
+  // work so the 36-ish tiles of one plane share that XCD's L2.
+  const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE);
+  const int64_t total = tiles * nbatch;
+  const int64_t L = blockIdx.x;
+  const int64_t per = (total + 7) / 8;
+  const int64_t w = (L % 8) * per + L / 8;
+  if (w >= total) return;
+  const int64_t bc = w / tiles, t = w % tiles;
+  const int64_t ti = t / (Np / TM_TILE), tj = t % (Np / TM_TILE);
+  const int64_t plane = Np * Np;
+  const uint16_t* a0 = A + bc * plane + ti * TM_TILE * Np;
+  const uint16_t* b0 = Bm + bc * plane + tj * TM_TILE * Np;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;     // the wave's 64 x 64 sub-tile
+  f32x16 acc[2][2] = {};
+  // global -> register prefetch: 128 rows x 64 k = 1024 16-byte chunks per operand, 4 per thread
+  u32x4 ra[4], rb[4];
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int i = tid + 256 * it, r = i >> 3, ch = i & 7;
+      ra[it] = *reinterpret_cast<const u32x4*>(a0 + r * Np + k0 + ch * 8);
+      rb[it] = *reinterpret_cast<const u32x4*>(b0 + r * Np + k0 + ch * 8);
+    }
+  };
+  gload(0);
+  for (int64_t k0 = 0; k0 < Np; k0 += CT_BK) {
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int i = tid + 256 * it, r = i >> 3, ch = i & 7;
+      *reinterpret_cast<u32x4*>(&sA[r * CT_LD + ch * 8]) = ra[it];
+      *reinterpret_cast<u32x4*>(&sB[r * CT_LD + ch * 8]) = rb[it];
+    }
+    __syncthreads();
+    if (k0 + CT_BK < Np) gload(k0 + CT_BK);
+#pragma unroll
+    for (int ks = 0; ks < CT_BK / 16; ++ks) {
+      bf16x8 fa[2], fb[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        fa[s] = as_bf8(*reinterpret_cast<const u32x4*>(&sA[(wr + 32 * s + n) * CT_LD + 16 * ks + 8 * g]));
+        fb[s] = as_bf8(*reinterpret_cast<const u32x4*>(&sB[(wc + 32 * s + n) * CT_LD + 16 * ks + 8 * g]));
+      }
+#pragma unroll
+      for (int si = 0; si < 2; ++si)
+#pragma unroll
+        for (int sj = 0; sj < 2; ++sj) acc[si][sj] = mfma32(fa[si], fb[sj], acc[si][sj]);
+    }
+  }
+  // D layout: row i = 8(v/4) + 4g + v%4 of the sub-tile, column j = n
+  uint16_t* x0 = X + bc * plane;
+#pragma unroll
+  for (int si = 0; si < 2; ++si)
+#pragma unroll
+    for (int sj = 0; sj < 2; ++sj) {
+      const int64_t j = tj * TM_TILE + wc + 32 * sj + n;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t i = ti * TM_TILE + wr + 32 * si + c_row(v, g);
+        if (i < N && j < N) x0[i * Np + j] = f2bf(acc[si][sj][v]);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- K3 (bf16)
+constexpr int K3_XLD = 32 + 8;       // LDS pitch of the staged X tile [c][32 pixels]
+
+__global__ void __launch_bounds__(256) trimul_k3_bf16(const uint16_t* zin, uint16_t* out, const uint16_t* __restrict__ X,
+                                                      const float* __restrict__ ln_in_w, const float* __restrict__ ln_in_b,
+                                                      const float* __restrict__ ln_out_w, const float* __restrict__ ln_out_b, float eps,
+                                                      const uint16_t* __restrict__ w_o, const uint16_t* __restrict__ w_og,
+                                                      int64_t N, int64_t Np, int residual) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[2][32 * TM_WLD];
+  __shared__ __attribute__((aligned(16))) uint16_t sX[4][TM_C * K3_XLD];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t tiles_per_row = Np / 32;
+  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t b = blockIdx.y;
+  const int64_t i = wt / tiles_per_row, j0 = (wt % tiles_per_row) * 32, j = j0 + n;
+  const bool live = i < N && j < N;
+  const int64_t pix = (b * N + i) * N + j;
+  const int64_t plane = Np * Np;
+  // stage X[c][i][j0 .. j0+31] (128 rows of 64 bytes) for this wave
+  uint16_t* sx = sX[wave];
+  if (i < N) {
+    const uint16_t* xs = X + b * TM_C * plane + i * Np + j0;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int q = l + 64 * it, c = q >> 2, ch = q & 3;
+      *reinterpret_cast<u32x4*>(&sx[c * K3_XLD + ch * 8]) = *reinterpret_cast<const u32x4*>(xs + (int64_t)c * plane + ch * 8);
+    }
+  }
+  __syncthreads();
+  float xv[64];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv[8 * t + e] = live ? bf2f(sx[(64 * g + 8 * t + e) * K3_XLD + n]) : 0.f;
+  bf16x8 xo[8];
+  ln128_from_regs(xv, g, ln_out_w, ln_out_b, eps, xo);
+  load_row128(zin + pix * TM_C, live, g, xv);
+  bf16x8 xi[8];
+  ln128_from_regs(xv, g, ln_in_w, ln_in_b, eps, xi);
+  for (int cb = 0; cb < 4; ++cb) {
+    __syncthreads();
+    stage_w32(sW[0], w_o, cb * 32, tid);
+    stage_w32(sW[1], w_og, cb * 32, tid);
+    __syncthreads();
+    const f32x16 o = gemm_rows32(sW[0], n, g, xo);
+    const f32x16 gt = gemm_rows32(sW[1], n, g, xi);
+    if (!live) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c0 = cb * 32 + 8 * q + 4 * g;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = sigmoidf_(gt[4 * q + e]) * o[4 * q + e];
+      if (residual) {
+        const u32x2 r = *reinterpret_cast<const u32x2*>(zin + pix * TM_C + c0);
+        y[0] += lo_bf(r[0]);
+        y[1] += hi_bf(r[0]);
+        y[2] += lo_bf(r[1]);
+        y[3] += hi_bf(r[1]);
+      }
+      *reinterpret_cast<u32x2*>(out + pix * TM_C + c0) = u32x2{pack2(y[0], y[1]), pack2(y[2], y[3])};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- fp32 path
+constexpr int F_R = 32;      // pixel rows per workgroup
+constexpr int F_CC = 16;     // output channels per chunk
+constexpr int F_CM = 128;    // max channel width
+
+// LayerNorm of 32 rows of fp32 held in LDS (8 threads per row), in place.
+__device__ __forceinline__ void ln_rows_lds(float (*xs)[F_CM + 1], int c, const float* w, const float* b, float eps, int tid) {
+  const int r = tid >> 3, sub = tid & 7;
+  float s = 0.f;
+  for (int cc = sub; cc < c; cc += 8) s += xs[r][cc];
+  for (int o = 4; o >= 1; o >>= 1) s += __shfl_xor(s, o, 8);
+  const float mean = s / (float)c;
+  float q = 0.f;
+  for (int cc = sub; cc < c; cc += 8) {
+    const float d = xs[r][cc] - mean;
+    q += d * d;
+  }
+  for (int o = 4; o >= 1; o >>= 1) q += __shfl_xor(q, o, 8);
+  const float rstd = 1.0f / sqrtf(q / (float)c + eps);
+  __syncthreads();
+  for (int cc = sub; cc < c; cc += 8) xs[r][cc] = (xs[r][cc] - mean) * rstd * (w ? w[cc] : 1.f) + (b ? b[cc] : 0.f);
+  __syncthreads();
+}
+
+__global__ void __launch_bounds__(256) trimul_k1_f32(const float* __restrict__ z, const float* __restrict__ mask, const float* __restrict__ ln_w,
+                                                     const float* __restrict__ ln_b, float eps, const float* __restrict__ w_ap,
+                                                     const float* __restrict__ w_ag, const float* __restrict__ w_bp, const float* __restrict__ w_bg,
+                                                     float* __restrict__ pa, float* __restrict__ pb, int64_t N, int64_t Np, int cz, int ch, int outgoing) {
+  __shared__ float xs[F_R][F_CM + 1];
+  __shared__ float ws[4][F_CC][F_CM + 1];
+  const int tid = threadIdx.x;
+  const int64_t tiles_per_row = Np / F_R;
+  const int64_t P = blockIdx.x / tiles_per_row, Q0 = (blockIdx.x % tiles_per_row) * F_R;
+  const int64_t b = blockIdx.y;
+  for (int i = tid; i < F_R * cz; i += 256) {
+    const int r = i / cz, cc = i % cz;
+    const int64_t Q = Q0 + r;
+    const bool live = P < N && Q < N;
+    const int64_t pix = outgoing ? (b * N + P) * N + Q : (b * N + Q) * N + P;
+    xs[r][cc] = live ? z[pix * cz + cc] : 0.f;
+  }
+  __syncthreads();
+  ln_rows_lds(xs, cz, ln_w, ln_b, eps, tid);
+  const int r = tid >> 3, sub = tid & 7;
+  const int64_t Q = Q0 + r;
+  const bool live = P < N && Q < N;
+  const int64_t pix = outgoing ? (b * N + P) * N + Q : (b * N + Q) * N + P;
+  const float m = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
+  const int64_t plane = Np * Np;
+  for (int c0 = 0; c0 < ch; c0 += F_CC) {
+    __syncthreads();
+    for (int i = tid; i < F_CC * cz; i += 256) {
+      const int j = i / cz, cc = i % cz;
+      const bool ok = c0 + j < ch;
+      ws[0][j][cc] = ok ? w_ap[(int64_t)(c0 + j) * cz + cc] : 0.f;
+      ws[1][j][cc] = ok ? w_ag[(int64_t)(c0 + j) * cz + cc] : 0.f;
+      ws[2][j][cc] = ok ? w_bp[(int64_t)(c0 + j) * cz + cc] : 0.f;
+      ws[3][j][cc] = ok ? w_bg[(int64_t)(c0 + j) * cz + cc] : 0.f;
+    }
+    __syncthreads();
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = sub * 2 + jj;
+      if (c0 + j >= ch) continue;
+      float ap = 0.f, ag = 0.f, bp = 0.f, bg = 0.f;
+      for (int cc = 0; cc < cz; ++cc) {
+        const float xv = xs[r][cc];
+        ap = fmaf(xv, ws[0][j][cc], ap);
+        ag = fmaf(xv, ws[1][j][cc], ag);
+        bp = fmaf(xv, ws[2][j][cc], bp);
+        bg = fmaf(xv, ws[3][j][cc], bg);
+      }
+      const int64_t o = (b * ch + c0 + j) * plane + P * Np + Q;
+      pa[o] = m * sigmoid_exact(ag) * ap;
+      pb[o] = m * sigmoid_exact(bg) * bp;
+    }
+  }
+}
+
+constexpr int SG_T = 64, SG_K = 16;
+
+__global__ void __launch_bounds__(256) trimul_contract_f32(const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ X,
+                                                           int64_t Np, int64_t N) {
+  __shared__ float sA[SG_K][SG_T + 4];
+  __shared__ float sB[SG_K][SG_T + 4];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int64_t bc = blockIdx.z;
+  const int64_t i0 = (int64_t)blockIdx.y * SG_T, j0 = (int64_t)blockIdx.x * SG_T;
+  const int64_t plane = Np * Np;
+  const float* a0 = A + bc * plane;
+  const float* b0 = Bm + bc * plane;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < Np; k0 += SG_K) {
+    __syncthreads();
+    for (int i = tid; i < SG_T * SG_K; i += 256) {
+      const int r = i / SG_K, kk = i % SG_K;
+      sA[kk][r] = a0[(i0 + r) * Np + k0 + kk];
+      sB[kk][r] = b0[(j0 + r) * Np + k0 + kk];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < SG_K; ++kk) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        av[u] = sA[kk][ty * 4 + u];
+        bv[u] = sB[kk][tx * 4 + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) acc[u][w] = fmaf(av[u], bv[w], acc[u][w]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int64_t i = i0 + ty * 4 + u, j = j0 + tx * 4 + w;
+      if (i < N && j < N) X[bc * plane + i * Np + j] = acc[u][w];
+    }
+}
+
+__global__ void __launch_bounds__(256) trimul_k3_f32(const float* zin, float* out, const float* __restrict__ X, const float* __restrict__ ln_in_w,
+                                                     const float* __restrict__ ln_in_b, const float* __restrict__ ln_out_w,
+                                                     const float* __restrict__ ln_out_b, float eps, const float* __restrict__ w_o,
+                                                     const float* __restrict__ w_og, int64_t N, int64_t Np, int cz, int ch, int residual) {
+  __shared__ float xs[F_R][F_CM + 1];
+  __shared__ float zs[F_R][F_CM + 1];
+  __shared__ float ws[2][F_CC][F_CM + 1];
+  const int tid = threadIdx.x;
+  const int64_t tiles_per_row = Np / F_R;
+  const int64_t i = blockIdx.x / tiles_per_row, j0 = (blockIdx.x % tiles_per_row) * F_R;
+  const int64_t b = blockIdx.y;
+  const int64_t plane = Np * Np;
+  for (int q = tid; q < F_R * ch; q += 256) {
+    const int c = q / F_R, r = q % F_R;
+    xs[r][c] = (i < N && j0 + r < N) ? X[(b * ch + c) * plane + i * Np + j0 + r] : 0.f;
+  }
+  for (int q = tid; q < F_R * cz; q += 256) {
+    const int r = q / cz, cc = q % cz;
+    const int64_t j = j0 + r;
+    zs[r][cc] = (i < N && j < N) ? zin[((b * N + i) * N + j) * cz + cc] : 0.f;
+  }
+  __syncthreads();
+  ln_rows_lds(xs, ch, ln_out_w, ln_out_b, eps, tid);
+  ln_rows_lds(zs, cz, ln_in_w, ln_in_b, eps, tid);
+  const int r = tid >> 3, sub = tid & 7;
+  const int64_t j = j0 + r;
+  const bool live = i < N && j < N;
+  const int64_t pix = (b * N + i) * N + j;
+  float y[F_CC / 8 * (F_CM / F_CC)];
+  int ny = 0;
+  for (int c0 = 0; c0 < cz; c0 += F_CC) {
+    __syncthreads();
+    for (int q = tid; q < F_CC * F_CM; q += 256) {
+      const int jj = q / F_CM, cc = q % F_CM;
+      const bool ok = c0 + jj < cz;
+      ws[0][jj][cc] = (ok && cc < ch) ? w_o[(int64_t)(c0 + jj) * ch + cc] : 0.f;
+      ws[1][jj][cc] = (ok && cc < cz) ? w_og[(int64_t)(c0 + jj) * cz + cc] : 0.f;
+    }
+    __syncthreads();
+    for (int jj = 0; jj < 2; ++jj) {
+      const int co = sub * 2 + jj;
+      float o = 0.f, gt = 0.f;
+      for (int cc = 0; cc < ch; ++cc) o = fmaf(xs[r][cc], ws[0][co][cc], o);
+      for (int cc = 0; cc < cz; ++cc) gt = fmaf(zs[r][cc], ws[1][co][cc], gt);
+      y[ny++] = sigmoid_exact(gt) * o;
+    }
+  }
+  if (!live) return;
+  ny = 0;
+  for (int c0 = 0; c0 < cz; c0 += F_CC)
+    for (int jj = 0; jj < 2; ++jj) {
+      const int co = c0 + sub * 2 + jj;
+      float v = y[ny++];
+      if (co >= cz) continue;
+      if (residual) v += zin[pix * cz + co];
+      out[pix * cz + co] = v;
+    }
+}
+
+static int64_t padded(int64_t n) { return cdiv(n, TM_TILE) * TM_TILE; }
+
+}  // namespace fpf
+
+extern "C" size_t fpf_trimul_workspace_bytes(int64_t batch, int64_t n, int32_t c_z, int32_t c_h, int32_t dtype) {
+  (void)c_z;
+  const int64_t Np = fpf::padded(n);
+  const size_t elt = dtype == FPF_DT_F32 ? 4 : 2;
+  return (size_t)3 * (size_t)batch * (size_t)c_h * (size_t)Np * (size_t)Np * elt;
+}
+
+extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->z || !a->out || !a->ln_in_w || !a->ln_in_b || !a->ln_out_w || !a->ln_out_b || !a->w_ag || !a->w_ap || !a->w_bg || !a->w_bp ||
+      !a->w_o || !a->w_og)
+    return fail(err, errlen, FPF_E_ARGS, "a required pointer is NULL (z, out, the ten weights)");
+  if (a->batch <= 0 || a->n <= 0) return a->batch == 0 || a->n == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "batch / n negative");
+  const size_t need = fpf_trimul_workspace_bytes(a->batch, a->n, a->c_z, a->c_h, a->dtype);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t N = a->n, Np = padded(N), B = a->batch;
+  if (B > 65535) return fail(err, errlen, FPF_E_SHAPE, "batch above 65535");
+  if (a->dtype == FPF_DT_BF16) {
+    if (a->c_z != TM_C || a->c_h != TM_C) return fail(err, errlen, FPF_E_SHAPE, "bf16 trimul serves c_z = c_h = 128 (got %d, %d)", a->c_z, a->c_h);
+    if (!aligned16(a->z) || !aligned16(a->out) || !aligned16(a->workspace) || !aligned16(a->w_ag) || !aligned16(a->w_ap) ||
+        !aligned16(a->w_bg) || !aligned16(a->w_bp) || !aligned16(a->w_o) || !aligned16(a->w_og))
+      return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
+    uint16_t* pa = static_cast<uint16_t*>(a->workspace);
+    uint16_t* pb = pa + B * TM_C * Np * Np;
+    uint16_t* X = pb + B * TM_C * Np * Np;
+    const int64_t waves = Np * Np / 32;
+    hipLaunchKernelGGL(trimul_k1_bf16, dim3((unsigned)(waves / 4), (unsigned)B), dim3(256), 0, st, (const uint16_t*)a->z, a->mask, a->ln_in_w,
+                       a->ln_in_b, a->eps, (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg,
+                       pa, pb, N, Np, a->outgoing);
+    int rc = launched(err, errlen, "trimul_k1_bf16");
+    if (rc) return rc;
+    const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE) * B * TM_C;
+    hipLaunchKernelGGL(trimul_contract_bf16, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, N, B * TM_C);
+    rc = launched(err, errlen, "trimul_contract_bf16");
+    if (rc) return rc;
+    hipLaunchKernelGGL(trimul_k3_bf16, dim3((unsigned)(waves / 4), (unsigned)B), dim3(256), 0, st, (const uint16_t*)a->z, (uint16_t*)a->out, X,
+                       a->ln_in_w, a->ln_in_b, a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np,
+                       a->residual);
+    return launched(err, errlen, "trimul_k3_bf16");
+  }
+  if (a->dtype == FPF_DT_F32) {
+    if (a->c_z > F_CM || a->c_h > F_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 trimul serves c_z, c_h <= %d", F_CM);
+    float* pa = static_cast<float*>(a->workspace);
+    float* pb = pa + B * a->c_h * Np * Np;
+    float* X = pb + B * a->c_h * Np * Np;
+    hipLaunchKernelGGL(trimul_k1_f32, dim3((unsigned)(Np * Np / F_R), (unsigned)B), dim3(256), 0, st, (const float*)a->z, a->mask, a->ln_in_w,
+                       a->ln_in_b, a->eps, (const float*)a->w_ap, (const float*)a->w_ag, (const float*)a->w_bp, (const float*)a->w_bg, pa, pb, N,
+                       Np, a->c_z, a->c_h, a->outgoing);
+    int rc = launched(err, errlen, "trimul_k1_f32");
+    if (rc) return rc;
+    hipLaunchKernelGGL(trimul_contract_f32, dim3((unsigned)(Np / SG_T), (unsigned)(Np / SG_T), (unsigned)(B * a->c_h)), dim3(256), 0, st, pa,
+                       pb, X, Np, N);
+    rc = launched(err, errlen, "trimul_contract_f32");
+    if (rc) return rc;
+    hipLaunchKernelGGL(trimul_k3_f32, dim3((unsigned)(Np * Np / F_R), (unsigned)B), dim3(256), 0, st, (const float*)a->z, (float*)a->out, X,
+                       a->ln_in_w, a->ln_in_b, a->ln_out_w, a->ln_out_b, a->eps, (const float*)a->w_o, (const float*)a->w_og, N, Np, a->c_z,
+                       a->c_h, a->residual);
+    return launched(err, errlen, "trimul_k3_f32");
+  }
+  return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);
+}

@@ -1,0 +1,90 @@
+"""Transition face: y = W_o(silu(W_a n) * (W_b n)), n = LayerNorm(x), optional row mask and residual folded in the kernel,
+served by libfpf_hip's ``fpf_transition_fwd`` (one launch; the hidden never reaches HBM).
+
+Mirrors common/opt_core/opt_core/kernels/transition/__init__.py: ``pack(*, w_o, w_a=None, w_b=None, w_ab=None, ln_w=None,
+ln_b=None, eps=1e-5, device=None) -> Weights`` (:1011), ``Weights`` (:928; operand packs built once per weight set and dtype)
+and ``transition(x, W, *, word, residual=False, x_ln=None, mask=None, out=None, ...) -> (y, Selection)`` (:1074).  ``out`` may
+be ``x`` itself (in place).  ``x_ln`` (the caller's own LayerNorm output) is refused by name: the kernels always normalise.
+"""
+import torch
+
+from .. import _face as F
+from .. import _lib as L
+
+Refusal, Selection = F.Refusal, F.Selection
+
+
+class Weights(object):
+    """Canonical transition weights: w_a / w_b [hidden, c], w_o [c, hidden], LayerNorm ln_w / ln_b [c] (None = no affine),
+    eps.  Device operand packs (bf16 or fp32 contiguous copies) are built on first use per (device, dtype) and kept."""
+
+    def __init__(self, w_a, w_b, w_o, ln_w, ln_b, eps, device):
+        self.c, self.hidden = int(w_o.shape[0]), int(w_o.shape[1])
+        if tuple(w_a.shape) != (self.hidden, self.c) or tuple(w_b.shape) != (self.hidden, self.c):
+            raise Refusal("weights:shapes:%s:%s:%s" % (tuple(w_a.shape), tuple(w_b.shape), tuple(w_o.shape)), None, F.ROW_STOCK)
+        dev = device if device is not None else w_o.device
+        self.w_a, self.w_b, self.w_o = (t.detach().to(dev) for t in (w_a, w_b, w_o))
+        self.ln_w = None if ln_w is None else ln_w.detach().to(dev).float().contiguous()
+        self.ln_b = None if ln_b is None else ln_b.detach().to(dev).float().contiguous()
+        self.eps = float(eps)
+        self.device = dev
+        self._packs = {}
+
+    def pack_for(self, dtype, device):
+        key = (str(device), dtype)
+        p = self._packs.get(key)
+        if p is None:
+            with torch.no_grad():
+                p = tuple(t.to(device=device, dtype=dtype).contiguous() for t in (self.w_a, self.w_b, self.w_o))
+                p = p + (None if self.ln_w is None else self.ln_w.to(device),
+                         None if self.ln_b is None else self.ln_b.to(device))
+            self._packs[key] = p
+        return p
+
+
+def pack(*, w_o, w_a=None, w_b=None, w_ab=None, ln_w=None, ln_b=None, eps=1e-5, device=None):
+    """w_ab [2*hidden, c] = rows a (silu branch) then b -- the Boltz fc1|fc2 concatenation."""
+    if w_ab is not None:
+        h = int(w_ab.shape[0]) // 2
+        w_a, w_b = w_ab[:h], w_ab[h:]
+    if w_a is None or w_b is None:
+        raise Refusal("weights:missing_w_a_w_b", None, F.ROW_STOCK)
+    return Weights(w_a, w_b, w_o, ln_w, ln_b, eps, device)
+
+
+def select(dtype, arch, c, hidden, *, word):
+    """Pure: the row serving a transition of (dtype, c, hidden) on this device word, or Refusal by name."""
+    sel = F.resolve(word, F.dtype_word(dtype), arch, "transition", cell="transition:c%dh%d" % (c, hidden))
+    if sel.row == F.ROW_FAST and (c != 128 or hidden % 32):
+        raise Refusal("shape:c%dh%d" % (c, hidden), sel.row, F.ROW_F32, "the bf16 kernel serves c = 128, hidden % 32 == 0")
+    if sel.row == F.ROW_F32 and c > 128:
+        raise Refusal("shape:c%d" % c, sel.row, F.ROW_STOCK, "the fp32 kernel serves c <= 128")
+    return sel
+
+
+def transition(x, W, *, word, residual=False, x_ln=None, mask=None, out=None, selection=None, **_unused):
+    if x_ln is not None:
+        raise Refusal("ln_given", None, F.ROW_STOCK, "the HIP rows normalise in-kernel; x_ln is not taken")
+    c = int(x.shape[-1])
+    if c != W.c:
+        raise Refusal("c:%d!=%d" % (c, W.c), word, F.ROW_STOCK)
+    sel = selection or select(x.dtype, F.device_word(x), W.c, W.hidden, word=word)
+    rows = x.numel() // c
+    if not x.is_contiguous():
+        raise Refusal("stride", sel.row, F.ROW_STOCK, "x must be contiguous")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+        raise Refusal("out", sel.row, F.ROW_STOCK, "out must be contiguous, x's shape and dtype")
+    m = None
+    if mask is not None:
+        m = mask.reshape(-1)
+        if m.numel() != rows:
+            raise Refusal("mask_rows", sel.row, F.ROW_STOCK, "one mask value per row")
+        m = m.to(device=x.device, dtype=torch.float32).contiguous()
+    wa, wb, wo, lw, lb = W.pack_for(x.dtype, x.device)
+    a = L.TransitionArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if x.dtype == torch.bfloat16 else L.DT_F32, c=c, hidden=W.hidden,
+                         rows=rows, x=L.ptr(x), out=L.ptr(out), ln_w=L.ptr(lw), ln_b=L.ptr(lb), eps=W.eps, w_a=L.ptr(wa), w_b=L.ptr(wb),
+                         w_o=L.ptr(wo), row_mask=L.ptr(m), residual=1 if residual else 0)
+    L.call("fpf_transition_fwd", a, L.stream_ptr(x.device))
+    return out, sel
