@@ -1,0 +1,174 @@
+"""GPU parity of the triangle-attention core (op) and block (prologue -> core -> epilogue) against the CPU oracle."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_bf16_close, assert_bf16_residual_close, assert_f32_close, max_abs, rel_l2
+from conftest import GOLDEN
+from oracle import stock as S
+from oracle import vectors as V
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+CASES = json.load(open(os.path.join(GOLDEN, "triattn_cases.json")))["cases"]
+BF16_CASES = [c for c in CASES if c["D"] == 32 and c["dtype"] == "bf16"]
+
+
+def _to_dev(t):
+    """Move a case's tensors to the GPU keeping strided views strided (the endstrided layout)."""
+    out = {}
+    for n in ("q", "k", "v"):
+        x = t[n]
+        if not x.is_contiguous():                       # [B,S,H,N,D] storage handed as a transposed view
+            out[n] = x.transpose(1, 3).contiguous().to(DEV).transpose(1, 3)
+        else:
+            out[n] = x.to(DEV)
+    out["bias"] = t["bias"].to(DEV)
+    out["mask"] = None if t["mask"] is None else t["mask"].to(DEV)
+    return out
+
+
+@pytest.mark.parametrize("case", BF16_CASES, ids=[c["id"] for c in BF16_CASES])
+def test_core_bf16_golden_cases(case):
+    from fpf_hip.kernels import triattn as TA
+    t = V.triattn_inputs(case)
+    d = _to_dev(t)
+    if case["layout"] == "endstrided":
+        assert not d["q"].is_contiguous()
+    out = TA.triangle_attention(d["q"], d["k"], d["v"], d["bias"], d["mask"], t["scale"], word="fast")
+    torch.cuda.synchronize()
+    ref32 = S.triangle_attention_op(t["q"], t["k"], t["v"], t["bias"], t["mask"], t["scale"], dtype=torch.float32)
+    assert_bf16_close(out, ref32, case["id"])
+    ref_row0 = torch.from_numpy(np.load(os.path.join(GOLDEN, "triattn_ref_%s.npy" % case["id"])))
+    o0 = out[:, 0:1].float().cpu()
+    print("[parity] %s row0 vs reference fp64: ours max_abs=%.3e | H100 recorded max_abs=%.3e (all rows)" % (
+        case["id"], max_abs(o0, ref_row0), case["err_vs_fp64"]["max_abs"]))
+    assert max_abs(o0, ref_row0) <= 2e-2
+
+
+def test_core_head_dim_16_refused_by_bf16_row_and_served_by_fp32_row():
+    from fpf_hip.kernels import triattn as TA
+    case = [c for c in CASES if c["id"] == "a80_d16_s512_prefix"][0]
+    t = V.triattn_inputs(case)
+    with pytest.raises(TA.Refusal) as ei:
+        TA.triangle_attention(t["q"].to(DEV), t["k"].to(DEV), t["v"].to(DEV), t["bias"].to(DEV), t["mask"].to(DEV), word="fast")
+    assert ei.value.kind == "no_row:head_dim16" and ei.value.fallback == "hip_gfx950_f32"
+    q, k, v = (t[n].float().to(DEV) for n in ("q", "k", "v"))
+    out = TA.triangle_attention(q, k, v, t["bias"].to(DEV), t["mask"].to(DEV), t["scale"], word="exact")
+    torch.cuda.synchronize()
+    ref = S.triangle_attention_op(t["q"].double(), t["k"].double(), t["v"].double(), t["bias"], t["mask"], t["scale"], dtype=torch.float64)
+    assert_f32_close(out, ref, "d16 fp32")
+
+
+def _rand_op(B, N, H, Sq, D, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, N, H, Sq, D, generator=g).to(dtype) for _ in range(3))
+    bias = (torch.randn(B, 1, H, Sq, Sq, generator=g) * 0.5)
+    return q, k, v, bias
+
+
+def test_core_bf16_dead_rows_are_uniform_mean():
+    from fpf_hip.kernels import triattn as TA
+    q, k, v, bias = _rand_op(1, 6, 4, 100, 32, 1, torch.bfloat16)
+    mask = torch.ones(1, 6, 1, 1, 100, dtype=torch.bool)
+    mask[0, 2] = False
+    mask[0, 4, ..., 50:] = False
+    out = TA.triangle_attention(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV), mask.to(DEV), word="fast").cpu()
+    ref = S.triangle_attention_op(q, k, v, bias, mask, dtype=torch.float32)
+    assert_bf16_close(out, ref, "dead rows")
+    mean = v[0, 2].float().mean(dim=-2, keepdim=True).expand(4, 100, 32)
+    assert max_abs(out[0, 2], mean) <= 2 ** -8 * max(1.0, mean.abs().max().item())
+
+
+def test_core_bf16_key_padding_is_bitwise_the_cropped_problem():
+    """Valid queries of a key-padded call equal the cropped call bit for bit (masked keys contribute exact zeros)."""
+    from fpf_hip.kernels import triattn as TA
+    S_, L = 384, 346
+    q, k, v, bias = _rand_op(1, 5, 4, S_, 32, 2, torch.bfloat16)
+    mask = torch.zeros(1, 5, 1, 1, S_, dtype=torch.bool)
+    mask[..., :L] = True
+    full = TA.triangle_attention(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV), mask.to(DEV), word="fast")
+    crop = TA.triangle_attention(q[..., :L, :].contiguous().to(DEV), k[..., :L, :].contiguous().to(DEV), v[..., :L, :].contiguous().to(DEV),
+                                 bias[..., :L, :L].contiguous().to(DEV), None, word="fast")
+    torch.cuda.synchronize()
+    assert torch.equal(full[..., :L, :], crop)
+
+
+def test_core_bf16_run_to_run_bitwise():
+    from fpf_hip.kernels import triattn as TA
+    q, k, v, bias = (t.to(DEV) for t in _rand_op(1, 8, 4, 200, 32, 3, torch.bfloat16))
+    a = TA.triangle_attention(q, k, v, bias, None, word="fast")
+    b = TA.triangle_attention(q, k, v, bias, None, word="fast")
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("D", [32, 64])
+def test_core_fp32_exact(D):
+    from fpf_hip.kernels import triattn as TA
+    q, k, v, bias = _rand_op(1, 4, 2, 150, D, 4, torch.float32)
+    mask = torch.ones(1, 4, 1, 1, 150, dtype=torch.bool)
+    mask[0, 1, ..., 120:] = False
+    mask[0, 3] = False
+    out = TA.triangle_attention(q.to(DEV), k.to(DEV), v.to(DEV), bias.to(DEV), mask.to(DEV), word="exact")
+    torch.cuda.synchronize()
+    ref = S.triangle_attention_op(q, k, v, bias, mask, dtype=torch.float64)
+    assert_f32_close(out, ref, "core fp32 D%d" % D)
+
+
+# ------------------------------------------------------------------------------------------------------------------ block
+def _block_weights(dtype, seed=0):
+    P = S.make_block_params(c_z=128, heads=4, head_dim=32, seed=seed)["tas"]
+    g = torch.Generator().manual_seed(seed + 100)
+    P["ln_w"] = 1 + 0.1 * torch.randn(128, generator=g)
+    P["ln_b"] = 0.1 * torch.randn(128, generator=g)
+    for n in ("w_q", "w_k", "w_v", "w_g", "w_b", "w_o"):
+        P[n] = P[n].to(dtype).float()                 # bf16-representable weights: the oracle and the kernel see the same values
+    return P
+
+
+def _pack(P, dtype):
+    from fpf_hip.attn import pair_fused as PF
+    return PF.pack_triattn_weights(w_o=P["w_o"].to(DEV), n_heads=4, head_dim=32, ln_w=P["ln_w"].to(DEV), ln_b=P["ln_b"].to(DEV),
+                                   w_q=P["w_q"].to(DEV), w_k=P["w_k"].to(DEV), w_v=P["w_v"].to(DEV), w_g=P["w_g"].to(DEV), w_b=P["w_b"].to(DEV))
+
+
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("N,pad", [(64, 0), (96, 10)])
+def test_block_bf16(ending, N, pad):
+    from fpf_hip.attn import pair_fused as PF
+    P = _block_weights(torch.bfloat16)
+    W = _pack(P, torch.bfloat16)
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(N)).to(torch.bfloat16)
+    mask = torch.ones(1, N, N)
+    if pad:
+        mask[:, N - pad:, :] = 0
+        mask[:, :, N - pad:] = 0
+    u = PF.tri_attn_block(z.to(DEV), W, mask.to(DEV), ending=ending, residual=False)
+    torch.cuda.synchronize()
+    ref = S.tri_attn(z.float(), P, mask, ending=ending, dtype=torch.float32)
+    assert_bf16_close(u, ref, "block ending=%s N%d pad%d" % (ending, N, pad))
+    zz = z.to(DEV).clone()
+    r = PF.tri_attn_block(zz, W, mask.to(DEV), ending=ending, residual=True)
+    torch.cuda.synchronize()
+    assert r.data_ptr() == zz.data_ptr()
+    assert_bf16_residual_close(zz, z.float() + ref, "block residual ending=%s" % ending)
+
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_block_fp32_exact(ending):
+    from fpf_hip.attn import pair_fused as PF
+    P = _block_weights(torch.float32, seed=1)
+    W = _pack(P, torch.float32)
+    N = 40
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(9))
+    mask = torch.ones(1, N, N)
+    mask[:, :, N - 4:] = 0
+    u = PF.tri_attn_block(z.to(DEV), W, mask.to(DEV), ending=ending, residual=False, word="exact")
+    torch.cuda.synchronize()
+    ref = S.tri_attn(z, P, mask, ending=ending, dtype=torch.float64)
+    live = slice(0, N - 4) if ending else slice(0, N)
+    assert_f32_close(u[:, :, live] if ending else u, ref[:, :, live] if ending else ref, "block fp32 ending=%s" % ending)

@@ -1,0 +1,786 @@
+// Triangle attention: the flash core (op) and the fused block (prologue -> core -> epilogue).
+// Replaces common/opt_core/opt_core/kernels/triattn/__init__.py:1094 (triangle_attention, op :3-8) and
+// common/opt_core/opt_core/attn/pair_fused.py:1500 (tri_attn_block; prologue :1136, core_attention :1391, epilogue :1416).
+//
+// bf16 core (head_dim 32): a workgroup = 4 waves x 32 queries of one (b, h) and R = 4 pair rows.  The per-key-tile bias tile
+// (one per wave: its 32 queries x 32 keys) is loaded ONCE into registers and reused by all R rows; the R rows' K and V^T tiles
+// are staged in LDS once and read by all 4 waves.  S^T = K Q^T is computed with v_mfma_f32_32x32x16_bf16 starting from the
+// bias tile as the accumulator, so each lane owns ONE query and 16 of the 32 keys (the other 16 in lane ^ 32): the softmax
+// max is 16 in-lane maxes + one cross-half exchange, the running sum stays per lane until the end, and P (bf16) is already
+// the B operand of O^T = V^T P^T -- the key order inside a k-step is permuted identically in V^T.  exp2 with scale*log2(e)
+// folded into one FMA.  A row whose keys are all masked attends uniformly to every key (the op's convention).
+// fp32 core (exact tier): one thread per query, LDS-staged K / V tiles, fp32 online softmax with expf.
+#include "fpf_common.h"
+
+namespace fpf {
+
+constexpr int TA_D = 32;
+constexpr int TA_R = 4;          // pair rows per workgroup sharing the bias tile
+constexpr int TA_KT = 32;        // keys per tile
+constexpr int TA_KLD = 40;       // LDS pitch (bf16) of a K row: 80 B, conflict-free 16-byte reads
+constexpr int TA_VLD = 36;       // LDS pitch (bf16) of a V^T row: 72 B, conflict-free 8-byte reads
+constexpr float LOG2E = 1.4426950408889634f;
+static_assert(TA_R == 4, "one wave computes the keep bits of one staged row");
+
+struct CoreParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t qs[5], ks[5], vs[5];
+  const void* bias;
+  int bias_bf16;
+  int64_t bs[4];
+  const void* mask;
+  int mask_f32;
+  int64_t ms[3];
+  uint16_t* out;
+  int64_t os[5];
+  int64_t B, N, H, S;
+  float scale;
+};
+
+__device__ __forceinline__ bool mask_keep(const CoreParams& p, int64_t b, int64_t i, int64_t key) {
+  if (!p.mask) return true;
+  const int64_t o = b * p.ms[0] + i * p.ms[1] + key * p.ms[2];
+  return p.mask_f32 ? (static_cast<const float*>(p.mask)[o] != 0.0f) : (static_cast<const uint8_t*>(p.mask)[o] != 0);
+}
+
+__device__ __forceinline__ float bias_at(const CoreParams& p, int64_t off) {
+  return p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[off]) : static_cast<const float*>(p.bias)[off];
+}
+
+__global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[TA_R][TA_KT * TA_KLD];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[TA_R][TA_D * TA_VLD];
+  __shared__ uint32_t sKeep[TA_R];
+  __shared__ int sAlive[TA_R];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  // logical work order (b h) -> row group -> query tile; dealt to the 8 XCDs in contiguous runs
+  const int64_t nq = cdiv(p.S, 128), nr = cdiv(p.N, TA_R);
+  const int64_t total = p.B * p.H * nr * nq;
+  const int64_t per = (total + 7) / 8;
+  const int64_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (w >= total) return;
+  const int64_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
+  const int64_t b = bh / p.H, h = bh % p.H;
+  const int64_t i0 = rg * TA_R;
+  const int64_t q = qt * 128 + wave * 32 + n;          // this lane's query
+  const bool qlive = q < p.S;
+  const float c2 = p.scale * LOG2E;                     // logits in qk units -> log2 units
+  const float inv_scale = 1.0f / p.scale;
+
+  // row liveness (a row with no kept key is "dead": uniform over all keys)
+  if (tid < TA_R) sAlive[tid] = 0;
+  __syncthreads();
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    if (i >= p.N) continue;
+    int any = 0;
+    for (int64_t key = tid; key < p.S && !any; key += 256) any = mask_keep(p, b, i, key);
+    if (any) sAlive[r] = 1;
+  }
+  __syncthreads();
+  bool dead[TA_R];
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) dead[r] = (i0 + r < p.N) && !sAlive[r];
+
+  // Q fragments (B operand of S^T = K Q^T): query n, d = 16t + 8g .. +7
+  bf16x8 qf[TA_R][2];
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    const bool ok = qlive && i < p.N;
+    const uint16_t* qp = p.q + b * p.qs[0] + i * p.qs[1] + h * p.qs[2] + q * p.qs[3];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) qf[r][t] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16 * t + 8 * g) : u32x4{0, 0, 0, 0});
+  }
+  f32x16 o[TA_R];
+  float mrow[TA_R], lrow[TA_R];
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    o[r] = f32x16{};
+    mrow[r] = -INFINITY;
+    lrow[r] = 0.f;
+  }
+
+  // staging map: 512 16-byte chunks per operand per tile, 2 per thread: row r, key kk, d-part
+  int sr[2], skk[2], sd[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int c = tid + 256 * it;
+    sr[it] = c >> 7;
+    skk[it] = (c >> 2) & 31;
+    sd[it] = (c & 3) * 8;
+  }
+  u32x4 rk[2], rv[2];
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int64_t i = i0 + sr[it], key = k0 + skk[it];
+      const bool ok = i < p.N && key < p.S;
+      rk[it] = ok ? *reinterpret_cast<const u32x4*>(p.k + b * p.ks[0] + i * p.ks[1] + h * p.ks[2] + key * p.ks[3] + sd[it]) : u32x4{0, 0, 0, 0};
+      rv[it] = ok ? *reinterpret_cast<const u32x4*>(p.v + b * p.vs[0] + i * p.vs[1] + h * p.vs[2] + key * p.vs[3] + sd[it]) : u32x4{0, 0, 0, 0};
+    }
+  };
+  gload(0);
+  const int64_t bias_row = b * p.bs[0] + h * p.bs[1] + q * p.bs[2];
+  for (int64_t k0 = 0; k0 < p.S; k0 += TA_KT) {
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      *reinterpret_cast<u32x4*>(&sK[sr[it]][skk[it] * TA_KLD + sd[it]]) = rk[it];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sV[sr[it]][(sd[it] + 2 * e) * TA_VLD + skk[it]] = (uint16_t)(rv[it][e] & 0xffff);
+        sV[sr[it]][(sd[it] + 2 * e + 1) * TA_VLD + skk[it]] = (uint16_t)(rv[it][e] >> 16);
+      }
+    }
+    {   // keep bits of row `wave` for this tile (dead rows keep every in-range key)
+      const int64_t i = i0 + wave, key = k0 + n;
+      const bool dw = !sAlive[wave];
+      const bool keep = (l < 32) && key < p.S && i < p.N && (dw || mask_keep(p, b, i, key));
+      const uint64_t bal = __ballot(keep);
+      if (l == 0) sKeep[wave] = (uint32_t)bal;
+    }
+    __syncthreads();
+    if (k0 + TA_KT < p.S) gload(k0 + TA_KT);
+    // bias tile (qk units) -> accumulator init; keys 8qd + 4g + 0..3
+    f32x16 bt;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int64_t key = k0 + 8 * qd + 4 * g;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bt[4 * qd + e] = (qlive && key + e < p.S) ? bias_at(p, bias_row + (key + e) * p.bs[3]) * inv_scale : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      const uint32_t kb = sKeep[r];
+      if (kb == 0) continue;                                  // nothing kept in this tile for row r
+      const uint16_t* kr = sK[r];
+      f32x16 s;
+      if (dead[r]) {
+        s = f32x16{};
+      } else {
+        s = bt;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) s = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&kr[n * TA_KLD + 16 * t + 8 * g])), qf[r][t], s);
+      }
+      if (kb != 0xffffffffu) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (!((kb >> c_row(v, g)) & 1u)) s[v] = -INFINITY;
+      }
+      float mx = s[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);
+      mx = fmaxf(mx, xor32(mx));
+      const float mnew = fmaxf(mrow[r], mx);
+      const float alpha = fast_exp2((mrow[r] - mnew) * c2);
+      const float mc = mnew * c2;
+      float ps = 0.f;
+      uint32_t pk[8];
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = fast_exp2(fmaf(s[v], c2, -mc));
+        const float p1 = fast_exp2(fmaf(s[v + 1], c2, -mc));
+        ps += p0 + p1;
+        pk[v >> 1] = pack2(p0, p1);
+      }
+      lrow[r] = lrow[r] * alpha + ps;
+      mrow[r] = mnew;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
+      const uint16_t* vr = sV[r];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const uint16_t* vrow = &vr[n * TA_VLD + 16 * st + 4 * g];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+        o[r] = mfma32(as_bf8(u32x4{lo[0], lo[1], hi[0], hi[1]}), as_bf8(u32x4{pk[4 * st], pk[4 * st + 1], pk[4 * st + 2], pk[4 * st + 3]}), o[r]);
+      }
+    }
+  }
+  if (!qlive) return;
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    if (i >= p.N) continue;
+    const float lt = lrow[r] + xor32(lrow[r]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int d0 = 8 * qd + 4 * g;
+      *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- fp32 core
+struct CoreParamsF {
+  const float* q;
+  const float* k;
+  const float* v;
+  int64_t qs[5], ks[5], vs[5];
+  const void* bias;
+  int bias_bf16;
+  int64_t bs[4];
+  const void* mask;
+  int mask_f32;
+  int64_t ms[3];
+  float* out;
+  int64_t os[5];
+  int64_t B, N, H, S;
+  float scale;
+};
+
+constexpr int TF_QT = 64;   // queries per workgroup (one per thread)
+constexpr int TF_KT = 32;
+
+template <int D>
+__global__ void __launch_bounds__(64) triattn_core_f32(const CoreParamsF p) {
+  __shared__ float sK[TF_KT][D + 1];
+  __shared__ float sV[TF_KT][D + 1];
+  __shared__ int sKeep[TF_KT];
+  __shared__ int sAlive;
+  const int tid = threadIdx.x;
+  const int64_t nq = cdiv(p.S, TF_QT);
+  const int64_t qt = blockIdx.x % nq, rest = blockIdx.x / nq;
+  const int64_t h = rest % p.H, i = (rest / p.H) % p.N, b = rest / (p.H * p.N);
+  const int64_t q = qt * TF_QT + tid;
+  const bool qlive = q < p.S;
+  if (tid == 0) sAlive = 0;
+  __syncthreads();
+  {
+    int any = 0;
+    for (int64_t key = tid; key < p.S && !any; key += TF_QT) {
+      if (!p.mask) { any = 1; break; }
+      const int64_t off = b * p.ms[0] + i * p.ms[1] + key * p.ms[2];
+      any = p.mask_f32 ? (static_cast<const float*>(p.mask)[off] != 0.f) : (static_cast<const uint8_t*>(p.mask)[off] != 0);
+    }
+    if (any) atomicOr(&sAlive, 1);
+  }
+  __syncthreads();
+  const bool dead = !sAlive;
+  float qv[D], ov[D];
+  const float* qp = p.q + b * p.qs[0] + i * p.qs[1] + h * p.qs[2] + q * p.qs[3];
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    qv[d] = qlive ? qp[d] : 0.f;
+    ov[d] = 0.f;
+  }
+  float m = -INFINITY, lsum = 0.f;
+  for (int64_t k0 = 0; k0 < p.S; k0 += TF_KT) {
+    __syncthreads();
+    for (int c = tid; c < TF_KT * D; c += TF_QT) {
+      const int kk = c / D, d = c % D;
+      const int64_t key = k0 + kk;
+      const bool ok = key < p.S;
+      sK[kk][d] = ok ? p.k[b * p.ks[0] + i * p.ks[1] + h * p.ks[2] + key * p.ks[3] + d] : 0.f;
+      sV[kk][d] = ok ? p.v[b * p.vs[0] + i * p.vs[1] + h * p.vs[2] + key * p.vs[3] + d] : 0.f;
+    }
+    if (tid < TF_KT) {
+      const int64_t key = k0 + tid;
+      bool keep = key < p.S;
+      if (keep && !dead && p.mask) {
+        const int64_t off = b * p.ms[0] + i * p.ms[1] + key * p.ms[2];
+        keep = p.mask_f32 ? (static_cast<const float*>(p.mask)[off] != 0.f) : (static_cast<const uint8_t*>(p.mask)[off] != 0);
+      }
+      sKeep[tid] = keep;
+    }
+    __syncthreads();
+    float sc[TF_KT];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kk = 0; kk < TF_KT; ++kk) {
+      float s = -INFINITY;
+      if (sKeep[kk]) {
+        if (dead) {
+          s = 0.f;
+        } else {
+          float dot = 0.f;
+#pragma unroll
+          for (int d = 0; d < D; ++d) dot = fmaf(qv[d], sK[kk][d], dot);
+          const int64_t key = k0 + kk;
+          const float bb = qlive ? (p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[b * p.bs[0] + h * p.bs[1] + q * p.bs[2] + key * p.bs[3]])
+                                                : static_cast<const float*>(p.bias)[b * p.bs[0] + h * p.bs[1] + q * p.bs[2] + key * p.bs[3]])
+                                 : 0.f;
+          s = dot * p.scale + bb;
+        }
+      }
+      sc[kk] = s;
+      tmax = fmaxf(tmax, s);
+    }
+    if (tmax == -INFINITY) continue;
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = expf(m - mnew);
+    lsum *= alpha;
+#pragma unroll
+    for (int d = 0; d < D; ++d) ov[d] *= alpha;
+#pragma unroll
+    for (int kk = 0; kk < TF_KT; ++kk) {
+      const float pe = expf(sc[kk] - mnew);
+      lsum += pe;
+#pragma unroll
+      for (int d = 0; d < D; ++d) ov[d] = fmaf(pe, sV[kk][d], ov[d]);
+    }
+    m = mnew;
+  }
+  if (!qlive) return;
+  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+  float* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
+#pragma unroll
+  for (int d = 0; d < D; ++d) op[d] = ov[d] * inv;
+}
+
+// ---------------------------------------------------------------------------------------------------------------- prologue (bf16)
+// x = LN(z or z^T) -> q, k, v [B,I,H,J,D] bf16, g [B,I,J,HD] bf16 (pre-sigmoid), bias [B,H,I,J] fp32.  A wave owns 32 positions
+// j of one attention row i; with `ending` the 32 z pixels are z[j][i] (strided rows, each a contiguous 256-byte pixel).
+constexpr int TP_C = 128, TP_HD = 128, TP_WLD = TP_C + 8;
+
+__device__ __forceinline__ void ln128_load(const uint16_t* __restrict__ row, bool live, int g, const float* __restrict__ w,
+                                           const float* __restrict__ bsh, float eps, bf16x8 (&xb)[8]) {
+  float xv[64];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const u32x4 r = live ? *reinterpret_cast<const u32x4*>(row + 64 * g + 8 * t) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xv[8 * t + 2 * e] = lo_bf(r[e]);
+      xv[8 * t + 2 * e + 1] = hi_bf(r[e]);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) s += xv[i];
+  s += xor32(s);
+  const float mean = s * (1.0f / 128.0f);
+  float qq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const float d = xv[i] - mean;
+    qq += d * d;
+  }
+  qq += xor32(qq);
+  const float rstd = 1.0f / sqrtf(qq * (1.0f / 128.0f) + eps);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int c0 = 64 * g + 8 * t;
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (xv[8 * t + e] - mean) * rstd * (w ? w[c0 + e] : 1.f) + (bsh ? bsh[c0 + e] : 0.f);
+    xb[t] = as_bf8(u32x4{pack2(y[0], y[1]), pack2(y[2], y[3]), pack2(y[4], y[5]), pack2(y[6], y[7])});
+  }
+}
+
+__global__ void __launch_bounds__(256) triattn_prologue_bf16(const uint16_t* __restrict__ z, const float* __restrict__ ln_w,
+                                                             const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ w_qkvg,
+                                                             const uint16_t* __restrict__ w_b, int H, uint16_t* __restrict__ qo,
+                                                             uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, uint16_t* __restrict__ go,
+                                                             float* __restrict__ bo, int64_t N, int ending) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[2][32 * TP_WLD];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t tpr = cdiv(N, 32);
+  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t b = blockIdx.y;
+  const int64_t i = wt / tpr, j = (wt % tpr) * 32 + n;
+  const bool live = i < N && j < N;
+  const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
+  bf16x8 xb[8];
+  ln128_load(z + zpix * TP_C, live, g, ln_w, ln_b, eps, xb);
+  const int D = TP_HD / H;
+  // 16 blocks of 32 output channels (q | k | v | g) + 1 bias block (rows >= H of it are zero)
+  for (int blk = 0; blk < 17; ++blk) {
+    __syncthreads();
+    if (blk < 16) {
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int c = tid + 256 * it, r = c >> 4, ch = c & 15;
+        *reinterpret_cast<u32x4*>(&sW[blk & 1][r * TP_WLD + ch * 8]) =
+            *reinterpret_cast<const u32x4*>(w_qkvg + (int64_t)(blk * 32 + r) * TP_C + ch * 8);
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int c = tid + 256 * it, r = c >> 4, ch = c & 15;
+        *reinterpret_cast<u32x4*>(&sW[blk & 1][r * TP_WLD + ch * 8]) =
+            r < H ? *reinterpret_cast<const u32x4*>(w_b + (int64_t)r * TP_C + ch * 8) : u32x4{0, 0, 0, 0};
+      }
+    }
+    __syncthreads();
+    f32x16 acc = {};
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&sW[blk & 1][n * TP_WLD + 64 * g + 8 * t])), xb[t], acc);
+    if (!live) continue;
+    if (blk < 12) {
+      uint16_t* dst = blk < 4 ? qo : (blk < 8 ? ko : vo);
+      const int cb = (blk & 3) * 32;      // channel base within q / k / v
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int c0 = cb + 8 * qd + 4 * g;       // channel = h * D + d
+        const int hh = c0 / D, d0 = c0 % D;
+        uint16_t* p = dst + (((b * N + i) * H + hh) * N + j) * D + d0;
+        *reinterpret_cast<u32x2*>(p) = u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
+      }
+    } else if (blk < 16) {
+      const int cb = (blk - 12) * 32;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int c0 = cb + 8 * qd + 4 * g;
+        *reinterpret_cast<u32x2*>(go + ((b * N + i) * N + j) * TP_HD + c0) =
+            u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
+      }
+    } else if (g == 0) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (v < H) bo[((b * H + v) * N + i) * N + j] = acc[v];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- epilogue (bf16)
+// u = (sigmoid(g) * o) W_o^T; residual: z[i,j] += u (ending: z[j,i] += u) in place; else out[zpix] = u.
+__global__ void __launch_bounds__(256) triattn_epilogue_bf16(const uint16_t* __restrict__ o, const uint16_t* __restrict__ gt,
+                                                             const uint16_t* __restrict__ w_o, int H, uint16_t* zout, int64_t N, int ending,
+                                                             int residual) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[32 * TP_WLD];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t tpr = cdiv(N, 32);
+  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t b = blockIdx.y;
+  const int64_t i = wt / tpr, j = (wt % tpr) * 32 + n;
+  const bool live = i < N && j < N;
+  const int D = TP_HD / H;
+  bf16x8 xb[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int hd0 = 64 * g + 8 * t;
+    const int hh = hd0 / D, d0 = hd0 % D;
+    u32x4 ov = {0, 0, 0, 0}, gv = {0, 0, 0, 0};
+    if (live) {
+      ov = *reinterpret_cast<const u32x4*>(o + (((b * N + i) * H + hh) * N + j) * D + d0);
+      gv = *reinterpret_cast<const u32x4*>(gt + ((b * N + i) * N + j) * TP_HD + hd0);
+    }
+    uint32_t w4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w4[e] = pack2(sigmoidf_(lo_bf(gv[e])) * lo_bf(ov[e]), sigmoidf_(hi_bf(gv[e])) * hi_bf(ov[e]));
+    xb[t] = as_bf8(u32x4{w4[0], w4[1], w4[2], w4[3]});
+  }
+  const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
+  for (int cb = 0; cb < 4; ++cb) {
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int c = tid + 256 * it, r = c >> 4, ch = c & 15;
+      *reinterpret_cast<u32x4*>(&sW[r * TP_WLD + ch * 8]) = *reinterpret_cast<const u32x4*>(w_o + (int64_t)(cb * 32 + r) * TP_HD + ch * 8);
+    }
+    __syncthreads();
+    f32x16 acc = {};
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&sW[n * TP_WLD + 64 * g + 8 * t])), xb[t], acc);
+    if (!live) continue;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int c0 = cb * 32 + 8 * qd + 4 * g;
+      uint16_t* p = zout + zpix * TP_C + c0;
+      float y0 = acc[4 * qd], y1 = acc[4 * qd + 1], y2 = acc[4 * qd + 2], y3 = acc[4 * qd + 3];
+      if (residual) {
+        const u32x2 r = *reinterpret_cast<const u32x2*>(p);
+        y0 += lo_bf(r[0]);
+        y1 += hi_bf(r[0]);
+        y2 += lo_bf(r[1]);
+        y3 += hi_bf(r[1]);
+      }
+      *reinterpret_cast<u32x2*>(p) = u32x2{pack2(y0, y1), pack2(y2, y3)};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- fp32 prologue / epilogue
+constexpr int PF_R = 32, PF_CC = 16, PF_CM = 128;
+
+__global__ void __launch_bounds__(256) triattn_prologue_f32(const float* __restrict__ z, const float* __restrict__ ln_w, const float* __restrict__ ln_b,
+                                                            float eps, const float* __restrict__ w_qkvg, const float* __restrict__ w_b, int C, int H,
+                                                            int D, float* __restrict__ qo, float* __restrict__ ko, float* __restrict__ vo,
+                                                            float* __restrict__ go, float* __restrict__ bo, int64_t N, int ending) {
+  __shared__ float xs[PF_R][PF_CM + 1];
+  __shared__ float ws[PF_CC][PF_CM + 1];
+  const int tid = threadIdx.x;
+  const int64_t tpr = cdiv(N, PF_R);
+  const int64_t i = blockIdx.x / tpr, j0 = (blockIdx.x % tpr) * PF_R;
+  const int64_t b = blockIdx.y;
+  const int HD = H * D;
+  for (int c = tid; c < PF_R * C; c += 256) {
+    const int r = c / C, cc = c % C;
+    const int64_t j = j0 + r;
+    const bool live = i < N && j < N;
+    const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
+    xs[r][cc] = live ? z[zpix * C + cc] : 0.f;
+  }
+  __syncthreads();
+  {
+    const int r = tid >> 3, sub = tid & 7;
+    float s = 0.f;
+    for (int cc = sub; cc < C; cc += 8) s += xs[r][cc];
+    for (int o = 4; o >= 1; o >>= 1) s += __shfl_xor(s, o, 8);
+    const float mean = s / (float)C;
+    float q = 0.f;
+    for (int cc = sub; cc < C; cc += 8) {
+      const float d = xs[r][cc] - mean;
+      q += d * d;
+    }
+    for (int o = 4; o >= 1; o >>= 1) q += __shfl_xor(q, o, 8);
+    const float rstd = 1.0f / sqrtf(q / (float)C + eps);
+    __syncthreads();
+    for (int cc = sub; cc < C; cc += 8) xs[r][cc] = (xs[r][cc] - mean) * rstd * (ln_w ? ln_w[cc] : 1.f) + (ln_b ? ln_b[cc] : 0.f);
+  }
+  const int r = tid >> 3, sub = tid & 7;
+  const int64_t j = j0 + r;
+  const bool live = i < N && j < N;
+  const int nout = 4 * HD + H;
+  for (int c0 = 0; c0 < nout; c0 += PF_CC) {
+    __syncthreads();
+    for (int c = tid; c < PF_CC * C; c += 256) {
+      const int jj = c / C, cc = c % C, ch = c0 + jj;
+      ws[jj][cc] = ch < 4 * HD ? w_qkvg[(int64_t)ch * C + cc] : (ch < nout ? w_b[(int64_t)(ch - 4 * HD) * C + cc] : 0.f);
+    }
+    __syncthreads();
+    for (int jj = 0; jj < 2; ++jj) {
+      const int oc = sub * 2 + jj, ch = c0 + oc;
+      if (ch >= nout || !live) continue;
+      float acc = 0.f;
+      for (int cc = 0; cc < C; ++cc) acc = fmaf(xs[r][cc], ws[oc][cc], acc);
+      if (ch < 3 * HD) {
+        const int part = ch / HD, hd = ch % HD, hh = hd / D, d = hd % D;
+        float* dst = part == 0 ? qo : (part == 1 ? ko : vo);
+        dst[(((b * N + i) * H + hh) * N + j) * D + d] = acc;
+      } else if (ch < 4 * HD) {
+        go[((b * N + i) * N + j) * HD + (ch - 3 * HD)] = acc;
+      } else {
+        bo[((b * H + (ch - 4 * HD)) * N + i) * N + j] = acc;
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) triattn_epilogue_f32(const float* __restrict__ o, const float* __restrict__ gt, const float* __restrict__ w_o,
+                                                            int C, int H, int D, float* zout, int64_t N, int ending, int residual) {
+  __shared__ float xs[PF_R][PF_CM + 1];
+  __shared__ float ws[PF_CC][PF_CM + 1];
+  const int tid = threadIdx.x;
+  const int64_t tpr = cdiv(N, PF_R);
+  const int64_t i = blockIdx.x / tpr, j0 = (blockIdx.x % tpr) * PF_R;
+  const int64_t b = blockIdx.y;
+  const int HD = H * D;
+  for (int c = tid; c < PF_R * HD; c += 256) {
+    const int r = c / HD, hd = c % HD, hh = hd / D, d = hd % D;
+    const int64_t j = j0 + r;
+    const bool live = i < N && j < N;
+    float v = 0.f;
+    if (live) {
+      const float gg = gt[((b * N + i) * N + j) * HD + hd];
+      v = sigmoid_exact(gg) * o[(((b * N + i) * H + hh) * N + j) * D + d];
+    }
+    xs[r][hd] = v;
+  }
+  const int r = tid >> 3, sub = tid & 7;
+  const int64_t j = j0 + r;
+  const bool live = i < N && j < N;
+  const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
+  for (int c0 = 0; c0 < C; c0 += PF_CC) {
+    __syncthreads();
+    for (int c = tid; c < PF_CC * HD; c += 256) {
+      const int jj = c / HD, hd = c % HD;
+      ws[jj][hd] = c0 + jj < C ? w_o[(int64_t)(c0 + jj) * HD + hd] : 0.f;
+    }
+    __syncthreads();
+    for (int jj = 0; jj < 2; ++jj) {
+      const int co = c0 + sub * 2 + jj;
+      if (co >= C || !live) continue;
+      float acc = 0.f;
+      for (int hd = 0; hd < HD; ++hd) acc = fmaf(xs[r][hd], ws[sub * 2 + jj][hd], acc);
+      float* p = zout + zpix * C + co;
+      *p = residual ? *p + acc : acc;
+    }
+  }
+}
+
+static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen) {
+  if (a->dtype == FPF_DT_BF16) {
+    if (a->D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 core serves head_dim 32 (got %lld)", (long long)a->D);
+    CoreParams p{};
+    p.q = (const uint16_t*)a->q;
+    p.k = (const uint16_t*)a->k;
+    p.v = (const uint16_t*)a->v;
+    for (int t = 0; t < 5; ++t) {
+      p.qs[t] = a->q_stride[t];
+      p.ks[t] = a->k_stride[t];
+      p.vs[t] = a->v_stride[t];
+      p.os[t] = a->out_stride[t];
+    }
+    for (int t = 0; t < 4; ++t) p.bs[t] = a->bias_stride[t];
+    for (int t = 0; t < 3; ++t) p.ms[t] = a->mask_stride[t];
+    p.bias = a->bias;
+    p.bias_bf16 = a->bias_dtype == FPF_DT_BF16;
+    p.mask = a->mask;
+    p.mask_f32 = a->mask_dtype == FPF_DT_F32;
+    p.out = (uint16_t*)a->out;
+    p.B = a->B;
+    p.N = a->N;
+    p.H = a->H;
+    p.S = a->S;
+    p.scale = a->scale;
+    for (int t = 0; t < 4; ++t)
+      if ((p.qs[t] | p.ks[t] | p.vs[t]) & 7) return fail(err, errlen, FPF_E_ALIGN, "bf16 core: q / k / v strides must be multiples of 8 elements");
+    for (int t = 0; t < 4; ++t)
+      if (p.os[t] & 3) return fail(err, errlen, FPF_E_ALIGN, "bf16 core: out strides must be multiples of 4 elements");
+    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || (reinterpret_cast<uintptr_t>(a->out) & 7))
+      return fail(err, errlen, FPF_E_ALIGN, "bf16 core: q / k / v 16-byte, out 8-byte aligned");
+    const int64_t total = a->B * a->H * cdiv(a->N, TA_R) * cdiv(a->S, 128);
+    if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
+    hipLaunchKernelGGL(triattn_core_bf16, dim3((unsigned)(cdiv(total, 8) * 8)), dim3(256), 0, st, p);
+    return launched(err, errlen, "triattn_core_bf16");
+  }
+  if (a->dtype == FPF_DT_F32) {
+    CoreParamsF p{};
+    p.q = (const float*)a->q;
+    p.k = (const float*)a->k;
+    p.v = (const float*)a->v;
+    for (int t = 0; t < 5; ++t) {
+      p.qs[t] = a->q_stride[t];
+      p.ks[t] = a->k_stride[t];
+      p.vs[t] = a->v_stride[t];
+      p.os[t] = a->out_stride[t];
+    }
+    for (int t = 0; t < 4; ++t) p.bs[t] = a->bias_stride[t];
+    for (int t = 0; t < 3; ++t) p.ms[t] = a->mask_stride[t];
+    p.bias = a->bias;
+    p.bias_bf16 = a->bias_dtype == FPF_DT_BF16;
+    p.mask = a->mask;
+    p.mask_f32 = a->mask_dtype == FPF_DT_F32;
+    p.out = (float*)a->out;
+    p.B = a->B;
+    p.N = a->N;
+    p.H = a->H;
+    p.S = a->S;
+    p.scale = a->scale;
+    const int64_t blocks = a->B * a->N * a->H * cdiv(a->S, TF_QT);
+    if (blocks > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
+#define FPF_TF(DD)                                                                                       \
+  if (a->D == DD) {                                                                                      \
+    hipLaunchKernelGGL(triattn_core_f32<DD>, dim3((unsigned)blocks), dim3(TF_QT), 0, st, p);             \
+    return launched(err, errlen, "triattn_core_f32");                                                    \
+  }
+    FPF_TF(16) FPF_TF(32) FPF_TF(64)
+#undef FPF_TF
+    return fail(err, errlen, FPF_E_SHAPE, "fp32 core serves head_dim 16 | 32 | 64 (got %lld)", (long long)a->D);
+  }
+  return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);
+}
+
+}  // namespace fpf
+
+extern "C" int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->q || !a->k || !a->v || !a->bias || !a->out) return fail(err, errlen, FPF_E_ARGS, "q / k / v / bias / out is NULL");
+  if (a->B < 0 || a->N < 0 || a->H <= 0 || a->S < 0 || a->D <= 0) return fail(err, errlen, FPF_E_SHAPE, "negative extent");
+  if (a->B == 0 || a->N == 0 || a->S == 0) return FPF_OK;
+  if (a->q_stride[4] != 1 || a->k_stride[4] != 1 || a->v_stride[4] != 1 || a->out_stride[4] != 1 || a->bias_stride[3] != 1)
+    return fail(err, errlen, FPF_E_SHAPE, "the last (head_dim / key) strides must be 1");
+  if (!(a->bias_dtype == FPF_DT_F32 || a->bias_dtype == FPF_DT_BF16)) return fail(err, errlen, FPF_E_DTYPE, "bias_dtype %d", a->bias_dtype);
+  if (a->mask && !(a->mask_dtype == FPF_DT_U8 || a->mask_dtype == FPF_DT_F32)) return fail(err, errlen, FPF_E_DTYPE, "mask_dtype %d", a->mask_dtype);
+  if (!(a->scale > 0.f)) return fail(err, errlen, FPF_E_ARGS, "scale must be > 0");
+  return core_launch(a, static_cast<hipStream_t>(stream), err, errlen);
+}
+
+extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int32_t C, int32_t H, int32_t D, int32_t dtype) {
+  (void)C;
+  const size_t elt = dtype == FPF_DT_F32 ? 4 : 2;
+  const size_t pix = (size_t)B * (size_t)N * (size_t)N;
+  const size_t HD = (size_t)H * (size_t)D;
+  // q, k, v, o, g (HD per pixel each) + bias (H fp32 per pixel), each region 256-byte aligned
+  const size_t r1 = (pix * HD * elt + 255) & ~(size_t)255;
+  const size_t r2 = (pix * (size_t)H * 4 + 255) & ~(size_t)255;
+  return 5 * r1 + r2;
+}
+
+extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->z || !a->w_qkvg || !a->w_b || !a->w_o || !a->out) return fail(err, errlen, FPF_E_ARGS, "z / weights / out is NULL");
+  if (a->B <= 0 || a->N <= 0) return a->B == 0 || a->N == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "negative extent");
+  if (a->residual && a->out != a->z) return fail(err, errlen, FPF_E_ARGS, "residual form updates z in place: out must be z");
+  if (a->mask && !(a->mask_dtype == FPF_DT_U8 || a->mask_dtype == FPF_DT_F32)) return fail(err, errlen, FPF_E_DTYPE, "mask_dtype %d", a->mask_dtype);
+  const size_t need = fpf_triattn_block_workspace_bytes(a->B, a->N, a->C, a->H, a->D, a->dtype);
+  if (!a->workspace || a->workspace_bytes < need) return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
+  if (a->B > 65535) return fail(err, errlen, FPF_E_SHAPE, "B above 65535");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t B = a->B, N = a->N, H = a->H, D = a->D, HD = H * D;
+  const size_t elt = a->dtype == FPF_DT_F32 ? 4 : 2;
+  const size_t pix = (size_t)B * N * N;
+  const size_t r1 = (pix * HD * elt + 255) & ~(size_t)255;
+  char* w = static_cast<char*>(a->workspace);
+  void *q = w, *k = w + r1, *v = w + 2 * r1, *o = w + 3 * r1, *g = w + 4 * r1;
+  float* bias = reinterpret_cast<float*>(w + 5 * r1);
+  const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)D);
+  FpfTriattnArgs c{};
+  c.abi_version = FPF_ABI_VERSION;
+  c.dtype = a->dtype;
+  c.B = B;
+  c.N = N;
+  c.H = H;
+  c.S = N;
+  c.D = D;
+  c.q = q;
+  c.k = k;
+  c.v = v;
+  const int64_t st5[5] = {N * H * N * D, H * N * D, N * D, D, 1};
+  for (int t = 0; t < 5; ++t) c.q_stride[t] = c.k_stride[t] = c.v_stride[t] = c.out_stride[t] = st5[t];
+  c.bias = bias;
+  c.bias_dtype = FPF_DT_F32;
+  c.bias_stride[0] = H * N * N;
+  c.bias_stride[1] = N * N;
+  c.bias_stride[2] = N;
+  c.bias_stride[3] = 1;
+  c.mask = a->mask;
+  c.mask_dtype = a->mask_dtype;
+  c.mask_stride[0] = N * N;                      // key mask of attention row i: z-frame pair mask row i (starting) / column i (ending)
+  c.mask_stride[1] = a->ending ? 1 : N;
+  c.mask_stride[2] = a->ending ? N : 1;
+  c.out = o;
+  c.scale = scale;
+  if (a->dtype == FPF_DT_BF16) {
+    if (a->C != TP_C || HD != TP_HD || D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 block serves C = 128, H*D = 128, D = 32");
+    if (!aligned16(a->z) || !aligned16(a->out) || !aligned16(a->workspace) || !aligned16(a->w_qkvg) || !aligned16(a->w_b) || !aligned16(a->w_o))
+      return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
+    const unsigned grid = (unsigned)(N * cdiv(N, 32) / 4 + ((N * cdiv(N, 32)) % 4 ? 1 : 0));
+    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid, (unsigned)B), dim3(256), 0, st, (const uint16_t*)a->z, a->ln_w, a->ln_b, a->eps,
+                       (const uint16_t*)a->w_qkvg, (const uint16_t*)a->w_b, (int)H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N,
+                       a->ending);
+    int rc = launched(err, errlen, "triattn_prologue_bf16");
+    if (rc) return rc;
+    rc = core_launch(&c, st, err, errlen);
+    if (rc) return rc;
+    hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(grid, (unsigned)B), dim3(256), 0, st, (const uint16_t*)o, (const uint16_t*)g,
+                       (const uint16_t*)a->w_o, (int)H, (uint16_t*)a->out, N, a->ending, a->residual);
+    return launched(err, errlen, "triattn_epilogue_bf16");
+  }
+  if (a->dtype == FPF_DT_F32) {
+    if (a->C > PF_CM || HD > PF_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 block serves C, H*D <= 128");
+    const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
+    hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)a->z, a->ln_w, a->ln_b, a->eps,
+                       (const float*)a->w_qkvg, (const float*)a->w_b, a->C, (int)H, (int)D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N,
+                       a->ending);
+    int rc = launched(err, errlen, "triattn_prologue_f32");
+    if (rc) return rc;
+    rc = core_launch(&c, st, err, errlen);
+    if (rc) return rc;
+    hipLaunchKernelGGL(triattn_epilogue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)o, (const float*)g, (const float*)a->w_o,
+                       a->C, (int)H, (int)D, (float*)a->out, N, a->ending, a->residual);
+    return launched(err, errlen, "triattn_epilogue_f32");
+  }
+  return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);
+}

@@ -1,0 +1,164 @@
+"""The pair track's fused block faces over libfpf_hip: the triangle-attention block (prologue -> core -> epilogue in three
+launches, ``fpf_triattn_block_fwd``) and the fused SwiGLU transition.
+
+Mirrors common/opt_core/opt_core/attn/pair_fused.py: ``Unsupported`` (:86), ``pack_triattn_weights`` (:679),
+``pack_transition_weights`` (:744), ``tri_attn_block(z, W, mask=None, *, ending, residual, ...)`` (:1500) and
+``transition(x, T, *, residual, out, mask, ...)`` (:1519).
+
+Frames: z is the pair tensor [B,N,N,C] (or [N,N,C]) in its OWN frame.  ``ending=True`` attends in the transposed frame
+x = z^T: the prologue reads z^T by address (no copy) and the epilogue writes the update back untransposed.  With
+``residual=True`` z is updated in place and returned; otherwise the update in z's frame is returned.
+"""
+import torch
+
+from .. import _face as F
+from .. import _lib as L
+from ..kernels import transition as _TR
+
+TRIATTN_KEYS = ("ln_w", "ln_b", "w_q", "w_k", "w_v", "w_g", "b_g", "w_b", "w_o", "b_o")
+TRANSITION_KEYS = ("ln_w", "ln_b", "w_a", "w_b", "w_out")
+
+
+class Unsupported(Exception):
+    """A named refusal, raised before any kernel launch.  ``reason`` is the short token a kit's ledger carries."""
+
+    def __init__(self, reason, detail=""):
+        Exception.__init__(self, reason + (": " + detail if detail else ""))
+        self.reason = reason
+        self.detail = detail
+
+
+class TriAttnWeights(object):
+    """Packed triangle-attention weights: w_qkvg [4HD, C] (rows q|k|v|g), w_b [H, C], w_o [C_out, HD], LN in fp32, per dtype."""
+
+    def __init__(self):
+        self._packs = {}
+        self._ws = {}
+
+
+def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=None, w_k=None, w_v=None, w_g=None, w_b=None, w_qkvg=None,
+                         qkvg_split=("q", "k", "v", "g"), b_g=None, b_o=None, eps=1e-5, device=None):
+    H, D = int(n_heads), int(head_dim)
+    HD = H * D
+    if w_qkvg is not None:
+        if int(w_qkvg.shape[0]) != 4 * HD:
+            raise Unsupported("w_qkvg-shape", str(tuple(w_qkvg.shape)))
+        blocks = {nm: w_qkvg[i * HD:(i + 1) * HD] for i, nm in enumerate(qkvg_split)}
+        w_q, w_k, w_v, w_g = blocks["q"], blocks["k"], blocks["v"], blocks["g"]
+    if w_g is None:
+        raise Unsupported("gate:none")
+    if w_b is None:
+        raise Unsupported("bias:none")
+    if b_g is not None or b_o is not None:
+        raise Unsupported("projection_bias", "the HIP block has no gate / output projection bias operand")
+    for nm, t in (("w_q", w_q), ("w_k", w_k), ("w_v", w_v), ("w_g", w_g)):
+        if t is None or t.dim() != 2 or int(t.shape[0]) != HD:
+            raise Unsupported(nm + "-shape", str(None if t is None else tuple(t.shape)))
+    C = int(w_q.shape[1])
+    if tuple(w_b.shape) != (H, C):
+        raise Unsupported("w_b-shape", str(tuple(w_b.shape)))
+    if w_o.dim() != 2 or int(w_o.shape[1]) != HD:
+        raise Unsupported("w_o-shape", str(tuple(w_o.shape)))
+    W = TriAttnWeights()
+    dev = device if device is not None else w_o.device
+    W.C, W.H, W.D, W.C_out, W.eps, W.dev = C, H, D, int(w_o.shape[0]), float(eps), dev
+    with torch.no_grad():
+        W.wqkvg = torch.cat([w_q, w_k, w_v, w_g], 0).detach().to(dev)
+        W.wb = w_b.detach().to(dev)
+        W.wo = w_o.detach().to(dev)
+        W.ln_w = None if ln_w is None else ln_w.detach().to(dev).float().contiguous()
+        W.ln_b = None if ln_b is None else ln_b.detach().to(dev).float().contiguous()
+    W.shapes = "c%dh%dd%do%d" % (C, H, D, W.C_out)
+    return W
+
+
+def _wpack(W, dtype, device):
+    key = (str(device), dtype)
+    p = W._packs.get(key)
+    if p is None:
+        with torch.no_grad():
+            p = W._packs[key] = tuple(t.to(device=device, dtype=dtype).contiguous() for t in (W.wqkvg, W.wb, W.wo))
+    return p
+
+
+def _pair_mask(mask, z4):
+    if mask is None:
+        return None, L.DT_U8
+    B, N = z4.shape[0], z4.shape[1]
+    m = mask if mask.dim() == 3 else mask.unsqueeze(0)
+    if tuple(m.shape) != (B, N, N):
+        raise Unsupported("mask-shape", str(tuple(mask.shape)))
+    if m.dtype == torch.bool:
+        return m.contiguous().view(torch.uint8), L.DT_U8
+    if m.dtype == torch.float32:
+        return m.contiguous(), L.DT_F32
+    return (m != 0).contiguous().view(torch.uint8), L.DT_U8
+
+
+def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None, word="fast", **_unused):
+    """The fused block; returns the update in z's frame (residual=False) or z updated in place (residual=True)."""
+    z4 = z if z.dim() == 4 else z.unsqueeze(0)
+    if z4.dim() != 4 or z4.shape[1] != z4.shape[2] or z4.shape[-1] != W.C:
+        raise Unsupported("shape", str(tuple(z.shape)))
+    if not z4.is_contiguous():
+        raise Unsupported("stride", "z must be contiguous")
+    try:
+        sel = F.resolve(word, F.dtype_word(z.dtype), F.device_word(z), "pair_fused:tri_attn_block", cell="block:%s" % W.shapes)
+    except F.Refusal as e:
+        raise Unsupported(e.kind, e.detail) from None
+    if sel.row == F.ROW_FAST and (W.C, W.H * W.D, W.D, W.C_out) != (128, 128, 32, 128):
+        raise Unsupported("shape:%s" % W.shapes, "the bf16 block serves C = 128, H*D = 128, D = 32")
+    if sel.row == F.ROW_F32 and (W.C > 128 or W.H * W.D > 128 or W.D not in (16, 32, 64) or W.C_out != W.C):
+        raise Unsupported("shape:%s" % W.shapes, "the fp32 block serves C, H*D <= 128, D 16 | 32 | 64")
+    B, N = int(z4.shape[0]), int(z4.shape[1])
+    m, mdt = _pair_mask(mask, z4)
+    wqkvg, wb, wo = _wpack(W, z.dtype, z.device)
+    dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
+    need = L.lib().fpf_triattn_block_workspace_bytes(B, N, W.C, W.H, W.D, dt)
+    wkey = str(z.device)
+    ws = W._ws.get(wkey)
+    if ws is None or ws.numel() < need:
+        ws = W._ws[wkey] = torch.empty(need, dtype=torch.uint8, device=z.device)
+    out = z4 if residual else torch.empty_like(z4)
+    a = L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=dt, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m), mask_dtype=mdt,
+                           ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), w_o=L.ptr(wo),
+                           ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out), scale=float(scale or 0.0),
+                           workspace=L.ptr(ws), workspace_bytes=ws.numel())
+    try:
+        L.call("fpf_triattn_block_fwd", a, L.stream_ptr(z.device))
+    except L.LibError as e:
+        raise Unsupported("lib:" + e.kind, e.msg) from None
+    if residual:
+        return z
+    return out if z.dim() == 4 else out[0]
+
+
+class TransitionWeights(object):
+    """The pair_fused transition pack: C, NH (hidden), n = NH / C, and the kernels.transition.Weights it serves through."""
+
+    def __init__(self, weights):
+        self.W = weights
+        self.C, self.NH = weights.c, weights.hidden
+        self.n = self.NH // self.C
+
+
+def pack_transition_weights(*, w_out, ln_w=None, ln_b=None, w_a=None, w_b=None, w_ab=None, ab_split=("a", "b"), eps=1e-5, device=None):
+    C, NH = int(w_out.shape[0]), int(w_out.shape[1])
+    if w_ab is not None:
+        if tuple(w_ab.shape) != (2 * NH, C):
+            raise Unsupported("w_ab-shape", str(tuple(w_ab.shape)))
+        blocks = {nm: w_ab[i * NH:(i + 1) * NH] for i, nm in enumerate(ab_split)}
+        w_a, w_b = blocks["a"], blocks["b"]
+    for nm, t in (("w_a", w_a), ("w_b", w_b)):
+        if t is None or tuple(t.shape) != (NH, C):
+            raise Unsupported(nm + "-shape", str(None if t is None else tuple(t.shape)))
+    return TransitionWeights(_TR.pack(w_o=w_out, w_a=w_a, w_b=w_b, ln_w=ln_w, ln_b=ln_b, eps=eps, device=device))
+
+
+def transition(x, T, *, residual=False, out=None, mask=None, word="fast", **_unused):
+    """y = W_out(silu(W_a n) * W_b n), n = LN(x) in-kernel; x + y when residual; ``out`` may be x (in place)."""
+    try:
+        y, _sel = _TR.transition(x, T.W, word=word, residual=residual, mask=mask, out=out)
+    except F.Refusal as e:
+        raise Unsupported(e.kind, e.detail) from None
+    return y
