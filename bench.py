@@ -1,0 +1,169 @@
+#!/usr/bin/env python3
+"""bench.py -- one Pairformer pair block (the hot path) on one MI355X: ms, TFLOP/s and fraction of the bf16 MFMA roofline.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--n 768] [--no-cpu]
+
+Step = one pair block on a resident z [1, N, N, 128] bf16, in place, in the reference order (trimul outgoing, trimul incoming,
+tri-att starting node, tri-att ending node, transition 4x): 13 launches of libfpf_hip on torch's current stream.  Synthetic
+z ~ N(0,1) and random-init weights N(0, 1/fan_in) (seed 0), pair mask all ones, inputs resident in HBM before timing.
+Prints ONE JSON line (the driver's contract) with the dominant kernel's roofline (timed live with HIP events on the launch
+stream) and the stock PyTorch CPU statement timed on this host (a reported baseline, not the target).
+"""
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "uplifting-biomolecular-modeling_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0        # MI355X dense bf16 MFMA (AMD datasheet, no sparsity)
+PEAK_HBM_GBS = 8000.0            # MI355X HBM3E
+
+
+def block_flops(N, C=128, CH=128, H=4, D=32, factor=4):
+    """Algorithmic FLOPs (2 per multiply-add) per site of one pair block."""
+    HD = H * D
+    tm = 2 * N * N * (4 * C * CH + C * C + CH * C) + 2 * N ** 3 * CH
+    ta_core = 4 * N ** 3 * HD
+    ta = 2 * N * N * C * (4 * HD + H) + ta_core + 2 * N * N * HD * C
+    tr = 2 * N * N * 3 * factor * C * C
+    return {"trimul": tm, "triatt": ta, "triatt_core": ta_core, "transition": tr, "block": 2 * tm + 2 * ta + tr}
+
+
+def time_events(fn, reps, torch):
+    """Mean ms per call of fn() over reps calls, bracketed by HIP events on the current stream."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def cpu_baseline(torch):
+    """The stock PyTorch statements (restated in oracle/stock.py) timed on this host: one BASELINE config-1 block
+    (N = 64, c_z = 128, 4 x 32 heads, transition 4x, fp32), 2 warm-ups then the median of 5."""
+    sys.path.insert(0, ROOT)
+    from oracle import stock as S
+    cores = torch.get_num_threads()
+    P = S.make_block_params(c_z=128, heads=4, head_dim=32, seed=0)
+    z = torch.randn(1, 64, 64, 128, generator=torch.Generator().manual_seed(0))
+    mask = torch.ones(1, 64, 64)
+    ts = []
+    for it in range(7):
+        t0 = time.perf_counter()
+        S.pair_block(z, mask, P, dtype=torch.float32)
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts[2:])
+    fl = block_flops(64)["block"]
+    return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": "BASELINE config 1: one pair block N=64 c_z=128 fp32 (stock statements, oracle/stock.py), median of 5 after 2 "
+                      "warm-ups; %.1f ms per block, %.2f GFLOP" % (med * 1e3, fl / 1e9)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--n", type=int, default=768)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py measures one GPU: this build runs the pair stack on a single MI355X (multi-GPU row sharding is a design "
+              "note, not built); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import triattn as TA
+    from fpf_hip.kernels import ln as LN
+
+    dev = torch.device("cuda:0")
+    N = a.n
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(dev)
+    mask = torch.ones(1, N, N, device=dev)
+    blk = PFM.PairBlock(PFM.random_params(seed=0), dev, torch.bfloat16)
+    fl = block_flops(N)
+
+    for _ in range(a.warmup):
+        PFM.pair_block(z, mask, blk)
+    torch.cuda.synchronize()
+    z.normal_()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(a.steps):
+        PFM.pair_block(z, mask, blk)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / a.steps
+    tflops = fl["block"] / (ms * 1e-3) / 1e12
+
+    # per-site breakdown (each site alone, same resident z)
+    from fpf_hip.attn import pair_fused as PF
+    from fpf_hip.kernels import transition as TR
+    from fpf_hip.kernels import trimul as TM
+    reps = max(3, a.steps // 2)
+    zb = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(dev)
+    sites = {
+        "trimul_out": (lambda: TM.triangle_multiplication(zb, mask, direction="outgoing", weights=blk.tmo, word="fast", residual=True,
+                                                          cache=blk.cache_o, out=zb), fl["trimul"]),
+        "trimul_in": (lambda: TM.triangle_multiplication(zb, mask, direction="incoming", weights=blk.tmi, word="fast", residual=True,
+                                                         cache=blk.cache_i, out=zb), fl["trimul"]),
+        "triatt_start": (lambda: PF.tri_attn_block(zb, blk.ta["tas"], mask, ending=False, residual=True), fl["triatt"]),
+        "triatt_end": (lambda: PF.tri_attn_block(zb, blk.ta["tae"], mask, ending=True, residual=True), fl["triatt"]),
+        "transition": (lambda: TR.transition(zb, blk.tr, word="fast", residual=True, out=zb), fl["transition"]),
+    }
+    breakdown = {}
+    for name, (fn, f) in sites.items():
+        fn()
+        t = time_events(fn, reps, torch)
+        breakdown[name] = {"ms": round(t, 4), "tflops": round(f / (t * 1e-3) / 1e12, 1), "mfma_frac": round(f / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    zbytes = N * N * 128 * 2
+    breakdown["transition"]["hbm_gbs_min_bytes"] = round(2 * zbytes / (breakdown["transition"]["ms"] * 1e-3) / 1e9, 1)
+    # standalone LayerNorm (HBM-bound): z in, bf16 out
+    yln = torch.empty_like(zb)
+    lw, lb = torch.ones(128, device=dev), torch.zeros(128, device=dev)
+    t_ln = time_events(lambda: LN.layer_norm(zb, (128,), lw, lb, 1e-5, word="fast", out=yln), reps, torch)
+    breakdown["layernorm"] = {"ms": round(t_ln, 4), "hbm_gbs": round(2 * zbytes / (t_ln * 1e-3) / 1e9, 1),
+                              "hbm_frac": round(2 * zbytes / (t_ln * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+    # dominant kernel: the triangle-attention core at the block's shape (q/k/v [1,N,4,N,32] bf16, bias fp32, mask ones)
+    q, k, v = (torch.randn(1, N, 4, N, 32, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+    bias = (torch.randn(1, 1, 4, N, N, generator=g) * 0.5).to(dev)
+    kmask = torch.ones(1, N, 1, 1, N, dtype=torch.bool, device=dev)
+    o = torch.empty_like(q)
+    core = lambda: TA.triangle_attention(q, k, v, bias, kmask, word="fast", out=o)
+    core()
+    t_core = time_events(core, reps, torch)
+    ach = fl["triatt_core"] / (t_core * 1e-3) / 1e12
+    traffic = None
+    tp = os.path.join(ROOT, "profiles", "traffic_triattn_core_n%d.json" % N)
+    if os.path.exists(tp):
+        with open(tp) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    roof = {"kernel": "triattn_core_bf16", "bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "ms_per_launch": round(t_core, 4),
+            "flops_per_launch": fl["triatt_core"]}
+
+    out = {"metric": "Pairformer block ms + TFLOP/s (% bf16 MFMA peak) at N=768 c_z=128, 1 GPU", "value": round(tflops, 2),
+           "unit": "TFLOP/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": "one pair block (trimul out, trimul in, tri-att start, tri-att end, transition 4x), in place", "N": N,
+                      "c_z": 128, "c_hidden": 128, "heads": 4, "head_dim": 32, "batch": 1, "mask": "all ones",
+                      "block_tflop": round(fl["block"] / 1e12, 4), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
+           "roofline": roof, "breakdown": breakdown}
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

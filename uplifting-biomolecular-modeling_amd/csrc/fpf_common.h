@@ -39,7 +39,16 @@ __device__ __forceinline__ bf16x8 as_bf8(const u32x4& u) { return __builtin_bit_
 __device__ __forceinline__ int c_row(int v, int g) { return 8 * (v >> 2) + 4 * g + (v & 3); }   // D-layout row of register v
 
 // ---------------------------------------------------------------------------------------------------------------- misc device
-__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, 64); }
+// Cross-half reductions of a wave64 (lanes l and l ^ 32) with v_permlane32_swap: after swapping x with itself, the two
+// results hold {x[0..31], x[0..31]} and {x[32..63], x[32..63]}, so their sum / max is the pair's in every lane.
+__device__ __forceinline__ float half_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float half_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float sigmoid_exact(float x) { return 1.0f / (1.0f + expf(-x)); }

@@ -16,19 +16,22 @@ namespace fpf {
 
 constexpr int TA_D = 32;
 constexpr int TA_R = 4;          // pair rows per workgroup sharing the bias tile
-constexpr int TA_KT = 32;        // keys per tile
+constexpr int TA_KT = 64;        // keys per staged tile (two MFMA sub-tiles of 32)
 constexpr int TA_KLD = 40;       // LDS pitch (bf16) of a K row: 80 B, conflict-free 16-byte reads
-constexpr int TA_VLD = 36;       // LDS pitch (bf16) of a V^T row: 72 B, conflict-free 8-byte reads
+constexpr int TA_VLD = 68;       // LDS pitch (bf16) of a V^T row: 136 B, conflict-free 8-byte reads
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr float TA_HEADROOM = 8.0f;   // log2 units the running max may lag the true one before O and l are rescaled
 static_assert(TA_R == 4, "one wave computes the keep bits of one staged row");
 
 struct CoreParams {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
-  int64_t qs[5], ks[5], vs[5];
+  int64_t qs[5], ks[5], vs[5];   // v_t = 0: vs = [b, n, h, key, d] strides; v_t = 1: [b, n, h, d, key] (V stored transposed)
+  int v_t;
   const void* bias;
   int bias_bf16;
+  int bias_vec;                  // fp32 bias whose rows start 16-byte aligned: float4 loads
   int64_t bs[4];
   const void* mask;
   int mask_f32;
@@ -49,13 +52,22 @@ __device__ __forceinline__ float bias_at(const CoreParams& p, int64_t off) {
   return p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[off]) : static_cast<const float*>(p.bias)[off];
 }
 
+// S^T tile of one pair row: keys of sub-tile `sub` (A = K rows from LDS) x this wave's 32 queries (B = Q^T), accumulated onto
+// the bias tile.
+__device__ __forceinline__ f32x16 qk_tile(const uint16_t* __restrict__ kr, int sub, int n, int g, const bf16x8 (&qf)[2], const f32x16& bt) {
+  const uint16_t* row = kr + (32 * sub + n) * TA_KLD + 8 * g;
+  f32x16 s = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(row)), qf[0], bt);
+  return mfma32(as_bf8(*reinterpret_cast<const u32x4*>(row + 16)), qf[1], s);
+}
+
+template <bool VT>
 __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_R][TA_KT * TA_KLD];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_R][TA_D * TA_VLD];
-  __shared__ uint32_t sKeep[TA_R];
+  __shared__ uint64_t sKeep[TA_R];
   __shared__ int sAlive[TA_R];
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
-  // logical work order (b h) -> row group -> query tile; dealt to the 8 XCDs in contiguous runs
+  // logical work order (b h) -> row group -> query tile, dealt to the 8 XCDs in contiguous runs
   const int64_t nq = cdiv(p.S, 128), nr = cdiv(p.N, TA_R);
   const int64_t total = p.B * p.H * nr * nq;
   const int64_t per = (total + 7) / 8;
@@ -66,10 +78,10 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
   const int64_t i0 = rg * TA_R;
   const int64_t q = qt * 128 + wave * 32 + n;          // this lane's query
   const bool qlive = q < p.S;
-  const float c2 = p.scale * LOG2E;                     // logits in qk units -> log2 units
+  const float c2 = p.scale * LOG2E;                     // qk units -> log2 units
   const float inv_scale = 1.0f / p.scale;
 
-  // row liveness (a row with no kept key is "dead": uniform over all keys)
+  // row liveness: a row with no kept key is "dead" and attends uniformly to every key
   if (tid < TA_R) sAlive[tid] = 0;
   __syncthreads();
   for (int r = 0; r < TA_R; ++r) {
@@ -81,8 +93,12 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
   }
   __syncthreads();
   bool dead[TA_R];
+  bool dead_any = false;
 #pragma unroll
-  for (int r = 0; r < TA_R; ++r) dead[r] = (i0 + r < p.N) && !sAlive[r];
+  for (int r = 0; r < TA_R; ++r) {
+    dead[r] = (i0 + r < p.N) && !sAlive[r];
+    dead_any |= dead[r];
+  }
 
   // Q fragments (B operand of S^T = K Q^T): query n, d = 16t + 8g .. +7
   bf16x8 qf[TA_R][2];
@@ -95,7 +111,7 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
     for (int t = 0; t < 2; ++t) qf[r][t] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16 * t + 8 * g) : u32x4{0, 0, 0, 0});
   }
   f32x16 o[TA_R];
-  float mrow[TA_R], lrow[TA_R];
+  float mrow[TA_R], lrow[TA_R];                         // running max (log2 units) and this lane's partial sum
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) {
     o[r] = f32x16{};
@@ -103,23 +119,40 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
     lrow[r] = 0.f;
   }
 
-  // staging map: 512 16-byte chunks per operand per tile, 2 per thread: row r, key kk, d-part
-  int sr[2], skk[2], sd[2];
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int c = tid + 256 * it;
-    sr[it] = c >> 7;
-    skk[it] = (c >> 2) & 31;
-    sd[it] = (c & 3) * 8;
-  }
-  u32x4 rk[2], rv[2];
+  // staging: 1024 16-byte chunks per operand per tile, 4 per thread
+  u32x4 rk[4], rv[4];
   auto gload = [&](int64_t k0) {
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int64_t i = i0 + sr[it], key = k0 + skk[it];
-      const bool ok = i < p.N && key < p.S;
-      rk[it] = ok ? *reinterpret_cast<const u32x4*>(p.k + b * p.ks[0] + i * p.ks[1] + h * p.ks[2] + key * p.ks[3] + sd[it]) : u32x4{0, 0, 0, 0};
-      rv[it] = ok ? *reinterpret_cast<const u32x4*>(p.v + b * p.vs[0] + i * p.vs[1] + h * p.vs[2] + key * p.vs[3] + sd[it]) : u32x4{0, 0, 0, 0};
+    for (int it = 0; it < 4; ++it) {
+      const int c = tid + 256 * it;
+      const int r = c >> 8;
+      const int64_t i = i0 + r;
+      {
+        const int kk = (c >> 2) & 63, part = c & 3;
+        const int64_t key = k0 + kk;
+        const bool ok = i < p.N && key < p.S;
+        rk[it] = ok ? *reinterpret_cast<const u32x4*>(p.k + b * p.ks[0] + i * p.ks[1] + h * p.ks[2] + key * p.ks[3] + 8 * part) : u32x4{0, 0, 0, 0};
+      }
+      if constexpr (VT) {
+        const int d = (c >> 3) & 31, kc = c & 7;
+        const int64_t key = k0 + 8 * kc;
+        const bool ok = i < p.N && key + 8 <= p.S;
+        const uint16_t* src = p.v + b * p.vs[0] + i * p.vs[1] + h * p.vs[2] + d * p.vs[3] + key;
+        if (ok) {
+          rv[it] = *reinterpret_cast<const u32x4*>(src);
+        } else {
+          uint16_t tmp[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) tmp[e] = (i < p.N && key + e < p.S) ? src[e] : (uint16_t)0;
+          rv[it] = u32x4{tmp[0] | ((uint32_t)tmp[1] << 16), tmp[2] | ((uint32_t)tmp[3] << 16), tmp[4] | ((uint32_t)tmp[5] << 16),
+                         tmp[6] | ((uint32_t)tmp[7] << 16)};
+        }
+      } else {
+        const int kk = (c >> 2) & 63, part = c & 3;
+        const int64_t key = k0 + kk;
+        const bool ok = i < p.N && key < p.S;
+        rv[it] = ok ? *reinterpret_cast<const u32x4*>(p.v + b * p.vs[0] + i * p.vs[1] + h * p.vs[2] + key * p.vs[3] + 8 * part) : u32x4{0, 0, 0, 0};
+      }
     }
   };
   gload(0);
@@ -127,76 +160,119 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
   for (int64_t k0 = 0; k0 < p.S; k0 += TA_KT) {
     __syncthreads();
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      *reinterpret_cast<u32x4*>(&sK[sr[it]][skk[it] * TA_KLD + sd[it]]) = rk[it];
+    for (int it = 0; it < 4; ++it) {
+      const int c = tid + 256 * it;
+      const int r = c >> 8;
+      {
+        const int kk = (c >> 2) & 63, part = c & 3;
+        *reinterpret_cast<u32x4*>(&sK[r][kk * TA_KLD + 8 * part]) = rk[it];
+      }
+      if constexpr (VT) {
+        const int d = (c >> 3) & 31, kc = c & 7;
+        uint16_t* dst = &sV[r][d * TA_VLD + 8 * kc];
+        *reinterpret_cast<u32x2*>(dst) = u32x2{rv[it][0], rv[it][1]};
+        *reinterpret_cast<u32x2*>(dst + 4) = u32x2{rv[it][2], rv[it][3]};
+      } else {
+        const int kk = (c >> 2) & 63, part = c & 3;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sV[sr[it]][(sd[it] + 2 * e) * TA_VLD + skk[it]] = (uint16_t)(rv[it][e] & 0xffff);
-        sV[sr[it]][(sd[it] + 2 * e + 1) * TA_VLD + skk[it]] = (uint16_t)(rv[it][e] >> 16);
+        for (int e = 0; e < 4; ++e) {
+          sV[r][(8 * part + 2 * e) * TA_VLD + kk] = (uint16_t)(rv[it][e] & 0xffff);
+          sV[r][(8 * part + 2 * e + 1) * TA_VLD + kk] = (uint16_t)(rv[it][e] >> 16);
+        }
       }
     }
-    {   // keep bits of row `wave` for this tile (dead rows keep every in-range key)
-      const int64_t i = i0 + wave, key = k0 + n;
-      const bool dw = !sAlive[wave];
-      const bool keep = (l < 32) && key < p.S && i < p.N && (dw || mask_keep(p, b, i, key));
+    {   // keep bits of row `wave` for this tile: lane l <-> key k0 + l (dead rows keep every in-range key)
+      const int64_t i = i0 + wave, key = k0 + l;
+      const bool keep = key < p.S && i < p.N && (!sAlive[wave] || mask_keep(p, b, i, key));
       const uint64_t bal = __ballot(keep);
-      if (l == 0) sKeep[wave] = (uint32_t)bal;
+      if (l == 0) sKeep[wave] = bal;
     }
     __syncthreads();
     if (k0 + TA_KT < p.S) gload(k0 + TA_KT);
-    // bias tile (qk units) -> accumulator init; keys 8qd + 4g + 0..3
-    f32x16 bt;
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int64_t key = k0 + 8 * qd + 4 * g;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bt[4 * qd + e] = (qlive && key + e < p.S) ? bias_at(p, bias_row + (key + e) * p.bs[3]) * inv_scale : 0.f;
-    }
+    uint64_t kall = ~0ull, kany = 0;
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      const uint32_t kb = sKeep[r];
-      if (kb == 0) continue;                                  // nothing kept in this tile for row r
-      const uint16_t* kr = sK[r];
-      f32x16 s;
-      if (dead[r]) {
-        s = f32x16{};
+      kall &= sKeep[r];
+      kany |= sKeep[r];
+    }
+    if (kany == 0) continue;                              // no row keeps a key of this tile
+    const bool full = (kall == ~0ull) && !dead_any;       // uniform: no masking work in this tile
+#pragma unroll 1
+    for (int sub = 0; sub < 2; ++sub) {
+      // bias tile (qk units) as the accumulator's initial value: keys 32 sub + 8 qd + 4 g + 0..3
+      f32x16 bt;
+      const int64_t kb0 = k0 + 32 * sub + 4 * g;
+      if (p.bias_vec && qlive && k0 + TA_KT <= p.S) {
+        const float* bp = static_cast<const float*>(p.bias) + bias_row + kb0;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4 v4 = *reinterpret_cast<const f32x4*>(bp + 8 * qd);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bt[4 * qd + e] = v4[e] * inv_scale;
+        }
       } else {
-        s = bt;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) s = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&kr[n * TA_KLD + 16 * t + 8 * g])), qf[r][t], s);
+        for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t key = kb0 + 8 * qd + e;
+            bt[4 * qd + e] = (qlive && key < p.S) ? bias_at(p, bias_row + key * p.bs[3]) * inv_scale : 0.f;
+          }
       }
-      if (kb != 0xffffffffu) {
+      f32x16 s[TA_R];
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          if (!((kb >> c_row(v, g)) & 1u)) s[v] = -INFINITY;
+      for (int r = 0; r < TA_R; ++r) s[r] = qk_tile(sK[r], sub, n, g, qf[r], bt);
+      if (!full) {
+#pragma unroll
+        for (int r = 0; r < TA_R; ++r) {
+          const uint32_t kb = (uint32_t)(sKeep[r] >> (32 * sub));
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float sv = dead[r] ? 0.f : s[r][v];
+            s[r][v] = ((kb >> c_row(v, g)) & 1u) ? sv : -INFINITY;
+          }
+        }
       }
-      float mx = s[0];
+      float mx[TA_R];
+      bool need = false;
 #pragma unroll
-      for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);
-      mx = fmaxf(mx, xor32(mx));
-      const float mnew = fmaxf(mrow[r], mx);
-      const float alpha = fast_exp2((mrow[r] - mnew) * c2);
-      const float mc = mnew * c2;
-      float ps = 0.f;
-      uint32_t pk[8];
-#pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const float p0 = fast_exp2(fmaf(s[v], c2, -mc));
-        const float p1 = fast_exp2(fmaf(s[v + 1], c2, -mc));
-        ps += p0 + p1;
-        pk[v >> 1] = pack2(p0, p1);
+      for (int r = 0; r < TA_R; ++r) {
+        float m0 = fmaxf(fmaxf(fmaxf(s[r][0], s[r][1]), fmaxf(s[r][2], s[r][3])), fmaxf(fmaxf(s[r][4], s[r][5]), fmaxf(s[r][6], s[r][7])));
+        m0 = fmaxf(m0, fmaxf(fmaxf(fmaxf(s[r][8], s[r][9]), fmaxf(s[r][10], s[r][11])), fmaxf(fmaxf(s[r][12], s[r][13]), fmaxf(s[r][14], s[r][15]))));
+        mx[r] = half_max(m0) * c2;
+        need |= mx[r] > mrow[r] + TA_HEADROOM;
       }
-      lrow[r] = lrow[r] * alpha + ps;
-      mrow[r] = mnew;
+      if (__ballot(need) != 0) {       // some query's max moved past the headroom: move the running max of every row (exact)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
-      const uint16_t* vr = sV[r];
+        for (int r = 0; r < TA_R; ++r) {
+          const float mnew = fmaxf(mrow[r], mx[r]);
+          const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(mrow[r] - mnew);
+          lrow[r] *= alpha;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const uint16_t* vrow = &vr[n * TA_VLD + 16 * st + 4 * g];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-        o[r] = mfma32(as_bf8(u32x4{lo[0], lo[1], hi[0], hi[1]}), as_bf8(u32x4{pk[4 * st], pk[4 * st + 1], pk[4 * st + 2], pk[4 * st + 3]}), o[r]);
+          for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
+          mrow[r] = mnew;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < TA_R; ++r) {
+        const float mb = (mrow[r] == -INFINITY) ? 0.f : mrow[r];
+        float ps = 0.f;
+        uint32_t pk[8];
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const float p0 = fast_exp2(fmaf(s[r][v], c2, -mb));
+          const float p1 = fast_exp2(fmaf(s[r][v + 1], c2, -mb));
+          ps += p0 + p1;
+          pk[v >> 1] = pack2(p0, p1);
+        }
+        lrow[r] += ps;
+        const uint16_t* vr = sV[r] + n * TA_VLD + 32 * sub + 4 * g;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(vr + 16 * st);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 16 * st + 8);
+          o[r] = mfma32(as_bf8(u32x4{lo[0], lo[1], hi[0], hi[1]}), as_bf8(u32x4{pk[4 * st], pk[4 * st + 1], pk[4 * st + 2], pk[4 * st + 3]}), o[r]);
+        }
       }
     }
   }
@@ -205,7 +281,7 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
   for (int r = 0; r < TA_R; ++r) {
     const int64_t i = i0 + r;
     if (i >= p.N) continue;
-    const float lt = lrow[r] + xor32(lrow[r]);
+    const float lt = half_sum(lrow[r]);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
 #pragma unroll
@@ -353,7 +429,7 @@ __device__ __forceinline__ void ln128_load(const uint16_t* __restrict__ row, boo
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 64; ++i) s += xv[i];
-  s += xor32(s);
+  s = half_sum(s);
   const float mean = s * (1.0f / 128.0f);
   float qq = 0.f;
 #pragma unroll
@@ -361,7 +437,7 @@ __device__ __forceinline__ void ln128_load(const uint16_t* __restrict__ row, boo
     const float d = xv[i] - mean;
     qq += d * d;
   }
-  qq += xor32(qq);
+  qq = half_sum(qq);
   const float rstd = 1.0f / sqrtf(qq * (1.0f / 128.0f) + eps);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
@@ -413,8 +489,13 @@ __global__ void __launch_bounds__(256) triattn_prologue_bf16(const uint16_t* __r
     for (int t = 0; t < 8; ++t)
       acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&sW[blk & 1][n * TP_WLD + 64 * g + 8 * t])), xb[t], acc);
     if (!live) continue;
-    if (blk < 12) {
-      uint16_t* dst = blk < 4 ? qo : (blk < 8 ? ko : vo);
+    if (blk >= 8 && blk < 12) {               // v, written transposed: vT[b][i][h][d][j] (the core's V^T staging copies rows)
+      const int hh = blk & 3;
+      uint16_t* dst = vo + ((b * N + i) * H + hh) * (int64_t)D * N + j;
+#pragma unroll
+      for (int vv = 0; vv < 16; ++vv) dst[(int64_t)c_row(vv, g) * N] = f2bf(acc[vv]);
+    } else if (blk < 12) {
+      uint16_t* dst = blk < 4 ? qo : ko;
       const int cb = (blk & 3) * 32;      // channel base within q / k / v
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
@@ -632,18 +713,25 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     p.H = a->H;
     p.S = a->S;
     p.scale = a->scale;
+    p.v_t = a->v_layout;
+    if (!(p.v_t == 0 || p.v_t == 1)) return fail(err, errlen, FPF_E_ARGS, "v_layout %d", a->v_layout);
     for (int t = 0; t < 4; ++t)
       if ((p.qs[t] | p.ks[t] | p.vs[t]) & 7) return fail(err, errlen, FPF_E_ALIGN, "bf16 core: q / k / v strides must be multiples of 8 elements");
     for (int t = 0; t < 4; ++t)
       if (p.os[t] & 3) return fail(err, errlen, FPF_E_ALIGN, "bf16 core: out strides must be multiples of 4 elements");
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || (reinterpret_cast<uintptr_t>(a->out) & 7))
       return fail(err, errlen, FPF_E_ALIGN, "bf16 core: q / k / v 16-byte, out 8-byte aligned");
+    p.bias_vec = !p.bias_bf16 && aligned16(a->bias) && (p.bs[0] % 4 == 0) && (p.bs[1] % 4 == 0) && (p.bs[2] % 4 == 0);
     const int64_t total = a->B * a->H * cdiv(a->N, TA_R) * cdiv(a->S, 128);
     if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
-    hipLaunchKernelGGL(triattn_core_bf16, dim3((unsigned)(cdiv(total, 8) * 8)), dim3(256), 0, st, p);
+    if (p.v_t)
+      hipLaunchKernelGGL(triattn_core_bf16<true>, dim3((unsigned)(cdiv(total, 8) * 8)), dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL(triattn_core_bf16<false>, dim3((unsigned)(cdiv(total, 8) * 8)), dim3(256), 0, st, p);
     return launched(err, errlen, "triattn_core_bf16");
   }
   if (a->dtype == FPF_DT_F32) {
+    if (a->v_layout != 0) return fail(err, errlen, FPF_E_ARGS, "fp32 core takes v as [B, N, H, S, D] (v_layout 0)");
     CoreParamsF p{};
     p.q = (const float*)a->q;
     p.k = (const float*)a->k;
@@ -739,6 +827,11 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.v = v;
   const int64_t st5[5] = {N * H * N * D, H * N * D, N * D, D, 1};
   for (int t = 0; t < 5; ++t) c.q_stride[t] = c.k_stride[t] = c.v_stride[t] = c.out_stride[t] = st5[t];
+  if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, I, H, D, J]
+    c.v_layout = 1;
+    c.v_stride[3] = N;
+    c.v_stride[4] = 1;
+  }
   c.bias = bias;
   c.bias_dtype = FPF_DT_F32;
   c.bias_stride[0] = H * N * N;

@@ -20,7 +20,7 @@ __device__ __forceinline__ void ln128_from_regs(float (&xv)[64], int g, const fl
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 64; ++i) s += xv[i];
-  s += xor32(s);
+  s = half_sum(s);
   const float mean = s * (1.0f / 128.0f);
   float q = 0.f;
 #pragma unroll
@@ -28,7 +28,7 @@ __device__ __forceinline__ void ln128_from_regs(float (&xv)[64], int g, const fl
     const float d = xv[i] - mean;
     q += d * d;
   }
-  q += xor32(q);
+  q = half_sum(q);
   const float rstd = 1.0f / sqrtf(q * (1.0f / 128.0f) + eps);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {

@@ -37,7 +37,7 @@ class TrimulArgs(C.Structure):
 
 class TriattnArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("H", i64), ("S", i64), ("D", i64),
-                ("q", vp), ("k", vp), ("v", vp), ("q_stride", i64 * 5), ("k_stride", i64 * 5), ("v_stride", i64 * 5),
+                ("q", vp), ("k", vp), ("v", vp), ("q_stride", i64 * 5), ("k_stride", i64 * 5), ("v_stride", i64 * 5), ("v_layout", i32),
                 ("bias", vp), ("bias_dtype", i32), ("bias_stride", i64 * 4), ("mask", vp), ("mask_dtype", i32),
                 ("mask_stride", i64 * 3), ("out", vp), ("out_stride", i64 * 5), ("scale", f32)]
 
