@@ -49,7 +49,7 @@ typedef struct {
   int32_t abi_version;
   int32_t dtype_in;        /* FPF_DT_BF16 | FPF_DT_F32 */
   int32_t dtype_out;       /* FPF_DT_BF16 | FPF_DT_F32 */
-  int32_t cols;            /* normalised width, <= 1024, a multiple of 8 (bf16) / 4 (fp32) */
+  int32_t cols;            /* normalised width: bf16 input <= 1024, multiple of 8; fp32 input <= 512, multiple of 4 (8 for bf16 out) */
   int64_t rows;
   const void* x;
   int64_t x_row_stride;    /* elements between rows (>= cols) */

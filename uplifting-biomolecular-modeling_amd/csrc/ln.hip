@@ -5,77 +5,94 @@
 
 namespace fpf {
 
+// 16 lanes per row, LN_RPT rows per thread: every row's loads are issued before any reduction so each lane keeps LN_RPT
+// 16-byte requests in flight (a single row per thread leaves the kernel latency-bound, not bandwidth-bound).
+constexpr int LN_RPT = 4;
+
 template <typename TI, typename TO, int VPL>
 __global__ void __launch_bounds__(256) ln_rows_kernel(const TI* __restrict__ x, int64_t xs, TO* __restrict__ y, int64_t ys,
                                                       const float* __restrict__ gamma, const float* __restrict__ beta,
                                                       int64_t rows, int cols, float eps) {
   constexpr int E = 16 / sizeof(TI);                 // elements per 16-byte vector
   const int lane = threadIdx.x & 15;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const bool live = row < rows;
-  float v[VPL * E];
-  float s = 0.f;
+  const int64_t row0 = (int64_t)blockIdx.x * (16 * LN_RPT) + (threadIdx.x >> 4);
+  float v[LN_RPT][VPL * E];
 #pragma unroll
-  for (int c = 0; c < VPL; ++c) {
-    const int e0 = (lane + 16 * c) * E;
-    if (live && e0 < cols) {
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(x + row * xs + e0);
+  for (int rr = 0; rr < LN_RPT; ++rr) {
+    const int64_t row = row0 + 16 * rr;
+#pragma unroll
+    for (int c = 0; c < VPL; ++c) {
+      const int e0 = (lane + 16 * c) * E;
+      u32x4 raw = {0, 0, 0, 0};
+      if (row < rows && e0 < cols) raw = *reinterpret_cast<const u32x4*>(x + row * xs + e0);
       if constexpr (sizeof(TI) == 4) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[c * E + e] = __uint_as_float(raw[e]);
+        for (int e = 0; e < 4; ++e) v[rr][c * E + e] = __uint_as_float(raw[e]);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[c * E + 2 * e] = lo_bf(raw[e]);
-          v[c * E + 2 * e + 1] = hi_bf(raw[e]);
+          v[rr][c * E + 2 * e] = lo_bf(raw[e]);
+          v[rr][c * E + 2 * e + 1] = hi_bf(raw[e]);
         }
       }
-    } else {
-#pragma unroll
-      for (int e = 0; e < E; ++e) v[c * E + e] = 0.f;
     }
-#pragma unroll
-    for (int e = 0; e < E; ++e) s += v[c * E + e];
   }
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
-  const float mean = s / (float)cols;
-  float q = 0.f;
+  float gw[VPL * E], bw[VPL * E];
 #pragma unroll
   for (int c = 0; c < VPL; ++c) {
     const int e0 = (lane + 16 * c) * E;
-    if (e0 < cols) {
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float d = v[c * E + e] - mean;
-        q += d * d;
+    for (int e = 0; e < E; e += 4) {
+      const bool ok = e0 + e < cols;
+      const f32x4 g4 = (gamma && ok) ? *reinterpret_cast<const f32x4*>(gamma + e0 + e) : f32x4{1, 1, 1, 1};
+      const f32x4 b4 = (beta && ok) ? *reinterpret_cast<const f32x4*>(beta + e0 + e) : f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        gw[c * E + e + u] = g4[u];
+        bw[c * E + e + u] = b4[u];
       }
     }
   }
 #pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 16);
-  const float rstd = 1.0f / sqrtf(q / (float)cols + eps);
-  if (!live) return;
+  for (int rr = 0; rr < LN_RPT; ++rr) {
+    const int64_t row = row0 + 16 * rr;
+    float s = 0.f;
 #pragma unroll
-  for (int c = 0; c < VPL; ++c) {
-    const int e0 = (lane + 16 * c) * E;
-    if (e0 >= cols) continue;
-    float o[E];
+    for (int i = 0; i < VPL * E; ++i) s += v[rr][i];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float gw = gamma ? gamma[e0 + e] : 1.f;
-      const float bw = beta ? beta[e0 + e] : 0.f;
-      o[e] = (v[c * E + e] - mean) * rstd * gw + bw;
+    for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, 16);
+    const float mean = s / (float)cols;
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < VPL; ++c) {
+      if ((lane + 16 * c) * E < cols) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float d = v[rr][c * E + e] - mean;
+          q += d * d;
+        }
+      }
     }
-    if constexpr (sizeof(TO) == 4) {
 #pragma unroll
-      for (int e = 0; e < E; e += 4)
-        *reinterpret_cast<f32x4*>(y + row * ys + e0 + e) = f32x4{o[e], o[e + 1], o[e + 2], o[e + 3]};
-    } else if constexpr (E == 8) {
-      u32x4 w{pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7])};
-      *reinterpret_cast<u32x4*>(y + row * ys + e0) = w;
-    } else {
-      *reinterpret_cast<u32x2*>(y + row * ys + e0) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+    for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, 16);
+    const float rstd = 1.0f / sqrtf(q / (float)cols + eps);
+    if (row >= rows) continue;
+#pragma unroll
+    for (int c = 0; c < VPL; ++c) {
+      const int e0 = (lane + 16 * c) * E;
+      if (e0 >= cols) continue;
+      float o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = (v[rr][c * E + e] - mean) * rstd * gw[c * E + e] + bw[c * E + e];
+      if constexpr (sizeof(TO) == 4) {
+#pragma unroll
+        for (int e = 0; e < E; e += 4)
+          *reinterpret_cast<f32x4*>(y + row * ys + e0 + e) = f32x4{o[e], o[e + 1], o[e + 2], o[e + 3]};
+      } else if constexpr (E == 8) {
+        *reinterpret_cast<u32x4*>(y + row * ys + e0) = u32x4{pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7])};
+      } else {
+        *reinterpret_cast<u32x2*>(y + row * ys + e0) = u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+      }
     }
   }
 }
@@ -84,7 +101,7 @@ template <typename TI, typename TO>
 static int launch_ln(const FpfLnArgs* a, hipStream_t st, char* err, size_t errlen) {
   constexpr int E = 16 / sizeof(TI);
   const int vpl_need = (int)cdiv(a->cols, 16 * E);
-  const dim3 grid((unsigned)cdiv(a->rows, 16)), block(256);
+  const dim3 grid((unsigned)cdiv(a->rows, 16 * LN_RPT)), block(256);
   const TI* x = static_cast<const TI*>(a->x);
   TO* y = static_cast<TO*>(a->y);
 #define FPF_LN(VPL)                                                                                                    \
@@ -94,9 +111,8 @@ static int launch_ln(const FpfLnArgs* a, hipStream_t st, char* err, size_t errle
     return launched(err, errlen, "fpf_layernorm_fwd");                                                               \
   }
   FPF_LN(1) FPF_LN(2) FPF_LN(4) FPF_LN(8)
-  if constexpr (E == 4) { FPF_LN(16) }
 #undef FPF_LN
-  return fail(err, errlen, FPF_E_SHAPE, "cols=%d above 1024", a->cols);
+  return fail(err, errlen, FPF_E_SHAPE, "cols=%d above %d", a->cols, E == 8 ? 1024 : 512);
 }
 
 }  // namespace fpf

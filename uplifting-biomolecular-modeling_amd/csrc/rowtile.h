@@ -1,0 +1,108 @@
+// Device building blocks of the persistent "32 pixel rows x 128 channels -> LayerNorm -> MFMA against LDS-resident weights"
+// kernels (trimul K1 / K3, tri-att prologue / epilogue).  One wave owns a tile of 32 pixel rows at a time and walks the
+// tile list on its own: weights are staged in LDS once per workgroup, so the tile loop has no workgroup barrier and the
+// 8 waves of a workgroup (2 per SIMD) overlap each other's loads, LayerNorm and MFMA.
+//
+// Operand layout (v_mfma_f32_32x32x16_bf16, lane = 32 * g + n): the normalised rows are the B operand -- lane (n, g) holds
+// pixel n's channels 64g + 8t .. +7 for k-step t -- and the weight rows (W[out][in], LDS pitch RT_LD) are the A operand
+// read at the same channel offsets, so D = W x^T comes out with lane (n, g) holding pixel n and the 16 output channels
+// c_row(v, g) of a 32-channel block.
+#pragma once
+#include "fpf_common.h"
+
+namespace fpf {
+
+constexpr int RT_C = 128;            // channels per pixel row
+constexpr int RT_LD = RT_C + 8;      // LDS pitch (bf16) of a 128-wide weight row: 272 B, conflict-free 16-byte reads
+constexpr int RT_WAVES = 8;          // waves per workgroup
+
+// Raw 16-byte loads of one lane's half of a 128-channel bf16 pixel row (zeros when !live).
+__device__ __forceinline__ void rt_load(const uint16_t* __restrict__ row, bool live, int g, u32x4 (&raw)[8]) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) raw[t] = live ? *reinterpret_cast<const u32x4*>(row + 64 * g + 8 * t) : u32x4{0, 0, 0, 0};
+}
+
+// LayerNorm over the 128 channels split across lanes n and n + 32 (fp32 statistics, two-pass variance), packed to bf16
+// B-operand fragments.  gb = the affine parameters staged in LDS as fp32 [gamma 128 | beta 128] (rt_stage_affine).
+__device__ __forceinline__ void rt_ln(const u32x4 (&raw)[8], int g, const float* __restrict__ gb, float eps, bf16x8 (&xb)[8]) {
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s += lo_bf(raw[t][e]) + hi_bf(raw[t][e]);
+  const float mean = half_sum(s) * (1.0f / 128.0f);
+  float q = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d0 = lo_bf(raw[t][e]) - mean, d1 = hi_bf(raw[t][e]) - mean;
+      q += d0 * d0 + d1 * d1;
+    }
+  const float rstd = 1.0f / sqrtf(half_sum(q) * (1.0f / 128.0f) + eps);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int c0 = 64 * g + 8 * t;
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(gb + c0), w1 = *reinterpret_cast<const f32x4*>(gb + c0 + 4);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(gb + RT_C + c0), b1 = *reinterpret_cast<const f32x4*>(gb + RT_C + c0 + 4);
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      o[e] = pack2((lo_bf(raw[t][e]) - mean) * rstd * w0[2 * e] + b0[2 * e], (hi_bf(raw[t][e]) - mean) * rstd * w0[2 * e + 1] + b0[2 * e + 1]);
+      o[2 + e] = pack2((lo_bf(raw[t][2 + e]) - mean) * rstd * w1[2 * e] + b1[2 * e],
+                       (hi_bf(raw[t][2 + e]) - mean) * rstd * w1[2 * e + 1] + b1[2 * e + 1]);
+    }
+    xb[t] = as_bf8(u32x4{o[0], o[1], o[2], o[3]});
+  }
+}
+
+// Stages LayerNorm gamma / beta (NULL = 1 / 0) as fp32 [gamma 128 | beta 128] in LDS.
+__device__ __forceinline__ void rt_stage_affine(float* __restrict__ s, const float* __restrict__ w, const float* __restrict__ b, int tid, int nthr) {
+  for (int i = tid; i < 2 * RT_C; i += nthr) s[i] = i < RT_C ? (w ? w[i] : 1.0f) : (b ? b[i - RT_C] : 0.0f);
+}
+
+// Cooperative copy of `rows` rows of a [rows x 128] bf16 weight matrix into LDS (pitch RT_LD); rows >= valid are zero.
+__device__ __forceinline__ void rt_stage_weights(uint16_t* __restrict__ s, const uint16_t* __restrict__ w, int rows, int valid, int tid, int nthr) {
+  for (int i = tid; i < rows * 16; i += nthr) {
+    const int r = i >> 4, ch = i & 15;
+    *reinterpret_cast<u32x4*>(&s[r * RT_LD + ch * 8]) = r < valid ? *reinterpret_cast<const u32x4*>(w + (int64_t)r * RT_C + ch * 8) : u32x4{0, 0, 0, 0};
+  }
+}
+
+// D = W[row0 .. row0 + 31] x^T over the 128 channels (8 k-steps), weights from LDS.
+__device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
+  const uint16_t* r = s + (row0 + n) * RT_LD + 64 * g;
+  f32x16 acc = {};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * t)), xb[t], acc);
+    __builtin_amdgcn_sched_barrier(0);   // keep the next k-step's LDS reads behind this MFMA: bounded register pressure
+  }
+  return acc;
+}
+
+// K GEMMs over the same B operand, k-step-major (the K weight fragments of one k-step are read, then K MFMAs issue).
+template <int K>
+__device__ __forceinline__ void rt_gemm32_multi(const uint16_t* const (&s)[K], int row0, int n, int g, const bf16x8 (&xb)[8], f32x16 (&acc)[K]) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) acc[k] = f32x16{};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    bf16x8 a[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * t));
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc[k] = mfma32(a[k], xb[t], acc[k]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Orders a wave's own LDS writes before its later LDS reads of other lanes' data (the LDS unit executes a wave's
+// operations in order; this keeps the compiler from moving the reads above the writes).
+__device__ __forceinline__ void rt_wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace fpf

@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(256) transition_bf16_kernel(const uint16_t* x,
   __shared__ __attribute__((aligned(16))) uint16_t sWa[TR_HB * TR_WLD];
   __shared__ __attribute__((aligned(16))) uint16_t sWb[TR_HB * TR_WLD];
   __shared__ __attribute__((aligned(16))) uint16_t sWo[TR_C * TR_OLD];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * (32 * PW);
 
   bf16x8 xb[PW][TR_KS];

@@ -10,7 +10,9 @@
 // the B operand of O^T = V^T P^T -- the key order inside a k-step is permuted identically in V^T.  exp2 with scale*log2(e)
 // folded into one FMA.  A row whose keys are all masked attends uniformly to every key (the op's convention).
 // fp32 core (exact tier): one thread per query, LDS-staged K / V tiles, fp32 online softmax with expf.
-#include "fpf_common.h"
+#include <algorithm>
+
+#include "rowtile.h"
 
 namespace fpf {
 
@@ -61,12 +63,12 @@ __device__ __forceinline__ f32x16 qk_tile(const uint16_t* __restrict__ kr, int s
 }
 
 template <bool VT>
-__global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_R][TA_KT * TA_KLD];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_R][TA_D * TA_VLD];
   __shared__ uint64_t sKeep[TA_R];
   __shared__ int sAlive[TA_R];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   // logical work order (b h) -> row group -> query tile, dealt to the 8 XCDs in contiguous runs
   const int64_t nq = cdiv(p.S, 128), nr = cdiv(p.N, TA_R);
   const int64_t total = p.B * p.H * nr * nq;
@@ -119,39 +121,46 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
     lrow[r] = 0.f;
   }
 
-  // staging: 1024 16-byte chunks per operand per tile, 4 per thread
+  // staging: 1024 16-byte chunks per operand per tile, 4 per thread; element offsets at key 0 are computed once
+  int64_t koff[4], voff[4];
+  bool rowok[4];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = tid + 256 * it;
+    const int64_t i = i0 + (c >> 8);
+    rowok[it] = i < p.N;
+    const int64_t ii = rowok[it] ? i : i0;
+    koff[it] = b * p.ks[0] + ii * p.ks[1] + h * p.ks[2] + ((c >> 2) & 63) * p.ks[3] + 8 * (c & 3);
+    if constexpr (VT)
+      voff[it] = b * p.vs[0] + ii * p.vs[1] + h * p.vs[2] + ((c >> 3) & 31) * p.vs[3] + 8 * (c & 7);
+    else
+      voff[it] = b * p.vs[0] + ii * p.vs[1] + h * p.vs[2] + ((c >> 2) & 63) * p.vs[3] + 8 * (c & 3);
+  }
   u32x4 rk[4], rv[4];
   auto gload = [&](int64_t k0) {
+    if (k0 + TA_KT <= p.S) {                              // whole tile in range (uniform)
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        rk[it] = rowok[it] ? *reinterpret_cast<const u32x4*>(p.k + koff[it] + k0 * p.ks[3]) : u32x4{0, 0, 0, 0};
+        rv[it] = rowok[it] ? *reinterpret_cast<const u32x4*>(p.v + voff[it] + (VT ? k0 : k0 * p.vs[3])) : u32x4{0, 0, 0, 0};
+      }
+      return;
+    }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int c = tid + 256 * it;
-      const int r = c >> 8;
-      const int64_t i = i0 + r;
-      {
-        const int kk = (c >> 2) & 63, part = c & 3;
-        const int64_t key = k0 + kk;
-        const bool ok = i < p.N && key < p.S;
-        rk[it] = ok ? *reinterpret_cast<const u32x4*>(p.k + b * p.ks[0] + i * p.ks[1] + h * p.ks[2] + key * p.ks[3] + 8 * part) : u32x4{0, 0, 0, 0};
-      }
+      const int64_t kkey = k0 + ((c >> 2) & 63);
+      rk[it] = (rowok[it] && kkey < p.S) ? *reinterpret_cast<const u32x4*>(p.k + koff[it] + k0 * p.ks[3]) : u32x4{0, 0, 0, 0};
       if constexpr (VT) {
-        const int d = (c >> 3) & 31, kc = c & 7;
-        const int64_t key = k0 + 8 * kc;
-        const bool ok = i < p.N && key + 8 <= p.S;
-        const uint16_t* src = p.v + b * p.vs[0] + i * p.vs[1] + h * p.vs[2] + d * p.vs[3] + key;
-        if (ok) {
-          rv[it] = *reinterpret_cast<const u32x4*>(src);
-        } else {
-          uint16_t tmp[8];
+        const int64_t key = k0 + 8 * (c & 7);
+        const uint16_t* src = p.v + voff[it] + k0;
+        uint16_t tmp[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) tmp[e] = (i < p.N && key + e < p.S) ? src[e] : (uint16_t)0;
-          rv[it] = u32x4{tmp[0] | ((uint32_t)tmp[1] << 16), tmp[2] | ((uint32_t)tmp[3] << 16), tmp[4] | ((uint32_t)tmp[5] << 16),
-                         tmp[6] | ((uint32_t)tmp[7] << 16)};
-        }
+        for (int e = 0; e < 8; ++e) tmp[e] = (rowok[it] && key + e < p.S) ? src[e] : (uint16_t)0;
+        rv[it] = u32x4{tmp[0] | ((uint32_t)tmp[1] << 16), tmp[2] | ((uint32_t)tmp[3] << 16), tmp[4] | ((uint32_t)tmp[5] << 16),
+                       tmp[6] | ((uint32_t)tmp[7] << 16)};
       } else {
-        const int kk = (c >> 2) & 63, part = c & 3;
-        const int64_t key = k0 + kk;
-        const bool ok = i < p.N && key < p.S;
-        rv[it] = ok ? *reinterpret_cast<const u32x4*>(p.v + b * p.vs[0] + i * p.vs[1] + h * p.vs[2] + key * p.vs[3] + 8 * part) : u32x4{0, 0, 0, 0};
+        rv[it] = (rowok[it] && kkey < p.S) ? *reinterpret_cast<const u32x4*>(p.v + voff[it] + k0 * p.vs[3]) : u32x4{0, 0, 0, 0};
       }
     }
   };
@@ -163,13 +172,9 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
     for (int it = 0; it < 4; ++it) {
       const int c = tid + 256 * it;
       const int r = c >> 8;
-      {
-        const int kk = (c >> 2) & 63, part = c & 3;
-        *reinterpret_cast<u32x4*>(&sK[r][kk * TA_KLD + 8 * part]) = rk[it];
-      }
+      *reinterpret_cast<u32x4*>(&sK[r][((c >> 2) & 63) * TA_KLD + 8 * (c & 3)]) = rk[it];
       if constexpr (VT) {
-        const int d = (c >> 3) & 31, kc = c & 7;
-        uint16_t* dst = &sV[r][d * TA_VLD + 8 * kc];
+        uint16_t* dst = &sV[r][((c >> 3) & 31) * TA_VLD + 8 * (c & 7)];
         *reinterpret_cast<u32x2*>(dst) = u32x2{rv[it][0], rv[it][1]};
         *reinterpret_cast<u32x2*>(dst + 4) = u32x2{rv[it][2], rv[it][3]};
       } else {
@@ -237,8 +242,9 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
       bool need = false;
 #pragma unroll
       for (int r = 0; r < TA_R; ++r) {
-        float m0 = fmaxf(fmaxf(fmaxf(s[r][0], s[r][1]), fmaxf(s[r][2], s[r][3])), fmaxf(fmaxf(s[r][4], s[r][5]), fmaxf(s[r][6], s[r][7])));
-        m0 = fmaxf(m0, fmaxf(fmaxf(fmaxf(s[r][8], s[r][9]), fmaxf(s[r][10], s[r][11])), fmaxf(fmaxf(s[r][12], s[r][13]), fmaxf(s[r][14], s[r][15]))));
+        float m0 = s[r][0];                      // a linear chain: the compiler folds it into v_max3_f32
+#pragma unroll
+        for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, s[r][v]);
         mx[r] = half_max(m0) * c2;
         need |= mx[r] > mrow[r] + TA_HEADROOM;
       }
@@ -256,16 +262,16 @@ __global__ void __launch_bounds__(256) triattn_core_bf16(const CoreParams p) {
 #pragma unroll
       for (int r = 0; r < TA_R; ++r) {
         const float mb = (mrow[r] == -INFINITY) ? 0.f : mrow[r];
-        float ps = 0.f;
         uint32_t pk[8];
+        float ps = lrow[r];
 #pragma unroll
         for (int v = 0; v < 16; v += 2) {
           const float p0 = fast_exp2(fmaf(s[r][v], c2, -mb));
           const float p1 = fast_exp2(fmaf(s[r][v + 1], c2, -mb));
-          ps += p0 + p1;
           pk[v >> 1] = pack2(p0, p1);
+          ps = dot2_bf16(pk[v >> 1], ps);         // the row sum of the bf16 P the PV MFMA consumes
         }
-        lrow[r] += ps;
+        lrow[r] = ps;
         const uint16_t* vr = sV[r] + n * TA_VLD + 32 * sub + 4 * g;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
@@ -410,171 +416,119 @@ __global__ void __launch_bounds__(64) triattn_core_f32(const CoreParamsF p) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------- prologue (bf16)
-// x = LN(z or z^T) -> q, k, v [B,I,H,J,D] bf16, g [B,I,J,HD] bf16 (pre-sigmoid), bias [B,H,I,J] fp32.  A wave owns 32 positions
-// j of one attention row i; with `ending` the 32 z pixels are z[j][i] (strided rows, each a contiguous 256-byte pixel).
-constexpr int TP_C = 128, TP_HD = 128, TP_WLD = TP_C + 8;
+// x = LN(z or z^T) -> q, k [B,I,H,J,D] bf16, v^T [B,I,H,D,J] bf16 (the core stages V^T rows directly), g [B,I,J,HD] bf16
+// (pre-sigmoid), bias [B,H,I,J] fp32.  Persistent: W_qkvg (512 rows) and W_b (padded to 32 rows) live in LDS (148 KB); a wave
+// owns 32 positions j of one attention row i; with `ending` the 32 z pixels are z[j][i] (strided rows, each a contiguous
+// 256-byte pixel).
+constexpr int TP_C = 128, TP_HD = 128;
 
-__device__ __forceinline__ void ln128_load(const uint16_t* __restrict__ row, bool live, int g, const float* __restrict__ w,
-                                           const float* __restrict__ bsh, float eps, bf16x8 (&xb)[8]) {
-  float xv[64];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const u32x4 r = live ? *reinterpret_cast<const u32x4*>(row + 64 * g + 8 * t) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xv[8 * t + 2 * e] = lo_bf(r[e]);
-      xv[8 * t + 2 * e + 1] = hi_bf(r[e]);
-    }
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) s += xv[i];
-  s = half_sum(s);
-  const float mean = s * (1.0f / 128.0f);
-  float qq = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const float d = xv[i] - mean;
-    qq += d * d;
-  }
-  qq = half_sum(qq);
-  const float rstd = 1.0f / sqrtf(qq * (1.0f / 128.0f) + eps);
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int c0 = 64 * g + 8 * t;
-    float y[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = (xv[8 * t + e] - mean) * rstd * (w ? w[c0 + e] : 1.f) + (bsh ? bsh[c0 + e] : 0.f);
-    xb[t] = as_bf8(u32x4{pack2(y[0], y[1]), pack2(y[2], y[3]), pack2(y[4], y[5]), pack2(y[6], y[7])});
-  }
-}
-
-__global__ void __launch_bounds__(256) triattn_prologue_bf16(const uint16_t* __restrict__ z, const float* __restrict__ ln_w,
+__global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __restrict__ z, const float* __restrict__ ln_w,
                                                              const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ w_qkvg,
                                                              const uint16_t* __restrict__ w_b, int H, uint16_t* __restrict__ qo,
                                                              uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, uint16_t* __restrict__ go,
-                                                             float* __restrict__ bo, int64_t N, int ending) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[2][32 * TP_WLD];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t tpr = cdiv(N, 32);
-  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;
-  const int64_t b = blockIdx.y;
-  const int64_t i = wt / tpr, j = (wt % tpr) * 32 + n;
-  const bool live = i < N && j < N;
-  const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
-  bf16x8 xb[8];
-  ln128_load(z + zpix * TP_C, live, g, ln_w, ln_b, eps, xb);
+                                                             float* __restrict__ bo, int64_t N, int64_t B, int ending) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[(4 * TP_HD + 32) * RT_LD];
+  __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
+  rt_stage_weights(sW, w_qkvg, 4 * TP_HD, 4 * TP_HD, tid, 512);
+  rt_stage_weights(sW + 4 * TP_HD * RT_LD, w_b, 32, H, tid, 512);
+  __syncthreads();
   const int D = TP_HD / H;
-  // 16 blocks of 32 output channels (q | k | v | g) + 1 bias block (rows >= H of it are zero)
-  for (int blk = 0; blk < 17; ++blk) {
-    __syncthreads();
-    if (blk < 16) {
+  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
+  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
+  for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
+    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+    const bool live = j < N;
+    const int64_t zpix = ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
+    u32x4 raw[8];
+    rt_load(z + zpix * RT_C, live, g, raw);
+    bf16x8 xb[8];
+    rt_ln(raw, g, sLN, eps, xb);
+#pragma unroll 1
+    for (int blk = 0; blk < 17; ++blk) {
+      const f32x16 acc = rt_gemm32(sW, blk * 32, n, g, xb);
+      if (!live) continue;
+      if (blk < 4 || (blk >= 4 && blk < 8)) {            // q | k: [B, I, H, J, D], 4 consecutive d per 8-byte store
+        uint16_t* dst = blk < 4 ? qo : ko;
+        const int hh = blk & 3;
 #pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int c = tid + 256 * it, r = c >> 4, ch = c & 15;
-        *reinterpret_cast<u32x4*>(&sW[blk & 1][r * TP_WLD + ch * 8]) =
-            *reinterpret_cast<const u32x4*>(w_qkvg + (int64_t)(blk * 32 + r) * TP_C + ch * 8);
+        for (int qd = 0; qd < 4; ++qd) {
+          const int d0 = 8 * qd + 4 * g;
+          *reinterpret_cast<u32x2*>(dst + (((b * N + i) * H + hh) * N + j) * D + d0) =
+              u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
+        }
+      } else if (blk < 12) {                              // v, transposed: vT[b][i][h][d][j]
+        uint16_t* dst = vo + ((b * N + i) * H + (blk & 3)) * (int64_t)D * N + j;
+#pragma unroll
+        for (int vv = 0; vv < 16; ++vv) dst[(int64_t)c_row(vv, g) * N] = f2bf(acc[vv]);
+      } else if (blk < 16) {                              // g (pre-sigmoid): [B, I, J, HD]
+        const int cb = (blk - 12) * 32;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int c0 = cb + 8 * qd + 4 * g;
+          *reinterpret_cast<u32x2*>(go + ((b * N + i) * N + j) * TP_HD + c0) =
+              u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
+        }
+      } else if (g == 0) {                                // bias (fp32): [B, H, I, J]
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (v < H) bo[((b * H + v) * N + i) * N + j] = acc[v];
       }
-    } else {
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int c = tid + 256 * it, r = c >> 4, ch = c & 15;
-        *reinterpret_cast<u32x4*>(&sW[blk & 1][r * TP_WLD + ch * 8]) =
-            r < H ? *reinterpret_cast<const u32x4*>(w_b + (int64_t)r * TP_C + ch * 8) : u32x4{0, 0, 0, 0};
-      }
-    }
-    __syncthreads();
-    f32x16 acc = {};
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-      acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&sW[blk & 1][n * TP_WLD + 64 * g + 8 * t])), xb[t], acc);
-    if (!live) continue;
-    if (blk >= 8 && blk < 12) {               // v, written transposed: vT[b][i][h][d][j] (the core's V^T staging copies rows)
-      const int hh = blk & 3;
-      uint16_t* dst = vo + ((b * N + i) * H + hh) * (int64_t)D * N + j;
-#pragma unroll
-      for (int vv = 0; vv < 16; ++vv) dst[(int64_t)c_row(vv, g) * N] = f2bf(acc[vv]);
-    } else if (blk < 12) {
-      uint16_t* dst = blk < 4 ? qo : ko;
-      const int cb = (blk & 3) * 32;      // channel base within q / k / v
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int c0 = cb + 8 * qd + 4 * g;       // channel = h * D + d
-        const int hh = c0 / D, d0 = c0 % D;
-        uint16_t* p = dst + (((b * N + i) * H + hh) * N + j) * D + d0;
-        *reinterpret_cast<u32x2*>(p) = u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
-      }
-    } else if (blk < 16) {
-      const int cb = (blk - 12) * 32;
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int c0 = cb + 8 * qd + 4 * g;
-        *reinterpret_cast<u32x2*>(go + ((b * N + i) * N + j) * TP_HD + c0) =
-            u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
-      }
-    } else if (g == 0) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (v < H) bo[((b * H + v) * N + i) * N + j] = acc[v];
     }
   }
 }
 
 // ---------------------------------------------------------------------------------------------------------------- epilogue (bf16)
-// u = (sigmoid(g) * o) W_o^T; residual: z[i,j] += u (ending: z[j,i] += u) in place; else out[zpix] = u.
-__global__ void __launch_bounds__(256) triattn_epilogue_bf16(const uint16_t* __restrict__ o, const uint16_t* __restrict__ gt,
-                                                             const uint16_t* __restrict__ w_o, int H, uint16_t* zout, int64_t N, int ending,
-                                                             int residual) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[32 * TP_WLD];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t tpr = cdiv(N, 32);
-  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;
-  const int64_t b = blockIdx.y;
-  const int64_t i = wt / tpr, j = (wt % tpr) * 32 + n;
-  const bool live = i < N && j < N;
+// u = (sigmoid(g) * o) W_o^T; residual: z[i,j] += u (ending: z[j,i] += u) in place; else out[zpix] = u.  Persistent: W_o lives in
+// LDS; a wave owns 32 positions of one attention row.
+__global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __restrict__ o, const uint16_t* __restrict__ gt,
+                                                             const uint16_t* __restrict__ w_o, int H, uint16_t* zout, int64_t N, int64_t B,
+                                                             int ending, int residual) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[RT_C * RT_LD];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  rt_stage_weights(sW, w_o, RT_C, RT_C, tid, 512);
+  __syncthreads();
   const int D = TP_HD / H;
-  bf16x8 xb[8];
+  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
+  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
+  for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
+    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+    const bool live = j < N;
+    bf16x8 xb[8];
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int hd0 = 64 * g + 8 * t;
-    const int hh = hd0 / D, d0 = hd0 % D;
-    u32x4 ov = {0, 0, 0, 0}, gv = {0, 0, 0, 0};
-    if (live) {
-      ov = *reinterpret_cast<const u32x4*>(o + (((b * N + i) * H + hh) * N + j) * D + d0);
-      gv = *reinterpret_cast<const u32x4*>(gt + ((b * N + i) * N + j) * TP_HD + hd0);
-    }
-    uint32_t w4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      w4[e] = pack2(sigmoidf_(lo_bf(gv[e])) * lo_bf(ov[e]), sigmoidf_(hi_bf(gv[e])) * hi_bf(ov[e]));
-    xb[t] = as_bf8(u32x4{w4[0], w4[1], w4[2], w4[3]});
-  }
-  const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
-  for (int cb = 0; cb < 4; ++cb) {
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int c = tid + 256 * it, r = c >> 4, ch = c & 15;
-      *reinterpret_cast<u32x4*>(&sW[r * TP_WLD + ch * 8]) = *reinterpret_cast<const u32x4*>(w_o + (int64_t)(cb * 32 + r) * TP_HD + ch * 8);
-    }
-    __syncthreads();
-    f32x16 acc = {};
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&sW[n * TP_WLD + 64 * g + 8 * t])), xb[t], acc);
-    if (!live) continue;
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int c0 = cb * 32 + 8 * qd + 4 * g;
-      uint16_t* p = zout + zpix * TP_C + c0;
-      float y0 = acc[4 * qd], y1 = acc[4 * qd + 1], y2 = acc[4 * qd + 2], y3 = acc[4 * qd + 3];
-      if (residual) {
-        const u32x2 r = *reinterpret_cast<const u32x2*>(p);
-        y0 += lo_bf(r[0]);
-        y1 += hi_bf(r[0]);
-        y2 += lo_bf(r[1]);
-        y3 += hi_bf(r[1]);
+    for (int tt = 0; tt < 8; ++tt) {
+      const int hd0 = 64 * g + 8 * tt;
+      const int hh = hd0 / D, d0 = hd0 % D;
+      u32x4 ov = {0, 0, 0, 0}, gv = {0, 0, 0, 0};
+      if (live) {
+        ov = *reinterpret_cast<const u32x4*>(o + (((b * N + i) * H + hh) * N + j) * D + d0);
+        gv = *reinterpret_cast<const u32x4*>(gt + ((b * N + i) * N + j) * TP_HD + hd0);
       }
-      *reinterpret_cast<u32x2*>(p) = u32x2{pack2(y0, y1), pack2(y2, y3)};
+      uint32_t w4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w4[e] = pack2(sigmoidf_(lo_bf(gv[e])) * lo_bf(ov[e]), sigmoidf_(hi_bf(gv[e])) * hi_bf(ov[e]));
+      xb[tt] = as_bf8(u32x4{w4[0], w4[1], w4[2], w4[3]});
+    }
+    const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
+#pragma unroll 1
+    for (int cb = 0; cb < 4; ++cb) {
+      const f32x16 acc = rt_gemm32(sW, cb * 32, n, g, xb);
+      if (!live) continue;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int c0 = cb * 32 + 8 * qd + 4 * g;
+        uint16_t* p = zout + zpix * RT_C + c0;
+        float y0 = acc[4 * qd], y1 = acc[4 * qd + 1], y2 = acc[4 * qd + 2], y3 = acc[4 * qd + 3];
+        if (residual) {
+          const u32x2 r = *reinterpret_cast<const u32x2*>(p);
+          y0 += lo_bf(r[0]);
+          y1 += hi_bf(r[0]);
+          y2 += lo_bf(r[1]);
+          y3 += hi_bf(r[1]);
+        }
+        *reinterpret_cast<u32x2*>(p) = u32x2{pack2(y0, y1), pack2(y2, y3)};
+      }
     }
   }
 }
@@ -849,16 +803,17 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
     if (a->C != TP_C || HD != TP_HD || D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 block serves C = 128, H*D = 128, D = 32");
     if (!aligned16(a->z) || !aligned16(a->out) || !aligned16(a->workspace) || !aligned16(a->w_qkvg) || !aligned16(a->w_b) || !aligned16(a->w_o))
       return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
-    const unsigned grid = (unsigned)(N * cdiv(N, 32) / 4 + ((N * cdiv(N, 32)) % 4 ? 1 : 0));
-    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid, (unsigned)B), dim3(256), 0, st, (const uint16_t*)a->z, a->ln_w, a->ln_b, a->eps,
+    const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
+    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, a->ln_w, a->ln_b, a->eps,
                        (const uint16_t*)a->w_qkvg, (const uint16_t*)a->w_b, (int)H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N,
-                       a->ending);
+                       B, a->ending);
     int rc = launched(err, errlen, "triattn_prologue_bf16");
     if (rc) return rc;
     rc = core_launch(&c, st, err, errlen);
     if (rc) return rc;
-    hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(grid, (unsigned)B), dim3(256), 0, st, (const uint16_t*)o, (const uint16_t*)g,
-                       (const uint16_t*)a->w_o, (int)H, (uint16_t*)a->out, N, a->ending, a->residual);
+    const unsigned egrid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
+    hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(egrid), dim3(512), 0, st, (const uint16_t*)o, (const uint16_t*)g,
+                       (const uint16_t*)a->w_o, (int)H, (uint16_t*)a->out, N, B, a->ending, a->residual);
     return launched(err, errlen, "triattn_epilogue_bf16");
   }
   if (a->dtype == FPF_DT_F32) {

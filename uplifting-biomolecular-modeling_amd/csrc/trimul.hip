@@ -7,106 +7,66 @@
 // Replaces common/opt_core/opt_core/kernels/trimul/__init__.py:1982 (triangle_multiplication), row `native`'s K1 | bmm | K3
 // structure (kernels/trimul/native/DESIGN.md:1-40).  Planes are padded to Np = ceil(N / 128) * 128 with zeros so the
 // contraction needs no bounds checks.  The fp32 path (exact tier) has the same three launches in fp32 scalar FMA.
-#include "fpf_common.h"
+#include <algorithm>
+
+#include "rowtile.h"
 
 namespace fpf {
 
 constexpr int TM_C = 128;            // c_z = c_h for the bf16 path
-constexpr int TM_WLD = TM_C + 8;     // LDS pitch (bf16) of a 128-wide weight row
 constexpr int TM_TILE = 128;         // contraction tile and plane padding
 
-__device__ __forceinline__ void ln128_from_regs(float (&xv)[64], int g, const float* __restrict__ w, const float* __restrict__ b, float eps,
-                                                bf16x8 (&xb)[8]) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) s += xv[i];
-  s = half_sum(s);
-  const float mean = s * (1.0f / 128.0f);
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const float d = xv[i] - mean;
-    q += d * d;
-  }
-  q = half_sum(q);
-  const float rstd = 1.0f / sqrtf(q * (1.0f / 128.0f) + eps);
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int c0 = 64 * g + 8 * t;
-    float y[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = (xv[8 * t + e] - mean) * rstd * (w ? w[c0 + e] : 1.f) + (b ? b[c0 + e] : 0.f);
-    xb[t] = as_bf8(u32x4{pack2(y[0], y[1]), pack2(y[2], y[3]), pack2(y[4], y[5]), pack2(y[6], y[7])});
-  }
-}
-
-__device__ __forceinline__ void load_row128(const uint16_t* __restrict__ row, bool live, int g, float (&xv)[64]) {
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const u32x4 r = live ? *reinterpret_cast<const u32x4*>(row + 64 * g + 8 * t) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xv[8 * t + 2 * e] = lo_bf(r[e]);
-      xv[8 * t + 2 * e + 1] = hi_bf(r[e]);
-    }
-  }
-}
-
-// Cooperative copy of 32 rows (r0 ..) of a [128 x 128] bf16 weight into LDS with pitch TM_WLD.
-__device__ __forceinline__ void stage_w32(uint16_t* __restrict__ s, const uint16_t* __restrict__ w, int r0, int tid) {
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int i = tid + 256 * it;
-    const int r = i >> 4, ch = i & 15;
-    *reinterpret_cast<u32x4*>(&s[r * TM_WLD + ch * 8]) = *reinterpret_cast<const u32x4*>(w + (int64_t)(r0 + r) * TM_C + ch * 8);
-  }
-}
-
-__device__ __forceinline__ f32x16 gemm_rows32(const uint16_t* __restrict__ s, int n, int g, const bf16x8 (&xb)[8]) {
-  f32x16 acc = {};
-#pragma unroll
-  for (int t = 0; t < 8; ++t) acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&s[n * TM_WLD + 64 * g + 8 * t])), xb[t], acc);
-  return acc;
-}
-
 // ---------------------------------------------------------------------------------------------------------------- K1 (bf16)
-__global__ void __launch_bounds__(256) trimul_k1_bf16(const uint16_t* __restrict__ z, const float* __restrict__ mask,
+// Persistent: the four [128 x 128] projection weights live in LDS (139 KB) for the workgroup's lifetime; each wave walks
+// 32-column plane tiles (plane row P, columns Q0 .. Q0+31), prefetching the next tile's 32 z rows while it computes.
+__global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict__ z, const float* __restrict__ mask,
                                                       const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
                                                       const uint16_t* __restrict__ w_ap, const uint16_t* __restrict__ w_ag,
                                                       const uint16_t* __restrict__ w_bp, const uint16_t* __restrict__ w_bg,
-                                                      uint16_t* __restrict__ pa, uint16_t* __restrict__ pb, int64_t N, int64_t Np, int outgoing) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[4][32 * TM_WLD];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t tiles_per_row = Np / 32;
-  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;           // wave tile: plane row P, columns Q0 .. Q0 + 31
-  const int64_t b = blockIdx.y;
-  const int64_t P = wt / tiles_per_row, Q = (wt % tiles_per_row) * 32 + n;
-  const bool live = P < N && Q < N;
-  const int64_t zi = outgoing ? P : Q, zj = outgoing ? Q : P;
-  const int64_t pix = (b * N + zi) * N + zj;
-  float xv[64];
-  load_row128(z + pix * TM_C, live, g, xv);
-  bf16x8 xb[8];
-  ln128_from_regs(xv, g, ln_w, ln_b, eps, xb);
-  const float m = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
+                                                      uint16_t* __restrict__ pa, uint16_t* __restrict__ pb, int64_t N, int64_t Np, int64_t B,
+                                                      int outgoing) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[4 * RT_C * RT_LD];
+  __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
+  rt_stage_weights(sW, w_ap, RT_C, RT_C, tid, 512);
+  rt_stage_weights(sW + 1 * RT_C * RT_LD, w_ag, RT_C, RT_C, tid, 512);
+  rt_stage_weights(sW + 2 * RT_C * RT_LD, w_bp, RT_C, RT_C, tid, 512);
+  rt_stage_weights(sW + 3 * RT_C * RT_LD, w_bg, RT_C, RT_C, tid, 512);
+  __syncthreads();
+  const int64_t tpr = Np / 32, per_b = Np * tpr, total = B * per_b;
+  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
   const int64_t plane = Np * Np;
-  uint16_t* oa = pa + b * TM_C * plane + P * Np + Q;
-  uint16_t* ob = pb + b * TM_C * plane + P * Np + Q;
-  for (int cb = 0; cb < 4; ++cb) {
-    __syncthreads();
-    stage_w32(sW[0], w_ap, cb * 32, tid);
-    stage_w32(sW[1], w_ag, cb * 32, tid);
-    stage_w32(sW[2], w_bp, cb * 32, tid);
-    stage_w32(sW[3], w_bg, cb * 32, tid);
-    __syncthreads();
-    if (P >= Np) continue;
-    const f32x16 ap = gemm_rows32(sW[0], n, g, xb), ag = gemm_rows32(sW[1], n, g, xb);
-    const f32x16 bp = gemm_rows32(sW[2], n, g, xb), bg = gemm_rows32(sW[3], n, g, xb);
+  int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave;
+  u32x4 raw[8];
+  auto fetch = [&](int64_t tt) {
+    const int64_t b = tt / per_b, P = (tt % per_b) / tpr, Q = (tt % tpr) * 32 + n;
+    const bool live = P < N && Q < N;
+    const int64_t pix = (b * N + (outgoing ? P : Q)) * N + (outgoing ? Q : P);
+    rt_load(z + (live ? pix : 0) * RT_C, live, g, raw);
+  };
+  if (t < total) fetch(t);
+  for (; t < total; t += stride) {
+    const int64_t b = t / per_b, P = (t % per_b) / tpr, Q = (t % tpr) * 32 + n;
+    const bool live = P < N && Q < N;
+    const int64_t pix = (b * N + (outgoing ? P : Q)) * N + (outgoing ? Q : P);
+    const float m = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
+    bf16x8 xb[8];
+    rt_ln(raw, g, sLN, eps, xb);
+    if (t + stride < total) fetch(t + stride);
+    uint16_t* oa = pa + b * RT_C * plane + P * Np + Q;
+    uint16_t* ob = pb + b * RT_C * plane + P * Np + Q;
+#pragma unroll 1
+    for (int cb = 0; cb < 4; ++cb) {
+      const uint16_t* const ws[4] = {sW, sW + 1 * RT_C * RT_LD, sW + 2 * RT_C * RT_LD, sW + 3 * RT_C * RT_LD};
+      f32x16 acc[4];
+      rt_gemm32_multi<4>(ws, cb * 32, n, g, xb, acc);
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int c = cb * 32 + c_row(v, g);
-      oa[c * plane] = f2bf(m * sigmoidf_(ag[v]) * ap[v]);
-      ob[c * plane] = f2bf(m * sigmoidf_(bg[v]) * bp[v]);
+      for (int v = 0; v < 16; ++v) {
+        const int64_t c = cb * 32 + c_row(v, g);
+        oa[c * plane] = f2bf(m * sigmoidf_(acc[1][v]) * acc[0][v]);
+        ob[c * plane] = f2bf(m * sigmoidf_(acc[3][v]) * acc[2][v]);
+      }
     }
   }
 }
@@ -119,7 +79,7 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
                                                             int64_t Np, int64_t N, int64_t nbatch) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[TM_TILE * CT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t sB[TM_TILE * CT_LD];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   // XCD-aware order: the hardware deals workgroups round-robin over 8 XCDs; give each XCD a contiguous run of (plane, tile)
   // work so the 36-ish tiles of one plane share that XCD's L2.
   const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE);
@@ -186,66 +146,88 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 }
 
 // ---------------------------------------------------------------------------------------------------------------- K3 (bf16)
-constexpr int K3_XLD = 32 + 8;       // LDS pitch of the staged X tile [c][32 pixels]
+// Persistent: W_o and W_og live in LDS (70 KB); each wave loads its X tile (issued with the tile's z rows at the top of the
+// iteration; the second wave of the SIMD covers the latency -- a register prefetch of the next tile costs occupancy) X[c][i][j0 .. j0+31] (channel-major, 128 rows of
+// 64 B, 16-byte loads) and scatters it pixel-major into a private LDS slot, so the LN_out / B-operand reads are 16-byte rows,
+// then LN_out(X) W_o^T * sigmoid(LN_in(z) W_og^T) [+ z].
+constexpr int K3_XLD = RT_C + 8;     // LDS pitch of the staged X tile, pixel-major [32 pixels][128 channels]
 
-__global__ void __launch_bounds__(256) trimul_k3_bf16(const uint16_t* zin, uint16_t* out, const uint16_t* __restrict__ X,
+__global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint16_t* out, const uint16_t* __restrict__ X,
                                                       const float* __restrict__ ln_in_w, const float* __restrict__ ln_in_b,
                                                       const float* __restrict__ ln_out_w, const float* __restrict__ ln_out_b, float eps,
                                                       const uint16_t* __restrict__ w_o, const uint16_t* __restrict__ w_og,
-                                                      int64_t N, int64_t Np, int residual) {
-  __shared__ __attribute__((aligned(16))) uint16_t sW[2][32 * TM_WLD];
-  __shared__ __attribute__((aligned(16))) uint16_t sX[4][TM_C * K3_XLD];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t tiles_per_row = Np / 32;
-  const int64_t wt = (int64_t)blockIdx.x * 4 + wave;
-  const int64_t b = blockIdx.y;
-  const int64_t i = wt / tiles_per_row, j0 = (wt % tiles_per_row) * 32, j = j0 + n;
-  const bool live = i < N && j < N;
-  const int64_t pix = (b * N + i) * N + j;
+                                                      int64_t N, int64_t Np, int64_t B, int residual) {
+  __shared__ __attribute__((aligned(16))) uint16_t sW[2 * RT_C * RT_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t sX[RT_WAVES][32 * K3_XLD];
+  __shared__ __attribute__((aligned(16))) float sLNo[2 * RT_C];
+  __shared__ __attribute__((aligned(16))) float sLNi[2 * RT_C];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  rt_stage_affine(sLNo, ln_out_w, ln_out_b, tid, 512);
+  rt_stage_affine(sLNi, ln_in_w, ln_in_b, tid, 512);
+  rt_stage_weights(sW, w_o, RT_C, RT_C, tid, 512);
+  rt_stage_weights(sW + RT_C * RT_LD, w_og, RT_C, RT_C, tid, 512);
+  __syncthreads();
+  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
+  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
   const int64_t plane = Np * Np;
-  // stage X[c][i][j0 .. j0+31] (128 rows of 64 bytes) for this wave
   uint16_t* sx = sX[wave];
-  if (i < N) {
-    const uint16_t* xs = X + b * TM_C * plane + i * Np + j0;
+  int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave;
+  u32x4 rx[8], rz[8];
+  auto fetch = [&](int64_t tt) {
+    const int64_t b = tt / per_b, i = (tt % per_b) / tpr, j0 = (tt % tpr) * 32, j = j0 + n;
+    const uint16_t* xs = X + b * RT_C * plane + i * Np + j0;      // X rows are padded to Np: the 32 columns are in bounds
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
       const int q = l + 64 * it, c = q >> 2, ch = q & 3;
-      *reinterpret_cast<u32x4*>(&sx[c * K3_XLD + ch * 8]) = *reinterpret_cast<const u32x4*>(xs + (int64_t)c * plane + ch * 8);
+      rx[it] = *reinterpret_cast<const u32x4*>(xs + (int64_t)c * plane + ch * 8);
     }
-  }
-  __syncthreads();
-  float xv[64];
+    const bool live = j < N;
+    rt_load(zin + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
+  };
+  for (; t < total; t += stride) {
+    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+    const bool live = j < N;
+    const int64_t pix = (b * N + i) * N + j;
+    fetch(t);
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+    for (int it = 0; it < 8; ++it) {
+      const int q = l + 64 * it, c = q >> 2, p0 = (q & 3) * 8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xv[8 * t + e] = live ? bf2f(sx[(64 * g + 8 * t + e) * K3_XLD + n]) : 0.f;
-  bf16x8 xo[8];
-  ln128_from_regs(xv, g, ln_out_w, ln_out_b, eps, xo);
-  load_row128(zin + pix * TM_C, live, g, xv);
-  bf16x8 xi[8];
-  ln128_from_regs(xv, g, ln_in_w, ln_in_b, eps, xi);
-  for (int cb = 0; cb < 4; ++cb) {
-    __syncthreads();
-    stage_w32(sW[0], w_o, cb * 32, tid);
-    stage_w32(sW[1], w_og, cb * 32, tid);
-    __syncthreads();
-    const f32x16 o = gemm_rows32(sW[0], n, g, xo);
-    const f32x16 gt = gemm_rows32(sW[1], n, g, xi);
-    if (!live) continue;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c0 = cb * 32 + 8 * q + 4 * g;
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = sigmoidf_(gt[4 * q + e]) * o[4 * q + e];
-      if (residual) {
-        const u32x2 r = *reinterpret_cast<const u32x2*>(zin + pix * TM_C + c0);
-        y[0] += lo_bf(r[0]);
-        y[1] += hi_bf(r[0]);
-        y[2] += lo_bf(r[1]);
-        y[3] += hi_bf(r[1]);
+      for (int e = 0; e < 4; ++e) {
+        sx[(p0 + 2 * e) * K3_XLD + c] = (uint16_t)(rx[it][e] & 0xffff);
+        sx[(p0 + 2 * e + 1) * K3_XLD + c] = (uint16_t)(rx[it][e] >> 16);
       }
-      *reinterpret_cast<u32x2*>(out + pix * TM_C + c0) = u32x2{pack2(y[0], y[1]), pack2(y[2], y[3])};
+    }
+    rt_wave_lds_sync();
+    u32x4 xr[8];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) xr[tt] = *reinterpret_cast<const u32x4*>(&sx[n * K3_XLD + 64 * g + 8 * tt]);
+    rt_wave_lds_sync();
+    bf16x8 xo[8], xi[8];
+    rt_ln(xr, g, sLNo, eps, xo);
+    __builtin_amdgcn_sched_barrier(0);      // one LayerNorm's temporaries at a time
+    rt_ln(rz, g, sLNi, eps, xi);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 1
+    for (int cb = 0; cb < 4; ++cb) {
+      const f32x16 o = rt_gemm32(sW, cb * 32, n, g, xo);
+      const f32x16 gt = rt_gemm32(sW + RT_C * RT_LD, cb * 32, n, g, xi);
+      if (!live) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c0 = cb * 32 + 8 * q + 4 * g;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = sigmoidf_(gt[4 * q + e]) * o[4 * q + e];
+        if (residual) {
+          const u32x2 r = *reinterpret_cast<const u32x2*>(zin + pix * RT_C + c0);
+          y[0] += lo_bf(r[0]);
+          y[1] += hi_bf(r[0]);
+          y[2] += lo_bf(r[1]);
+          y[3] += hi_bf(r[1]);
+        }
+        *reinterpret_cast<u32x2*>(out + pix * RT_C + c0) = u32x2{pack2(y[0], y[1]), pack2(y[2], y[3])};
+      }
     }
   }
 }
@@ -463,19 +445,21 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
     uint16_t* pa = static_cast<uint16_t*>(a->workspace);
     uint16_t* pb = pa + B * TM_C * Np * Np;
     uint16_t* X = pb + B * TM_C * Np * Np;
-    const int64_t waves = Np * Np / 32;
-    hipLaunchKernelGGL(trimul_k1_bf16, dim3((unsigned)(waves / 4), (unsigned)B), dim3(256), 0, st, (const uint16_t*)a->z, a->mask, a->ln_in_w,
-                       a->ln_in_b, a->eps, (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg,
-                       pa, pb, N, Np, a->outgoing);
+    const int64_t k1_tiles = B * Np * (Np / 32);
+    const unsigned k1_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k1_tiles, RT_WAVES));
+    hipLaunchKernelGGL(trimul_k1_bf16, dim3(k1_grid), dim3(512), 0, st, (const uint16_t*)a->z, a->mask, a->ln_in_w, a->ln_in_b, a->eps,
+                       (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B,
+                       a->outgoing);
     int rc = launched(err, errlen, "trimul_k1_bf16");
     if (rc) return rc;
     const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE) * B * TM_C;
     hipLaunchKernelGGL(trimul_contract_bf16, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, N, B * TM_C);
     rc = launched(err, errlen, "trimul_contract_bf16");
     if (rc) return rc;
-    hipLaunchKernelGGL(trimul_k3_bf16, dim3((unsigned)(waves / 4), (unsigned)B), dim3(256), 0, st, (const uint16_t*)a->z, (uint16_t*)a->out, X,
-                       a->ln_in_w, a->ln_in_b, a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np,
-                       a->residual);
+    const int64_t k3_tiles = B * N * cdiv(N, 32);
+    const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
+    hipLaunchKernelGGL(trimul_k3_bf16, dim3(k3_grid), dim3(512), 0, st, (const uint16_t*)a->z, (uint16_t*)a->out, X, a->ln_in_w, a->ln_in_b,
+                       a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np, B, a->residual);
     return launched(err, errlen, "trimul_k3_bf16");
   }
   if (a->dtype == FPF_DT_F32) {
