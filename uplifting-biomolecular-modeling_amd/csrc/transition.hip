@@ -5,9 +5,10 @@
 // B operand of v_mfma_f32_32x32x16_bf16 (lane n%32 = pixel, channels 64*(lane/32) + 8t .. +7 for k-step t).  GEMM 1 is
 // computed transposed, a^T = W_a n^T, so its D layout (lane = pixel, 16 hidden values) IS the B operand of GEMM 2
 // out^T = W_o h^T once the hidden index of each k-step is permuted the same way in W_o: the 4c hidden never leaves the
-// registers.  Weights stream through LDS in 32-hidden chunks shared by the 4 waves of a workgroup.
+// registers.  Weights stream through double-buffered LDS in 32-hidden chunks shared by the 8 waves of a workgroup (the next
+// chunk's global loads are in flight while the current one feeds the MFMAs; one barrier per chunk).
 // fp32 path (exact tier): LDS-tiled scalar FMA, fp32 throughout.
-#include "fpf_common.h"
+#include "rowtile.h"
 
 namespace fpf {
 
@@ -16,104 +17,78 @@ constexpr int TR_KS = TR_C / 16;      // k-steps of GEMM 1
 constexpr int TR_HB = 32;             // hidden rows per chunk
 constexpr int TR_WLD = TR_C + 8;      // LDS pitch of a W_a / W_b chunk row (bf16): 272 B, conflict-free 16-byte reads
 constexpr int TR_OLD = TR_HB + 4;     // LDS pitch of a W_o chunk row (bf16): 72 B, conflict-free 8-byte reads
-
-// Loads 32 pixel rows of 128 bf16 (lane: pixel n, channel half g) and returns LN(x) as 8 B-operand fragments.
-__device__ __forceinline__ void ln128_fragments(const uint16_t* __restrict__ xrow, bool live, int g, const float* __restrict__ ln_w,
-                                                const float* __restrict__ ln_b, float eps, bf16x8 (&xb)[TR_KS]) {
-  float xv[64];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    u32x4 r = live ? *reinterpret_cast<const u32x4*>(xrow + 64 * g + 8 * t) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xv[8 * t + 2 * e] = lo_bf(r[e]);
-      xv[8 * t + 2 * e + 1] = hi_bf(r[e]);
-    }
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) s += xv[i];
-  s = half_sum(s);
-  const float mean = s * (1.0f / 128.0f);
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const float d = xv[i] - mean;
-    q += d * d;
-  }
-  q = half_sum(q);
-  const float rstd = 1.0f / sqrtf(q * (1.0f / 128.0f) + eps);
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int c0 = 64 * g + 8 * t;
-    f32x4 w0 = ln_w ? *reinterpret_cast<const f32x4*>(ln_w + c0) : f32x4{1, 1, 1, 1};
-    f32x4 w1 = ln_w ? *reinterpret_cast<const f32x4*>(ln_w + c0 + 4) : f32x4{1, 1, 1, 1};
-    f32x4 b0 = ln_b ? *reinterpret_cast<const f32x4*>(ln_b + c0) : f32x4{0, 0, 0, 0};
-    f32x4 b1 = ln_b ? *reinterpret_cast<const f32x4*>(ln_b + c0 + 4) : f32x4{0, 0, 0, 0};
-    float y[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      y[e] = (xv[8 * t + e] - mean) * rstd * w0[e] + b0[e];
-      y[4 + e] = (xv[8 * t + 4 + e] - mean) * rstd * w1[e] + b1[e];
-    }
-    xb[t] = as_bf8(u32x4{pack2(y[0], y[1]), pack2(y[2], y[3]), pack2(y[4], y[5]), pack2(y[6], y[7])});
-  }
-}
+constexpr int TR_WAVES = 8;           // waves per workgroup (2 per SIMD), 32 pixel rows each
 
 template <int PW>
-__global__ void __launch_bounds__(256) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
+__global__ void __launch_bounds__(512) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
                                                               const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ wa,
                                                               const uint16_t* __restrict__ wb, const uint16_t* __restrict__ wo,
                                                               const float* __restrict__ mask, int residual, int64_t rows, int hidden) {
-  __shared__ __attribute__((aligned(16))) uint16_t sWa[TR_HB * TR_WLD];
-  __shared__ __attribute__((aligned(16))) uint16_t sWb[TR_HB * TR_WLD];
-  __shared__ __attribute__((aligned(16))) uint16_t sWo[TR_C * TR_OLD];
+  // double-buffered weight chunks: W_a / W_b rows hb*32 .. +31 (all 128 inputs) and W_o columns hb*32 .. +31 (all 128 outputs)
+  __shared__ __attribute__((aligned(16))) uint16_t sWa[2][TR_HB * TR_WLD];
+  __shared__ __attribute__((aligned(16))) uint16_t sWb[2][TR_HB * TR_WLD];
+  __shared__ __attribute__((aligned(16))) uint16_t sWo[2][TR_C * TR_OLD];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t pix0 = ((int64_t)blockIdx.x * 4 + wave) * (32 * PW);
-
+  const int64_t pix0 = ((int64_t)blockIdx.x * TR_WAVES + wave) * (32 * PW);
+  // staging map: 1536 16-byte chunks per weight chunk (512 W_a, 512 W_b, 512 W_o), 3 per thread
+  const int sr = tid >> 4, sc = tid & 15;          // W_a / W_b: row, 16-byte column
+  const int so = tid >> 2, soc = tid & 3;          // W_o: row (c_out), 16-byte column within the 32 hidden
+  u32x4 pa, pb, po;
+  auto gload = [&](int hb) {
+    pa = *reinterpret_cast<const u32x4*>(wa + (int64_t)(hb * TR_HB + sr) * TR_C + sc * 8);
+    pb = *reinterpret_cast<const u32x4*>(wb + (int64_t)(hb * TR_HB + sr) * TR_C + sc * 8);
+    po = *reinterpret_cast<const u32x4*>(wo + (int64_t)so * hidden + hb * TR_HB + soc * 8);
+  };
+  auto lstore = [&](int buf) {
+    *reinterpret_cast<u32x4*>(&sWa[buf][sr * TR_WLD + sc * 8]) = pa;
+    *reinterpret_cast<u32x4*>(&sWb[buf][sr * TR_WLD + sc * 8]) = pb;
+    *reinterpret_cast<u32x2*>(&sWo[buf][so * TR_OLD + soc * 8]) = u32x2{po[0], po[1]};
+    *reinterpret_cast<u32x2*>(&sWo[buf][so * TR_OLD + soc * 8 + 4]) = u32x2{po[2], po[3]};
+  };
+  __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
+  rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
+  gload(0);
+  lstore(0);
+  __syncthreads();
   bf16x8 xb[PW][TR_KS];
 #pragma unroll
   for (int p = 0; p < PW; ++p) {
     const int64_t pix = pix0 + 32 * p + n;
-    ln128_fragments(x + pix * TR_C, pix < rows, g, ln_w, ln_b, eps, xb[p]);
+    u32x4 raw[8];
+    rt_load(x + (pix < rows ? pix : 0) * TR_C, pix < rows, g, raw);
+    rt_ln(raw, g, sLN, eps, xb[p]);
   }
   f32x16 acc[PW][4];
 #pragma unroll
   for (int p = 0; p < PW; ++p)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) acc[p][cb] = f32x16{};
-
   const int nhb = hidden / TR_HB;
   for (int hb = 0; hb < nhb; ++hb) {
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int i = tid + 256 * it;
-      const int r = i >> 4, ch = i & 15;
-      const int64_t src = (int64_t)(hb * TR_HB + r) * TR_C + ch * 8;
-      *reinterpret_cast<u32x4*>(&sWa[r * TR_WLD + ch * 8]) = *reinterpret_cast<const u32x4*>(wa + src);
-      *reinterpret_cast<u32x4*>(&sWb[r * TR_WLD + ch * 8]) = *reinterpret_cast<const u32x4*>(wb + src);
-      const int ro = i >> 2, co = i & 3;
-      const u32x4 w = *reinterpret_cast<const u32x4*>(wo + (int64_t)ro * hidden + hb * TR_HB + co * 8);
-      *reinterpret_cast<u32x2*>(&sWo[ro * TR_OLD + co * 8]) = u32x2{w[0], w[1]};
-      *reinterpret_cast<u32x2*>(&sWo[ro * TR_OLD + co * 8 + 4]) = u32x2{w[2], w[3]};
-    }
-    __syncthreads();
+    const int buf = hb & 1;
+    if (hb + 1 < nhb) gload(hb + 1);
     f32x16 a[PW], b[PW];
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
       a[p] = f32x16{};
       b[p] = f32x16{};
     }
+    const uint16_t* ra = &sWa[buf][n * TR_WLD + 64 * g];
+    const uint16_t* rb = &sWb[buf][n * TR_WLD + 64 * g];
+    bf16x8 fa = as_bf8(*reinterpret_cast<const u32x4*>(ra)), fb = as_bf8(*reinterpret_cast<const u32x4*>(rb));
 #pragma unroll
     for (int t = 0; t < TR_KS; ++t) {
-      const bf16x8 fa = as_bf8(*reinterpret_cast<const u32x4*>(&sWa[n * TR_WLD + 64 * g + 8 * t]));
-      const bf16x8 fb = as_bf8(*reinterpret_cast<const u32x4*>(&sWb[n * TR_WLD + 64 * g + 8 * t]));
+      const bf16x8 ca = fa, cbf = fb;
+      if (t + 1 < TR_KS) {                      // one k-step of fragment lookahead
+        fa = as_bf8(*reinterpret_cast<const u32x4*>(ra + 8 * (t + 1)));
+        fb = as_bf8(*reinterpret_cast<const u32x4*>(rb + 8 * (t + 1)));
+      }
 #pragma unroll
       for (int p = 0; p < PW; ++p) {
-        a[p] = mfma32(fa, xb[p][t], a[p]);
-        b[p] = mfma32(fb, xb[p][t], b[p]);
+        a[p] = mfma32(ca, xb[p][t], a[p]);
+        b[p] = mfma32(cbf, xb[p][t], b[p]);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     // h = silu(a) * b; registers 8s .. 8s+7 form the B operand of k-step s (hidden 16s + 8(e/4) + 4g + e%4)
     bf16x8 hf[PW][2];
@@ -126,23 +101,27 @@ __global__ void __launch_bounds__(256) transition_bf16_kernel(const uint16_t* x,
         for (int e = 0; e < 4; ++e) {
           const int v0 = 8 * s + 2 * e;
           const float a0 = a[p][v0], a1 = a[p][v0 + 1];
-          const float h0 = a0 / (1.0f + __expf(-a0)) * b[p][v0];
-          const float h1 = a1 / (1.0f + __expf(-a1)) * b[p][v0 + 1];
+          const float h0 = siluf_(a0) * b[p][v0];
+          const float h1 = siluf_(a1) * b[p][v0 + 1];
           w[e] = pack2(h0, h1);
         }
         hf[p][s] = as_bf8(u32x4{w[0], w[1], w[2], w[3]});
       }
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < 4; ++cb) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const uint16_t* wrow = &sWo[(cb * 32 + n) * TR_OLD + 16 * s + 4 * g];
+        const uint16_t* wrow = &sWo[buf][(cb * 32 + n) * TR_OLD + 16 * s + 4 * g];
         const u32x2 lo = *reinterpret_cast<const u32x2*>(wrow);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(wrow + 8);
         const bf16x8 fo = as_bf8(u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
         for (int p = 0; p < PW; ++p) acc[p][cb] = mfma32(fo, hf[p][s], acc[p][cb]);
       }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (hb + 1 < nhb) lstore(buf ^ 1);        // buf ^ 1 was last read before the previous barrier
+    __syncthreads();
   }
   // epilogue: lane (pixel n, half g) holds c_out = 32 cb + 8 q + 4 g + 0..3 in registers 4q .. 4q+3
 #pragma unroll
@@ -267,7 +246,7 @@ extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char
         (a->ln_w && !aligned16(a->ln_w)) || (a->ln_b && !aligned16(a->ln_b)))
       return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
     const int PW = 1;
-    const dim3 grid((unsigned)cdiv(a->rows, 128 * PW)), block(256);
+    const dim3 grid((unsigned)cdiv(a->rows, 32 * TR_WAVES * PW)), block(64 * TR_WAVES);
     hipLaunchKernelGGL((transition_bf16_kernel<PW>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b, a->eps,
                        (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows, a->hidden);
     return launched(err, errlen, "fpf_transition_fwd(bf16)");

@@ -66,6 +66,7 @@ template <bool VT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_R][TA_KT * TA_KLD];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_R][TA_D * TA_VLD];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ[TA_R][128 * TA_KLD];
   __shared__ uint64_t sKeep[TA_R];
   __shared__ int sAlive[TA_R];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
@@ -83,8 +84,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const float c2 = p.scale * LOG2E;                     // qk units -> log2 units
   const float inv_scale = 1.0f / p.scale;
 
-  // row liveness: a row with no kept key is "dead" and attends uniformly to every key
+  // Q tile of the R rows -> LDS (read back as B-operand fragments every sub-tile); row liveness
   if (tid < TA_R) sAlive[tid] = 0;
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int c = tid + 256 * it, r = c >> 9, qq = (c >> 2) & 127, part = c & 3;
+    const int64_t i = i0 + r, qg = qt * 128 + qq;
+    *reinterpret_cast<u32x4*>(&sQ[r][qq * TA_KLD + 8 * part]) =
+        (i < p.N && qg < p.S) ? *reinterpret_cast<const u32x4*>(p.q + b * p.qs[0] + i * p.qs[1] + h * p.qs[2] + qg * p.qs[3] + 8 * part)
+                              : u32x4{0, 0, 0, 0};
+  }
   __syncthreads();
   for (int r = 0; r < TA_R; ++r) {
     const int64_t i = i0 + r;
@@ -101,17 +110,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     dead[r] = (i0 + r < p.N) && !sAlive[r];
     dead_any |= dead[r];
   }
+  const bool wave_row_dead = !sAlive[wave];
 
-  // Q fragments (B operand of S^T = K Q^T): query n, d = 16t + 8g .. +7
-  bf16x8 qf[TA_R][2];
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    const int64_t i = i0 + r;
-    const bool ok = qlive && i < p.N;
-    const uint16_t* qp = p.q + b * p.qs[0] + i * p.qs[1] + h * p.qs[2] + q * p.qs[3];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) qf[r][t] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16 * t + 8 * g) : u32x4{0, 0, 0, 0});
-  }
   f32x16 o[TA_R];
   float mrow[TA_R], lrow[TA_R];                         // running max (log2 units) and this lane's partial sum
 #pragma unroll
@@ -122,22 +122,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
   // staging: 1024 16-byte chunks per operand per tile, 4 per thread; element offsets at key 0 are computed once
-  int64_t koff[4], voff[4];
+  // chunk `it` of a thread belongs to row i0 + it (256 threads x 4 chunks): row bases are wave-uniform, the in-row part per lane
+  int64_t kbase[4], vbase[4];
   bool rowok[4];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int c = tid + 256 * it;
-    const int64_t i = i0 + (c >> 8);
+    const int64_t i = i0 + it;
     rowok[it] = i < p.N;
     const int64_t ii = rowok[it] ? i : i0;
-    koff[it] = b * p.ks[0] + ii * p.ks[1] + h * p.ks[2] + ((c >> 2) & 63) * p.ks[3] + 8 * (c & 3);
-    if constexpr (VT)
-      voff[it] = b * p.vs[0] + ii * p.vs[1] + h * p.vs[2] + ((c >> 3) & 31) * p.vs[3] + 8 * (c & 7);
-    else
-      voff[it] = b * p.vs[0] + ii * p.vs[1] + h * p.vs[2] + ((c >> 2) & 63) * p.vs[3] + 8 * (c & 3);
+    kbase[it] = b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
+    vbase[it] = b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
+  }
+  const int64_t kin = ((tid >> 2) & 63) * p.ks[3] + 8 * (tid & 3);
+  const int64_t vin = VT ? ((tid >> 3) & 31) * p.vs[3] + 8 * (tid & 7) : ((tid >> 2) & 63) * p.vs[3] + 8 * (tid & 3);
+  int64_t koff[4], voff[4];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    koff[it] = kbase[it] + kin;
+    voff[it] = vbase[it] + vin;
   }
   u32x4 rk[4], rv[4];
+  bool keepn;                                           // prefetched mask bit: row i0 + wave, key k0 + l of the next tile
   auto gload = [&](int64_t k0) {
+    {
+      const int64_t i = i0 + wave, key = k0 + l;
+      keepn = key < p.S && i < p.N && (wave_row_dead || mask_keep(p, b, i, key));
+    }
     if (k0 + TA_KT <= p.S) {                              // whole tile in range (uniform)
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
@@ -164,8 +174,31 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
   };
+  // bias of one 32-key sub-tile (raw values, keys kb + 8 qd + 4 g + 0..3), prefetched one sub-tile ahead
+  const int64_t bias_row = b * p.bs[0] + h * p.bs[1] + (qlive ? q : 0) * p.bs[2];
+  auto bload = [&](int64_t kb, f32x16& dst) {
+    const int64_t kb0 = kb + 4 * g;
+    if (p.bias_vec && kb + 32 <= p.S) {
+      const float* bp = static_cast<const float*>(p.bias) + bias_row + kb0;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(bp + 8 * qd);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[4 * qd + e] = v4[e];
+      }
+    } else {
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t key = kb0 + 8 * qd + e;
+          dst[4 * qd + e] = key < p.S ? bias_at(p, bias_row + key * p.bs[3]) : 0.f;
+        }
+    }
+  };
   gload(0);
-  const int64_t bias_row = b * p.bs[0] + h * p.bs[1] + q * p.bs[2];
+  f32x16 bnext;
+  bload(0, bnext);
   for (int64_t k0 = 0; k0 < p.S; k0 += TA_KT) {
     __syncthreads();
 #pragma unroll
@@ -186,10 +219,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
       }
     }
-    {   // keep bits of row `wave` for this tile: lane l <-> key k0 + l (dead rows keep every in-range key)
-      const int64_t i = i0 + wave, key = k0 + l;
-      const bool keep = key < p.S && i < p.N && (!sAlive[wave] || mask_keep(p, b, i, key));
-      const uint64_t bal = __ballot(keep);
+    {
+      const uint64_t bal = __ballot(keepn);               // keep bits of row `wave`: lane l <-> key k0 + l
       if (l == 0) sKeep[wave] = bal;
     }
     __syncthreads();
@@ -200,33 +231,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       kall &= sKeep[r];
       kany |= sKeep[r];
     }
-    if (kany == 0) continue;                              // no row keeps a key of this tile
     const bool full = (kall == ~0ull) && !dead_any;       // uniform: no masking work in this tile
 #pragma unroll 1
     for (int sub = 0; sub < 2; ++sub) {
-      // bias tile (qk units) as the accumulator's initial value: keys 32 sub + 8 qd + 4 g + 0..3
       f32x16 bt;
-      const int64_t kb0 = k0 + 32 * sub + 4 * g;
-      if (p.bias_vec && qlive && k0 + TA_KT <= p.S) {
-        const float* bp = static_cast<const float*>(p.bias) + bias_row + kb0;
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const f32x4 v4 = *reinterpret_cast<const f32x4*>(bp + 8 * qd);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bt[4 * qd + e] = v4[e] * inv_scale;
-        }
-      } else {
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int64_t key = kb0 + 8 * qd + e;
-            bt[4 * qd + e] = (qlive && key < p.S) ? bias_at(p, bias_row + key * p.bs[3]) * inv_scale : 0.f;
-          }
+      for (int v = 0; v < 16; ++v) bt[v] = bnext[v] * inv_scale;      // qk units: the accumulator's initial value
+      {
+        const int64_t kn = sub == 0 ? k0 + 32 : k0 + TA_KT;             // prefetch the next sub-tile's bias
+        if (kn < p.S) bload(kn, bnext);
       }
+      if ((uint32_t)(kany >> (32 * sub)) == 0) continue;               // no row keeps a key of this sub-tile
       f32x16 s[TA_R];
 #pragma unroll
-      for (int r = 0; r < TA_R; ++r) s[r] = qk_tile(sK[r], sub, n, g, qf[r], bt);
+      for (int r = 0; r < TA_R; ++r) {
+        const uint16_t* qr = &sQ[r][(wave * 32 + n) * TA_KLD + 8 * g];
+        const bf16x8 qf[2] = {as_bf8(*reinterpret_cast<const u32x4*>(qr)), as_bf8(*reinterpret_cast<const u32x4*>(qr + 16))};
+        s[r] = qk_tile(sK[r], sub, n, g, qf, bt);
+      }
       if (!full) {
 #pragma unroll
         for (int r = 0; r < TA_R; ++r) {
@@ -263,15 +285,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int r = 0; r < TA_R; ++r) {
         const float mb = (mrow[r] == -INFINITY) ? 0.f : mrow[r];
         uint32_t pk[8];
-        float ps = lrow[r];
+        float ps0 = lrow[r], ps1 = 0.f;
 #pragma unroll
         for (int v = 0; v < 16; v += 2) {
           const float p0 = fast_exp2(fmaf(s[r][v], c2, -mb));
           const float p1 = fast_exp2(fmaf(s[r][v + 1], c2, -mb));
           pk[v >> 1] = pack2(p0, p1);
-          ps = dot2_bf16(pk[v >> 1], ps);         // the row sum of the bf16 P the PV MFMA consumes
+          if (v & 2) ps1 = dot2_bf16(pk[v >> 1], ps1);      // the row sum of the bf16 P the PV MFMA consumes
+          else ps0 = dot2_bf16(pk[v >> 1], ps0);
         }
-        lrow[r] = ps;
+        lrow[r] = ps0 + ps1;
         const uint16_t* vr = sV[r] + n * TA_VLD + 32 * sub + 4 * g;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
