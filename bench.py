@@ -2,6 +2,7 @@
 """bench.py -- one Pairformer pair block (the hot path) on one MI355X: ms, TFLOP/s and fraction of the bf16 MFMA roofline.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--n 768] [--no-cpu]
+    python bench.py --probe triattn_core|copy [--n 768] [--steps 5]     (launch-only runs for rocprofv3 --pmc passes)
 
 Step = one pair block on a resident z [1, N, N, 128] bf16, in place, in the reference order (trimul outgoing, trimul incoming,
 tri-att starting node, tri-att ending node, transition 4x): 13 launches of libfpf_hip on torch's current stream.  Synthetic
@@ -46,6 +47,59 @@ def time_events(fn, reps, torch):
     return s.elapsed_time(e) / reps
 
 
+def time_raw(entry, args, reps, torch):
+    """Mean ms per call of one C-ABI entry point called back to back with a prebuilt argument block (HIP events on torch's
+    current stream, the stream the library launches on)."""
+    import ctypes
+    from fpf_hip import _lib as L
+    fn = getattr(L.lib(), entry)
+    st = L.stream_ptr()
+    err = ctypes.create_string_buffer(512)
+    ref = ctypes.byref(args)
+    if fn(ref, st, err, 512) != 0:
+        raise RuntimeError("%s: %s" % (entry, err.value.decode()))
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn(ref, st, err, 512)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def ln_args(x, y, w, b):
+    from fpf_hip import _lib as L
+    C = x.shape[-1]
+    return L.LnArgs(abi_version=L.ABI_VERSION, dtype_in=L.DT_BF16, dtype_out=L.DT_BF16, cols=C, rows=x.numel() // C, x=L.ptr(x),
+                    x_row_stride=C, y=L.ptr(y), y_row_stride=C, gamma=L.ptr(w), beta=L.ptr(b), eps=1e-5)
+
+
+def probe(kind, N, reps):
+    """Launch-only runs for hardware-counter passes (rocprofv3 --pmc): `triattn_core` = the core at the block's shape, reps
+    times; `copy` = a device copy of a known byte count (the calibration kernel for FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+    from fpf_hip.kernels import triattn as TA
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(0)
+    if kind == "triattn_core":
+        q, k, v = (torch.randn(1, N, 4, N, 32, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
+        bias = (torch.randn(1, 1, 4, N, N, generator=g) * 0.5).to(dev)
+        kmask = torch.ones(1, N, 1, 1, N, dtype=torch.bool, device=dev)
+        o = torch.empty_like(q)
+        for _ in range(reps):
+            TA.triangle_attention(q, k, v, bias, kmask, word="fast", out=o)
+    elif kind == "copy":
+        x = torch.randn(N * N * 128, generator=g).to(torch.bfloat16).to(dev)
+        y = torch.empty_like(x)
+        for _ in range(reps):
+            y.copy_(x)
+    else:
+        raise SystemExit("unknown probe %r (triattn_core | copy)" % kind)
+    torch.cuda.synchronize()
+    print("probe %s N=%d reps=%d done" % (kind, N, reps), flush=True)
+
+
 def cpu_baseline(torch):
     """The stock PyTorch statements (restated in oracle/stock.py) timed on this host: one BASELINE config-1 block
     (N = 64, c_z = 128, 4 x 32 heads, transition 4x, fp32), 2 warm-ups then the median of 5."""
@@ -74,11 +128,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--n", type=int, default=768)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe", default=None, help="launch-only run for counter passes: triattn_core | copy")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this build runs the pair stack on a single MI355X (multi-GPU row sharding is a design "
               "note, not built); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if a.probe:
+        probe(a.probe, a.n, a.steps)
+        return
     import torch
     from fpf_hip import pairformer as PFM
     from fpf_hip.kernels import triattn as TA
@@ -128,10 +186,12 @@ def main():
         breakdown[name] = {"ms": round(t, 4), "tflops": round(f / (t * 1e-3) / 1e12, 1), "mfma_frac": round(f / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
     zbytes = N * N * 128 * 2
     breakdown["transition"]["hbm_gbs_min_bytes"] = round(2 * zbytes / (breakdown["transition"]["ms"] * 1e-3) / 1e9, 1)
-    # standalone LayerNorm (HBM-bound): z in, bf16 out
+    # standalone LayerNorm (HBM-bound): z in, bf16 out.  A 50 us kernel: timed through the C ABI with the argument block built
+    # once (what a ctypes caller does), so the face's per-call Python work does not leave the GPU idle between launches.
     yln = torch.empty_like(zb)
     lw, lb = torch.ones(128, device=dev), torch.zeros(128, device=dev)
-    t_ln = time_events(lambda: LN.layer_norm(zb, (128,), lw, lb, 1e-5, word="fast", out=yln), reps, torch)
+    LN.layer_norm(zb, (128,), lw, lb, 1e-5, word="fast", out=yln)
+    t_ln = time_raw("fpf_layernorm_fwd", ln_args(zb, yln, lw, lb), 4 * reps, torch)
     breakdown["layernorm"] = {"ms": round(t_ln, 4), "hbm_gbs": round(2 * zbytes / (t_ln * 1e-3) / 1e9, 1),
                               "hbm_frac": round(2 * zbytes / (t_ln * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 

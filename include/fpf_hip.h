@@ -178,6 +178,46 @@ typedef struct {
 size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int32_t C, int32_t H, int32_t D, int32_t dtype);
 int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen);
 
+/* ---------------------------------------------------------------------------------------------------------------- triangle attention (block stages)
+ * The block's prologue and epilogue as separate calls, for callers that run their own core between them.
+ * Prologue replaces common/opt_core/opt_core/attn/pair_fused.py:1136 prologue (-> q, k, v, g, bias in the attention frame
+ * x = z or z^T): x_ln = LN(x); q|k|v|g = x_ln W_qkvg^T; bias = x_ln W_b^T.
+ * Epilogue replaces pair_fused.py:1416 epilogue: u = (sigmoid(g) * o) W_o^T, written in z's frame (the ending node's u[i, j]
+ * lands at pixel (j, i)), or added to z in place. */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* FPF_DT_BF16 (C = 128, H*D = 128, D = 32) | FPF_DT_F32 (C, H*D <= 128) */
+  int64_t B, N;
+  int32_t C, H, D;
+  const void* z;           /* [B, N, N, C] contiguous, z's own frame */
+  const float* ln_w;       /* [C] or NULL */
+  const float* ln_b;
+  float eps;
+  const void* w_qkvg;      /* [4*H*D, C] rows q | k | v | g */
+  const void* w_b;         /* [H, C] */
+  int32_t ending;          /* 1: attention frame x = z^T (read by address) */
+  void* q;                 /* [B, I, H, J, D] contiguous */
+  void* k;                 /* [B, I, H, J, D] */
+  void* v;                 /* bf16: [B, I, H, D, J] (stored transposed, the core's v_layout 1); fp32: [B, I, H, J, D] */
+  void* g;                 /* [B, I, J, H*D] pre-sigmoid */
+  float* bias;             /* [B, H, I, J] fp32 (the [B,1,H,I,J] operand without its unit axis) */
+} FpfTriattnPrologueArgs;
+int fpf_triattn_prologue_fwd(const FpfTriattnPrologueArgs* a, void* stream, char* err, size_t errlen);
+
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* as the prologue */
+  int64_t B, N;
+  int32_t C, H, D;
+  const void* o;           /* [B, I, H, J, D] contiguous (the core's output) */
+  const void* g;           /* [B, I, J, H*D] pre-sigmoid */
+  const void* w_o;         /* [C, H*D] */
+  int32_t ending;
+  int32_t residual;        /* 1: out is z and z += u in place */
+  void* out;               /* [B, N, N, C] in z's frame */
+} FpfTriattnEpilogueArgs;
+int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* stream, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,8 +72,9 @@ def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_ste
     """Stock TriangleAttention{Starting,Ending}Node forward -> the update in z's frame ([B,N,N,C] or [N,N,C]).
     P: dict ln_w, ln_b [C], w_q, w_k, w_v, w_g [H*D, C], w_b [H, C], w_o [C, H*D], plus ints H, D.
     The ending node transposes z (and the mask) in and the update out (attention.py:140-142, :175-176).
-    Pinned by: ending(z) == starting(z^T)^T, the op form (triangle_attention_op) on the same projections, and the BASELINE
-    config-1 block (tests/test_oracle.py)."""
+    Pinned by: scalar loops over the published equations (starting and ending node each in its own index form), ending(z) ==
+    starting(z^T)^T, the op form (triangle_attention_op) on the same projections, and the BASELINE config-1 block
+    (tests/test_oracle.py)."""
     z4, sq = _as4(z)
     B, N, _, C = z4.shape
     H, D = int(P["H"]), int(P["D"])

@@ -1,0 +1,91 @@
+"""The C ABI without a GPU: libfpf_hip.so loads, exports every entry point include/fpf_hip.h declares, reports its version,
+and the ctypes argument blocks match the header's field order.  No compute call is made (there is no device here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "fpf_hip.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:int|size_t|const char\*)\s+(fpf_\w+)\s*\(", txt, flags=re.M)))
+
+
+def _structs():
+    """{struct name: [field names in order]} parsed from the header's typedef blocks."""
+    txt = open(HEADER).read()
+    out = {}
+    for body, name in re.findall(r"typedef struct \{(.*?)\}\s*(\w+);", txt, flags=re.S):
+        fields = []
+        for ln in body.splitlines():
+            ln = re.sub(r"/\*.*?\*/", "", ln).strip()
+            if not ln or ln.startswith("/*") or ln.startswith("*"):
+                continue
+            decl = ln.rstrip(";").strip()
+            m = re.match(r"(?:const\s+)?[\w]+\s*\*?\s*(.+)$", decl)
+            for part in m.group(1).split(","):
+                part = part.strip().lstrip("*").strip()
+                fields.append(re.sub(r"\[.*\]", "", part))
+        out[name] = fields
+    return out
+
+
+def test_header_declares_the_entry_points():
+    d = _declared()
+    for must in ("fpf_abi_version", "fpf_describe", "fpf_layernorm_fwd", "fpf_transition_fwd", "fpf_trimul_fwd", "fpf_trimul_workspace_bytes",
+                 "fpf_triattn_fwd", "fpf_triattn_block_fwd", "fpf_triattn_block_workspace_bytes", "fpf_triattn_prologue_fwd",
+                 "fpf_triattn_epilogue_fwd"):
+        assert must in d, must
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from fpf_hip import _lib as L
+    if not os.path.exists(L.LIB_PATH):
+        pytest.fail("libfpf_hip.so is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(L.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(L.ENTRY_POINTS) == _declared(), "ctypes binding and header disagree"
+    assert L.lib().fpf_abi_version() == L.ABI_VERSION
+    assert b"gfx950" in L.lib().fpf_describe()
+
+
+def test_ctypes_blocks_follow_the_header_field_order():
+    from fpf_hip import _lib as L
+    st = _structs()
+    pairs = {"FpfLnArgs": L.LnArgs, "FpfTransitionArgs": L.TransitionArgs, "FpfTrimulArgs": L.TrimulArgs, "FpfTriattnArgs": L.TriattnArgs,
+             "FpfTriattnBlockArgs": L.TriattnBlockArgs, "FpfTriattnPrologueArgs": L.TriattnPrologueArgs,
+             "FpfTriattnEpilogueArgs": L.TriattnEpilogueArgs}
+    assert set(pairs) == set(st), sorted(st)
+    for cname, py in pairs.items():
+        assert [f[0] for f in py._fields_] == st[cname], cname
+
+
+def test_workspace_queries_need_no_device():
+    from fpf_hip import _lib as L
+    lib = L.lib()
+    # trimul: 3 channel-major bf16 planes of Np^2, Np = ceil(N / 128) * 128
+    assert lib.fpf_trimul_workspace_bytes(1, 768, 128, 128, L.DT_BF16) >= 3 * 128 * 768 * 768 * 2
+    assert lib.fpf_trimul_workspace_bytes(1, 100, 128, 128, L.DT_BF16) >= 3 * 128 * 128 * 128 * 2
+    # tri-att block: q, k, v, o, g (H*D per pixel) + fp32 bias (H per pixel)
+    need = lib.fpf_triattn_block_workspace_bytes(1, 768, 128, 4, 32, L.DT_BF16)
+    assert need >= 5 * 768 * 768 * 128 * 2 + 768 * 768 * 4 * 4
+    assert lib.fpf_triattn_block_workspace_bytes(1, 768, 128, 4, 32, L.DT_F32) > need
+
+
+def test_version_mismatch_is_refused_before_any_launch():
+    """A wrong abi_version is rejected by the argument gate (no device work is reached, so this runs without a GPU)."""
+    from fpf_hip import _lib as L
+    a = L.LnArgs(abi_version=L.ABI_VERSION + 1, dtype_in=L.DT_BF16, dtype_out=L.DT_BF16, cols=128, rows=4)
+    with pytest.raises(L.LibError) as e:
+        L.call("fpf_layernorm_fwd", a, None)
+    assert e.value.kind == "version"
+    a = L.TrimulArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, c_z=128, c_h=128, batch=1, n=8)
+    with pytest.raises(L.LibError) as e:
+        L.call("fpf_trimul_fwd", a, None)                  # NULL z / weights
+    assert e.value.kind == "args"

@@ -172,3 +172,68 @@ def test_block_fp32_exact(ending):
     ref = S.tri_attn(z, P, mask, ending=ending, dtype=torch.float64)
     live = slice(0, N - 4) if ending else slice(0, N)
     assert_f32_close(u[:, :, live] if ending else u, ref[:, :, live] if ending else ref, "block fp32 ending=%s" % ending)
+
+
+# ------------------------------------------------------------------------------------------------------------------ block stages
+@pytest.mark.parametrize("ending", [False, True])
+def test_stages_bf16_prologue_core_epilogue(ending):
+    """prologue / core_attention / epilogue as separate faces: each stage against the oracle's stage, and the chain bitwise equal
+    to the fused block (same kernels, same intermediate layout)."""
+    from fpf_hip.attn import pair_fused as PF
+    P = _block_weights(torch.bfloat16, seed=3)
+    W = _pack(P, torch.bfloat16)
+    N = 80
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(31)).to(torch.bfloat16)
+    mask = torch.ones(1, N, N)
+    mask[:, N - 6:, :] = 0
+    mask[:, :, N - 6:] = 0
+    zd, md = z.to(DEV), mask.to(DEV)
+    print("[case] stages bf16 ending=%s N=%d" % (ending, N), flush=True)
+    q, k, v, g, bias = PF.prologue(zd, W, ending=ending)
+    torch.cuda.synchronize()
+    assert v.stride(-1) != 1 and v.stride(-2) == 1          # V handed over transposed, served without a copy
+    rq, rk, rv, rg, rb = S.triatt_prologue(z.float(), P, ending=ending, dtype=torch.float32)
+    for name, got, ref in (("q", q, rq), ("k", k, rk), ("v", v, rv), ("g", g, rg), ("bias", bias, rb)):
+        assert tuple(got.shape) == tuple(ref.shape), name
+        if name == "bias":                                    # fp32 output
+            assert_bf16_close(got, ref, "prologue %s ending=%s" % (name, ending))
+        else:                                                 # bf16 outputs: half an output ulp on top of the bar
+            assert_bf16_residual_close(got, ref, "prologue %s ending=%s" % (name, ending))
+    o = PF.core_attention(q, k, v, bias, PF._key_mask(md, zd, ending), core="tier:fast")
+    u = PF.epilogue(o, g, W, zd, ending=ending, residual=False)
+    torch.cuda.synchronize()
+    ref_o = S.triangle_attention_op(q.float().cpu(), k.float().cpu(), v.float().cpu(), bias.cpu(),
+                                    PF._key_mask(mask, z, ending), dtype=torch.float32)
+    assert_bf16_close(o, ref_o, "core on the prologue's tensors ending=%s" % ending)
+    ref_u = S.triatt_epilogue(o.float().cpu(), g.float().cpu(), P, dtype=torch.float32)
+    assert_bf16_residual_close(u, ref_u, "epilogue ending=%s" % ending)
+    blk = PF.tri_attn_block(zd, W, md, ending=ending, residual=False)
+    torch.cuda.synchronize()
+    assert torch.equal(u.transpose(1, 2) if ending else u, blk), "staged chain differs from the fused block"
+    zz = zd.clone()
+    r = PF.epilogue(o, g, W, zz, ending=ending, residual=True)
+    torch.cuda.synchronize()
+    assert r.data_ptr() == zz.data_ptr()
+    zb = zd.clone()
+    PF.tri_attn_block(zb, W, md, ending=ending, residual=True)
+    torch.cuda.synchronize()
+    assert torch.equal(zz, zb)
+
+
+def test_stages_fp32_exact():
+    from fpf_hip.attn import pair_fused as PF
+    P = _block_weights(torch.float32, seed=4)
+    W = _pack(P, torch.float32)
+    N = 24
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(41))
+    print("[case] stages fp32 N=%d" % N, flush=True)
+    for ending in (False, True):
+        q, k, v, g, bias = PF.prologue(z.to(DEV), W, ending=ending, word="exact")
+        torch.cuda.synchronize()
+        for name, got, ref in zip(("q", "k", "v", "g", "bias"), (q, k, v, g, bias), S.triatt_prologue(z, P, ending=ending, dtype=torch.float64)):
+            assert_f32_close(got, ref, "prologue fp32 %s ending=%s" % (name, ending))
+        o = PF.core_attention(q, k, v, bias, None, core="tier:exact")
+        u = PF.epilogue(o, g, W, ending=ending, residual=False, word="exact")
+        torch.cuda.synchronize()
+        ref = S.tri_attn(z, P, None, ending=ending, dtype=torch.float64)
+        assert_f32_close(u.transpose(1, 2) if ending else u, ref, "staged fp32 ending=%s" % ending)

@@ -113,6 +113,76 @@ def test_tri_attn_ending_is_transposed_starting():
     assert torch.allclose(e, s, atol=1e-12)
 
 
+def _brute_tri_attn(z, P, mask, ending):
+    """Scalar loops over the published triangle-attention equations (AlphaFold 2 supplement, Algorithms 13 / 14), written
+    per element with the ending node in its own index form (keys k run over z[k, j], bias b[k, i]) rather than as a
+    transpose: z_ij <- LN(z_ij); q, k, v, b, g from z_ij; a_ijk = softmax_k(q_ij . k_ik / sqrt(D) + b_jk) (starting) or
+    softmax_k(q_ij . k_kj / sqrt(D) + b_ki) (ending); o_ij = sigmoid(g_ij) * sum_k a_ijk v_ik (v_kj); out_ij = W_o o_ij.
+    Masked keys (mask[i, k] starting, mask[k, j] ending) are left out of the softmax."""
+    import numpy as np
+    zz = z[0].numpy()
+    m = mask[0].numpy()
+    N, C = zz.shape[0], zz.shape[2]
+    H, D = int(P["H"]), int(P["D"])
+    lw, lb = P["ln_w"].numpy(), P["ln_b"].numpy()
+    W = {n: P[n].numpy() for n in ("w_q", "w_k", "w_v", "w_g", "w_b", "w_o")}
+    x = np.zeros_like(zz)
+    for i in range(N):
+        for j in range(N):
+            mu = sum(zz[i, j, c] for c in range(C)) / C
+            var = sum((zz[i, j, c] - mu) ** 2 for c in range(C)) / C
+            for c in range(C):
+                x[i, j, c] = (zz[i, j, c] - mu) / math.sqrt(var + 1e-5) * lw[c] + lb[c]
+
+    def lin(w, i, j, r):
+        return sum(w[r, c] * x[i, j, c] for c in range(C))
+    out = np.zeros((N, N, W["w_o"].shape[0]))
+    for i in range(N):
+        for j in range(N):
+            o = np.zeros(H * D)
+            for h in range(H):
+                logits = []
+                for kx in range(N):
+                    keep = m[i, kx] if not ending else m[kx, j]
+                    if not keep:
+                        continue
+                    dot = 0.0
+                    for d in range(D):
+                        qv = lin(W["w_q"], i, j, h * D + d)
+                        kv = lin(W["w_k"], i, kx, h * D + d) if not ending else lin(W["w_k"], kx, j, h * D + d)
+                        dot += qv * kv
+                    bb = lin(W["w_b"], j, kx, h) if not ending else lin(W["w_b"], kx, i, h)
+                    logits.append((kx, dot / math.sqrt(D) + bb))
+                mx = max(l_ for _, l_ in logits)
+                den = sum(math.exp(l_ - mx) for _, l_ in logits)
+                for d in range(D):
+                    acc = 0.0
+                    for kx, l_ in logits:
+                        vv = lin(W["w_v"], i, kx, h * D + d) if not ending else lin(W["w_v"], kx, j, h * D + d)
+                        acc += math.exp(l_ - mx) / den * vv
+                    gate = 1.0 / (1.0 + math.exp(-lin(W["w_g"], i, j, h * D + d)))
+                    o[h * D + d] = gate * acc
+            for c in range(out.shape[2]):
+                out[i, j, c] = sum(W["w_o"][c, r] * o[r] for r in range(H * D))
+    return torch.from_numpy(out).unsqueeze(0)
+
+
+def test_tri_attn_brute_force_published_equations():
+    g = torch.Generator().manual_seed(11)
+    H, D, C = 2, 3, 6
+    P = {n: torch.randn(H * D, C, generator=g, dtype=torch.float64) / math.sqrt(C) for n in ("w_q", "w_k", "w_v", "w_g")}
+    P.update(w_b=torch.randn(H, C, generator=g, dtype=torch.float64), w_o=torch.randn(5, H * D, generator=g, dtype=torch.float64),
+             ln_w=1 + 0.1 * torch.randn(C, generator=g, dtype=torch.float64), ln_b=0.1 * torch.randn(C, generator=g, dtype=torch.float64), H=H, D=D)
+    z = torch.randn(1, 4, 4, C, generator=g, dtype=torch.float64)
+    mask = torch.ones(1, 4, 4, dtype=torch.float64)
+    mask[0, 0, 3] = 0          # a masked key in row 0 (starting) / column 3 (ending); every row keeps a key
+    mask[0, 2, 1] = 0
+    for ending in (False, True):
+        ref = _brute_tri_attn(z, P, mask, ending)
+        got = S.tri_attn(z, P, mask, ending=ending)
+        assert torch.allclose(got, ref, atol=1e-10, rtol=0), (ending, (got - ref).abs().max().item())
+
+
 def test_tri_attn_equals_prologue_op_epilogue():
     """The stock module statement (additive 1e9 mask) and the op form (-inf mask) agree on rows with a valid key.  On a fully
     masked row they agree only where 1e9 absorbs the logits (fp32: uniform); in fp64 the stock statement keeps softmax(s) there,

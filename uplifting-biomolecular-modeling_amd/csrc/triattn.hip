@@ -772,6 +772,83 @@ extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int32_
   return 5 * r1 + r2;
 }
 
+namespace fpf {
+
+// Shape / alignment gate shared by the block and its two stages.
+static int block_shape_check(int dtype, int64_t B, int C, int64_t H, int64_t D, char* err, size_t errlen) {
+  if (B > 65535) return fail(err, errlen, FPF_E_SHAPE, "B above 65535");
+  if (dtype == FPF_DT_BF16) {
+    if (C != TP_C || H * D != TP_HD || D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 block serves C = 128, H*D = 128, D = 32");
+    return FPF_OK;
+  }
+  if (dtype == FPF_DT_F32) {
+    if (C > PF_CM || H * D > PF_CM || C <= 0 || H <= 0 || D <= 0) return fail(err, errlen, FPF_E_SHAPE, "fp32 block serves C, H*D <= 128");
+    return FPF_OK;
+  }
+  return fail(err, errlen, FPF_E_DTYPE, "dtype %d", dtype);
+}
+
+static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
+                           int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, void* g, float* bias,
+                           hipStream_t st, char* err, size_t errlen) {
+  if (dtype == FPF_DT_BF16) {
+    if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(g) ||
+        !aligned16(bias))
+      return fail(err, errlen, FPF_E_ALIGN, "prologue operands must be 16-byte aligned");
+    const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
+    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)z, ln_w, ln_b, eps, (const uint16_t*)w_qkvg,
+                       (const uint16_t*)w_b, H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N, B, ending);
+    return launched(err, errlen, "triattn_prologue_bf16");
+  }
+  const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
+  hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
+                     (const float*)w_b, C, H, D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N, ending);
+  return launched(err, errlen, "triattn_prologue_f32");
+}
+
+static int epilogue_launch(int dtype, const void* o, const void* g, const void* w_o, int64_t B, int64_t N, int C, int H, int D, int ending,
+                           int residual, void* out, hipStream_t st, char* err, size_t errlen) {
+  if (dtype == FPF_DT_BF16) {
+    if (!aligned16(o) || !aligned16(g) || !aligned16(w_o) || !aligned16(out))
+      return fail(err, errlen, FPF_E_ALIGN, "epilogue operands must be 16-byte aligned");
+    const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
+    hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)o, (const uint16_t*)g, (const uint16_t*)w_o, H,
+                       (uint16_t*)out, N, B, ending, residual);
+    return launched(err, errlen, "triattn_epilogue_bf16");
+  }
+  const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
+  hipLaunchKernelGGL(triattn_epilogue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)o, (const float*)g, (const float*)w_o, C, H, D,
+                     (float*)out, N, ending, residual);
+  return launched(err, errlen, "triattn_epilogue_f32");
+}
+
+}  // namespace fpf
+
+extern "C" int fpf_triattn_prologue_fwd(const FpfTriattnPrologueArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->z || !a->w_qkvg || !a->w_b || !a->q || !a->k || !a->v || !a->g || !a->bias)
+    return fail(err, errlen, FPF_E_ARGS, "z / weights / q / k / v / g / bias is NULL");
+  if (a->B < 0 || a->N < 0) return fail(err, errlen, FPF_E_SHAPE, "negative extent");
+  if (a->B == 0 || a->N == 0) return FPF_OK;
+  const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
+  if (rc) return rc;
+  return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending, a->q, a->k, a->v,
+                         a->g, a->bias, static_cast<hipStream_t>(stream), err, errlen);
+}
+
+extern "C" int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->o || !a->g || !a->w_o || !a->out) return fail(err, errlen, FPF_E_ARGS, "o / g / w_o / out is NULL");
+  if (a->B < 0 || a->N < 0) return fail(err, errlen, FPF_E_SHAPE, "negative extent");
+  if (a->B == 0 || a->N == 0) return FPF_OK;
+  const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
+  if (rc) return rc;
+  return epilogue_launch(a->dtype, a->o, a->g, a->w_o, a->B, a->N, a->C, a->H, a->D, a->ending, a->residual, a->out,
+                         static_cast<hipStream_t>(stream), err, errlen);
+}
+
 extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen) {
   using namespace fpf;
   FPF_CHECK_VERSION(a);
@@ -781,7 +858,10 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   if (a->mask && !(a->mask_dtype == FPF_DT_U8 || a->mask_dtype == FPF_DT_F32)) return fail(err, errlen, FPF_E_DTYPE, "mask_dtype %d", a->mask_dtype);
   const size_t need = fpf_triattn_block_workspace_bytes(a->B, a->N, a->C, a->H, a->D, a->dtype);
   if (!a->workspace || a->workspace_bytes < need) return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
-  if (a->B > 65535) return fail(err, errlen, FPF_E_SHAPE, "B above 65535");
+  {
+    const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
+    if (rc) return rc;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t B = a->B, N = a->N, H = a->H, D = a->D, HD = H * D;
   const size_t elt = a->dtype == FPF_DT_F32 ? 4 : 2;
@@ -822,36 +902,10 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.mask_stride[2] = a->ending ? N : 1;
   c.out = o;
   c.scale = scale;
-  if (a->dtype == FPF_DT_BF16) {
-    if (a->C != TP_C || HD != TP_HD || D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 block serves C = 128, H*D = 128, D = 32");
-    if (!aligned16(a->z) || !aligned16(a->out) || !aligned16(a->workspace) || !aligned16(a->w_qkvg) || !aligned16(a->w_b) || !aligned16(a->w_o))
-      return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
-    const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
-    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, a->ln_w, a->ln_b, a->eps,
-                       (const uint16_t*)a->w_qkvg, (const uint16_t*)a->w_b, (int)H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N,
-                       B, a->ending);
-    int rc = launched(err, errlen, "triattn_prologue_bf16");
-    if (rc) return rc;
-    rc = core_launch(&c, st, err, errlen);
-    if (rc) return rc;
-    const unsigned egrid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
-    hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(egrid), dim3(512), 0, st, (const uint16_t*)o, (const uint16_t*)g,
-                       (const uint16_t*)a->w_o, (int)H, (uint16_t*)a->out, N, B, a->ending, a->residual);
-    return launched(err, errlen, "triattn_epilogue_bf16");
-  }
-  if (a->dtype == FPF_DT_F32) {
-    if (a->C > PF_CM || HD > PF_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 block serves C, H*D <= 128");
-    const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
-    hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)a->z, a->ln_w, a->ln_b, a->eps,
-                       (const float*)a->w_qkvg, (const float*)a->w_b, a->C, (int)H, (int)D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N,
-                       a->ending);
-    int rc = launched(err, errlen, "triattn_prologue_f32");
-    if (rc) return rc;
-    rc = core_launch(&c, st, err, errlen);
-    if (rc) return rc;
-    hipLaunchKernelGGL(triattn_epilogue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)o, (const float*)g, (const float*)a->w_o,
-                       a->C, (int)H, (int)D, (float*)a->out, N, a->ending, a->residual);
-    return launched(err, errlen, "triattn_epilogue_f32");
-  }
-  return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);
+  int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, g, bias,
+                           st, err, errlen);
+  if (rc) return rc;
+  rc = core_launch(&c, st, err, errlen);
+  if (rc) return rc;
+  return epilogue_launch(a->dtype, o, g, a->w_o, B, N, a->C, (int)H, (int)D, a->ending, a->residual, a->out, st, err, errlen);
 }

@@ -35,16 +35,42 @@ class Refusal(RuntimeError):
                                                                    ("; bind instead: %r" % fallback) if fallback else ""))
 
 
+_ARCH_BY_DEVICE = {}
+
+
 def device_word(t):
-    """'gfx950' for an MI355X tensor (the arch name without feature suffixes), 'cpu' for a host tensor."""
-    import torch
+    """'gfx950' for an MI355X tensor (the arch name without feature suffixes), 'cpu' for a host tensor.  Memoised per device
+    index (the property query is a runtime call)."""
     if not t.is_cuda:
         return "cpu"
-    return torch.cuda.get_device_properties(t.device).gcnArchName.split(":")[0]
+    idx = t.device.index
+    w = _ARCH_BY_DEVICE.get(idx)
+    if w is None:
+        import torch
+        w = _ARCH_BY_DEVICE[idx] = torch.cuda.get_device_properties(t.device).gcnArchName.split(":")[0]
+    return w
+
+
+_RESOLVED = {}
 
 
 def resolve(word, dtype_word, arch, face, cell=None):
-    """Pure selection shared by the faces: (word, 'bf16' | 'fp32', arch) -> Selection, or Refusal by name."""
+    """Pure selection shared by the faces: (word, 'bf16' | 'fp32', arch) -> Selection, or Refusal by name.  Memoised per
+    argument tuple like the reference's selection memo (refusals are re-raised from the memo)."""
+    key = (word, dtype_word, arch, face, cell)
+    hit = _RESOLVED.get(key)
+    if hit is None:
+        try:
+            hit = _resolve(word, dtype_word, arch, face, cell)
+        except Refusal as r:
+            hit = r
+        _RESOLVED[key] = hit
+    if isinstance(hit, Refusal):
+        raise Refusal(hit.kind, hit.row, hit.fallback, hit.detail)
+    return hit
+
+
+def _resolve(word, dtype_word, arch, face, cell):
     if word is None:
         raise ValueError("word is required (a row name or one of %s)" % (TIER_WORDS,))
     w = str(word)

@@ -48,6 +48,17 @@ class TriattnBlockArgs(C.Structure):
                 ("ending", i32), ("residual", i32), ("out", vp), ("scale", f32), ("workspace", vp), ("workspace_bytes", sz)]
 
 
+class TriattnPrologueArgs(C.Structure):
+    _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp), ("ln_w", vp),
+                ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("ending", i32), ("q", vp), ("k", vp), ("v", vp), ("g", vp),
+                ("bias", vp)]
+
+
+class TriattnEpilogueArgs(C.Structure):
+    _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("o", vp), ("g", vp),
+                ("w_o", vp), ("ending", i32), ("residual", i32), ("out", vp)]
+
+
 ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol include/fpf_hip.h declares
     "fpf_abi_version": ([], C.c_int),
     "fpf_describe": ([], C.c_char_p),
@@ -58,6 +69,8 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_triattn_fwd": ([C.POINTER(TriattnArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_workspace_bytes": ([i64, i64, i32, i32, i32, i32], sz),
     "fpf_triattn_block_fwd": ([C.POINTER(TriattnBlockArgs), vp, C.c_char_p, sz], C.c_int),
+    "fpf_triattn_prologue_fwd": ([C.POINTER(TriattnPrologueArgs), vp, C.c_char_p, sz], C.c_int),
+    "fpf_triattn_epilogue_fwd": ([C.POINTER(TriattnEpilogueArgs), vp, C.c_char_p, sz], C.c_int),
 }
 
 

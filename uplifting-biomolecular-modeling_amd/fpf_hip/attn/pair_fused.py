@@ -2,8 +2,9 @@
 launches, ``fpf_triattn_block_fwd``) and the fused SwiGLU transition.
 
 Mirrors common/opt_core/opt_core/attn/pair_fused.py: ``Unsupported`` (:86), ``pack_triattn_weights`` (:679),
-``pack_transition_weights`` (:744), ``tri_attn_block(z, W, mask=None, *, ending, residual, ...)`` (:1500) and
-``transition(x, T, *, residual, out, mask, ...)`` (:1519).
+``pack_transition_weights`` (:744), ``_key_mask`` (:806), ``prologue`` (:1136), ``core_attention`` (:1391), ``epilogue``
+(:1416), ``tri_attn_block(z, W, mask=None, *, ending, residual, ...)`` (:1500) and ``transition(x, T, *, residual, out, mask,
+...)`` (:1519).
 
 Frames: z is the pair tensor [B,N,N,C] (or [N,N,C]) in its OWN frame.  ``ending=True`` attends in the transposed frame
 x = z^T: the prologue reads z^T by address (no copy) and the epilogue writes the update back untransposed.  With
@@ -95,21 +96,118 @@ def _pair_mask(mask, z4):
     return (m != 0).contiguous().view(torch.uint8), L.DT_U8
 
 
-def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None, word="fast", **_unused):
-    """The fused block; returns the update in z's frame (residual=False) or z updated in place (residual=True)."""
+def _block_check(z, W, word, face):
+    """Shape / row gate shared by the block and its stages: -> (z4, Selection), or Unsupported before any launch."""
     z4 = z if z.dim() == 4 else z.unsqueeze(0)
     if z4.dim() != 4 or z4.shape[1] != z4.shape[2] or z4.shape[-1] != W.C:
         raise Unsupported("shape", str(tuple(z.shape)))
     if not z4.is_contiguous():
         raise Unsupported("stride", "z must be contiguous")
     try:
-        sel = F.resolve(word, F.dtype_word(z.dtype), F.device_word(z), "pair_fused:tri_attn_block", cell="block:%s" % W.shapes)
+        sel = F.resolve(word, F.dtype_word(z.dtype), F.device_word(z), "pair_fused:" + face, cell="block:%s" % W.shapes)
     except F.Refusal as e:
         raise Unsupported(e.kind, e.detail) from None
     if sel.row == F.ROW_FAST and (W.C, W.H * W.D, W.D, W.C_out) != (128, 128, 32, 128):
         raise Unsupported("shape:%s" % W.shapes, "the bf16 block serves C = 128, H*D = 128, D = 32")
     if sel.row == F.ROW_F32 and (W.C > 128 or W.H * W.D > 128 or W.D not in (16, 32, 64) or W.C_out != W.C):
         raise Unsupported("shape:%s" % W.shapes, "the fp32 block serves C, H*D <= 128, D 16 | 32 | 64")
+    return z4, sel
+
+
+def _key_mask(mask, z, ending):
+    """Pair mask [B,N,N] / [N,N] in z's frame -> the core's key mask [B, I, 1, 1, J] bool in the attention frame (transposed for
+    the ending node), as pair_fused.py:806-829 builds it.  None stays None."""
+    if mask is None:
+        return None
+    m = mask if mask.dim() == 3 else mask.unsqueeze(0)
+    if ending:
+        m = m.transpose(1, 2)
+    return (m != 0)[:, :, None, None, :]
+
+
+def prologue(z, W, *, ending=False, word="fast", **_unused):
+    """-> (q, k, v, g, bias) in the attention frame x = z (z^T for the ending node, read by address): q, k, v [B, I, H, J, D]
+    (bf16: v is a view of storage [B, I, H, D, J], which the op face serves without a copy), g [B, I, J, H*D] pre-sigmoid, bias
+    [B, 1, H, I, J] fp32.  Mirrors pair_fused.py:1136 (``prologue``); one launch of ``fpf_triattn_prologue_fwd``."""
+    z4, sel = _block_check(z, W, word, "prologue")
+    B, N = int(z4.shape[0]), int(z4.shape[1])
+    H, D = W.H, W.D
+    wqkvg, wb, _wo = _wpack(W, z.dtype, z.device)
+    e = dict(dtype=z.dtype, device=z.device)
+    q = torch.empty(B, N, H, N, D, **e)
+    k = torch.empty(B, N, H, N, D, **e)
+    bf = z.dtype == torch.bfloat16
+    vs = torch.empty(B, N, H, D, N, **e) if bf else torch.empty(B, N, H, N, D, **e)
+    g = torch.empty(B, N, N, H * D, **e)
+    bias = torch.empty(B, H, N, N, dtype=torch.float32, device=z.device)
+    a = L.TriattnPrologueArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if bf else L.DT_F32, B=B, N=N, C=W.C, H=H, D=D, z=L.ptr(z4),
+                              ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb),
+                              ending=1 if ending else 0, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vs), g=L.ptr(g), bias=L.ptr(bias))
+    try:
+        L.call("fpf_triattn_prologue_fwd", a, L.stream_ptr(z.device))
+    except L.LibError as e_:
+        raise Unsupported("lib:" + e_.kind, e_.msg) from None
+    v = vs.transpose(-1, -2) if bf else vs
+    return q, k, v, g, bias.unsqueeze(1)
+
+
+def core_attention(q, k, v, bias, mask5=None, *, core="tier:fast", scale=None):
+    """o [B, I, H, J, D] = softmax_j(scale q.k + bias, -inf at masked keys) v through the op face (pair_fused.py:1391);
+    ``core`` = "tier:<word>" / a row name of kernels.triattn, or a callable core(q, k, v, bias, mask, scale)."""
+    from ..kernels import triattn as _TA
+    if callable(core):
+        import math
+        return core(q, k, v, bias, mask5, (1.0 / math.sqrt(q.shape[-1])) if scale is None else float(scale))
+    w = str(core)
+    if w.startswith("tier:"):
+        w = w[len("tier:"):]
+    try:
+        return _TA.triangle_attention(q, k, v, bias, mask5, scale, word=w)
+    except F.Refusal as e:
+        raise Unsupported("core:" + e.kind, e.detail) from None
+
+
+def epilogue(o, g, W, z=None, *, ending=False, residual=False, out=None, word="fast", **_unused):
+    """u = (sigmoid(g) * o) W_o^T (pair_fused.py:1416).  residual=True: z (its own frame) is updated in place (the ending node's
+    u[i, j] is added at z[j, i]) and returned; else the update in the attention frame [B, I, J, C_out] (for the ending node a
+    transposed view of a z-frame tensor, as the reference returns it).  One launch of ``fpf_triattn_epilogue_fwd``."""
+    if o.dim() != 5:
+        raise Unsupported("o-shape", str(tuple(o.shape)))
+    B, N, H, J, D = (int(x) for x in o.shape)
+    if (H, D) != (W.H, W.D) or J != N or tuple(g.shape) != (B, N, N, H * D):
+        raise Unsupported("o/g-shape", "%s %s" % (tuple(o.shape), tuple(g.shape)))
+    if not (o.is_contiguous() and g.is_contiguous()) or g.dtype != o.dtype:
+        raise Unsupported("o/g-layout", "o [B,I,H,J,D] and g [B,I,J,HD] contiguous, one dtype")
+    if residual:
+        if z is None:
+            raise Unsupported("residual-needs-z")
+        z4, sel = _block_check(z, W, word, "epilogue")
+        if z4.dtype != o.dtype or tuple(z4.shape[:3]) != (B, N, N):
+            raise Unsupported("z-shape", str(tuple(z.shape)))
+        dst = z4
+    else:
+        if out is not None:
+            dst = out if out.dim() == 4 else out.unsqueeze(0)
+            if tuple(dst.shape) != (B, N, N, W.C_out) or not dst.is_contiguous() or dst.dtype != o.dtype:
+                raise Unsupported("out", "a contiguous [B, N, N, C_out] tensor of o's dtype (z's frame)")
+        else:
+            dst = torch.empty(B, N, N, W.C_out, dtype=o.dtype, device=o.device)
+        _block_check(dst, W, word, "epilogue")
+    _, _, wo = _wpack(W, o.dtype, o.device)
+    a = L.TriattnEpilogueArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if o.dtype == torch.bfloat16 else L.DT_F32, B=B, N=N, C=W.C, H=H, D=D,
+                              o=L.ptr(o), g=L.ptr(g), w_o=L.ptr(wo), ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(dst))
+    try:
+        L.call("fpf_triattn_epilogue_fwd", a, L.stream_ptr(o.device))
+    except L.LibError as e_:
+        raise Unsupported("lib:" + e_.kind, e_.msg) from None
+    if residual:
+        return z
+    return dst.transpose(1, 2) if ending else dst
+
+
+def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None, word="fast", **_unused):
+    """The fused block; returns the update in z's frame (residual=False) or z updated in place (residual=True)."""
+    z4, sel = _block_check(z, W, word, "tri_attn_block")
     B, N = int(z4.shape[0]), int(z4.shape[1])
     m, mdt = _pair_mask(mask, z4)
     wqkvg, wb, wo = _wpack(W, z.dtype, z.device)

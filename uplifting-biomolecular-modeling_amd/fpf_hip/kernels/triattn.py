@@ -47,8 +47,13 @@ def triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, selection=
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise Refusal("dtype_mix", word, F.ROW_STOCK)
     sel = selection or select(F.device_word(q), q.dtype, D, H, S, word=word)
-    if q.stride(-1) != 1 or k.stride(-1) != 1 or v.stride(-1) != 1:
+    # v stored transposed ([B,N,H,D,S] storage viewed as [B,N,H,S,D], as the block prologue returns it) is served as it is by
+    # the bf16 core (v_layout 1); every other operand needs a contiguous head_dim
+    v_t = v.stride(-1) != 1 and v.stride(-2) == 1 and D > 1
+    if q.stride(-1) != 1 or k.stride(-1) != 1 or (v.stride(-1) != 1 and not v_t):
         raise Refusal("stride", sel.row, F.ROW_STOCK, "head_dim must be contiguous")
+    if v_t and sel.row != F.ROW_FAST:
+        raise Refusal("stride:v_transposed", sel.row, F.ROW_FAST, "the fp32 core takes v with a contiguous head_dim")
     if bias.dim() != 5 or tuple(bias.shape) != (B, 1, H, S, S) or bias.stride(-1) != 1:
         raise Refusal("bias_shape", sel.row, F.ROW_STOCK, str(tuple(bias.shape)))
     if bias.dtype not in (torch.float32, torch.bfloat16):
@@ -73,6 +78,10 @@ def triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, selection=
                       mask=L.ptr(m), mask_dtype=mdt, out=L.ptr(out), scale=sc)
     for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("out_stride", out)):
         getattr(a, name)[:] = _strides(t, 5)
+    if v_t:
+        vs = _strides(v, 5)
+        a.v_layout = 1
+        a.v_stride[:] = [vs[0], vs[1], vs[2], vs[4], vs[3]]
     bs = _strides(bias, 5)
     a.bias_stride[:] = [bs[0], bs[2], bs[3], bs[4]]
     if m is not None:
