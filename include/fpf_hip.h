@@ -198,7 +198,9 @@ typedef struct {
   int32_t ending;          /* 1: attention frame x = z^T (read by address) */
   void* q;                 /* [B, I, H, J, D] contiguous */
   void* k;                 /* [B, I, H, J, D] */
-  void* v;                 /* bf16: [B, I, H, D, J] (stored transposed, the core's v_layout 1); fp32: [B, I, H, J, D] */
+  void* v;                 /* bf16: [B, I, H, D, v_ld] (stored transposed, the core's v_layout 1; columns >= N are padding);
+                              fp32: [B, I, H, J, D] */
+  int64_t v_ld;            /* bf16: elements between V^T rows, >= N rounded up to 32 and a multiple of 8; fp32: ignored */
   void* g;                 /* [B, I, J, H*D] pre-sigmoid */
   float* bias;             /* [B, H, I, J] fp32 (the [B,1,H,I,J] operand without its unit axis) */
 } FpfTriattnPrologueArgs;

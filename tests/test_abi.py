@@ -22,9 +22,10 @@ def _structs():
     out = {}
     for body, name in re.findall(r"typedef struct \{(.*?)\}\s*(\w+);", txt, flags=re.S):
         fields = []
+        body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         for ln in body.splitlines():
-            ln = re.sub(r"/\*.*?\*/", "", ln).strip()
-            if not ln or ln.startswith("/*") or ln.startswith("*"):
+            ln = ln.strip()
+            if not ln:
                 continue
             decl = ln.rstrip(";").strip()
             m = re.match(r"(?:const\s+)?[\w]+\s*\*?\s*(.+)$", decl)

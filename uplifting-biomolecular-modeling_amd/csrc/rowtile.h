@@ -81,6 +81,19 @@ __device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int 
   return acc;
 }
 
+// The swapped product D = x W[row0 .. row0 + 31]^T (same fragments, operands exchanged): lane (n, g) then holds output
+// channel row0 + n for the 16 pixels c_row(v, g) of the tile.
+__device__ __forceinline__ f32x16 rt_gemm32_xw(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
+  const uint16_t* r = s + (row0 + n) * RT_LD + 64 * g;
+  f32x16 acc = {};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    acc = mfma32(xb[t], as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * t)), acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return acc;
+}
+
 // K GEMMs over the same B operand, k-step-major (the K weight fragments of one k-step are read, then K MFMAs issue).
 template <int K>
 __device__ __forceinline__ void rt_gemm32_multi(const uint16_t* const (&s)[K], int row0, int n, int g, const bf16x8 (&xb)[8], f32x16 (&acc)[K]) {
@@ -95,6 +108,65 @@ __device__ __forceinline__ void rt_gemm32_multi(const uint16_t* const (&s)[K], i
     for (int k = 0; k < K; ++k) acc[k] = mfma32(a[k], xb[t], acc[k]);
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// The swapped form of rt_gemm32_multi: D_k = x W_k[row0 .. row0 + 31]^T, lane (n, g) holding output channel row0 + n for the
+// 16 pixels c_row(v, g).
+template <int K>
+__device__ __forceinline__ void rt_gemm32_multi_xw(const uint16_t* const (&s)[K], int row0, int n, int g, const bf16x8 (&xb)[8], f32x16 (&acc)[K]) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) acc[k] = f32x16{};
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    bf16x8 a[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * t));
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc[k] = mfma32(xb[t], a[k], acc[k]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Repacks a 32 x 32 D fragment (lane (n, g) holds rows c_row(v, g) of column n) into bf16 16-byte chunks: afterwards lane
+// (n, g) holds rows 8g .. 8g + 7 (lo) and 16 + 8g .. 16 + 8g + 7 (hi) of column n.  Lanes n and n + 32 trade the four-row
+// groups the other one needs with v_permlane32_swap (swap(A, B) exchanges A's upper half-wave with B's lower half-wave),
+// so a pixel's 32 consecutive channels leave in two 16-byte stores instead of four 8-byte ones.
+__device__ __forceinline__ void rt_pack16(const f32x16& acc, u32x4& lo, u32x4& hi) {
+  uint32_t p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = pack2(acc[2 * e], acc[2 * e + 1]);
+  // p[0], p[1]: rows 4g + 0..3;  p[2], p[3]: rows 8 + 4g + 0..3;  p[4], p[5]: rows 16 + 4g + 0..3;  p[6], p[7]: rows 24 + 4g + 0..3
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(p[e], p[2 + e], false, false);
+    p[e] = s0[0];
+    p[2 + e] = s0[1];
+    const auto s1 = __builtin_amdgcn_permlane32_swap(p[4 + e], p[6 + e], false, false);
+    p[4 + e] = s1[0];
+    p[6 + e] = s1[1];
+  }
+  lo = u32x4{p[0], p[1], p[2], p[3]};
+  hi = u32x4{p[4], p[5], p[6], p[7]};
+}
+
+// The same exchange on fp32 values (two 16-byte chunks of 4 rows each per half): lane (n, g) ends with rows
+// 8g .. 8g + 7 and 16 + 8g .. 16 + 8g + 7 of column n in out[0..15] (row order).
+__device__ __forceinline__ void rt_regroup_f32(const f32x16& acc, float (&out)[16]) {
+  uint32_t p[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) p[e] = __float_as_uint(acc[e]);
+  // p[0..3]: rows 4g + 0..3;  p[4..7]: 8 + 4g;  p[8..11]: 16 + 4g;  p[12..15]: 24 + 4g
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(p[e], p[4 + e], false, false);
+    p[e] = s0[0];
+    p[4 + e] = s0[1];
+    const auto s1 = __builtin_amdgcn_permlane32_swap(p[8 + e], p[12 + e], false, false);
+    p[8 + e] = s1[0];
+    p[12 + e] = s1[1];
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) out[e] = __uint_as_float(p[e]);
 }
 
 // Orders a wave's own LDS writes before its later LDS reads of other lanes' data (the LDS unit executes a wave's

@@ -123,27 +123,35 @@ __global__ void __launch_bounds__(512) transition_bf16_kernel(const uint16_t* x,
     if (hb + 1 < nhb) lstore(buf ^ 1);        // buf ^ 1 was last read before the previous barrier
     __syncthreads();
   }
-  // epilogue: lane (pixel n, half g) holds c_out = 32 cb + 8 q + 4 g + 0..3 in registers 4q .. 4q+3
+  // epilogue: lane (pixel n, half g) holds c_out = 32 cb + c_row(v, g); after the lane exchange it holds channels
+  // 32 cb + 8g .. +7 and 32 cb + 16 + 8g .. +7, stored (with mask and residual) in 16-byte pieces
 #pragma unroll
   for (int p = 0; p < PW; ++p) {
     const int64_t pix = pix0 + 32 * p + n;
-    if (pix >= rows) continue;
-    const float m = mask ? mask[pix] : 1.0f;
+    const bool live = pix < rows;
+    const float m = (mask && live) ? mask[pix] : 1.0f;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < 4; ++cb) {
+      float y[16];
+      rt_regroup_f32(acc[p][cb], y);
+      if (!live) continue;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c0 = 32 * cb + 8 * q + 4 * g;
-        float y0 = acc[p][cb][4 * q] * m, y1 = acc[p][cb][4 * q + 1] * m, y2 = acc[p][cb][4 * q + 2] * m, y3 = acc[p][cb][4 * q + 3] * m;
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int64_t c0 = pix * TR_C + 32 * cb + 16 * h2 + 8 * g;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = y[8 * h2 + e] * m;
         if (residual) {
-          const u32x2 r = *reinterpret_cast<const u32x2*>(x + pix * TR_C + c0);
-          y0 += lo_bf(r[0]);
-          y1 += hi_bf(r[0]);
-          y2 += lo_bf(r[1]);
-          y3 += hi_bf(r[1]);
+          const u32x4 r = *reinterpret_cast<const u32x4*>(x + c0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[2 * e] += lo_bf(r[e]);
+            v[2 * e + 1] += hi_bf(r[e]);
+          }
         }
-        *reinterpret_cast<u32x2*>(out + pix * TR_C + c0) = u32x2{pack2(y0, y1), pack2(y2, y3)};
+        *reinterpret_cast<u32x4*>(out + c0) = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
       }
+    }
   }
 }
 

@@ -439,8 +439,8 @@ __global__ void __launch_bounds__(64) triattn_core_f32(const CoreParamsF p) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------- prologue (bf16)
-// x = LN(z or z^T) -> q, k [B,I,H,J,D] bf16, v^T [B,I,H,D,J] bf16 (the core stages V^T rows directly), g [B,I,J,HD] bf16
-// (pre-sigmoid), bias [B,H,I,J] fp32.  Persistent: W_qkvg (512 rows) and W_b (padded to 32 rows) live in LDS (148 KB); a wave
+// x = LN(z or z^T) -> q, k [B,I,H,J,D] bf16, v^T [B,I,H,D,Jp] bf16 (Jp = N rounded up to 32; the core stages V^T rows
+// directly), g [B,I,J,HD] bf16 (pre-sigmoid), bias [B,H,I,J] fp32.  Every bf16 output leaves in 16-byte stores.  Persistent: W_qkvg (512 rows) and W_b (padded to 32 rows) live in LDS (148 KB); a wave
 // owns 32 positions j of one attention row i; with `ending` the 32 z pixels are z[j][i] (strided rows, each a contiguous
 // 256-byte pixel).
 constexpr int TP_C = 128, TP_HD = 128;
@@ -449,7 +449,7 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __r
                                                              const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ w_qkvg,
                                                              const uint16_t* __restrict__ w_b, int H, uint16_t* __restrict__ qo,
                                                              uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, uint16_t* __restrict__ go,
-                                                             float* __restrict__ bo, int64_t N, int64_t B, int ending) {
+                                                             float* __restrict__ bo, int64_t N, int64_t Jp, int64_t B, int ending) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[(4 * TP_HD + 32) * RT_LD];
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
@@ -470,30 +470,26 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __r
     rt_ln(raw, g, sLN, eps, xb);
 #pragma unroll 1
     for (int blk = 0; blk < 17; ++blk) {
+      if (blk >= 8 && blk < 12) {                         // v, transposed: vT[b][i][h][d][Jp] -- the swapped product x W_v^T
+        // puts d on the lanes and 16 pixels in the registers; the lane exchange then gives each lane 8 consecutive pixels
+        const f32x16 acc = rt_gemm32_xw(sW, blk * 32, n, g, xb);
+        u32x4 lo, hi;
+        rt_pack16(acc, lo, hi);
+        uint16_t* dst = vo + (((b * N + i) * H + (blk & 3)) * (int64_t)D + n) * Jp + (j - n) + 8 * g;
+        *reinterpret_cast<u32x4*>(dst) = lo;               // whole 32-pixel tile: Jp covers it (padding is never read)
+        *reinterpret_cast<u32x4*>(dst + 16) = hi;
+        continue;
+      }
       const f32x16 acc = rt_gemm32(sW, blk * 32, n, g, xb);
-      if (!live) continue;
-      if (blk < 4 || (blk >= 4 && blk < 8)) {            // q | k: [B, I, H, J, D], 4 consecutive d per 8-byte store
-        uint16_t* dst = blk < 4 ? qo : ko;
-        const int hh = blk & 3;
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int d0 = 8 * qd + 4 * g;
-          *reinterpret_cast<u32x2*>(dst + (((b * N + i) * H + hh) * N + j) * D + d0) =
-              u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
-        }
-      } else if (blk < 12) {                              // v, transposed: vT[b][i][h][d][j]
-        uint16_t* dst = vo + ((b * N + i) * H + (blk & 3)) * (int64_t)D * N + j;
-#pragma unroll
-        for (int vv = 0; vv < 16; ++vv) dst[(int64_t)c_row(vv, g) * N] = f2bf(acc[vv]);
-      } else if (blk < 16) {                              // g (pre-sigmoid): [B, I, J, HD]
-        const int cb = (blk - 12) * 32;
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int c0 = cb + 8 * qd + 4 * g;
-          *reinterpret_cast<u32x2*>(go + ((b * N + i) * N + j) * TP_HD + c0) =
-              u32x2{pack2(acc[4 * qd], acc[4 * qd + 1]), pack2(acc[4 * qd + 2], acc[4 * qd + 3])};
-        }
-      } else if (g == 0) {                                // bias (fp32): [B, H, I, J]
+      if (blk < 16) {                                     // q | k | g
+        u32x4 lo, hi;
+        rt_pack16(acc, lo, hi);
+        if (!live) continue;
+        uint16_t* dst = blk < 8 ? (blk < 4 ? qo : ko) + (((b * N + i) * H + (blk & 3)) * N + j) * D + 8 * g   // [B, I, H, J, D]
+                                : go + ((b * N + i) * N + j) * TP_HD + (blk - 12) * 32 + 8 * g;            // [B, I, J, HD]
+        *reinterpret_cast<u32x4*>(dst) = lo;
+        *reinterpret_cast<u32x4*>(dst + 16) = hi;
+      } else if (g == 0 && live) {                        // bias (fp32): [B, H, I, J]
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (v < H) bo[((b * H + v) * N + i) * N + j] = acc[v];
@@ -534,23 +530,30 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
       xb[tt] = as_bf8(u32x4{w4[0], w4[1], w4[2], w4[3]});
     }
     const int64_t zpix = ending ? (b * N + j) * N + i : (b * N + i) * N + j;
+    uint16_t* zp = zout + zpix * RT_C + 8 * g;
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
       const f32x16 acc = rt_gemm32(sW, cb * 32, n, g, xb);
-      if (!live) continue;
+      // lane (n, g) stores channels cb*32 + 8g .. +7 and cb*32 + 16 + 8g .. +7 of pixel n: two 16-byte stores
+      if (residual) {
+        float y[16];
+        rt_regroup_f32(acc, y);
+        if (!live) continue;
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int c0 = cb * 32 + 8 * qd + 4 * g;
-        uint16_t* p = zout + zpix * RT_C + c0;
-        float y0 = acc[4 * qd], y1 = acc[4 * qd + 1], y2 = acc[4 * qd + 2], y3 = acc[4 * qd + 3];
-        if (residual) {
-          const u32x2 r = *reinterpret_cast<const u32x2*>(p);
-          y0 += lo_bf(r[0]);
-          y1 += hi_bf(r[0]);
-          y2 += lo_bf(r[1]);
-          y3 += hi_bf(r[1]);
+        for (int h2 = 0; h2 < 2; ++h2) {
+          uint16_t* p = zp + cb * 32 + 16 * h2;
+          const u32x4 r = *reinterpret_cast<const u32x4*>(p);
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = pack2(y[8 * h2 + 2 * e] + lo_bf(r[e]), y[8 * h2 + 2 * e + 1] + hi_bf(r[e]));
+          *reinterpret_cast<u32x4*>(p) = w;
         }
-        *reinterpret_cast<u32x2*>(p) = u32x2{pack2(y0, y1), pack2(y2, y3)};
+      } else {
+        u32x4 lo, hi;
+        rt_pack16(acc, lo, hi);
+        if (!live) continue;
+        *reinterpret_cast<u32x4*>(zp + cb * 32) = lo;
+        *reinterpret_cast<u32x4*>(zp + cb * 32 + 16) = hi;
       }
     }
   }
@@ -766,8 +769,8 @@ extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int32_
   const size_t elt = dtype == FPF_DT_F32 ? 4 : 2;
   const size_t pix = (size_t)B * (size_t)N * (size_t)N;
   const size_t HD = (size_t)H * (size_t)D;
-  // q, k, v, o, g (HD per pixel each) + bias (H fp32 per pixel), each region 256-byte aligned
-  const size_t r1 = (pix * HD * elt + 255) & ~(size_t)255;
+  // q, k, v, o, g (HD per pixel each; V^T rows padded to N rounded up to 32) + bias (H fp32 per pixel), 256-byte aligned regions
+  const size_t r1 = ((size_t)B * N * fpf::cdiv(N, 32) * 32 * HD * elt + 255) & ~(size_t)255;
   const size_t r2 = (pix * (size_t)H * 4 + 255) & ~(size_t)255;
   return 5 * r1 + r2;
 }
@@ -789,15 +792,16 @@ static int block_shape_check(int dtype, int64_t B, int C, int64_t H, int64_t D, 
 }
 
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
-                           int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, void* g, float* bias,
+                           int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen) {
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(g) ||
         !aligned16(bias))
       return fail(err, errlen, FPF_E_ALIGN, "prologue operands must be 16-byte aligned");
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
+    if (v_ld < cdiv(N, 32) * 32 || v_ld % 8) return fail(err, errlen, FPF_E_SHAPE, "v_ld %lld: V^T rows need N rounded up to 32", (long long)v_ld);
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)z, ln_w, ln_b, eps, (const uint16_t*)w_qkvg,
-                       (const uint16_t*)w_b, H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N, B, ending);
+                       (const uint16_t*)w_b, H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N, v_ld, B, ending);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
@@ -834,7 +838,7 @@ extern "C" int fpf_triattn_prologue_fwd(const FpfTriattnPrologueArgs* a, void* s
   const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
   if (rc) return rc;
   return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending, a->q, a->k, a->v,
-                         a->g, a->bias, static_cast<hipStream_t>(stream), err, errlen);
+                         a->v_ld, a->g, a->bias, static_cast<hipStream_t>(stream), err, errlen);
 }
 
 extern "C" int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* stream, char* err, size_t errlen) {
@@ -865,8 +869,8 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t B = a->B, N = a->N, H = a->H, D = a->D, HD = H * D;
   const size_t elt = a->dtype == FPF_DT_F32 ? 4 : 2;
-  const size_t pix = (size_t)B * N * N;
-  const size_t r1 = (pix * HD * elt + 255) & ~(size_t)255;
+  const int64_t Jp = cdiv(N, 32) * 32;
+  const size_t r1 = ((size_t)B * N * Jp * HD * elt + 255) & ~(size_t)255;
   char* w = static_cast<char*>(a->workspace);
   void *q = w, *k = w + r1, *v = w + 2 * r1, *o = w + 3 * r1, *g = w + 4 * r1;
   float* bias = reinterpret_cast<float*>(w + 5 * r1);
@@ -884,9 +888,12 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.v = v;
   const int64_t st5[5] = {N * H * N * D, H * N * D, N * D, D, 1};
   for (int t = 0; t < 5; ++t) c.q_stride[t] = c.k_stride[t] = c.v_stride[t] = c.out_stride[t] = st5[t];
-  if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, I, H, D, J]
+  if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, I, H, D, Jp]
     c.v_layout = 1;
-    c.v_stride[3] = N;
+    c.v_stride[0] = N * H * D * Jp;
+    c.v_stride[1] = H * D * Jp;
+    c.v_stride[2] = D * Jp;
+    c.v_stride[3] = Jp;
     c.v_stride[4] = 1;
   }
   c.bias = bias;
@@ -902,8 +909,8 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.mask_stride[2] = a->ending ? N : 1;
   c.out = o;
   c.scale = scale;
-  int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, g, bias,
-                           st, err, errlen);
+  int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
+                           bias, st, err, errlen);
   if (rc) return rc;
   rc = core_launch(&c, st, err, errlen);
   if (rc) return rc;

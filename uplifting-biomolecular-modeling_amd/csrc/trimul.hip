@@ -27,6 +27,7 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
                                                       int outgoing) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[4 * RT_C * RT_LD];
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
+  __shared__ __attribute__((aligned(16))) float sM[RT_WAVES][32];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
   rt_stage_weights(sW, w_ap, RT_C, RT_C, tid, 512);
@@ -54,19 +55,41 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
     bf16x8 xb[8];
     rt_ln(raw, g, sLN, eps, xb);
     if (t + stride < total) fetch(t + stride);
-    uint16_t* oa = pa + b * RT_C * plane + P * Np + Q;
-    uint16_t* ob = pb + b * RT_C * plane + P * Np + Q;
+    // the swapped products put the channel on the lanes and 16 pixels of the tile in the registers: the pixel masks come back
+    // from LDS in that order (pixels c_row(v, g) = four runs of 4), and after the lane exchange each lane stores two runs of 8
+    // consecutive plane columns
+    if (g == 0) sM[wave][n] = m;
+    rt_wave_lds_sync();
+    float mv[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 m4 = *reinterpret_cast<const f32x4*>(&sM[wave][8 * q + 4 * g]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mv[4 * q + e] = m4[e];
+    }
+    rt_wave_lds_sync();
+    const int64_t Q0 = Q - n;
+    uint16_t* oa = pa + b * RT_C * plane + P * Np + Q0 + 8 * g;
+    uint16_t* ob = pb + b * RT_C * plane + P * Np + Q0 + 8 * g;
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
       const uint16_t* const ws[4] = {sW, sW + 1 * RT_C * RT_LD, sW + 2 * RT_C * RT_LD, sW + 3 * RT_C * RT_LD};
       f32x16 acc[4];
-      rt_gemm32_multi<4>(ws, cb * 32, n, g, xb, acc);
+      rt_gemm32_multi_xw<4>(ws, cb * 32, n, g, xb, acc);
+      f32x16 va, vb;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t c = cb * 32 + c_row(v, g);
-        oa[c * plane] = f2bf(m * sigmoidf_(acc[1][v]) * acc[0][v]);
-        ob[c * plane] = f2bf(m * sigmoidf_(acc[3][v]) * acc[2][v]);
+        va[v] = mv[v] * sigmoidf_(acc[1][v]) * acc[0][v];
+        vb[v] = mv[v] * sigmoidf_(acc[3][v]) * acc[2][v];
       }
+      const int64_t c = cb * 32 + n;
+      u32x4 lo, hi;
+      rt_pack16(va, lo, hi);
+      *reinterpret_cast<u32x4*>(oa + c * plane) = lo;
+      *reinterpret_cast<u32x4*>(oa + c * plane + 16) = hi;
+      rt_pack16(vb, lo, hi);
+      *reinterpret_cast<u32x4*>(ob + c * plane) = lo;
+      *reinterpret_cast<u32x4*>(ob + c * plane + 16) = hi;
     }
   }
 }
@@ -212,21 +235,26 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
     for (int cb = 0; cb < 4; ++cb) {
       const f32x16 o = rt_gemm32(sW, cb * 32, n, g, xo);
       const f32x16 gt = rt_gemm32(sW + RT_C * RT_LD, cb * 32, n, g, xi);
+      f32x16 u;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) u[v] = sigmoidf_(gt[v]) * o[v];
+      // lane (n, g) ends with channels cb*32 + 8g .. +7 and cb*32 + 16 + 8g .. +7 of pixel n: two 16-byte stores
+      float y[16];
+      rt_regroup_f32(u, y);
       if (!live) continue;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c0 = cb * 32 + 8 * q + 4 * g;
-        float y[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = sigmoidf_(gt[4 * q + e]) * o[4 * q + e];
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int64_t c0 = pix * RT_C + cb * 32 + 16 * h2 + 8 * g;
         if (residual) {
-          const u32x2 r = *reinterpret_cast<const u32x2*>(zin + pix * RT_C + c0);
-          y[0] += lo_bf(r[0]);
-          y[1] += hi_bf(r[0]);
-          y[2] += lo_bf(r[1]);
-          y[3] += hi_bf(r[1]);
+          const u32x4 r = *reinterpret_cast<const u32x4*>(zin + c0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y[8 * h2 + 2 * e] += lo_bf(r[e]);
+            y[8 * h2 + 2 * e + 1] += hi_bf(r[e]);
+          }
         }
-        *reinterpret_cast<u32x2*>(out + pix * RT_C + c0) = u32x2{pack2(y[0], y[1]), pack2(y[2], y[3])};
+        *reinterpret_cast<u32x4*>(out + c0) = u32x4{pack2(y[8 * h2], y[8 * h2 + 1]), pack2(y[8 * h2 + 2], y[8 * h2 + 3]),
+                                                    pack2(y[8 * h2 + 4], y[8 * h2 + 5]), pack2(y[8 * h2 + 6], y[8 * h2 + 7])};
       }
     }
   }

@@ -50,8 +50,8 @@ class TriattnBlockArgs(C.Structure):
 
 class TriattnPrologueArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp), ("ln_w", vp),
-                ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("ending", i32), ("q", vp), ("k", vp), ("v", vp), ("g", vp),
-                ("bias", vp)]
+                ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("ending", i32), ("q", vp), ("k", vp), ("v", vp), ("v_ld", i64),
+                ("g", vp), ("bias", vp)]
 
 
 class TriattnEpilogueArgs(C.Structure):

@@ -137,17 +137,19 @@ def prologue(z, W, *, ending=False, word="fast", **_unused):
     q = torch.empty(B, N, H, N, D, **e)
     k = torch.empty(B, N, H, N, D, **e)
     bf = z.dtype == torch.bfloat16
-    vs = torch.empty(B, N, H, D, N, **e) if bf else torch.empty(B, N, H, N, D, **e)
+    jp = -(-N // 32) * 32                                 # V^T rows padded to a multiple of 32 columns (16-byte stores)
+    vs = torch.empty(B, N, H, D, jp, **e) if bf else torch.empty(B, N, H, N, D, **e)
     g = torch.empty(B, N, N, H * D, **e)
     bias = torch.empty(B, H, N, N, dtype=torch.float32, device=z.device)
     a = L.TriattnPrologueArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if bf else L.DT_F32, B=B, N=N, C=W.C, H=H, D=D, z=L.ptr(z4),
                               ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb),
-                              ending=1 if ending else 0, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vs), g=L.ptr(g), bias=L.ptr(bias))
+                              ending=1 if ending else 0, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vs), v_ld=jp if bf else 0, g=L.ptr(g),
+                              bias=L.ptr(bias))
     try:
         L.call("fpf_triattn_prologue_fwd", a, L.stream_ptr(z.device))
     except L.LibError as e_:
         raise Unsupported("lib:" + e_.kind, e_.msg) from None
-    v = vs.transpose(-1, -2) if bf else vs
+    v = vs[..., :N].transpose(-1, -2) if bf else vs
     return q, k, v, g, bias.unsqueeze(1)
 
 
