@@ -168,6 +168,133 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------- contraction, 256 x 256 tiles
+// For planes padded to a multiple of 256: a workgroup (4 waves, one per SIMD) computes a 256 x 256 tile of X, each wave a
+// 128 x 128 quarter in 16 accumulators.  The A and B k-slabs (256 rows x 32 k each) go straight from global memory into LDS
+// (global_load_lds_dwordx4: no VGPR staging), three slabs in the ring so the loads of slab k + 2 overlap the MFMAs of slab
+// k; within a slab row the four 16-byte chunks are XOR-swizzled by (row >> 2) & 3, so the fragment reads of 16 consecutive
+// rows land on 16 distinct bank groups.  The MFMA runs with the operands exchanged (D = B A^T): lane = row i, registers =
+// 16 columns j, and after the half-wave lane exchange each lane stores 8 consecutive columns per 16-byte store.
+constexpr int CB_T = 256, CB_K = 32, CB_NBUF = 4;
+
+// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): the wave's 64 chunks land at lds_base + 16 * lane.
+// Issued through inline assembly so that the only waits on it are the explicit s_waitcnt vmcnt of the slab ring (the
+// compiler would otherwise drain every outstanding transfer before each LDS read it cannot prove disjoint).  lds_base is
+// wave-uniform (it goes through M0).
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t nbatch) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[CB_NBUF][CB_T * CB_K];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[CB_NBUF][CB_T * CB_K];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t tpd = Np / CB_T, tiles = tpd * tpd, total = tiles * nbatch;
+  const int64_t per = (total + 7) / 8;
+  const int64_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;     // each XCD gets a contiguous run: one plane's 9 tiles share its L2
+  if (w >= total) return;
+  const int64_t bc = w / tiles, t = w % tiles, ti = t / tpd, tj = t % tpd;
+  const int64_t plane = Np * Np;
+  const uint16_t* a0 = A + bc * plane + ti * CB_T * Np;
+  const uint16_t* b0 = Bm + bc * plane + tj * CB_T * Np;
+  // slab loads: 1024 16-byte chunks per operand; instruction q of thread tid fills LDS slot s = 256 q + tid (each wave
+  // instruction writes 1 KB contiguously); slot s = row s >> 2, position s & 3, holding chunk (s & 3) ^ ((row >> 2) & 3)
+  int64_t goff[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int sl = 256 * q + tid, r = sl >> 2, c = (sl & 3) ^ ((r >> 2) & 3);
+    goff[q] = (int64_t)r * Np + 8 * c;
+  }
+  auto issue = [&](int buf, int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      lds_dma16(a0 + goff[q] + k0, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16(b0 + goff[q] + k0, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
+    }
+  };
+  const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
+  // fragment read offsets (elements) of this lane's rows for chunk position 0 / 1 of each k16 half: row r, chunk c
+  auto frag_off = [&](int r, int c) { return (r * 4 + (c ^ ((r >> 2) & 3))) * 8; };
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int si = 0; si < 4; ++si)
+#pragma unroll
+    for (int sj = 0; sj < 4; ++sj) acc[si][sj] = f32x16{};
+  const int nk = (int)(Np / CB_K);
+  // the 16 fragments of one slab: A rows wr + 32 s + n, B rows wc + 32 s + n, chunks 2 ks + g
+  auto read_frags = [&](int buf, bf16x8 (&fa)[2][4], bf16x8 (&fb)[2][4]) {
+    const uint16_t* pa = sA[buf];
+    const uint16_t* pb = sB[buf];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        fa[ks][s4] = as_bf8(*reinterpret_cast<const u32x4*>(pa + frag_off(wr + 32 * s4 + n, 2 * ks + g)));
+        fb[ks][s4] = as_bf8(*reinterpret_cast<const u32x4*>(pb + frag_off(wc + 32 * s4 + n, 2 * ks + g)));
+      }
+  };
+  // ring: slab k lives in buffer k % 4, three slabs in flight.  Iteration kt issues slab kt + 3, runs 8 of slab kt's 32
+  // MFMAs, waits for slab kt + 1 at the barrier (the matrix core keeps working), then reads slab kt + 1's 16 fragments
+  // ahead of the other 24 MFMAs.
+  issue(0, 0);
+  if (nk > 1) issue(1, CB_K);
+  if (nk > 2) issue(2, 2 * CB_K);
+  if (nk > 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (nk > 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  bf16x8 fa[2][4], fb[2][4], na[2][4], nb[2][4];
+  read_frags(0, fa, fb);
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 3 < nk) issue((kt + 3) % CB_NBUF, (int64_t)(kt + 3) * CB_K);   // its buffer held slab kt - 1, read before the last barrier
+#pragma unroll
+    for (int si = 0; si < 4; ++si)
+#pragma unroll
+      for (int sj = 0; sj < 2; ++sj) acc[si][sj] = mfma32(fb[0][sj], fa[0][si], acc[si][sj]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) {                                   // slab kt + 1 landed: at most the later slabs' transfers outstanding
+      if (kt + 3 < nk) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      else if (kt + 2 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) read_frags((kt + 1) % CB_NBUF, na, nb);
+#pragma unroll
+    for (int si = 0; si < 4; ++si)
+#pragma unroll
+      for (int sj = 2; sj < 4; ++sj) acc[si][sj] = mfma32(fb[0][sj], fa[0][si], acc[si][sj]);
+#pragma unroll
+    for (int si = 0; si < 4; ++si)
+#pragma unroll
+      for (int sj = 0; sj < 4; ++sj) acc[si][sj] = mfma32(fb[1][sj], fa[1][si], acc[si][sj]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        fa[ks][s4] = na[ks][s4];
+        fb[ks][s4] = nb[ks][s4];
+      }
+  }
+  uint16_t* x0 = X + bc * plane;
+#pragma unroll
+  for (int si = 0; si < 4; ++si)
+#pragma unroll
+    for (int sj = 0; sj < 4; ++sj) {
+      u32x4 lo, hi;
+      rt_pack16(acc[si][sj], lo, hi);
+      uint16_t* xp = x0 + (ti * CB_T + wr + 32 * si + n) * Np + tj * CB_T + wc + 32 * sj + 8 * g;
+      *reinterpret_cast<u32x4*>(xp) = lo;
+      *reinterpret_cast<u32x4*>(xp + 16) = hi;
+      __builtin_amdgcn_sched_barrier(0);                 // one accumulator at a time (bounded VGPR use)
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------- K3 (bf16)
 // Persistent: W_o and W_og live in LDS (70 KB); each wave loads its X tile (issued with the tile's z rows at the top of the
 // iteration; the second wave of the SIMD covers the latency -- a register prefetch of the next tile costs occupancy) X[c][i][j0 .. j0+31] (channel-major, 128 rows of
@@ -480,9 +607,15 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
                        a->outgoing);
     int rc = launched(err, errlen, "trimul_k1_bf16");
     if (rc) return rc;
-    const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE) * B * TM_C;
-    hipLaunchKernelGGL(trimul_contract_bf16, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, N, B * TM_C);
-    rc = launched(err, errlen, "trimul_contract_bf16");
+    if (Np % CB_T == 0) {
+      const int64_t tiles = (Np / CB_T) * (Np / CB_T) * B * TM_C;
+      hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, B * TM_C);
+      rc = launched(err, errlen, "trimul_contract_bf16_256");
+    } else {
+      const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE) * B * TM_C;
+      hipLaunchKernelGGL(trimul_contract_bf16, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, N, B * TM_C);
+      rc = launched(err, errlen, "trimul_contract_bf16");
+    }
     if (rc) return rc;
     const int64_t k3_tiles = B * N * cdiv(N, 32);
     const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
