@@ -69,14 +69,19 @@ __device__ __forceinline__ void rt_stage_weights(uint16_t* __restrict__ s, const
   }
 }
 
-// D = W[row0 .. row0 + 31] x^T over the 128 channels (8 k-steps), weights from LDS.
+// D = W[row0 .. row0 + 31] x^T over the 128 channels (8 k-steps), weights from LDS.  The weight fragment of k-step t + 1 is
+// read before the MFMA of k-step t issues, so the LDS latency hides behind the matrix core.
 __device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
   const uint16_t* r = s + (row0 + n) * RT_LD + 64 * g;
   f32x16 acc = {};
+  bf16x8 w = as_bf8(*reinterpret_cast<const u32x4*>(r));
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    acc = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * t)), xb[t], acc);
-    __builtin_amdgcn_sched_barrier(0);   // keep the next k-step's LDS reads behind this MFMA: bounded register pressure
+    bf16x8 wn = w;
+    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * (t + 1)));
+    acc = mfma32(w, xb[t], acc);
+    __builtin_amdgcn_sched_barrier(0);   // one k-step of lookahead: bounded register pressure
+    w = wn;
   }
   return acc;
 }
@@ -86,27 +91,38 @@ __device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int 
 __device__ __forceinline__ f32x16 rt_gemm32_xw(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
   const uint16_t* r = s + (row0 + n) * RT_LD + 64 * g;
   f32x16 acc = {};
+  bf16x8 w = as_bf8(*reinterpret_cast<const u32x4*>(r));
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    acc = mfma32(xb[t], as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * t)), acc);
+    bf16x8 wn = w;
+    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * (t + 1)));
+    acc = mfma32(xb[t], w, acc);
     __builtin_amdgcn_sched_barrier(0);
+    w = wn;
   }
   return acc;
 }
 
-// K GEMMs over the same B operand, k-step-major (the K weight fragments of one k-step are read, then K MFMAs issue).
+// K GEMMs over the same B operand, k-step-major (the K weight fragments of k-step t + 1 are read while the K MFMAs of
+// k-step t issue).
 template <int K>
 __device__ __forceinline__ void rt_gemm32_multi(const uint16_t* const (&s)[K], int row0, int n, int g, const bf16x8 (&xb)[8], f32x16 (&acc)[K]) {
+  bf16x8 a[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) acc[k] = f32x16{};
+  for (int k = 0; k < K; ++k) {
+    acc[k] = f32x16{};
+    a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g));
+  }
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    bf16x8 a[K];
+    bf16x8 an[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * t));
+    for (int k = 0; k < K; ++k) an[k] = t < 7 ? as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * (t + 1))) : a[k];
 #pragma unroll
     for (int k = 0; k < K; ++k) acc[k] = mfma32(a[k], xb[t], acc[k]);
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < K; ++k) a[k] = an[k];
   }
 }
 
@@ -114,16 +130,22 @@ __device__ __forceinline__ void rt_gemm32_multi(const uint16_t* const (&s)[K], i
 // 16 pixels c_row(v, g).
 template <int K>
 __device__ __forceinline__ void rt_gemm32_multi_xw(const uint16_t* const (&s)[K], int row0, int n, int g, const bf16x8 (&xb)[8], f32x16 (&acc)[K]) {
+  bf16x8 a[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) acc[k] = f32x16{};
+  for (int k = 0; k < K; ++k) {
+    acc[k] = f32x16{};
+    a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g));
+  }
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    bf16x8 a[K];
+    bf16x8 an[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * t));
+    for (int k = 0; k < K; ++k) an[k] = t < 7 ? as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * (t + 1))) : a[k];
 #pragma unroll
     for (int k = 0; k < K; ++k) acc[k] = mfma32(xb[t], a[k], acc[k]);
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < K; ++k) a[k] = an[k];
   }
 }
 

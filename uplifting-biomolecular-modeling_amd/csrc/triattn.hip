@@ -460,14 +460,20 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __r
   const int D = TP_HD / H;
   const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
   const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
+  u32x4 raw[8];                                         // the next tile's pixel rows, loaded while this tile computes
+  auto fetch = [&](int64_t tt) {
+    const int64_t b = tt / per_b, i = (tt % per_b) / tpr, j = (tt % tpr) * 32 + n;
+    const bool live = j < N;
+    const int64_t zpix = ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
+    rt_load(z + zpix * RT_C, live, g, raw);
+  };
+  if ((int64_t)blockIdx.x * RT_WAVES + wave < total) fetch((int64_t)blockIdx.x * RT_WAVES + wave);
   for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
     const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
     const bool live = j < N;
-    const int64_t zpix = ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
-    u32x4 raw[8];
-    rt_load(z + zpix * RT_C, live, g, raw);
     bf16x8 xb[8];
     rt_ln(raw, g, sLN, eps, xb);
+    if (t + stride < total) fetch(t + stride);
 #pragma unroll 1
     for (int blk = 0; blk < 17; ++blk) {
       if (blk >= 8 && blk < 12) {                         // v, transposed: vT[b][i][h][d][Jp] -- the swapped product x W_v^T
