@@ -207,17 +207,18 @@ def test_stages_bf16_prologue_core_epilogue(ending):
     assert_bf16_close(o, ref_o, "core on the prologue's tensors ending=%s" % ending)
     ref_u = S.triatt_epilogue(o.float().cpu(), g.float().cpu(), P, dtype=torch.float32)
     assert_bf16_residual_close(u, ref_u, "epilogue ending=%s" % ending)
+    # the fused block recomputes the gate from z in fp32 (the staged chain reads the stored bf16 g): same statement, one
+    # rounding fewer, so the two agree to bf16 tolerance rather than bitwise; both are held to the oracle
     blk = PF.tri_attn_block(zd, W, md, ending=ending, residual=False)
     torch.cuda.synchronize()
-    assert torch.equal(u.transpose(1, 2) if ending else u, blk), "staged chain differs from the fused block"
+    ref_blk = S.tri_attn(z.float(), P, mask, ending=ending, dtype=torch.float32)
+    assert_bf16_close(blk, ref_blk, "fused block ending=%s" % ending)
+    assert_bf16_close(u.transpose(1, 2) if ending else u, blk.float(), "staged chain vs fused block ending=%s" % ending)
     zz = zd.clone()
     r = PF.epilogue(o, g, W, zz, ending=ending, residual=True)
     torch.cuda.synchronize()
     assert r.data_ptr() == zz.data_ptr()
-    zb = zd.clone()
-    PF.tri_attn_block(zb, W, md, ending=ending, residual=True)
-    torch.cuda.synchronize()
-    assert torch.equal(zz, zb)
+    assert_bf16_residual_close(zz, z.float() + (u.transpose(1, 2) if ending else u).float().cpu(), "staged residual ending=%s" % ending)
 
 
 def test_stages_fp32_exact():

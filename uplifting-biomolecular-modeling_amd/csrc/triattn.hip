@@ -449,7 +449,8 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __r
                                                              const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ w_qkvg,
                                                              const uint16_t* __restrict__ w_b, int H, uint16_t* __restrict__ qo,
                                                              uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, uint16_t* __restrict__ go,
-                                                             float* __restrict__ bo, int64_t N, int64_t Jp, int64_t B, int ending) {
+                                                             float* __restrict__ bo, int64_t N, int64_t Jp, int64_t B, int ending,
+                                                             int write_g) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[(4 * TP_HD + 32) * RT_LD];
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
@@ -476,6 +477,7 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __r
     if (t + stride < total) fetch(t + stride);
 #pragma unroll 1
     for (int blk = 0; blk < 17; ++blk) {
+      if (blk >= 12 && blk < 16 && !write_g) continue;  // the gate-fused epilogue recomputes g
       if (blk >= 8 && blk < 12) {                         // v, transposed: vT[b][i][h][d][Jp] -- the swapped product x W_v^T
         // puts d on the lanes and 16 pixels in the registers; the lane exchange then gives each lane 8 consecutive pixels
         const f32x16 acc = rt_gemm32_xw(sW, blk * 32, n, g, xb);
@@ -560,6 +562,96 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
         if (!live) continue;
         *reinterpret_cast<u32x4*>(zp + cb * 32) = lo;
         *reinterpret_cast<u32x4*>(zp + cb * 32 + 16) = hi;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- gate-fused epilogue (bf16)
+// The block's epilogue without the g round trip: the gate is recomputed from the block's own input, g = LN(x) W_g^T (x = z
+// or z^T, the pixel this wave updates anyway), so the prologue never writes g (151 MB at N = 768) and this kernel never
+// reads it back.  u = (sigmoid(g) * o) W_o^T; residual: z += u in place (the LN input is read before the pixel is written,
+// by the same lane).  The g GEMM's output fragments are used directly as the B operand of the W_o GEMM: k-step s = 2 cb +
+// half takes, in lane half g, the channels cb*32 + 16 half + {4g .. 4g+3, 8+4g .. 8+4g+3} that the D layout leaves there,
+// and W_o's columns are permuted identically when staged.
+__global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t* zin, const uint16_t* __restrict__ o,
+                                                                  const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
+                                                                  const uint16_t* __restrict__ w_g, const uint16_t* __restrict__ w_o,
+                                                                  uint16_t* zout, int64_t N, int64_t B, int ending, int residual) {
+  __shared__ __attribute__((aligned(16))) uint16_t sWg[RT_C * RT_LD];
+  __shared__ __attribute__((aligned(16))) uint16_t sWo[RT_C * RT_LD];   // columns permuted to the k-step order above
+  __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
+  rt_stage_weights(sWg, w_g, RT_C, RT_C, tid, 512);
+  for (int q = tid; q < RT_C * RT_C; q += 512) {
+    const int m = q >> 7, kp = q & 127;
+    const int st = kp >> 4, gg = (kp >> 3) & 1, e = kp & 7;
+    const int c = (st >> 1) * 32 + 16 * (st & 1) + 8 * (e >> 2) + 4 * gg + (e & 3);
+    sWo[m * RT_LD + kp] = w_o[m * RT_C + c];
+  }
+  __syncthreads();
+  constexpr int H = TP_HD / TA_D;
+  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
+  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
+  for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
+    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+    const bool live = j < N;
+    const int64_t zpix = ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
+    bf16x8 xb[8];
+    {
+      u32x4 raw[8];
+      rt_load(zin + zpix * RT_C, live, g, raw);
+      rt_ln(raw, g, sLN, eps, xb);
+    }
+    f32x16 acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] = f32x16{};
+    const uint16_t* op = o + (((b * N + i) * H) * N + (live ? j : 0)) * TA_D + 4 * g;
+#pragma unroll 1
+    for (int cb = 0; cb < 4; ++cb) {
+      const f32x16 gacc = rt_gemm32(sWg, cb * 32, n, g, xb);     // g of head cb: channels cb*32 + c_row(v, g)
+      const uint16_t* oh = op + (int64_t)cb * N * TA_D;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x2 o0 = {0, 0}, o1 = {0, 0};
+        if (live) {
+          o0 = *reinterpret_cast<const u32x2*>(oh + 16 * half);
+          o1 = *reinterpret_cast<const u32x2*>(oh + 16 * half + 8);
+        }
+        const float ov[8] = {lo_bf(o0[0]), hi_bf(o0[0]), lo_bf(o0[1]), hi_bf(o0[1]), lo_bf(o1[0]), hi_bf(o1[0]), lo_bf(o1[1]), hi_bf(o1[1])};
+        uint32_t w4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w4[e] = pack2(sigmoidf_(gacc[8 * half + 2 * e]) * ov[2 * e], sigmoidf_(gacc[8 * half + 2 * e + 1]) * ov[2 * e + 1]);
+        const bf16x8 bop = as_bf8(u32x4{w4[0], w4[1], w4[2], w4[3]});
+        const int kst = 2 * cb + half;
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk)
+          acc[blk] = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(&sWo[(blk * 32 + n) * RT_LD + 16 * kst + 8 * g])), bop, acc[blk]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // lane (n, g) stores channels blk*32 + 8g .. +7 and blk*32 + 16 + 8g .. +7 of pixel n: two 16-byte stores per block
+    uint16_t* zp = zout + zpix * RT_C + 8 * g;
+    const uint16_t* zr = zin + zpix * RT_C + 8 * g;
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+      float y[16];
+      rt_regroup_f32(acc[blk], y);
+      if (!live) continue;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        u32x4 w;
+        if (residual) {
+          const u32x4 r = *reinterpret_cast<const u32x4*>(zr + blk * 32 + 16 * h2);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = pack2(y[8 * h2 + 2 * e] + lo_bf(r[e]), y[8 * h2 + 2 * e + 1] + hi_bf(r[e]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = pack2(y[8 * h2 + 2 * e], y[8 * h2 + 2 * e + 1]);
+        }
+        *reinterpret_cast<u32x4*>(zp + blk * 32 + 16 * h2) = w;
       }
     }
   }
@@ -799,15 +891,15 @@ static int block_shape_check(int dtype, int64_t B, int C, int64_t H, int64_t D, 
 
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
-                           hipStream_t st, char* err, size_t errlen) {
+                           hipStream_t st, char* err, size_t errlen, int write_g = 1) {
   if (dtype == FPF_DT_BF16) {
-    if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(g) ||
+    if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || !aligned16(q) || !aligned16(k) || !aligned16(v) || (write_g && !aligned16(g)) ||
         !aligned16(bias))
       return fail(err, errlen, FPF_E_ALIGN, "prologue operands must be 16-byte aligned");
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
     if (v_ld < cdiv(N, 32) * 32 || v_ld % 8) return fail(err, errlen, FPF_E_SHAPE, "v_ld %lld: V^T rows need N rounded up to 32", (long long)v_ld);
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)z, ln_w, ln_b, eps, (const uint16_t*)w_qkvg,
-                       (const uint16_t*)w_b, H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N, v_ld, B, ending);
+                       (const uint16_t*)w_b, H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N, v_ld, B, ending, write_g);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
@@ -915,10 +1007,19 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.mask_stride[2] = a->ending ? N : 1;
   c.out = o;
   c.scale = scale;
+  const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
   int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
-                           bias, st, err, errlen);
+                           bias, st, err, errlen, fused_gate ? 0 : 1);
   if (rc) return rc;
   rc = core_launch(&c, st, err, errlen);
   if (rc) return rc;
+  if (fused_gate) {
+    if (!aligned16(a->out)) return fail(err, errlen, FPF_E_ALIGN, "out must be 16-byte aligned");
+    const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
+    hipLaunchKernelGGL(triattn_epilogue_gate_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w, a->ln_b,
+                       a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, (uint16_t*)a->out, N, B, a->ending,
+                       a->residual);
+    return launched(err, errlen, "triattn_epilogue_gate_bf16");
+  }
   return epilogue_launch(a->dtype, o, g, a->w_o, B, N, a->C, (int)H, (int)D, a->ending, a->residual, a->out, st, err, errlen);
 }
