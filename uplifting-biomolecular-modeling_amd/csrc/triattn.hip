@@ -17,13 +17,13 @@
 namespace fpf {
 
 constexpr int TA_D = 32;
-constexpr int TA_R = 4;          // pair rows per workgroup sharing the bias tile
+constexpr int TA_R = 3;          // pair rows per workgroup sharing the bias tile (3: the register budget of 2 waves / SIMD)
 constexpr int TA_KT = 64;        // keys per staged tile (two MFMA sub-tiles of 32)
 constexpr int TA_KLD = 40;       // LDS pitch (bf16) of a K row: 80 B, conflict-free 16-byte reads
 constexpr int TA_VLD = 68;       // LDS pitch (bf16) of a V^T row: 136 B, conflict-free 8-byte reads
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float TA_HEADROOM = 8.0f;   // log2 units the running max may lag the true one before O and l are rescaled
-static_assert(TA_R == 4, "one wave computes the keep bits of one staged row");
+static_assert(TA_R <= 4, "one wave computes the keep bits of one staged row");
 
 struct CoreParams {
   const uint16_t* q;
@@ -62,7 +62,9 @@ __device__ __forceinline__ f32x16 qk_tile(const uint16_t* __restrict__ kr, int s
   return mfma32(as_bf8(*reinterpret_cast<const u32x4*>(row + 16)), qf[1], s);
 }
 
-template <bool VT>
+// VT: V stored transposed ([.., D, S]); BVEC: fp32 bias with 16-byte aligned rows (float4 loads; the generic variant reads
+// element by element and serves bf16 or unaligned bias)
+template <bool VT, bool BVEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_R][TA_KT * TA_KLD];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_R][TA_D * TA_VLD];
@@ -87,7 +89,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   // Q tile of the R rows -> LDS (read back as B-operand fragments every sub-tile); row liveness
   if (tid < TA_R) sAlive[tid] = 0;
 #pragma unroll
-  for (int it = 0; it < 8; ++it) {
+  for (int it = 0; it < 2 * TA_R; ++it) {
     const int c = tid + 256 * it, r = c >> 9, qq = (c >> 2) & 127, part = c & 3;
     const int64_t i = i0 + r, qg = qt * 128 + qq;
     *reinterpret_cast<u32x4*>(&sQ[r][qq * TA_KLD + 8 * part]) =
@@ -110,7 +112,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     dead[r] = (i0 + r < p.N) && !sAlive[r];
     dead_any |= dead[r];
   }
-  const bool wave_row_dead = !sAlive[wave];
+  const bool wave_row_dead = wave < TA_R ? !sAlive[wave] : true;
 
   f32x16 o[TA_R];
   float mrow[TA_R], lrow[TA_R];                         // running max (log2 units) and this lane's partial sum
@@ -123,54 +125,50 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   // staging: 1024 16-byte chunks per operand per tile, 4 per thread; element offsets at key 0 are computed once
   // chunk `it` of a thread belongs to row i0 + it (256 threads x 4 chunks): row bases are wave-uniform, the in-row part per lane
-  int64_t kbase[4], vbase[4];
-  bool rowok[4];
+  // row base pointers are wave-uniform (scalar registers); the in-row part is one 32-bit per-lane offset per operand
+  const uint16_t* kbase[TA_R];
+  const uint16_t* vbase[TA_R];
+  bool rowok[TA_R];
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
+  for (int it = 0; it < TA_R; ++it) {
     const int64_t i = i0 + it;
     rowok[it] = i < p.N;
     const int64_t ii = rowok[it] ? i : i0;
-    kbase[it] = b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
-    vbase[it] = b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
+    kbase[it] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
+    vbase[it] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
   }
-  const int64_t kin = ((tid >> 2) & 63) * p.ks[3] + 8 * (tid & 3);
-  const int64_t vin = VT ? ((tid >> 3) & 31) * p.vs[3] + 8 * (tid & 7) : ((tid >> 2) & 63) * p.vs[3] + 8 * (tid & 3);
-  int64_t koff[4], voff[4];
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    koff[it] = kbase[it] + kin;
-    voff[it] = vbase[it] + vin;
-  }
-  u32x4 rk[4], rv[4];
+  const uint32_t kin = (uint32_t)(((tid >> 2) & 63) * p.ks[3] + 8 * (tid & 3));
+  const uint32_t vin = (uint32_t)(VT ? ((tid >> 3) & 31) * p.vs[3] + 8 * (tid & 7) : ((tid >> 2) & 63) * p.vs[3] + 8 * (tid & 3));
+  u32x4 rk[TA_R], rv[TA_R];
   bool keepn;                                           // prefetched mask bit: row i0 + wave, key k0 + l of the next tile
   auto gload = [&](int64_t k0) {
     {
       const int64_t i = i0 + wave, key = k0 + l;
-      keepn = key < p.S && i < p.N && (wave_row_dead || mask_keep(p, b, i, key));
+      keepn = wave < TA_R && key < p.S && i < p.N && (wave_row_dead || mask_keep(p, b, i, key));
     }
     if (k0 + TA_KT <= p.S) {                              // whole tile in range (uniform)
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        rk[it] = rowok[it] ? *reinterpret_cast<const u32x4*>(p.k + koff[it] + k0 * p.ks[3]) : u32x4{0, 0, 0, 0};
-        rv[it] = rowok[it] ? *reinterpret_cast<const u32x4*>(p.v + voff[it] + (VT ? k0 : k0 * p.vs[3])) : u32x4{0, 0, 0, 0};
+      for (int it = 0; it < TA_R; ++it) {
+        rk[it] = rowok[it] ? *reinterpret_cast<const u32x4*>(kbase[it] + k0 * p.ks[3] + kin) : u32x4{0, 0, 0, 0};
+        rv[it] = rowok[it] ? *reinterpret_cast<const u32x4*>(vbase[it] + (VT ? k0 : k0 * p.vs[3]) + vin) : u32x4{0, 0, 0, 0};
       }
       return;
     }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
+    for (int it = 0; it < TA_R; ++it) {
       const int c = tid + 256 * it;
       const int64_t kkey = k0 + ((c >> 2) & 63);
-      rk[it] = (rowok[it] && kkey < p.S) ? *reinterpret_cast<const u32x4*>(p.k + koff[it] + k0 * p.ks[3]) : u32x4{0, 0, 0, 0};
+      rk[it] = (rowok[it] && kkey < p.S) ? *reinterpret_cast<const u32x4*>(kbase[it] + k0 * p.ks[3] + kin) : u32x4{0, 0, 0, 0};
       if constexpr (VT) {
         const int64_t key = k0 + 8 * (c & 7);
-        const uint16_t* src = p.v + voff[it] + k0;
+        const uint16_t* src = vbase[it] + k0 + vin;
         uint16_t tmp[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) tmp[e] = (rowok[it] && key + e < p.S) ? src[e] : (uint16_t)0;
         rv[it] = u32x4{tmp[0] | ((uint32_t)tmp[1] << 16), tmp[2] | ((uint32_t)tmp[3] << 16), tmp[4] | ((uint32_t)tmp[5] << 16),
                        tmp[6] | ((uint32_t)tmp[7] << 16)};
       } else {
-        rv[it] = (rowok[it] && kkey < p.S) ? *reinterpret_cast<const u32x4*>(p.v + voff[it] + k0 * p.vs[3]) : u32x4{0, 0, 0, 0};
+        rv[it] = (rowok[it] && kkey < p.S) ? *reinterpret_cast<const u32x4*>(vbase[it] + k0 * p.vs[3] + vin) : u32x4{0, 0, 0, 0};
       }
     }
   };
@@ -178,11 +176,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int64_t bias_row = b * p.bs[0] + h * p.bs[1] + (qlive ? q : 0) * p.bs[2];
   auto bload = [&](int64_t kb, f32x16& dst) {
     const int64_t kb0 = kb + 4 * g;
-    if (p.bias_vec && kb + 32 <= p.S) {
-      const float* bp = static_cast<const float*>(p.bias) + bias_row + kb0;
+    if constexpr (BVEC) {                           // S % 4 == 0: a 4-key chunk lies wholly below S or wholly past it
+      const float* bp = static_cast<const float*>(p.bias) + bias_row;
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(bp + 8 * qd);
+        const int64_t k4 = kb0 + 8 * qd;
+        const f32x4 v4 = k4 < p.S ? *reinterpret_cast<const f32x4*>(bp + k4) : f32x4{0.f, 0.f, 0.f, 0.f};   // past S: masked keys
 #pragma unroll
         for (int e = 0; e < 4; ++e) dst[4 * qd + e] = v4[e];
       }
@@ -196,13 +195,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
     }
   };
+
   gload(0);
   f32x16 bnext;
   bload(0, bnext);
   for (int64_t k0 = 0; k0 < p.S; k0 += TA_KT) {
     __syncthreads();
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
+    for (int it = 0; it < TA_R; ++it) {
       const int c = tid + 256 * it;
       const int r = c >> 8;
       *reinterpret_cast<u32x4*>(&sK[r][((c >> 2) & 63) * TA_KLD + 8 * (c & 3)]) = rk[it];
@@ -221,7 +221,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     {
       const uint64_t bal = __ballot(keepn);               // keep bits of row `wave`: lane l <-> key k0 + l
-      if (l == 0) sKeep[wave] = bal;
+      if (l == 0 && wave < TA_R) sKeep[wave] = bal;
     }
     __syncthreads();
     if (k0 + TA_KT < p.S) gload(k0 + TA_KT);
@@ -799,13 +799,14 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
       if (p.os[t] & 3) return fail(err, errlen, FPF_E_ALIGN, "bf16 core: out strides must be multiples of 4 elements");
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || (reinterpret_cast<uintptr_t>(a->out) & 7))
       return fail(err, errlen, FPF_E_ALIGN, "bf16 core: q / k / v 16-byte, out 8-byte aligned");
-    p.bias_vec = !p.bias_bf16 && aligned16(a->bias) && (p.bs[0] % 4 == 0) && (p.bs[1] % 4 == 0) && (p.bs[2] % 4 == 0);
+    p.bias_vec = !p.bias_bf16 && aligned16(a->bias) && (p.bs[0] % 4 == 0) && (p.bs[1] % 4 == 0) && (p.bs[2] % 4 == 0) && (p.S % 4 == 0);
     const int64_t total = a->B * a->H * cdiv(a->N, TA_R) * cdiv(a->S, 128);
     if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
-    if (p.v_t)
-      hipLaunchKernelGGL(triattn_core_bf16<true>, dim3((unsigned)(cdiv(total, 8) * 8)), dim3(256), 0, st, p);
-    else
-      hipLaunchKernelGGL(triattn_core_bf16<false>, dim3((unsigned)(cdiv(total, 8) * 8)), dim3(256), 0, st, p);
+    const dim3 grid((unsigned)(cdiv(total, 8) * 8)), block(256);
+    if (p.v_t && p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<true, true>), grid, block, 0, st, p);
+    else if (p.v_t) hipLaunchKernelGGL((triattn_core_bf16<true, false>), grid, block, 0, st, p);
+    else if (p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<false, true>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((triattn_core_bf16<false, false>), grid, block, 0, st, p);
     return launched(err, errlen, "triattn_core_bf16");
   }
   if (a->dtype == FPF_DT_F32) {
