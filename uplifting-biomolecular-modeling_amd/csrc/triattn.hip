@@ -68,7 +68,6 @@ template <bool VT, bool BVEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_R][TA_KT * TA_KLD];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_R][TA_D * TA_VLD];
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[TA_R][128 * TA_KLD];
   __shared__ uint64_t sKeep[TA_R];
   __shared__ int sAlive[TA_R];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
@@ -86,15 +85,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const float c2 = p.scale * LOG2E;                     // qk units -> log2 units
   const float inv_scale = 1.0f / p.scale;
 
-  // Q tile of the R rows -> LDS (read back as B-operand fragments every sub-tile); row liveness
+  // this lane's Q fragments of the R rows (B operand of S^T = K Q^T: query q, d = 8g .. +7 and 16 + 8g .. +7), kept in
+  // registers for the whole kernel; row liveness
   if (tid < TA_R) sAlive[tid] = 0;
+  bf16x8 qf[TA_R][2];
 #pragma unroll
-  for (int it = 0; it < 2 * TA_R; ++it) {
-    const int c = tid + 256 * it, r = c >> 9, qq = (c >> 2) & 127, part = c & 3;
-    const int64_t i = i0 + r, qg = qt * 128 + qq;
-    *reinterpret_cast<u32x4*>(&sQ[r][qq * TA_KLD + 8 * part]) =
-        (i < p.N && qg < p.S) ? *reinterpret_cast<const u32x4*>(p.q + b * p.qs[0] + i * p.qs[1] + h * p.qs[2] + qg * p.qs[3] + 8 * part)
-                              : u32x4{0, 0, 0, 0};
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    const bool ok = i < p.N && qlive;
+    const uint16_t* qp = p.q + b * p.qs[0] + (ok ? i : 0) * p.qs[1] + h * p.qs[2] + (ok ? q : 0) * p.qs[3] + 8 * g;
+    qf[r][0] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0, 0, 0, 0});
+    qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
   }
   __syncthreads();
   for (int r = 0; r < TA_R; ++r) {
@@ -245,9 +246,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       f32x16 s[TA_R];
 #pragma unroll
       for (int r = 0; r < TA_R; ++r) {
-        const uint16_t* qr = &sQ[r][(wave * 32 + n) * TA_KLD + 8 * g];
-        const bf16x8 qf[2] = {as_bf8(*reinterpret_cast<const u32x4*>(qr)), as_bf8(*reinterpret_cast<const u32x4*>(qr + 16))};
-        s[r] = qk_tile(sK[r], sub, n, g, qf, bt);
+        s[r] = qk_tile(sK[r], sub, n, g, qf[r], bt);
       }
       if (!full) {
 #pragma unroll
