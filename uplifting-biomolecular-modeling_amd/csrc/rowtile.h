@@ -191,6 +191,17 @@ __device__ __forceinline__ void rt_regroup_f32(const f32x16& acc, float (&out)[1
   for (int e = 0; e < 16; ++e) out[e] = __uint_as_float(p[e]);
 }
 
+// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): the wave's 64 chunks land at lds_base + 16 * lane.
+// Issued through inline assembly so that the only waits on it are the explicit s_waitcnt vmcnt of the slab ring (the
+// compiler would otherwise drain every outstanding transfer before each LDS read it cannot prove disjoint).  lds_base is
+// wave-uniform (it goes through M0).
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
+}
+
 // Orders a wave's own LDS writes before its later LDS reads of other lanes' data (the LDS unit executes a wave's
 // operations in order; this keeps the compiler from moving the reads above the writes).
 __device__ __forceinline__ void rt_wave_lds_sync() {

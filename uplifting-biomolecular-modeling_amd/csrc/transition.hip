@@ -15,41 +15,45 @@ namespace fpf {
 constexpr int TR_C = 128;
 constexpr int TR_KS = TR_C / 16;      // k-steps of GEMM 1
 constexpr int TR_HB = 32;             // hidden rows per chunk
-constexpr int TR_WLD = TR_C + 8;      // LDS pitch of a W_a / W_b chunk row (bf16): 272 B, conflict-free 16-byte reads
-constexpr int TR_OLD = TR_HB + 4;     // LDS pitch of a W_o chunk row (bf16): 72 B, conflict-free 8-byte reads
-constexpr int TR_WAVES = 8;           // waves per workgroup (2 per SIMD), 32 pixel rows each
+constexpr int TR_PW = 1, TR_NW = 8;   // 32-row tiles per wave, waves per workgroup (2 per SIMD; measured faster than 2 tiles x 1 wave per SIMD)
+constexpr int TR_NBUF = 4;            // weight-chunk ring: 3 chunks in flight
 
-template <int PW>
-__global__ void __launch_bounds__(512) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
+template <int PW, int NW>
+__global__ void __launch_bounds__(64 * NW) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
                                                               const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ wa,
                                                               const uint16_t* __restrict__ wb, const uint16_t* __restrict__ wo,
                                                               const float* __restrict__ mask, int residual, int64_t rows, int hidden) {
-  // double-buffered weight chunks: W_a / W_b rows hb*32 .. +31 (all 128 inputs) and W_o columns hb*32 .. +31 (all 128 outputs)
-  __shared__ __attribute__((aligned(16))) uint16_t sWa[2][TR_HB * TR_WLD];
-  __shared__ __attribute__((aligned(16))) uint16_t sWb[2][TR_HB * TR_WLD];
-  __shared__ __attribute__((aligned(16))) uint16_t sWo[2][TR_C * TR_OLD];
+  // weight chunk hb = W_a / W_b rows hb*32 .. +31 (all 128 inputs) and W_o columns hb*32 .. +31 (all 128 outputs), 24 KB,
+  // streamed by DMA (global_load_lds_dwordx4, no VGPR staging) through a ring of TR_NBUF buffers, TR_NBUF - 1 chunks in
+  // flight.  W_a / W_b rows are 16 chunks of 16 bytes stored at position c ^ (row & 15) (conflict-free fragment reads of 16
+  // consecutive rows); W_o rows are 4 chunks stored at position c ^ ((row >> 2) & 3).
+  __shared__ __attribute__((aligned(16))) uint16_t sWa[TR_NBUF][TR_HB * TR_C];
+  __shared__ __attribute__((aligned(16))) uint16_t sWb[TR_NBUF][TR_HB * TR_C];
+  __shared__ __attribute__((aligned(16))) uint16_t sWo[TR_NBUF][TR_C * TR_HB];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t pix0 = ((int64_t)blockIdx.x * TR_WAVES + wave) * (32 * PW);
-  // staging map: 1536 16-byte chunks per weight chunk (512 W_a, 512 W_b, 512 W_o), 3 per thread
-  const int sr = tid >> 4, sc = tid & 15;          // W_a / W_b: row, 16-byte column
-  const int so = tid >> 2, soc = tid & 3;          // W_o: row (c_out), 16-byte column within the 32 hidden
-  u32x4 pa, pb, po;
-  auto gload = [&](int hb) {
-    pa = *reinterpret_cast<const u32x4*>(wa + (int64_t)(hb * TR_HB + sr) * TR_C + sc * 8);
-    pb = *reinterpret_cast<const u32x4*>(wb + (int64_t)(hb * TR_HB + sr) * TR_C + sc * 8);
-    po = *reinterpret_cast<const u32x4*>(wo + (int64_t)so * hidden + hb * TR_HB + soc * 8);
-  };
-  auto lstore = [&](int buf) {
-    *reinterpret_cast<u32x4*>(&sWa[buf][sr * TR_WLD + sc * 8]) = pa;
-    *reinterpret_cast<u32x4*>(&sWb[buf][sr * TR_WLD + sc * 8]) = pb;
-    *reinterpret_cast<u32x2*>(&sWo[buf][so * TR_OLD + soc * 8]) = u32x2{po[0], po[1]};
-    *reinterpret_cast<u32x2*>(&sWo[buf][so * TR_OLD + soc * 8 + 4]) = u32x2{po[2], po[3]};
+  const int64_t pix0 = ((int64_t)blockIdx.x * NW + wave) * (32 * PW);
+  // DMA map: slot sl = tid + 64 NW q of each 512-slot matrix chunk (each wave instruction fills 64 contiguous slots)
+  constexpr int NQ = 512 / (64 * NW);
+  auto issue = [&](int hb) {
+    const int buf = hb % TR_NBUF;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int sl = tid + 64 * NW * q;
+      const int ar = sl >> 4, ac = (sl & 15) ^ (ar & 15);              // W_a / W_b: row, source 16-byte column
+      const int orow = sl >> 2, oc = (sl & 3) ^ ((orow >> 2) & 3);     // W_o: row (c_out), source 16-byte column
+      const int lslot = (64 * NW * q + 64 * wave) * 8;
+      lds_dma16(wa + (int64_t)(hb * TR_HB + ar) * TR_C + ac * 8, lds_addr(&sWa[buf][lslot]));
+      lds_dma16(wb + (int64_t)(hb * TR_HB + ar) * TR_C + ac * 8, lds_addr(&sWb[buf][lslot]));
+      lds_dma16(wo + (int64_t)orow * hidden + hb * TR_HB + oc * 8, lds_addr(&sWo[buf][lslot]));
+    }
   };
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
-  rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
-  gload(0);
-  lstore(0);
-  __syncthreads();
+  rt_stage_affine(sLN, ln_w, ln_b, tid, 64 * NW);
+  const int nhb = hidden / TR_HB;
+#pragma unroll
+  for (int q = 0; q < TR_NBUF - 1; ++q)
+    if (q < nhb) issue(q);
+  __syncthreads();                                     // sLN visible
   bf16x8 xb[PW][TR_KS];
 #pragma unroll
   for (int p = 0; p < PW; ++p) {
@@ -58,30 +62,33 @@ __global__ void __launch_bounds__(512) transition_bf16_kernel(const uint16_t* x,
     rt_load(x + (pix < rows ? pix : 0) * TR_C, pix < rows, g, raw);
     rt_ln(raw, g, sLN, eps, xb[p]);
   }
+  // chunk 0 landed (the row loads above are younger and may still be counted), then published
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
   f32x16 acc[PW][4];
 #pragma unroll
   for (int p = 0; p < PW; ++p)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) acc[p][cb] = f32x16{};
-  const int nhb = hidden / TR_HB;
   for (int hb = 0; hb < nhb; ++hb) {
-    const int buf = hb & 1;
-    if (hb + 1 < nhb) gload(hb + 1);
+    const int buf = hb % TR_NBUF;
+    if (hb + TR_NBUF - 1 < nhb) issue(hb + TR_NBUF - 1);  // its buffer held chunk hb - 1, finished before the last barrier
     f32x16 a[PW], b[PW];
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
       a[p] = f32x16{};
       b[p] = f32x16{};
     }
-    const uint16_t* ra = &sWa[buf][n * TR_WLD + 64 * g];
-    const uint16_t* rb = &sWb[buf][n * TR_WLD + 64 * g];
-    bf16x8 fa = as_bf8(*reinterpret_cast<const u32x4*>(ra)), fb = as_bf8(*reinterpret_cast<const u32x4*>(rb));
+    const uint16_t* ra = &sWa[buf][n * TR_C];
+    const uint16_t* rb = &sWb[buf][n * TR_C];
+    auto wfrag = [&](const uint16_t* r, int t) { return as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * ((8 * g + t) ^ (n & 15)))); };
+    bf16x8 fa = wfrag(ra, 0), fb = wfrag(rb, 0);
 #pragma unroll
     for (int t = 0; t < TR_KS; ++t) {
       const bf16x8 ca = fa, cbf = fb;
       if (t + 1 < TR_KS) {                      // one k-step of fragment lookahead
-        fa = as_bf8(*reinterpret_cast<const u32x4*>(ra + 8 * (t + 1)));
-        fb = as_bf8(*reinterpret_cast<const u32x4*>(rb + 8 * (t + 1)));
+        fa = wfrag(ra, t + 1);
+        fb = wfrag(rb, t + 1);
       }
 #pragma unroll
       for (int p = 0; p < PW; ++p) {
@@ -109,19 +116,32 @@ __global__ void __launch_bounds__(512) transition_bf16_kernel(const uint16_t* x,
       }
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
+      const int orr = cb * 32 + n, sw = (orr >> 2) & 3;
+      const uint16_t* wrow = &sWo[buf][orr * TR_HB];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const uint16_t* wrow = &sWo[buf][(cb * 32 + n) * TR_OLD + 16 * s + 4 * g];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(wrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(wrow + 8);
+        // hidden 16s + 4g + 0..3 (chunk 2s, bytes 8g) and 16s + 8 + 4g + 0..3 (chunk 2s + 1)
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(wrow + 8 * ((2 * s) ^ sw) + 4 * g);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(wrow + 8 * ((2 * s + 1) ^ sw) + 4 * g);
         const bf16x8 fo = as_bf8(u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
         for (int p = 0; p < PW; ++p) acc[p][cb] = mfma32(fo, hf[p][s], acc[p][cb]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (hb + 1 < nhb) lstore(buf ^ 1);        // buf ^ 1 was last read before the previous barrier
-    __syncthreads();
+    if (hb + 1 < nhb) {                          // chunk hb + 1 landed: only the later chunks' transfers may be outstanding
+      if constexpr (NQ == 1) {
+        if (hb + 3 < nhb) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      } else {
+        static_assert(NQ == 2, "4 or 8 waves");
+        if (hb + 3 < nhb) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+        else if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __builtin_amdgcn_s_barrier();
+    }
   }
   // epilogue: lane (pixel n, half g) holds c_out = 32 cb + c_row(v, g); after the lane exchange it holds channels
   // 32 cb + 8g .. +7 and 32 cb + 16 + 8g .. +7, stored (with mask and residual) in 16-byte pieces
@@ -253,9 +273,9 @@ extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char
     if (!aligned16(a->x) || !aligned16(a->out) || !aligned16(a->w_a) || !aligned16(a->w_b) || !aligned16(a->w_o) ||
         (a->ln_w && !aligned16(a->ln_w)) || (a->ln_b && !aligned16(a->ln_b)))
       return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
-    const int PW = 1;
-    const dim3 grid((unsigned)cdiv(a->rows, 32 * TR_WAVES * PW)), block(64 * TR_WAVES);
-    hipLaunchKernelGGL((transition_bf16_kernel<PW>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b, a->eps,
+    constexpr int PW = TR_PW, NW = TR_NW;
+    const dim3 grid((unsigned)cdiv(a->rows, 32 * NW * PW)), block(64 * NW);
+    hipLaunchKernelGGL((transition_bf16_kernel<PW, NW>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b, a->eps,
                        (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows, a->hidden);
     return launched(err, errlen, "fpf_transition_fwd(bf16)");
   }

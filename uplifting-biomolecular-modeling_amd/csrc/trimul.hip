@@ -177,17 +177,6 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 // 16 columns j, and after the half-wave lane exchange each lane stores 8 consecutive columns per 16-byte store.
 constexpr int CB_T = 256, CB_K = 32, CB_NBUF = 4;
 
-// One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): the wave's 64 chunks land at lds_base + 16 * lane.
-// Issued through inline assembly so that the only waits on it are the explicit s_waitcnt vmcnt of the slab ring (the
-// compiler would otherwise drain every outstanding transfer before each LDS read it cannot prove disjoint).  lds_base is
-// wave-uniform (it goes through M0).
-__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
-}
-
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t nbatch) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[CB_NBUF][CB_T * CB_K];
