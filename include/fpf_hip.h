@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 1
+#define FPF_ABI_VERSION 2
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
 enum {
@@ -174,9 +174,33 @@ typedef struct {
   float scale;             /* <= 0: 1/sqrt(D) */
   void* workspace;
   size_t workspace_bytes;
+  int64_t row0;            /* attention rows [row0, row0 + rows) only (bf16; the `big` row-chunked driver); rows <= 0: all N */
+  int64_t rows;
+  const float* bias_in;    /* NULL: the block computes the bias; else the full [B, H, N, N] fp32 bias of fpf_triattn_bias_fwd
+                              (required with a row range: every attention row needs the bias of every pair) */
 } FpfTriattnBlockArgs;
-size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int32_t C, int32_t H, int32_t D, int32_t dtype);
+/* Workspace for `rows` attention rows (rows <= 0: all N). */
+size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_t rows, int32_t C, int32_t H, int32_t D, int32_t dtype);
 int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen);
+
+/* The bias pass of the row-chunked (`big`) triangle-attention block: bias[b, h, i, j] = LN(x)[i, j] . w_b[h] for every pixel of
+ * the attention frame (x = z or z^T), fp32, bf16 block only.  Replaces pass 1 of common/opt_core/opt_core/mem/chunk.py:424
+ * (triangle_attention_chunked: the full bias assembled block by block before the per-row attention pass). */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* FPF_DT_BF16 */
+  int64_t B, N;
+  int32_t C, H, D;
+  const void* z;           /* [B, N, N, C] */
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
+  const void* w_qkvg;      /* may be NULL (not read) */
+  const void* w_b;         /* [H, C] */
+  int32_t ending;
+  float* bias;             /* [B, H, N, N] fp32 out */
+} FpfTriattnBiasArgs;
+int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen);
 
 /* ---------------------------------------------------------------------------------------------------------------- triangle attention (block stages)
  * The block's prologue and epilogue as separate calls, for callers that run their own core between them.

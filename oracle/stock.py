@@ -24,8 +24,8 @@ import math
 
 import torch
 
-__all__ = ["layer_norm", "triangle_attention_op", "tri_attn", "triatt_prologue", "triatt_epilogue", "trimul", "transition",
-           "pair_block", "make_block_params", "block_flops"]
+__all__ = ["layer_norm", "triangle_attention_op", "tri_attn", "triatt_prologue", "triatt_epilogue", "trimul", "trimul_rows",
+           "tri_attn_rows", "transition", "pair_block", "make_block_params", "block_flops"]
 
 
 def layer_norm(x, w=None, b=None, eps=1e-5):
@@ -160,6 +160,53 @@ def trimul(z, mask=None, *, direction, weights, residual=False, dtype=torch.floa
     upd = torch.sigmoid(torch.matmul(x, w["w_og"].t())) * torch.matmul(layer_norm(X, w["ln_out_w"], w["ln_out_b"], eps), w["w_o"].t())
     out = z4.to(dtype) + upd if residual else upd
     return out[0] if sq else out
+
+
+def trimul_rows(z, mask, rows, *, direction, weights, dtype=torch.float32, eps=1e-5):
+    """Rows ``rows`` of ``trimul``'s update (no residual) for one pair tensor z [N, N, c_z]: the statement above with a computed
+    only for the rows (outgoing) / columns (incoming) those output rows read, so that sampled rows of an N = 2048 problem fit a
+    CPU check.  Pinned by: equality with ``trimul(...)[rows]`` (tests/test_oracle.py)."""
+    w = {k_: v_.to(dtype) for k_, v_ in weights.items() if hasattr(v_, "to")}
+    x = layer_norm(z.to(dtype), w["ln_in_w"], w["ln_in_b"], eps)
+    m = torch.ones(z.shape[0], z.shape[1], 1, dtype=dtype) if mask is None else mask.to(dtype).unsqueeze(-1)
+    idx = torch.as_tensor(rows, dtype=torch.long)
+    b = torch.sigmoid(torch.matmul(x, w["w_bg"].t())) * torch.matmul(x, w["w_bp"].t()) * m
+    if direction in ("outgoing", "out"):
+        xa, ma = x[idx], m[idx]                                                      # [R, N(k), C]
+        a = torch.sigmoid(torch.matmul(xa, w["w_ag"].t())) * torch.matmul(xa, w["w_ap"].t()) * ma
+        X = torch.einsum("rkd,jkd->rjd", a, b)
+    elif direction in ("incoming", "in"):
+        xa, ma = x[:, idx], m[:, idx]                                                # [N(k), R, C]
+        a = torch.sigmoid(torch.matmul(xa, w["w_ag"].t())) * torch.matmul(xa, w["w_ap"].t()) * ma
+        X = torch.einsum("krd,kjd->rjd", a, b)
+    else:
+        raise ValueError(direction)
+    xr = x[idx]
+    return torch.sigmoid(torch.matmul(xr, w["w_og"].t())) * torch.matmul(layer_norm(X, w["ln_out_w"], w["ln_out_b"], eps), w["w_o"].t())
+
+
+def tri_attn_rows(z, P, mask, rows, *, ending=False, dtype=torch.float32):
+    """Attention-frame rows ``rows`` of the triangle-attention update for one pair tensor z [N, N, C] (x = z, or z^T for the ending
+    node): the full bias from every pixel, then the op (-inf mask; a fully masked row is the uniform mean) and the gated output
+    projection for those rows only.  Row i of the result is z row i (starting) / z column i (ending) of the update.  Pinned by:
+    equality with ``triatt_epilogue(triangle_attention_op(triatt_prologue(...)))`` restricted to the rows (tests/test_oracle.py)."""
+    H, D = int(P["H"]), int(P["D"])
+    x = z.to(dtype)
+    m = torch.ones(z.shape[0], z.shape[1], dtype=torch.bool) if mask is None else mask != 0
+    if ending:
+        x = x.transpose(0, 1)
+        m = m.transpose(0, 1)
+    xl = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
+    N = xl.shape[0]
+    idx = torch.as_tensor(rows, dtype=torch.long)
+    bias = torch.matmul(xl, P["w_b"].to(dtype).t()).permute(2, 0, 1).unsqueeze(0).unsqueeze(0)       # [1, 1, H, N, N]
+    xr = xl[idx]                                                                                      # [R, N, C]
+
+    def heads(wn):
+        return torch.matmul(xr, P[wn].to(dtype).t()).view(len(idx), N, H, D).permute(0, 2, 1, 3).unsqueeze(0)
+    o = triangle_attention_op(heads("w_q"), heads("w_k"), heads("w_v"), bias, m[idx][None, :, None, None, :], dtype=dtype)
+    g = torch.matmul(xr, P["w_g"].to(dtype).t()).unsqueeze(0)
+    return triatt_epilogue(o, g, P, dtype=dtype)[0]
 
 
 def transition(x, w_a, w_b, w_o, ln_w=None, ln_b=None, *, eps=1e-5, mask=None, residual=False, dtype=torch.float64):

@@ -29,13 +29,17 @@ def assert_f32_close(out, ref, what=""):
     return rl
 
 
-def assert_bf16_residual_close(out, ref, what=""):
-    """Residual-form outputs (z + update stored in bf16): the update bars plus the half-ulp of the bf16 output itself, which no
-    kernel can avoid once |z + update| >= 4 (half-ulp 2^-7 there, 2^-6 from 8)."""
+def assert_bf16_ulp_close(out, ref, what=""):
+    """bf16 outputs whose magnitude reaches 4 and beyond (residual forms z + update, large updates): the bars applied to the
+    error in excess of the half-ulp of the bf16 output itself, which no kernel with a bf16 output can avoid once |value| >= 4
+    (half-ulp 2^-7 there, 2^-6 from 8).  The relative-L2 bar is unchanged."""
     o, r = out.double().cpu(), ref.double().cpu()
     ulp = torch.pow(2.0, torch.floor(torch.log2(r.abs().clamp_min(2.0 ** -126))) - 7)
     excess = ((o - r).abs() - 0.5 * ulp).max().item()
     rl = rel_l2(o, r)
-    print("[parity] %s max(|err| - ulp/2)=%.3e rel_l2=%.3e" % (what, excess, rl))
+    print("[parity] %s max_abs=%.3e max(|err| - ulp/2)=%.3e rel_l2=%.3e" % (what, max_abs(o, r), excess, rl))
     assert excess <= BF16_MAX_ABS and rl <= BF16_REL_L2, "%s excess=%.3e rel_l2=%.3e" % (what, excess, rl)
     return excess, rl
+
+
+assert_bf16_residual_close = assert_bf16_ulp_close

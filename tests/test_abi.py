@@ -40,7 +40,7 @@ def test_header_declares_the_entry_points():
     d = _declared()
     for must in ("fpf_abi_version", "fpf_describe", "fpf_layernorm_fwd", "fpf_transition_fwd", "fpf_trimul_fwd", "fpf_trimul_workspace_bytes",
                  "fpf_triattn_fwd", "fpf_triattn_block_fwd", "fpf_triattn_block_workspace_bytes", "fpf_triattn_prologue_fwd",
-                 "fpf_triattn_epilogue_fwd"):
+                 "fpf_triattn_epilogue_fwd", "fpf_triattn_bias_fwd"):
         assert must in d, must
 
 
@@ -61,7 +61,7 @@ def test_ctypes_blocks_follow_the_header_field_order():
     st = _structs()
     pairs = {"FpfLnArgs": L.LnArgs, "FpfTransitionArgs": L.TransitionArgs, "FpfTrimulArgs": L.TrimulArgs, "FpfTriattnArgs": L.TriattnArgs,
              "FpfTriattnBlockArgs": L.TriattnBlockArgs, "FpfTriattnPrologueArgs": L.TriattnPrologueArgs,
-             "FpfTriattnEpilogueArgs": L.TriattnEpilogueArgs}
+             "FpfTriattnEpilogueArgs": L.TriattnEpilogueArgs, "FpfTriattnBiasArgs": L.TriattnBiasArgs}
     assert set(pairs) == set(st), sorted(st)
     for cname, py in pairs.items():
         assert [f[0] for f in py._fields_] == st[cname], cname
@@ -74,9 +74,12 @@ def test_workspace_queries_need_no_device():
     assert lib.fpf_trimul_workspace_bytes(1, 768, 128, 128, L.DT_BF16) >= 3 * 128 * 768 * 768 * 2
     assert lib.fpf_trimul_workspace_bytes(1, 100, 128, 128, L.DT_BF16) >= 3 * 128 * 128 * 128 * 2
     # tri-att block: q, k, v, o, g (H*D per pixel) + fp32 bias (H per pixel)
-    need = lib.fpf_triattn_block_workspace_bytes(1, 768, 128, 4, 32, L.DT_BF16)
+    need = lib.fpf_triattn_block_workspace_bytes(1, 768, 0, 128, 4, 32, L.DT_BF16)
     assert need >= 5 * 768 * 768 * 128 * 2 + 768 * 768 * 4 * 4
-    assert lib.fpf_triattn_block_workspace_bytes(1, 768, 128, 4, 32, L.DT_F32) > need
+    assert lib.fpf_triattn_block_workspace_bytes(1, 768, 0, 128, 4, 32, L.DT_F32) > need
+    # a row chunk holds the q / k / v / o / g of its rows only (plus the full bias)
+    part = lib.fpf_triattn_block_workspace_bytes(1, 2048, 256, 128, 4, 32, L.DT_BF16)
+    assert 5 * 256 * 2048 * 128 * 2 <= part < 5 * 300 * 2048 * 128 * 2 + 2048 * 2048 * 4 * 4 + 4096
 
 
 def test_version_mismatch_is_refused_before_any_launch():

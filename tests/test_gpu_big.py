@@ -1,0 +1,191 @@
+"""The memory-lean `big` line (common/opt_core/opt_core/mem/chunk.py:424, the row-chunked triangle attention) on the GPU.
+
+Two bars:
+  * chunked == whole-tensor, bit for bit: every attention row's arithmetic is independent of the others (per-lane running max,
+    per-row softmax, per-pixel projections), so the chunk size may not change one bit of the result;
+  * config 4 of the benchmark set (N = 2048, ragged mask of chains 900 + 700 + 300 and 148 padded positions, one pair block in
+    `big` mode): equal to the `fast` line bitwise, and sampled rows of every site against the fp32 oracle restated per row.
+Byte offsets past 2^31 (N = 3072, a 2.4 GB pair tensor) are exercised on the per-pixel kernels (LayerNorm, transition).
+"""
+import pytest
+import torch
+
+from _util import assert_bf16_close, assert_bf16_residual_close, assert_bf16_ulp_close
+from oracle import stock as S
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _ta_weights(seed):
+    P = S.make_block_params(c_z=128, heads=4, head_dim=32, seed=seed)["tas"]
+    g = torch.Generator().manual_seed(seed + 100)
+    P["ln_w"] = 1 + 0.1 * torch.randn(128, generator=g)
+    P["ln_b"] = 0.1 * torch.randn(128, generator=g)
+    for n in ("w_q", "w_k", "w_v", "w_g", "w_b", "w_o"):
+        P[n] = P[n].to(torch.bfloat16).float()
+    return P
+
+
+def _ta_pack(P):
+    from fpf_hip.attn import pair_fused as PF
+    return PF.pack_triattn_weights(w_o=P["w_o"].to(DEV, torch.bfloat16), n_heads=4, head_dim=32, ln_w=P["ln_w"].to(DEV),
+                                   ln_b=P["ln_b"].to(DEV), w_q=P["w_q"].to(DEV, torch.bfloat16), w_k=P["w_k"].to(DEV, torch.bfloat16),
+                                   w_v=P["w_v"].to(DEV, torch.bfloat16), w_g=P["w_g"].to(DEV, torch.bfloat16),
+                                   w_b=P["w_b"].to(DEV, torch.bfloat16))
+
+
+def _ragged_mask(N, chains, pad):
+    valid = torch.zeros(N)
+    valid[:sum(chains)] = 1
+    assert sum(chains) + pad == N
+    return torch.outer(valid, valid)
+
+
+# ------------------------------------------------------------------------------------------------------- chunked == whole
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("residual", [False, True])
+@pytest.mark.parametrize("chunk", [64, 7])
+def test_chunked_block_bitwise_equals_whole(ending, residual, chunk):
+    from fpf_hip.attn import pair_fused as PF
+    N = 300
+    P = _ta_weights(3)
+    W = _ta_pack(P)
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(31)).to(torch.bfloat16).to(DEV)
+    mask = _ragged_mask(N, (150, 90, 40), 20).unsqueeze(0).to(DEV)
+    print("[big] N=%d chunk=%d ending=%s residual=%s" % (N, chunk, ending, residual), flush=True)
+    z1, z2 = z.clone(), z.clone()
+    u1 = PF.tri_attn_block(z1, W, mask, ending=ending, residual=residual)
+    u2 = PF.tri_attn_block_chunked(z2, W, mask, ending=ending, residual=residual, chunk=chunk)
+    torch.cuda.synchronize()
+    if residual:
+        assert u1.data_ptr() == z1.data_ptr() and u2.data_ptr() == z2.data_ptr()
+    else:
+        assert torch.equal(z1, z) and torch.equal(z2, z), "residual=False must leave z untouched"
+    assert torch.equal(u1, u2), "chunked != whole: max diff %.3e" % (u1.float() - u2.float()).abs().max().item()
+
+
+def test_chunked_block_against_oracle():
+    from fpf_hip.attn import pair_fused as PF
+    N = 130
+    P = _ta_weights(4)
+    W = _ta_pack(P)
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(41)).to(torch.bfloat16)
+    mask = _ragged_mask(N, (60, 50), 20).unsqueeze(0)
+    for ending in (False, True):
+        u = PF.tri_attn_block_chunked(z.to(DEV), W, mask.to(DEV), ending=ending, residual=False, chunk=48)
+        torch.cuda.synchronize()
+        ref = S.tri_attn(z.float(), P, mask, ending=ending, dtype=torch.float32)
+        assert_bf16_close(u, ref, "chunked block ending=%s" % ending)
+
+
+def test_chunked_block_refuses_bad_chunk():
+    from fpf_hip.attn import pair_fused as PF
+    W = _ta_pack(_ta_weights(5))
+    z = torch.randn(1, 16, 16, 128).to(torch.bfloat16).to(DEV)
+    with pytest.raises(PF.Unsupported):
+        PF.tri_attn_block_chunked(z, W, None, chunk=0)
+
+
+# ------------------------------------------------------------------------------------------------------- config 4 (N = 2048)
+N_BIG = 2048
+CHAINS = (900, 700, 300)
+PAD = 148
+SAMPLE = [0, 1, 255, 256, 899, 900, 1599, 1600, 1899, 1900, 2047]     # chunk edges, chain edges, padded rows
+
+
+@pytest.fixture(scope="module")
+def big_case():
+    from fpf_hip import pairformer as PFM
+    params = PFM.random_params(seed=0)
+    blk = PFM.PairBlock(params, DEV, torch.bfloat16)
+    z = torch.randn(1, N_BIG, N_BIG, 128, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+    mask = _ragged_mask(N_BIG, CHAINS, PAD).unsqueeze(0)
+    return params, blk, z, mask
+
+
+def test_config4_pair_block_big_equals_fast(big_case):
+    from fpf_hip import pairformer as PFM
+    _, blk, z, mask = big_case
+    zd, md = z.to(DEV), mask.to(DEV)
+    print("[big] config4 pair block N=%d fast" % N_BIG, flush=True)
+    z_fast = PFM.pair_block(zd.clone(), md, blk, word="fast")
+    print("[big] config4 pair block N=%d big rows=256" % N_BIG, flush=True)
+    z_big = PFM.pair_block(zd.clone(), md, blk, word="big", rows=256)
+    torch.cuda.synchronize()
+    assert torch.isfinite(z_big.float()).all()
+    assert torch.equal(z_fast, z_big), "big != fast: max diff %.3e" % (z_fast.float() - z_big.float()).abs().max().item()
+    assert not torch.equal(z_big, zd)
+
+
+@pytest.mark.parametrize("ending", [False, True])
+def test_config4_tri_attn_sampled_rows(big_case, ending):
+    from fpf_hip.attn import pair_fused as PF
+    params, blk, z, mask = big_case
+    site = "tae" if ending else "tas"
+    P = {k: (v.to(torch.bfloat16).float() if k.startswith("w_") else v) for k, v in params[site].items()}
+    print("[big] config4 tri-att ending=%s" % ending, flush=True)
+    u = PF.tri_attn_block_chunked(z.to(DEV), blk.ta[site], mask.to(DEV), ending=ending, residual=False, chunk=256)
+    torch.cuda.synchronize()
+    u = u[0].cpu()
+    got = u[:, SAMPLE].transpose(0, 1) if ending else u[SAMPLE]
+    ref = S.tri_attn_rows(z[0].float(), P, mask[0], SAMPLE, ending=ending, dtype=torch.float32)
+    assert_bf16_close(got, ref, "config4 tri-att ending=%s rows %s" % (ending, SAMPLE))
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_config4_trimul_sampled_rows(big_case, direction):
+    from fpf_hip.kernels import trimul as TM
+    params, blk, z, mask = big_case
+    site = "tmo" if direction == "outgoing" else "tmi"
+    w = blk.tmo if direction == "outgoing" else blk.tmi
+    print("[big] config4 trimul %s" % direction, flush=True)
+    u = TM.triangle_multiplication(z.to(DEV), mask.to(DEV), direction=direction, weights=w, word="big", residual=False)
+    torch.cuda.synchronize()
+    got = u[0, SAMPLE].cpu()
+    wf = {k: (v.to(torch.bfloat16).float() if k.startswith("w_") else v) for k, v in params[site].items()}
+    ref = S.trimul_rows(z[0].float(), mask[0], SAMPLE, direction=direction, weights=wf, dtype=torch.float32)
+    # The update reaches |u| ~ 5 here, where the bf16 output's own half-ulp is 7.8e-3 of the 2e-2 max-abs budget: the bar is
+    # applied above that half-ulp (the rel-L2 bar is unchanged).  For scale: the stock bf16-autocast statement (bf16 after every
+    # op) measures max-abs 3.7e-2 / rel-L2 6.1e-3 against fp32 on inputs of this kind (c = 128, N = 384), this path 2.1e-2 / 4.5e-3.
+    assert_bf16_ulp_close(got, ref, "config4 trimul %s rows %s" % (direction, SAMPLE))
+
+
+def test_config4_transition_sampled_rows(big_case):
+    from fpf_hip.kernels import transition as TR
+    params, blk, z, mask = big_case
+    print("[big] config4 transition", flush=True)
+    y, sel = TR.transition(z.to(DEV), blk.tr, word="big", residual=True)
+    torch.cuda.synchronize()
+    assert sel.row == "hip_gfx950"
+    p = {k: v.to(torch.bfloat16).float() if k.startswith("w_") else v for k, v in params["tr"].items()}
+    got = y[0, SAMPLE].cpu()
+    ref = S.transition(z[0, SAMPLE].float(), p["w_a"], p["w_b"], p["w_o"], p["ln_w"], p["ln_b"], residual=True, dtype=torch.float32)
+    assert_bf16_residual_close(got, ref, "config4 transition rows %s" % SAMPLE)
+
+
+# ------------------------------------------------------------------------------------------------------- offsets past 2^31 bytes
+def test_per_pixel_kernels_past_2gb():
+    """A 3072 x 3072 x 128 bf16 pair tensor (2.4 GB): the last rows, whose byte offsets exceed 2^31, against the oracle."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import ln as LN
+    from fpf_hip.kernels import transition as TR
+    N = 3072
+    params = PFM.random_params(seed=2)
+    blk = PFM.PairBlock(params, DEV, torch.bfloat16)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    z = torch.randn(1, N, N, 128, generator=g, device=DEV).to(torch.bfloat16)
+    assert z.numel() * 2 > 2 ** 31
+    print("[big] N=%d transition + layer_norm" % N, flush=True)
+    y, _ = TR.transition(z, blk.tr, word="fast", residual=False)
+    w = torch.linspace(0.5, 1.5, 128, device=DEV)
+    b = torch.linspace(-0.1, 0.1, 128, device=DEV)
+    x_ln, _ = LN.layer_norm(z, (128,), w, b, 1e-5, word="fast")
+    torch.cuda.synchronize()
+    rows = [0, N - 2, N - 1]
+    zs = z[0, rows].float().cpu()                                        # [3, N, 128]: the last two z rows sit past 2^31 bytes
+    p = {k: v.to(torch.bfloat16).float() if k.startswith("w_") else v for k, v in params["tr"].items()}
+    ref = S.transition(zs, p["w_a"], p["w_b"], p["w_o"], p["ln_w"], p["ln_b"], dtype=torch.float32)
+    assert_bf16_close(y[0, rows].cpu(), ref, "transition N=%d rows %s" % (N, rows))
+    ref_ln = S.layer_norm(zs, w.cpu(), b.cpu(), 1e-5)
+    assert_bf16_close(x_ln[0, rows].cpu(), ref_ln, "layer_norm N=%d rows %s" % (N, rows))

@@ -323,3 +323,35 @@ def test_pair_block_config1_runs_and_is_finite():
     z = torch.randn(1, 8, 8, 32, generator=torch.Generator().manual_seed(0))
     out = S.pair_block(z, torch.ones(1, 8, 8), P, dtype=torch.float64)
     assert out.shape == z.shape and torch.isfinite(out).all()
+
+
+# ----------------------------------------------------------------------------------------------------------------- row-sampled forms
+def test_trimul_rows_equal_the_full_statement():
+    g = torch.Generator().manual_seed(21)
+    N, C = 9, 8
+    W = {n: torch.randn(C, C, generator=g, dtype=torch.float64) / math.sqrt(C) for n in ("w_ag", "w_ap", "w_bg", "w_bp", "w_o", "w_og")}
+    W.update(ln_in_w=1 + 0.1 * torch.randn(C, generator=g, dtype=torch.float64), ln_in_b=0.1 * torch.randn(C, generator=g, dtype=torch.float64),
+             ln_out_w=1 + 0.1 * torch.randn(C, generator=g, dtype=torch.float64), ln_out_b=0.1 * torch.randn(C, generator=g, dtype=torch.float64))
+    z = torch.randn(N, N, C, generator=g, dtype=torch.float64)
+    mask = (torch.rand(N, N, generator=g) > 0.2).double()
+    rows = [0, 4, 8]
+    for d in ("outgoing", "incoming"):
+        full = S.trimul(z, mask, direction=d, weights=W)
+        part = S.trimul_rows(z, mask, rows, direction=d, weights=W, dtype=torch.float64)
+        assert torch.allclose(part, full[rows], atol=1e-12), d
+
+
+def test_tri_attn_rows_equal_the_full_statement():
+    P = _small_triatt_params()
+    g = torch.Generator().manual_seed(22)
+    z = torch.randn(7, 7, 16, generator=g, dtype=torch.float64)
+    mask = torch.ones(7, 7, dtype=torch.float64)
+    mask[:, 5:] = 0
+    mask[5:, :] = 0
+    rows = [0, 3, 6]
+    for ending in (False, True):
+        q, k, v, gg, bias = S.triatt_prologue(z.unsqueeze(0), P, ending=ending)
+        mx = (mask.t() if ending else mask).bool()[None, :, None, None, :]
+        full = S.triatt_epilogue(S.triangle_attention_op(q, k, v, bias, mx), gg, P)[0]
+        part = S.tri_attn_rows(z, P, mask, rows, ending=ending, dtype=torch.float64)
+        assert torch.allclose(part, full[rows], atol=1e-12), ending

@@ -269,10 +269,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
         mx[r] = half_max(m0) * c2;
         need |= mx[r] > mrow[r] + TA_HEADROOM;
       }
-      if (__ballot(need) != 0) {       // some query's max moved past the headroom: move the running max of every row (exact)
+      if (__ballot(need) != 0) {       // some query's max moved past the headroom: move that query's running max (exact)
 #pragma unroll
         for (int r = 0; r < TA_R; ++r) {
-          const float mnew = fmaxf(mrow[r], mx[r]);
+          // per lane and row: a query's trajectory depends on its own logits only, so results do not depend on which rows
+          // share a workgroup (row-chunked calls are bitwise equal to whole-tensor ones)
+          const float mnew = (mx[r] > mrow[r] + TA_HEADROOM) ? fmaxf(mrow[r], mx[r]) : mrow[r];
           const float alpha = (mnew == -INFINITY) ? 1.0f : fast_exp2(mrow[r] - mnew);
           lrow[r] *= alpha;
 #pragma unroll
@@ -444,45 +446,64 @@ __global__ void __launch_bounds__(64) triattn_core_f32(const CoreParamsF p) {
 // 256-byte pixel).
 constexpr int TP_C = 128, TP_HD = 128;
 
-__global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __restrict__ z, const float* __restrict__ ln_w,
-                                                             const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ w_qkvg,
-                                                             const uint16_t* __restrict__ w_b, int H, uint16_t* __restrict__ qo,
-                                                             uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, uint16_t* __restrict__ go,
-                                                             float* __restrict__ bo, int64_t N, int64_t Jp, int64_t B, int ending,
-                                                             int write_g) {
+// Outputs are selected by flags (PRO_QKV: q, k, v^T; PRO_G: g; PRO_BIAS: the full bias) and cover the attention rows
+// [row0, row0 + rows): q / k / v^T / g are indexed by the row within that range, the bias by the absolute row.  The `big`
+// chunked driver runs a bias-only pass over every row, then q / k / v^T per row chunk.
+enum { PRO_QKV = 1, PRO_G = 2, PRO_BIAS = 4 };
+struct ProParams {
+  const uint16_t* z;
+  const float* ln_w;
+  const float* ln_b;
+  float eps;
+  const uint16_t* w_qkvg;
+  const uint16_t* w_b;
+  int H;
+  uint16_t* q;
+  uint16_t* k;
+  uint16_t* v;
+  uint16_t* g;
+  float* bias;
+  int64_t N, Jp, B, row0, rows;
+  int ending, flags;
+};
+
+__global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[(4 * TP_HD + 32) * RT_LD];
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
-  rt_stage_weights(sW, w_qkvg, 4 * TP_HD, 4 * TP_HD, tid, 512);
-  rt_stage_weights(sW + 4 * TP_HD * RT_LD, w_b, 32, H, tid, 512);
+  rt_stage_affine(sLN, p.ln_w, p.ln_b, tid, 512);
+  rt_stage_weights(sW, p.w_qkvg, 4 * TP_HD, 4 * TP_HD, tid, 512);
+  rt_stage_weights(sW + 4 * TP_HD * RT_LD, p.w_b, 32, p.H, tid, 512);
   __syncthreads();
-  const int D = TP_HD / H;
-  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
+  const int H = p.H, D = TP_HD / H;
+  const int64_t N = p.N, Jp = p.Jp, R = p.rows;
+  const int64_t tpr = cdiv(N, 32), per_b = R * tpr, total = p.B * per_b;
   const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
   u32x4 raw[8];                                         // the next tile's pixel rows, loaded while this tile computes
   auto fetch = [&](int64_t tt) {
-    const int64_t b = tt / per_b, i = (tt % per_b) / tpr, j = (tt % tpr) * 32 + n;
+    const int64_t b = tt / per_b, i = p.row0 + (tt % per_b) / tpr, j = (tt % tpr) * 32 + n;
     const bool live = j < N;
-    const int64_t zpix = ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
-    rt_load(z + zpix * RT_C, live, g, raw);
+    const int64_t zpix = p.ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
+    rt_load(p.z + zpix * RT_C, live, g, raw);
   };
   if ((int64_t)blockIdx.x * RT_WAVES + wave < total) fetch((int64_t)blockIdx.x * RT_WAVES + wave);
   for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
-    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+    const int64_t b = t / per_b, ii = (t % per_b) / tpr, i = p.row0 + ii, j = (t % tpr) * 32 + n;
     const bool live = j < N;
     bf16x8 xb[8];
-    rt_ln(raw, g, sLN, eps, xb);
+    rt_ln(raw, g, sLN, p.eps, xb);
     if (t + stride < total) fetch(t + stride);
 #pragma unroll 1
     for (int blk = 0; blk < 17; ++blk) {
-      if (blk >= 12 && blk < 16 && !write_g) continue;  // the gate-fused epilogue recomputes g
-      if (blk >= 8 && blk < 12) {                         // v, transposed: vT[b][i][h][d][Jp] -- the swapped product x W_v^T
+      if (blk < 12 && !(p.flags & PRO_QKV)) continue;
+      if (blk >= 12 && blk < 16 && !(p.flags & PRO_G)) continue;
+      if (blk == 16 && !(p.flags & PRO_BIAS)) continue;
+      if (blk >= 8 && blk < 12) {                         // v, transposed: vT[b][ii][h][d][Jp] -- the swapped product x W_v^T
         // puts d on the lanes and 16 pixels in the registers; the lane exchange then gives each lane 8 consecutive pixels
         const f32x16 acc = rt_gemm32_xw(sW, blk * 32, n, g, xb);
         u32x4 lo, hi;
         rt_pack16(acc, lo, hi);
-        uint16_t* dst = vo + (((b * N + i) * H + (blk & 3)) * (int64_t)D + n) * Jp + (j - n) + 8 * g;
+        uint16_t* dst = p.v + (((b * R + ii) * H + (blk & 3)) * (int64_t)D + n) * Jp + (j - n) + 8 * g;
         *reinterpret_cast<u32x4*>(dst) = lo;               // whole 32-pixel tile: Jp covers it (padding is never read)
         *reinterpret_cast<u32x4*>(dst + 16) = hi;
         continue;
@@ -492,14 +513,14 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const uint16_t* __r
         u32x4 lo, hi;
         rt_pack16(acc, lo, hi);
         if (!live) continue;
-        uint16_t* dst = blk < 8 ? (blk < 4 ? qo : ko) + (((b * N + i) * H + (blk & 3)) * N + j) * D + 8 * g   // [B, I, H, J, D]
-                                : go + ((b * N + i) * N + j) * TP_HD + (blk - 12) * 32 + 8 * g;            // [B, I, J, HD]
+        uint16_t* dst = blk < 8 ? (blk < 4 ? p.q : p.k) + (((b * R + ii) * H + (blk & 3)) * N + j) * D + 8 * g   // [B, R, H, J, D]
+                                : p.g + ((b * R + ii) * N + j) * TP_HD + (blk - 12) * 32 + 8 * g;             // [B, R, J, HD]
         *reinterpret_cast<u32x4*>(dst) = lo;
         *reinterpret_cast<u32x4*>(dst + 16) = hi;
-      } else if (g == 0 && live) {                        // bias (fp32): [B, H, I, J]
+      } else if (g == 0 && live) {                        // bias (fp32): [B, H, I, J], absolute row
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          if (v < H) bo[((b * H + v) * N + i) * N + j] = acc[v];
+          if (v < H) p.bias[((b * H + v) * N + i) * N + j] = acc[v];
       }
     }
   }
@@ -576,7 +597,8 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
 __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t* zin, const uint16_t* __restrict__ o,
                                                                   const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
                                                                   const uint16_t* __restrict__ w_g, const uint16_t* __restrict__ w_o,
-                                                                  uint16_t* zout, int64_t N, int64_t B, int ending, int residual) {
+                                                                  uint16_t* zout, int64_t N, int64_t B, int64_t row0, int64_t rows, int ending,
+                                                                  int residual) {
   __shared__ __attribute__((aligned(16))) uint16_t sWg[RT_C * RT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t sWo[RT_C * RT_LD];   // columns permuted to the k-step order above
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
@@ -591,10 +613,10 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
   }
   __syncthreads();
   constexpr int H = TP_HD / TA_D;
-  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
+  const int64_t tpr = cdiv(N, 32), per_b = rows * tpr, total = B * per_b;
   const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
   for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
-    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+    const int64_t b = t / per_b, ii = (t % per_b) / tpr, i = row0 + ii, j = (t % tpr) * 32 + n;
     const bool live = j < N;
     const int64_t zpix = ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
     bf16x8 xb[8];
@@ -606,7 +628,7 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
     f32x16 acc[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[k] = f32x16{};
-    const uint16_t* op = o + (((b * N + i) * H) * N + (live ? j : 0)) * TA_D + 4 * g;
+    const uint16_t* op = o + (((b * rows + ii) * H) * N + (live ? j : 0)) * TA_D + 4 * g;   // o rows of this range
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
       const f32x16 gacc = rt_gemm32(sWg, cb * 32, n, g, xb);     // g of head cb: channels cb*32 + c_row(v, g)
@@ -862,17 +884,6 @@ extern "C" int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err,
   return core_launch(a, static_cast<hipStream_t>(stream), err, errlen);
 }
 
-extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int32_t C, int32_t H, int32_t D, int32_t dtype) {
-  (void)C;
-  const size_t elt = dtype == FPF_DT_F32 ? 4 : 2;
-  const size_t pix = (size_t)B * (size_t)N * (size_t)N;
-  const size_t HD = (size_t)H * (size_t)D;
-  // q, k, v, o, g (HD per pixel each; V^T rows padded to N rounded up to 32) + bias (H fp32 per pixel), 256-byte aligned regions
-  const size_t r1 = ((size_t)B * N * fpf::cdiv(N, 32) * 32 * HD * elt + 255) & ~(size_t)255;
-  const size_t r2 = (pix * (size_t)H * 4 + 255) & ~(size_t)255;
-  return 5 * r1 + r2;
-}
-
 namespace fpf {
 
 // Shape / alignment gate shared by the block and its two stages.
@@ -891,17 +902,41 @@ static int block_shape_check(int dtype, int64_t B, int C, int64_t H, int64_t D, 
 
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
-                           hipStream_t st, char* err, size_t errlen, int write_g = 1) {
+                           hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
+                           int64_t rows = -1) {
+  if (rows < 0) rows = N;
   if (dtype == FPF_DT_BF16) {
-    if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || !aligned16(q) || !aligned16(k) || !aligned16(v) || (write_g && !aligned16(g)) ||
-        !aligned16(bias))
+    if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || ((flags & PRO_QKV) && (!aligned16(q) || !aligned16(k) || !aligned16(v))) ||
+        ((flags & PRO_G) && !aligned16(g)) || ((flags & PRO_BIAS) && !aligned16(bias)))
       return fail(err, errlen, FPF_E_ALIGN, "prologue operands must be 16-byte aligned");
-    const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
-    if (v_ld < cdiv(N, 32) * 32 || v_ld % 8) return fail(err, errlen, FPF_E_SHAPE, "v_ld %lld: V^T rows need N rounded up to 32", (long long)v_ld);
-    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)z, ln_w, ln_b, eps, (const uint16_t*)w_qkvg,
-                       (const uint16_t*)w_b, H, (uint16_t*)q, (uint16_t*)k, (uint16_t*)v, (uint16_t*)g, bias, N, v_ld, B, ending, write_g);
+    if ((flags & PRO_QKV) && (v_ld < cdiv(N, 32) * 32 || v_ld % 8))
+      return fail(err, errlen, FPF_E_SHAPE, "v_ld %lld: V^T rows need N rounded up to 32", (long long)v_ld);
+    ProParams p{};
+    p.z = (const uint16_t*)z;
+    p.ln_w = ln_w;
+    p.ln_b = ln_b;
+    p.eps = eps;
+    p.w_qkvg = (const uint16_t*)w_qkvg;
+    p.w_b = (const uint16_t*)w_b;
+    p.H = H;
+    p.q = (uint16_t*)q;
+    p.k = (uint16_t*)k;
+    p.v = (uint16_t*)v;
+    p.g = (uint16_t*)g;
+    p.bias = bias;
+    p.N = N;
+    p.Jp = v_ld;
+    p.B = B;
+    p.row0 = row0;
+    p.rows = rows;
+    p.ending = ending;
+    p.flags = flags;
+    const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
+    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
+  if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS))
+    return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output)");
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
                      (const float*)w_b, C, H, D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N, ending);
@@ -951,6 +986,32 @@ extern "C" int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* s
                          static_cast<hipStream_t>(stream), err, errlen);
 }
 
+extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_t rows, int32_t C, int32_t H, int32_t D, int32_t dtype) {
+  (void)C;
+  if (rows <= 0 || rows > N) rows = N;
+  const size_t elt = dtype == FPF_DT_F32 ? 4 : 2;
+  const size_t pix = (size_t)B * (size_t)N * (size_t)N;
+  const size_t HD = (size_t)H * (size_t)D;
+  // q, k, v, o, g of `rows` attention rows (HD per pixel each; V^T rows padded to N rounded up to 32) + the full bias (H fp32
+  // per pixel), 256-byte aligned regions
+  const size_t r1 = ((size_t)B * rows * fpf::cdiv(N, 32) * 32 * HD * elt + 255) & ~(size_t)255;
+  const size_t r2 = (pix * (size_t)H * 4 + 255) & ~(size_t)255;
+  return 5 * r1 + r2;
+}
+
+extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->z || !a->w_b || !a->bias) return fail(err, errlen, FPF_E_ARGS, "z / w_b / bias is NULL");
+  if (a->B <= 0 || a->N <= 0) return a->B == 0 || a->N == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "negative extent");
+  if (a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_DTYPE, "the bias pass serves the bf16 block");
+  const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
+  if (rc) return rc;
+  // the prologue kernel with only its bias output; the q|k|v|g weights are not read (the weight staging still needs a pointer)
+  return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg ? a->w_qkvg : a->w_b, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending,
+                         nullptr, nullptr, nullptr, 0, nullptr, a->bias, static_cast<hipStream_t>(stream), err, errlen, PRO_BIAS);
+}
+
 extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen) {
   using namespace fpf;
   FPF_CHECK_VERSION(a);
@@ -958,37 +1019,43 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   if (a->B <= 0 || a->N <= 0) return a->B == 0 || a->N == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "negative extent");
   if (a->residual && a->out != a->z) return fail(err, errlen, FPF_E_ARGS, "residual form updates z in place: out must be z");
   if (a->mask && !(a->mask_dtype == FPF_DT_U8 || a->mask_dtype == FPF_DT_F32)) return fail(err, errlen, FPF_E_DTYPE, "mask_dtype %d", a->mask_dtype);
-  const size_t need = fpf_triattn_block_workspace_bytes(a->B, a->N, a->C, a->H, a->D, a->dtype);
+  const int64_t B = a->B, N = a->N, H = a->H, D = a->D, HD = H * D;
+  const int64_t R = a->rows > 0 ? a->rows : N, row0 = a->row0;
+  if (row0 < 0 || row0 + R > N) return fail(err, errlen, FPF_E_SHAPE, "rows [%lld, %lld) outside [0, %lld)", (long long)row0, (long long)(row0 + R), (long long)N);
+  const bool ranged = R < N;
+  if (ranged && a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_SHAPE, "the fp32 block serves whole tensors (no row range)");
+  if (ranged && !a->bias_in) return fail(err, errlen, FPF_E_ARGS, "a row range needs bias_in (the full bias from fpf_triattn_bias_fwd)");
+  if (a->bias_in && a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_DTYPE, "bias_in serves the bf16 block");
+  const size_t need = fpf_triattn_block_workspace_bytes(B, N, R, a->C, a->H, a->D, a->dtype);
   if (!a->workspace || a->workspace_bytes < need) return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
   {
     const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
     if (rc) return rc;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t B = a->B, N = a->N, H = a->H, D = a->D, HD = H * D;
   const size_t elt = a->dtype == FPF_DT_F32 ? 4 : 2;
   const int64_t Jp = cdiv(N, 32) * 32;
-  const size_t r1 = ((size_t)B * N * Jp * HD * elt + 255) & ~(size_t)255;
+  const size_t r1 = ((size_t)B * R * Jp * HD * elt + 255) & ~(size_t)255;
   char* w = static_cast<char*>(a->workspace);
   void *q = w, *k = w + r1, *v = w + 2 * r1, *o = w + 3 * r1, *g = w + 4 * r1;
-  float* bias = reinterpret_cast<float*>(w + 5 * r1);
+  float* bias = a->bias_in ? const_cast<float*>(a->bias_in) : reinterpret_cast<float*>(w + 5 * r1);
   const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)D);
   FpfTriattnArgs c{};
   c.abi_version = FPF_ABI_VERSION;
   c.dtype = a->dtype;
   c.B = B;
-  c.N = N;
+  c.N = R;                                       // the attention rows of this call
   c.H = H;
   c.S = N;
   c.D = D;
   c.q = q;
   c.k = k;
   c.v = v;
-  const int64_t st5[5] = {N * H * N * D, H * N * D, N * D, D, 1};
+  const int64_t st5[5] = {R * H * N * D, H * N * D, N * D, D, 1};
   for (int t = 0; t < 5; ++t) c.q_stride[t] = c.k_stride[t] = c.v_stride[t] = c.out_stride[t] = st5[t];
-  if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, I, H, D, Jp]
+  if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, R, H, D, Jp]
     c.v_layout = 1;
-    c.v_stride[0] = N * H * D * Jp;
+    c.v_stride[0] = R * H * D * Jp;
     c.v_stride[1] = H * D * Jp;
     c.v_stride[2] = D * Jp;
     c.v_stride[3] = Jp;
@@ -1000,24 +1067,26 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.bias_stride[1] = N * N;
   c.bias_stride[2] = N;
   c.bias_stride[3] = 1;
-  c.mask = a->mask;
+  // key mask of attention row i: z-frame pair mask row i (starting) / column i (ending), rows from row0
   c.mask_dtype = a->mask_dtype;
-  c.mask_stride[0] = N * N;                      // key mask of attention row i: z-frame pair mask row i (starting) / column i (ending)
+  c.mask_stride[0] = N * N;
   c.mask_stride[1] = a->ending ? 1 : N;
   c.mask_stride[2] = a->ending ? N : 1;
+  c.mask = a->mask ? static_cast<const char*>(a->mask) + row0 * c.mask_stride[1] * (a->mask_dtype == FPF_DT_F32 ? 4 : 1) : nullptr;
   c.out = o;
   c.scale = scale;
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
+  const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS);
   int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
-                           bias, st, err, errlen, fused_gate ? 0 : 1);
+                           bias, st, err, errlen, flags, row0, R);
   if (rc) return rc;
   rc = core_launch(&c, st, err, errlen);
   if (rc) return rc;
   if (fused_gate) {
     if (!aligned16(a->out)) return fail(err, errlen, FPF_E_ALIGN, "out must be 16-byte aligned");
-    const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
+    const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * R * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_epilogue_gate_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w, a->ln_b,
-                       a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, (uint16_t*)a->out, N, B, a->ending,
+                       a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, (uint16_t*)a->out, N, B, row0, R, a->ending,
                        a->residual);
     return launched(err, errlen, "triattn_epilogue_gate_bf16");
   }

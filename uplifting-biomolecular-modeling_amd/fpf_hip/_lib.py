@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 DT_BF16, DT_F32, DT_U8 = 1, 2, 3
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
 
@@ -45,7 +45,13 @@ class TriattnArgs(C.Structure):
 class TriattnBlockArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp),
                 ("mask", vp), ("mask_dtype", i32), ("ln_w", vp), ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("w_o", vp),
-                ("ending", i32), ("residual", i32), ("out", vp), ("scale", f32), ("workspace", vp), ("workspace_bytes", sz)]
+                ("ending", i32), ("residual", i32), ("out", vp), ("scale", f32), ("workspace", vp), ("workspace_bytes", sz),
+                ("row0", i64), ("rows", i64), ("bias_in", vp)]
+
+
+class TriattnBiasArgs(C.Structure):
+    _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp), ("ln_w", vp),
+                ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("ending", i32), ("bias", vp)]
 
 
 class TriattnPrologueArgs(C.Structure):
@@ -67,7 +73,8 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_trimul_workspace_bytes": ([i64, i64, i32, i32, i32], sz),
     "fpf_trimul_fwd": ([C.POINTER(TrimulArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_fwd": ([C.POINTER(TriattnArgs), vp, C.c_char_p, sz], C.c_int),
-    "fpf_triattn_block_workspace_bytes": ([i64, i64, i32, i32, i32, i32], sz),
+    "fpf_triattn_block_workspace_bytes": ([i64, i64, i64, i32, i32, i32, i32], sz),
+    "fpf_triattn_bias_fwd": ([C.POINTER(TriattnBiasArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_fwd": ([C.POINTER(TriattnBlockArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_prologue_fwd": ([C.POINTER(TriattnPrologueArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_epilogue_fwd": ([C.POINTER(TriattnEpilogueArgs), vp, C.c_char_p, sz], C.c_int),

@@ -214,7 +214,7 @@ def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None,
     m, mdt = _pair_mask(mask, z4)
     wqkvg, wb, wo = _wpack(W, z.dtype, z.device)
     dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
-    need = L.lib().fpf_triattn_block_workspace_bytes(B, N, W.C, W.H, W.D, dt)
+    need = L.lib().fpf_triattn_block_workspace_bytes(B, N, 0, W.C, W.H, W.D, dt)
     wkey = str(z.device)
     ws = W._ws.get(wkey)
     if ws is None or ws.numel() < need:
@@ -228,6 +228,57 @@ def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None,
         L.call("fpf_triattn_block_fwd", a, L.stream_ptr(z.device))
     except L.LibError as e:
         raise Unsupported("lib:" + e.kind, e.msg) from None
+    if residual:
+        return z
+    return out if z.dim() == 4 else out[0]
+
+
+def tri_attn_block_chunked(z, W, mask=None, *, ending=False, residual=False, chunk=256, scale=None, word="big", **_unused):
+    """The row-chunked (`big`) triangle-attention block, after common/opt_core/opt_core/mem/chunk.py:424
+    (triangle_attention_chunked): pass 1 computes the full bias [B, H, N, N] from every pixel (one launch of
+    ``fpf_triattn_bias_fwd``); pass 2 runs prologue -> core -> gate-fused epilogue on ``chunk`` attention rows at a time (z rows
+    for the starting node, z columns for the ending node), so the q / k / v / o workspace holds one chunk.  In place
+    (``residual=True``) the update of a chunk only touches its own rows / columns, which no later chunk reads, and every row's
+    arithmetic is independent of the others: the result is bitwise the whole-tensor block's.  fp32 operands run the whole
+    block (the reference's fp32 passthrough)."""
+    z4, sel = _block_check(z, W, word, "tri_attn_block_chunked")
+    if sel.row != F.ROW_FAST:
+        return tri_attn_block(z, W, mask, ending=ending, residual=residual, scale=scale, word=word)
+    chunk = int(chunk)
+    if chunk <= 0:
+        raise Unsupported("chunk:%d" % chunk)
+    B, N = int(z4.shape[0]), int(z4.shape[1])
+    m, mdt = _pair_mask(mask, z4)
+    wqkvg, wb, wo = _wpack(W, z.dtype, z.device)
+    rows = min(chunk, N)
+    lib = L.lib()
+    need = lib.fpf_triattn_block_workspace_bytes(B, N, rows, W.C, W.H, W.D, L.DT_BF16)
+    key = (str(z.device), "chunked")
+    ws = W._ws.get(key)
+    if ws is None or ws.numel() < need:
+        ws = W._ws[key] = torch.empty(need, dtype=torch.uint8, device=z.device)
+    bkey = (str(z.device), "bias")
+    bias = W._ws.get(bkey)
+    if bias is None or bias.numel() < B * W.H * N * N:
+        bias = W._ws[bkey] = torch.empty(B * W.H * N * N, dtype=torch.float32, device=z.device)
+    stream = L.stream_ptr(z.device)
+    ab = L.TriattnBiasArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), ln_w=L.ptr(W.ln_w),
+                           ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), ending=1 if ending else 0, bias=L.ptr(bias))
+    try:
+        L.call("fpf_triattn_bias_fwd", ab, stream)
+    except L.LibError as e:
+        raise Unsupported("lib:" + e.kind, e.msg) from None
+    out = z4 if residual else torch.empty_like(z4)
+    for r0 in range(0, N, rows):
+        a = L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m),
+                               mask_dtype=mdt, ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb),
+                               w_o=L.ptr(wo), ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out),
+                               scale=float(scale or 0.0), workspace=L.ptr(ws), workspace_bytes=ws.numel(), row0=r0, rows=min(rows, N - r0),
+                               bias_in=L.ptr(bias))
+        try:
+            L.call("fpf_triattn_block_fwd", a, stream)
+        except L.LibError as e:
+            raise Unsupported("lib:" + e.kind, e.msg) from None
     if residual:
         return z
     return out if z.dim() == 4 else out[0]
