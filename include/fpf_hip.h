@@ -135,8 +135,10 @@ typedef struct {
   const void* v;
   int64_t q_stride[5];     /* [B, N, H, S, D] element strides; stride[4] must be 1 */
   int64_t k_stride[5];
-  int64_t v_stride[5];     /* v_layout 0: strides of [B, N, H, S, D]; v_layout 1: strides of [B, N, H, D, S] (V stored transposed) */
-  int32_t v_layout;        /* 0 | 1 (bf16 only); the last stride must be 1 */
+  int64_t v_stride[5];     /* v_layout 0: strides of [B, N, H, S, D]; v_layout 1 / 2: strides of [B, N, H, D, S] (V stored transposed) */
+  int32_t v_layout;        /* 0 | 1 | 2 (1, 2 bf16 only); the last stride must be 1.  2 is the fused block's internal layout: V^T
+                              with the keys of every 16-key block stored in the order 0-3, 8-11, 4-7, 12-15, q already multiplied
+                              by the scale (scale must be 1), fp32 bias with 16-byte aligned rows, S a multiple of 64 up to 8192 */
   const void* bias;        /* [B, H, S, S] (the [B,1,H,S,S] operand without its unit axis) */
   int32_t bias_dtype;      /* FPF_DT_F32 | FPF_DT_BF16 */
   int64_t bias_stride[4];  /* stride[3] must be 1 */

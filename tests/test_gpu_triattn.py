@@ -137,7 +137,7 @@ def _pack(P, dtype):
 
 
 @pytest.mark.parametrize("ending", [False, True])
-@pytest.mark.parametrize("N,pad", [(64, 0), (96, 10), (37, 3)])
+@pytest.mark.parametrize("N,pad", [(64, 0), (96, 10), (37, 3), (128, 10), (192, 70)])
 def test_block_bf16(ending, N, pad):
     from fpf_hip.attn import pair_fused as PF
     P = _block_weights(torch.bfloat16)

@@ -21,6 +21,7 @@ constexpr int TA_R = 3;          // pair rows per workgroup sharing the bias til
 constexpr int TA_KT = 64;        // keys per staged tile (two MFMA sub-tiles of 32)
 constexpr int TA_KLD = 40;       // LDS pitch (bf16) of a K row: 80 B, conflict-free 16-byte reads
 constexpr int TA_VLD = 68;       // LDS pitch (bf16) of a V^T row: 136 B, conflict-free 8-byte reads
+constexpr int TA_MAXW = 128;     // block-layout core: keep-bit words per row held in LDS (S <= 8192)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float TA_HEADROOM = 8.0f;   // log2 units the running max may lag the true one before O and l are rescaled
 static_assert(TA_R <= 4, "one wave computes the keep bits of one staged row");
@@ -322,6 +323,278 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------- bf16 core, block layout
+// The fused block's core: same work split and arithmetic as triattn_core_bf16, for the operands the block's prologue lays out
+// (q pre-multiplied by the scale, V^T with the keys of each 16-key block stored {0-3, 8-11 | 4-7, 12-15}, fp32 bias, S a
+// multiple of 64).  What differs is how operands arrive:
+//   * K and V^T tiles go global -> LDS by DMA (global_load_lds_dwordx4), double-buffered, in XOR-swizzled 16-byte chunks so
+//     the MFMA fragment reads are conflict-free 16-byte reads (K: chunk c of key k at c ^ ((k >> 2) & 3); V^T: chunk c of
+//     row d at c ^ ((d >> 1) & 7)); the permuted key order makes a lane's V^T fragment one 16-byte chunk;
+//   * the bias sub-tiles and the DMA are issued from inline assembly and waited for with explicit counts, one key tile
+//     ahead: the memory counter retires in order, and with every load in the loop issued unconditionally the counts are
+//     exact, so no wait covers a load that is not needed yet;
+//   * the keep bits of all keys of the R rows are built once (LDS table), so the key loop reads no mask.
+constexpr float TD_PS_MAX = 18446744073709551616.0f;   // 2^64: a sub-tile's partial row sum at or above it moves the max
+constexpr float TD_HEADROOM = 60.0f;                     // log2 units a logit may exceed the reference max before it moves
+
+__device__ __forceinline__ f32x4 gload4_async(const float* p) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+  return v;
+}
+// waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
+// through the statement so nothing reads them earlier
+template <int N>
+__device__ __forceinline__ void vm_wait4(f32x4& a, f32x4& b, f32x4& c, f32x4& d) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_dma(const CoreParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[2][TA_R][TA_KT * TA_D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[2][TA_R][TA_D * TA_KT];
+  __shared__ uint64_t sKeepAll[TA_R][TA_MAXW];
+  __shared__ int sAlive[TA_R];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t nq = cdiv(p.S, 128), nr = cdiv(p.N, TA_R);
+  const int64_t total = p.B * p.H * nr * nq;
+  const int64_t per = (total + 7) / 8;
+  const int64_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (w >= total) return;
+  const int64_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
+  const int64_t b = bh / p.H, h = bh % p.H;
+  const int64_t i0 = rg * TA_R;
+  const int64_t q = qt * 128 + wave * 32 + n;
+  const bool qlive = q < p.S;
+  const float c2 = LOG2E;                               // q carries the scale: the accumulator is in natural-log units
+
+  bf16x8 qf[TA_R][2];
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    const bool ok = i < p.N && qlive;
+    const uint16_t* qp = p.q + b * p.qs[0] + (ok ? i : 0) * p.qs[1] + h * p.qs[2] + (ok ? q : 0) * p.qs[3] + 8 * g;
+    qf[r][0] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0, 0, 0, 0});
+    qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
+  }
+  // the Q loads complete here: inside the key loop the only vector-memory operations are the counted ones below
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
+
+  // keep table (8 mask loads in flight per wave); a row with no kept key attends uniformly to every key
+  const int64_t nw = p.S >> 6, npair = TA_R * nw;
+  auto build = [&](auto elt) {
+    using T = decltype(elt);
+    for (int64_t base = wave; base < npair; base += 32) {
+      T raw[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t pr = base + 4 * u < npair ? base + 4 * u : base;
+        const int64_t r = pr / nw, c = pr % nw, i = i0 + r < p.N ? i0 + r : p.N - 1;
+        raw[u] = p.mask ? static_cast<const T*>(p.mask)[b * p.ms[0] + i * p.ms[1] + (c * 64 + l) * p.ms[2]] : (T)1;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t pr = base + 4 * u;
+        const int64_t r = pr < npair ? pr / nw : 0, c = pr < npair ? pr % nw : 0;
+        const uint64_t bal = __ballot(pr < npair && i0 + r < p.N && raw[u] != (T)0);
+        if (pr < npair && l == 0) sKeepAll[r][c] = bal;
+      }
+    }
+  };
+  if (p.mask_f32) build(0.0f);
+  else build((uint8_t)0);
+  __syncthreads();
+  if (tid < TA_R) {
+    uint64_t any = 0;
+    for (int64_t c = 0; c < nw; ++c) any |= sKeepAll[tid][c];
+    sAlive[tid] = any != 0;
+  }
+  __syncthreads();
+  for (int64_t x = tid; x < npair; x += 256) {
+    const int64_t r = x / nw;
+    if (i0 + r < p.N && !sAlive[r]) sKeepAll[r][x % nw] = ~0ull;
+  }
+  __syncthreads();
+  bool dead[TA_R];
+  bool dead_any = false;
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    dead[r] = (i0 + r < p.N) && !sAlive[r];
+    dead_any |= dead[r];
+  }
+
+  // DMA: wave w moves chunk block w (1 KB) of each row's K tile (keys 16w .. 16w + 15) and V^T tile (rows 8w .. 8w + 7);
+  // rows past N read row i0 (never stored)
+  const uint16_t* kb[TA_R];
+  const uint16_t* vb[TA_R];
+  {
+    const int kk = 16 * wave + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
+    const int vd = 8 * wave + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      const int64_t ii = i0 + r < p.N ? i0 + r : i0;
+      kb[r] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2] + kk * p.ks[3] + 8 * kc;
+      vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2] + vd * p.vs[3] + 8 * vc;
+    }
+  }
+  auto dma_tile = [&](int64_t k0, int buf) {
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      lds_dma16(kb[r] + k0 * p.ks[3], lds_addr(&sK[buf][r][512 * wave]));
+      lds_dma16(vb[r] + k0, lds_addr(&sV[buf][r][512 * wave]));
+    }
+  };
+  constexpr int DMA_OPS = 2 * TA_R;                     // vector-memory operations per dma_tile per wave
+
+  const int64_t bias_row = b * p.bs[0] + h * p.bs[1] + (qlive ? q : 0) * p.bs[2];
+  const float* bp0 = static_cast<const float*>(p.bias) + bias_row + 4 * g;
+  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator)
+  auto bias_issue = [&](int64_t kb, f32x4 (&dst)[4]) {
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) dst[qd] = gload4_async(bp0 + kb + 8 * qd);
+  };
+
+  f32x16 o[TA_R];
+  float lrow[TA_R], mb[TA_R], thr[TA_R];
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    o[r] = f32x16{};
+    lrow[r] = 0.f;
+    mb[r] = 0.f;
+    thr[r] = -INFINITY;
+  }
+  // fragment offsets (bf16 elements) inside a row's K / V^T tile
+  const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile adds 32 keys
+  const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
+  const int vsw = (n >> 1) & 7;
+
+  f32x4 bq[2][4];
+  dma_tile(0, 0);
+  bias_issue(0, bq[0]);
+  bias_issue(32, bq[1]);
+  int buf = 0;
+  for (int64_t k0 = 0; k0 < p.S; k0 += TA_KT) {
+    const bool more = k0 + TA_KT < p.S;
+    vm_wait<8>();                                       // this tile's DMA (the two bias sub-tiles after it may be pending)
+    __builtin_amdgcn_s_barrier();                       // every wave's part of the tile is in; the other buffer is free
+    dma_tile(more ? k0 + TA_KT : k0, buf ^ 1);          // the last tile re-reads itself: the wait counts stay exact
+    uint64_t kw[TA_R], kall = ~0ull, kany = 0;
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      kw[r] = sKeepAll[r][k0 >> 6];
+      kall &= kw[r];
+      kany |= kw[r];
+    }
+    const bool full = (kall == ~0ull) && !dead_any;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      vm_wait4<DMA_OPS + 4>(bq[sub][0], bq[sub][1], bq[sub][2], bq[sub][3]);
+      f32x16 bc;
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bq[sub][qd][e];
+      const bool live_sub = (uint32_t)(kany >> (32 * sub)) != 0;
+      f32x16 s[TA_R];
+      if (live_sub) {
+#pragma unroll
+        for (int r = 0; r < TA_R; ++r) {
+          const uint16_t* kt = &sK[buf][r][32 * sub * TA_D];
+          s[r] = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(kt + kfo0)), qf[r][0], bc);
+          s[r] = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(kt + kfo1)), qf[r][1], s[r]);
+        }
+      }
+      bias_issue(more ? k0 + TA_KT + 32 * sub : 32 * sub, bq[sub]);
+      if (!live_sub) continue;
+      if (!full) {
+#pragma unroll
+        for (int r = 0; r < TA_R; ++r) {
+          const uint32_t kbits = (uint32_t)(kw[r] >> (32 * sub));
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float sv = dead[r] ? 0.f : s[r][v];
+            s[r][v] = ((kbits >> c_row(v, g)) & 1u) ? sv : -INFINITY;
+          }
+        }
+      }
+      // p = exp2(logit - mb) straight away; the row's running max is only looked at on the row's first live sub-tile and
+      // when this sub-tile's partial sum leaves [0, 2^64) -- a logit more than ~60 (log2 units) above mb.  Every value is
+      // relative to mb, so a stale mb costs no precision; fp32 / bf16 hold p up to 2^64 with room to spare.
+      uint32_t pk[TA_R][8];
+      float ps[TA_R];
+      auto expsum = [&](int r) {
+        float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          pk[r][v >> 1] = pack2(fast_exp2(s[r][v]), fast_exp2(s[r][v + 1]));
+          if (v & 2) ps1 = dot2_bf16(pk[r][v >> 1], ps1);     // the sum of the bf16 P the PV MFMA consumes
+          else ps0 = dot2_bf16(pk[r][v >> 1], ps0);
+        }
+        ps[r] = ps0 + ps1;
+      };
+      bool bad = false;
+#pragma unroll
+      for (int r = 0; r < TA_R; ++r) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[r][v] = fmaf(s[r][v], c2, -mb[r]);
+        expsum(r);
+        bad |= thr[r] == -INFINITY || !(ps[r] < TD_PS_MAX);
+      }
+      if (__ballot(bad) != 0) {        // move the reference max of the queries that need it (per lane; others unchanged)
+#pragma unroll
+        for (int r = 0; r < TA_R; ++r) {
+          float m0 = s[r][0];
+#pragma unroll
+          for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, s[r][v]);
+          const float mt = half_max(m0);
+          const bool mv = mt > thr[r];
+          const float shift = mv ? mt : 0.f;
+          const float alpha = (mv && thr[r] != -INFINITY) ? fast_exp2(-mt) : 1.0f;
+          lrow[r] *= alpha;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) s[r][v] -= shift;
+          mb[r] += shift;
+          thr[r] = mv ? TD_HEADROOM : thr[r];
+          expsum(r);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < TA_R; ++r) {
+        lrow[r] += ps[r];
+        const uint16_t* vt = &sV[buf][r][n * TA_KT];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const int ch = (4 * sub + 2 * st + g) ^ vsw;
+          o[r] = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(vt + 8 * ch)),
+                        as_bf8(u32x4{pk[r][4 * st], pk[r][4 * st + 1], pk[r][4 * st + 2], pk[r][4 * st + 3]}), o[r]);
+        }
+      }
+    }
+    buf ^= 1;
+  }
+  vm_wait<0>();                                         // no DMA may land after the wave ends
+  if (!qlive) return;
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    if (i >= p.N) continue;
+    const float lt = half_sum(lrow[r]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int d0 = 8 * qd + 4 * g;
+      *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------- fp32 core
 struct CoreParamsF {
   const float* q;
@@ -449,7 +722,7 @@ constexpr int TP_C = 128, TP_HD = 128;
 // Outputs are selected by flags (PRO_QKV: q, k, v^T; PRO_G: g; PRO_BIAS: the full bias) and cover the attention rows
 // [row0, row0 + rows): q / k / v^T / g are indexed by the row within that range, the bias by the absolute row.  The `big`
 // chunked driver runs a bias-only pass over every row, then q / k / v^T per row chunk.
-enum { PRO_QKV = 1, PRO_G = 2, PRO_BIAS = 4 };
+enum { PRO_QKV = 1, PRO_G = 2, PRO_BIAS = 4, PRO_VPERM = 8 };  // VPERM: V^T keys in the core's 16-block order
 struct ProParams {
   const uint16_t* z;
   const float* ln_w;
@@ -465,6 +738,7 @@ struct ProParams {
   float* bias;
   int64_t N, Jp, B, row0, rows;
   int ending, flags;
+  float q_scale;                 // q is stored times this (the fused block folds the attention scale into q)
 };
 
 __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
@@ -502,13 +776,19 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
         // puts d on the lanes and 16 pixels in the registers; the lane exchange then gives each lane 8 consecutive pixels
         const f32x16 acc = rt_gemm32_xw(sW, blk * 32, n, g, xb);
         u32x4 lo, hi;
-        rt_pack16(acc, lo, hi);
+        if (p.flags & PRO_VPERM) {                        // keys of each 16-block as {0-3, 8-11 | 4-7, 12-15}: the lane's
+          lo = u32x4{pack2(acc[0], acc[1]), pack2(acc[2], acc[3]), pack2(acc[4], acc[5]), pack2(acc[6], acc[7])};   // D-layout
+          hi = u32x4{pack2(acc[8], acc[9]), pack2(acc[10], acc[11]), pack2(acc[12], acc[13]), pack2(acc[14], acc[15])};  // rows
+        } else {
+          rt_pack16(acc, lo, hi);
+        }
         uint16_t* dst = p.v + (((b * R + ii) * H + (blk & 3)) * (int64_t)D + n) * Jp + (j - n) + 8 * g;
         *reinterpret_cast<u32x4*>(dst) = lo;               // whole 32-pixel tile: Jp covers it (padding is never read)
         *reinterpret_cast<u32x4*>(dst + 16) = hi;
         continue;
       }
-      const f32x16 acc = rt_gemm32(sW, blk * 32, n, g, xb);
+      f32x16 acc = rt_gemm32(sW, blk * 32, n, g, xb);
+      if (blk < 4 && p.q_scale != 1.0f) acc *= p.q_scale;
       if (blk < 16) {                                     // q | k | g
         u32x4 lo, hi;
         rt_pack16(acc, lo, hi);
@@ -813,7 +1093,7 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     p.S = a->S;
     p.scale = a->scale;
     p.v_t = a->v_layout;
-    if (!(p.v_t == 0 || p.v_t == 1)) return fail(err, errlen, FPF_E_ARGS, "v_layout %d", a->v_layout);
+    if (!(p.v_t == 0 || p.v_t == 1 || p.v_t == 2)) return fail(err, errlen, FPF_E_ARGS, "v_layout %d", a->v_layout);
     for (int t = 0; t < 4; ++t)
       if ((p.qs[t] | p.ks[t] | p.vs[t]) & 7) return fail(err, errlen, FPF_E_ALIGN, "bf16 core: q / k / v strides must be multiples of 8 elements");
     for (int t = 0; t < 4; ++t)
@@ -824,6 +1104,13 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     const int64_t total = a->B * a->H * cdiv(a->N, TA_R) * cdiv(a->S, 128);
     if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
     const dim3 grid((unsigned)(cdiv(total, 8) * 8)), block(256);
+    if (p.v_t == 2) {                  // the block layout (V^T keys permuted in 16-blocks, q times the scale): the DMA-staged core
+      if (!p.bias_vec || p.S % TA_KT != 0 || p.S > 64 * TA_MAXW || p.vs[3] % 8 != 0)
+        return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
+      if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
+      hipLaunchKernelGGL(triattn_core_bf16_dma, grid, block, 0, st, p);
+      return launched(err, errlen, "triattn_core_bf16_dma");
+    }
     if (p.v_t && p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<true, true>), grid, block, 0, st, p);
     else if (p.v_t) hipLaunchKernelGGL((triattn_core_bf16<true, false>), grid, block, 0, st, p);
     else if (p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<false, true>), grid, block, 0, st, p);
@@ -903,7 +1190,7 @@ static int block_shape_check(int dtype, int64_t B, int C, int64_t H, int64_t D, 
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
-                           int64_t rows = -1) {
+                           int64_t rows = -1, float q_scale = 1.0f) {
   if (rows < 0) rows = N;
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || ((flags & PRO_QKV) && (!aligned16(q) || !aligned16(k) || !aligned16(v))) ||
@@ -931,12 +1218,13 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.rows = rows;
     p.ending = ending;
     p.flags = flags;
+    p.q_scale = q_scale;
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
-  if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS))
-    return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output)");
+  if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS) || q_scale != 1.0f)
+    return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output, q unscaled)");
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
                      (const float*)w_b, C, H, D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N, ending);
@@ -1053,8 +1341,10 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.v = v;
   const int64_t st5[5] = {R * H * N * D, H * N * D, N * D, D, 1};
   for (int t = 0; t < 5; ++t) c.q_stride[t] = c.k_stride[t] = c.v_stride[t] = c.out_stride[t] = st5[t];
+  // bf16 with N a multiple of 64 (up to 8192): the DMA-staged core, fed q times the scale and V^T keys in its 16-block order
+  const bool dma_core = a->dtype == FPF_DT_BF16 && N % TA_KT == 0 && N <= 64 * TA_MAXW;
   if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, R, H, D, Jp]
-    c.v_layout = 1;
+    c.v_layout = dma_core ? 2 : 1;
     c.v_stride[0] = R * H * D * Jp;
     c.v_stride[1] = H * D * Jp;
     c.v_stride[2] = D * Jp;
@@ -1074,11 +1364,11 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.mask_stride[2] = a->ending ? N : 1;
   c.mask = a->mask ? static_cast<const char*>(a->mask) + row0 * c.mask_stride[1] * (a->mask_dtype == FPF_DT_F32 ? 4 : 1) : nullptr;
   c.out = o;
-  c.scale = scale;
+  c.scale = dma_core ? 1.0f : scale;
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
-  const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS);
+  const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM : 0);
   int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
-                           bias, st, err, errlen, flags, row0, R);
+                           bias, st, err, errlen, flags, row0, R, dma_core ? scale : 1.0f);
   if (rc) return rc;
   rc = core_launch(&c, st, err, errlen);
   if (rc) return rc;
