@@ -75,6 +75,29 @@ def ln_args(x, y, w, b):
                     x_row_stride=C, y=L.ptr(y), y_row_stride=C, gamma=L.ptr(w), beta=L.ptr(b), eps=1e-5)
 
 
+def core_block_args(N, torch, dev, g):
+    """Argument block of the triangle-attention core exactly as the fused block launches it (v_layout 2: q already times the
+    scale, V^T [B, N, H, D, N] with the keys of each 16-key block in MFMA order, fp32 bias [B, H, N, N], u8 pair mask of ones),
+    with random contents; plus the tensors it points at (kept alive by the caller)."""
+    from fpf_hip import _lib as L
+    H, D = 4, 32
+    q = (torch.randn(1, N, H, N, D, generator=g) / math.sqrt(D)).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, N, H, N, D, generator=g).to(torch.bfloat16).to(dev)
+    vt = torch.randn(1, N, H, D, N, generator=g).to(torch.bfloat16).to(dev)
+    bias = (torch.randn(1, H, N, N, generator=g) * 0.5).to(dev)
+    mask = torch.ones(1, N, N, dtype=torch.uint8, device=dev)
+    out = torch.empty(1, N, H, N, D, dtype=torch.bfloat16, device=dev)
+    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=1, N=N, H=H, S=N, D=D, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vt), v_layout=2,
+                      bias=L.ptr(bias), bias_dtype=L.DT_F32, mask=L.ptr(mask), mask_dtype=L.DT_U8, out=L.ptr(out), scale=1.0)
+    a.q_stride[:] = q.stride()
+    a.k_stride[:] = k.stride()
+    a.v_stride[:] = vt.stride()
+    a.out_stride[:] = out.stride()
+    a.bias_stride[:] = [bias.stride(0), bias.stride(1), bias.stride(2), bias.stride(3)]
+    a.mask_stride[:] = [mask.stride(0), mask.stride(1), mask.stride(2)]
+    return a, (q, k, vt, bias, mask, out)
+
+
 def probe(kind, N, reps):
     """Launch-only runs for hardware-counter passes (rocprofv3 --pmc): `triattn_core` = the core at the block's shape, reps
     times; `copy` = a device copy of a known byte count (the calibration kernel for FETCH_SIZE / WRITE_SIZE)."""
@@ -83,12 +106,11 @@ def probe(kind, N, reps):
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
     if kind == "triattn_core":
-        q, k, v = (torch.randn(1, N, 4, N, 32, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
-        bias = (torch.randn(1, 1, 4, N, N, generator=g) * 0.5).to(dev)
-        kmask = torch.ones(1, N, 1, 1, N, dtype=torch.bool, device=dev)
-        o = torch.empty_like(q)
+        import ctypes
+        from fpf_hip import _lib as L
+        a, keep = core_block_args(N, torch, dev, g)
         for _ in range(reps):
-            TA.triangle_attention(q, k, v, bias, kmask, word="fast", out=o)
+            L.call("fpf_triattn_fwd", a, L.stream_ptr(dev))
     elif kind == "copy":
         x = torch.randn(N * N * 128, generator=g).to(torch.bfloat16).to(dev)
         y = torch.empty_like(x)
@@ -195,21 +217,17 @@ def main():
     breakdown["layernorm"] = {"ms": round(t_ln, 4), "hbm_gbs": round(2 * zbytes / (t_ln * 1e-3) / 1e9, 1),
                               "hbm_frac": round(2 * zbytes / (t_ln * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
-    # dominant kernel: the triangle-attention core at the block's shape (q/k/v [1,N,4,N,32] bf16, bias fp32, mask ones)
-    q, k, v = (torch.randn(1, N, 4, N, 32, generator=g).to(torch.bfloat16).to(dev) for _ in range(3))
-    bias = (torch.randn(1, 1, 4, N, N, generator=g) * 0.5).to(dev)
-    kmask = torch.ones(1, N, 1, 1, N, dtype=torch.bool, device=dev)
-    o = torch.empty_like(q)
-    core = lambda: TA.triangle_attention(q, k, v, bias, kmask, word="fast", out=o)
-    core()
-    t_core = time_events(core, reps, torch)
+    # dominant kernel: the triangle-attention core as the block launches it (q / k / V^T [1,N,4,N,32] bf16, bias fp32, mask
+    # ones), timed through the C ABI with HIP events on the launch stream
+    core_args, keep = core_block_args(N, torch, dev, g)
+    t_core = time_raw("fpf_triattn_fwd", core_args, reps, torch)
     ach = fl["triatt_core"] / (t_core * 1e-3) / 1e12
     traffic = None
     tp = os.path.join(ROOT, "profiles", "traffic_triattn_core_n%d.json" % N)
     if os.path.exists(tp):
         with open(tp) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
-    roof = {"kernel": "triattn_core_bf16", "bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+    roof = {"kernel": "triattn_core_bf16_dma", "bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "ms_per_launch": round(t_core, 4),
             "flops_per_launch": fl["triatt_core"]}
 

@@ -337,10 +337,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 constexpr float TD_PS_MAX = 18446744073709551616.0f;   // 2^64: a sub-tile's partial row sum at or above it moves the max
 constexpr float TD_HEADROOM = 60.0f;                     // log2 units a logit may exceed the reference max before it moves
 
-__device__ __forceinline__ f32x4 gload4_async(const float* p) {
+// 16 bytes at sbase + voff + IMM (scalar base, 32-bit per-lane byte offset) into registers, not waited for here
+template <int IMM>
+__device__ __forceinline__ f32x4 gload4_async(uint32_t voff, const void* sbase) {
   f32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p));
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(v) : "v"(voff), "s"(sbase), "n"(IMM));
   return v;
+}
+// 16 bytes per lane from sbase + voff into LDS at lds_base + 16 * lane (global_load_lds_dwordx4, scalar base)
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "memory");
 }
 // waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
 // through the statement so nothing reads them earlier
@@ -428,34 +434,43 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
   // DMA: wave w moves chunk block w (1 KB) of each row's K tile (keys 16w .. 16w + 15) and V^T tile (rows 8w .. 8w + 7);
-  // rows past N read row i0 (never stored)
+  // rows past N read row i0 (never stored).  Row bases are scalar, the in-tile byte offsets per lane are fixed.
   const uint16_t* kb[TA_R];
   const uint16_t* vb[TA_R];
+  uint32_t koff, voff;
   {
     const int kk = 16 * wave + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
     const int vd = 8 * wave + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+    koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
+    voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
       const int64_t ii = i0 + r < p.N ? i0 + r : i0;
-      kb[r] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2] + kk * p.ks[3] + 8 * kc;
-      vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2] + vd * p.vs[3] + 8 * vc;
+      kb[r] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
+      vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
     }
   }
   auto dma_tile = [&](int64_t k0, int buf) {
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      lds_dma16(kb[r] + k0 * p.ks[3], lds_addr(&sK[buf][r][512 * wave]));
-      lds_dma16(vb[r] + k0, lds_addr(&sV[buf][r][512 * wave]));
+      lds_dma16_s(koff, kb[r] + k0 * p.ks[3], lds_addr(&sK[buf][r][512 * wave]));
+      lds_dma16_s(voff, vb[r] + k0, lds_addr(&sV[buf][r][512 * wave]));
     }
   };
-  constexpr int DMA_OPS = 2 * TA_R;                     // vector-memory operations per dma_tile per wave
+  // The wait counts in the key loop (vm_wait<8>, vm_wait4<DMA_OPS + 4>) assume exactly DMA_OPS operations per dma_tile and
+  // 4 per bias_issue, every one issued unconditionally: a wait that counted fewer operations than were issued after the
+  // load it guards would let that load land in registers already reused.
+  constexpr int DMA_OPS = 2 * TA_R;
 
-  const int64_t bias_row = b * p.bs[0] + h * p.bs[1] + (qlive ? q : 0) * p.bs[2];
-  const float* bp0 = static_cast<const float*>(p.bias) + bias_row + 4 * g;
-  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator)
+  const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
+  const uint32_t boff = (uint32_t)(((qlive ? q : 0) * p.bs[2] + 4 * g) * 4);
+  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
   auto bias_issue = [&](int64_t kb, f32x4 (&dst)[4]) {
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) dst[qd] = gload4_async(bp0 + kb + 8 * qd);
+    const float* sb = brow + kb;
+    dst[0] = gload4_async<0>(boff, sb);
+    dst[1] = gload4_async<32>(boff, sb);
+    dst[2] = gload4_async<64>(boff, sb);
+    dst[3] = gload4_async<96>(boff, sb);
   };
 
   f32x16 o[TA_R];
@@ -485,7 +500,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     uint64_t kw[TA_R], kall = ~0ull, kany = 0;
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      kw[r] = sKeepAll[r][k0 >> 6];
+      const uint64_t wv = sKeepAll[r][k0 >> 6];                         // uniform: keep it in scalar registers
+      const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
+      const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);   // unsigned: no sign extension
+      kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
       kall &= kw[r];
       kany |= kw[r];
     }
@@ -513,11 +531,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       if (!full) {
 #pragma unroll
         for (int r = 0; r < TA_R; ++r) {
-          const uint32_t kbits = (uint32_t)(kw[r] >> (32 * sub));
+          const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const float sv = dead[r] ? 0.f : s[r][v];
-            s[r][v] = ((kbits >> c_row(v, g)) & 1u) ? sv : -INFINITY;
+            s[r][v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? sv : -INFINITY;
           }
         }
       }
