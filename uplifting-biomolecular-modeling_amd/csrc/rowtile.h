@@ -4,7 +4,7 @@
 // 8 waves of a workgroup (2 per SIMD) overlap each other's loads, LayerNorm and MFMA.
 //
 // Operand layout (v_mfma_f32_32x32x16_bf16, lane = 32 * g + n): the normalised rows are the B operand -- lane (n, g) holds
-// pixel n's channels 64g + 8t .. +7 for k-step t -- and the weight rows (W[out][in], LDS pitch RT_LD) are the A operand
+// pixel n's channels 16t + 8g .. +7 for k-step t -- and the weight rows (W[out][in], LDS pitch RT_LD) are the A operand
 // read at the same channel offsets, so D = W x^T comes out with lane (n, g) holding pixel n and the 16 output channels
 // c_row(v, g) of a 32-channel block.
 #pragma once
@@ -16,10 +16,14 @@ constexpr int RT_C = 128;            // channels per pixel row
 constexpr int RT_LD = RT_C + 8;      // LDS pitch (bf16) of a 128-wide weight row: 272 B, conflict-free 16-byte reads
 constexpr int RT_WAVES = 8;          // waves per workgroup
 
+// K-step t of a 128-channel reduction takes channels 16 t .. 16 t + 15: lane (n, g) holds the 8-channel chunk 2 t + g.  The two
+// lanes of a pixel read adjacent chunks, so each 16-byte load instruction touches one 32-byte piece of 32 pixel rows.
+__device__ __forceinline__ constexpr int rt_chunk(int t, int g) { return 2 * t + g; }
+
 // Raw 16-byte loads of one lane's half of a 128-channel bf16 pixel row (zeros when !live).
 __device__ __forceinline__ void rt_load(const uint16_t* __restrict__ row, bool live, int g, u32x4 (&raw)[8]) {
 #pragma unroll
-  for (int t = 0; t < 8; ++t) raw[t] = live ? *reinterpret_cast<const u32x4*>(row + 64 * g + 8 * t) : u32x4{0, 0, 0, 0};
+  for (int t = 0; t < 8; ++t) raw[t] = live ? *reinterpret_cast<const u32x4*>(row + 8 * rt_chunk(t, g)) : u32x4{0, 0, 0, 0};
 }
 
 // LayerNorm over the 128 channels split across lanes n and n + 32 (fp32 statistics, two-pass variance), packed to bf16
@@ -42,7 +46,7 @@ __device__ __forceinline__ void rt_ln(const u32x4 (&raw)[8], int g, const float*
   const float rstd = 1.0f / sqrtf(half_sum(q) * (1.0f / 128.0f) + eps);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const int c0 = 64 * g + 8 * t;
+    const int c0 = 8 * rt_chunk(t, g);
     const f32x4 w0 = *reinterpret_cast<const f32x4*>(gb + c0), w1 = *reinterpret_cast<const f32x4*>(gb + c0 + 4);
     const f32x4 b0 = *reinterpret_cast<const f32x4*>(gb + RT_C + c0), b1 = *reinterpret_cast<const f32x4*>(gb + RT_C + c0 + 4);
     uint32_t o[4];
@@ -72,13 +76,13 @@ __device__ __forceinline__ void rt_stage_weights(uint16_t* __restrict__ s, const
 // D = W[row0 .. row0 + 31] x^T over the 128 channels (8 k-steps), weights from LDS.  The weight fragment of k-step t + 1 is
 // read before the MFMA of k-step t issues, so the LDS latency hides behind the matrix core.
 __device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
-  const uint16_t* r = s + (row0 + n) * RT_LD + 64 * g;
+  const uint16_t* r = s + (row0 + n) * RT_LD + 8 * g;
   f32x16 acc = {};
   bf16x8 w = as_bf8(*reinterpret_cast<const u32x4*>(r));
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     bf16x8 wn = w;
-    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * (t + 1)));
+    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 16 * (t + 1)));
     acc = mfma32(w, xb[t], acc);
     __builtin_amdgcn_sched_barrier(0);   // one k-step of lookahead: bounded register pressure
     w = wn;
@@ -89,13 +93,13 @@ __device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int 
 // The swapped product D = x W[row0 .. row0 + 31]^T (same fragments, operands exchanged): lane (n, g) then holds output
 // channel row0 + n for the 16 pixels c_row(v, g) of the tile.
 __device__ __forceinline__ f32x16 rt_gemm32_xw(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
-  const uint16_t* r = s + (row0 + n) * RT_LD + 64 * g;
+  const uint16_t* r = s + (row0 + n) * RT_LD + 8 * g;
   f32x16 acc = {};
   bf16x8 w = as_bf8(*reinterpret_cast<const u32x4*>(r));
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     bf16x8 wn = w;
-    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * (t + 1)));
+    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 16 * (t + 1)));
     acc = mfma32(xb[t], w, acc);
     __builtin_amdgcn_sched_barrier(0);
     w = wn;
@@ -111,13 +115,13 @@ __device__ __forceinline__ void rt_gemm32_multi(const uint16_t* const (&s)[K], i
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     acc[k] = f32x16{};
-    a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g));
+    a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 8 * g));
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     bf16x8 an[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) an[k] = t < 7 ? as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * (t + 1))) : a[k];
+    for (int k = 0; k < K; ++k) an[k] = t < 7 ? as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 8 * rt_chunk(t + 1, g))) : a[k];
 #pragma unroll
     for (int k = 0; k < K; ++k) acc[k] = mfma32(a[k], xb[t], acc[k]);
     __builtin_amdgcn_sched_barrier(0);
@@ -134,13 +138,13 @@ __device__ __forceinline__ void rt_gemm32_multi_xw(const uint16_t* const (&s)[K]
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     acc[k] = f32x16{};
-    a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g));
+    a[k] = as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 8 * g));
   }
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     bf16x8 an[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) an[k] = t < 7 ? as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 64 * g + 8 * (t + 1))) : a[k];
+    for (int k = 0; k < K; ++k) an[k] = t < 7 ? as_bf8(*reinterpret_cast<const u32x4*>(s[k] + (row0 + n) * RT_LD + 8 * rt_chunk(t + 1, g))) : a[k];
 #pragma unroll
     for (int k = 0; k < K; ++k) acc[k] = mfma32(xb[t], a[k], acc[k]);
     __builtin_amdgcn_sched_barrier(0);

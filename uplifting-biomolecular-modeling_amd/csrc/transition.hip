@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(64 * NW) transition_bf16_kernel(const uint16_t
     }
     const uint16_t* ra = &sWa[buf][n * TR_C];
     const uint16_t* rb = &sWb[buf][n * TR_C];
-    auto wfrag = [&](const uint16_t* r, int t) { return as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * ((8 * g + t) ^ (n & 15)))); };
+    auto wfrag = [&](const uint16_t* r, int t) { return as_bf8(*reinterpret_cast<const u32x4*>(r + 8 * (rt_chunk(t, g) ^ (n & 15)))); };
     bf16x8 fa = wfrag(ra, 0), fb = wfrag(rb, 0);
 #pragma unroll
     for (int t = 0; t < TR_KS; ++t) {

@@ -843,7 +843,7 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
     bf16x8 xb[8];
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt) {
-      const int hd0 = 64 * g + 8 * tt;
+      const int hd0 = 8 * rt_chunk(tt, g);
       const int hh = hd0 / D, d0 = hd0 % D;
       u32x4 ov = {0, 0, 0, 0}, gv = {0, 0, 0, 0};
       if (live) {

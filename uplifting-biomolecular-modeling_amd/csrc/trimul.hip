@@ -340,7 +340,7 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
     rt_wave_lds_sync();
     u32x4 xr[8];
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) xr[tt] = *reinterpret_cast<const u32x4*>(&sx[n * K3_XLD + 64 * g + 8 * tt]);
+    for (int tt = 0; tt < 8; ++tt) xr[tt] = *reinterpret_cast<const u32x4*>(&sx[n * K3_XLD + 8 * rt_chunk(tt, g)]);
     rt_wave_lds_sync();
     bf16x8 xo[8], xi[8];
     rt_ln(xr, g, sLNo, eps, xo);
