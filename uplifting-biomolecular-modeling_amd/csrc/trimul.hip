@@ -1,5 +1,5 @@
 // Triangle multiplication (outgoing / incoming), three launches on the caller's stream:
-//   K1        LN_in(z) -> four gated projections -> mask -> channel-major planes A[c][P][Q], B[c][P][Q] (bf16)
+//   K1        LN_in(z) -> four gated projections -> mask -> channel planes A[c][P][Q], B[c][P][Q] (bf16, tiled: see tl_off)
 //             outgoing: plane (P, Q) = z pixel (P, Q);  incoming: plane (P, Q) = z pixel (Q, P) (the transposed load: a wave's
 //             32 plane columns are 32 z rows of one column, each a contiguous 256-byte pixel row)
 //   contract  X[c][i][j] = sum_k A[c][i][k] B[c][j][k] -- a batched "NT" bf16 MFMA GEMM, fp32 accumulation, bf16 X
@@ -15,6 +15,17 @@ namespace fpf {
 
 constexpr int TM_C = 128;            // c_z = c_h for the bf16 path
 constexpr int TM_TILE = 128;         // contraction tile and plane padding
+
+// Tiled plane layout of the bf16 path: element (b, c, P, Q) of a [B, 128, Np, Np] plane set lives at
+// ((b (Np / 32) + Q / 32) Np + P) 4096 + 32 c + Q % 32 -- for each plane row P and 32-column block, the 128 channels' 32
+// values form one contiguous 8 KB block, and the blocks of one column block follow each other row by row.  K1 writes a
+// 32-pixel tile as whole blocks and K3 reads one as 1 KB-contiguous loads; the contraction reads 64-byte runs of k along
+// rows 8 KB apart (TL_ROW) and steps one column block (TL_KBLK(Np)) per 32-wide k slab.
+constexpr int64_t TL_ROW = 4096;
+__device__ __forceinline__ int64_t tl_kblk(int64_t Np) { return Np * 4096; }
+__device__ __forceinline__ int64_t tl_off(int64_t b, int64_t c, int64_t P, int64_t Q, int64_t Np) {
+  return ((b * (Np >> 5) + (Q >> 5)) * Np + P) * 4096 + c * 32 + (Q & 31);
+}
 
 // ---------------------------------------------------------------------------------------------------------------- K1 (bf16)
 // Persistent: the four [128 x 128] projection weights live in LDS (139 KB) for the workgroup's lifetime; each wave walks
@@ -37,7 +48,6 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
   __syncthreads();
   const int64_t tpr = Np / 32, per_b = Np * tpr, total = B * per_b;
   const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
-  const int64_t plane = Np * Np;
   int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave;
   u32x4 raw[8];
   auto fetch = [&](int64_t tt) {
@@ -69,8 +79,8 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
     }
     rt_wave_lds_sync();
     const int64_t Q0 = Q - n;
-    uint16_t* oa = pa + b * RT_C * plane + P * Np + Q0 + 8 * g;
-    uint16_t* ob = pb + b * RT_C * plane + P * Np + Q0 + 8 * g;
+    uint16_t* oa = pa + tl_off(b, 0, P, Q0, Np) + 8 * g;
+    uint16_t* ob = pb + tl_off(b, 0, P, Q0, Np) + 8 * g;
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
       const uint16_t* const ws[4] = {sW, sW + 1 * RT_C * RT_LD, sW + 2 * RT_C * RT_LD, sW + 3 * RT_C * RT_LD};
@@ -85,11 +95,11 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
       const int64_t c = cb * 32 + n;
       u32x4 lo, hi;
       rt_pack16(va, lo, hi);
-      *reinterpret_cast<u32x4*>(oa + c * plane) = lo;
-      *reinterpret_cast<u32x4*>(oa + c * plane + 16) = hi;
+      *reinterpret_cast<u32x4*>(oa + c * 32) = lo;
+      *reinterpret_cast<u32x4*>(oa + c * 32 + 16) = hi;
       rt_pack16(vb, lo, hi);
-      *reinterpret_cast<u32x4*>(ob + c * plane) = lo;
-      *reinterpret_cast<u32x4*>(ob + c * plane + 16) = hi;
+      *reinterpret_cast<u32x4*>(ob + c * 32) = lo;
+      *reinterpret_cast<u32x4*>(ob + c * 32 + 16) = hi;
     }
   }
 }
@@ -113,9 +123,9 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
   if (w >= total) return;
   const int64_t bc = w / tiles, t = w % tiles;
   const int64_t ti = t / (Np / TM_TILE), tj = t % (Np / TM_TILE);
-  const int64_t plane = Np * Np;
-  const uint16_t* a0 = A + bc * plane + ti * TM_TILE * Np;
-  const uint16_t* b0 = Bm + bc * plane + tj * TM_TILE * Np;
+  const int64_t pb_ = bc / TM_C, pc = bc % TM_C, rstride = TL_ROW, kstride = tl_kblk(Np);   // tiled planes
+  const uint16_t* a0 = A + tl_off(pb_, pc, ti * TM_TILE, 0, Np);
+  const uint16_t* b0 = Bm + tl_off(pb_, pc, tj * TM_TILE, 0, Np);
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;     // the wave's 64 x 64 sub-tile
   f32x16 acc[2][2] = {};
   // global -> register prefetch: 128 rows x 64 k = 1024 16-byte chunks per operand, 4 per thread
@@ -124,8 +134,9 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int i = tid + 256 * it, r = i >> 3, ch = i & 7;
-      ra[it] = *reinterpret_cast<const u32x4*>(a0 + r * Np + k0 + ch * 8);
-      rb[it] = *reinterpret_cast<const u32x4*>(b0 + r * Np + k0 + ch * 8);
+      const int64_t kk = k0 + ch * 8, o = r * rstride + (kk >> 5) * kstride + (kk & 31);
+      ra[it] = *reinterpret_cast<const u32x4*>(a0 + o);
+      rb[it] = *reinterpret_cast<const u32x4*>(b0 + o);
     }
   };
   gload(0);
@@ -154,7 +165,6 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
     }
   }
   // D layout: row i = 8(v/4) + 4g + v%4 of the sub-tile, column j = n
-  uint16_t* x0 = X + bc * plane;
 #pragma unroll
   for (int si = 0; si < 2; ++si)
 #pragma unroll
@@ -163,7 +173,7 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t i = ti * TM_TILE + wr + 32 * si + c_row(v, g);
-        if (i < N && j < N) x0[i * Np + j] = f2bf(acc[si][sj][v]);
+        if (i < N && j < N) X[tl_off(pb_, pc, i, j, Np)] = f2bf(acc[si][sj][v]);
       }
     }
 }
@@ -187,22 +197,22 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   const int64_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;     // each XCD gets a contiguous run: one plane's 9 tiles share its L2
   if (w >= total) return;
   const int64_t bc = w / tiles, t = w % tiles, ti = t / tpd, tj = t % tpd;
-  const int64_t plane = Np * Np;
-  const uint16_t* a0 = A + bc * plane + ti * CB_T * Np;
-  const uint16_t* b0 = Bm + bc * plane + tj * CB_T * Np;
+  const int64_t pb_ = bc / TM_C, pc = bc % TM_C, rstride = TL_ROW, kstride = tl_kblk(Np);   // tiled planes
+  const uint16_t* a0 = A + tl_off(pb_, pc, ti * CB_T, 0, Np);
+  const uint16_t* b0 = Bm + tl_off(pb_, pc, tj * CB_T, 0, Np);
   // slab loads: 1024 16-byte chunks per operand; instruction q of thread tid fills LDS slot s = 256 q + tid (each wave
   // instruction writes 1 KB contiguously); slot s = row s >> 2, position s & 3, holding chunk (s & 3) ^ ((row >> 2) & 3)
   int64_t goff[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int sl = 256 * q + tid, r = sl >> 2, c = (sl & 3) ^ ((r >> 2) & 3);
-    goff[q] = (int64_t)r * Np + 8 * c;
+    goff[q] = (int64_t)r * rstride + 8 * c;
   }
-  auto issue = [&](int buf, int64_t k0) {
+  auto issue = [&](int buf, int64_t k0) {              // k0 is a multiple of 32: one column block per slab
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      lds_dma16(a0 + goff[q] + k0, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
-      lds_dma16(b0 + goff[q] + k0, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16(a0 + goff[q] + (k0 >> 5) * kstride, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16(b0 + goff[q] + (k0 >> 5) * kstride, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
     }
   };
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
@@ -270,14 +280,13 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
         fb[ks][s4] = nb[ks][s4];
       }
   }
-  uint16_t* x0 = X + bc * plane;
 #pragma unroll
   for (int si = 0; si < 4; ++si)
 #pragma unroll
     for (int sj = 0; sj < 4; ++sj) {
       u32x4 lo, hi;
       rt_pack16(acc[si][sj], lo, hi);
-      uint16_t* xp = x0 + (ti * CB_T + wr + 32 * si + n) * Np + tj * CB_T + wc + 32 * sj + 8 * g;
+      uint16_t* xp = X + tl_off(pb_, pc, ti * CB_T + wr + 32 * si + n, tj * CB_T + wc + 32 * sj, Np) + 8 * g;
       *reinterpret_cast<u32x4*>(xp) = lo;
       *reinterpret_cast<u32x4*>(xp + 16) = hi;
       __builtin_amdgcn_sched_barrier(0);                 // one accumulator at a time (bounded VGPR use)
@@ -308,18 +317,14 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
   __syncthreads();
   const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
   const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
-  const int64_t plane = Np * Np;
   uint16_t* sx = sX[wave];
   int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave;
   u32x4 rx[8], rz[8];
   auto fetch = [&](int64_t tt) {
     const int64_t b = tt / per_b, i = (tt % per_b) / tpr, j0 = (tt % tpr) * 32, j = j0 + n;
-    const uint16_t* xs = X + b * RT_C * plane + i * Np + j0;      // X rows are padded to Np: the 32 columns are in bounds
+    const uint16_t* xs = X + tl_off(b, 0, i, j0, Np);      // the tile's 8 KB block (rows padded to Np: in bounds)
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int q = l + 64 * it, c = q >> 2, ch = q & 3;
-      rx[it] = *reinterpret_cast<const u32x4*>(xs + (int64_t)c * plane + ch * 8);
-    }
+    for (int it = 0; it < 8; ++it) rx[it] = *reinterpret_cast<const u32x4*>(xs + 8 * (l + 64 * it));   // channel q >> 2, chunk q & 3
     const bool live = j < N;
     rt_load(zin + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
   };
