@@ -76,9 +76,9 @@ def ln_args(x, y, w, b):
 
 
 def core_block_args(N, torch, dev, g):
-    """Argument block of the triangle-attention core exactly as the fused block launches it (v_layout 2: q already times the
-    scale, V^T [B, N, H, D, N] with the keys of each 16-key block in MFMA order, fp32 bias [B, H, N, N], u8 pair mask of ones),
-    with random contents; plus the tensors it points at (kept alive by the caller)."""
+    """Argument block of the triangle-attention core exactly as the fused block launches it (v_layout 2: q already times
+    scale * log2(e), V^T [B, N, H, D, N] with the keys of each 16-key block in MFMA order, fp32 bias [B, H, N, N] in log2 units,
+    u8 pair mask of ones), with random contents; plus the tensors it points at (kept alive by the caller)."""
     from fpf_hip import _lib as L
     H, D = 4, 32
     q = (torch.randn(1, N, H, N, D, generator=g) / math.sqrt(D)).to(torch.bfloat16).to(dev)

@@ -138,7 +138,8 @@ typedef struct {
   int64_t v_stride[5];     /* v_layout 0: strides of [B, N, H, S, D]; v_layout 1 / 2: strides of [B, N, H, D, S] (V stored transposed) */
   int32_t v_layout;        /* 0 | 1 | 2 (1, 2 bf16 only); the last stride must be 1.  2 is the fused block's internal layout: V^T
                               with the keys of every 16-key block stored in the order 0-3, 8-11, 4-7, 12-15, q already multiplied
-                              by the scale (scale must be 1), fp32 bias with 16-byte aligned rows, S a multiple of 64 up to 8192 */
+                              by scale * log2(e) (scale must be 1), fp32 bias times log2(e) with 16-byte aligned rows (logits in
+                              log2 units), S a multiple of 64 up to 8192 */
   const void* bias;        /* [B, H, S, S] (the [B,1,H,S,S] operand without its unit axis) */
   int32_t bias_dtype;      /* FPF_DT_F32 | FPF_DT_BF16 */
   int64_t bias_stride[4];  /* stride[3] must be 1 */
@@ -200,7 +201,8 @@ typedef struct {
   const void* w_qkvg;      /* may be NULL (not read) */
   const void* w_b;         /* [H, C] */
   int32_t ending;
-  float* bias;             /* [B, H, N, N] fp32 out */
+  float* bias;             /* [B, H, N, N] fp32 out, in the units fpf_triattn_block_fwd's core takes: times log2(e) when N is
+                              a multiple of 64 up to 8192 (the v_layout 2 core), else as is */
 } FpfTriattnBiasArgs;
 int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen);
 

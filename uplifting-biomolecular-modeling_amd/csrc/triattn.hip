@@ -324,18 +324,28 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 }
 
 // ---------------------------------------------------------------------------------------------------------------- bf16 core, block layout
-// The fused block's core: same work split and arithmetic as triattn_core_bf16, for the operands the block's prologue lays out
-// (q pre-multiplied by the scale, V^T with the keys of each 16-key block stored {0-3, 8-11 | 4-7, 12-15}, fp32 bias, S a
-// multiple of 64).  What differs is how operands arrive:
-//   * K and V^T tiles go global -> LDS by DMA (global_load_lds_dwordx4), double-buffered, in XOR-swizzled 16-byte chunks so
-//     the MFMA fragment reads are conflict-free 16-byte reads (K: chunk c of key k at c ^ ((k >> 2) & 3); V^T: chunk c of
-//     row d at c ^ ((d >> 1) & 7)); the permuted key order makes a lane's V^T fragment one 16-byte chunk;
-//   * the bias sub-tiles and the DMA are issued from inline assembly and waited for with explicit counts, one key tile
-//     ahead: the memory counter retires in order, and with every load in the loop issued unconditionally the counts are
-//     exact, so no wait covers a load that is not needed yet;
-//   * the keep bits of all keys of the R rows are built once (LDS table), so the key loop reads no mask.
-constexpr float TD_PS_MAX = 18446744073709551616.0f;   // 2^64: a sub-tile's partial row sum at or above it moves the max
-constexpr float TD_HEADROOM = 60.0f;                     // log2 units a logit may exceed the reference max before it moves
+// The fused block's core: the work split of triattn_core_bf16 (a workgroup = TA_R pair rows x 128 queries of one (b, h); a
+// wave = 32 queries, lane n = query, lane group g = key half) on the operands the block's prologue lays out: q pre-multiplied
+// by scale * log2(e) and the fp32 bias by log2(e), so the S^T accumulator is already in log2 units; V^T with the keys of each
+// 16-key block stored {0-3, 8-11 | 4-7, 12-15}; S a multiple of 64.
+//   * Software pipeline over (sub-tile, row) steps.  A step turns the row's S^T tile into P (exp2, bf16, row sums), issues
+//     the row's P.V MFMAs and then the row's S^T MFMAs of the NEXT sub-tile, so the matrix core works through those while
+//     the wave computes the other rows' exponentials.  (A wave issues in order: with the S^T MFMAs of all rows issued
+//     together, its MFMA and VALU phases would alternate and only the second wave of the SIMD could fill the gaps.)
+//   * p = exp2(acc) with no per-element shift.  A row's reference max stays 0 while its logits stay inside +-TD_BAND (checked
+//     on the row's first live sub-tile) and each sub-tile's partial row sum stays below 2^64; otherwise the row moves its
+//     reference and from then on subtracts it.  Every value is relative to the reference, so its choice costs no precision.
+//   * K and V^T tiles (64 keys) go global -> LDS by DMA (global_load_lds_dwordx4) into a ring of TA_NB buffers, in
+//     XOR-swizzled 16-byte chunks so the MFMA fragment reads are conflict-free 16-byte reads (K: chunk c of key k at
+//     c ^ ((k >> 2) & 3); V^T: chunk c of row d at c ^ ((d >> 1) & 7)); the permuted key order makes a lane's V^T fragment
+//     one 16-byte chunk.  Three buffers let the barrier that publishes tile T + 1 come before the last reads of tile T.
+//   * the bias sub-tiles and the DMA are issued from inline assembly, every one unconditionally, and waited for with exact
+//     counts (the memory counter retires in order), so no wait covers a load that is not needed yet;
+//   * the keep bits of all keys of the TA_R rows are built once (LDS table), so the key loop reads no mask.
+constexpr int TA_NB = 3;                                 // K / V^T tile buffers of the block-layout core
+constexpr float TD_PS_MAX = 18446744073709551616.0f;     // 2^64: a sub-tile's partial row sum at or above it moves the reference
+constexpr float TD_BAND = 32.0f;                         // first live sub-tile: a max outside +-TD_BAND (log2 units) sets it
+constexpr float TD_MOVE = 48.0f;                         // later sub-tiles: a max more than TD_MOVE above it moves it
 
 // 16 bytes at sbase + voff + IMM (scalar base, 32-bit per-lane byte offset) into registers, not waited for here
 template <int IMM>
@@ -360,22 +370,22 @@ __device__ __forceinline__ void vm_wait() {
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_dma(const CoreParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][TA_R][TA_KT * TA_D];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][TA_R][TA_D * TA_KT];
+  __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][TA_R][TA_KT * TA_D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[TA_NB][TA_R][TA_D * TA_KT];
   __shared__ uint64_t sKeepAll[TA_R][TA_MAXW];
   __shared__ int sAlive[TA_R];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t nq = cdiv(p.S, 128), nr = cdiv(p.N, TA_R);
-  const int64_t total = p.B * p.H * nr * nq;
-  const int64_t per = (total + 7) / 8;
-  const int64_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  // the host checks that the grid fits 31 bits: the workgroup decode is 32-bit
+  const uint32_t nq = (uint32_t)cdiv(p.S, 128), nr = (uint32_t)cdiv(p.N, TA_R), H = (uint32_t)p.H;
+  const uint32_t total = (uint32_t)p.B * H * nr * nq;
+  const uint32_t per = (total + 7) / 8;
+  const uint32_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
   if (w >= total) return;
-  const int64_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
-  const int64_t b = bh / p.H, h = bh % p.H;
-  const int64_t i0 = rg * TA_R;
-  const int64_t q = qt * 128 + wave * 32 + n;
+  const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
+  const int64_t b = bh / H, h = bh % H;
+  const int64_t i0 = (int64_t)rg * TA_R;
+  const int64_t q = (int64_t)qt * 128 + wave * 32 + n;
   const bool qlive = q < p.S;
-  const float c2 = LOG2E;                               // q carries the scale: the accumulator is in natural-log units
 
   bf16x8 qf[TA_R][2];
 #pragma unroll
@@ -386,44 +396,39 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     qf[r][0] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0, 0, 0, 0});
     qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
   }
-  // the Q loads complete here: inside the key loop the only vector-memory operations are the counted ones below
+
+  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys, all of the row's mask loads in flight together
+  // (overlapping the Q loads); a row with no kept key attends uniformly to every key (its words become all ones)
+  const int nw = (int)(p.S >> 6);
+  if (wave < TA_R) {
+    const int64_t i = i0 + wave;
+    const bool rowok = i < p.N;
+    auto build = [&](auto elt) {
+      using T = decltype(elt);
+      const T* mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + (rowok ? i : 0) * p.ms[1];
+      uint64_t any = 0;
+      for (int c0 = 0; c0 < nw; c0 += 16) {
+        T raw[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) raw[u] = (p.mask && c0 + u < nw) ? mrow[(int64_t)(64 * (c0 + u) + l) * p.ms[2]] : (T)1;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (c0 + u >= nw) break;
+          const uint64_t bal = __ballot(rowok && raw[u] != (T)0);
+          any |= bal;
+          if (l == 0) sKeepAll[wave][c0 + u] = bal;
+        }
+      }
+      if (rowok && any == 0)
+        for (int c = l; c < nw; c += 64) sKeepAll[wave][c] = ~0ull;
+      if (l == 0) sAlive[wave] = any != 0;
+    };
+    if (p.mask_f32) build(0.0f);
+    else build((uint8_t)0);
+  }
+  // the Q and mask loads complete here: inside the key loop the only vector-memory operations are the counted ones below
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
-
-  // keep table (8 mask loads in flight per wave); a row with no kept key attends uniformly to every key
-  const int64_t nw = p.S >> 6, npair = TA_R * nw;
-  auto build = [&](auto elt) {
-    using T = decltype(elt);
-    for (int64_t base = wave; base < npair; base += 32) {
-      T raw[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int64_t pr = base + 4 * u < npair ? base + 4 * u : base;
-        const int64_t r = pr / nw, c = pr % nw, i = i0 + r < p.N ? i0 + r : p.N - 1;
-        raw[u] = p.mask ? static_cast<const T*>(p.mask)[b * p.ms[0] + i * p.ms[1] + (c * 64 + l) * p.ms[2]] : (T)1;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int64_t pr = base + 4 * u;
-        const int64_t r = pr < npair ? pr / nw : 0, c = pr < npair ? pr % nw : 0;
-        const uint64_t bal = __ballot(pr < npair && i0 + r < p.N && raw[u] != (T)0);
-        if (pr < npair && l == 0) sKeepAll[r][c] = bal;
-      }
-    }
-  };
-  if (p.mask_f32) build(0.0f);
-  else build((uint8_t)0);
-  __syncthreads();
-  if (tid < TA_R) {
-    uint64_t any = 0;
-    for (int64_t c = 0; c < nw; ++c) any |= sKeepAll[tid][c];
-    sAlive[tid] = any != 0;
-  }
-  __syncthreads();
-  for (int64_t x = tid; x < npair; x += 256) {
-    const int64_t r = x / nw;
-    if (i0 + r < p.N && !sAlive[r]) sKeepAll[r][x % nw] = ~0ull;
-  }
   __syncthreads();
   bool dead[TA_R];
   bool dead_any = false;
@@ -450,16 +455,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
     }
   }
+  // LDS byte addresses of this wave's chunk block in buffer 0, row 0 (buffer / row steps are constants)
+  const uint32_t kl0 = lds_addr(&sK[0][0][512 * wave]), vl0 = lds_addr(&sV[0][0][512 * wave]);
+  constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
   auto dma_tile = [&](int64_t k0, int buf) {
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      lds_dma16_s(koff, kb[r] + k0 * p.ks[3], lds_addr(&sK[buf][r][512 * wave]));
-      lds_dma16_s(voff, vb[r] + k0, lds_addr(&sV[buf][r][512 * wave]));
+      lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
+      lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
     }
   };
-  // The wait counts in the key loop (vm_wait<8>, vm_wait4<DMA_OPS + 4>) assume exactly DMA_OPS operations per dma_tile and
-  // 4 per bias_issue, every one issued unconditionally: a wait that counted fewer operations than were issued after the
-  // load it guards would let that load land in registers already reused.
+  // The wait counts (vm_wait4<DMA_OPS + 4>, vm_wait4<4>) assume exactly DMA_OPS operations per dma_tile and 4 per
+  // bias_issue, every one issued unconditionally and in the order of the loop below: a wait that counted fewer operations
+  // than were issued after the load it guards would let that load land in registers already reused.
   constexpr int DMA_OPS = 2 * TA_R;
 
   const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
@@ -473,34 +481,69 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     dst[3] = gload4_async<96>(boff, sb);
   };
 
-  f32x16 o[TA_R];
-  float lrow[TA_R], mb[TA_R], thr[TA_R];
+  f32x16 o[TA_R], s[TA_R];
+  float lrow[TA_R], mb[TA_R];
+  bool seen[TA_R], sh[TA_R];       // seen: the row's first live sub-tile has set its reference (per lane, equal in l and
+                                   // l ^ 32; rows past N count as seen); sh: some lane of the row has a nonzero reference
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) {
     o[r] = f32x16{};
     lrow[r] = 0.f;
     mb[r] = 0.f;
-    thr[r] = -INFINITY;
+    seen[r] = i0 + r >= p.N;
+    sh[r] = false;
   }
   // fragment offsets (bf16 elements) inside a row's K / V^T tile
   const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile adds 32 keys
   const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
   const int vsw = (n >> 1) & 7;
+  auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
+    f32x16 bc;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
+    return mfma32(as_bf8(k1f), qf[r][1], mfma32(as_bf8(k0f), qf[r][0], bc));
+  };
+  // P of one row step: bf16 pairs of exp2(s) and the sum of the bf16 values the P.V MFMA consumes
+  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8]) {
+    float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
+      if (v & 2) ps1 = dot2_bf16(pk[v >> 1], ps1);
+      else ps0 = dot2_bf16(pk[v >> 1], ps0);
+    }
+    return ps0 + ps1;
+  };
 
-  f32x4 bq[2][4];
+  const int64_t nT = p.S / TA_KT;
+  f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
+  // issue order DMA(0), bias(0), bias(1), DMA(1): the loop's wait counts continue from it
   dma_tile(0, 0);
   bias_issue(0, bq[0]);
   bias_issue(32, bq[1]);
-  int buf = 0;
-  for (int64_t k0 = 0; k0 < p.S; k0 += TA_KT) {
-    const bool more = k0 + TA_KT < p.S;
-    vm_wait<8>();                                       // this tile's DMA (the two bias sub-tiles after it may be pending)
-    __builtin_amdgcn_s_barrier();                       // every wave's part of the tile is in; the other buffer is free
-    dma_tile(more ? k0 + TA_KT : k0, buf ^ 1);          // the last tile re-reads itself: the wait counts stay exact
+  dma_tile(nT > 1 ? TA_KT : 0, 1);
+  vm_wait4<4 + DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);    // tile 0 and bias 0 are in (bias 1, tile 1 may be pending)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const uint16_t* kt = &sK[0][r][0];
+    s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
+  }
+
+  int bt = 0;                      // buffer of tile T
+  for (int64_t T = 0; T < nT; ++T) {
+    const bool moreT = T + 1 < nT;
+    const int bn = bt == TA_NB - 1 ? 0 : bt + 1;      // buffer of tile T + 1
+    const int bf = bn == TA_NB - 1 ? 0 : bn + 1;      // buffer of tile T + 2: tile T - 1's, free once every wave is past it
+    const int64_t k0 = T * TA_KT;
+    bias_issue(moreT ? k0 + TA_KT : 0, bq[0]);         // sub-tile 2T + 2 (past the end: a valid re-read, the counts stay exact)
     uint64_t kw[TA_R], kall = ~0ull, kany = 0;
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      const uint64_t wv = sKeepAll[r][k0 >> 6];                         // uniform: keep it in scalar registers
+      const uint64_t wv = sKeepAll[r][T];                               // uniform: keep it in scalar registers
       const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
       const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);   // unsigned: no sign extension
       kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
@@ -510,91 +553,73 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const bool full = (kall == ~0ull) && !dead_any;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      vm_wait4<DMA_OPS + 4>(bq[sub][0], bq[sub][1], bq[sub][2], bq[sub][3]);
-      f32x16 bc;
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bq[sub][qd][e];
+      if (sub == 0) {
+        vm_wait4<DMA_OPS + 4>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);   // bias 2T + 1 (tile T + 1, bias 2T + 2 may be pending)
+      } else {
+        bias_issue(moreT ? k0 + TA_KT + 32 : 32, bq[1]);                 // sub-tile 2T + 3
+        vm_wait4<4>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);             // bias 2T + 2 and tile T + 1 are in
+        __builtin_amdgcn_s_barrier();                                     // every wave's part of tile T + 1 is in, and every
+        asm volatile("" ::: "memory");                                    // wave is done with tile T - 1
+        dma_tile((T + 2 < nT ? T + 2 : nT - 1) * TA_KT, bf);
+      }
       const bool live_sub = (uint32_t)(kany >> (32 * sub)) != 0;
-      f32x16 s[TA_R];
-      if (live_sub) {
+      const bool next = sub == 0 || moreT;                                // the next sub-tile exists
+      const uint16_t* knext = sub == 0 ? &sK[bt][0][32 * TA_D] : &sK[bn][0][0];
 #pragma unroll
-        for (int r = 0; r < TA_R; ++r) {
-          const uint16_t* kt = &sK[buf][r][32 * sub * TA_D];
-          s[r] = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(kt + kfo0)), qf[r][0], bc);
-          s[r] = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(kt + kfo1)), qf[r][1], s[r]);
+      for (int r = 0; r < TA_R; ++r) {
+        // fragment reads first: V^T of this step, K of the row's next S^T
+        const uint16_t* vt = &sV[bt][r][n * TA_KT];
+        const u32x4 vf0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + g) ^ vsw));
+        const u32x4 vf1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + 2 + g) ^ vsw));
+        const uint16_t* kt = knext + r * (TA_KT * TA_D);
+        u32x4 kf0 = u32x4{0, 0, 0, 0}, kf1 = u32x4{0, 0, 0, 0};
+        if (next) {
+          kf0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
+          kf1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
         }
-      }
-      bias_issue(more ? k0 + TA_KT + 32 * sub : 32 * sub, bq[sub]);
-      if (!live_sub) continue;
-      if (!full) {
+        if (live_sub) {
+          if (!full) {
+            const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
 #pragma unroll
-        for (int r = 0; r < TA_R; ++r) {
-          const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float sv = dead[r] ? 0.f : s[r][v];
-            s[r][v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? sv : -INFINITY;
+            for (int v = 0; v < 16; ++v) {
+              const float sv = dead[r] ? 0.f : s[r][v];
+              s[r][v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? sv : -INFINITY;
+            }
           }
+          if (sh[r]) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[r][v] -= mb[r];
+          }
+          uint32_t pk[8];
+          float ps = expsum(s[r], pk);
+          if (__ballot(!seen[r] || !(ps < TD_PS_MAX)) != 0) {
+            // set or move the reference of the queries that need it; the decision depends only on the sub-tile max over
+            // both key halves, so lanes l and l ^ 32 (one query) always agree
+            float m0 = s[r][0];
+#pragma unroll
+            for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, s[r][v]);
+            const float mt = half_max(m0);
+            const bool fin = mt > -INFINITY;
+            const float shift = !seen[r] ? ((fin && (mt > TD_BAND || mt < -TD_BAND)) ? mt : 0.f) : (mt > TD_MOVE ? mt : 0.f);
+            const float alpha = seen[r] && shift != 0.f ? fast_exp2(-shift) : 1.0f;   // before the first live sub-tile o, l are 0
+            lrow[r] *= alpha;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[r][v] -= shift;
+            mb[r] += shift;
+            seen[r] = seen[r] || fin;
+            sh[r] = __ballot(mb[r] != 0.f) != 0;
+            ps = expsum(s[r], pk);
+          }
+          lrow[r] += ps;
+          o[r] = mfma32(as_bf8(vf0), as_bf8(u32x4{pk[0], pk[1], pk[2], pk[3]}), o[r]);
+          o[r] = mfma32(as_bf8(vf1), as_bf8(u32x4{pk[4], pk[5], pk[6], pk[7]}), o[r]);
         }
-      }
-      // p = exp2(logit - mb) straight away; the row's running max is only looked at on the row's first live sub-tile and
-      // when this sub-tile's partial sum leaves [0, 2^64) -- a logit more than ~60 (log2 units) above mb.  Every value is
-      // relative to mb, so a stale mb costs no precision; fp32 / bf16 hold p up to 2^64 with room to spare.
-      uint32_t pk[TA_R][8];
-      float ps[TA_R];
-      auto expsum = [&](int r) {
-        float ps0 = 0.f, ps1 = 0.f;
-#pragma unroll
-        for (int v = 0; v < 16; v += 2) {
-          pk[r][v >> 1] = pack2(fast_exp2(s[r][v]), fast_exp2(s[r][v + 1]));
-          if (v & 2) ps1 = dot2_bf16(pk[r][v >> 1], ps1);     // the sum of the bf16 P the PV MFMA consumes
-          else ps0 = dot2_bf16(pk[r][v >> 1], ps0);
-        }
-        ps[r] = ps0 + ps1;
-      };
-      bool bad = false;
-#pragma unroll
-      for (int r = 0; r < TA_R; ++r) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) s[r][v] = fmaf(s[r][v], c2, -mb[r]);
-        expsum(r);
-        bad |= thr[r] == -INFINITY || !(ps[r] < TD_PS_MAX);
-      }
-      if (__ballot(bad) != 0) {        // move the reference max of the queries that need it (per lane; others unchanged)
-#pragma unroll
-        for (int r = 0; r < TA_R; ++r) {
-          float m0 = s[r][0];
-#pragma unroll
-          for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, s[r][v]);
-          const float mt = half_max(m0);
-          const bool mv = mt > thr[r];
-          const float shift = mv ? mt : 0.f;
-          const float alpha = (mv && thr[r] != -INFINITY) ? fast_exp2(-mt) : 1.0f;
-          lrow[r] *= alpha;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) s[r][v] -= shift;
-          mb[r] += shift;
-          thr[r] = mv ? TD_HEADROOM : thr[r];
-          expsum(r);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < TA_R; ++r) {
-        lrow[r] += ps[r];
-        const uint16_t* vt = &sV[buf][r][n * TA_KT];
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const int ch = (4 * sub + 2 * st + g) ^ vsw;
-          o[r] = mfma32(as_bf8(*reinterpret_cast<const u32x4*>(vt + 8 * ch)),
-                        as_bf8(u32x4{pk[r][4 * st], pk[r][4 * st + 1], pk[r][4 * st + 2], pk[r][4 * st + 3]}), o[r]);
-        }
+        if (next) s[r] = qk(kf0, kf1, r, sub == 0 ? bq[1] : bq[0]);
       }
     }
-    buf ^= 1;
+    bt = bn;
   }
   vm_wait<0>();                                         // no DMA may land after the wave ends
   if (!qlive) return;
@@ -757,6 +782,7 @@ struct ProParams {
   int64_t N, Jp, B, row0, rows;
   int ending, flags;
   float q_scale;                 // q is stored times this (the fused block folds the attention scale into q)
+  float bias_scale;              // and the bias times this (log2(e) for the block-layout core: logits in log2 units)
 };
 
 __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
@@ -818,7 +844,7 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
       } else if (g == 0 && live) {                        // bias (fp32): [B, H, I, J], absolute row
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          if (v < H) p.bias[((b * H + v) * N + i) * N + j] = acc[v];
+          if (v < H) p.bias[((b * H + v) * N + i) * N + j] = acc[v] * p.bias_scale;
       }
     }
   }
@@ -1205,10 +1231,14 @@ static int block_shape_check(int dtype, int64_t B, int C, int64_t H, int64_t D, 
   return fail(err, errlen, FPF_E_DTYPE, "dtype %d", dtype);
 }
 
+// The bf16 block with N a multiple of 64 (up to 8192) runs the block-layout core (v_layout 2): its q carries scale * log2(e),
+// its bias (computed in the block or by fpf_triattn_bias_fwd for bias_in) log2(e).
+static bool block_layout2(int dtype, int64_t N) { return dtype == FPF_DT_BF16 && N % TA_KT == 0 && N <= 64 * TA_MAXW; }
+
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
-                           int64_t rows = -1, float q_scale = 1.0f) {
+                           int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f) {
   if (rows < 0) rows = N;
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || ((flags & PRO_QKV) && (!aligned16(q) || !aligned16(k) || !aligned16(v))) ||
@@ -1237,11 +1267,12 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.ending = ending;
     p.flags = flags;
     p.q_scale = q_scale;
+    p.bias_scale = bias_scale;
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
-  if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS) || q_scale != 1.0f)
+  if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS) || q_scale != 1.0f || bias_scale != 1.0f)
     return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output, q unscaled)");
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
@@ -1315,7 +1346,8 @@ extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, c
   if (rc) return rc;
   // the prologue kernel with only its bias output; the q|k|v|g weights are not read (the weight staging still needs a pointer)
   return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg ? a->w_qkvg : a->w_b, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending,
-                         nullptr, nullptr, nullptr, 0, nullptr, a->bias, static_cast<hipStream_t>(stream), err, errlen, PRO_BIAS);
+                         nullptr, nullptr, nullptr, 0, nullptr, a->bias, static_cast<hipStream_t>(stream), err, errlen, PRO_BIAS, 0, -1, 1.0f,
+                         block_layout2(a->dtype, a->N) ? LOG2E : 1.0f);
 }
 
 extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen) {
@@ -1359,8 +1391,9 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.v = v;
   const int64_t st5[5] = {R * H * N * D, H * N * D, N * D, D, 1};
   for (int t = 0; t < 5; ++t) c.q_stride[t] = c.k_stride[t] = c.v_stride[t] = c.out_stride[t] = st5[t];
-  // bf16 with N a multiple of 64 (up to 8192): the DMA-staged core, fed q times the scale and V^T keys in its 16-block order
-  const bool dma_core = a->dtype == FPF_DT_BF16 && N % TA_KT == 0 && N <= 64 * TA_MAXW;
+  // bf16 with N a multiple of 64 (up to 8192): the block-layout core, fed q times scale * log2(e), the bias times log2(e)
+  // and V^T keys in its 16-block order
+  const bool dma_core = block_layout2(a->dtype, N);
   if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, R, H, D, Jp]
     c.v_layout = dma_core ? 2 : 1;
     c.v_stride[0] = R * H * D * Jp;
@@ -1386,7 +1419,7 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
   const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM : 0);
   int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
-                           bias, st, err, errlen, flags, row0, R, dma_core ? scale : 1.0f);
+                           bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f);
   if (rc) return rc;
   rc = core_launch(&c, st, err, errlen);
   if (rc) return rc;
