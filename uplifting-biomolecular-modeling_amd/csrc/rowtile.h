@@ -16,6 +16,17 @@ constexpr int RT_C = 128;            // channels per pixel row
 constexpr int RT_LD = RT_C + 8;      // LDS pitch (bf16) of a 128-wide weight row: 272 B, conflict-free 16-byte reads
 constexpr int RT_WAVES = 8;          // waves per workgroup
 
+// Tile t of a persistent loop's [B][rows][tpr] list of 32-pixel tiles: image b, row r, column tile c.  32-bit division (the
+// launchers refuse lists of 2^31 tiles or more: rt_tiles_ok); t, per_b and tpr are wave-uniform, so this is scalar code.
+struct RtTile {
+  int64_t b, r, c;
+};
+__device__ __forceinline__ RtTile rt_tile(uint32_t t, uint32_t per_b, uint32_t tpr) {
+  const uint32_t b = t / per_b, rem = t - b * per_b, r = rem / tpr;
+  return {(int64_t)b, (int64_t)r, (int64_t)(rem - r * tpr)};
+}
+inline bool rt_tiles_ok(int64_t tiles) { return tiles >= 0 && tiles < (int64_t(1) << 31); }
+
 // K-step t of a 128-channel reduction takes channels 16 t .. 16 t + 15: lane (n, g) holds the 8-channel chunk 2 t + g.  The two
 // lanes of a pixel read adjacent chunks, so each 16-byte load instruction touches one 32-byte piece of 32 pixel rows.
 __device__ __forceinline__ constexpr int rt_chunk(int t, int g) { return 2 * t + g; }

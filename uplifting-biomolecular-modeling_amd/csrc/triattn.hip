@@ -795,18 +795,20 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
   __syncthreads();
   const int H = p.H, D = TP_HD / H;
   const int64_t N = p.N, Jp = p.Jp, R = p.rows;
-  const int64_t tpr = cdiv(N, 32), per_b = R * tpr, total = p.B * per_b;
-  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
+  const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)R * tpr, total = (uint32_t)p.B * per_b;
+  const uint32_t stride = gridDim.x * RT_WAVES;
   u32x4 raw[8];                                         // the next tile's pixel rows, loaded while this tile computes
-  auto fetch = [&](int64_t tt) {
-    const int64_t b = tt / per_b, i = p.row0 + (tt % per_b) / tpr, j = (tt % tpr) * 32 + n;
+  auto fetch = [&](uint32_t tt) {
+    const RtTile tl = rt_tile(tt, per_b, tpr);
+    const int64_t b = tl.b, i = p.row0 + tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
     const int64_t zpix = p.ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
     rt_load(p.z + zpix * RT_C, live, g, raw);
   };
-  if ((int64_t)blockIdx.x * RT_WAVES + wave < total) fetch((int64_t)blockIdx.x * RT_WAVES + wave);
-  for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
-    const int64_t b = t / per_b, ii = (t % per_b) / tpr, i = p.row0 + ii, j = (t % tpr) * 32 + n;
+  if (blockIdx.x * RT_WAVES + wave < total) fetch(blockIdx.x * RT_WAVES + wave);
+  for (uint32_t t = blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
+    const RtTile tl = rt_tile(t, per_b, tpr);
+    const int64_t b = tl.b, ii = tl.r, i = p.row0 + ii, j = tl.c * 32 + n;
     const bool live = j < N;
     bf16x8 xb[8];
     rt_ln(raw, g, sLN, p.eps, xb);
@@ -861,10 +863,11 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
   rt_stage_weights(sW, w_o, RT_C, RT_C, tid, 512);
   __syncthreads();
   const int D = TP_HD / H;
-  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
-  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
-  for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
-    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+  const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)N * tpr, total = (uint32_t)B * per_b;
+  const uint32_t stride = gridDim.x * RT_WAVES;
+  for (uint32_t t = blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
+    const RtTile tl = rt_tile(t, per_b, tpr);
+    const int64_t b = tl.b, i = tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
     bf16x8 xb[8];
 #pragma unroll
@@ -937,33 +940,48 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
   }
   __syncthreads();
   constexpr int H = TP_HD / TA_D;
-  const int64_t tpr = cdiv(N, 32), per_b = rows * tpr, total = B * per_b;
-  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
-  for (int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
-    const int64_t b = t / per_b, ii = (t % per_b) / tpr, i = row0 + ii, j = (t % tpr) * 32 + n;
-    const bool live = j < N;
-    const int64_t zpix = ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
+  const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)rows * tpr, total = (uint32_t)B * per_b;
+  const uint32_t stride = gridDim.x * RT_WAVES;
+  // z rows of a tile: lane (n, g) chunk t holds channels 16t + 8g .. +7, exactly the channels its output stores cover, so the
+  // residual reuses them; the next tile's rows are loaded while this tile computes
+  u32x4 raw[8];
+  auto zpix_of = [&](uint32_t tt, bool& live) {
+    const RtTile tl = rt_tile(tt, per_b, tpr);
+    const int64_t b = tl.b, i = row0 + tl.r, j = tl.c * 32 + n;
+    live = j < N;
+    return ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
+  };
+  if (blockIdx.x * RT_WAVES + wave < total) {
+    bool lv;
+    const int64_t zp0 = zpix_of(blockIdx.x * RT_WAVES + wave, lv);
+    rt_load(zin + zp0 * RT_C, lv, g, raw);
+  }
+  for (uint32_t t = blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
+    const RtTile tl = rt_tile(t, per_b, tpr);
+    const int64_t b = tl.b, ii = tl.r, j = tl.c * 32 + n;
+    bool live;
+    const int64_t zpix = zpix_of(t, live);
+    // o of all four heads for this tile, issued before the LayerNorm
+    u32x2 ov2[4][2][2];
+    const uint16_t* op = o + (((b * rows + ii) * H) * N + (live ? j : 0)) * TA_D + 4 * g;   // o rows of this range
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          ov2[cb][half][e] = live ? *reinterpret_cast<const u32x2*>(op + (int64_t)cb * N * TA_D + 16 * half + 8 * e) : u32x2{0, 0};
     bf16x8 xb[8];
-    {
-      u32x4 raw[8];
-      rt_load(zin + zpix * RT_C, live, g, raw);
-      rt_ln(raw, g, sLN, eps, xb);
-    }
+    rt_ln(raw, g, sLN, eps, xb);
     f32x16 acc[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[k] = f32x16{};
-    const uint16_t* op = o + (((b * rows + ii) * H) * N + (live ? j : 0)) * TA_D + 4 * g;   // o rows of this range
-#pragma unroll 1
+#pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       const f32x16 gacc = rt_gemm32(sWg, cb * 32, n, g, xb);     // g of head cb: channels cb*32 + c_row(v, g)
-      const uint16_t* oh = op + (int64_t)cb * N * TA_D;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        u32x2 o0 = {0, 0}, o1 = {0, 0};
-        if (live) {
-          o0 = *reinterpret_cast<const u32x2*>(oh + 16 * half);
-          o1 = *reinterpret_cast<const u32x2*>(oh + 16 * half + 8);
-        }
+        const u32x2 o0 = ov2[cb][half][0], o1 = ov2[cb][half][1];
         const float ov[8] = {lo_bf(o0[0]), hi_bf(o0[0]), lo_bf(o0[1]), hi_bf(o0[1]), lo_bf(o1[0]), hi_bf(o1[0]), lo_bf(o1[1]), hi_bf(o1[1])};
         uint32_t w4[4];
 #pragma unroll
@@ -979,7 +997,6 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
     }
     // lane (n, g) stores channels blk*32 + 8g .. +7 and blk*32 + 16 + 8g .. +7 of pixel n: two 16-byte stores per block
     uint16_t* zp = zout + zpix * RT_C + 8 * g;
-    const uint16_t* zr = zin + zpix * RT_C + 8 * g;
 #pragma unroll
     for (int blk = 0; blk < 4; ++blk) {
       float y[16];
@@ -989,7 +1006,7 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
       for (int h2 = 0; h2 < 2; ++h2) {
         u32x4 w;
         if (residual) {
-          const u32x4 r = *reinterpret_cast<const u32x4*>(zr + blk * 32 + 16 * h2);
+          const u32x4 r = raw[2 * blk + h2];                     // channels blk*32 + 16 h2 + 8g .. +7 of this pixel
 #pragma unroll
           for (int e = 0; e < 4; ++e) w[e] = pack2(y[8 * h2 + 2 * e] + lo_bf(r[e]), y[8 * h2 + 2 * e + 1] + hi_bf(r[e]));
         } else {
@@ -998,6 +1015,11 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
         }
         *reinterpret_cast<u32x4*>(zp + blk * 32 + 16 * h2) = w;
       }
+    }
+    if (t + stride < total) {
+      bool lvn;
+      const int64_t zpn = zpix_of(t + stride, lvn);
+      rt_load(zin + zpn * RT_C, lvn, g, raw);
     }
   }
 }
@@ -1268,6 +1290,7 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.flags = flags;
     p.q_scale = q_scale;
     p.bias_scale = bias_scale;
+    if (!rt_tiles_ok(B * rows * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "prologue: 2^31 or more 32-pixel tiles");
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
@@ -1285,6 +1308,7 @@ static int epilogue_launch(int dtype, const void* o, const void* g, const void* 
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(o) || !aligned16(g) || !aligned16(w_o) || !aligned16(out))
       return fail(err, errlen, FPF_E_ALIGN, "epilogue operands must be 16-byte aligned");
+    if (!rt_tiles_ok(B * N * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "epilogue: 2^31 or more 32-pixel tiles");
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)o, (const uint16_t*)g, (const uint16_t*)w_o, H,
                        (uint16_t*)out, N, B, ending, residual);
@@ -1425,6 +1449,7 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   if (rc) return rc;
   if (fused_gate) {
     if (!aligned16(a->out)) return fail(err, errlen, FPF_E_ALIGN, "out must be 16-byte aligned");
+    if (!rt_tiles_ok(B * R * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "epilogue: 2^31 or more 32-pixel tiles");
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * R * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_epilogue_gate_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w, a->ln_b,
                        a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, (uint16_t*)a->out, N, B, row0, R, a->ending,

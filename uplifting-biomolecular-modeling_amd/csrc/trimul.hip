@@ -46,19 +46,21 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
   rt_stage_weights(sW + 2 * RT_C * RT_LD, w_bp, RT_C, RT_C, tid, 512);
   rt_stage_weights(sW + 3 * RT_C * RT_LD, w_bg, RT_C, RT_C, tid, 512);
   __syncthreads();
-  const int64_t tpr = Np / 32, per_b = Np * tpr, total = B * per_b;
-  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
-  int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave;
+  const uint32_t tpr = (uint32_t)(Np / 32), per_b = (uint32_t)Np * tpr, total = (uint32_t)B * per_b;
+  const uint32_t stride = gridDim.x * RT_WAVES;
+  uint32_t t = blockIdx.x * RT_WAVES + wave;
   u32x4 raw[8];
-  auto fetch = [&](int64_t tt) {
-    const int64_t b = tt / per_b, P = (tt % per_b) / tpr, Q = (tt % tpr) * 32 + n;
+  auto fetch = [&](uint32_t tt) {
+    const RtTile tl = rt_tile(tt, per_b, tpr);
+    const int64_t b = tl.b, P = tl.r, Q = tl.c * 32 + n;
     const bool live = P < N && Q < N;
     const int64_t pix = (b * N + (outgoing ? P : Q)) * N + (outgoing ? Q : P);
     rt_load(z + (live ? pix : 0) * RT_C, live, g, raw);
   };
   if (t < total) fetch(t);
   for (; t < total; t += stride) {
-    const int64_t b = t / per_b, P = (t % per_b) / tpr, Q = (t % tpr) * 32 + n;
+    const RtTile tl = rt_tile(t, per_b, tpr);
+    const int64_t b = tl.b, P = tl.r, Q = tl.c * 32 + n;
     const bool live = P < N && Q < N;
     const int64_t pix = (b * N + (outgoing ? P : Q)) * N + (outgoing ? Q : P);
     const float m = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
@@ -315,13 +317,14 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
   rt_stage_weights(sW, w_o, RT_C, RT_C, tid, 512);
   rt_stage_weights(sW + RT_C * RT_LD, w_og, RT_C, RT_C, tid, 512);
   __syncthreads();
-  const int64_t tpr = cdiv(N, 32), per_b = N * tpr, total = B * per_b;
-  const int64_t stride = (int64_t)gridDim.x * RT_WAVES;
+  const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)N * tpr, total = (uint32_t)B * per_b;
+  const uint32_t stride = gridDim.x * RT_WAVES;
   uint16_t* sx = sX[wave];
-  int64_t t = (int64_t)blockIdx.x * RT_WAVES + wave;
+  uint32_t t = blockIdx.x * RT_WAVES + wave;
   u32x4 rx[8], rz[8];
-  auto fetch = [&](int64_t tt) {
-    const int64_t b = tt / per_b, i = (tt % per_b) / tpr, j0 = (tt % tpr) * 32, j = j0 + n;
+  auto fetch = [&](uint32_t tt) {
+    const RtTile tl = rt_tile(tt, per_b, tpr);
+    const int64_t b = tl.b, i = tl.r, j0 = tl.c * 32, j = j0 + n;
     const uint16_t* xs = X + tl_off(b, 0, i, j0, Np);      // the tile's 8 KB block (rows padded to Np: in bounds)
 #pragma unroll
     for (int it = 0; it < 8; ++it) rx[it] = *reinterpret_cast<const u32x4*>(xs + 8 * (l + 64 * it));   // channel q >> 2, chunk q & 3
@@ -329,7 +332,8 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
     rt_load(zin + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
   };
   for (; t < total; t += stride) {
-    const int64_t b = t / per_b, i = (t % per_b) / tpr, j = (t % tpr) * 32 + n;
+    const RtTile tl = rt_tile(t, per_b, tpr);
+    const int64_t b = tl.b, i = tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
     const int64_t pix = (b * N + i) * N + j;
     fetch(t);
@@ -594,7 +598,8 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
     uint16_t* pa = static_cast<uint16_t*>(a->workspace);
     uint16_t* pb = pa + B * TM_C * Np * Np;
     uint16_t* X = pb + B * TM_C * Np * Np;
-    const int64_t k1_tiles = B * Np * (Np / 32);
+    const int64_t k1_tiles = B * Np * (Np / 32), k3_tiles = B * N * cdiv(N, 32);
+    if (!rt_tiles_ok(k1_tiles) || !rt_tiles_ok(k3_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
     const unsigned k1_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k1_tiles, RT_WAVES));
     hipLaunchKernelGGL(trimul_k1_bf16, dim3(k1_grid), dim3(512), 0, st, (const uint16_t*)a->z, a->mask, a->ln_in_w, a->ln_in_b, a->eps,
                        (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B,
@@ -611,7 +616,6 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
       rc = launched(err, errlen, "trimul_contract_bf16");
     }
     if (rc) return rc;
-    const int64_t k3_tiles = B * N * cdiv(N, 32);
     const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
     hipLaunchKernelGGL(trimul_k3_bf16, dim3(k3_grid), dim3(512), 0, st, (const uint16_t*)a->z, (uint16_t*)a->out, X, a->ln_in_w, a->ln_in_b,
                        a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np, B, a->residual);
