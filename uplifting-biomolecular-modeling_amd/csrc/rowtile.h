@@ -84,38 +84,32 @@ __device__ __forceinline__ void rt_stage_weights(uint16_t* __restrict__ s, const
   }
 }
 
-// D = W[row0 .. row0 + 31] x^T over the 128 channels (8 k-steps), weights from LDS.  The weight fragment of k-step t + 1 is
-// read before the MFMA of k-step t issues, so the LDS latency hides behind the matrix core.
-__device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
+// D = W[row0 .. row0 + 31] x^T over the 128 channels (8 k-steps), weights from LDS.  The weight fragments run LA k-steps
+// ahead of the MFMAs (a single MFMA covers ~32 cycles, an LDS read under load ~100), so the matrix core does not wait on
+// the reads; LA + 1 fragments are live at a time.
+template <int LA = 3, bool XW = false>
+__device__ __forceinline__ f32x16 rt_gemm32_la(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
   const uint16_t* r = s + (row0 + n) * RT_LD + 8 * g;
   f32x16 acc = {};
-  bf16x8 w = as_bf8(*reinterpret_cast<const u32x4*>(r));
+  bf16x8 w[8];
+#pragma unroll
+  for (int t = 0; t < LA; ++t) w[t] = as_bf8(*reinterpret_cast<const u32x4*>(r + 16 * t));
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    bf16x8 wn = w;
-    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 16 * (t + 1)));
-    acc = mfma32(w, xb[t], acc);
-    __builtin_amdgcn_sched_barrier(0);   // one k-step of lookahead: bounded register pressure
-    w = wn;
+    if (t + LA < 8) w[t + LA] = as_bf8(*reinterpret_cast<const u32x4*>(r + 16 * (t + LA)));
+    acc = XW ? mfma32(xb[t], w[t], acc) : mfma32(w[t], xb[t], acc);
+    __builtin_amdgcn_sched_barrier(0);   // keep the read ring as written: bounded register pressure
   }
   return acc;
+}
+__device__ __forceinline__ f32x16 rt_gemm32(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
+  return rt_gemm32_la<3, false>(s, row0, n, g, xb);
 }
 
 // The swapped product D = x W[row0 .. row0 + 31]^T (same fragments, operands exchanged): lane (n, g) then holds output
 // channel row0 + n for the 16 pixels c_row(v, g) of the tile.
 __device__ __forceinline__ f32x16 rt_gemm32_xw(const uint16_t* __restrict__ s, int row0, int n, int g, const bf16x8 (&xb)[8]) {
-  const uint16_t* r = s + (row0 + n) * RT_LD + 8 * g;
-  f32x16 acc = {};
-  bf16x8 w = as_bf8(*reinterpret_cast<const u32x4*>(r));
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    bf16x8 wn = w;
-    if (t < 7) wn = as_bf8(*reinterpret_cast<const u32x4*>(r + 16 * (t + 1)));
-    acc = mfma32(xb[t], w, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    w = wn;
-  }
-  return acc;
+  return rt_gemm32_la<3, true>(s, row0, n, g, xb);
 }
 
 // K GEMMs over the same B operand, k-step-major (the K weight fragments of k-step t + 1 are read while the K MFMAs of

@@ -978,7 +978,7 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
     for (int k = 0; k < 4; ++k) acc[k] = f32x16{};
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
-      const f32x16 gacc = rt_gemm32(sWg, cb * 32, n, g, xb);     // g of head cb: channels cb*32 + c_row(v, g)
+      const f32x16 gacc = rt_gemm32_la<1>(sWg, cb * 32, n, g, xb);   // g of head cb: channels cb*32 + c_row(v, g)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const u32x2 o0 = ov2[cb][half][0], o1 = ov2[cb][half][1];

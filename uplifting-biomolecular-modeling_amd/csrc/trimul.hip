@@ -296,10 +296,11 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
 }
 
 // ---------------------------------------------------------------------------------------------------------------- K3 (bf16)
-// Persistent: W_o and W_og live in LDS (70 KB); each wave loads its X tile (issued with the tile's z rows at the top of the
-// iteration; the second wave of the SIMD covers the latency -- a register prefetch of the next tile costs occupancy) X[c][i][j0 .. j0+31] (channel-major, 128 rows of
-// 64 B, 16-byte loads) and scatters it pixel-major into a private LDS slot, so the LN_out / B-operand reads are 16-byte rows,
-// then LN_out(X) W_o^T * sigmoid(LN_in(z) W_og^T) [+ z].
+// Persistent: W_o and W_og live in LDS (70 KB; with the per-wave X slots one workgroup of 8 waves per CU, so registers up
+// to 256 cost no occupancy).  Each wave scatters its X tile X[c][i][j0 .. j0+31] (channel-major, 128 rows of 64 B, loaded
+// during the previous tile) pixel-major into a private LDS slot, so the LN_out / B-operand reads are 16-byte rows, issues
+// the next tile's X loads, then LN_out(X) W_o^T * sigmoid(LN_in(z) W_og^T) [+ z] (the residual reuses the z rows the
+// LayerNorm read).
 constexpr int K3_XLD = RT_C + 8;     // LDS pitch of the staged X tile, pixel-major [32 pixels][128 channels]
 
 __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint16_t* out, const uint16_t* __restrict__ X,
@@ -322,21 +323,19 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
   uint16_t* sx = sX[wave];
   uint32_t t = blockIdx.x * RT_WAVES + wave;
   u32x4 rx[8], rz[8];
-  auto fetch = [&](uint32_t tt) {
+  auto fetch_x = [&](uint32_t tt) {                       // the tile's 8 KB X block (rows padded to Np: in bounds)
     const RtTile tl = rt_tile(tt, per_b, tpr);
-    const int64_t b = tl.b, i = tl.r, j0 = tl.c * 32, j = j0 + n;
-    const uint16_t* xs = X + tl_off(b, 0, i, j0, Np);      // the tile's 8 KB block (rows padded to Np: in bounds)
+    const uint16_t* xs = X + tl_off(tl.b, 0, tl.r, tl.c * 32, Np);
 #pragma unroll
     for (int it = 0; it < 8; ++it) rx[it] = *reinterpret_cast<const u32x4*>(xs + 8 * (l + 64 * it));   // channel q >> 2, chunk q & 3
-    const bool live = j < N;
-    rt_load(zin + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
   };
+  if (t < total) fetch_x(t);
   for (; t < total; t += stride) {
     const RtTile tl = rt_tile(t, per_b, tpr);
     const int64_t b = tl.b, i = tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
     const int64_t pix = (b * N + i) * N + j;
-    fetch(t);
+    rt_load(zin + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
       const int q = l + 64 * it, c = q >> 2, p0 = (q & 3) * 8;
@@ -347,6 +346,7 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
       }
     }
     rt_wave_lds_sync();
+    if (t + stride < total) fetch_x(t + stride);            // the next tile's X lands while this one computes
     u32x4 xr[8];
 #pragma unroll
     for (int tt = 0; tt < 8; ++tt) xr[tt] = *reinterpret_cast<const u32x4*>(&sx[n * K3_XLD + 8 * rt_chunk(tt, g)]);
@@ -356,7 +356,7 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
     __builtin_amdgcn_sched_barrier(0);      // one LayerNorm's temporaries at a time
     rt_ln(rz, g, sLNi, eps, xi);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll 1
+#pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       const f32x16 o = rt_gemm32(sW, cb * 32, n, g, xo);
       const f32x16 gt = rt_gemm32(sW + RT_C * RT_LD, cb * 32, n, g, xi);
@@ -371,7 +371,7 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
       for (int h2 = 0; h2 < 2; ++h2) {
         const int64_t c0 = pix * RT_C + cb * 32 + 16 * h2 + 8 * g;
         if (residual) {
-          const u32x4 r = *reinterpret_cast<const u32x4*>(zin + c0);
+          const u32x4 r = rz[2 * cb + h2];                  // z rows chunk 2cb + h2: channels cb*32 + 16 h2 + 8g .. +7
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             y[8 * h2 + 2 * e] += lo_bf(r[e]);
