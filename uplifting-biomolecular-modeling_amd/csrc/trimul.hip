@@ -183,11 +183,20 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 // ---------------------------------------------------------------------------------------------------------------- contraction, 256 x 256 tiles
 // For planes padded to a multiple of 256: a workgroup (4 waves, one per SIMD) computes a 256 x 256 tile of X, each wave a
 // 128 x 128 quarter in 16 accumulators.  The A and B k-slabs (256 rows x 32 k each) go straight from global memory into LDS
-// (global_load_lds_dwordx4: no VGPR staging), three slabs in the ring so the loads of slab k + 2 overlap the MFMAs of slab
-// k; within a slab row the four 16-byte chunks are XOR-swizzled by (row >> 2) & 3, so the fragment reads of 16 consecutive
-// rows land on 16 distinct bank groups.  The MFMA runs with the operands exchanged (D = B A^T): lane = row i, registers =
+// (global_load_lds_dwordx4: no VGPR staging) through a ring of CB_NBUF buffers with CB_IF slabs in flight, so each slab's
+// loads have CB_IF - 1 slabs of MFMAs to land behind (a fifth buffer, the whole 160 KB of LDS, measured no faster); within
+// a slab row the four 16-byte chunks are XOR-swizzled by (row >> 2) & 3, so the fragment reads of 16 consecutive rows land
+// on 16 distinct bank groups.  The MFMA runs with the operands exchanged (D = B A^T): lane = row i, registers =
 // 16 columns j, and after the half-wave lane exchange each lane stores 8 consecutive columns per 16-byte store.
-constexpr int CB_T = 256, CB_K = 32, CB_NBUF = 4;
+constexpr int CB_T = 256, CB_K = 32, CB_NBUF = 4, CB_IF = CB_NBUF - 1;
+
+// waits until at most p slabs (8 transfers of this wave each) are outstanding
+__device__ __forceinline__ void cb_wait(int p) {
+  if (p >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+  else if (p == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (p == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t nbatch) {
@@ -238,29 +247,25 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
         fb[ks][s4] = as_bf8(*reinterpret_cast<const u32x4*>(pb + frag_off(wc + 32 * s4 + n, 2 * ks + g)));
       }
   };
-  // ring: slab k lives in buffer k % 4, three slabs in flight.  Iteration kt issues slab kt + 3, runs 8 of slab kt's 32
-  // MFMAs, waits for slab kt + 1 at the barrier (the matrix core keeps working), then reads slab kt + 1's 16 fragments
-  // ahead of the other 24 MFMAs.
-  issue(0, 0);
-  if (nk > 1) issue(1, CB_K);
-  if (nk > 2) issue(2, 2 * CB_K);
-  if (nk > 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if (nk > 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // ring: slab k lives in buffer k % CB_NBUF, CB_IF slabs in flight.  Iteration kt issues slab kt + CB_IF, runs 8 of slab
+  // kt's 32 MFMAs, waits for slab kt + 1 at the barrier (the matrix core keeps working), then reads slab kt + 1's 16
+  // fragments ahead of the other 24 MFMAs.
+  for (int s = 0; s < CB_IF && s < nk; ++s) issue(s, (int64_t)s * CB_K);
+  cb_wait((nk < CB_IF ? nk : CB_IF) - 1);
   __builtin_amdgcn_s_barrier();
-  bf16x8 fa[2][4], fb[2][4], na[2][4], nb[2][4];
-  read_frags(0, fa, fb);
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 3 < nk) issue((kt + 3) % CB_NBUF, (int64_t)(kt + 3) * CB_K);   // its buffer held slab kt - 1, read before the last barrier
+  // two fragment sets that trade roles every slab (no register copies between slabs: a copy into registers the queued
+  // MFMAs still read would hold the wave until those MFMAs start)
+  bf16x8 f0a[2][4], f0b[2][4], f1a[2][4], f1b[2][4];
+  read_frags(0, f0a, f0b);
+  auto slab = [&](int kt, const bf16x8 (&fa)[2][4], const bf16x8 (&fb)[2][4], bf16x8 (&na)[2][4], bf16x8 (&nb)[2][4]) {
+    if (kt + CB_IF < nk) issue((kt + CB_IF) % CB_NBUF, (int64_t)(kt + CB_IF) * CB_K);   // its buffer held slab kt - 1, read before the last barrier
 #pragma unroll
     for (int si = 0; si < 4; ++si)
 #pragma unroll
       for (int sj = 0; sj < 2; ++sj) acc[si][sj] = mfma32(fb[0][sj], fa[0][si], acc[si][sj]);
     __builtin_amdgcn_sched_barrier(0);
     if (kt + 1 < nk) {                                   // slab kt + 1 landed: at most the later slabs' transfers outstanding
-      if (kt + 3 < nk) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-      else if (kt + 2 < nk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      cb_wait(nk - 2 - kt < CB_IF - 1 ? nk - 2 - kt : CB_IF - 1);
       __builtin_amdgcn_s_barrier();
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -274,13 +279,10 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
 #pragma unroll
       for (int sj = 0; sj < 4; ++sj) acc[si][sj] = mfma32(fb[1][sj], fa[1][si], acc[si][sj]);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        fa[ks][s4] = na[ks][s4];
-        fb[ks][s4] = nb[ks][s4];
-      }
+  };
+  for (int kt = 0; kt < nk; kt += 2) {                   // nk is even: Np is a multiple of 256
+    slab(kt, f0a, f0b, f1a, f1b);
+    slab(kt + 1, f1a, f1b, f0a, f0b);
   }
 #pragma unroll
   for (int si = 0; si < 4; ++si)
