@@ -8,7 +8,8 @@ Step = one pair block on a resident z [1, N, N, 128] bf16, in place, in the refe
 tri-att starting node, tri-att ending node, transition 4x): 13 launches of libfpf_hip on torch's current stream.  Synthetic
 z ~ N(0,1) and random-init weights N(0, 1/fan_in) (seed 0), pair mask all ones, inputs resident in HBM before timing.
 Prints ONE JSON line (the driver's contract) with the dominant kernel's roofline (timed live with HIP events on the launch
-stream) and the stock PyTorch CPU statement timed on this host (a reported baseline, not the target).
+stream) and the stock PyTorch CPU statement timed on this host (a reported baseline, not the target).  The `trunk` field is
+BASELINE config 3 (a 48-layer Pairformer trunk at N = 512, pair and single tracks; --trunk-layers 0 skips it).
 """
 import argparse
 import json
@@ -33,6 +34,36 @@ def block_flops(N, C=128, CH=128, H=4, D=32, factor=4):
     ta = 2 * N * N * C * (4 * HD + H) + ta_core + 2 * N * N * HD * C
     tr = 2 * N * N * 3 * factor * C * C
     return {"trimul": tm, "triatt": ta, "triatt_core": ta_core, "transition": tr, "block": 2 * tm + 2 * ta + tr}
+
+
+def single_flops(N, c_s=384, c_z=128, heads=16, factor=4):
+    """Algorithmic FLOPs of one layer's single track: projections q|k|v|g|o 10 N c_s^2, attention 4 N^2 c_s, pair-bias producer
+    2 N^2 c_z H, transition 6 factor N c_s^2."""
+    return 10 * N * c_s * c_s + 4 * N * N * c_s + 2 * N * N * c_z * heads + 6 * factor * N * c_s * c_s
+
+
+def trunk(torch, dev, layers, N=512, reps=2):
+    """BASELINE config 3: a Pairformer trunk of ``layers`` layers at N tokens (pair track bf16, c_z = 128, 4 x 32 triangle heads;
+    single track fp32, c_s = 384, 16 heads x 24), random-init weights per layer (seeds 1000 + l), s, z ~ N(0, 1), masks all ones.
+    One warm-up pass, then the mean of ``reps`` passes, HIP events on the current stream."""
+    from fpf_hip import pairformer as PFM
+    stack = [(PFM.PairBlock(PFM.random_params(seed=1000 + l), dev, torch.bfloat16),
+              PFM.SingleBlock(PFM.random_single_params(seed=2000 + l), dev)) for l in range(layers)]
+    g = torch.Generator().manual_seed(3)
+    z0 = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(dev)
+    s0 = torch.randn(1, N, 384, generator=g).to(dev)
+    mask = torch.ones(1, N, device=dev)
+    pmask = torch.ones(1, N, N, device=dev)
+
+    def run():
+        z = z0.clone()
+        return PFM.pairformer_trunk(s0, z, mask, pmask, stack)
+    run()
+    t = time_events(run, reps, torch)
+    fl = layers * (block_flops(N)["block"] + single_flops(N))
+    return {"layers": layers, "N": N, "ms": round(t, 3), "tflop": round(fl / 1e12, 3), "tflops": round(fl / (t * 1e-3) / 1e12, 1),
+            "mfma_frac": round(fl / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "ms_per_layer": round(t / layers, 4),
+            "workload": "BASELINE config 3: %d-layer Pairformer trunk, pair track bf16 + single track fp32 (c_s 384, 16 x 24 heads)" % layers}
 
 
 def time_events(fn, reps, torch):
@@ -150,6 +181,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--n", type=int, default=768)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--trunk-layers", type=int, default=48, help="BASELINE config-3 trunk leg (0: skip)")
     ap.add_argument("--probe", default=None, help="launch-only run for counter passes: triattn_core | copy")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -238,6 +270,9 @@ def main():
                       "c_z": 128, "c_hidden": 128, "heads": 4, "head_dim": 32, "batch": 1, "mask": "all ones",
                       "block_tflop": round(fl["block"] / 1e12, 4), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
            "roofline": roof, "breakdown": breakdown}
+    if a.trunk_layers > 0:
+        del keep, zb, yln
+        out["trunk"] = trunk(torch, dev, a.trunk_layers)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(out), flush=True)

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 2
+#define FPF_ABI_VERSION 3   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
 enum {
@@ -68,7 +68,7 @@ int fpf_layernorm_fwd(const FpfLnArgs* a, void* stream, char* err, size_t errlen
 typedef struct {
   int32_t abi_version;
   int32_t dtype;           /* FPF_DT_BF16 (x, out, w_* bf16) | FPF_DT_F32 (all fp32) */
-  int32_t c;               /* bf16: 128; fp32: any multiple of 4 <= 256 */
+  int32_t c;               /* bf16: 128; fp32: any <= 384 */
   int32_t hidden;          /* bf16: multiple of 32; fp32: any */
   int64_t rows;
   const void* x;           /* [rows, c] contiguous */
@@ -247,6 +247,57 @@ typedef struct {
   void* out;               /* [B, N, N, C] in z's frame */
 } FpfTriattnEpilogueArgs;
 int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* stream, char* err, size_t errlen);
+
+/* ---------------------------------------------------------------------------------------------------------------- attention with a pair bias
+ * The single track's attention (and a sample batch's token attention sharing one bias):
+ * out[s,n,h,:] = sigmoid(gate[s,n,h,:]) * softmax_m(scale q[s,n,h,:].k[s,m,h,:] + bias[s|0,h,n,m], keys with key_mask[s|0,m] == 0
+ *                excluded) @ v[s,m,h,:]; a sample whose keys are all masked gives the uniform mean of v over all keys.
+ * fp32 arithmetic for fp32 or bf16 storage.
+ * Replaces: common/opt_core/opt_core/attn/apb_core.py:89 pair_bias_attention (its "rows" and "shnd" layouts are strided views
+ * of [S, N, H, D] here); the stock statement is boltz2/stock/src/boltz/model/layers/attentionv2.py:98-111. */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* q / k / v / gate / out: FPF_DT_F32 | FPF_DT_BF16 */
+  int64_t S, N, NK, H, D;  /* samples, queries, keys, heads, head_dim (16 | 24 | 32 | 48 | 64) */
+  const void* q;           /* [S, N, H, D] element strides below, stride[3] = 1 */
+  const void* k;           /* [S, NK, H, D] */
+  const void* v;           /* [S, NK, H, D] */
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  const void* gate;        /* [S, N, H, D] pre-sigmoid, or NULL (no gate) */
+  int64_t gate_stride[4];
+  const void* bias;        /* [SB, H, N, NK]: stride[0] = 0 shares one plane across the samples */
+  int32_t bias_dtype;      /* FPF_DT_F32 | FPF_DT_BF16 */
+  int64_t bias_stride[4];  /* stride[3] = 1 */
+  const void* key_mask;    /* [S | 1, NK] nonzero = attend, or NULL */
+  int32_t mask_dtype;      /* FPF_DT_U8 | FPF_DT_F32 */
+  int64_t mask_stride[2];  /* stride[0] = 0 shares one mask across the samples */
+  void* out;               /* [S, N, H, D] */
+  int64_t out_stride[4];
+  float scale;             /* > 0 (the face passes head_dim ** -0.5 by default) */
+} FpfApbArgs;
+int fpf_apb_fwd(const FpfApbArgs* a, void* stream, char* err, size_t errlen);
+
+/* The pair-bias producer: bias[b, h, i, j] = LN(z[b, i, j, :]) . w_z[h, :] over every pixel (fp32 LayerNorm statistics, the
+ * normalised row rounded to bf16, fp32 accumulation), head-major with a row pitch, fp32 or bf16.
+ * Replaces: the `producer` boundary of common/opt_core/opt_core/kernels/apb (DESIGN.md:5-7); the stock statement is the
+ * proj_z of boltz2/stock/src/boltz/model/layers/attentionv2.py:53-58 (LayerNorm(c_z) -> Linear(c_z, H, bias=False) -> heads first). */
+typedef struct {
+  int32_t abi_version;
+  int32_t dtype;           /* z: FPF_DT_BF16 */
+  int64_t B, N;
+  int32_t C, H;            /* C = 128, 1 <= H <= 32 */
+  const void* z;           /* [B, N, N, C] contiguous */
+  const float* ln_w;       /* [C] or NULL (1) */
+  const float* ln_b;       /* [C] or NULL (0) */
+  float eps;
+  const void* w_z;         /* [H, C] bf16 */
+  void* bias;              /* [B, H, N, bias_ld] out */
+  int32_t bias_dtype;      /* FPF_DT_F32 | FPF_DT_BF16 */
+  int64_t bias_ld;         /* >= N; <= 0 means N */
+} FpfApbBiasArgs;
+int fpf_apb_bias_fwd(const FpfApbBiasArgs* a, void* stream, char* err, size_t errlen);
 
 #ifdef __cplusplus
 }

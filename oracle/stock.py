@@ -19,13 +19,22 @@ Reference statements followed (paths under the reference tree):
     triatt_prologue /     common/opt_core/opt_core/attn/pair_fused.py:1136-1233 (q,k,v [B,I,H,J,D], g [B,I,J,HD] pre-sigmoid,
     triatt_epilogue       bias [B,1,H,I,J] in the attention frame) and :1416-1498 (u = (sigmoid(g) o) W_o^T, residual into z,
                           transposed scatter for the ending node)
+    pair_bias_attention_op common/opt_core/opt_core/attn/apb_core.py:1-12 (op contract: shared or per-sample bias, key mask,
+                          sigmoid gate; a sample whose keys are all masked is uniform over all keys)
+    pair_bias             boltz2/stock/src/boltz/model/layers/attentionv2.py:53-58 (proj_z: LayerNorm(c_z) -> Linear(c_z, H) ->
+                          heads first)
+    attention_pair_bias   attentionv2.py:62-111 (AttentionPairBias forward, compute_pair_bias=True: q with bias, k / v / g
+                          without, fp32 softmax with the additive (1 - mask) * -inf key mask, sigmoid gate, proj_o)
+    single_track /        boltz2/stock/src/boltz/model/layers/pairformer.py:104-111 (pre_norm_s, s += attention(s_n, z, mask,
+    pairformer_layer      k_in = s_n), s += transition_s(s); post norm = identity) after the pair stack :75-102
 """
 import math
 
 import torch
 
 __all__ = ["layer_norm", "triangle_attention_op", "tri_attn", "triatt_prologue", "triatt_epilogue", "trimul", "trimul_rows",
-           "tri_attn_rows", "transition", "pair_block", "make_block_params", "block_flops"]
+           "tri_attn_rows", "transition", "pair_block", "make_block_params", "block_flops", "pair_bias_attention_op", "pair_bias",
+           "attention_pair_bias", "single_track", "pairformer_layer", "make_single_params", "single_flops"]
 
 
 def layer_norm(x, w=None, b=None, eps=1e-5):
@@ -282,3 +291,96 @@ def block_flops(n, c_z=128, c_h=128, heads=4, head_dim=32, factor=4):
     tr = 2 * N * N * 3 * factor * c_z * c_z
     return {"trimul": tm, "triatt": ta_pro + ta_core + ta_epi, "triatt_core": ta_core, "triatt_prologue": ta_pro,
             "triatt_epilogue": ta_epi, "transition": tr, "block": 2 * tm + 2 * (ta_pro + ta_core + ta_epi) + tr}
+
+
+# ---------------------------------------------------------------------------------------------------------------- single track
+def pair_bias_attention_op(q, k, v, bias, key_mask=None, gate=None, scale=None, dtype=torch.float64):
+    """out[s,n,h,:] = sigmoid(gate[s,n,h,:]) * softmax_m(scale q[s,n,h].k[s,m,h] + bias[s|0,h,n,m], masked keys excluded) @ v[s,m,h].
+    q [S,N,H,D], k / v [S,NK,H,D], bias [H,N,NK] or [SB,H,N,NK] (SB in {1, S}), key_mask [NK] / [S|1,NK] (nonzero = attend) or None,
+    gate [S,N,H,D] or None.  A sample whose keys are all masked attends uniformly to every key (apb_core.py:1-12).
+    Pinned by: brute-force scalar loops, key-permutation equivariance, a shared bias equals the per-sample copy, S = 1 with one key
+    -> v (tests/test_oracle.py)."""
+    S, N, H, D = q.shape
+    NK = k.shape[1]
+    sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
+    b = bias.to(dtype)
+    if b.dim() == 3:
+        b = b.unsqueeze(0)
+    logits = torch.einsum("snhd,smhd->shnm", q.to(dtype), k.to(dtype)) * sc + b          # [S, H, N, NK]
+    if key_mask is not None:
+        km = key_mask.reshape(-1, NK).to(torch.bool)
+        km = km.expand(S, NK)
+        dead = ~km.any(dim=-1)                                                          # [S]
+        keep = km | dead[:, None]
+        logits = logits.masked_fill(~keep[:, None, None, :], float("-inf"))
+        logits = torch.where(dead[:, None, None, None], torch.zeros_like(logits), logits)
+    p = torch.softmax(logits, dim=-1)
+    o = torch.einsum("shnm,smhd->snhd", p, v.to(dtype))
+    if gate is not None:
+        o = o * torch.sigmoid(gate.to(dtype))
+    return o
+
+
+def pair_bias(z, ln_w, ln_b, w_z, *, eps=1e-5, dtype=torch.float64):
+    """bias[b, h, i, j] = LayerNorm(z[b, i, j, :]) . w_z[h, :] (attentionv2.py:53-58).  z [B,N,N,C] -> [B,H,N,N]."""
+    zz = _as4(z)[0].to(dtype)
+    return torch.matmul(layer_norm(zz, ln_w, ln_b, eps), w_z.to(dtype).t()).permute(0, 3, 1, 2)
+
+
+def attention_pair_bias(s, z, mask, P, *, dtype=torch.float64, inf=1e6, eps=1e-5):
+    """AttentionPairBias.forward (attentionv2.py:62-111) with k_in = s: q = s W_q^T + b_q, k = s W_k^T, v = s W_v^T, g = sigmoid(s W_g^T),
+    bias = proj_z(z), attn = softmax_j(q.k / sqrt(D) + bias + (1 - mask[b, j]) * -inf), out = (g * (attn v)) W_o^T.
+    s [B,N,c_s] (already normalised by the caller), z [B,N,N,c_z], mask [B,N] token mask."""
+    ss = s.to(dtype)
+    B, N, CS = ss.shape
+    H = int(P["H"])
+    D = CS // H
+    q = (torch.matmul(ss, P["w_q"].to(dtype).t()) + P["b_q"].to(dtype)).view(B, N, H, D)
+    k = torch.matmul(ss, P["w_k"].to(dtype).t()).view(B, N, H, D)
+    v = torch.matmul(ss, P["w_v"].to(dtype).t()).view(B, N, H, D)
+    bias = pair_bias(z, P["ln_z_w"], P["ln_z_b"], P["w_z"], eps=eps, dtype=dtype)
+    g = torch.sigmoid(torch.matmul(ss, P["w_g"].to(dtype).t()))
+    attn = torch.einsum("bihd,bjhd->bhij", q, k) / math.sqrt(D) + bias
+    attn = attn + (1 - mask.to(dtype)[:, None, None, :]) * -inf
+    attn = torch.softmax(attn, dim=-1)
+    o = torch.einsum("bhij,bjhd->bihd", attn, v).reshape(B, N, CS)
+    return torch.matmul(g * o, P["w_o"].to(dtype).t())
+
+
+def single_track(s, z, mask, P, *, dtype=torch.float64, eps=1e-5):
+    """The sequence stack of PairformerLayer.forward (pairformer.py:104-111, autocast off, post norm identity): s_n = LN_s(s);
+    s += attention(s_n, z, mask, k_in = s_n); s += transition_s(s).  ``P`` = make_single_params(...)["apb"|"trs"] merged."""
+    ss = s.to(dtype)
+    a = P["apb"]
+    sn = layer_norm(ss, a["ln_s_w"], a["ln_s_b"], eps)
+    ss = ss + attention_pair_bias(sn, z, mask, a, dtype=dtype, eps=eps)
+    t = P["trs"]
+    return ss + transition(ss, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"], eps=eps, dtype=dtype)
+
+
+def pairformer_layer(s, z, mask, pair_mask, params, *, dtype=torch.float64):
+    """One PairformerLayer (pairformer.py:75-111, eval): the pair stack updates z, then the single track reads the updated z.
+    Returns (s, z)."""
+    z = pair_block(z, pair_mask, params, dtype=dtype)
+    return single_track(s, z, mask, params["single"], dtype=dtype), z
+
+
+def make_single_params(c_s=384, c_z=128, heads=16, factor=4, seed=0):
+    """Single-track weights of one layer (N(0, 1/fan_in), LayerNorm 1 / 0, proj_q bias 0) in module order
+    (pre_norm_s, proj_q, proj_k, proj_v, proj_g, proj_z, proj_o, transition_s).  fp32 CPU tensors."""
+    g = torch.Generator("cpu").manual_seed(seed)
+
+    def lin(o, i):
+        return torch.randn(o, i, generator=g, dtype=torch.float32) / math.sqrt(i)
+    apb = {"H": heads, "ln_s_w": torch.ones(c_s), "ln_s_b": torch.zeros(c_s), "w_q": lin(c_s, c_s), "b_q": torch.zeros(c_s),
+           "w_k": lin(c_s, c_s), "w_v": lin(c_s, c_s), "w_g": lin(c_s, c_s), "ln_z_w": torch.ones(c_z), "ln_z_b": torch.zeros(c_z),
+           "w_z": lin(heads, c_z), "w_o": lin(c_s, c_s)}
+    hid = factor * c_s
+    trs = {"ln_w": torch.ones(c_s), "ln_b": torch.zeros(c_s), "w_a": lin(hid, c_s), "w_b": lin(hid, c_s), "w_o": lin(c_s, hid)}
+    return {"apb": apb, "trs": trs}
+
+
+def single_flops(n, c_s=384, c_z=128, heads=16, factor=4):
+    """Algorithmic FLOPs of one layer's single track: projections q|k|v|g|o 10 N c_s^2, attention 4 N^2 c_s, pair-bias producer
+    2 N^2 c_z H, transition 6 factor N c_s^2."""
+    return 10 * n * c_s * c_s + 4 * n * n * c_s + 2 * n * n * c_z * heads + 6 * factor * n * c_s * c_s

@@ -40,7 +40,7 @@ def test_header_declares_the_entry_points():
     d = _declared()
     for must in ("fpf_abi_version", "fpf_describe", "fpf_layernorm_fwd", "fpf_transition_fwd", "fpf_trimul_fwd", "fpf_trimul_workspace_bytes",
                  "fpf_triattn_fwd", "fpf_triattn_block_fwd", "fpf_triattn_block_workspace_bytes", "fpf_triattn_prologue_fwd",
-                 "fpf_triattn_epilogue_fwd", "fpf_triattn_bias_fwd"):
+                 "fpf_triattn_epilogue_fwd", "fpf_triattn_bias_fwd", "fpf_apb_fwd", "fpf_apb_bias_fwd"):
         assert must in d, must
 
 
@@ -61,7 +61,8 @@ def test_ctypes_blocks_follow_the_header_field_order():
     st = _structs()
     pairs = {"FpfLnArgs": L.LnArgs, "FpfTransitionArgs": L.TransitionArgs, "FpfTrimulArgs": L.TrimulArgs, "FpfTriattnArgs": L.TriattnArgs,
              "FpfTriattnBlockArgs": L.TriattnBlockArgs, "FpfTriattnPrologueArgs": L.TriattnPrologueArgs,
-             "FpfTriattnEpilogueArgs": L.TriattnEpilogueArgs, "FpfTriattnBiasArgs": L.TriattnBiasArgs}
+             "FpfTriattnEpilogueArgs": L.TriattnEpilogueArgs, "FpfTriattnBiasArgs": L.TriattnBiasArgs, "FpfApbArgs": L.ApbArgs,
+             "FpfApbBiasArgs": L.ApbBiasArgs}
     assert set(pairs) == set(st), sorted(st)
     for cname, py in pairs.items():
         assert [f[0] for f in py._fields_] == st[cname], cname
@@ -92,4 +93,17 @@ def test_version_mismatch_is_refused_before_any_launch():
     a = L.TrimulArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, c_z=128, c_h=128, batch=1, n=8)
     with pytest.raises(L.LibError) as e:
         L.call("fpf_trimul_fwd", a, None)                  # NULL z / weights
+    assert e.value.kind == "args"
+
+
+def test_apb_refusals_need_no_device():
+    """The attention-with-pair-bias gate refuses NULL operands and unserved head dims by name (nothing is launched)."""
+    from fpf_hip import _lib as L
+    a = L.ApbArgs(abi_version=L.ABI_VERSION, dtype=L.DT_F32, S=1, N=8, NK=8, H=2, D=24)
+    with pytest.raises(L.LibError) as e:
+        L.call("fpf_apb_fwd", a, None)
+    assert e.value.kind == "args"
+    b = L.ApbBiasArgs(abi_version=L.ABI_VERSION, dtype=L.DT_F32, B=1, N=8, C=128, H=16)
+    with pytest.raises(L.LibError) as e:
+        L.call("fpf_apb_bias_fwd", b, None)
     assert e.value.kind == "args"

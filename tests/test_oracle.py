@@ -355,3 +355,126 @@ def test_tri_attn_rows_equal_the_full_statement():
         full = S.triatt_epilogue(S.triangle_attention_op(q, k, v, bias, mx), gg, P)[0]
         part = S.tri_attn_rows(z, P, mask, rows, ending=ending, dtype=torch.float64)
         assert torch.allclose(part, full[rows], atol=1e-12), ending
+
+
+# ----------------------------------------------------------------------------------------------------------------- single track
+def _apb_brute(q, k, v, bias, key_mask, gate, scale):
+    """Scalar loops over the published op (common/opt_core/opt_core/attn/apb_core.py:7): per (s, h, n) the logits of the kept keys,
+    a max-shifted exponential, the weighted mean of v, then the sigmoid gate; a sample with no kept key weighs every key 1."""
+    S_, N, H, D = q.shape
+    NK = k.shape[1]
+    out = torch.zeros(S_, N, H, D, dtype=torch.float64)
+    for s in range(S_):
+        keep = [True] * NK if key_mask is None else [bool(key_mask[s if key_mask.shape[0] > 1 else 0, j]) for j in range(NK)]
+        dead = not any(keep)
+        bs = s if bias.shape[0] > 1 else 0
+        for h in range(H):
+            for n in range(N):
+                lg = []
+                for j in range(NK):
+                    if dead:
+                        lg.append(0.0)
+                    elif not keep[j]:
+                        lg.append(None)
+                    else:
+                        dot = sum(float(q[s, n, h, d]) * float(k[s, j, h, d]) for d in range(D))
+                        lg.append(dot * scale + float(bias[bs, h, n, j]))
+                mx = max(x for x in lg if x is not None)
+                w = [math.exp(x - mx) if x is not None else 0.0 for x in lg]
+                tot = sum(w)
+                for d in range(D):
+                    o = sum(w[j] * float(v[s, j, h, d]) for j in range(NK)) / tot
+                    if gate is not None:
+                        o /= 1.0 + math.exp(-float(gate[s, n, h, d]))
+                    out[s, n, h, d] = o
+    return out
+
+
+def _apb_case(seed, S_=2, N=5, NK=7, H=2, D=3, per_sample=False):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(S_, n_, H, D, generator=g, dtype=torch.float64) for n_ in (N, NK, NK))
+    bias = torch.randn(S_ if per_sample else 1, H, N, NK, generator=g, dtype=torch.float64)
+    gate = torch.randn(S_, N, H, D, generator=g, dtype=torch.float64)
+    return q, k, v, bias, gate
+
+
+@pytest.mark.parametrize("per_sample", [False, True])
+def test_pair_bias_attention_op_matches_brute_force(per_sample):
+    q, k, v, bias, gate = _apb_case(3, per_sample=per_sample)
+    mask = torch.tensor([[1, 0, 1, 1, 0, 1, 1], [0, 0, 0, 0, 0, 0, 0]])      # sample 1: every key masked -> uniform
+    for km, gt in ((None, None), (mask, gate), (mask[:1], None)):
+        ref = _apb_brute(q, k, v, bias, km, gt, 0.7)
+        out = S.pair_bias_attention_op(q, k, v, bias, km, gt, scale=0.7)
+        assert torch.allclose(out, ref, rtol=0, atol=1e-12)
+    dead = S.pair_bias_attention_op(q, k, v, bias, mask, None)[1]
+    assert torch.allclose(dead, v[1].mean(dim=0, keepdim=True).expand_as(dead), atol=1e-12)
+
+
+def test_pair_bias_attention_op_invariants():
+    q, k, v, bias, gate = _apb_case(5, S_=3, N=6, NK=9, H=3, D=4)
+    mask = (torch.arange(9) % 3 != 1).reshape(1, 9)
+    ref = S.pair_bias_attention_op(q, k, v, bias, mask, gate)
+    perm = torch.randperm(9, generator=torch.Generator().manual_seed(2))
+    out = S.pair_bias_attention_op(q, k[:, perm], v[:, perm], bias[..., perm], mask[:, perm], gate)
+    assert torch.allclose(out, ref, atol=1e-12)                                # key-permutation equivariance
+    out = S.pair_bias_attention_op(q, k, v, bias.expand(3, -1, -1, -1).clone(), mask, gate)
+    assert torch.allclose(out, ref, atol=1e-12)                                # shared bias == per-sample copies
+    one = S.pair_bias_attention_op(q, k[:, :1], v[:, :1], bias[..., :1], None, None)
+    assert torch.allclose(one, v[:, :1].expand_as(one), atol=1e-12)            # one key -> v
+
+
+def test_pair_bias_matches_library_layer_norm():
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(2, 5, 5, 128, generator=g, dtype=torch.float64)
+    w, b = torch.randn(128, generator=g, dtype=torch.float64), torch.randn(128, generator=g, dtype=torch.float64)
+    wz = torch.randn(16, 128, generator=g, dtype=torch.float64)
+    ref = (F.layer_norm(z, (128,), w, b, 1e-5) @ wz.t()).permute(0, 3, 1, 2)
+    assert torch.allclose(S.pair_bias(z, w, b, wz), ref, atol=1e-12)
+
+
+def _single_params(seed=0, c_s=48, heads=4):
+    P = S.make_single_params(c_s=c_s, heads=heads, seed=seed)
+    for key in ("ln_s_w", "ln_s_b", "b_q", "ln_z_w", "ln_z_b"):
+        P["apb"][key] = torch.randn(P["apb"][key].shape, generator=torch.Generator().manual_seed(seed + 7))
+    return P
+
+
+def test_attention_pair_bias_equals_the_op_composition():
+    """The module statement equals the op on its own projections (the op is pinned by brute force above)."""
+    P = _single_params(1)["apb"]
+    g = torch.Generator().manual_seed(9)
+    s = torch.randn(2, 6, 48, generator=g, dtype=torch.float64)
+    z = torch.randn(2, 6, 6, 128, generator=g, dtype=torch.float64)
+    mask = torch.tensor([[1, 1, 1, 0, 1, 0], [1, 0, 1, 1, 1, 1]], dtype=torch.float64)
+    out = S.attention_pair_bias(s, z, mask, P)
+    H, D = 4, 12
+    q = (s @ P["w_q"].double().t() + P["b_q"].double()).view(2, 6, H, D)
+    k = (s @ P["w_k"].double().t()).view(2, 6, H, D)
+    v = (s @ P["w_v"].double().t()).view(2, 6, H, D)
+    gt = (s @ P["w_g"].double().t()).view(2, 6, H, D)
+    bias = S.pair_bias(z, P["ln_z_w"], P["ln_z_b"], P["w_z"])
+    for b in range(2):
+        o = S.pair_bias_attention_op(q[b:b + 1], k[b:b + 1], v[b:b + 1], bias[b:b + 1], mask[b:b + 1], gt[b:b + 1])
+        ref = o.reshape(6, 48) @ P["w_o"].double().t()
+        assert torch.allclose(out[b], ref, atol=1e-10)
+
+
+def test_attention_pair_bias_closed_forms():
+    P = _single_params(2)["apb"]
+    g = torch.Generator().manual_seed(10)
+    s = torch.randn(1, 1, 48, generator=g, dtype=torch.float64)                 # one token: softmax over one key = 1
+    z = torch.randn(1, 1, 1, 128, generator=g, dtype=torch.float64)
+    ref = (torch.sigmoid(s @ P["w_g"].double().t()) * (s @ P["w_v"].double().t())) @ P["w_o"].double().t()
+    assert torch.allclose(S.attention_pair_bias(s, z, torch.ones(1, 1), P), ref, atol=1e-12)
+    P0 = dict(P, w_o=torch.zeros(48, 48))
+    s3 = torch.randn(1, 4, 48, generator=g, dtype=torch.float64)
+    assert torch.count_nonzero(S.attention_pair_bias(s3, torch.randn(1, 4, 4, 128, generator=g), torch.ones(1, 4), P0)) == 0
+
+
+def test_single_track_with_zero_outputs_is_identity():
+    P = _single_params(3)
+    P["apb"]["w_o"] = torch.zeros(48, 48)
+    P["trs"]["w_o"] = torch.zeros(48, 4 * 48)
+    g = torch.Generator().manual_seed(11)
+    s = torch.randn(1, 5, 48, generator=g, dtype=torch.float64)
+    assert torch.equal(S.single_track(s, torch.randn(1, 5, 5, 128, generator=g), torch.ones(1, 5), P), s)

@@ -178,16 +178,18 @@ __global__ void __launch_bounds__(64 * NW) transition_bf16_kernel(const uint16_t
 // ---------------------------------------------------------------------------------------------------------------- fp32 (exact tier)
 constexpr int TF_R = 32;    // rows per workgroup
 constexpr int TF_HC = 16;   // hidden per chunk
-constexpr int TF_CM = 128;  // max c
+constexpr int TF_CM = 384;  // max c (the single track's c_s; the pair track's 128 takes the narrow instance)
 
+// CM: the widest c an instance serves (LDS tiles [TF_R][CM + 1] of x and [TF_HC][CM + 1] of W_a, W_b)
+template <int CM>
 __global__ void __launch_bounds__(256) transition_f32_kernel(const float* x, float* out, const float* __restrict__ ln_w,
                                                              const float* __restrict__ ln_b, float eps, const float* __restrict__ wa,
                                                              const float* __restrict__ wb, const float* __restrict__ wo,
                                                              const float* __restrict__ mask, int residual, int64_t rows, int c, int hidden) {
-  __shared__ float xs[TF_R][TF_CM + 1];
-  __shared__ float was[TF_HC][TF_CM + 1];
-  __shared__ float wbs[TF_HC][TF_CM + 1];
-  __shared__ float wos[TF_CM][TF_HC + 1];
+  __shared__ float xs[TF_R][CM + 1];
+  __shared__ float was[TF_HC][CM + 1];
+  __shared__ float wbs[TF_HC][CM + 1];
+  __shared__ float wos[CM][TF_HC + 1];
   __shared__ float hs[TF_R][TF_HC + 1];
   const int tid = threadIdx.x;
   const int r = tid >> 3, sub = tid & 7;   // 8 threads per row
@@ -210,9 +212,9 @@ __global__ void __launch_bounds__(256) transition_f32_kernel(const float* x, flo
     const float v = live ? x[row * c + cc] : 0.f;
     xs[r][cc] = (v - mean) * rstd * (ln_w ? ln_w[cc] : 1.f) + (ln_b ? ln_b[cc] : 0.f);
   }
-  float acc[TF_CM / 8];
+  float acc[CM / 8];
 #pragma unroll
-  for (int i = 0; i < TF_CM / 8; ++i) acc[i] = 0.f;
+  for (int i = 0; i < CM / 8; ++i) acc[i] = 0.f;
   for (int h0 = 0; h0 < hidden; h0 += TF_HC) {
     const int hc = min(TF_HC, hidden - h0);
     __syncthreads();
@@ -237,7 +239,7 @@ __global__ void __launch_bounds__(256) transition_f32_kernel(const float* x, flo
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < TF_CM / 8; ++i) {
+    for (int i = 0; i < CM / 8; ++i) {
       const int cc = sub + 8 * i;
       if (cc < c) {
         float a2 = acc[i];
@@ -249,7 +251,7 @@ __global__ void __launch_bounds__(256) transition_f32_kernel(const float* x, flo
   if (!live) return;
   const float m = mask ? mask[row] : 1.0f;
 #pragma unroll
-  for (int i = 0; i < TF_CM / 8; ++i) {
+  for (int i = 0; i < CM / 8; ++i) {
     const int cc = sub + 8 * i;
     if (cc < c) {
       float y = acc[i] * m;
@@ -282,8 +284,12 @@ extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char
   if (a->dtype == FPF_DT_F32) {
     if (a->c > TF_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 transition serves c <= %d (got %d)", TF_CM, a->c);
     const dim3 grid((unsigned)cdiv(a->rows, TF_R)), block(256);
-    hipLaunchKernelGGL(transition_f32_kernel, grid, block, 0, st, (const float*)a->x, (float*)a->out, a->ln_w, a->ln_b, a->eps,
-                       (const float*)a->w_a, (const float*)a->w_b, (const float*)a->w_o, a->row_mask, a->residual, a->rows, a->c, a->hidden);
+    if (a->c <= 128)
+      hipLaunchKernelGGL(transition_f32_kernel<128>, grid, block, 0, st, (const float*)a->x, (float*)a->out, a->ln_w, a->ln_b, a->eps,
+                         (const float*)a->w_a, (const float*)a->w_b, (const float*)a->w_o, a->row_mask, a->residual, a->rows, a->c, a->hidden);
+    else
+      hipLaunchKernelGGL(transition_f32_kernel<TF_CM>, grid, block, 0, st, (const float*)a->x, (float*)a->out, a->ln_w, a->ln_b, a->eps,
+                         (const float*)a->w_a, (const float*)a->w_b, (const float*)a->w_o, a->row_mask, a->residual, a->rows, a->c, a->hidden);
     return launched(err, errlen, "fpf_transition_fwd(f32)");
   }
   return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);

@@ -783,6 +783,8 @@ struct ProParams {
   int ending, flags;
   float q_scale;                 // q is stored times this (the fused block folds the attention scale into q)
   float bias_scale;              // and the bias times this (log2(e) for the block-layout core: logits in log2 units)
+  int64_t bias_ld;               // elements between bias rows (>= N)
+  int bias_bf16;                 // bias stored as bf16 (else fp32)
 };
 
 __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
@@ -790,7 +792,7 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   rt_stage_affine(sLN, p.ln_w, p.ln_b, tid, 512);
-  rt_stage_weights(sW, p.w_qkvg, 4 * TP_HD, 4 * TP_HD, tid, 512);
+  if (p.flags & (PRO_QKV | PRO_G)) rt_stage_weights(sW, p.w_qkvg, 4 * TP_HD, 4 * TP_HD, tid, 512);
   rt_stage_weights(sW + 4 * TP_HD * RT_LD, p.w_b, 32, p.H, tid, 512);
   __syncthreads();
   const int H = p.H, D = TP_HD / H;
@@ -843,10 +845,15 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
                                 : p.g + ((b * R + ii) * N + j) * TP_HD + (blk - 12) * 32 + 8 * g;             // [B, R, J, HD]
         *reinterpret_cast<u32x4*>(dst) = lo;
         *reinterpret_cast<u32x4*>(dst + 16) = hi;
-      } else if (g == 0 && live) {                        // bias (fp32): [B, H, I, J], absolute row
+      } else if (live) {                                  // bias: [B, H, I, bias_ld] fp32 | bf16, absolute row; head c_row(v, g)
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (v < H) p.bias[((b * H + v) * N + i) * N + j] = acc[v] * p.bias_scale;
+        for (int v = 0; v < 16; ++v) {
+          const int hh = c_row(v, g);
+          if (hh >= H) continue;
+          const int64_t o = ((b * H + hh) * N + i) * p.bias_ld + j;
+          if (p.bias_bf16) reinterpret_cast<uint16_t*>(p.bias)[o] = f2bf(acc[v] * p.bias_scale);
+          else p.bias[o] = acc[v] * p.bias_scale;
+        }
       }
     }
   }
@@ -1260,8 +1267,9 @@ static bool block_layout2(int dtype, int64_t N) { return dtype == FPF_DT_BF16 &&
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
-                           int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f) {
+                           int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f, int64_t bias_ld = -1, int bias_bf16 = 0) {
   if (rows < 0) rows = N;
+  if (bias_ld < 0) bias_ld = N;
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || ((flags & PRO_QKV) && (!aligned16(q) || !aligned16(k) || !aligned16(v))) ||
         ((flags & PRO_G) && !aligned16(g)) || ((flags & PRO_BIAS) && !aligned16(bias)))
@@ -1290,12 +1298,14 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.flags = flags;
     p.q_scale = q_scale;
     p.bias_scale = bias_scale;
+    p.bias_ld = bias_ld;
+    p.bias_bf16 = bias_bf16;
     if (!rt_tiles_ok(B * rows * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "prologue: 2^31 or more 32-pixel tiles");
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
-  if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS) || q_scale != 1.0f || bias_scale != 1.0f)
+  if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS) || q_scale != 1.0f || bias_scale != 1.0f || bias_ld != N || bias_bf16)
     return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output, q unscaled)");
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
@@ -1368,10 +1378,27 @@ extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, c
   if (a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_DTYPE, "the bias pass serves the bf16 block");
   const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
   if (rc) return rc;
-  // the prologue kernel with only its bias output; the q|k|v|g weights are not read (the weight staging still needs a pointer)
+  // the prologue kernel with only its bias output (the q|k|v|g weights are neither staged nor read)
   return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg ? a->w_qkvg : a->w_b, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending,
                          nullptr, nullptr, nullptr, 0, nullptr, a->bias, static_cast<hipStream_t>(stream), err, errlen, PRO_BIAS, 0, -1, 1.0f,
                          block_layout2(a->dtype, a->N) ? LOG2E : 1.0f);
+}
+
+extern "C" int fpf_apb_bias_fwd(const FpfApbBiasArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->z || !a->w_z || !a->bias) return fail(err, errlen, FPF_E_ARGS, "z / w_z / bias is NULL");
+  if (a->B < 0 || a->N < 0) return fail(err, errlen, FPF_E_SHAPE, "negative extent");
+  if (a->B == 0 || a->N == 0) return FPF_OK;
+  if (a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_DTYPE, "the pair-bias producer reads bf16 z");
+  if (a->C != TP_C || a->H < 1 || a->H > 32) return fail(err, errlen, FPF_E_SHAPE, "the pair-bias producer serves C = 128, 1 <= H <= 32 (got C=%d H=%d)", a->C, a->H);
+  if (a->B > 65535) return fail(err, errlen, FPF_E_SHAPE, "B above 65535");
+  if (!(a->bias_dtype == FPF_DT_F32 || a->bias_dtype == FPF_DT_BF16)) return fail(err, errlen, FPF_E_DTYPE, "bias_dtype %d", a->bias_dtype);
+  const int64_t ld = a->bias_ld > 0 ? a->bias_ld : a->N;
+  if (ld < a->N) return fail(err, errlen, FPF_E_SHAPE, "bias_ld %lld < N %lld", (long long)ld, (long long)a->N);
+  return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_z, a->w_z, a->B, a->N, a->C, a->H, 1, 0, nullptr, nullptr, nullptr, 0,
+                         nullptr, static_cast<float*>(a->bias), static_cast<hipStream_t>(stream), err, errlen, PRO_BIAS, 0, -1, 1.0f, 1.0f, ld,
+                         a->bias_dtype == FPF_DT_BF16);
 }
 
 extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream, char* err, size_t errlen) {

@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 DT_BF16, DT_F32, DT_U8 = 1, 2, 3
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
 
@@ -65,6 +65,18 @@ class TriattnEpilogueArgs(C.Structure):
                 ("w_o", vp), ("ending", i32), ("residual", i32), ("out", vp)]
 
 
+class ApbArgs(C.Structure):
+    _fields_ = [("abi_version", i32), ("dtype", i32), ("S", i64), ("N", i64), ("NK", i64), ("H", i64), ("D", i64), ("q", vp), ("k", vp),
+                ("v", vp), ("q_stride", i64 * 4), ("k_stride", i64 * 4), ("v_stride", i64 * 4), ("gate", vp), ("gate_stride", i64 * 4),
+                ("bias", vp), ("bias_dtype", i32), ("bias_stride", i64 * 4), ("key_mask", vp), ("mask_dtype", i32),
+                ("mask_stride", i64 * 2), ("out", vp), ("out_stride", i64 * 4), ("scale", f32)]
+
+
+class ApbBiasArgs(C.Structure):
+    _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("z", vp), ("ln_w", vp), ("ln_b", vp),
+                ("eps", f32), ("w_z", vp), ("bias", vp), ("bias_dtype", i32), ("bias_ld", i64)]
+
+
 ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol include/fpf_hip.h declares
     "fpf_abi_version": ([], C.c_int),
     "fpf_describe": ([], C.c_char_p),
@@ -78,6 +90,8 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_triattn_block_fwd": ([C.POINTER(TriattnBlockArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_prologue_fwd": ([C.POINTER(TriattnPrologueArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_epilogue_fwd": ([C.POINTER(TriattnEpilogueArgs), vp, C.c_char_p, sz], C.c_int),
+    "fpf_apb_fwd": ([C.POINTER(ApbArgs), vp, C.c_char_p, sz], C.c_int),
+    "fpf_apb_bias_fwd": ([C.POINTER(ApbBiasArgs), vp, C.c_char_p, sz], C.c_int),
 }
 
 

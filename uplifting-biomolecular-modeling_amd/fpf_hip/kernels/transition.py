@@ -57,8 +57,8 @@ def select(dtype, arch, c, hidden, *, word):
     sel = F.resolve(word, F.dtype_word(dtype), arch, "transition", cell="transition:c%dh%d" % (c, hidden))
     if sel.row == F.ROW_FAST and (c != 128 or hidden % 32):
         raise Refusal("shape:c%dh%d" % (c, hidden), sel.row, F.ROW_F32, "the bf16 kernel serves c = 128, hidden % 32 == 0")
-    if sel.row == F.ROW_F32 and c > 128:
-        raise Refusal("shape:c%d" % c, sel.row, F.ROW_STOCK, "the fp32 kernel serves c <= 128")
+    if sel.row == F.ROW_F32 and c > 384:
+        raise Refusal("shape:c%d" % c, sel.row, F.ROW_STOCK, "the fp32 kernel serves c <= 384")
     return sel
 
 
