@@ -47,6 +47,31 @@ def test_trimul_bf16(direction, B, N, masked):
     assert_bf16_close(out, ref, "trimul %s B%d N%d" % (direction, B, N))
 
 
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("N", [512, 768])
+def test_trimul_bf16_256_tiles_sampled_rows(direction, N):
+    """Planes padded to a multiple of 256 take the persistent 256 x 256 contraction, whose slab ring runs across tile
+    boundaries (N = 512: two tiles per workgroup; N = 768, the bench shape: four or five).  Sampled rows on both sides of
+    every tile boundary against the fp32 oracle, with a ragged mask; a second call is bitwise the first."""
+    from fpf_hip.kernels import trimul as TM
+    w = _weights(128, 11, torch.bfloat16)
+    g = torch.Generator().manual_seed(N + 1)
+    z = torch.randn(N, N, 128, generator=g).to(torch.bfloat16)
+    mask = torch.ones(N, N)
+    mask[N - 7:, :] = 0
+    mask[:, N - 7:] = 0
+    print("[trimul256] %s N=%d" % (direction, N), flush=True)
+    zd, md, wd = z.to(DEV), mask.to(DEV), _dev(w)
+    u1 = TM.triangle_multiplication(zd, md, direction=direction, weights=wd, word="fast")
+    u2 = TM.triangle_multiplication(zd, md, direction=direction, weights=wd, word="fast")
+    torch.cuda.synchronize()
+    assert torch.equal(u1, u2)
+    rows = [0, 1, 130, 255, 256, 383, N // 2 + 3, N - 256, N - 8, N - 1]
+    got = u1[rows].cpu()
+    ref = S.trimul_rows(z.float(), mask, rows, direction=direction, weights={k: v.float() for k, v in w.items()}, dtype=torch.float32)
+    assert_bf16_close(got, ref, "trimul256 %s N%d rows %s" % (direction, N, rows))
+
+
 def test_trimul_bf16_residual_in_place_equals_out_of_place():
     from fpf_hip.kernels import trimul as TM
     w = _dev(_weights(128, 2, torch.bfloat16))

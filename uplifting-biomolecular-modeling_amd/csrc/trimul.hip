@@ -181,21 +181,31 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 }
 
 // ---------------------------------------------------------------------------------------------------------------- contraction, 256 x 256 tiles
-// For planes padded to a multiple of 256: a workgroup (4 waves, one per SIMD) computes a 256 x 256 tile of X, each wave a
-// 128 x 128 quarter in 16 accumulators.  The A and B k-slabs (256 rows x 32 k each) go straight from global memory into LDS
-// (global_load_lds_dwordx4: no VGPR staging) through a ring of CB_NBUF buffers with CB_IF slabs in flight, so each slab's
-// loads have CB_IF - 1 slabs of MFMAs to land behind (a fifth buffer, the whole 160 KB of LDS, measured no faster); within
-// a slab row the four 16-byte chunks are XOR-swizzled by (row >> 2) & 3, so the fragment reads of 16 consecutive rows land
-// on 16 distinct bank groups.  The MFMA runs with the operands exchanged (D = B A^T): lane = row i, registers =
+// For planes padded to a multiple of 256: a workgroup (4 waves, one per SIMD) computes 256 x 256 tiles of X, each wave a
+// 128 x 128 quarter in 16 accumulators.  The grid is persistent (one workgroup per CU): workgroup b runs on XCD b % 8
+// (round-robin dispatch), XCD x owns the contiguous tile range [x per, (x + 1) per) and its workgroups take every
+// (grid / 8)-th tile of it, so the tiles that share A rows / B rows of one plane are computed by one XCD at the same time.
+// The A and B k-slabs (256 rows x 32 k each) go straight from global memory into LDS (global_load_lds_dwordx4: no VGPR
+// staging) through a ring of CB_NBUF buffers with CB_IF slabs in flight; the slab stream runs across tile boundaries, so
+// the next tile's first slabs land while the current tile finishes and its stores drain behind the next tile's MFMAs.
+// Within a slab row the four 16-byte chunks are XOR-swizzled by (row >> 2) & 3, so the fragment reads of 16 consecutive
+// rows land on 16 distinct bank groups.  The MFMA runs with the operands exchanged (D = B A^T): lane = row i, registers =
 // 16 columns j, and after the half-wave lane exchange each lane stores 8 consecutive columns per 16-byte store.
 constexpr int CB_T = 256, CB_K = 32, CB_NBUF = 4, CB_IF = CB_NBUF - 1;
 
-// waits until at most p slabs (8 transfers of this wave each) are outstanding
-__device__ __forceinline__ void cb_wait(int p) {
-  if (p >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
-  else if (p == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if (p == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// waits until at most p slabs (8 transfers of this wave each) are outstanding, plus the 32 stores of the previous tile when
+// they were issued after the awaited slab (the vector-memory counter retires loads and stores in issue order)
+__device__ __forceinline__ void cb_wait(int p, bool stores) {
+  if (stores) {
+    if (p >= 2) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    else if (p == 1) asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+  } else {
+    if (p >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    else if (p == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (p == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -204,37 +214,52 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   __shared__ __attribute__((aligned(16))) uint16_t sB[CB_NBUF][CB_T * CB_K];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   const int64_t tpd = Np / CB_T, tiles = tpd * tpd, total = tiles * nbatch;
-  const int64_t per = (total + 7) / 8;
-  const int64_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;     // each XCD gets a contiguous run: one plane's 9 tiles share its L2
-  if (w >= total) return;
-  const int64_t bc = w / tiles, t = w % tiles, ti = t / tpd, tj = t % tpd;
-  const int64_t pb_ = bc / TM_C, pc = bc % TM_C, rstride = TL_ROW, kstride = tl_kblk(Np);   // tiled planes
-  const uint16_t* a0 = A + tl_off(pb_, pc, ti * CB_T, 0, Np);
-  const uint16_t* b0 = Bm + tl_off(pb_, pc, tj * CB_T, 0, Np);
+  const int64_t per = (total + 7) / 8, g8 = gridDim.x / 8;     // the host launches a multiple of 8 workgroups
+  const int64_t x0 = (blockIdx.x % 8) * per, first = x0 + blockIdx.x / 8, end = total < x0 + per ? total : x0 + per;
+  if (first >= end) return;
+  const int ntile = (int)((end - first + g8 - 1) / g8);       // tiles first, first + g8, ... below end
+  const int nk = (int)(Np / CB_K), U = ntile * nk;             // slabs per tile, slabs of this workgroup (host: U < 2^31)
+  const int64_t kstride = tl_kblk(Np);
+  auto tile_of = [&](int r, int64_t& bc, int64_t& ti, int64_t& tj) {
+    const int64_t w = first + (int64_t)r * g8, t = w % tiles;
+    bc = w / tiles;
+    ti = t / tpd;
+    tj = t % tpd;
+  };
   // slab loads: 1024 16-byte chunks per operand; instruction q of thread tid fills LDS slot s = 256 q + tid (each wave
   // instruction writes 1 KB contiguously); slot s = row s >> 2, position s & 3, holding chunk (s & 3) ^ ((row >> 2) & 3)
-  int64_t goff[4];
+  uint32_t goff[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int sl = 256 * q + tid, r = sl >> 2, c = (sl & 3) ^ ((r >> 2) & 3);
-    goff[q] = (int64_t)r * rstride + 8 * c;
+    goff[q] = (uint32_t)(r * TL_ROW + 8 * c);
   }
-  auto issue = [&](int buf, int64_t k0) {              // k0 is a multiple of 32: one column block per slab
+  // issue cursor: the next slab to load is slab ikt of tile ir (operand bases ia0 / ib0)
+  int ir = 0, ikt = 0;
+  const uint16_t *ia0, *ib0;
+  auto set_bases = [&](int r) {
+    int64_t bc, ti, tj;
+    tile_of(r, bc, ti, tj);
+    ia0 = A + tl_off(bc / TM_C, bc % TM_C, ti * CB_T, 0, Np);
+    ib0 = Bm + tl_off(bc / TM_C, bc % TM_C, tj * CB_T, 0, Np);
+  };
+  set_bases(0);
+  auto issue_next = [&](int buf) {
+    const int64_t ko = (int64_t)ikt * kstride;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      lds_dma16(a0 + goff[q] + (k0 >> 5) * kstride, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
-      lds_dma16(b0 + goff[q] + (k0 >> 5) * kstride, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16(ia0 + goff[q] + ko, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16(ib0 + goff[q] + ko, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
+    }
+    if (++ikt == nk) {
+      ikt = 0;
+      if (++ir < ntile) set_bases(ir);
     }
   };
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
   // fragment read offsets (elements) of this lane's rows for chunk position 0 / 1 of each k16 half: row r, chunk c
   auto frag_off = [&](int r, int c) { return (r * 4 + (c ^ ((r >> 2) & 3))) * 8; };
   f32x16 acc[4][4];
-#pragma unroll
-  for (int si = 0; si < 4; ++si)
-#pragma unroll
-    for (int sj = 0; sj < 4; ++sj) acc[si][sj] = f32x16{};
-  const int nk = (int)(Np / CB_K);
   // the 16 fragments of one slab: A rows wr + 32 s + n, B rows wc + 32 s + n, chunks 2 ks + g
   auto read_frags = [&](int buf, bf16x8 (&fa)[2][4], bf16x8 (&fb)[2][4]) {
     const uint16_t* pa = sA[buf];
@@ -247,29 +272,31 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
         fb[ks][s4] = as_bf8(*reinterpret_cast<const u32x4*>(pb + frag_off(wc + 32 * s4 + n, 2 * ks + g)));
       }
   };
-  // ring: slab k lives in buffer k % CB_NBUF, CB_IF slabs in flight.  Iteration kt issues slab kt + CB_IF, runs 8 of slab
-  // kt's 32 MFMAs, waits for slab kt + 1 at the barrier (the matrix core keeps working), then reads slab kt + 1's 16
-  // fragments ahead of the other 24 MFMAs.
-  for (int s = 0; s < CB_IF && s < nk; ++s) issue(s, (int64_t)s * CB_K);
-  cb_wait((nk < CB_IF ? nk : CB_IF) - 1);
+  // ring: slab u lives in buffer u % CB_NBUF, CB_IF slabs in flight.  Slab u issues slab u + CB_IF (its buffer held slab
+  // u - 1, whose fragments every wave read before slab u - 1's barrier), runs 8 of its 32 MFMAs, waits for slab u + 1 at
+  // the barrier (the matrix core keeps working), then reads slab u + 1's 16 fragments ahead of the other 24 MFMAs.  A
+  // tile's stores are issued after the DMA of the next tile's slabs 0 .. 2 and before that of slab 3, so the waits for
+  // slabs 1 and 2 of every tile but the first count them.
+  for (int s = 0; s < CB_IF && s < U; ++s) issue_next(s);
+  cb_wait((U < CB_IF ? U : CB_IF) - 1, false);
   __builtin_amdgcn_s_barrier();
   // two fragment sets that trade roles every slab (no register copies between slabs: a copy into registers the queued
   // MFMAs still read would hold the wave until those MFMAs start)
   bf16x8 f0a[2][4], f0b[2][4], f1a[2][4], f1b[2][4];
   read_frags(0, f0a, f0b);
-  auto slab = [&](int kt, const bf16x8 (&fa)[2][4], const bf16x8 (&fb)[2][4], bf16x8 (&na)[2][4], bf16x8 (&nb)[2][4]) {
-    if (kt + CB_IF < nk) issue((kt + CB_IF) % CB_NBUF, (int64_t)(kt + CB_IF) * CB_K);   // its buffer held slab kt - 1, read before the last barrier
+  auto slab = [&](bool stores, int u, const bf16x8 (&fa)[2][4], const bf16x8 (&fb)[2][4], bf16x8 (&na)[2][4], bf16x8 (&nb)[2][4]) {
+    if (u + CB_IF < U) issue_next((u + CB_IF) % CB_NBUF);
 #pragma unroll
     for (int si = 0; si < 4; ++si)
 #pragma unroll
       for (int sj = 0; sj < 2; ++sj) acc[si][sj] = mfma32(fb[0][sj], fa[0][si], acc[si][sj]);
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < nk) {                                   // slab kt + 1 landed: at most the later slabs' transfers outstanding
-      cb_wait(nk - 2 - kt < CB_IF - 1 ? nk - 2 - kt : CB_IF - 1);
+    if (u + 1 < U) {                                     // slab u + 1 landed
+      cb_wait(U - 2 - u < CB_IF - 1 ? U - 2 - u : CB_IF - 1, stores);
       __builtin_amdgcn_s_barrier();
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < nk) read_frags((kt + 1) % CB_NBUF, na, nb);
+    if (u + 1 < U) read_frags((u + 1) % CB_NBUF, na, nb);
 #pragma unroll
     for (int si = 0; si < 4; ++si)
 #pragma unroll
@@ -280,21 +307,38 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
       for (int sj = 0; sj < 4; ++sj) acc[si][sj] = mfma32(fb[1][sj], fa[1][si], acc[si][sj]);
     __builtin_amdgcn_sched_barrier(0);
   };
-  for (int kt = 0; kt < nk; kt += 2) {                   // nk is even: Np is a multiple of 256
-    slab(kt, f0a, f0b, f1a, f1b);
-    slab(kt + 1, f1a, f1b, f0a, f0b);
-  }
+  for (int r = 0; r < ntile; ++r) {
 #pragma unroll
-  for (int si = 0; si < 4; ++si)
+    for (int si = 0; si < 4; ++si)
 #pragma unroll
-    for (int sj = 0; sj < 4; ++sj) {
-      u32x4 lo, hi;
-      rt_pack16(acc[si][sj], lo, hi);
-      uint16_t* xp = X + tl_off(pb_, pc, ti * CB_T + wr + 32 * si + n, tj * CB_T + wc + 32 * sj, Np) + 8 * g;
-      *reinterpret_cast<u32x4*>(xp) = lo;
-      *reinterpret_cast<u32x4*>(xp + 16) = hi;
-      __builtin_amdgcn_sched_barrier(0);                 // one accumulator at a time (bounded VGPR use)
+      for (int sj = 0; sj < 4; ++sj) acc[si][sj] = f32x16{};
+    const int u0 = r * nk;
+    slab(r > 0, u0, f0a, f0b, f1a, f1b);                 // nk is even: Np is a multiple of 256
+    slab(r > 0, u0 + 1, f1a, f1b, f0a, f0b);
+    for (int kt = 2; kt < nk; kt += 2) {
+      slab(false, u0 + kt, f0a, f0b, f1a, f1b);
+      slab(false, u0 + kt + 1, f1a, f1b, f0a, f0b);
     }
+    int64_t bc, ti, tj;
+    tile_of(r, bc, ti, tj);
+    const int64_t pb_ = bc / TM_C, pc = bc % TM_C;
+    // the lane's part of the store offsets, recomputed per tile (kept live across the slab loop it would take registers
+    // the loop needs): row n of each 32-row block, 8 g columns in
+    uint32_t lane;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    const uint32_t lane_el = (lane & 31) * (uint32_t)TL_ROW + 8 * (lane >> 5);
+#pragma unroll
+    for (int si = 0; si < 4; ++si)
+#pragma unroll
+      for (int sj = 0; sj < 4; ++sj) {
+        u32x4 lo, hi;
+        rt_pack16(acc[si][sj], lo, hi);
+        uint16_t* xp = X + tl_off(pb_, pc, ti * CB_T + wr + 32 * si, tj * CB_T + wc + 32 * sj, Np) + lane_el;
+        *reinterpret_cast<u32x4*>(xp) = lo;
+        *reinterpret_cast<u32x4*>(xp + 16) = hi;
+        __builtin_amdgcn_sched_barrier(0);               // one accumulator at a time (bounded VGPR use)
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------- K3 (bf16)
@@ -610,7 +654,9 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
     if (rc) return rc;
     if (Np % CB_T == 0) {
       const int64_t tiles = (Np / CB_T) * (Np / CB_T) * B * TM_C;
-      hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, B * TM_C);
+      const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;    // persistent, a multiple of 8
+      if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
+      hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * TM_C);
       rc = launched(err, errlen, "trimul_contract_bf16_256");
     } else {
       const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE) * B * TM_C;
