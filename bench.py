@@ -9,7 +9,9 @@ tri-att starting node, tri-att ending node, transition 4x): 13 launches of libfp
 z ~ N(0,1) and random-init weights N(0, 1/fan_in) (seed 0), pair mask all ones, inputs resident in HBM before timing.
 Prints ONE JSON line (the driver's contract) with the dominant kernel's roofline (timed live with HIP events on the launch
 stream) and the stock PyTorch CPU statement timed on this host (a reported baseline, not the target).  The `trunk` field is
-BASELINE config 3 (a 48-layer Pairformer trunk at N = 512, pair and single tracks; --trunk-layers 0 skips it).
+BASELINE config 3 (a 48-layer Pairformer trunk at N = 512, pair and single tracks; --trunk-layers 0 skips it); `configs` holds
+config 1 (isolated triangle attention at N = 384 with padding) and config 4 (the `big` line at N = 2048); --no-configs skips
+them.  Config 2 (isolated triangle multiplication at N = 768) is the breakdown's trimul_out / trimul_in.
 """
 import argparse
 import json
@@ -64,6 +66,49 @@ def trunk(torch, dev, layers, N=512, reps=2):
     return {"layers": layers, "N": N, "ms": round(t, 3), "tflop": round(fl / 1e12, 3), "tflops": round(fl / (t * 1e-3) / 1e12, 1),
             "mfma_frac": round(fl / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "ms_per_layer": round(t / layers, 4),
             "workload": "BASELINE config 3: %d-layer Pairformer trunk, pair track bf16 + single track fp32 (c_s 384, 16 x 24 heads)" % layers}
+
+
+def configs_legs(torch, dev, big_blocks=4):
+    """The other BASELINE configs as measured legs (parity cases elsewhere; reported here as ms and TFLOP/s):
+    config 1 -- isolated triangle attention, N = 384, both nodes, pair mask zeroing the last 38 residues on both axes
+    (rows past 346 fully masked: uniform mean), residual in place, algorithmic FLOPs of the full N;
+    config 4 -- the memory-lean `big` line, N = 2048, `big_blocks` pair blocks with 256-row tri-att chunks, ragged mask of
+    chains 900 + 700 + 300 and 148 padded positions."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.attn import pair_fused as PF
+    blk = PFM.PairBlock(PFM.random_params(seed=0), dev, torch.bfloat16)
+    legs = {}
+    N = 384
+    g = torch.Generator().manual_seed(1)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(dev)
+    valid = (torch.arange(N) < N - 38).float()
+    mask = torch.outer(valid, valid).unsqueeze(0).to(dev)
+    f = block_flops(N)["triatt"]
+    for name, ending in (("start", False), ("end", True)):
+        fn = lambda: PF.tri_attn_block(z, blk.ta["tae" if ending else "tas"], mask, ending=ending, residual=True)
+        fn()
+        t = time_events(fn, 20, torch)
+        legs["c1_triatt_%s" % name] = {"N": N, "ms": round(t, 4), "tflops": round(f / (t * 1e-3) / 1e12, 1)}
+    del z
+    N = 2048
+    zb = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
+    valid = torch.zeros(N)
+    valid[:1900] = 1
+    mb = torch.outer(valid, valid).unsqueeze(0).to(dev)
+    PFM.pair_block(zb, mb, blk, word="big", rows=256)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(big_blocks):
+        PFM.pair_block(zb, mb, blk, word="big", rows=256)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e)
+    fb = block_flops(N)["block"] * big_blocks
+    legs["c4_big"] = {"N": N, "blocks": big_blocks, "rows_per_chunk": 256, "ms": round(ms, 2), "ms_per_block": round(ms / big_blocks, 2),
+                      "tflops": round(fb / (ms * 1e-3) / 1e12, 1), "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2)}
+    del zb
+    return legs
 
 
 def time_events(fn, reps, torch):
@@ -170,7 +215,7 @@ def cpu_baseline(torch):
     med = statistics.median(ts[2:])
     fl = block_flops(64)["block"]
     return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": "BASELINE config 1: one pair block N=64 c_z=128 fp32 (stock statements, oracle/stock.py), median of 5 after 2 "
+            "sample": "BASELINE configs[0]: one pair block N=64 c_z=128 fp32 (stock statements, oracle/stock.py), median of 5 after 2 "
                       "warm-ups; %.1f ms per block, %.2f GFLOP" % (med * 1e3, fl / 1e9)}
 
 
@@ -182,6 +227,7 @@ def main():
     ap.add_argument("--n", type=int, default=768)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trunk-layers", type=int, default=48, help="BASELINE config-3 trunk leg (0: skip)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the config-1 (tri-att N = 384) and config-4 (big, N = 2048) legs")
     ap.add_argument("--probe", default=None, help="launch-only run for counter passes: triattn_core | copy")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -270,9 +316,11 @@ def main():
                       "c_z": 128, "c_hidden": 128, "heads": 4, "head_dim": 32, "batch": 1, "mask": "all ones",
                       "block_tflop": round(fl["block"] / 1e12, 4), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
            "roofline": roof, "breakdown": breakdown}
+    del keep, zb, yln
     if a.trunk_layers > 0:
-        del keep, zb, yln
         out["trunk"] = trunk(torch, dev, a.trunk_layers)
+    if not a.no_configs:
+        out["configs"] = configs_legs(torch, dev)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(out), flush=True)

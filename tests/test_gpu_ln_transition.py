@@ -64,6 +64,19 @@ def test_transition_bf16(rows, residual, masked):
         assert torch.equal(y.cpu()[mask == 0], x[mask == 0]), "masked rows must equal x bit for bit"
 
 
+@pytest.mark.parametrize("hidden", [32, 64, 96, 256])
+def test_transition_bf16_chunk_counts(hidden):
+    """Hidden sizes of 1, 2, 3 and 8 weight chunks: the skewed early / late waves and the chunk ring's edges."""
+    from fpf_hip.kernels import transition as T
+    wa, wb, wo, lw, lb = _tr_weights(128, hidden, 13, torch.bfloat16)
+    x = torch.randn(1000, 128, generator=_g(hidden)).to(torch.bfloat16)
+    W = T.pack(w_a=wa.to(DEV), w_b=wb.to(DEV), w_o=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV))
+    y, _ = T.transition(x.to(DEV), W, word="fast", residual=True)
+    torch.cuda.synchronize()
+    ref = S.transition(x.float(), wa.float(), wb.float(), wo.float(), lw, lb, residual=True, dtype=torch.float32)
+    assert_bf16_residual_close(y, ref, "transition hidden %d" % hidden)
+
+
 def test_transition_bf16_in_place_equals_out_of_place():
     from fpf_hip.kernels import transition as T
     wa, wb, wo, lw, lb = _tr_weights(128, 512, 12, torch.bfloat16)

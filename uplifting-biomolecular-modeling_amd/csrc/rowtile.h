@@ -207,6 +207,18 @@ __device__ __forceinline__ void rt_regroup_f32(const f32x16& acc, float (&out)[1
 __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
 }
+// The lane index, computed where it is called (volatile: never hoisted, so values derived from it are not kept live
+// across a loop in registers the loop needs)
+__device__ __forceinline__ int opaque_lane() {
+  uint32_t lane;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+  return (int)lane;
+}
+
+// The same transfer from a wave-uniform base plus a 32-bit per-lane byte offset (scalar base: no 64-bit address per lane).
+__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "memory");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
 }

@@ -354,10 +354,6 @@ __device__ __forceinline__ f32x4 gload4_async(uint32_t voff, const void* sbase) 
   asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(v) : "v"(voff), "s"(sbase), "n"(IMM));
   return v;
 }
-// 16 bytes per lane from sbase + voff into LDS at lds_base + 16 * lane (global_load_lds_dwordx4, scalar base)
-__device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "memory");
-}
 // waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
 // through the statement so nothing reads them earlier
 template <int N>
@@ -790,7 +786,7 @@ struct ProParams {
 __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[(4 * TP_HD + 32) * RT_LD];
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   rt_stage_affine(sLN, p.ln_w, p.ln_b, tid, 512);
   if (p.flags & (PRO_QKV | PRO_G)) rt_stage_weights(sW, p.w_qkvg, 4 * TP_HD, 4 * TP_HD, tid, 512);
   rt_stage_weights(sW + 4 * TP_HD * RT_LD, p.w_b, 32, p.H, tid, 512);
@@ -800,7 +796,10 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
   const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)R * tpr, total = (uint32_t)p.B * per_b;
   const uint32_t stride = gridDim.x * RT_WAVES;
   u32x4 raw[8];                                         // the next tile's pixel rows, loaded while this tile computes
+  // the lane index is re-read per tile (opaque_lane): lane-dependent address parts kept live across the tile loop would
+  // be spilled, and each reload's wait would also drain the next tile's prefetch
   auto fetch = [&](uint32_t tt) {
+    const int ln = opaque_lane(), n = ln & 31, g = ln >> 5;
     const RtTile tl = rt_tile(tt, per_b, tpr);
     const int64_t b = tl.b, i = p.row0 + tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
@@ -809,6 +808,7 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
   };
   if (blockIdx.x * RT_WAVES + wave < total) fetch(blockIdx.x * RT_WAVES + wave);
   for (uint32_t t = blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
+    const int ln = opaque_lane(), n = ln & 31, g = ln >> 5;
     const RtTile tl = rt_tile(t, per_b, tpr);
     const int64_t b = tl.b, ii = tl.r, i = p.row0 + ii, j = tl.c * 32 + n;
     const bool live = j < N;

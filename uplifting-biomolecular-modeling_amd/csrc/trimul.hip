@@ -324,8 +324,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
     const int64_t pb_ = bc / TM_C, pc = bc % TM_C;
     // the lane's part of the store offsets, recomputed per tile (kept live across the slab loop it would take registers
     // the loop needs): row n of each 32-row block, 8 g columns in
-    uint32_t lane;
-    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    const uint32_t lane = (uint32_t)opaque_lane();
     const uint32_t lane_el = (lane & 31) * (uint32_t)TL_ROW + 8 * (lane >> 5);
 #pragma unroll
     for (int si = 0; si < 4; ++si)
