@@ -343,6 +343,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 //     counts (the memory counter retires in order), so no wait covers a load that is not needed yet;
 //   * the keep bits of all keys of the TA_R rows are built once (LDS table), so the key loop reads no mask.
 constexpr int TA_NB = 3;                                 // K / V^T tile buffers of the block-layout core
+constexpr int TA_DMA_WAVES = 4;                          // waves (32 queries each) per workgroup of the block-layout core
 constexpr float TD_PS_MAX = 18446744073709551616.0f;     // 2^64: a sub-tile's partial row sum at or above it moves the reference
 constexpr float TD_BAND = 32.0f;                         // first live sub-tile: a max outside +-TD_BAND (log2 units) sets it
 constexpr float TD_MOVE = 48.0f;                         // later sub-tiles: a max more than TD_MOVE above it moves it
@@ -365,14 +366,15 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_dma(const CoreParams p) {
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_dma(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][TA_R][TA_KT * TA_D];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_NB][TA_R][TA_D * TA_KT];
   __shared__ uint64_t sKeepAll[TA_R][TA_MAXW];
   __shared__ int sAlive[TA_R];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   // the host checks that the grid fits 31 bits: the workgroup decode is 32-bit
-  const uint32_t nq = (uint32_t)cdiv(p.S, 128), nr = (uint32_t)cdiv(p.N, TA_R), H = (uint32_t)p.H;
+  const uint32_t nq = (uint32_t)cdiv(p.S, 32 * NW), nr = (uint32_t)cdiv(p.N, TA_R), H = (uint32_t)p.H;
   const uint32_t total = (uint32_t)p.B * H * nr * nq;
   const uint32_t per = (total + 7) / 8;
   const uint32_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
@@ -380,7 +382,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
   const int64_t b = bh / H, h = bh % H;
   const int64_t i0 = (int64_t)rg * TA_R;
-  const int64_t q = (int64_t)qt * 128 + wave * 32 + n;
+  const int64_t q = (int64_t)qt * (32 * NW) + wave * 32 + n;
   const bool qlive = q < p.S;
 
   bf16x8 qf[TA_R][2];
@@ -434,14 +436,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     dead_any |= dead[r];
   }
 
-  // DMA: wave w moves chunk block w (1 KB) of each row's K tile (keys 16w .. 16w + 15) and V^T tile (rows 8w .. 8w + 7);
-  // rows past N read row i0 (never stored).  Row bases are scalar, the in-tile byte offsets per lane are fixed.
+  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
+  // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves); rows past N read row i0 (never stored).  Row bases are
+  // scalar, the in-tile byte offsets per lane are fixed.
+  const int wc = wave & 3;
   const uint16_t* kb[TA_R];
   const uint16_t* vb[TA_R];
   uint32_t koff, voff;
   {
-    const int kk = 16 * wave + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
-    const int vd = 8 * wave + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+    const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
+    const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
     koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
     voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
 #pragma unroll
@@ -452,19 +456,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   }
   // LDS byte addresses of this wave's chunk block in buffer 0, row 0 (buffer / row steps are constants)
-  const uint32_t kl0 = lds_addr(&sK[0][0][512 * wave]), vl0 = lds_addr(&sV[0][0][512 * wave]);
+  const uint32_t kl0 = lds_addr(&sK[0][0][512 * wc]), vl0 = lds_addr(&sV[0][0][512 * wc]);
   constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
+  const bool v_mover = NW > 4 && wave >= 4;
   auto dma_tile = [&](int64_t k0, int buf) {
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
-      lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
+      if (NW == 4 || !v_mover) lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
+      if (NW == 4 || v_mover) lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
     }
   };
   // The wait counts (vm_wait4<DMA_OPS + 4>, vm_wait4<4>) assume exactly DMA_OPS operations per dma_tile and 4 per
   // bias_issue, every one issued unconditionally and in the order of the loop below: a wait that counted fewer operations
   // than were issued after the load it guards would let that load land in registers already reused.
-  constexpr int DMA_OPS = 2 * TA_R;
+  constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * TA_R;
 
   const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
   const uint32_t boff = (uint32_t)(((qlive ? q : 0) * p.bs[2] + 4 * g) * 4);
@@ -1181,7 +1186,9 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
       if (!p.bias_vec || p.S % TA_KT != 0 || p.S > 64 * TA_MAXW || p.vs[3] % 8 != 0)
         return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
       if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
-      hipLaunchKernelGGL(triattn_core_bf16_dma, grid, block, 0, st, p);
+      constexpr int NW = TA_DMA_WAVES;
+      const int64_t total_w = a->B * a->H * cdiv(a->N, TA_R) * cdiv(a->S, 32 * NW);
+      hipLaunchKernelGGL(triattn_core_bf16_dma<NW>, dim3((unsigned)(cdiv(total_w, 8) * 8)), dim3(64 * NW), 0, st, p);
       return launched(err, errlen, "triattn_core_bf16_dma");
     }
     if (p.v_t && p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<true, true>), grid, block, 0, st, p);
