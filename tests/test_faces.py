@@ -111,3 +111,56 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 2, r.stderr
     assert "single MI355X" in r.stderr
+
+
+def test_cell_keys_follow_the_reference_grammar_and_bucket_rule():
+    from fpf_hip import cells as C
+    assert C.bucket(1) == (256, True) and C.bucket(511) == (511, True) and C.bucket(512) == (800, True)
+    assert C.bucket(2049) == (2048, False)                     # above the largest listed size: its cell, unmeasured
+    assert C.triattn_key("bf16", 32, 4, 768) == "9.5|bf16|D32|H4|N<=800|fwd"
+    assert C.trimul_key("bf16", 128, 128, 384, "in") == "9.5|bf16|C128|H128|N<=400|in|fwd"
+    assert C.transition_key("fp32", 128, 4, 300) == "9.5|fp32|pair_c128_n4|N<=400|eager|fwd"
+    from fpf_hip.kernels import triattn as TA
+    from fpf_hip.kernels import trimul as TM
+    assert TA.select("gfx950", torch.bfloat16, 32, 4, 768, word="fast").cell == "9.5|bf16|D32|H4|N<=800|fwd"
+    assert TM.select("gfx950", torch.bfloat16, 128, 128, 768, "outgoing", word="fast").cell == "9.5|bf16|C128|H128|N<=800|out|fwd"
+
+
+def test_measured_table_covers_every_bucket_and_follows_the_exact_rule():
+    """The committed MI355X column: every (face, dtype, bucket[, direction]) cell measured; 'fast' is the bf16 row; 'exact'
+    is the fp32 row exactly where it measured at least as fast as the fp32 torch statement (the reference's exact rule)."""
+    from fpf_hip import cells as C
+    t = C.table()
+    assert set(("triattn", "trimul", "transition")) <= set(t)
+    for n in C.BUCKETS:
+        for dw in ("bf16", "fp32"):
+            keys = {"triattn": [C.triattn_key(dw, 32, 4, n)], "transition": [C.transition_key(dw, 128, 4, n)],
+                    "trimul": [C.trimul_key(dw, 128, 128, n, d) for d in ("in", "out")]}
+            for face, ks in keys.items():
+                for k in ks:
+                    c = C.lookup(face, k)
+                    assert c is not None, k
+                    row = "hip_gfx950" if dw == "bf16" else "hip_gfx950_f32"
+                    assert c["ms"][row] > 0 and c["stock_ms"] > 0
+                    if dw == "bf16":
+                        assert c["fast"] == row
+                    else:
+                        assert c["exact"] == (row if c["stock_ms"] >= c["ms"][row] else "stock"), k
+
+
+def test_exact_word_follows_the_measured_cell():
+    from fpf_hip import cells as C
+    from fpf_hip.kernels import trimul as TM
+    from fpf_hip.kernels import triattn as TA
+    for n in (100, 768, 2000):
+        cell = C.lookup("trimul", C.trimul_key("fp32", 128, 128, n, "out"))
+        if cell["exact"] == "stock":
+            with pytest.raises(TM.Refusal) as e:
+                TM.select("gfx950", torch.float32, 128, 128, n, "outgoing", word="exact")
+            assert e.value.kind == "exact:stock_faster" and e.value.fallback == "stock"
+        else:
+            assert TM.select("gfx950", torch.float32, 128, 128, n, "outgoing", word="exact").row == "hip_gfx950_f32"
+        # the row name always serves the row
+        assert TM.select("gfx950", torch.float32, 128, 128, n, "outgoing", word="hip_gfx950_f32").row == "hip_gfx950_f32"
+        cell = C.lookup("triattn", C.triattn_key("fp32", 32, 4, n))
+        assert (TA.select("gfx950", torch.float32, 32, 4, n, word="exact").row == "hip_gfx950_f32") == (cell["exact"] == "hip_gfx950_f32")

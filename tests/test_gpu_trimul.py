@@ -138,7 +138,7 @@ def test_trimul_fp32_exact(direction, N, masked):
     if masked:
         mask = torch.ones(N, N)
         mask[N - 4:, :] = 0
-    out = TM.triangle_multiplication(z.to(DEV), None if mask is None else mask.to(DEV), direction=direction, weights=_dev(w), word="exact")
+    out = TM.triangle_multiplication(z.to(DEV), None if mask is None else mask.to(DEV), direction=direction, weights=_dev(w), word="hip_gfx950_f32")
     torch.cuda.synchronize()
     ref = S.trimul(z, mask, direction=direction, weights=w, dtype=torch.float64)
     assert_f32_close(out, ref, "trimul fp32 %s N%d" % (direction, N))

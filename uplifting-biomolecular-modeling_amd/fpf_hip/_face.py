@@ -8,7 +8,9 @@ Rows served by this package (one per arithmetic class; the reference's faces nam
 Words (the reference's vocabulary, common/opt_core/opt_core/kernels/triattn/__init__.py:25-36):
     fast / big      -> hip_gfx950 for bf16 inputs, hip_gfx950_f32 for fp32 inputs
     exact           -> hip_gfx950_f32 for fp32 inputs; bf16 inputs are refused by name (fallback 'stock'): the fp32 path is this
-                       package's exact tier, and a bf16 call has no vouched bitwise row here
+                       package's exact tier, and a bf16 call has no vouched bitwise row here.  Where the measured cell table
+                       (fpf_hip/cells) names the stock statement as the cell's exact row (it measured faster than
+                       hip_gfx950_f32), 'exact' is refused by name with fallback 'stock', as the reference's exact rule does
     a row name      -> exactly that row, or a Refusal naming the fallback row
 A refusal is raised before anything is launched and never after a kernel started (the reference's rule,
 triattn/__init__.py:129-136).
@@ -92,7 +94,16 @@ def _resolve(word, dtype_word, arch, face, cell):
     if dtype_word != want:
         raise Refusal("dtype:%s" % dtype_word, row, ROW_F32 if row == ROW_FAST else ROW_FAST, "row %s takes %s operands" % (row, want))
     cls = "fast" if row == ROW_FAST else "exact"
-    return Selection(row, w, cell, cls, "%s: %s -> %s (%s, %s)" % (face, w, row, dtype_word, arch))
+    reason = "%s: %s -> %s (%s, %s)" % (face, w, row, dtype_word, arch)
+    if cell:
+        from . import cells
+        m = cells.lookup(face, cell)
+        if w == "exact" and m is not None and m.get("exact") == ROW_STOCK:
+            raise Refusal("exact:stock_faster", w, ROW_STOCK, "%s: the fp32 torch statement measured x%.2f faster than %s in cell %s"
+                          % (face, 1.0 / max(m.get("x_stock", {}).get(row, 1.0), 1e-9), row, cell))
+        if m is not None and row in m.get("ms", {}):
+            reason += "; cell %s: %.3f ms measured, x%.2f over the torch statement" % (cell, m["ms"][row], m.get("x_stock", {}).get(row, float("nan")))
+    return Selection(row, w, cell, cls, reason)
 
 
 def dtype_word(dtype):

@@ -10,6 +10,7 @@ import torch
 
 from .. import _face as F
 from .. import _lib as L
+from .. import cells as CELLS
 
 Refusal, Selection = F.Refusal, F.Selection
 
@@ -52,9 +53,13 @@ def pack(*, w_o, w_a=None, w_b=None, w_ab=None, ln_w=None, ln_b=None, eps=1e-5, 
     return Weights(w_a, w_b, w_o, ln_w, ln_b, eps, device)
 
 
-def select(dtype, arch, c, hidden, *, word):
-    """Pure: the row serving a transition of (dtype, c, hidden) on this device word, or Refusal by name."""
-    sel = F.resolve(word, F.dtype_word(dtype), arch, "transition", cell="transition:c%dh%d" % (c, hidden))
+def select(dtype, arch, c, hidden, *, word, n_tokens=None):
+    """Pure: the row serving a transition of (dtype, c, hidden) on this device word, or Refusal by name.  ``n_tokens`` (the
+    pair tensor's N) names the measured cell; without it the cell is the class only."""
+    cell = "%s|%s|pair_c%d_n%d|eager|fwd" % (CELLS.CC, F.dtype_word(dtype), c, hidden // max(c, 1))
+    if n_tokens is not None and hidden % c == 0:
+        cell = CELLS.transition_key(F.dtype_word(dtype), c, hidden // c, n_tokens)
+    sel = F.resolve(word, F.dtype_word(dtype), arch, "transition", cell=cell)
     if sel.row == F.ROW_FAST and (c != 128 or hidden % 32):
         raise Refusal("shape:c%dh%d" % (c, hidden), sel.row, F.ROW_F32, "the bf16 kernel serves c = 128, hidden % 32 == 0")
     if sel.row == F.ROW_F32 and c > 384:
@@ -68,7 +73,7 @@ def transition(x, W, *, word, residual=False, x_ln=None, mask=None, out=None, se
     c = int(x.shape[-1])
     if c != W.c:
         raise Refusal("c:%d!=%d" % (c, W.c), word, F.ROW_STOCK)
-    sel = selection or select(x.dtype, F.device_word(x), W.c, W.hidden, word=word)
+    sel = selection or select(x.dtype, F.device_word(x), W.c, W.hidden, word=word, n_tokens=int(x.shape[-2]) if x.dim() >= 3 else None)
     rows = x.numel() // c
     if not x.is_contiguous():
         raise Refusal("stride", sel.row, F.ROW_STOCK, "x must be contiguous")

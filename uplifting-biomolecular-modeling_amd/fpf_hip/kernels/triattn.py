@@ -16,6 +16,7 @@ import torch
 
 from .. import _face as F
 from .. import _lib as L
+from .. import cells as CELLS
 
 Refusal, Selection = F.Refusal, F.Selection
 
@@ -24,7 +25,7 @@ def select(arch, dtype, head_dim, heads, n_tokens, direction="fwd", *, word):
     """Pure: the row serving a triangle-attention call of this class on this device word, or Refusal by name."""
     if direction not in ("fwd", "forward", "inference", "start", "starting", "end", "ending"):
         raise Refusal("direction:%s" % direction, word, F.ROW_STOCK, "forward only")
-    sel = F.resolve(word, F.dtype_word(dtype), arch, "triattn", cell="triattn:d%dh%d:s%d" % (head_dim, heads, n_tokens))
+    sel = F.resolve(word, F.dtype_word(dtype), arch, "triattn", cell=CELLS.triattn_key(F.dtype_word(dtype), head_dim, heads, n_tokens))
     if sel.row == F.ROW_FAST and head_dim != 32:
         raise Refusal("no_row:head_dim%d" % head_dim, sel.row, F.ROW_F32, "the bf16 core serves head_dim 32")
     if sel.row == F.ROW_F32 and head_dim not in (16, 32, 64):

@@ -10,6 +10,7 @@ import torch
 
 from .. import _face as F
 from .. import _lib as L
+from .. import cells as CELLS
 
 Refusal, Selection = F.Refusal, F.Selection
 WEIGHT_KEYS = ("ln_in_w", "ln_in_b", "w_ag", "w_ap", "w_bg", "w_bp", "ln_out_w", "ln_out_b", "w_o", "w_og")
@@ -26,7 +27,8 @@ def direction_word(direction):
 def select(arch, dtype, c_z, c_hidden, n_tokens, direction="outgoing", *, word):
     """Pure: the row serving a TriMul call of this class, or Refusal by name."""
     d = direction_word(direction)
-    sel = F.resolve(word, F.dtype_word(dtype), arch, "trimul", cell="trimul:c%dx%d:n%d:%s" % (c_z, c_hidden, n_tokens, d))
+    sel = F.resolve(word, F.dtype_word(dtype), arch, "trimul",
+                    cell=CELLS.trimul_key(F.dtype_word(dtype), c_z, c_hidden, n_tokens, "out" if d == "outgoing" else "in"))
     if sel.row == F.ROW_FAST and (c_z, c_hidden) != (128, 128):
         raise Refusal("shape:c%dx%d" % (c_z, c_hidden), sel.row, F.ROW_F32, "the bf16 kernels serve c_z = c_hidden = 128")
     if sel.row == F.ROW_F32 and (c_z > 128 or c_hidden > 128):
