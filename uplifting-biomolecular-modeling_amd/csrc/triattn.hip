@@ -484,6 +484,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 
   f32x16 o[TA_R], s[TA_R];
   float lrow[TA_R], mb[TA_R];
+  uint64_t unseen[TA_R];           // lanes whose `seen` is still false (a wave-uniform mask: the fast path tests it in scalar code)
   bool seen[TA_R], sh[TA_R];       // seen: the row's first live sub-tile has set its reference (per lane, equal in l and
                                    // l ^ 32; rows past N count as seen); sh: some lane of the row has a nonzero reference
 #pragma unroll
@@ -492,6 +493,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     lrow[r] = 0.f;
     mb[r] = 0.f;
     seen[r] = i0 + r >= p.N;
+    unseen[r] = seen[r] ? 0ull : ~0ull;
     sh[r] = false;
   }
   // fragment offsets (bf16 elements) inside a row's K / V^T tile
@@ -593,7 +595,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
           }
           uint32_t pk[8];
           float ps = expsum(s[r], pk);
-          if (__ballot(!seen[r] || !(ps < TD_PS_MAX)) != 0) {
+          if ((__builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX)) | unseen[r]) != 0) {
             // set or move the reference of the queries that need it; the decision depends only on the sub-tile max over
             // both key halves, so lanes l and l ^ 32 (one query) always agree
             float m0 = s[r][0];
@@ -610,6 +612,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
             for (int v = 0; v < 16; ++v) s[r][v] -= shift;
             mb[r] += shift;
             seen[r] = seen[r] || fin;
+            unseen[r] = __builtin_amdgcn_ballot_w64(!seen[r]);
             sh[r] = __ballot(mb[r] != 0.f) != 0;
             ps = expsum(s[r], pk);
           }
