@@ -395,46 +395,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
   }
 
-  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys, all of the row's mask loads in flight together
-  // (overlapping the Q loads); a row with no kept key attends uniformly to every key (its words become all ones)
-  const int nw = (int)(p.S >> 6);
-  if (wave < TA_R) {
-    const int64_t i = i0 + wave;
-    const bool rowok = i < p.N;
-    auto build = [&](auto elt) {
-      using T = decltype(elt);
-      const T* mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + (rowok ? i : 0) * p.ms[1];
-      uint64_t any = 0;
-      for (int c0 = 0; c0 < nw; c0 += 16) {
-        T raw[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) raw[u] = (p.mask && c0 + u < nw) ? mrow[(int64_t)(64 * (c0 + u) + l) * p.ms[2]] : (T)1;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          if (c0 + u >= nw) break;
-          const uint64_t bal = __ballot(rowok && raw[u] != (T)0);
-          any |= bal;
-          if (l == 0) sKeepAll[wave][c0 + u] = bal;
-        }
-      }
-      if (rowok && any == 0)
-        for (int c = l; c < nw; c += 64) sKeepAll[wave][c] = ~0ull;
-      if (l == 0) sAlive[wave] = any != 0;
-    };
-    if (p.mask_f32) build(0.0f);
-    else build((uint8_t)0);
-  }
-  // the Q and mask loads complete here: inside the key loop the only vector-memory operations are the counted ones below
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
-  __syncthreads();
-  bool dead[TA_R];
-  bool dead_any = false;
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    dead[r] = (i0 + r < p.N) && !sAlive[r];
-    dead_any |= dead[r];
-  }
 
   // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
   // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves); rows past N read row i0 (never stored).  Row bases are
@@ -527,6 +487,48 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   bias_issue(0, bq[0]);
   bias_issue(32, bq[1]);
   dma_tile(nT > 1 ? TA_KT : 0, 1);
+  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys, all of the row's mask loads in flight together
+  // (overlapping the Q loads and the first tiles' transfers, issued above); a row with no kept key attends uniformly to
+  // every key (its words become all ones)
+  const int nw = (int)(p.S >> 6);
+  if (wave < TA_R) {
+    const int64_t i = i0 + wave;
+    const bool rowok = i < p.N;
+    auto build = [&](auto elt) {
+      using T = decltype(elt);
+      const T* mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + (rowok ? i : 0) * p.ms[1];
+      uint64_t any = 0;
+      for (int c0 = 0; c0 < nw; c0 += 16) {
+        T raw[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) raw[u] = (p.mask && c0 + u < nw) ? mrow[(int64_t)(64 * (c0 + u) + l) * p.ms[2]] : (T)1;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (c0 + u >= nw) break;
+          const uint64_t bal = __ballot(rowok && raw[u] != (T)0);
+          any |= bal;
+          if (l == 0) sKeepAll[wave][c0 + u] = bal;
+        }
+      }
+      if (rowok && any == 0)
+        for (int c = l; c < nw; c += 64) sKeepAll[wave][c] = ~0ull;
+      if (l == 0) sAlive[wave] = any != 0;
+    };
+    if (p.mask_f32) build(0.0f);
+    else build((uint8_t)0);
+  }
+  // the Q and mask loads complete here (and the older transfers with them: the counter retires in order); inside the key
+  // loop the only vector-memory operations are the counted ones
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
+  __syncthreads();
+  bool dead[TA_R];
+  bool dead_any = false;
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    dead[r] = (i0 + r < p.N) && !sAlive[r];
+    dead_any |= dead[r];
+  }
   vm_wait4<4 + DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);    // tile 0 and bias 0 are in (bias 1, tile 1 may be pending)
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
