@@ -498,6 +498,30 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       using T = decltype(elt);
       const T* mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + (rowok ? i : 0) * p.ms[1];
       uint64_t any = 0;
+      if (sizeof(T) == 1 && p.mask && p.ms[2] == 1 && (reinterpret_cast<uintptr_t>(mrow) & 15) == 0) {
+        // contiguous u8 keys: lane l reads keys 16 l .. 16 l + 15 of each 1024-key block with one 16-byte load and writes
+        // their keep bits as the 16-bit piece l of the block's words (bit k of piece j = key 16 j + k, the ballot layout)
+        uint16_t* kw16 = reinterpret_cast<uint16_t*>(&sKeepAll[wave][0]);
+        uint32_t anyl = 0;
+        for (int c0 = 0; c0 < (int)p.S; c0 += 1024) {
+          const int key = c0 + 16 * l;
+          uint32_t bits = 0;
+          if (rowok && key < (int)p.S) {
+            const u32x4 m = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(mrow) + key);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              uint32_t t = m[e] | (m[e] >> 1);           // the low bit of each byte: byte != 0
+              t |= t >> 2;
+              t |= t >> 4;
+              t &= 0x01010101u;
+              bits |= ((t * 0x01020408u) >> 24 & 0xfu) << (4 * e);   // gathers the 4 byte flags, key order
+            }
+          }
+          if (key < (int)p.S) kw16[key >> 4] = (uint16_t)bits;
+          anyl |= bits;
+        }
+        any = __ballot(anyl != 0);
+      } else
       for (int c0 = 0; c0 < nw; c0 += 16) {
         T raw[16];
 #pragma unroll

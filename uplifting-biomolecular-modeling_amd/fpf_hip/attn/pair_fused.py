@@ -82,7 +82,13 @@ def _wpack(W, dtype, device):
     return p
 
 
+_MASK_U8 = {}
+
+
 def _pair_mask(mask, z4):
+    """The pair mask as the kernels take it: u8 (nonzero = keep), contiguous [B, N, N].  A non-bool mask is converted once and
+    the copy kept while the same tensor (same object, unmodified) comes back -- a pair stack passes one mask to every
+    block -- because the core builds its key table from contiguous u8 rows with one 16-byte load per 16 keys."""
     if mask is None:
         return None, L.DT_U8
     B, N = z4.shape[0], z4.shape[1]
@@ -91,9 +97,12 @@ def _pair_mask(mask, z4):
         raise Unsupported("mask-shape", str(tuple(mask.shape)))
     if m.dtype == torch.bool:
         return m.contiguous().view(torch.uint8), L.DT_U8
-    if m.dtype == torch.float32:
-        return m.contiguous(), L.DT_F32
-    return (m != 0).contiguous().view(torch.uint8), L.DT_U8
+    hit = _MASK_U8.get("m")
+    if hit is not None and hit[0] is mask and hit[1] == mask._version:
+        return hit[2], L.DT_U8
+    u8 = (m != 0).contiguous().view(torch.uint8)
+    _MASK_U8["m"] = (mask, mask._version, u8)           # holding the tensor keeps its storage from being reused
+    return u8, L.DT_U8
 
 
 def _block_check(z, W, word, face):
