@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 3   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd */
+#define FPF_ABI_VERSION 4   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
 enum {
@@ -181,6 +181,8 @@ typedef struct {
   int64_t rows;
   const float* bias_in;    /* NULL: the block computes the bias; else the full [B, H, N, N] fp32 bias of fpf_triattn_bias_fwd
                               (required with a row range: every attention row needs the bias of every pair) */
+  int32_t mask_frame;      /* 0: mask in z's frame (the ending node reads its columns); 1: mask already in the attention
+                              frame (for the ending node the transposed pair mask, so every key row is contiguous) */
 } FpfTriattnBlockArgs;
 /* Workspace for `rows` attention rows (rows <= 0: all N). */
 size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_t rows, int32_t C, int32_t H, int32_t D, int32_t dtype);

@@ -1498,8 +1498,9 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   // key mask of attention row i: z-frame pair mask row i (starting) / column i (ending), rows from row0
   c.mask_dtype = a->mask_dtype;
   c.mask_stride[0] = N * N;
-  c.mask_stride[1] = a->ending ? 1 : N;
-  c.mask_stride[2] = a->ending ? N : 1;
+  const bool by_col = a->ending && !a->mask_frame;
+  c.mask_stride[1] = by_col ? 1 : N;
+  c.mask_stride[2] = by_col ? N : 1;
   c.mask = a->mask ? static_cast<const char*>(a->mask) + row0 * c.mask_stride[1] * (a->mask_dtype == FPF_DT_F32 ? 4 : 1) : nullptr;
   c.out = o;
   c.scale = dma_core ? 1.0f : scale;

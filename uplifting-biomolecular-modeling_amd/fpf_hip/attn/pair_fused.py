@@ -85,24 +85,25 @@ def _wpack(W, dtype, device):
 _MASK_U8 = {}
 
 
-def _pair_mask(mask, z4):
-    """The pair mask as the kernels take it: u8 (nonzero = keep), contiguous [B, N, N].  A non-bool mask is converted once and
-    the copy kept while the same tensor (same object, unmodified) comes back -- a pair stack passes one mask to every
-    block -- because the core builds its key table from contiguous u8 rows with one 16-byte load per 16 keys."""
+def _pair_mask(mask, z4, ending=False):
+    """The pair mask as the kernels take it: u8 (nonzero = keep), contiguous, in the attention frame (the ending node gets the
+    transposed mask, mask_frame 1, so each attention row's keys are contiguous) -> (tensor, dtype, mask_frame).  The copies
+    are made once and kept while the same tensor (same object, unmodified) comes back -- a pair stack passes one mask to
+    every block -- because the core builds its key table from contiguous u8 rows with one 16-byte load per 16 keys."""
     if mask is None:
-        return None, L.DT_U8
+        return None, L.DT_U8, 0
     B, N = z4.shape[0], z4.shape[1]
     m = mask if mask.dim() == 3 else mask.unsqueeze(0)
     if tuple(m.shape) != (B, N, N):
         raise Unsupported("mask-shape", str(tuple(mask.shape)))
-    if m.dtype == torch.bool:
-        return m.contiguous().view(torch.uint8), L.DT_U8
-    hit = _MASK_U8.get("m")
+    key = "t" if ending else "m"
+    hit = _MASK_U8.get(key)
     if hit is not None and hit[0] is mask and hit[1] == mask._version:
-        return hit[2], L.DT_U8
-    u8 = (m != 0).contiguous().view(torch.uint8)
-    _MASK_U8["m"] = (mask, mask._version, u8)           # holding the tensor keeps its storage from being reused
-    return u8, L.DT_U8
+        return hit[2], L.DT_U8, 1
+    mm = m.transpose(1, 2) if ending else m
+    u8 = (mm != 0).contiguous().view(torch.uint8)
+    _MASK_U8[key] = (mask, mask._version, u8)           # holding the tensor keeps its storage from being reused
+    return u8, L.DT_U8, 1
 
 
 def _block_check(z, W, word, face):
@@ -220,7 +221,7 @@ def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None,
     """The fused block; returns the update in z's frame (residual=False) or z updated in place (residual=True)."""
     z4, sel = _block_check(z, W, word, "tri_attn_block")
     B, N = int(z4.shape[0]), int(z4.shape[1])
-    m, mdt = _pair_mask(mask, z4)
+    m, mdt, mframe = _pair_mask(mask, z4, ending)
     wqkvg, wb, wo = _wpack(W, z.dtype, z.device)
     dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
     need = L.lib().fpf_triattn_block_workspace_bytes(B, N, 0, W.C, W.H, W.D, dt)
@@ -232,7 +233,7 @@ def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None,
     a = L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=dt, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m), mask_dtype=mdt,
                            ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), w_o=L.ptr(wo),
                            ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out), scale=float(scale or 0.0),
-                           workspace=L.ptr(ws), workspace_bytes=ws.numel())
+                           workspace=L.ptr(ws), workspace_bytes=ws.numel(), mask_frame=mframe)
     try:
         L.call("fpf_triattn_block_fwd", a, L.stream_ptr(z.device))
     except L.LibError as e:
@@ -257,7 +258,7 @@ def tri_attn_block_chunked(z, W, mask=None, *, ending=False, residual=False, chu
     if chunk <= 0:
         raise Unsupported("chunk:%d" % chunk)
     B, N = int(z4.shape[0]), int(z4.shape[1])
-    m, mdt = _pair_mask(mask, z4)
+    m, mdt, mframe = _pair_mask(mask, z4, ending)
     wqkvg, wb, wo = _wpack(W, z.dtype, z.device)
     rows = min(chunk, N)
     lib = L.lib()
@@ -283,7 +284,7 @@ def tri_attn_block_chunked(z, W, mask=None, *, ending=False, residual=False, chu
                                mask_dtype=mdt, ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb),
                                w_o=L.ptr(wo), ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out),
                                scale=float(scale or 0.0), workspace=L.ptr(ws), workspace_bytes=ws.numel(), row0=r0, rows=min(rows, N - r0),
-                               bias_in=L.ptr(bias))
+                               bias_in=L.ptr(bias), mask_frame=mframe)
         try:
             L.call("fpf_triattn_block_fwd", a, stream)
         except L.LibError as e:
