@@ -64,6 +64,7 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
     const bool live = P < N && Q < N;
     const int64_t pix = (b * N + (outgoing ? P : Q)) * N + (outgoing ? Q : P);
     const float m = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
+    const bool ones = __builtin_amdgcn_ballot_w64(m != 1.0f) == 0;   // every pixel of the tile kept: no mask products
     bf16x8 xb[8];
     rt_ln(raw, g, sLN, eps, xb);
     if (t + stride < total) fetch(t + stride);
@@ -89,10 +90,18 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
       f32x16 acc[4];
       rt_gemm32_multi_xw<4>(ws, cb * 32, n, g, xb, acc);
       f32x16 va, vb;
+      if (ones) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        va[v] = mv[v] * sigmoidf_(acc[1][v]) * acc[0][v];
-        vb[v] = mv[v] * sigmoidf_(acc[3][v]) * acc[2][v];
+        for (int v = 0; v < 16; ++v) {
+          va[v] = sigmoidf_(acc[1][v]) * acc[0][v];
+          vb[v] = sigmoidf_(acc[3][v]) * acc[2][v];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          va[v] = mv[v] * sigmoidf_(acc[1][v]) * acc[0][v];
+          vb[v] = mv[v] * sigmoidf_(acc[3][v]) * acc[2][v];
+        }
       }
       const int64_t c = cb * 32 + n;
       u32x4 lo, hi;
