@@ -182,7 +182,8 @@ typedef struct {
   const float* bias_in;    /* NULL: the block computes the bias; else the full [B, H, N, N] fp32 bias of fpf_triattn_bias_fwd
                               (required with a row range: every attention row needs the bias of every pair) */
   int32_t mask_frame;      /* 0: mask in z's frame (the ending node reads its columns); 1: mask already in the attention
-                              frame (for the ending node the transposed pair mask, so every key row is contiguous) */
+                              frame (for the ending node the transposed pair mask, so every key row is contiguous); other values:
+                              FPF_E_ARGS */
 } FpfTriattnBlockArgs;
 /* Workspace for `rows` attention rows (rows <= 0: all N). */
 size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_t rows, int32_t C, int32_t H, int32_t D, int32_t dtype);

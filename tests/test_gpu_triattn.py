@@ -158,6 +158,51 @@ def test_block_bf16(ending, N, pad):
     assert_bf16_residual_close(zz, z.float() + ref, "block residual ending=%s" % ending)
 
 
+def _block_abi(z4, W, m, mdt, mframe, ending):
+    """fpf_triattn_block_fwd called directly with a caller-chosen mask tensor, dtype and frame."""
+    from fpf_hip import _lib as L
+    from fpf_hip.attn import pair_fused as PF
+    B, N = int(z4.shape[0]), int(z4.shape[1])
+    wqkvg, wb, wo = PF._wpack(W, z4.dtype, z4.device)
+    ws = torch.empty(L.lib().fpf_triattn_block_workspace_bytes(B, N, 0, W.C, W.H, W.D, L.DT_BF16), dtype=torch.uint8, device=z4.device)
+    out = torch.empty_like(z4)
+    a = L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m), mask_dtype=mdt,
+                           ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), w_o=L.ptr(wo),
+                           ending=int(ending), residual=0, out=L.ptr(out), scale=0.0, workspace=L.ptr(ws), workspace_bytes=ws.numel(),
+                           mask_frame=mframe)
+    L.call("fpf_triattn_block_fwd", a, L.stream_ptr(z4.device))
+    return out
+
+
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("N", [100, 128])
+def test_block_bf16_mask_frames_asymmetric_mask(ending, N):
+    """An asymmetric pair mask (a transposed key mask would be caught, unlike the symmetric padding masks above) given in
+    the z frame (mask_frame 0, u8 and fp32: the ending node reads key k of row i at mask[k, i]) is bitwise the attention-frame
+    u8 mask the pair stack passes (mask_frame 1), and all match the oracle.  N = 128 takes the 64-key DMA core with the
+    16-byte keep-table loads; N = 100 the generic core."""
+    from fpf_hip import _lib as L
+    from fpf_hip.attn import pair_fused as PF
+    P = _block_weights(torch.bfloat16, seed=3)
+    W = _pack(P, torch.bfloat16)
+    g = torch.Generator().manual_seed(N + 7)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16)
+    mask = (torch.rand(1, N, N, generator=g) > 0.3).float()
+    mask[:, :, N - 5:] = 0                               # whole key columns off on one side only
+    print("[case] mask frames ending=%s N=%d" % (ending, N), flush=True)
+    zd, md = z.to(DEV), mask.to(DEV)
+    u = PF.tri_attn_block(zd, W, md, ending=ending, residual=False)
+    u_z8 = _block_abi(zd, W, (md != 0).view(torch.uint8).contiguous(), L.DT_U8, 0, ending)
+    u_zf = _block_abi(zd, W, md.contiguous(), L.DT_F32, 0, ending)
+    torch.cuda.synchronize()
+    assert torch.equal(u.view_as(u_z8), u_z8), "z-frame u8 mask differs from the attention-frame mask"
+    assert torch.equal(u_z8, u_zf), "u8 and fp32 z-frame masks differ"
+    ref = S.tri_attn(z.float(), P, mask, ending=ending, dtype=torch.float32)
+    assert_bf16_close(u, ref, "block asymmetric mask ending=%s N%d" % (ending, N))
+    with pytest.raises(L.LibError):
+        _block_abi(zd, W, md.contiguous(), L.DT_F32, 2, ending)
+
+
 @pytest.mark.parametrize("ending", [False, True])
 def test_block_fp32_exact(ending):
     from fpf_hip.attn import pair_fused as PF

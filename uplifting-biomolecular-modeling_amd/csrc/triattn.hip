@@ -1444,6 +1444,7 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   if (a->B <= 0 || a->N <= 0) return a->B == 0 || a->N == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "negative extent");
   if (a->residual && a->out != a->z) return fail(err, errlen, FPF_E_ARGS, "residual form updates z in place: out must be z");
   if (a->mask && !(a->mask_dtype == FPF_DT_U8 || a->mask_dtype == FPF_DT_F32)) return fail(err, errlen, FPF_E_DTYPE, "mask_dtype %d", a->mask_dtype);
+  if (a->mask_frame != 0 && a->mask_frame != 1) return fail(err, errlen, FPF_E_ARGS, "mask_frame %d (0: z frame, 1: attention frame)", a->mask_frame);
   const int64_t B = a->B, N = a->N, H = a->H, D = a->D, HD = H * D;
   const int64_t R = a->rows > 0 ? a->rows : N, row0 = a->row0;
   if (row0 < 0 || row0 + R > N) return fail(err, errlen, FPF_E_SHAPE, "rows [%lld, %lld) outside [0, %lld)", (long long)row0, (long long)(row0 + R), (long long)N);
