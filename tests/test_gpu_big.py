@@ -46,14 +46,21 @@ def _ragged_mask(N, chains, pad):
 @pytest.mark.parametrize("ending", [False, True])
 @pytest.mark.parametrize("residual", [False, True])
 @pytest.mark.parametrize("chunk", [64, 7])
-def test_chunked_block_bitwise_equals_whole(ending, residual, chunk):
+@pytest.mark.parametrize("asym", [False, True])
+def test_chunked_block_bitwise_equals_whole(ending, residual, chunk, asym):
+    """asym: the ragged mask times a random keep pattern, so a chunk that offset the wrong axis of the (transposed, for the
+    ending node) mask would differ from the whole-tensor block."""
     from fpf_hip.attn import pair_fused as PF
     N = 300
     P = _ta_weights(3)
     W = _ta_pack(P)
-    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(31)).to(torch.bfloat16).to(DEV)
-    mask = _ragged_mask(N, (150, 90, 40), 20).unsqueeze(0).to(DEV)
-    print("[big] N=%d chunk=%d ending=%s residual=%s" % (N, chunk, ending, residual), flush=True)
+    g = torch.Generator().manual_seed(31)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(DEV)
+    mask = _ragged_mask(N, (150, 90, 40), 20).unsqueeze(0)
+    if asym:
+        mask = mask * (torch.rand(1, N, N, generator=g) > 0.25).float()
+    mask = mask.to(DEV)
+    print("[big] N=%d chunk=%d ending=%s residual=%s asym=%s" % (N, chunk, ending, residual, asym), flush=True)
     z1, z2 = z.clone(), z.clone()
     u1 = PF.tri_attn_block(z1, W, mask, ending=ending, residual=residual)
     u2 = PF.tri_attn_block_chunked(z2, W, mask, ending=ending, residual=residual, chunk=chunk)
