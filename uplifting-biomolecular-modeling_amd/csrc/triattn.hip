@@ -343,7 +343,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 //     counts (the memory counter retires in order), so no wait covers a load that is not needed yet;
 //   * the keep bits of all keys of the TA_R rows are built once (LDS table), so the key loop reads no mask.
 constexpr int TA_NB = 3;                                 // K / V^T tile buffers of the block-layout core
-constexpr int TA_DMA_WAVES = 4;                          // waves (32 queries each) per workgroup of the block-layout core
+constexpr int TA_DMA_WAVES = 8;                          // waves (32 queries each) per workgroup of the block-layout core:
+                                                         // 8 share each K / V^T tile among 256 queries (4 move K, 4 V^T)
 constexpr float TD_PS_MAX = 18446744073709551616.0f;     // 2^64: a sub-tile's partial row sum at or above it moves the reference
 constexpr float TD_BAND = 32.0f;                         // first live sub-tile: a max outside +-TD_BAND (log2 units) sets it
 constexpr float TD_MOVE = 48.0f;                         // later sub-tiles: a max more than TD_MOVE above it moves it
@@ -1215,9 +1216,16 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
       if (!p.bias_vec || p.S % TA_KT != 0 || p.S > 64 * TA_MAXW || p.vs[3] % 8 != 0)
         return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
       if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
-      constexpr int NW = TA_DMA_WAVES;
-      const int64_t total_w = a->B * a->H * cdiv(a->N, TA_R) * cdiv(a->S, 32 * NW);
-      hipLaunchKernelGGL(triattn_core_bf16_dma<NW>, dim3((unsigned)(cdiv(total_w, 8) * 8)), dim3(64 * NW), 0, st, p);
+      // 8 waves share each K / V^T tile among 256 queries; they pay where S fills whole 256-query tiles and the grid still
+      // has at least 8 workgroups per CU (N = 768: 3072; N = 512: 1368, where 4 waves and twice the workgroups are faster)
+      const int64_t rows_heads = a->B * a->H * cdiv(a->N, TA_R);
+      if (p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * 256) {
+        const int64_t total_w = rows_heads * (p.S / (32 * TA_DMA_WAVES));
+        hipLaunchKernelGGL(triattn_core_bf16_dma<TA_DMA_WAVES>, dim3((unsigned)(cdiv(total_w, 8) * 8)), dim3(64 * TA_DMA_WAVES), 0, st, p);
+      } else {
+        const int64_t total_w = rows_heads * cdiv(p.S, 128);
+        hipLaunchKernelGGL(triattn_core_bf16_dma<4>, dim3((unsigned)(cdiv(total_w, 8) * 8)), dim3(256), 0, st, p);
+      }
       return launched(err, errlen, "triattn_core_bf16_dma");
     }
     if (p.v_t && p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<true, true>), grid, block, 0, st, p);
