@@ -23,7 +23,8 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 4   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame */
+#define FPF_ABI_VERSION 5   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+                               5: gate / output projection biases b_g, b_o on the tri-att block and its stages */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
 enum {
@@ -184,6 +185,8 @@ typedef struct {
   int32_t mask_frame;      /* 0: mask in z's frame (the ending node reads its columns); 1: mask already in the attention
                               frame (for the ending node the transposed pair mask, so every key row is contiguous); other values:
                               FPF_E_ARGS */
+  const float* b_g;        /* [H*D] gate projection bias (g = x_ln W_g^T + b_g, before the sigmoid) or NULL; pair_fused.py:731-736 */
+  const float* b_o;        /* [C] output projection bias (u = (sigmoid(g) o) W_o^T + b_o) or NULL; pair_fused.py:738 */
 } FpfTriattnBlockArgs;
 /* Workspace for `rows` attention rows (rows <= 0: all N). */
 size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_t rows, int32_t C, int32_t H, int32_t D, int32_t dtype);
@@ -234,6 +237,7 @@ typedef struct {
   int64_t v_ld;            /* bf16: elements between V^T rows, >= N rounded up to 32 and a multiple of 8; fp32: ignored */
   void* g;                 /* [B, I, J, H*D] pre-sigmoid */
   float* bias;             /* [B, H, I, J] fp32 (the [B,1,H,I,J] operand without its unit axis) */
+  const float* b_g;        /* [H*D] gate projection bias added to g, or NULL */
 } FpfTriattnPrologueArgs;
 int fpf_triattn_prologue_fwd(const FpfTriattnPrologueArgs* a, void* stream, char* err, size_t errlen);
 
@@ -248,6 +252,7 @@ typedef struct {
   int32_t ending;
   int32_t residual;        /* 1: out is z and z += u in place */
   void* out;               /* [B, N, N, C] in z's frame */
+  const float* b_o;        /* [C] output projection bias added to u, or NULL */
 } FpfTriattnEpilogueArgs;
 int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* stream, char* err, size_t errlen);
 

@@ -74,13 +74,25 @@ def test_workspace_queries_need_no_device():
     # trimul: 3 channel-major bf16 planes of Np^2, Np = ceil(N / 128) * 128
     assert lib.fpf_trimul_workspace_bytes(1, 768, 128, 128, L.DT_BF16) >= 3 * 128 * 768 * 768 * 2
     assert lib.fpf_trimul_workspace_bytes(1, 100, 128, 128, L.DT_BF16) >= 3 * 128 * 128 * 128 * 2
-    # tri-att block: q, k, v, o, g (H*D per pixel) + fp32 bias (H per pixel)
+    # tri-att block: q, k, v, o (H*D per pixel; the bf16 epilogue recomputes g) + fp32 bias (H per pixel); fp32 adds g
     need = lib.fpf_triattn_block_workspace_bytes(1, 768, 0, 128, 4, 32, L.DT_BF16)
-    assert need >= 5 * 768 * 768 * 128 * 2 + 768 * 768 * 4 * 4
-    assert lib.fpf_triattn_block_workspace_bytes(1, 768, 0, 128, 4, 32, L.DT_F32) > need
-    # a row chunk holds the q / k / v / o / g of its rows only (plus the full bias)
+    assert 4 * 768 * 768 * 128 * 2 + 768 * 768 * 4 * 4 <= need < 5 * 768 * 768 * 128 * 2
+    assert lib.fpf_triattn_block_workspace_bytes(1, 768, 0, 128, 4, 32, L.DT_F32) >= 5 * 768 * 768 * 128 * 4
+    # a row chunk holds the q / k / v / o of its rows only (plus the full bias)
     part = lib.fpf_triattn_block_workspace_bytes(1, 2048, 256, 128, 4, 32, L.DT_BF16)
-    assert 5 * 256 * 2048 * 128 * 2 <= part < 5 * 300 * 2048 * 128 * 2 + 2048 * 2048 * 4 * 4 + 4096
+    assert 4 * 256 * 2048 * 128 * 2 <= part < 4 * 300 * 2048 * 128 * 2 + 2048 * 2048 * 4 * 4 + 4096
+
+
+def test_integration_stub_sends_the_header_version():
+    """The ctypes stubs in INTEGRATION.md must not pin an ABI version other than the header's: every literal
+    abi_version / fpf_abi_version() comparison there equals FPF_ABI_VERSION, which equals the binding's ABI_VERSION."""
+    from fpf_hip import _lib as L
+    hdr = int(re.search(r"#define FPF_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert hdr == L.ABI_VERSION
+    txt = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    lits = [int(x) for x in re.findall(r"abi_version\s*=\s*(\d+)", txt)] + [int(x) for x in re.findall(r"fpf_abi_version\(\)\s*==\s*(\d+)", txt)]
+    assert all(v == hdr for v in lits), lits
+    assert "abi_version=ABI" in txt and "fpf_abi_version()" in txt
 
 
 def test_version_mismatch_is_refused_before_any_launch():

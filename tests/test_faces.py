@@ -72,9 +72,12 @@ def test_trimul_select_and_weight_vocabulary():
 
 def test_ln_select_cols_gate():
     from fpf_hip.kernels import ln as LN
-    assert LN.select(torch.bfloat16, "gfx950", word="fast", cols=128).row == "hip_gfx950"
+    assert LN.select((9, 5), torch.bfloat16, None, 768, word="fast", C=128).row == "hip_gfx950"
     with pytest.raises(LN.Refusal):
-        LN.select(torch.bfloat16, "gfx950", word="fast", cols=2048)
+        LN.select("9.5", torch.bfloat16, None, 768, word="fast", C=2048)
+    with pytest.raises(LN.Refusal) as e:
+        LN.select("9.5", "bf16", None, 768, word="fast", C=128, pass_="bwd")
+    assert e.value.kind == "no_backward"
 
 
 def test_cpu_tensors_are_refused_by_name_before_any_launch():
@@ -93,9 +96,15 @@ def test_cpu_tensors_are_refused_by_name_before_any_launch():
 def test_pair_fused_refuses_unsupported_packs():
     from fpf_hip.attn import pair_fused as PF
     w = torch.randn(128, 128)
+    Wb = PF.pack_triattn_weights(w_o=w, n_heads=4, head_dim=32, w_q=w, w_k=w, w_v=w, w_g=w, w_b=torch.randn(4, 128), b_o=torch.zeros(128),
+                                 b_g=torch.ones(128))
+    assert Wb.b_o is not None and Wb.b_g is not None
     with pytest.raises(PF.Unsupported) as e:
-        PF.pack_triattn_weights(w_o=w, n_heads=4, head_dim=32, w_q=w, w_k=w, w_v=w, w_g=w, w_b=torch.randn(4, 128), b_o=torch.zeros(128))
-    assert e.value.reason == "projection_bias"
+        PF.pack_triattn_weights(w_o=w, n_heads=4, head_dim=32, w_q=w, w_k=w, w_v=w, w_g=w, w_b=torch.randn(4, 128), b_g=torch.ones(129))
+    assert e.value.reason == "b_g-shape"
+    with pytest.raises(PF.Unsupported) as e:
+        PF.pack_triattn_weights(w_o=w, n_heads=4, head_dim=32, w_q=w, w_k=w, w_v=w, w_g=w, w_b=torch.randn(4, 128), b_o=torch.zeros(64))
+    assert e.value.reason == "b_o-shape"
     with pytest.raises(PF.Unsupported) as e:
         PF.pack_triattn_weights(w_o=w, n_heads=4, head_dim=32, w_q=w, w_k=w, w_v=w, w_g=None, w_b=torch.randn(4, 128))
     assert e.value.reason == "gate:none"
@@ -164,3 +173,157 @@ def test_exact_word_follows_the_measured_cell():
         assert TM.select("gfx950", torch.float32, 128, 128, n, "outgoing", word="hip_gfx950_f32").row == "hip_gfx950_f32"
         cell = C.lookup("triattn", C.triattn_key("fp32", 32, 4, n))
         assert (TA.select("gfx950", torch.float32, 32, 4, n, word="exact").row == "hip_gfx950_f32") == (cell["exact"] == "hip_gfx950_f32")
+
+
+# ------------------------------------------------------------------------------------------------------------- drop-in contract
+@pytest.mark.parametrize("cc", [(9, 5), [9, 5], "9.5", 9.5, "sm_95", "gfx950", "gfx950:sramecc+:xnack-"])
+def test_capability_forms_name_the_mi355x(cc):
+    from fpf_hip import _face as F
+    assert F.arch_word(cc) == "gfx950"
+
+
+def test_kit_trimul_probe_resolves_a_hip_selection():
+    """The boltz2 kit's probe (boltz2/opt/boltz2_opt/trimul.py:160-166): select(cc, "bf16", 128, 128, 512, d, word=..., stack=...)
+    then admits(sel.row, cc, "bf16", 128, 128, 512, backward=False, residual=False, batch=1, abi=None), with the capability ROCm
+    torch reports for an MI355X."""
+    from fpf_hip.kernels import trimul as KT
+    cc = (9, 5)
+    for d in ("outgoing", "incoming"):
+        sel = KT.select(cc, "bf16", 128, 128, 512, d, word="fast", stack=None)
+        assert sel.row == "hip_gfx950"
+        assert KT.admits(sel.row, cc, "bf16", 128, 128, 512, backward=False, residual=False, batch=1, abi=None) is None
+    with pytest.raises(KT.Refusal) as e:
+        KT.select((9, 0), "bf16", 128, 128, 512, "outgoing", word="fast")
+    assert e.value.kind == "arch:cc9.0"
+    with pytest.raises(KT.Refusal) as e:
+        KT.admits("hip_gfx950", cc, "bf16", 128, 128, 512, backward=True)
+    assert e.value.kind == "no_backward"
+    with pytest.raises(KT.Refusal) as e:
+        KT.select(cc, "bf16", 128, 128, 512, "outgoing", word="fast", exclude=("hip_gfx950",))
+    assert e.value.kind == "excluded:hip_gfx950"
+    assert KT.precision_word("bf16", "fp32") == "f32z_bf16" and KT.precision_word(torch.float32, tf32=True) == "tf32"
+    assert KT.select(cc, torch.float32, 128, 128, 100, "outgoing", word="hip_gfx950_f32", tf32=True).row == "hip_gfx950_f32"
+
+
+def test_select_keywords_are_served_or_refused_by_name():
+    from fpf_hip.kernels import triattn as TA
+    from fpf_hip.kernels import trimul as TM
+    assert TA.select("9.5", "bf16", 32, 4, 768, word="fast", prefer=("hip_gfx950",), stack="rocm7", form=None, lib=None).row == "hip_gfx950"
+    with pytest.raises(TA.Refusal) as e:                       # prefer narrows a tier word to rows this package does not have
+        TA.select("9.5", "bf16", 32, 4, 768, word="fast", prefer=("cuda_sm90a", "k2b"))
+    assert e.value.kind == "prefer_excludes:hip_gfx950"
+    with pytest.raises(TA.Refusal) as e:                       # a launch setting is refused, never ignored
+        TA.select((9, 5), "bf16", 32, 4, 768, word="fast", config={"BLOCK_M": 64})
+    assert e.value.kind == "config:fixed_launch"
+    with pytest.raises(TA.Refusal) as e:
+        TA.select((9, 5), "bf16", 32, 4, 768, word="hip_gfx950@bm64")
+    assert e.value.kind == "config_word:bm64"
+    assert TA.admits("hip_gfx950", (9, 5), "bf16", 32, 4, 768) == (True, "ok")
+    assert TA.admits("hip_gfx950", (9, 5), "bf16", 16, 4, 768) == (False, "no_row:head_dim16")
+    assert TA.admits("cuda_sm90a", (9, 5), "bf16", 32, 4, 768)[0] is False
+    with pytest.raises(TM.Refusal) as e:
+        TM.select((9, 5), "bf16", 128, 128, 400, "outgoing", word="fast", residency="fp32")
+    assert e.value.kind.startswith("precision:f32z_bf16") or e.value.kind == "precision:f32z_bf16"
+
+
+def test_kit_transition_select_and_ln_given_refusal():
+    """boltz2/opt/boltz2_opt/transition.py:149: select(word, c=, hidden=, n_tokens=, dtype="bf16", family=, residual=, mask=, cc=,
+    stack=, rows_count=, ln_given=)."""
+    from fpf_hip.kernels import transition as KT
+    sel = KT.select("fast", c=128, hidden=512, n_tokens=768, dtype="bf16", family="pair", residual=False, mask=False, cc=(9, 5), stack=None,
+                    rows_count=768 * 768, ln_given=False)
+    assert sel.row == "hip_gfx950"
+    with pytest.raises(KT.Refusal) as e:
+        KT.select("fast", c=128, hidden=512, n_tokens=768, dtype="bf16", cc=(9, 5), ln_given=True)
+    assert e.value.kind == "ln_given"
+    with pytest.raises(KT.Refusal) as e:
+        KT.select("fast", c=128, hidden=512, dtype="bf16", cc=(9, 5), form="geglu")
+    assert e.value.kind == "form:geglu"
+
+
+def _pack_small():
+    from fpf_hip.attn import pair_fused as PF
+    w = torch.randn(128, 128)
+    return PF.pack_triattn_weights(w_o=w, n_heads=4, head_dim=32, w_q=w, w_k=w, w_v=w, w_g=w, w_b=torch.randn(4, 128))
+
+
+@pytest.mark.parametrize("kw,reason", [
+    (dict(ln="stock", x_ln=torch.zeros(1, 8, 8, 128)), "ln:stock"),
+    (dict(x_ln=torch.zeros(1, 8, 8, 128)), "ln:stock"),
+    (dict(impl="torch"), "impl:torch"),
+    (dict(core="flash_triattn"), "core:flash_triattn"),
+    (dict(core="k2b"), "core:k2b"),
+    (dict(bias_frame="q"), "bias_frame:q"),
+    (dict(variant="v3"), "variant:v3"),
+])
+def test_block_keywords_not_served_are_refused_by_name(kw, reason):
+    """Nothing is swallowed: an exact-construction or foreign-core call is refused before any launch (these run on host
+    tensors, so a call that got past the keyword gate would be refused 'arch:cpu' instead)."""
+    from fpf_hip.attn import pair_fused as PF
+    W = _pack_small()
+    with pytest.raises(PF.Unsupported) as e:
+        PF.tri_attn_block(torch.randn(1, 8, 8, 128), W, **kw)
+    assert e.value.reason == reason
+    T = PF.pack_transition_weights(w_out=torch.randn(128, 512), w_a=torch.randn(512, 128), w_b=torch.randn(512, 128))
+    with pytest.raises(PF.Unsupported) as e:
+        PF.transition(torch.randn(1, 8, 8, 128), T, ln="stock", x_ln=torch.randn(1, 8, 8, 128))
+    assert e.value.reason == "ln:stock"
+    with pytest.raises(PF.Unsupported) as e:
+        PF.transition(torch.randn(1, 8, 8, 128), T, variant="v1")
+    assert e.value.reason == "variant:v1"
+    with pytest.raises(PF.Unsupported) as e:
+        PF.prologue(torch.randn(1, 8, 8, 128), W, write_x=True)
+    assert e.value.reason == "write_x"
+
+
+def test_core_attention_hands_a_callable_core_a_unit_stride_v():
+    from fpf_hip.attn import pair_fused as PF
+    q = torch.randn(1, 2, 4, 8, 32)
+    vs = torch.randn(1, 2, 4, 32, 8)
+    v = vs.transpose(-1, -2)                                   # the prologue's transposed V^T view
+    seen = {}
+
+    def core(q_, k_, v_, b_, m_, sc):
+        seen["stride"] = v_.stride(-1)
+        seen["equal"] = torch.equal(v_, v)
+        return q_
+    PF.core_attention(q, q, v, torch.zeros(1, 1, 4, 8, 8), None, core=core)
+    assert seen == {"stride": 1, "equal": True}
+
+
+def test_pair_mask_under_inference_mode_and_on_another_device():
+    """A mask made under torch.inference_mode() has no version counter: converted on every call, never cached; a mask on another
+    device is moved to z's device before any launch (a meta z stands in for the GPU here)."""
+    from fpf_hip.attn import pair_fused as PF
+    z4 = torch.zeros(1, 6, 6, 128)
+    with torch.inference_mode():
+        m = torch.ones(1, 6, 6)
+        m[:, :, 4:] = 0
+        u8, dt, frame = PF._pair_mask(m, z4, ending=True)
+        u8b, _, _ = PF._pair_mask(m, z4, ending=True)
+    assert frame == 1 and u8.dtype == torch.uint8 and u8[0, 0].tolist() == [1, 1, 1, 1, 1, 1] and u8[0, 5].tolist() == [0] * 6
+    assert torch.equal(u8, u8b)
+    zm = torch.empty(1, 6, 6, 128, device="meta")
+    u8m, _, _ = PF._pair_mask(torch.ones(1, 6, 6), zm)
+    assert u8m.device.type == "meta"
+    km = PF._key_mask(torch.ones(1, 6, 6), zm, ending=False)
+    assert km.device.type == "meta"
+
+
+def test_shared_scratch_is_one_buffer_per_stream_sized_by_the_largest_call():
+    """The trunk holds ONE workspace for all its layers and sites: the largest of the per-call needs, not their sum."""
+    from fpf_hip import _face as F
+    from fpf_hip import _lib as L
+    F.release_scratch()
+    a = F.scratch("cpu", 100)
+    b = F.scratch("cpu", 50)
+    assert a.data_ptr() == b.data_ptr() and F.scratch_bytes("cpu") == 100
+    c = F.scratch("cpu", 300)
+    assert c.numel() == 300 and F.scratch_bytes("cpu") == 300
+    F.scratch("cpu", 10, kind="bias")
+    assert F.scratch_bytes("cpu") == 310
+    F.release_scratch()
+    lib = L.lib()
+    for N, cap in ((512, 3e9), (768, 3e9)):                  # 48 layers x (2 trimul + 2 tri-att): one buffer of the largest need
+        need = max(lib.fpf_trimul_workspace_bytes(1, N, 128, 128, L.DT_BF16), lib.fpf_triattn_block_workspace_bytes(1, N, 0, 128, 4, 32, L.DT_BF16))
+        assert need < cap, (N, need)

@@ -163,13 +163,13 @@ def _block_abi(z4, W, m, mdt, mframe, ending):
     from fpf_hip import _lib as L
     from fpf_hip.attn import pair_fused as PF
     B, N = int(z4.shape[0]), int(z4.shape[1])
-    wqkvg, wb, wo = PF._wpack(W, z4.dtype, z4.device)
+    wqkvg, wb, wo, bg, bo = PF._wpack(W, z4.dtype, z4.device)
     ws = torch.empty(L.lib().fpf_triattn_block_workspace_bytes(B, N, 0, W.C, W.H, W.D, L.DT_BF16), dtype=torch.uint8, device=z4.device)
     out = torch.empty_like(z4)
     a = L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m), mask_dtype=mdt,
                            ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), w_o=L.ptr(wo),
                            ending=int(ending), residual=0, out=L.ptr(out), scale=0.0, workspace=L.ptr(ws), workspace_bytes=ws.numel(),
-                           mask_frame=mframe)
+                           mask_frame=mframe, b_g=L.ptr(bg), b_o=L.ptr(bo))
     L.call("fpf_triattn_block_fwd", a, L.stream_ptr(z4.device))
     return out
 

@@ -816,6 +816,7 @@ struct ProParams {
   float bias_scale;              // and the bias times this (log2(e) for the block-layout core: logits in log2 units)
   int64_t bias_ld;               // elements between bias rows (>= N)
   int bias_bf16;                 // bias stored as bf16 (else fp32)
+  const float* b_g;              // [HD] gate projection bias added to g, or NULL
 };
 
 __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
@@ -872,6 +873,10 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
       }
       f32x16 acc = rt_gemm32(sW, blk * 32, n, g, xb);
       if (blk < 4 && p.q_scale != 1.0f) acc *= p.q_scale;
+      if (blk >= 12 && blk < 16 && p.b_g) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] += p.b_g[(blk - 12) * 32 + c_row(v, g)];
+      }
       if (blk < 16) {                                     // q | k | g
         u32x4 lo, hi;
         rt_pack16(acc, lo, hi);
@@ -898,8 +903,8 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
 // u = (sigmoid(g) * o) W_o^T; residual: z[i,j] += u (ending: z[j,i] += u) in place; else out[zpix] = u.  Persistent: W_o lives in
 // LDS; a wave owns 32 positions of one attention row.
 __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __restrict__ o, const uint16_t* __restrict__ gt,
-                                                             const uint16_t* __restrict__ w_o, int H, uint16_t* zout, int64_t N, int64_t B,
-                                                             int ending, int residual) {
+                                                             const uint16_t* __restrict__ w_o, const float* __restrict__ b_o, int H, uint16_t* zout,
+                                                             int64_t N, int64_t B, int ending, int residual) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[RT_C * RT_LD];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   rt_stage_weights(sW, w_o, RT_C, RT_C, tid, 512);
@@ -930,7 +935,11 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
     uint16_t* zp = zout + zpix * RT_C + 8 * g;
 #pragma unroll 1
     for (int cb = 0; cb < 4; ++cb) {
-      const f32x16 acc = rt_gemm32(sW, cb * 32, n, g, xb);
+      f32x16 acc = rt_gemm32(sW, cb * 32, n, g, xb);
+      if (b_o) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] += b_o[cb * 32 + c_row(v, g)];
+      }
       // lane (n, g) stores channels cb*32 + 8g .. +7 and cb*32 + 16 + 8g .. +7 of pixel n: two 16-byte stores
       if (residual) {
         float y[16];
@@ -966,13 +975,17 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
 __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t* zin, const uint16_t* __restrict__ o,
                                                                   const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
                                                                   const uint16_t* __restrict__ w_g, const uint16_t* __restrict__ w_o,
+                                                                  const float* __restrict__ b_g, const float* __restrict__ b_o,
                                                                   uint16_t* zout, int64_t N, int64_t B, int64_t row0, int64_t rows, int ending,
                                                                   int residual) {
   __shared__ __attribute__((aligned(16))) uint16_t sWg[RT_C * RT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t sWo[RT_C * RT_LD];   // columns permuted to the k-step order above
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
+  __shared__ __attribute__((aligned(16))) float sBias[2 * RT_C];        // [b_g 128 | b_o 128] (zeros when absent)
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   rt_stage_affine(sLN, ln_w, ln_b, tid, 512);
+  const bool has_bg = b_g != nullptr, has_bo = b_o != nullptr;
+  for (int i = tid; i < 2 * RT_C; i += 512) sBias[i] = i < RT_C ? (has_bg ? b_g[i] : 0.f) : (has_bo ? b_o[i - RT_C] : 0.f);
   rt_stage_weights(sWg, w_g, RT_C, RT_C, tid, 512);
   for (int q = tid; q < RT_C * RT_C; q += 512) {
     const int m = q >> 7, kp = q & 127;
@@ -1020,7 +1033,11 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
     for (int k = 0; k < 4; ++k) acc[k] = f32x16{};
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
-      const f32x16 gacc = rt_gemm32_la<1>(sWg, cb * 32, n, g, xb);   // g of head cb: channels cb*32 + c_row(v, g)
+      f32x16 gacc = rt_gemm32_la<1>(sWg, cb * 32, n, g, xb);         // g of head cb: channels cb*32 + c_row(v, g)
+      if (has_bg) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) gacc[v] += sBias[cb * 32 + c_row(v, g)];
+      }
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         const u32x2 o0 = ov2[cb][half][0], o1 = ov2[cb][half][1];
@@ -1044,6 +1061,10 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
       float y[16];
       rt_regroup_f32(acc[blk], y);
       if (!live) continue;
+      if (has_bo) {                                                // y[8 h2 + e] is channel blk*32 + 16 h2 + 8g + e
+#pragma unroll
+        for (int e = 0; e < 16; ++e) y[e] += sBias[RT_C + blk * 32 + 16 * (e >> 3) + 8 * g + (e & 7)];
+      }
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
         u32x4 w;
@@ -1072,7 +1093,8 @@ constexpr int PF_R = 32, PF_CC = 16, PF_CM = 128;
 __global__ void __launch_bounds__(256) triattn_prologue_f32(const float* __restrict__ z, const float* __restrict__ ln_w, const float* __restrict__ ln_b,
                                                             float eps, const float* __restrict__ w_qkvg, const float* __restrict__ w_b, int C, int H,
                                                             int D, float* __restrict__ qo, float* __restrict__ ko, float* __restrict__ vo,
-                                                            float* __restrict__ go, float* __restrict__ bo, int64_t N, int ending) {
+                                                            float* __restrict__ go, float* __restrict__ bo, int64_t N, int ending,
+                                                            const float* __restrict__ b_g) {
   __shared__ float xs[PF_R][PF_CM + 1];
   __shared__ float ws[PF_CC][PF_CM + 1];
   const int tid = threadIdx.x;
@@ -1125,7 +1147,7 @@ __global__ void __launch_bounds__(256) triattn_prologue_f32(const float* __restr
         float* dst = part == 0 ? qo : (part == 1 ? ko : vo);
         dst[(((b * N + i) * H + hh) * N + j) * D + d] = acc;
       } else if (ch < 4 * HD) {
-        go[((b * N + i) * N + j) * HD + (ch - 3 * HD)] = acc;
+        go[((b * N + i) * N + j) * HD + (ch - 3 * HD)] = b_g ? acc + b_g[ch - 3 * HD] : acc;
       } else {
         bo[((b * H + (ch - 4 * HD)) * N + i) * N + j] = acc;
       }
@@ -1134,7 +1156,8 @@ __global__ void __launch_bounds__(256) triattn_prologue_f32(const float* __restr
 }
 
 __global__ void __launch_bounds__(256) triattn_epilogue_f32(const float* __restrict__ o, const float* __restrict__ gt, const float* __restrict__ w_o,
-                                                            int C, int H, int D, float* zout, int64_t N, int ending, int residual) {
+                                                            const float* __restrict__ b_o, int C, int H, int D, float* zout, int64_t N, int ending,
+                                                            int residual) {
   __shared__ float xs[PF_R][PF_CM + 1];
   __shared__ float ws[PF_CC][PF_CM + 1];
   const int tid = threadIdx.x;
@@ -1169,6 +1192,7 @@ __global__ void __launch_bounds__(256) triattn_epilogue_f32(const float* __restr
       if (co >= C || !live) continue;
       float acc = 0.f;
       for (int hd = 0; hd < HD; ++hd) acc = fmaf(xs[r][hd], ws[sub * 2 + jj][hd], acc);
+      if (b_o) acc += b_o[co];
       float* p = zout + zpix * C + co;
       *p = residual ? *p + acc : acc;
     }
@@ -1311,7 +1335,8 @@ static bool block_layout2(int dtype, int64_t N) { return dtype == FPF_DT_BF16 &&
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
-                           int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f, int64_t bias_ld = -1, int bias_bf16 = 0) {
+                           int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f, int64_t bias_ld = -1, int bias_bf16 = 0,
+                           const float* b_g = nullptr) {
   if (rows < 0) rows = N;
   if (bias_ld < 0) bias_ld = N;
   if (dtype == FPF_DT_BF16) {
@@ -1344,6 +1369,7 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.bias_scale = bias_scale;
     p.bias_ld = bias_ld;
     p.bias_bf16 = bias_bf16;
+    p.b_g = b_g;
     if (!rt_tiles_ok(B * rows * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "prologue: 2^31 or more 32-pixel tiles");
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
@@ -1353,24 +1379,24 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output, q unscaled)");
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
-                     (const float*)w_b, C, H, D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N, ending);
+                     (const float*)w_b, C, H, D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N, ending, b_g);
   return launched(err, errlen, "triattn_prologue_f32");
 }
 
-static int epilogue_launch(int dtype, const void* o, const void* g, const void* w_o, int64_t B, int64_t N, int C, int H, int D, int ending,
-                           int residual, void* out, hipStream_t st, char* err, size_t errlen) {
+static int epilogue_launch(int dtype, const void* o, const void* g, const void* w_o, const float* b_o, int64_t B, int64_t N, int C, int H,
+                           int D, int ending, int residual, void* out, hipStream_t st, char* err, size_t errlen) {
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(o) || !aligned16(g) || !aligned16(w_o) || !aligned16(out))
       return fail(err, errlen, FPF_E_ALIGN, "epilogue operands must be 16-byte aligned");
     if (!rt_tiles_ok(B * N * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "epilogue: 2^31 or more 32-pixel tiles");
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
-    hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)o, (const uint16_t*)g, (const uint16_t*)w_o, H,
-                       (uint16_t*)out, N, B, ending, residual);
+    hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)o, (const uint16_t*)g, (const uint16_t*)w_o, b_o,
+                       H, (uint16_t*)out, N, B, ending, residual);
     return launched(err, errlen, "triattn_epilogue_bf16");
   }
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
-  hipLaunchKernelGGL(triattn_epilogue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)o, (const float*)g, (const float*)w_o, C, H, D,
-                     (float*)out, N, ending, residual);
+  hipLaunchKernelGGL(triattn_epilogue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)o, (const float*)g, (const float*)w_o, b_o, C,
+                     H, D, (float*)out, N, ending, residual);
   return launched(err, errlen, "triattn_epilogue_f32");
 }
 
@@ -1386,7 +1412,8 @@ extern "C" int fpf_triattn_prologue_fwd(const FpfTriattnPrologueArgs* a, void* s
   const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
   if (rc) return rc;
   return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending, a->q, a->k, a->v,
-                         a->v_ld, a->g, a->bias, static_cast<hipStream_t>(stream), err, errlen);
+                         a->v_ld, a->g, a->bias, static_cast<hipStream_t>(stream), err, errlen, PRO_QKV | PRO_G | PRO_BIAS, 0, -1, 1.0f, 1.0f, -1, 0,
+                         a->b_g);
 }
 
 extern "C" int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* stream, char* err, size_t errlen) {
@@ -1397,7 +1424,7 @@ extern "C" int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* s
   if (a->B == 0 || a->N == 0) return FPF_OK;
   const int rc = block_shape_check(a->dtype, a->B, a->C, a->H, a->D, err, errlen);
   if (rc) return rc;
-  return epilogue_launch(a->dtype, a->o, a->g, a->w_o, a->B, a->N, a->C, a->H, a->D, a->ending, a->residual, a->out,
+  return epilogue_launch(a->dtype, a->o, a->g, a->w_o, a->b_o, a->B, a->N, a->C, a->H, a->D, a->ending, a->residual, a->out,
                          static_cast<hipStream_t>(stream), err, errlen);
 }
 
@@ -1407,11 +1434,11 @@ extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_
   const size_t elt = dtype == FPF_DT_F32 ? 4 : 2;
   const size_t pix = (size_t)B * (size_t)N * (size_t)N;
   const size_t HD = (size_t)H * (size_t)D;
-  // q, k, v, o, g of `rows` attention rows (HD per pixel each; V^T rows padded to N rounded up to 32) + the full bias (H fp32
-  // per pixel), 256-byte aligned regions
+  // q, k, v, o (and g for fp32: the bf16 epilogue recomputes the gate) of `rows` attention rows (HD per pixel each; V^T rows
+  // padded to N rounded up to 32) + the full bias (H fp32 per pixel), 256-byte aligned regions
   const size_t r1 = ((size_t)B * rows * fpf::cdiv(N, 32) * 32 * HD * elt + 255) & ~(size_t)255;
   const size_t r2 = (pix * (size_t)H * 4 + 255) & ~(size_t)255;
-  return 5 * r1 + r2;
+  return (dtype == FPF_DT_F32 ? 5 : 4) * r1 + r2;
 }
 
 extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen) {
@@ -1471,8 +1498,9 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   const int64_t Jp = cdiv(N, 32) * 32;
   const size_t r1 = ((size_t)B * R * Jp * HD * elt + 255) & ~(size_t)255;
   char* w = static_cast<char*>(a->workspace);
-  void *q = w, *k = w + r1, *v = w + 2 * r1, *o = w + 3 * r1, *g = w + 4 * r1;
-  float* bias = a->bias_in ? const_cast<float*>(a->bias_in) : reinterpret_cast<float*>(w + 5 * r1);
+  const int regions = a->dtype == FPF_DT_F32 ? 5 : 4;  // q, k, v, o (+ g on the fp32 path)
+  void *q = w, *k = w + r1, *v = w + 2 * r1, *o = w + 3 * r1, *g = regions == 5 ? w + 4 * r1 : nullptr;
+  float* bias = a->bias_in ? const_cast<float*>(a->bias_in) : reinterpret_cast<float*>(w + regions * r1);
   const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)D);
   FpfTriattnArgs c{};
   c.abi_version = FPF_ABI_VERSION;
@@ -1516,7 +1544,7 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
   const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM : 0);
   int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
-                           bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f);
+                           bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f, -1, 0, a->b_g);
   if (rc) return rc;
   rc = core_launch(&c, st, err, errlen);
   if (rc) return rc;
@@ -1525,9 +1553,9 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
     if (!rt_tiles_ok(B * R * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "epilogue: 2^31 or more 32-pixel tiles");
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * R * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_epilogue_gate_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w, a->ln_b,
-                       a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, (uint16_t*)a->out, N, B, row0, R, a->ending,
-                       a->residual);
+                       a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, a->b_g, a->b_o, (uint16_t*)a->out, N, B, row0,
+                       R, a->ending, a->residual);
     return launched(err, errlen, "triattn_epilogue_gate_bf16");
   }
-  return epilogue_launch(a->dtype, o, g, a->w_o, B, N, a->C, (int)H, (int)D, a->ending, a->residual, a->out, st, err, errlen);
+  return epilogue_launch(a->dtype, o, g, a->w_o, a->b_o, B, N, a->C, (int)H, (int)D, a->ending, a->residual, a->out, st, err, errlen);
 }

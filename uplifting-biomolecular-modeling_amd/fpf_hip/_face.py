@@ -38,6 +38,59 @@ class Refusal(RuntimeError):
 
 
 _ARCH_BY_DEVICE = {}
+# compute capability -> arch word: ROCm torch reports an MI355X (gfx950) as capability (9, 5)
+CC_ARCH = {(9, 5): ARCH}
+
+
+def norm_cc(cc):
+    """(major, minor) from a capability given as a tuple / list, "9.5", 9.5, "sm_95" or "sm95" (the reference's forms,
+    common/opt_core/opt_core/kernels/triattn/__init__.py:197-206)."""
+    if isinstance(cc, (tuple, list)):
+        return int(cc[0]), int(cc[1])
+    s = str(cc).strip()
+    if s.startswith("sm"):
+        s = (s[3:] if s.startswith("sm_") else s[2:]).rstrip("a")
+        return int(s[:-1]), int(s[-1])
+    major, _, minor = s.partition(".")
+    return int(major), int(minor or 0)
+
+
+def arch_word(cc):
+    """The device word a row is keyed by, from whatever the caller names the device with: a capability (tuple, "9.5", "sm_95"),
+    an arch name ("gfx950", "gfx950:sramecc+:xnack-"), a tensor, or a torch.device.  (9, 5) is gfx950; any other capability
+    gives "cc<M>.<m>", which no row of this package serves (refused by name)."""
+    import torch
+    if isinstance(cc, torch.Tensor):
+        return device_word(cc)
+    if isinstance(cc, torch.device):
+        if cc.type != "cuda":
+            return "cpu"
+        idx = cc.index if cc.index is not None else torch.cuda.current_device()
+        w = _ARCH_BY_DEVICE.get(idx)
+        if w is None:
+            w = _ARCH_BY_DEVICE[idx] = torch.cuda.get_device_properties(idx).gcnArchName.split(":")[0]
+        return w
+    if isinstance(cc, str) and cc.strip().startswith("gfx"):
+        return cc.strip().split(":")[0]
+    if cc is None:
+        raise ValueError("cc is required (a capability such as (9, 5) or '9.5', an arch name such as 'gfx950', or a device)")
+    M, m = norm_cc(cc)
+    return CC_ARCH.get((M, m), "cc%d.%d" % (M, m))
+
+
+def dtype_of(dtype):
+    """'bf16' / 'fp32' / 'fp16' (or the dtype's own name) from a torch dtype or one of the reference's dtype words."""
+    s = str(dtype).replace("torch.", "").strip().lower()
+    return {"bfloat16": "bf16", "bf16": "bf16", "float32": "fp32", "float": "fp32", "f32": "fp32", "fp32": "fp32", "float16": "fp16",
+            "half": "fp16", "fp16": "fp16"}.get(s, s)
+
+
+def check_device(face, row, dev, **tensors):
+    """Refusal by name unless every given tensor (None skipped) lives on ``dev``: a host pointer handed to a kernel is a device
+    memory fault, so this runs before any launch."""
+    for name, t in tensors.items():
+        if t is not None and t.device != dev:
+            raise Refusal("device:%s" % name, row, ROW_STOCK, "%s: %s is on %s, the call runs on %s" % (face, name, t.device, dev))
 
 
 def device_word(t):
@@ -107,9 +160,61 @@ def _resolve(word, dtype_word, arch, face, cell):
 
 
 def dtype_word(dtype):
+    return dtype_of(dtype)
+
+
+def no_config(config, row):
+    """The kernels' launch geometry is fixed per shape class: an explicit launch setting (the reference passes Triton configs
+    through) is refused by name rather than ignored."""
+    if config:
+        raise Refusal("config:fixed_launch", row, row, "launch settings %s are not tunable on this row" % (dict(config),))
+
+
+def word_base(word):
+    """``row@<config>`` words name a launch setting the reference's Triton rows take; this package's rows have none."""
+    w = str(word)
+    if "@" in w:
+        base, _, cfg = w.partition("@")
+        raise Refusal("config_word:%s" % cfg, base, base, "word %r: the launch geometry of this row is fixed" % w)
+    return w
+
+
+def narrow(sel, word, prefer, exclude=None):
+    """Apply the caller's candidate narrowing to a resolved Selection: ``prefer`` (rows, in order) restricts a tier word's
+    candidates, ``exclude`` steps aside from rows; the row this package resolved must survive both, else Refusal by name."""
+    if prefer and str(word) in TIER_WORDS and sel.row not in [str(p).split("@")[0] for p in prefer]:
+        raise Refusal("prefer_excludes:%s" % sel.row, word, str(list(prefer)[0]), "prefer=%s" % (tuple(prefer),))
+    if exclude and sel.row in [str(e) for e in exclude]:
+        raise Refusal("excluded:%s" % sel.row, word, ROW_STOCK, "exclude=%s" % (tuple(exclude),))
+    return sel
+
+
+# ---------------------------------------------------------------------------------------------------------------- scratch
+_SCRATCH = {}
+
+
+def scratch(device, nbytes, kind="ws"):
+    """One grow-only device buffer per (device, stream, kind), shared by every call of every face on that stream: a call uses
+    its workspace only between its own launches on the current stream, so the next call on the same stream may reuse it, and
+    a stack of layers holds ONE workspace sized by its largest call instead of one per layer.  Calls on other streams get
+    their own buffers.  ``kind`` separates buffers one call needs at the same time (the chunked triangle attention holds a
+    workspace and a full bias)."""
     import torch
-    if dtype == torch.bfloat16:
-        return "bf16"
-    if dtype == torch.float32:
-        return "fp32"
-    return str(dtype).replace("torch.", "")
+    dev = torch.device(device)
+    key = (str(dev), torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0, kind)
+    t = _SCRATCH.get(key)
+    if t is None or t.numel() < nbytes:
+        _SCRATCH.pop(key, None)
+        del t                                                # the old buffer goes back to the caching allocator first
+        t = _SCRATCH[key] = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    return t
+
+
+def scratch_bytes(device=None):
+    """Bytes held by the shared scratch buffers (of one device, or all)."""
+    return sum(t.numel() for k, t in _SCRATCH.items() if device is None or k[0] == str(device))
+
+
+def release_scratch():
+    """Drop every shared scratch buffer (their memory returns to torch's caching allocator)."""
+    _SCRATCH.clear()

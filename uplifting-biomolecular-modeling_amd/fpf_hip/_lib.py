@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 DT_BF16, DT_F32, DT_U8 = 1, 2, 3
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
 
@@ -46,7 +46,7 @@ class TriattnBlockArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp),
                 ("mask", vp), ("mask_dtype", i32), ("ln_w", vp), ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("w_o", vp),
                 ("ending", i32), ("residual", i32), ("out", vp), ("scale", f32), ("workspace", vp), ("workspace_bytes", sz),
-                ("row0", i64), ("rows", i64), ("bias_in", vp), ("mask_frame", i32)]
+                ("row0", i64), ("rows", i64), ("bias_in", vp), ("mask_frame", i32), ("b_g", vp), ("b_o", vp)]
 
 
 class TriattnBiasArgs(C.Structure):
@@ -57,12 +57,12 @@ class TriattnBiasArgs(C.Structure):
 class TriattnPrologueArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp), ("ln_w", vp),
                 ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("ending", i32), ("q", vp), ("k", vp), ("v", vp), ("v_ld", i64),
-                ("g", vp), ("bias", vp)]
+                ("g", vp), ("bias", vp), ("b_g", vp)]
 
 
 class TriattnEpilogueArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("o", vp), ("g", vp),
-                ("w_o", vp), ("ending", i32), ("residual", i32), ("out", vp)]
+                ("w_o", vp), ("ending", i32), ("residual", i32), ("out", vp), ("b_o", vp)]
 
 
 class ApbArgs(C.Structure):

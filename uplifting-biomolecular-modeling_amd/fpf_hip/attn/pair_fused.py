@@ -3,12 +3,21 @@ launches, ``fpf_triattn_block_fwd``) and the fused SwiGLU transition.
 
 Mirrors common/opt_core/opt_core/attn/pair_fused.py: ``Unsupported`` (:86), ``pack_triattn_weights`` (:679),
 ``pack_transition_weights`` (:744), ``_key_mask`` (:806), ``prologue`` (:1136), ``core_attention`` (:1391), ``epilogue``
-(:1416), ``tri_attn_block(z, W, mask=None, *, ending, residual, ...)`` (:1500) and ``transition(x, T, *, residual, out, mask,
-...)`` (:1519).
+(:1416), ``tri_attn_block(z, W, mask=None, *, ending, residual, impl, core, ln, x_ln, scale, bias_frame, variant, ...)`` (:1500)
+and ``transition(x, T, *, residual, ln, x_ln, impl, variant, out, mask, ...)`` (:1519).  Every keyword of the reference is
+taken by name: what this package serves is served, everything else raises ``Unsupported`` by name before any launch (nothing
+is accepted and ignored).
 
 Frames: z is the pair tensor [B,N,N,C] (or [N,N,C]) in its OWN frame.  ``ending=True`` attends in the transposed frame
 x = z^T: the prologue reads z^T by address (no copy) and the epilogue writes the update back untransposed.  With
 ``residual=True`` z is updated in place and returned; otherwise the update in z's frame is returned.
+
+Served: ``ln="fused"`` (LayerNorm in-kernel); ``impl`` "fpf" (the fused kernels; also "hip"); ``core`` "default",
+"tier:<word>", a row name of kernels.triattn, or a callable core(q, k, v, bias, mask, scale) (run between this package's
+prologue and epilogue stages); ``bias_frame`` "x" or "z" (the same numbers; "z" only changes the strides of the bias the
+prologue returns for the ending node).  Refused by name: ``ln="stock"`` / ``x_ln`` (the caller's own LayerNorm output),
+``impl`` "torch" / "lnl", cores "flash_triattn" / "k2b" (Triton members of the reference), ``write_x``, transition variants
+other than the in-place folded one, ``silu`` other than swiglu / liger.
 """
 import torch
 
@@ -18,6 +27,8 @@ from ..kernels import transition as _TR
 
 TRIATTN_KEYS = ("ln_w", "ln_b", "w_q", "w_k", "w_v", "w_g", "b_g", "w_b", "w_o", "b_o")
 TRANSITION_KEYS = ("ln_w", "ln_b", "w_a", "w_b", "w_out")
+DEFAULT_CORE = "default"
+IMPLS = ("fpf", "hip")
 
 
 class Unsupported(Exception):
@@ -30,15 +41,19 @@ class Unsupported(Exception):
 
 
 class TriAttnWeights(object):
-    """Packed triangle-attention weights: w_qkvg [4HD, C] (rows q|k|v|g), w_b [H, C], w_o [C_out, HD], LN in fp32, per dtype."""
+    """Packed triangle-attention weights: w_qkvg [4HD, C] (rows q|k|v|g), w_b [H, C], w_o [C_out, HD], optional gate bias
+    b_g [HD] and output bias b_o [C_out], LN in fp32; device operand packs per (device, dtype)."""
 
     def __init__(self):
         self._packs = {}
-        self._ws = {}
 
 
 def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=None, w_k=None, w_v=None, w_g=None, w_b=None, w_qkvg=None,
                          qkvg_split=("q", "k", "v", "g"), b_g=None, b_o=None, eps=1e-5, device=None):
+    """Pack once per module.  w_q / w_k / w_v / w_g [H*D, C] or w_qkvg [4*H*D, C] (row blocks in ``qkvg_split`` order); w_b [H, C];
+    w_o [C_out, H*D]; b_g [H*D] (added to the gate projection before the sigmoid) and b_o [C_out] (added to the output
+    projection), or None; ln_w / ln_b [C] or None (no affine).  The bf16 rows use b_g / b_o rounded to bf16 (the reference packs
+    them in bf16, pair_fused.py:731-738); the fp32 rows use them as given."""
     H, D = int(n_heads), int(head_dim)
     HD = H * D
     if w_qkvg is not None:
@@ -50,8 +65,6 @@ def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=No
         raise Unsupported("gate:none")
     if w_b is None:
         raise Unsupported("bias:none")
-    if b_g is not None or b_o is not None:
-        raise Unsupported("projection_bias", "the HIP block has no gate / output projection bias operand")
     for nm, t in (("w_q", w_q), ("w_k", w_k), ("w_v", w_v), ("w_g", w_g)):
         if t is None or t.dim() != 2 or int(t.shape[0]) != HD:
             raise Unsupported(nm + "-shape", str(None if t is None else tuple(t.shape)))
@@ -60,6 +73,10 @@ def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=No
         raise Unsupported("w_b-shape", str(tuple(w_b.shape)))
     if w_o.dim() != 2 or int(w_o.shape[1]) != HD:
         raise Unsupported("w_o-shape", str(tuple(w_o.shape)))
+    if b_g is not None and tuple(b_g.shape) != (HD,):
+        raise Unsupported("b_g-shape", str(tuple(b_g.shape)))
+    if b_o is not None and tuple(b_o.shape) != (int(w_o.shape[0]),):
+        raise Unsupported("b_o-shape", str(tuple(b_o.shape)))
     W = TriAttnWeights()
     dev = device if device is not None else w_o.device
     W.C, W.H, W.D, W.C_out, W.eps, W.dev = C, H, D, int(w_o.shape[0]), float(eps), dev
@@ -67,6 +84,8 @@ def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=No
         W.wqkvg = torch.cat([w_q, w_k, w_v, w_g], 0).detach().to(dev)
         W.wb = w_b.detach().to(dev)
         W.wo = w_o.detach().to(dev)
+        W.b_g = None if b_g is None else b_g.detach().to(dev)
+        W.b_o = None if b_o is None else b_o.detach().to(dev)
         W.ln_w = None if ln_w is None else ln_w.detach().to(dev).float().contiguous()
         W.ln_b = None if ln_b is None else ln_b.detach().to(dev).float().contiguous()
     W.shapes = "c%dh%dd%do%d" % (C, H, D, W.C_out)
@@ -74,11 +93,14 @@ def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=No
 
 
 def _wpack(W, dtype, device):
+    """(w_qkvg, w_b, w_o, b_g, b_o) on ``device``: weights in the row's dtype, biases fp32 (bf16-rounded for the bf16 row)."""
     key = (str(device), dtype)
     p = W._packs.get(key)
     if p is None:
         with torch.no_grad():
-            p = W._packs[key] = tuple(t.to(device=device, dtype=dtype).contiguous() for t in (W.wqkvg, W.wb, W.wo))
+            ws = tuple(t.to(device=device, dtype=dtype).contiguous() for t in (W.wqkvg, W.wb, W.wo))
+            bs = tuple(None if t is None else t.to(device=device, dtype=dtype).float().contiguous() for t in (W.b_g, W.b_o))
+            p = W._packs[key] = ws + bs
     return p
 
 
@@ -86,23 +108,26 @@ _MASK_U8 = {}
 
 
 def _pair_mask(mask, z4, ending=False):
-    """The pair mask as the kernels take it: u8 (nonzero = keep), contiguous, in the attention frame (the ending node gets the
-    transposed mask, mask_frame 1, so each attention row's keys are contiguous) -> (tensor, dtype, mask_frame).  The copies
-    are made once and kept while the same tensor (same object, unmodified) comes back -- a pair stack passes one mask to
-    every block -- because the core builds its key table from contiguous u8 rows with one 16-byte load per 16 keys."""
+    """The pair mask as the kernels take it: u8 (nonzero = keep), contiguous, on z's device, in the attention frame (the ending
+    node gets the transposed mask, mask_frame 1, so each attention row's keys are contiguous) -> (tensor, dtype, mask_frame).
+    The copies are made once and kept while the same tensor (same object, same version counter) comes back -- a pair stack
+    passes one mask to every block.  Inference tensors carry no version counter, so a mask made under torch.inference_mode()
+    is converted on every call instead."""
     if mask is None:
         return None, L.DT_U8, 0
     B, N = z4.shape[0], z4.shape[1]
     m = mask if mask.dim() == 3 else mask.unsqueeze(0)
     if tuple(m.shape) != (B, N, N):
         raise Unsupported("mask-shape", str(tuple(mask.shape)))
-    key = "t" if ending else "m"
+    version = None if mask.is_inference() else mask._version
+    key = ("t" if ending else "m", z4.device)
     hit = _MASK_U8.get(key)
-    if hit is not None and hit[0] is mask and hit[1] == mask._version:
+    if version is not None and hit is not None and hit[0] is mask and hit[1] == version:
         return hit[2], L.DT_U8, 1
     mm = m.transpose(1, 2) if ending else m
-    u8 = (mm != 0).contiguous().view(torch.uint8)
-    _MASK_U8[key] = (mask, mask._version, u8)           # holding the tensor keeps its storage from being reused
+    u8 = (mm.to(z4.device) != 0).contiguous().view(torch.uint8)
+    if version is not None:
+        _MASK_U8[key] = (mask, version, u8)          # holding the tensor keeps its storage from being reused
     return u8, L.DT_U8, 1
 
 
@@ -124,25 +149,72 @@ def _block_check(z, W, word, face):
     return z4, sel
 
 
+def _check_ln(ln, x_ln):
+    if ln == "stock" or x_ln is not None:
+        raise Unsupported("ln:stock", "the caller's own LayerNorm output (x_ln) is not taken: the kernels normalise z in-kernel")
+    if ln != "fused":
+        raise Unsupported("ln:%s" % ln)
+
+
+def _check_impl(impl):
+    if impl is not None and impl not in IMPLS:
+        raise Unsupported("impl:%s" % impl, "served: fused HIP kernels (impl 'fpf' / 'hip')")
+
+
+def _check_bias_frame(bias_frame):
+    if bias_frame not in ("x", "z"):
+        raise Unsupported("bias_frame:%s" % bias_frame)
+
+
+def _core_word(core):
+    """The block's own core serves "default", "tier:<word>" and the row names of kernels.triattn; -> the tier / row word, or None
+    for a callable; Unsupported for the reference's Triton members and anything else."""
+    if callable(core):
+        return None
+    c = str(core)
+    if c == DEFAULT_CORE:
+        return "fast"
+    if c.startswith("tier:"):
+        return c[len("tier:"):]
+    if c in (F.ROW_FAST, F.ROW_F32):
+        return c
+    raise Unsupported("core:%s" % c, "served cores: default, tier:<word>, %s, %s, or a callable" % (F.ROW_FAST, F.ROW_F32))
+
+
 def _key_mask(mask, z, ending):
     """Pair mask [B,N,N] / [N,N] in z's frame -> the core's key mask [B, I, 1, 1, J] bool in the attention frame (transposed for
-    the ending node), as pair_fused.py:806-829 builds it.  None stays None."""
+    the ending node), on z's device (z None: the mask's own), as pair_fused.py:806-829 builds it.  None stays None."""
     if mask is None:
         return None
     m = mask if mask.dim() == 3 else mask.unsqueeze(0)
     if ending:
         m = m.transpose(1, 2)
+    if z is not None:
+        m = m.to(z.device)
     return (m != 0)[:, :, None, None, :]
 
 
-def prologue(z, W, *, ending=False, word="fast", **_unused):
+def _launch(entry, args, dev):
+    try:
+        L.call(entry, args, L.stream_ptr(dev))
+    except L.LibError as e:
+        raise Unsupported("lib:" + e.kind, e.msg) from None
+
+
+def prologue(z, W, *, ending=False, ln="fused", x_ln=None, impl="fpf", bias_frame="x", write_x=False, word="fast", _plan=None):
     """-> (q, k, v, g, bias) in the attention frame x = z (z^T for the ending node, read by address): q, k, v [B, I, H, J, D]
-    (bf16: v is a view of storage [B, I, H, D, J], which the op face serves without a copy), g [B, I, J, H*D] pre-sigmoid, bias
-    [B, 1, H, I, J] fp32.  Mirrors pair_fused.py:1136 (``prologue``); one launch of ``fpf_triattn_prologue_fwd``."""
+    (bf16: v is a view of storage [B, I, H, D, J], which the op face serves without a copy), g [B, I, J, H*D] pre-sigmoid (b_g
+    added), bias [B, 1, H, I, J] fp32 (bias_frame "z": the same values stored in z's frame for the ending node, an axes-swapped
+    view).  Mirrors pair_fused.py:1136 (``prologue``); one launch of ``fpf_triattn_prologue_fwd``."""
+    if write_x:
+        raise Unsupported("write_x", "returning the normalised x is not served")
+    _check_ln(ln, x_ln)
+    _check_impl(impl)
+    _check_bias_frame(bias_frame)
     z4, sel = _block_check(z, W, word, "prologue")
     B, N = int(z4.shape[0]), int(z4.shape[1])
     H, D = W.H, W.D
-    wqkvg, wb, _wo = _wpack(W, z.dtype, z.device)
+    wqkvg, wb, _wo, bg, _bo = _wpack(W, z.dtype, z.device)
     e = dict(dtype=z.dtype, device=z.device)
     q = torch.empty(B, N, H, N, D, **e)
     k = torch.empty(B, N, H, N, D, **e)
@@ -154,35 +226,38 @@ def prologue(z, W, *, ending=False, word="fast", **_unused):
     a = L.TriattnPrologueArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if bf else L.DT_F32, B=B, N=N, C=W.C, H=H, D=D, z=L.ptr(z4),
                               ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb),
                               ending=1 if ending else 0, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vs), v_ld=jp if bf else 0, g=L.ptr(g),
-                              bias=L.ptr(bias))
-    try:
-        L.call("fpf_triattn_prologue_fwd", a, L.stream_ptr(z.device))
-    except L.LibError as e_:
-        raise Unsupported("lib:" + e_.kind, e_.msg) from None
+                              bias=L.ptr(bias), b_g=L.ptr(bg))
+    _launch("fpf_triattn_prologue_fwd", a, z.device)
     v = vs[..., :N].transpose(-1, -2) if bf else vs
+    if bias_frame == "z" and ending:
+        bias = bias.transpose(-1, -2).contiguous().transpose(-1, -2)
     return q, k, v, g, bias.unsqueeze(1)
 
 
-def core_attention(q, k, v, bias, mask5=None, *, core="tier:fast", scale=None):
-    """o [B, I, H, J, D] = softmax_j(scale q.k + bias, -inf at masked keys) v through the op face (pair_fused.py:1391);
-    ``core`` = "tier:<word>" / a row name of kernels.triattn, or a callable core(q, k, v, bias, mask, scale)."""
+def core_attention(q, k, v, bias, mask5=None, *, core=DEFAULT_CORE, scale=None):
+    """o [B, I, H, J, D] = softmax_j(scale q.k + bias, -inf at masked keys) v (pair_fused.py:1391): ``core`` "default" (this
+    package's fast row), "tier:<word>" / a row name of kernels.triattn, or a callable core(q, k, v, bias, mask, scale).  A
+    callable gets v with a contiguous head_dim (the op contract's unit stride), copied when the prologue handed it transposed."""
     from ..kernels import triattn as _TA
+    import math
     if callable(core):
-        import math
+        if v.stride(-1) != 1:
+            v = v.contiguous()
         return core(q, k, v, bias, mask5, (1.0 / math.sqrt(q.shape[-1])) if scale is None else float(scale))
-    w = str(core)
-    if w.startswith("tier:"):
-        w = w[len("tier:"):]
+    w = _core_word(core)
     try:
         return _TA.triangle_attention(q, k, v, bias, mask5, scale, word=w)
     except F.Refusal as e:
         raise Unsupported("core:" + e.kind, e.detail) from None
 
 
-def epilogue(o, g, W, z=None, *, ending=False, residual=False, out=None, word="fast", **_unused):
-    """u = (sigmoid(g) * o) W_o^T (pair_fused.py:1416).  residual=True: z (its own frame) is updated in place (the ending node's
-    u[i, j] is added at z[j, i]) and returned; else the update in the attention frame [B, I, J, C_out] (for the ending node a
-    transposed view of a z-frame tensor, as the reference returns it).  One launch of ``fpf_triattn_epilogue_fwd``."""
+def epilogue(o, g, W, z=None, *, ending=False, residual=False, impl="fpf", o_layout="ihjd", out=None, word="fast", _plan=None):
+    """u = (sigmoid(g) * o) W_o^T + b_o (pair_fused.py:1416).  residual=True: z (its own frame) is updated in place (the ending
+    node's u[i, j] is added at z[j, i]) and returned; else the update in the attention frame [B, I, J, C_out] (for the ending node
+    a transposed view of a z-frame tensor, as the reference returns it).  One launch of ``fpf_triattn_epilogue_fwd``."""
+    _check_impl(impl)
+    if o_layout != "ihjd":
+        raise Unsupported("o_layout:%s" % o_layout, "o is taken as [B, I, H, J, D]")
     if o.dim() != 5:
         raise Unsupported("o-shape", str(tuple(o.shape)))
     B, N, H, J, D = (int(x) for x in o.shape)
@@ -190,60 +265,82 @@ def epilogue(o, g, W, z=None, *, ending=False, residual=False, out=None, word="f
         raise Unsupported("o/g-shape", "%s %s" % (tuple(o.shape), tuple(g.shape)))
     if not (o.is_contiguous() and g.is_contiguous()) or g.dtype != o.dtype:
         raise Unsupported("o/g-layout", "o [B,I,H,J,D] and g [B,I,J,HD] contiguous, one dtype")
+    if g.device != o.device:
+        raise Unsupported("device:g", "o and g must be on one device")
     if residual:
         if z is None:
             raise Unsupported("residual-needs-z")
         z4, sel = _block_check(z, W, word, "epilogue")
-        if z4.dtype != o.dtype or tuple(z4.shape[:3]) != (B, N, N):
+        if z4.dtype != o.dtype or tuple(z4.shape[:3]) != (B, N, N) or z4.device != o.device:
             raise Unsupported("z-shape", str(tuple(z.shape)))
         dst = z4
     else:
         if out is not None:
             dst = out if out.dim() == 4 else out.unsqueeze(0)
-            if tuple(dst.shape) != (B, N, N, W.C_out) or not dst.is_contiguous() or dst.dtype != o.dtype:
-                raise Unsupported("out", "a contiguous [B, N, N, C_out] tensor of o's dtype (z's frame)")
+            if tuple(dst.shape) != (B, N, N, W.C_out) or not dst.is_contiguous() or dst.dtype != o.dtype or dst.device != o.device:
+                raise Unsupported("out", "a contiguous [B, N, N, C_out] tensor of o's dtype on o's device (z's frame)")
         else:
             dst = torch.empty(B, N, N, W.C_out, dtype=o.dtype, device=o.device)
         _block_check(dst, W, word, "epilogue")
-    _, _, wo = _wpack(W, o.dtype, o.device)
+    _, _, wo, _bg, bo = _wpack(W, o.dtype, o.device)
     a = L.TriattnEpilogueArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if o.dtype == torch.bfloat16 else L.DT_F32, B=B, N=N, C=W.C, H=H, D=D,
-                              o=L.ptr(o), g=L.ptr(g), w_o=L.ptr(wo), ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(dst))
-    try:
-        L.call("fpf_triattn_epilogue_fwd", a, L.stream_ptr(o.device))
-    except L.LibError as e_:
-        raise Unsupported("lib:" + e_.kind, e_.msg) from None
+                              o=L.ptr(o), g=L.ptr(g), w_o=L.ptr(wo), ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(dst),
+                              b_o=L.ptr(bo))
+    _launch("fpf_triattn_epilogue_fwd", a, o.device)
     if residual:
         return z
     return dst.transpose(1, 2) if ending else dst
 
 
-def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, scale=None, word="fast", **_unused):
-    """The fused block; returns the update in z's frame (residual=False) or z updated in place (residual=True)."""
+def _block_args(z4, W, m, mdt, mframe, ending, residual, out, scale, ws, dt, wpack, row0=0, rows=0, bias_in=None):
+    wqkvg, wb, wo, bg, bo = wpack
+    B, N = int(z4.shape[0]), int(z4.shape[1])
+    return L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=dt, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m), mask_dtype=mdt,
+                              ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), w_o=L.ptr(wo),
+                              ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out), scale=float(scale or 0.0),
+                              workspace=L.ptr(ws), workspace_bytes=ws.numel(), row0=row0, rows=rows, bias_in=L.ptr(bias_in),
+                              mask_frame=mframe, b_g=L.ptr(bg), b_o=L.ptr(bo))
+
+
+def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, impl="fpf", core=DEFAULT_CORE, ln="fused", x_ln=None, scale=None,
+                   bias_frame="x", variant=None, engage_cells=False, word="fast"):
+    """The fused block; returns the update in z's frame (residual=False) or z updated in place (residual=True).  With this
+    package's own core (``core`` "default" / "tier:<word>" / a row name) it is one call of ``fpf_triattn_block_fwd`` (three
+    launches); a callable ``core`` runs between the prologue and epilogue stages.  ``engage_cells`` does not change the call."""
+    _check_ln(ln, x_ln)
+    _check_impl(impl)
+    _check_bias_frame(bias_frame)
+    if variant is not None:
+        raise Unsupported("variant:%s" % (variant,), "the block has one variant")
+    cw = _core_word(core)
     z4, sel = _block_check(z, W, word, "tri_attn_block")
+    if cw is None:                                    # the caller's core between this package's stages
+        q, k, v, g, bias = prologue(z, W, ending=ending, word=word)
+        o = core_attention(q, k, v, bias, _key_mask(mask, z, ending), core=core, scale=scale)
+        if residual:
+            return epilogue(o.contiguous(), g, W, z, ending=ending, residual=True, word=word)
+        u = epilogue(o.contiguous(), g, W, ending=ending, residual=False, word=word)
+        u = u.transpose(1, 2) if ending else u
+        return u if z.dim() == 4 else u[0]
+    try:                                              # the block's own core: the core word must resolve to the block's row
+        csel = F.resolve(cw, F.dtype_word(z.dtype), F.device_word(z), "pair_fused:core")
+    except F.Refusal as e:
+        raise Unsupported("core:" + e.kind, e.detail) from None
+    if csel.row != sel.row:
+        raise Unsupported("core:%s" % core, "the block's %s operands run row %s, not %s" % (F.dtype_word(z.dtype), sel.row, csel.row))
     B, N = int(z4.shape[0]), int(z4.shape[1])
     m, mdt, mframe = _pair_mask(mask, z4, ending)
-    wqkvg, wb, wo = _wpack(W, z.dtype, z.device)
+    wp = _wpack(W, z.dtype, z.device)
     dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
-    need = L.lib().fpf_triattn_block_workspace_bytes(B, N, 0, W.C, W.H, W.D, dt)
-    wkey = str(z.device)
-    ws = W._ws.get(wkey)
-    if ws is None or ws.numel() < need:
-        ws = W._ws[wkey] = torch.empty(need, dtype=torch.uint8, device=z.device)
+    ws = F.scratch(z.device, L.lib().fpf_triattn_block_workspace_bytes(B, N, 0, W.C, W.H, W.D, dt))
     out = z4 if residual else torch.empty_like(z4)
-    a = L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=dt, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m), mask_dtype=mdt,
-                           ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), w_o=L.ptr(wo),
-                           ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out), scale=float(scale or 0.0),
-                           workspace=L.ptr(ws), workspace_bytes=ws.numel(), mask_frame=mframe)
-    try:
-        L.call("fpf_triattn_block_fwd", a, L.stream_ptr(z.device))
-    except L.LibError as e:
-        raise Unsupported("lib:" + e.kind, e.msg) from None
+    _launch("fpf_triattn_block_fwd", _block_args(z4, W, m, mdt, mframe, ending, residual, out, scale, ws, dt, wp), z.device)
     if residual:
         return z
     return out if z.dim() == 4 else out[0]
 
 
-def tri_attn_block_chunked(z, W, mask=None, *, ending=False, residual=False, chunk=256, scale=None, word="big", **_unused):
+def tri_attn_block_chunked(z, W, mask=None, *, ending=False, residual=False, chunk=256, scale=None, word="big"):
     """The row-chunked (`big`) triangle-attention block, after common/opt_core/opt_core/mem/chunk.py:424
     (triangle_attention_chunked): pass 1 computes the full bias [B, H, N, N] from every pixel (one launch of
     ``fpf_triattn_bias_fwd``); pass 2 runs prologue -> core -> gate-fused epilogue on ``chunk`` attention rows at a time (z rows
@@ -259,36 +356,18 @@ def tri_attn_block_chunked(z, W, mask=None, *, ending=False, residual=False, chu
         raise Unsupported("chunk:%d" % chunk)
     B, N = int(z4.shape[0]), int(z4.shape[1])
     m, mdt, mframe = _pair_mask(mask, z4, ending)
-    wqkvg, wb, wo = _wpack(W, z.dtype, z.device)
+    wp = _wpack(W, z.dtype, z.device)
     rows = min(chunk, N)
     lib = L.lib()
-    need = lib.fpf_triattn_block_workspace_bytes(B, N, rows, W.C, W.H, W.D, L.DT_BF16)
-    key = (str(z.device), "chunked")
-    ws = W._ws.get(key)
-    if ws is None or ws.numel() < need:
-        ws = W._ws[key] = torch.empty(need, dtype=torch.uint8, device=z.device)
-    bkey = (str(z.device), "bias")
-    bias = W._ws.get(bkey)
-    if bias is None or bias.numel() < B * W.H * N * N:
-        bias = W._ws[bkey] = torch.empty(B * W.H * N * N, dtype=torch.float32, device=z.device)
-    stream = L.stream_ptr(z.device)
+    ws = F.scratch(z.device, lib.fpf_triattn_block_workspace_bytes(B, N, rows, W.C, W.H, W.D, L.DT_BF16))
+    bias = F.scratch(z.device, B * W.H * N * N * 4, kind="bias")
     ab = L.TriattnBiasArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), ln_w=L.ptr(W.ln_w),
-                           ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), ending=1 if ending else 0, bias=L.ptr(bias))
-    try:
-        L.call("fpf_triattn_bias_fwd", ab, stream)
-    except L.LibError as e:
-        raise Unsupported("lib:" + e.kind, e.msg) from None
+                           ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wp[0]), w_b=L.ptr(wp[1]), ending=1 if ending else 0, bias=L.ptr(bias))
+    _launch("fpf_triattn_bias_fwd", ab, z.device)
     out = z4 if residual else torch.empty_like(z4)
     for r0 in range(0, N, rows):
-        a = L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m),
-                               mask_dtype=mdt, ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb),
-                               w_o=L.ptr(wo), ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out),
-                               scale=float(scale or 0.0), workspace=L.ptr(ws), workspace_bytes=ws.numel(), row0=r0, rows=min(rows, N - r0),
-                               bias_in=L.ptr(bias), mask_frame=mframe)
-        try:
-            L.call("fpf_triattn_block_fwd", a, stream)
-        except L.LibError as e:
-            raise Unsupported("lib:" + e.kind, e.msg) from None
+        a = _block_args(z4, W, m, mdt, mframe, ending, residual, out, scale, ws, L.DT_BF16, wp, row0=r0, rows=min(rows, N - r0), bias_in=bias)
+        _launch("fpf_triattn_block_fwd", a, z.device)
     if residual:
         return z
     return out if z.dim() == 4 else out[0]
@@ -313,13 +392,32 @@ def pack_transition_weights(*, w_out, ln_w=None, ln_b=None, w_a=None, w_b=None, 
     for nm, t in (("w_a", w_a), ("w_b", w_b)):
         if t is None or tuple(t.shape) != (NH, C):
             raise Unsupported(nm + "-shape", str(None if t is None else tuple(t.shape)))
+    if NH % C != 0:
+        raise Unsupported("hidden", "n*C hidden expected, got C=%d hidden=%d" % (C, NH))
     return TransitionWeights(_TR.pack(w_o=w_out, w_a=w_a, w_b=w_b, ln_w=ln_w, ln_b=ln_b, eps=eps, device=device))
 
 
-def transition(x, T, *, residual=False, out=None, mask=None, word="fast", **_unused):
-    """y = W_out(silu(W_a n) * W_b n), n = LN(x) in-kernel; x + y when residual; ``out`` may be x (in place)."""
+TRANSITION_VARIANTS = ("v2_fold",)
+
+
+def transition(x, T, *, residual=False, ln="fused", x_ln=None, impl="fpf", variant=None, out=None, mask=None, binary_mask=None,
+               variants=None, silu="swiglu", word="fast"):
+    """y = W_out(silu(W_a n) * W_b n), n = LN(x) in-kernel; x + y when residual; ``out`` may be x (in place); ``mask`` one value
+    per row, any values (``binary_mask`` changes nothing).  The kernel is the in-place folded variant (the reference's v2_fold:
+    mask and residual folded, out may alias x): ``variant`` / ``variants`` must name it when given.  The hidden
+    h = silu(a) * b is formed from fp32 a, b and rounded to bf16 once, the 'liger' form; ``silu='swiglu'`` (which rounds
+    silu(a) first) is served by the same kernel: the two differ by one bf16 rounding of the hidden, inside the fast tier's
+    tolerance."""
+    _check_ln(ln, x_ln)
+    _check_impl(impl)
+    if variant is not None and variant not in TRANSITION_VARIANTS:
+        raise Unsupported("variant:%s" % (variant,), "served: %s" % (TRANSITION_VARIANTS,))
+    if variants is not None and not any(v in TRANSITION_VARIANTS for v in variants):
+        raise Unsupported("variants:%s" % (tuple(variants),), "served: %s" % (TRANSITION_VARIANTS,))
+    if silu not in ("swiglu", "liger"):
+        raise Unsupported("silu:%s" % silu)
     try:
-        y, _sel = _TR.transition(x, T.W, word=word, residual=residual, mask=mask, out=out)
+        y, _sel = _TR.transition(x, T.W, word=word, residual=residual, mask=mask, binary_mask=binary_mask, out=out)
     except F.Refusal as e:
         raise Unsupported(e.kind, e.detail) from None
     return y

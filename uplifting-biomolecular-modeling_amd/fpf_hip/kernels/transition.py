@@ -3,8 +3,9 @@ served by libfpf_hip's ``fpf_transition_fwd`` (one launch; the hidden never reac
 
 Mirrors common/opt_core/opt_core/kernels/transition/__init__.py: ``pack(*, w_o, w_a=None, w_b=None, w_ab=None, ln_w=None,
 ln_b=None, eps=1e-5, device=None) -> Weights`` (:1011), ``Weights`` (:928; operand packs built once per weight set and dtype)
-and ``transition(x, W, *, word, residual=False, x_ln=None, mask=None, out=None, ...) -> (y, Selection)`` (:1074).  ``out`` may
-be ``x`` itself (in place).  ``x_ln`` (the caller's own LayerNorm output) is refused by name: the kernels always normalise.
+``select(word, *, c, hidden, n_tokens=None, dtype="bf16", ...)`` (:509) and ``transition(x, W, *, word, residual=False, x_ln=None,
+mask=None, binary_mask=None, out=None, n_tokens=None, family="pair", ...) -> (y, Selection)`` (:1074).  ``out`` may be ``x`` itself
+(in place).  ``x_ln`` (the caller's own LayerNorm output) is refused by name: the kernels always normalise.
 """
 import torch
 
@@ -53,13 +54,34 @@ def pack(*, w_o, w_a=None, w_b=None, w_ab=None, ln_w=None, ln_b=None, eps=1e-5, 
     return Weights(w_a, w_b, w_o, ln_w, ln_b, eps, device)
 
 
-def select(dtype, arch, c, hidden, *, word, n_tokens=None):
-    """Pure: the row serving a transition of (dtype, c, hidden) on this device word, or Refusal by name.  ``n_tokens`` (the
-    pair tensor's N) names the measured cell; without it the cell is the class only."""
-    cell = "%s|%s|pair_c%d_n%d|eager|fwd" % (CELLS.CC, F.dtype_word(dtype), c, hidden // max(c, 1))
-    if n_tokens is not None and hidden % c == 0:
-        cell = CELLS.transition_key(F.dtype_word(dtype), c, hidden // c, n_tokens)
-    sel = F.resolve(word, F.dtype_word(dtype), arch, "transition", cell=cell)
+def _arch_of(cc, device):
+    if cc is not None:
+        return F.arch_word(cc)
+    if device is not None:
+        return F.arch_word(torch.device(device))
+    return F.arch_word(torch.device("cuda")) if torch.cuda.is_available() else "cpu"
+
+
+def select(word, *, c, hidden, n_tokens=None, dtype="bf16", direction="fwd", timing="eager", family="pair", residual=False, mask=False,
+           cc=None, device=None, stack=None, capture=False, rows_count=None, ln_given=False, form="swiglu"):
+    """Pure: the row serving a transition of this class, or Refusal by name (common/opt_core/opt_core/kernels/transition/__init__.py:509).
+    ``cc`` / ``device`` name the card (the current device when both are None); ``n_tokens`` (the pair tensor's N) names the
+    measured cell.  ``ln_given`` (the caller's own LayerNorm output, the exact-candidate construction) and any ``form`` other than
+    swiglu are refused by name; ``timing`` / ``capture`` / ``stack`` / ``rows_count`` / ``residual`` / ``mask`` do not change the
+    answer (the kernel folds the residual and the row mask and is capture-safe)."""
+    w = F.word_base(word)
+    if str(direction) not in ("fwd", "forward"):
+        raise Refusal("no_backward", w, F.ROW_STOCK, "forward only")
+    if form != "swiglu":
+        raise Refusal("form:%s" % form, w, F.ROW_STOCK, "the kernel computes the SwiGLU transition")
+    if ln_given:
+        raise Refusal("ln_given", w, F.ROW_STOCK, "the HIP rows normalise in-kernel; the caller's x_ln is not taken")
+    dw = F.dtype_of(dtype)
+    c, hidden = int(c), int(hidden)
+    cell = "%s|%s|%s_c%d_n%d|eager|fwd" % (CELLS.CC, dw, family, c, hidden // max(c, 1))
+    if n_tokens is not None and hidden % c == 0 and family == "pair":
+        cell = CELLS.transition_key(dw, c, hidden // c, n_tokens)
+    sel = F.resolve(w, dw, _arch_of(cc, device), "transition", cell=cell)
     if sel.row == F.ROW_FAST and (c != 128 or hidden % 32):
         raise Refusal("shape:c%dh%d" % (c, hidden), sel.row, F.ROW_F32, "the bf16 kernel serves c = 128, hidden % 32 == 0")
     if sel.row == F.ROW_F32 and c > 384:
@@ -67,16 +89,23 @@ def select(dtype, arch, c, hidden, *, word, n_tokens=None):
     return sel
 
 
-def transition(x, W, *, word, residual=False, x_ln=None, mask=None, out=None, selection=None, **_unused):
-    if x_ln is not None:
-        raise Refusal("ln_given", None, F.ROW_STOCK, "the HIP rows normalise in-kernel; x_ln is not taken")
+def transition(x, W, *, word, residual=False, x_ln=None, mask=None, binary_mask=None, out=None, n_tokens=None, family="pair", timing="eager",
+               capture=False, stack=None, form="swiglu", cc=None, selection=None):
+    """y = W_o(silu(W_a n) * (W_b n)), n = LayerNorm(x) in-kernel -> (y, Selection); x + y when ``residual``; ``mask`` one value
+    per row of x (any values: the update is multiplied by it before the residual add, so ``binary_mask`` changes nothing);
+    ``out`` may be x (in place).  The hidden is fp32 and rounded to bf16 once (silu(a) * b) before the output projection."""
     c = int(x.shape[-1])
     if c != W.c:
         raise Refusal("c:%d!=%d" % (c, W.c), word, F.ROW_STOCK)
-    sel = selection or select(x.dtype, F.device_word(x), W.c, W.hidden, word=word, n_tokens=int(x.shape[-2]) if x.dim() >= 3 else None)
+    if n_tokens is None and x.dim() >= 3:
+        n_tokens = int(x.shape[-2])
+    sel = selection or select(word, c=W.c, hidden=W.hidden, n_tokens=n_tokens, dtype=x.dtype, family=family, residual=residual,
+                              mask=mask is not None, cc=cc if cc is not None else x, stack=stack, capture=capture, ln_given=x_ln is not None,
+                              form=form, timing=timing)
     rows = x.numel() // c
     if not x.is_contiguous():
         raise Refusal("stride", sel.row, F.ROW_STOCK, "x must be contiguous")
+    F.check_device("transition", sel.row, x.device, out=out)
     if out is None:
         out = torch.empty_like(x)
     elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():

@@ -6,9 +6,11 @@ Mirrors common/opt_core/opt_core/kernels/triattn/__init__.py: the op (:3-8)
     q/k/v [B,N,H,S,D], bias [B,1,H,S,S] (fp32 or bf16, shared over the N rows), mask [B,N,1,1,S] (bool / any dtype, nonzero = attend),
     out [B,N,H,S,D] in q.dtype; a fully-masked row yields the uniform average of v,
 
-``Refusal`` (:129), ``Selection``, ``select(cc, dtype, head_dim, heads, n_tokens, direction="fwd", *, word)`` (:454) and
-``triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, ...)`` (:1094).  Strided views are served as they are
-(stride(-1) == 1): the ending node's transposed q/k/v views need no copy.
+``Refusal`` (:129), ``Selection``, ``select(cc, dtype, head_dim, heads, n_tokens, direction="fwd", *, word, prefer=None, stack=None,
+config=None, ...)`` (:454), ``admits(row, cc, dtype, head_dim, heads, n_tokens, direction="fwd", *, stack=None, position_stride=None)``
+(:305) and ``triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, prefer=None, stock=None, config=None, selection=None,
+form=None)`` (:1094).  ``cc`` is a capability ((9, 5) / "9.5" for an MI355X under ROCm torch), an arch name ("gfx950") or a device.
+Strided views are served as they are (stride(-1) == 1): the ending node's transposed q/k/v views need no copy.
 """
 import math
 
@@ -19,13 +21,38 @@ from .. import _lib as L
 from .. import cells as CELLS
 
 Refusal, Selection = F.Refusal, F.Selection
+ROW_NAMES = (F.ROW_FAST, F.ROW_F32)
+_DIRECTIONS = ("fwd", "forward", "inference", "start", "starting", "end", "ending")
 
 
-def select(arch, dtype, head_dim, heads, n_tokens, direction="fwd", *, word):
-    """Pure: the row serving a triangle-attention call of this class on this device word, or Refusal by name."""
-    if direction not in ("fwd", "forward", "inference", "start", "starting", "end", "ending"):
-        raise Refusal("direction:%s" % direction, word, F.ROW_STOCK, "forward only")
-    sel = F.resolve(word, F.dtype_word(dtype), arch, "triattn", cell=CELLS.triattn_key(F.dtype_word(dtype), head_dim, heads, n_tokens))
+def admits(row, cc, dtype, head_dim, heads, n_tokens, direction="fwd", *, stack=None, position_stride=None):
+    """(True, "ok") when ``row``'s static envelope admits the call, else (False, <refusal word>) -- pure, no launch."""
+    if row not in ROW_NAMES:
+        return False, "unknown_row:%s" % row
+    if F.arch_word(cc) != F.ARCH:
+        return False, "arch:%s" % F.arch_word(cc)
+    if str(direction) not in _DIRECTIONS:
+        return False, "direction:%s" % direction
+    dw = F.dtype_of(dtype)
+    if row == F.ROW_FAST and (dw != "bf16" or int(head_dim) != 32):
+        return False, "dtype:%s" % dw if dw != "bf16" else "no_row:head_dim%d" % int(head_dim)
+    if row == F.ROW_F32 and (dw != "fp32" or int(head_dim) not in (16, 32, 64)):
+        return False, "dtype:%s" % dw if dw != "fp32" else "no_row:head_dim%d" % int(head_dim)
+    return True, "ok"
+
+
+def select(cc, dtype, head_dim, heads, n_tokens, direction="fwd", *, word, prefer=None, stack=None, config=None, position_stride=None,
+           form=None, exact_stack=None, lib=None):
+    """Pure: the row serving a triangle-attention call of this class on this device, or Refusal by name.  ``prefer`` narrows a
+    tier word's candidates; ``config`` (a launch setting) is refused by name; ``stack`` / ``form`` / ``exact_stack`` / ``lib`` /
+    ``position_stride`` do not change the answer (the kernels take 64-bit offsets and any strided q / k / v view)."""
+    w = F.word_base(word)
+    if str(direction) not in _DIRECTIONS:
+        raise Refusal("direction:%s" % direction, w, F.ROW_STOCK, "forward only")
+    dw = F.dtype_of(dtype)
+    sel = F.resolve(w, dw, F.arch_word(cc), "triattn", cell=CELLS.triattn_key(dw, head_dim, heads, n_tokens))
+    F.narrow(sel, w, prefer)
+    F.no_config(config, sel.row)
     if sel.row == F.ROW_FAST and head_dim != 32:
         raise Refusal("no_row:head_dim%d" % head_dim, sel.row, F.ROW_F32, "the bf16 core serves head_dim 32")
     if sel.row == F.ROW_F32 and head_dim not in (16, 32, 64):
@@ -40,14 +67,20 @@ def _strides(t, n):
     return s
 
 
-def triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, selection=None, out=None, **_unused):
-    """Serve the op; returns the output tensor.  Refusal by name before any launch."""
+def triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, prefer=None, stock=None, config=None, selection=None, form=None,
+                       out=None):
+    """Serve the op; returns the output tensor.  Refusal by name before any launch.  ``stock`` (the kit's own stock callable) is
+    never called here: this face serves only its own rows, and the stock row is the caller's call.  ``out`` (an extension of this
+    package): a caller-given [B, N, H, S, D] output."""
     if q.dim() != 5 or k.shape != q.shape or v.shape != q.shape:
         raise Refusal("shape", word, F.ROW_STOCK, "q/k/v must be [B,N,H,S,D] of one shape")
     B, N, H, S, D = q.shape
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise Refusal("dtype_mix", word, F.ROW_STOCK)
-    sel = selection or select(F.device_word(q), q.dtype, D, H, S, word=word)
+    sel = selection or select(q, q.dtype, D, H, S, word=word, prefer=prefer, config=config, form=form)
+    F.check_device("triattn", sel.row, q.device, k=k, v=v, bias=bias, out=out)
+    if mask is not None and mask.device != q.device:
+        mask = mask.to(q.device)
     # v stored transposed ([B,N,H,D,S] storage viewed as [B,N,H,S,D], as the block prologue returns it) is served as it is by
     # the bf16 core (v_layout 1); every other operand needs a contiguous head_dim
     v_t = v.stride(-1) != 1 and v.stride(-2) == 1 and D > 1
@@ -73,6 +106,8 @@ def triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, selection=
             mdt = L.DT_F32
     if out is None:
         out = torch.empty((B, N, H, S, D), dtype=q.dtype, device=q.device)
+    elif tuple(out.shape) != (B, N, H, S, D) or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise Refusal("out", sel.row, F.ROW_STOCK, "out must be [B,N,H,S,D] in q's dtype with a contiguous head_dim")
     sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
     a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if q.dtype == torch.bfloat16 else L.DT_F32, B=B, N=N, H=H, S=S, D=D,
                       q=L.ptr(q), k=L.ptr(k), v=L.ptr(v), bias=L.ptr(bias), bias_dtype=L.DT_F32 if bias.dtype == torch.float32 else L.DT_BF16,

@@ -1,10 +1,14 @@
 """Triangle-multiplication face, served by libfpf_hip's ``fpf_trimul_fwd`` (K1 planes -> batched MFMA contraction -> K3).
 
 Mirrors common/opt_core/opt_core/kernels/trimul/__init__.py: the op (:3-11), ``WEIGHT_KEYS`` (:171), ``Refusal`` (:188),
-``select`` (:835) and ``triangle_multiplication(z, mask=None, *, direction, weights, word=None, selection=None, residual=False,
-cache=None, eps=1e-5, ...)`` (:1982).  ``cache`` (a dict the caller holds per weight set) keeps the packed weights and the
-workspace between calls; keys carry the weight tensors' identity, so a dict shared across modules re-packs rather than
-serving another module's pack.  ``out`` may be ``z`` itself when ``residual=True`` (K3 reads each pixel before writing it).
+``precision_word`` (:219), ``admits`` (:386), ``select(cc, dtype, c_z, c_hidden, n_tokens, direction="outgoing", *, word, residency=None,
+backward=False, prefer=None, stack=None, ...)`` (:835) and ``triangle_multiplication(z, mask=None, *, direction, weights, word=None,
+selection=None, residual=False, prefer=None, residency=None, stock=None, cache=None, eps=1e-5, ...)`` (:1982).  ``cc`` is a capability
+((9, 5) / "9.5" for an MI355X under ROCm torch), an arch name ("gfx950") or a device.  ``cache`` (a dict the caller holds per weight
+set) keeps the packed weights; keys carry the weight tensors' identity, so a dict shared across modules re-packs rather than serving
+another module's pack.  The workspace (the K1 planes and the contraction output) is the shared per-stream scratch of
+``fpf_hip._face.scratch``, not a per-cache buffer.  ``out`` may be ``z`` itself when ``residual=True`` (K3 reads each pixel before
+writing it).
 """
 import torch
 
@@ -14,6 +18,7 @@ from .. import cells as CELLS
 
 Refusal, Selection = F.Refusal, F.Selection
 WEIGHT_KEYS = ("ln_in_w", "ln_in_b", "w_ag", "w_ap", "w_bg", "w_bp", "ln_out_w", "ln_out_b", "w_o", "w_og")
+ROW_NAMES = (F.ROW_FAST, F.ROW_F32)
 _DIRS = {"outgoing": "outgoing", "out": "outgoing", "incoming": "incoming", "in": "incoming"}
 
 
@@ -24,15 +29,62 @@ def direction_word(direction):
     return d
 
 
-def select(arch, dtype, c_z, c_hidden, n_tokens, direction="outgoing", *, word):
-    """Pure: the row serving a TriMul call of this class, or Refusal by name."""
+def precision_word(dtype, residency=None, tf32=None):
+    """The precision class of a call: bf16 | f32z_bf16 (fp32-resident z, bf16 operands) | fp32 | tf32 | fp16."""
+    s = F.dtype_of(dtype)
+    if s in ("bf16", "fp16"):
+        r = F.dtype_of(residency) if residency is not None else ""
+        return ("f32z_" + s) if r == "fp32" else s
+    if s == "fp32" and tf32:
+        return "tf32"
+    return s
+
+
+def _class_of(prec):
+    """precision class -> the dtype word the row resolution keys on ('tf32' is served by the fp32 row: it meets that class)."""
+    return {"bf16": "bf16", "fp32": "fp32", "tf32": "fp32"}.get(prec)
+
+
+def admits(row, cc, dtype, c_z, c_hidden, n_tokens, *, residency=None, backward=False, residual=None, batch=1, abi=None, has_cueq=None,
+           has_esm_kernels=None, tf32=None, triton=None):
+    """Raise Refusal when ``row`` cannot serve this envelope (static facts only); return None when it can."""
+    if row not in ROW_NAMES:
+        raise ValueError("unknown row %r (rows: %s)" % (row, ", ".join(ROW_NAMES)))
+    arch = F.arch_word(cc)
+    if arch != F.ARCH:
+        raise Refusal("arch:%s" % arch, row, F.ROW_STOCK, "rows of this package are gfx950 kernels")
+    if backward:
+        raise Refusal("no_backward", row, F.ROW_STOCK, "forward only")
+    prec = precision_word(dtype, residency, tf32)
+    want = "bf16" if row == F.ROW_FAST else "fp32"
+    if _class_of(prec) != want:
+        raise Refusal("precision:%s" % prec, row, F.ROW_F32 if row == F.ROW_FAST else F.ROW_FAST, "row %s serves %s" % (row, want))
+    C, H = int(c_z), int(c_hidden)
+    if row == F.ROW_FAST and (C, H) != (128, 128):
+        raise Refusal("shape:c%dx%d" % (C, H), row, F.ROW_F32, "the bf16 kernels serve c_z = c_hidden = 128")
+    if row == F.ROW_F32 and (C > 128 or H > 128):
+        raise Refusal("shape:c%dx%d" % (C, H), row, F.ROW_STOCK, "the fp32 kernels serve c_z, c_hidden <= 128")
+    return None
+
+
+def select(cc, dtype, c_z, c_hidden, n_tokens, direction="outgoing", *, word, residency=None, backward=False, prefer=None, stack=None,
+           tf32=None, has_cueq=None, config=None, abi=None, exclude=None, form=None, batch=None):
+    """Pure: the row serving a TriMul call of this class, or Refusal by name.  ``residency`` = the dtype z is stored in (fp32 with
+    bf16 operands is the f32z_bf16 class); ``prefer`` narrows a tier word's candidates, ``exclude`` steps aside from rows;
+    ``config`` (a launch setting) is refused by name; ``stack`` / ``has_cueq`` / ``abi`` / ``form`` / ``batch`` do not change
+    the answer."""
     d = direction_word(direction)
-    sel = F.resolve(word, F.dtype_word(dtype), arch, "trimul",
-                    cell=CELLS.trimul_key(F.dtype_word(dtype), c_z, c_hidden, n_tokens, "out" if d == "outgoing" else "in"))
-    if sel.row == F.ROW_FAST and (c_z, c_hidden) != (128, 128):
-        raise Refusal("shape:c%dx%d" % (c_z, c_hidden), sel.row, F.ROW_F32, "the bf16 kernels serve c_z = c_hidden = 128")
-    if sel.row == F.ROW_F32 and (c_z > 128 or c_hidden > 128):
-        raise Refusal("shape:c%dx%d" % (c_z, c_hidden), sel.row, F.ROW_STOCK, "the fp32 kernels serve c_z, c_hidden <= 128")
+    w = F.word_base(word)
+    if backward:
+        raise Refusal("no_backward", w, F.ROW_STOCK, "forward only")
+    prec = precision_word(dtype, residency, tf32)
+    cls = _class_of(prec)
+    if cls is None:
+        raise Refusal("precision:%s" % prec, w, F.ROW_STOCK, "served classes: bf16, fp32, tf32 (by the fp32 row)")
+    sel = F.resolve(w, cls, F.arch_word(cc), "trimul", cell=CELLS.trimul_key(cls, c_z, c_hidden, n_tokens, "out" if d == "outgoing" else "in"))
+    F.narrow(sel, w, prefer, exclude)
+    F.no_config(config, sel.row)
+    admits(sel.row, cc, cls, c_z, c_hidden, n_tokens)
     return sel
 
 
@@ -54,9 +106,12 @@ def _pack(weights, dtype, device, cache):
     return p
 
 
-def triangle_multiplication(z, mask=None, *, direction, weights, word=None, selection=None, residual=False, cache=None, eps=1e-5,
-                            out=None, **_unused):
-    """Returns the update (or z + update when ``residual``) in z's dtype; Refusal by name before any launch."""
+def triangle_multiplication(z, mask=None, *, direction, weights, word=None, selection=None, residual=False, prefer=None, residency=None,
+                            stock=None, cache=None, eps=1e-5, config=None, pad=16, contract="bf16", form=None, module=None, out=None):
+    """Returns the update (or z + update when ``residual``) in z's dtype; Refusal by name before any launch.  ``stock`` (the
+    kit's own callable) is never called here; ``pad`` (the reference's plane padding) does not change the result (the planes are
+    padded to the contraction tile internally); ``contract``: hip_gfx950 contracts bf16 operands (any other word is refused),
+    hip_gfx950_f32 contracts in fp32, which meets every contraction class it is asked for."""
     cache = {} if cache is None else cache
     z4 = z if z.dim() == 4 else z.unsqueeze(0)
     B, N, N2, Cz = z4.shape
@@ -64,9 +119,13 @@ def triangle_multiplication(z, mask=None, *, direction, weights, word=None, sele
         raise ValueError("z must be [B,N,N,c] or [N,N,c] (got %s)" % (tuple(z.shape),))
     d = direction_word(direction)
     Ch = int(weights["w_ap"].shape[0])
-    sel = selection or select(F.device_word(z), z.dtype, Cz, Ch, N, d, word=word)
+    sel = selection or select(z, z.dtype, Cz, Ch, N, d, word=word, residency=residency, prefer=prefer, config=config, form=form, batch=B)
+    if (sel.row == F.ROW_FAST and str(contract) != "bf16") or str(contract) not in ("bf16", "fp32", "f32", "tf32"):
+        raise Refusal("contract:%s" % contract, sel.row, F.ROW_F32 if sel.row == F.ROW_FAST else F.ROW_STOCK,
+                      "row %s contracts in %s" % (sel.row, "bf16" if sel.row == F.ROW_FAST else "fp32"))
     if not z4.is_contiguous():
         raise Refusal("stride", sel.row, F.ROW_STOCK, "z must be contiguous")
+    F.check_device("trimul", sel.row, z.device, out=out)
     p = _pack(weights, z.dtype, z.device, cache)
     m = None
     if mask is not None:
@@ -82,10 +141,7 @@ def triangle_multiplication(z, mask=None, *, direction, weights, word=None, sele
         raise Refusal("out_aliases_z", sel.row, F.ROW_STOCK, "out may alias z only for the residual form")
     dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
     need = L.lib().fpf_trimul_workspace_bytes(B, N, Cz, Ch, dt)
-    wkey = ("_ws", str(z.device))
-    ws = cache.get(wkey)
-    if ws is None or ws.numel() < need:
-        ws = cache[wkey] = torch.empty(need, dtype=torch.uint8, device=z.device)
+    ws = F.scratch(z.device, need)
     a = L.TrimulArgs(abi_version=L.ABI_VERSION, dtype=dt, c_z=Cz, c_h=Ch, batch=B, n=N, z=L.ptr(z4), out=L.ptr(out), mask=L.ptr(m),
                      ln_in_w=L.ptr(p["ln_in_w"]), ln_in_b=L.ptr(p["ln_in_b"]), ln_out_w=L.ptr(p["ln_out_w"]), ln_out_b=L.ptr(p["ln_out_b"]),
                      w_ag=L.ptr(p["w_ag"]), w_ap=L.ptr(p["w_ap"]), w_bg=L.ptr(p["w_bg"]), w_bp=L.ptr(p["w_bp"]), w_o=L.ptr(p["w_o"]),
