@@ -60,12 +60,38 @@ def trunk(torch, dev, layers, N=512, reps=2):
     def run():
         z = z0.clone()
         return PFM.pairformer_trunk(s0, z, mask, pmask, stack)
+    from fpf_hip import _face as F
+    F.release_scratch()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
     run()
-    t = time_events(run, reps, torch)
+    t = statistics.median(step_times(run, reps, torch))
     fl = layers * (block_flops(N)["block"] + single_flops(N))
     return {"layers": layers, "N": N, "ms": round(t, 3), "tflop": round(fl / 1e12, 3), "tflops": round(fl / (t * 1e-3) / 1e12, 1),
             "mfma_frac": round(fl / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "ms_per_layer": round(t / layers, 4),
+            "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 3), "scratch_gb": round(F.scratch_bytes() / 1e9, 3),
             "workload": "BASELINE config 3: %d-layer Pairformer trunk, pair track bf16 + single track fp32 (c_s 384, 16 x 24 heads)" % layers}
+
+
+def pair_stack_leg(torch, dev, layers, N=768, reps=3):
+    """The north-star workload: a ``layers``-block Pairformer pair stack at N = 768, c_z = 128, bf16, in place on one resident z,
+    random-init weights per block (seeds 100 + l), z ~ N(0, 1), mask all ones.  One warm-up pass, then the median of ``reps``
+    passes (HIP events); the peak is this leg's own (the shared scratch holds one workspace of the largest call)."""
+    from fpf_hip import _face as F
+    from fpf_hip import pairformer as PFM
+    blocks = [PFM.PairBlock(PFM.random_params(seed=100 + l), dev, torch.bfloat16) for l in range(layers)]
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
+    mask = torch.ones(1, N, N, device=dev)
+    F.release_scratch()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    PFM.pair_stack(z, mask, blocks)
+    t = statistics.median(step_times(lambda: PFM.pair_stack(z, mask, blocks), reps, torch))
+    fl = layers * block_flops(N)["block"]
+    return {"layers": layers, "N": N, "ms": round(t, 2), "ms_per_block": round(t / layers, 4), "tflop": round(fl / 1e12, 2),
+            "tflops": round(fl / (t * 1e-3) / 1e12, 1), "mfma_frac": round(fl / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 3), "scratch_gb": round(F.scratch_bytes() / 1e9, 3),
+            "workload": "north star: %d-block Pairformer pair stack, N = %d, c_z = 128, bf16, in place" % (layers, N)}
 
 
 def configs_legs(torch, dev, big_blocks=4):
@@ -76,6 +102,7 @@ def configs_legs(torch, dev, big_blocks=4):
     chains 900 + 700 + 300 and 148 padded positions."""
     from fpf_hip import pairformer as PFM
     from fpf_hip.attn import pair_fused as PF
+    from fpf_hip import _face as F
     blk = PFM.PairBlock(PFM.random_params(seed=0), dev, torch.bfloat16)
     legs = {}
     N = 384
@@ -90,6 +117,9 @@ def configs_legs(torch, dev, big_blocks=4):
         t = time_events(fn, 20, torch)
         legs["c1_triatt_%s" % name] = {"N": N, "ms": round(t, 4), "tflops": round(f / (t * 1e-3) / 1e12, 1)}
     del z
+    F.release_scratch()                                     # the big leg's peak is its own: no scratch left from earlier legs
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
     N = 2048
     zb = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(0)).to(torch.bfloat16).to(dev)
     valid = torch.zeros(N)
@@ -106,25 +136,32 @@ def configs_legs(torch, dev, big_blocks=4):
     ms = s.elapsed_time(e)
     fb = block_flops(N)["block"] * big_blocks
     legs["c4_big"] = {"N": N, "blocks": big_blocks, "rows_per_chunk": 256, "ms": round(ms, 2), "ms_per_block": round(ms / big_blocks, 2),
-                      "tflops": round(fb / (ms * 1e-3) / 1e12, 1), "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2)}
+                      "tflops": round(fb / (ms * 1e-3) / 1e12, 1), "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
+                      "peak_note": "this leg alone: z 1.07 GB + the shared scratch of its largest call"}
     del zb
     return legs
 
 
-def time_events(fn, reps, torch):
-    """Mean ms per call of fn() over reps calls, bracketed by HIP events on the current stream."""
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+def step_times(fn, reps, torch):
+    """Per-call ms of fn() over reps back-to-back calls: a HIP event before every call and one after the last, all on the current
+    stream (the stream the library launches on), synchronised before the first and after the last."""
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     torch.cuda.synchronize()
-    s.record()
-    for _ in range(reps):
+    for i in range(reps):
+        ev[i].record()
         fn()
-    e.record()
+    ev[reps].record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / reps
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(reps)]
+
+
+def time_events(fn, reps, torch):
+    """Median ms per call of fn() over max(reps, 20) calls (median of >= 20 after warm-up)."""
+    return statistics.median(step_times(fn, max(reps, 20), torch))
 
 
 def time_raw(entry, args, reps, torch):
-    """Mean ms per call of one C-ABI entry point called back to back with a prebuilt argument block (HIP events on torch's
+    """Median ms per call of one C-ABI entry point called back to back with a prebuilt argument block (HIP events on torch's
     current stream, the stream the library launches on)."""
     import ctypes
     from fpf_hip import _lib as L
@@ -134,14 +171,7 @@ def time_raw(entry, args, reps, torch):
     ref = ctypes.byref(args)
     if fn(ref, st, err, 512) != 0:
         raise RuntimeError("%s: %s" % (entry, err.value.decode()))
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    s.record()
-    for _ in range(reps):
-        fn(ref, st, err, 512)
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / reps
+    return time_events(lambda: fn(ref, st, err, 512), reps, torch)
 
 
 def ln_args(x, y, w, b):
@@ -203,7 +233,11 @@ def cpu_baseline(torch):
     (N = 64, c_z = 128, 4 x 32 heads, transition 4x, fp32), 2 warm-ups then the median of 5."""
     sys.path.insert(0, ROOT)
     from oracle import stock as S
-    cores = torch.get_num_threads()
+    # every core this process may run on, capped by the box's per-job thread budget (OMP_NUM_THREADS, set by the GPU pool)
+    avail = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS") or avail)
+    cores = max(1, min(avail, cap))
+    torch.set_num_threads(cores)
     P = S.make_block_params(c_z=128, heads=4, head_dim=32, seed=0)
     z = torch.randn(1, 64, 64, 128, generator=torch.Generator().manual_seed(0))
     mask = torch.ones(1, 64, 64)
@@ -215,8 +249,9 @@ def cpu_baseline(torch):
     med = statistics.median(ts[2:])
     fl = block_flops(64)["block"]
     return {"value": round(fl / med / 1e12, 5), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "host_cpus": os.cpu_count(), "affinity_cpus": avail,
             "sample": "BASELINE configs[0]: one pair block N=64 c_z=128 fp32 (stock statements, oracle/stock.py), median of 5 after 2 "
-                      "warm-ups; %.1f ms per block, %.2f GFLOP" % (med * 1e3, fl / 1e9)}
+                      "warm-ups; %.1f ms per block, %.2f GFLOP; torch threads = the process's CPUs capped by OMP_NUM_THREADS" % (med * 1e3, fl / 1e9)}
 
 
 def main():
@@ -227,6 +262,7 @@ def main():
     ap.add_argument("--n", type=int, default=768)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trunk-layers", type=int, default=48, help="BASELINE config-3 trunk leg (0: skip)")
+    ap.add_argument("--stack-layers", type=int, default=48, help="the north star's pair stack at N (0: skip)")
     ap.add_argument("--no-configs", action="store_true", help="skip the config-1 (tri-att N = 384) and config-4 (big, N = 2048) legs")
     ap.add_argument("--probe", default=None, help="launch-only run for counter passes: triattn_core | copy")
     a = ap.parse_args()
@@ -254,14 +290,9 @@ def main():
         PFM.pair_block(z, mask, blk)
     torch.cuda.synchronize()
     z.normal_()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    s.record()
-    for _ in range(a.steps):
-        PFM.pair_block(z, mask, blk)
-    e.record()
-    torch.cuda.synchronize()
-    ms = s.elapsed_time(e) / a.steps
+    # exactly `steps` steps, synchronised on both sides, an event pair around each: ms_per_step = the median step
+    per = step_times(lambda: PFM.pair_block(z, mask, blk), a.steps, torch)
+    ms = statistics.median(per)
     tflops = fl["block"] / (ms * 1e-3) / 1e12
 
     # per-site breakdown (each site alone, same resident z)
@@ -314,9 +345,12 @@ def main():
            "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
            "config": {"workload": "one pair block (trimul out, trimul in, tri-att start, tri-att end, transition 4x), in place", "N": N,
                       "c_z": 128, "c_hidden": 128, "heads": 4, "head_dim": 32, "batch": 1, "mask": "all ones",
-                      "block_tflop": round(fl["block"] / 1e12, 4), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
+                      "block_tflop": round(fl["block"] / 1e12, 4), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                      "timing": "median of %d per-step HIP-event intervals (mean %.4f ms, min %.4f)" % (len(per), statistics.mean(per), min(per))},
            "roofline": roof, "breakdown": breakdown}
     del keep, zb, yln
+    if a.stack_layers > 0:
+        out["pair_stack"] = pair_stack_leg(torch, dev, a.stack_layers, N=N)
     if a.trunk_layers > 0:
         out["trunk"] = trunk(torch, dev, a.trunk_layers)
     if not a.no_configs:

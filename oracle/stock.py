@@ -33,6 +33,7 @@ import math
 import torch
 
 __all__ = ["layer_norm", "triangle_attention_op", "tri_attn", "triatt_prologue", "triatt_epilogue", "trimul", "trimul_rows",
+           "trimul_autocast", "tri_attn_autocast", "transition_autocast", "pair_block_autocast",
            "tri_attn_rows", "transition", "pair_block", "make_block_params", "block_flops", "pair_bias_attention_op", "pair_bias",
            "attention_pair_bias", "single_track", "pairformer_layer", "make_single_params", "single_flops"]
 
@@ -79,7 +80,8 @@ def _as4(z):
 
 def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_step=64, inf=1e9):
     """Stock TriangleAttention{Starting,Ending}Node forward -> the update in z's frame ([B,N,N,C] or [N,N,C]).
-    P: dict ln_w, ln_b [C], w_q, w_k, w_v, w_g [H*D, C], w_b [H, C], w_o [C, H*D], plus ints H, D.
+    P: dict ln_w, ln_b [C], w_q, w_k, w_v, w_g [H*D, C], w_b [H, C], w_o [C, H*D], plus ints H, D; optional b_g [H*D] (linear_g
+    bias) and b_o [C] (linear_o bias), the Linear biases of primitives.py:259-270 where a kit's module carries them.
     The ending node transposes z (and the mask) in and the update out (attention.py:140-142, :175-176).
     Pinned by: scalar loops over the published equations (starting and ending node each in its own index form), ending(z) ==
     starting(z^T)^T, the op form (triangle_attention_op) on the same projections, and the BASELINE config-1 block
@@ -95,6 +97,8 @@ def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_ste
     x = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
     wq, wk, wv, wg = (P[n].to(dtype) for n in ("w_q", "w_k", "w_v", "w_g"))
     wb, wo = P["w_b"].to(dtype), P["w_o"].to(dtype)
+    bg = None if P.get("b_g") is None else P["b_g"].to(dtype)
+    bo = None if P.get("b_o") is None else P["b_o"].to(dtype)
     tri_bias = torch.matmul(x, wb.t()).permute(0, 3, 1, 2).unsqueeze(1)          # [B, 1, H, I, J]
     out = torch.empty(B, N, N, wo.shape[0], dtype=dtype)
     for i0 in range(0, N, rows_per_step):
@@ -107,8 +111,10 @@ def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_ste
         a = torch.matmul(q, kk.transpose(-1, -2)) + mask_bias + tri_bias            # [B, r, H, J, J]
         a = torch.softmax(a, dim=-1)
         o = torch.matmul(a, vv).transpose(-2, -3)                                   # [B, r, J, H, D]
-        g = torch.sigmoid(torch.matmul(xi, wg.t())).view(B, i1 - i0, N, H, D)
-        out[:, i0:i1] = torch.matmul((o * g).reshape(B, i1 - i0, N, H * D), wo.t())
+        gl = torch.matmul(xi, wg.t())
+        g = torch.sigmoid(gl if bg is None else gl + bg).view(B, i1 - i0, N, H, D)
+        u = torch.matmul((o * g).reshape(B, i1 - i0, N, H * D), wo.t())
+        out[:, i0:i1] = u if bo is None else u + bo
     if ending:
         out = out.transpose(1, 2)
     return out[0] if sq else out
@@ -130,15 +136,18 @@ def triatt_prologue(z, P, *, ending=False, dtype=torch.float64):
         return torch.matmul(x, w.to(dtype).t()).view(B, N, N, H, D).permute(0, 1, 3, 2, 4)
     q, k, v = heads(P["w_q"]), heads(P["w_k"]), heads(P["w_v"])
     g = torch.matmul(x, P["w_g"].to(dtype).t())
+    if P.get("b_g") is not None:
+        g = g + P["b_g"].to(dtype)
     bias = torch.matmul(x, P["w_b"].to(dtype).t()).permute(0, 3, 1, 2).unsqueeze(1)
     return q, k, v, g, bias
 
 
 def triatt_epilogue(o, g, P, *, dtype=torch.float64):
-    """u [B,I,J,C_out] = (sigmoid(g) * o) @ w_o^T in the attention frame; o [B,I,H,J,D], g [B,I,J,H*D]."""
+    """u [B,I,J,C_out] = (sigmoid(g) * o) @ w_o^T (+ b_o) in the attention frame; o [B,I,H,J,D], g [B,I,J,H*D] (b_g already in)."""
     B, I, H, J, D = o.shape
     ot = o.to(dtype).permute(0, 1, 3, 2, 4).reshape(B, I, J, H * D)
-    return torch.matmul(torch.sigmoid(g.to(dtype)) * ot, P["w_o"].to(dtype).t())
+    u = torch.matmul(torch.sigmoid(g.to(dtype)) * ot, P["w_o"].to(dtype).t())
+    return u if P.get("b_o") is None else u + P["b_o"].to(dtype)
 
 
 def trimul(z, mask=None, *, direction, weights, residual=False, dtype=torch.float64, eps=1e-5):
@@ -214,8 +223,10 @@ def tri_attn_rows(z, P, mask, rows, *, ending=False, dtype=torch.float32):
     def heads(wn):
         return torch.matmul(xr, P[wn].to(dtype).t()).view(len(idx), N, H, D).permute(0, 2, 1, 3).unsqueeze(0)
     o = triangle_attention_op(heads("w_q"), heads("w_k"), heads("w_v"), bias, m[idx][None, :, None, None, :], dtype=dtype)
-    g = torch.matmul(xr, P["w_g"].to(dtype).t()).unsqueeze(0)
-    return triatt_epilogue(o, g, P, dtype=dtype)[0]
+    g = torch.matmul(xr, P["w_g"].to(dtype).t())
+    if P.get("b_g") is not None:
+        g = g + P["b_g"].to(dtype)
+    return triatt_epilogue(o, g.unsqueeze(0), P, dtype=dtype)[0]
 
 
 def transition(x, w_a, w_b, w_o, ln_w=None, ln_b=None, *, eps=1e-5, mask=None, residual=False, dtype=torch.float64):
@@ -243,6 +254,101 @@ def pair_block(z, mask, params, *, dtype=torch.float64):
     t = params["tr"]
     z = z + transition(z, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"], dtype=dtype)
     return z
+
+
+# ------------------------------------------------------------------------------------------------ the bf16-autocast statement
+# The stock modules run under torch.autocast(bfloat16) in the reference's fast paths; the reference admits a bf16 kernel when its
+# error vs an fp64 statement is at most 1.25x (rms) / 2.5x (max-abs) THIS statement's own error (SAME_CLASS,
+# common/opt_core/opt_core/kernels/fpf_trimul_v4/generic.py:42-43).  Restated here with autocast's rounding points made explicit
+# (fp32 arithmetic, bf16 rounding where autocast stores bf16): Linear = bf16 operands, fp32 accumulation, bf16 output; LayerNorm
+# runs in fp32 (autocast's fp32 list) and returns fp32; elementwise ops on bf16 tensors return bf16; an in-place add into a bf16
+# tensor rounds to bf16; a bf16 * fp32 product promotes to fp32; the residual stream z stays fp32 (pairformer.py:75-102).
+
+def _bf(t):
+    return t.to(torch.bfloat16).to(torch.float32)
+
+
+def _lin_ac(x, w, rnd=_bf):
+    """autocast Linear / matmul: bf16 operands, fp32 accumulation, bf16 result."""
+    return rnd(torch.matmul(rnd(x), rnd(w).t()))
+
+
+def trimul_autocast(z, mask, *, direction, weights, eps=1e-5, rnd=_bf):
+    """TriangleMultiplication{Outgoing,Incoming}.forward under bf16 autocast (triangular_mult.py:110-124 / :198-212): x = LN_in(z)
+    fp32; p_in(x), g_in(x) bf16, sigmoid and product bf16; * mask promotes to fp32 (exact); the einsum runs as an autocast bmm
+    (bf16 operands, fp32 accumulation, bf16 result); LN_out fp32; p_out, g_out bf16; sigmoid and product bf16."""
+    w = {k_: v_.to(torch.float32) for k_, v_ in weights.items() if hasattr(v_, "to")}
+    z4, sq = _as4(z)
+    x = layer_norm(z4.to(torch.float32), w["ln_in_w"], w["ln_in_b"], eps)
+    a = rnd(_lin_ac(x, w["w_ap"], rnd) * rnd(torch.sigmoid(_lin_ac(x, w["w_ag"], rnd))))
+    b = rnd(_lin_ac(x, w["w_bp"], rnd) * rnd(torch.sigmoid(_lin_ac(x, w["w_bg"], rnd))))
+    if mask is not None:
+        m = (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(torch.float32).unsqueeze(-1)
+        a, b = a * m, b * m
+    if direction in ("outgoing", "out"):
+        X = torch.einsum("bikd,bjkd->bijd", a, b)
+    else:
+        X = torch.einsum("bkid,bkjd->bijd", a, b)
+    X = rnd(X)
+    out = rnd(_lin_ac(layer_norm(X, w["ln_out_w"], w["ln_out_b"], eps), w["w_o"], rnd) * rnd(torch.sigmoid(_lin_ac(x, w["w_og"], rnd))))
+    return out[0] if sq else out
+
+
+def tri_attn_autocast(z, P, mask=None, *, ending=False, inf=1e9, rows_per_step=64, rnd=_bf):
+    """TriangleAttention.forward under bf16 autocast (attention.py:140-176, primitives.py:176-196, :265-366): x = LN(x) fp32;
+    triangle_bias = linear(x) bf16; q, k, v bf16, q / sqrt(c) bf16; a = q k^T bf16; a += mask_bias then a += triangle_bias, each
+    rounded to bf16 in place; softmax in bf16 (softmax_no_cast); a v bf16; g = sigmoid(linear_g) bf16; o * g bf16; linear_o bf16."""
+    z4, sq = _as4(z)
+    B, N, _, C = z4.shape
+    H, D = int(P["H"]), int(P["D"])
+    x = z4.to(torch.float32)
+    m = torch.ones(B, N, N) if mask is None else (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(torch.float32)
+    if ending:
+        x, m = x.transpose(1, 2), m.transpose(1, 2)
+    x = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
+    tri_bias = _lin_ac(x, P["w_b"], rnd).permute(0, 3, 1, 2).unsqueeze(1)            # [B, 1, H, I, J]
+    out = torch.empty(B, N, N, P["w_o"].shape[0])
+    for i0 in range(0, N, rows_per_step):
+        i1 = min(N, i0 + rows_per_step)
+        xi = x[:, i0:i1]
+        r = i1 - i0
+
+        def heads(w):
+            return _lin_ac(xi, w, rnd).view(B, r, N, H, D).transpose(-2, -3)
+        q = rnd(heads(P["w_q"]) / math.sqrt(D))
+        k, v = heads(P["w_k"]), heads(P["w_v"])
+        a = rnd(torch.matmul(q, k.transpose(-1, -2)))
+        a = rnd(a + (inf * (m[:, i0:i1] - 1.0))[:, :, None, None, :])
+        a = rnd(a + tri_bias)
+        a = rnd(torch.softmax(a, dim=-1))
+        o = rnd(torch.matmul(a, v)).transpose(-2, -3)                                    # [B, r, J, H, D]
+        gl = _lin_ac(xi, P["w_g"], rnd)
+        if P.get("b_g") is not None:
+            gl = rnd(gl + rnd(P["b_g"]))
+        g = rnd(torch.sigmoid(gl)).view(B, r, N, H, D)
+        u = _lin_ac(rnd(o * g).reshape(B, r, N, H * D), P["w_o"], rnd)
+        out[:, i0:i1] = u if P.get("b_o") is None else rnd(u + rnd(P["b_o"]))
+    if ending:
+        out = out.transpose(1, 2)
+    return out[0] if sq else out
+
+
+def transition_autocast(x, w_a, w_b, w_o, ln_w=None, ln_b=None, *, eps=1e-5, rnd=_bf):
+    """Transition.forward under bf16 autocast (transition.py:63-66): LN fp32; fc1, fc2 bf16; silu bf16; product bf16; fc3 bf16."""
+    n = layer_norm(x.to(torch.float32), ln_w, ln_b, eps)
+    return _lin_ac(rnd(rnd(torch.nn.functional.silu(_lin_ac(n, w_a, rnd))) * _lin_ac(n, w_b, rnd)), w_o, rnd)
+
+
+def pair_block_autocast(z, mask, params, *, rnd=_bf):
+    """The pair stack of pairformer.py:75-102 under bf16 autocast: every site's statement above, the residual stream fp32.
+    ``rnd`` = the identity turns every rounding point off (then this is the fp32 statement ``pair_block``: its pin)."""
+    z = z.to(torch.float32)
+    z = z + trimul_autocast(z, mask, direction="outgoing", weights=params["tmo"], rnd=rnd)
+    z = z + trimul_autocast(z, mask, direction="incoming", weights=params["tmi"], rnd=rnd)
+    z = z + tri_attn_autocast(z, params["tas"], mask, ending=False, rnd=rnd)
+    z = z + tri_attn_autocast(z, params["tae"], mask, ending=True, rnd=rnd)
+    t = params["tr"]
+    return z + transition_autocast(z, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"], rnd=rnd)
 
 
 def make_block_params(c_z=128, heads=4, head_dim=32, factor=4, seed=0):

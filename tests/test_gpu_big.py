@@ -72,6 +72,30 @@ def test_chunked_block_bitwise_equals_whole(ending, residual, chunk, asym):
     assert torch.equal(u1, u2), "chunked != whole: max diff %.3e" % (u1.float() - u2.float()).abs().max().item()
 
 
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("chunk", [256, 100])
+def test_chunked_block_bitwise_equals_whole_n768(ending, chunk):
+    """The metric size: the whole block takes the 8-wave block-layout core, 256-row chunks the 4-wave one (fewer workgroups),
+    100-row chunks ranges that are not a multiple of the core's 3-row groups; with an asymmetric mask (a random keep pattern and a
+    masked key band on one side only) both must equal the whole block bit for bit."""
+    from fpf_hip.attn import pair_fused as PF
+    N = 768
+    P = _ta_weights(6)
+    W = _ta_pack(P)
+    g = torch.Generator().manual_seed(61)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(DEV)
+    mask = (torch.rand(1, N, N, generator=g) > 0.25).float()
+    mask[:, :, 600:650] = 0
+    mask = mask.to(DEV)
+    print("[big] N=%d chunk=%d ending=%s asym" % (N, chunk, ending), flush=True)
+    z1, z2 = z.clone(), z.clone()
+    PF.tri_attn_block(z1, W, mask, ending=ending, residual=True)
+    PF.tri_attn_block_chunked(z2, W, mask, ending=ending, residual=True, chunk=chunk)
+    torch.cuda.synchronize()
+    assert torch.equal(z1, z2), "chunked != whole: max diff %.3e" % (z1.float() - z2.float()).abs().max().item()
+    assert not torch.equal(z1, z)
+
+
 def test_chunked_block_against_oracle():
     from fpf_hip.attn import pair_fused as PF
     N = 130

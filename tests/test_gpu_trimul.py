@@ -109,7 +109,7 @@ def test_trimul_bf16_masked_rows_update_is_gate_times_bias_projection():
 
 
 TRIMUL = json.load(open(os.path.join(GOLDEN, "trimul_cases.json")))["cases"]
-CF = [c for c in TRIMUL if c["form"] == "bf16" and c["c_z"] == 128 and c["n"] <= 256]
+CF = [c for c in TRIMUL if c["form"] == "bf16" and c["c_z"] == 128]          # N 32 .. 403 (the ragged incoming N = 403 included)
 
 
 @pytest.mark.parametrize("case", CF, ids=[c["id"] for c in CF])
@@ -118,6 +118,7 @@ def test_trimul_closed_form_vectors(case):
     kernel's recorded error for the same inputs."""
     from fpf_hip.kernels import trimul as TM
     z, mask, w = V.trimul_inputs(case)
+    print("[case] %s" % case["id"], flush=True)
     out = TM.triangle_multiplication(z.to(DEV), None if mask is None else mask.to(DEV), direction=case["direction"], weights=_dev(w),
                                      word="fast", residual=case["residual"])
     torch.cuda.synchronize()

@@ -126,6 +126,8 @@ def _brute_tri_attn(z, P, mask, ending):
     H, D = int(P["H"]), int(P["D"])
     lw, lb = P["ln_w"].numpy(), P["ln_b"].numpy()
     W = {n: P[n].numpy() for n in ("w_q", "w_k", "w_v", "w_g", "w_b", "w_o")}
+    bg = None if P.get("b_g") is None else P["b_g"].numpy()
+    bo = None if P.get("b_o") is None else P["b_o"].numpy()
     x = np.zeros_like(zz)
     for i in range(N):
         for j in range(N):
@@ -160,10 +162,11 @@ def _brute_tri_attn(z, P, mask, ending):
                     for kx, l_ in logits:
                         vv = lin(W["w_v"], i, kx, h * D + d) if not ending else lin(W["w_v"], kx, j, h * D + d)
                         acc += math.exp(l_ - mx) / den * vv
-                    gate = 1.0 / (1.0 + math.exp(-lin(W["w_g"], i, j, h * D + d)))
+                    gl = lin(W["w_g"], i, j, h * D + d) + (0.0 if bg is None else bg[h * D + d])
+                    gate = 1.0 / (1.0 + math.exp(-gl))
                     o[h * D + d] = gate * acc
             for c in range(out.shape[2]):
-                out[i, j, c] = sum(W["w_o"][c, r] * o[r] for r in range(H * D))
+                out[i, j, c] = sum(W["w_o"][c, r] * o[r] for r in range(H * D)) + (0.0 if bo is None else bo[c])
     return torch.from_numpy(out).unsqueeze(0)
 
 
@@ -181,6 +184,17 @@ def test_tri_attn_brute_force_published_equations():
         ref = _brute_tri_attn(z, P, mask, ending)
         got = S.tri_attn(z, P, mask, ending=ending)
         assert torch.allclose(got, ref, atol=1e-10, rtol=0), (ending, (got - ref).abs().max().item())
+    # the Linear biases a kit's module may carry (linear_g, linear_o): in the brute force per element, and in the stage forms
+    Pb = dict(P, b_g=torch.randn(H * D, generator=g, dtype=torch.float64), b_o=torch.randn(5, generator=g, dtype=torch.float64))
+    for ending in (False, True):
+        ref = _brute_tri_attn(z, Pb, mask, ending)
+        got = S.tri_attn(z, Pb, mask, ending=ending)
+        assert torch.allclose(got, ref, atol=1e-10, rtol=0), (ending, (got - ref).abs().max().item())
+        assert (got - S.tri_attn(z, P, mask, ending=ending)).abs().max() > 0.1          # the biases matter on these inputs
+        q, k, v, gg, bias = S.triatt_prologue(z, Pb, ending=ending)
+        mx = mask.transpose(1, 2) if ending else mask
+        staged = S.triatt_epilogue(S.triangle_attention_op(q, k, v, bias, mx.bool()[:, :, None, None, :]), gg, Pb)
+        assert torch.allclose(staged.transpose(1, 2) if ending else staged, ref, atol=1e-10, rtol=0)
 
 
 def test_tri_attn_equals_prologue_op_epilogue():
@@ -323,6 +337,115 @@ def test_pair_block_config1_runs_and_is_finite():
     z = torch.randn(1, 8, 8, 32, generator=torch.Generator().manual_seed(0))
     out = S.pair_block(z, torch.ones(1, 8, 8), P, dtype=torch.float64)
     assert out.shape == z.shape and torch.isfinite(out).all()
+
+
+def _site_fns(P, mask):
+    t = P["tr"]
+    return {"tmo": lambda z: S.trimul(z, mask, direction="outgoing", weights=P["tmo"]),
+            "tmi": lambda z: S.trimul(z, mask, direction="incoming", weights=P["tmi"]),
+            "tas": lambda z: S.tri_attn(z, P["tas"], mask, ending=False),
+            "tae": lambda z: S.tri_attn(z, P["tae"], mask, ending=True),
+            "tr": lambda z: S.transition(z, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"])}
+
+
+def test_pair_block_site_order_is_pinned():
+    """boltz2/stock/src/boltz/model/layers/pairformer.py:75-102: z += tri_mul_out; z += tri_mul_in; z += tri_att_start;
+    z += tri_att_end; z += transition_z, each site reading the z the previous one updated.  pair_block equals that composition,
+    and on these inputs swapping any two adjacent sites (or reading the block input at every site) moves the result by far more
+    than rounding, so a wrong order would fail here."""
+    P = S.make_block_params(c_z=128, heads=4, head_dim=32, seed=0)
+    N = 10
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
+    mask = torch.ones(1, N, N, dtype=torch.float64)
+    fn = _site_fns(P, mask)
+    order = ["tmo", "tmi", "tas", "tae", "tr"]
+
+    def compose(seq):
+        x = z
+        for name in seq:
+            x = x + fn[name](x)
+        return x
+    got = S.pair_block(z, mask, P, dtype=torch.float64)
+    want = compose(order)
+    assert torch.allclose(got, want, atol=1e-12, rtol=0)
+    scale = want.norm()
+    for i in range(len(order) - 1):
+        sw = list(order)
+        sw[i], sw[i + 1] = sw[i + 1], sw[i]
+        assert (compose(sw) - want).norm() / scale > 1e-3, sw
+    parallel = z + sum(fn[name](z) for name in order)
+    assert (parallel - want).norm() / scale > 1e-3
+
+
+def test_pairformer_layer_single_track_reads_the_updated_z_in_order():
+    """pairformer.py:75-111: the pair stack first, then the sequence stack on the UPDATED z: s_n = LN_s(s);
+    s += attention(s_n, z_new, mask, k_in = s_n); s += transition_s(s).  Each composition step is checked against its alternative
+    (the block-input z, the transition on the pre-attention s), which moves the result on these inputs."""
+    C, CS, H, N = 32, 48, 4, 6
+    P = S.make_block_params(c_z=C, heads=2, head_dim=8, seed=2)
+    P["single"] = S.make_single_params(c_s=CS, c_z=C, heads=H, seed=3)
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(1, N, N, C, generator=g, dtype=torch.float64)
+    s = torch.randn(1, N, CS, generator=g, dtype=torch.float64)
+    mask = torch.ones(1, N, dtype=torch.float64)
+    pmask = torch.ones(1, N, N, dtype=torch.float64)
+    s_out, z_out = S.pairformer_layer(s, z, mask, pmask, P, dtype=torch.float64)
+    z_new = S.pair_block(z, pmask, P, dtype=torch.float64)
+    assert torch.allclose(z_out, z_new, atol=1e-12, rtol=0)
+    a, t = P["single"]["apb"], P["single"]["trs"]
+
+    def track(zz, post_attn=True):
+        sn = S.layer_norm(s, a["ln_s_w"], a["ln_s_b"], 1e-5)
+        s1 = s + S.attention_pair_bias(sn, zz, mask, a, dtype=torch.float64)
+        src = s1 if post_attn else s
+        return s1 + S.transition(src, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"], dtype=torch.float64)
+    want = track(z_new)
+    assert torch.allclose(s_out, want, atol=1e-12, rtol=0)
+    assert (track(z) - want).norm() / want.norm() > 1e-4          # the block-input z would be caught
+    assert (track(z_new, post_attn=False) - want).norm() / want.norm() > 1e-4
+
+
+# ----------------------------------------------------------------------------------------------------------------- bf16-autocast yardstick
+def test_autocast_statements_without_rounding_are_the_fp32_statements():
+    """The bf16-autocast restatements differ from the fp32 statements ONLY by their rounding points: with rounding off they
+    equal the pinned fp32 statements (a dropped term, a wrong index or a transposed operand would show here)."""
+    P = S.make_block_params(c_z=128, heads=4, head_dim=32, seed=5)
+    N = 12
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(6))
+    mask = torch.ones(1, N, N)
+    mask[:, :, N - 2:] = 0
+    ident = lambda t: t                                                  # noqa: E731
+    for d in ("outgoing", "incoming"):
+        a = S.trimul_autocast(z, mask, direction=d, weights=P["tmo"], rnd=ident)
+        assert torch.allclose(a, S.trimul(z, mask, direction=d, weights=P["tmo"], dtype=torch.float32), atol=1e-5, rtol=0)
+    for ending in (False, True):
+        Pb = dict(P["tas"], b_g=torch.randn(128, generator=torch.Generator().manual_seed(7)), b_o=0.1 * torch.ones(128))
+        a = S.tri_attn_autocast(z, Pb, mask, ending=ending, rnd=ident)
+        assert torch.allclose(a, S.tri_attn(z, Pb, mask, ending=ending, dtype=torch.float32), atol=1e-5, rtol=0)
+    got = S.pair_block_autocast(z, mask, P, rnd=ident)
+    assert torch.allclose(got, S.pair_block(z, mask, P, dtype=torch.float32), atol=1e-4, rtol=0)
+    # and with rounding on they are a bf16-class statement: within a few e-3 of the fp32 statement, not equal to it
+    ac = S.pair_block_autocast(z, mask, P)
+    ref = S.pair_block(z, mask, P, dtype=torch.float32)
+    rel = ((ac - ref).norm() / ref.norm()).item()
+    assert 1e-3 < rel < 2e-2, rel
+
+
+def test_transition_autocast_reproduces_the_recorded_stock_error():
+    """The reference records the stock bf16 statement's error vs fp64 for the pair transition at N <= 800: relrms 4.575e-3
+    (common/opt_core/opt_core/kernels/transition/TRANSITION_CELLS.json, cell 9.0|bf16|pair_c128_n4|N<=800, row torch_swiglu).
+    The restated rounding points reproduce it on inputs of that cell's class (c 128, hidden 512, z ~ N(0, 1), weights
+    N(0, 1/fan_in) in bf16); dropping or adding one bf16 rounding of the hidden moves it by ~10 %."""
+    g = torch.Generator().manual_seed(0)
+    C, Hd = 128, 512
+    x = torch.randn(120 * 120, C, generator=g).to(torch.bfloat16).double()
+    wa = (torch.randn(Hd, C, generator=g) / math.sqrt(C)).to(torch.bfloat16).double()
+    wb = (torch.randn(Hd, C, generator=g) / math.sqrt(C)).to(torch.bfloat16).double()
+    wo = (torch.randn(C, Hd, generator=g) / math.sqrt(Hd)).to(torch.bfloat16).double()
+    ref = S.transition(x, wa, wb, wo)
+    ac = S.transition_autocast(x, wa, wb, wo).double()
+    rel = ((ac - ref).pow(2).mean().sqrt() / ref.pow(2).mean().sqrt()).item()
+    assert abs(rel / 4.575e-3 - 1) < 0.05, rel
 
 
 # ----------------------------------------------------------------------------------------------------------------- row-sampled forms

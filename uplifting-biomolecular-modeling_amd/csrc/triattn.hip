@@ -1243,7 +1243,7 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
       // 8 waves share each K / V^T tile among 256 queries; they pay where S fills whole 256-query tiles and the grid still
       // has at least 8 workgroups per CU (N = 768: 3072; N = 512: 1368, where 4 waves and twice the workgroups are faster)
       const int64_t rows_heads = a->B * a->H * cdiv(a->N, TA_R);
-      if (p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * 256) {
+      if (p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * (int64_t)num_cus()) {
         const int64_t total_w = rows_heads * (p.S / (32 * TA_DMA_WAVES));
         hipLaunchKernelGGL(triattn_core_bf16_dma<TA_DMA_WAVES>, dim3((unsigned)(cdiv(total_w, 8) * 8)), dim3(64 * TA_DMA_WAVES), 0, st, p);
       } else {
