@@ -122,6 +122,15 @@ typedef struct {
 size_t fpf_trimul_workspace_bytes(int64_t batch, int64_t n, int32_t c_z, int32_t c_h, int32_t dtype);
 int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, size_t errlen);
 
+/* The same triangle multiplication without a caller workspace.  No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The workspace
+ * is a static per-device array of FPF_TRIMUL_NOALLOC_SCRATCH_BYTES (48 MiB, held by every GPU the library runs on until the
+ * process ends): a call needing more (fpf_trimul_workspace_bytes; bf16 at B = 1: N <= 256) is refused with FPF_E_WORKSPACE.
+ * a->workspace must be NULL and a->workspace_bytes 0.  The entry allocates nothing and uses the current device's array (the
+ * device of `stream` must be current).  Calls that overlap on one GPU (two streams or host threads) share the array and race. */
+#define FPF_TRIMUL_NOALLOC_SCRATCH_BYTES 50331648
+int fpf_trimul_fwd_noalloc(const FpfTrimulArgs* a, void* stream, char* err, size_t errlen);
+
 /* ---------------------------------------------------------------------------------------------------------------- triangle attention (op)
  * out[b,n,h,i,:] = softmax_j(scale q.k + bias[b,h,i,j], -inf where mask[b,n,j] == 0) @ v[b,n,h,j,:];
  * a row whose keys are all masked is the uniform mean of v over all keys.

@@ -9,6 +9,8 @@
 // contraction needs no bounds checks.  The fp32 path (exact tier) has the same three launches in fp32 scalar FMA.
 #include <algorithm>
 
+#include <mutex>
+
 #include "rowtile.h"
 
 namespace fpf {
@@ -697,4 +699,51 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
     return launched(err, errlen, "trimul_k3_f32");
   }
   return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);
+}
+
+// ---------------------------------------------------------------------------------------------------------------- no-allocation entry
+// fpf_trimul_fwd for callers that cannot allocate (graph capture, serving loops, harnesses that forbid hipMalloc): the
+// workspace is a file-scope device array, `scratch`, which every GPU the library runs on holds until the process ends.  In
+// host code `scratch` names a host-side stand-in, not device memory: its device address is taken once per device with that
+// device current (hipGetSymbolAddress) and only that address is handed to kernels.  The K1 planes need no clearing (K1
+// writes every padded element, zeros outside the N x N pixels), so nothing is reset between calls.  Calls that overlap on
+// one GPU (two streams, two host threads) share the array and race.
+namespace fpf {
+static __device__ __align__(256) unsigned char scratch[FPF_TRIMUL_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+// The device address of this device's `scratch` (looked up on its first use here, with the device current).
+static int scratch_address(void** out, char* err, size_t errlen) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(err, errlen, FPF_E_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(err, errlen, FPF_E_ARGS, "device %d outside the 64 this library tracks", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(err, errlen, FPF_E_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FPF_OK;
+}
+}  // namespace fpf
+
+extern "C" int fpf_trimul_fwd_noalloc(const FpfTrimulArgs* a, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (a->workspace || a->workspace_bytes)
+    return fail(err, errlen, FPF_E_ARGS, "the no-allocation entry uses the library's static scratch: pass workspace NULL, workspace_bytes 0");
+  if (a->batch < 0 || a->n < 0) return fail(err, errlen, FPF_E_SHAPE, "batch / n negative");
+  const size_t need = fpf_trimul_workspace_bytes(a->batch, a->n, a->c_z, a->c_h, a->dtype);
+  if (need > (size_t)FPF_TRIMUL_NOALLOC_SCRATCH_BYTES)
+    return fail(err, errlen, FPF_E_WORKSPACE, "needs %zu workspace bytes, above the %zu-byte static scratch (bf16, B = 1: N <= 256)", need,
+                (size_t)FPF_TRIMUL_NOALLOC_SCRATCH_BYTES);
+  FpfTrimulArgs b = *a;
+  const int rc = scratch_address(&b.workspace, err, errlen);
+  if (rc) return rc;
+  b.workspace_bytes = (size_t)FPF_TRIMUL_NOALLOC_SCRATCH_BYTES;
+  return fpf_trimul_fwd(&b, stream, err, errlen);
 }

@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
 ABI_VERSION = 5
 DT_BF16, DT_F32, DT_U8 = 1, 2, 3
+TRIMUL_NOALLOC_SCRATCH_BYTES = 50331648          # include/fpf_hip.h FPF_TRIMUL_NOALLOC_SCRATCH_BYTES
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
 
 i32, i64, f32, vp, sz = C.c_int32, C.c_int64, C.c_float, C.c_void_p, C.c_size_t
@@ -84,6 +85,7 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_transition_fwd": ([C.POINTER(TransitionArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_trimul_workspace_bytes": ([i64, i64, i32, i32, i32], sz),
     "fpf_trimul_fwd": ([C.POINTER(TrimulArgs), vp, C.c_char_p, sz], C.c_int),
+    "fpf_trimul_fwd_noalloc": ([C.POINTER(TrimulArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_fwd": ([C.POINTER(TriattnArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_workspace_bytes": ([i64, i64, i64, i32, i32, i32, i32], sz),
     "fpf_triattn_bias_fwd": ([C.POINTER(TriattnBiasArgs), vp, C.c_char_p, sz], C.c_int),
