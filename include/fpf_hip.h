@@ -23,8 +23,10 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 5   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
-                               5: gate / output projection biases b_g, b_o on the tri-att block and its stages */
+#define FPF_ABI_VERSION 6   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+                               5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
+                               6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
+                                  (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes) */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
 enum {
@@ -159,8 +161,18 @@ typedef struct {
   void* out;
   int64_t out_stride[5];   /* stride[4] must be 1 */
   float scale;
+  const uint64_t* keep;    /* v_layout 2 only: the mask as a keep-bit table [B, N, S / 64 + 1] (per attention row: word 0 = flags,
+                              bit 0 some key kept, bit 1 every key kept; word 1 + t = keep bits of keys 64 t .. 64 t + 63, all set
+                              for a row with no kept key), or NULL with mask NULL (every key kept).  The fused block builds it from
+                              its pair mask in its workspace; v_layout 2 with a mask and no table is refused (FPF_E_ARGS).  Other
+                              layouts read `mask` and ignore this field. */
+  void* workspace;         /* v_layout 2 only: device memory of fpf_triattn_workspace_bytes(B, N, H, S, 2) bytes (per work item a
+                              flag the fast kernel writes and its fallback reads); other layouts ignore it */
+  size_t workspace_bytes;
 } FpfTriattnArgs;
 int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err, size_t errlen);
+/* Workspace of fpf_triattn_fwd for this layout (0 for v_layout 0 / 1). */
+size_t fpf_triattn_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t S, int32_t v_layout);
 
 /* ---------------------------------------------------------------------------------------------------------------- triangle attention (block)
  * The fused block: prologue (LN -> q|k|v|g and the pair-bias projection, reading z or z^T by address) -> core -> epilogue

@@ -283,3 +283,78 @@ def test_stages_fp32_exact():
         torch.cuda.synchronize()
         ref = S.tri_attn(z, P, None, ending=ending, dtype=torch.float64)
         assert_f32_close(u.transpose(1, 2) if ending else u, ref, "staged fp32 ending=%s" % ending)
+
+
+# ------------------------------------------------------------------------------------------------ block-layout core fallback
+_VPERM = [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]      # stored position p of a 16-key block holds key _VPERM[p]
+
+
+def _keep_table(mask):
+    """The keep-bit table of the block-layout core (include/fpf_hip.h, FpfTriattnArgs.keep), built on the host from a [B, N, S]
+    0/1 mask: per attention row, word 0 = flags (1 some key kept, 2 every key kept), word 1 + t = bits of keys 64 t .. 64 t + 63;
+    a row with no kept key has every bit set."""
+    B, N, S = mask.shape
+    m = (mask != 0).cpu().numpy().reshape(B, N, S // 64, 64).astype(np.uint64)
+    words = (m << np.arange(64, dtype=np.uint64)).sum(axis=-1, dtype=np.uint64)
+    alive = m.reshape(B, N, S).any(axis=-1)
+    full = m.reshape(B, N, S).all(axis=-1)
+    words[~alive] = np.uint64(0xFFFFFFFFFFFFFFFF)
+    flags = alive.astype(np.uint64) | (full.astype(np.uint64) << np.uint64(1))
+    table = np.concatenate([flags[..., None], words], axis=-1)
+    return torch.from_numpy(table.view(np.int64).copy()).to(DEV)
+
+
+@pytest.mark.parametrize("N", [256, 768])
+@pytest.mark.parametrize("masked", [False, True])
+def test_block_layout_core_fallback_extreme_logits(N, masked):
+    """The block's own core layout (v_layout 2, logits in log2 units) with query tiles whose logits need a reference max other
+    than 0: bias +150 on queries 64..127 (a partial row sum far above 2^64) and -120 on queries 192..255 (every logit of a
+    query's first sub-tile below -32), next to ordinary query tiles.  The fast kernel flags the work items of the extreme
+    tiles and the fallback recomputes them; every sampled row is held to the bf16 bars against a max-subtracted fp32 softmax.
+    N = 256 takes the 4-wave split, N = 768 the 8-wave one; `masked` adds a random keep pattern with dead rows (uniform mean)."""
+    import ctypes
+    from fpf_hip import _lib as L
+    H, D = 4, 32
+    g = torch.Generator().manual_seed(N + masked)
+    q = (torch.randn(1, N, H, N, D, generator=g) / np.sqrt(D)).to(torch.bfloat16).to(DEV)
+    k = torch.randn(1, N, H, N, D, generator=g).to(torch.bfloat16).to(DEV)
+    vt = torch.randn(1, N, H, D, N, generator=g).to(torch.bfloat16).to(DEV)
+    bias = torch.randn(1, H, N, N, generator=g) * 0.5
+    bias[:, :, 64:128, :] += 150.0
+    bias[:, :, 192:256, :] -= 120.0
+    bias = bias.to(DEV)
+    mask = keep = None
+    if masked:
+        mask = (torch.rand(1, N, N, generator=g) > 0.3).float()
+        mask[:, 5:9, :] = 0                                                   # dead rows
+        mask = mask.to(DEV)
+        keep = _keep_table(mask)
+    out = torch.full((1, N, H, N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(max(1, L.lib().fpf_triattn_workspace_bytes(1, N, H, N, 2)), dtype=torch.uint8, device=DEV)
+    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=1, N=N, H=H, S=N, D=D, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vt), v_layout=2,
+                      bias=L.ptr(bias), bias_dtype=L.DT_F32, mask=L.ptr(mask), mask_dtype=L.DT_F32, out=L.ptr(out), scale=1.0,
+                      keep=None if keep is None else ctypes.c_void_p(keep.data_ptr()), workspace=L.ptr(ws), workspace_bytes=ws.numel())
+    a.q_stride[:] = q.stride()
+    a.k_stride[:] = k.stride()
+    a.v_stride[:] = vt.stride()
+    a.out_stride[:] = out.stride()
+    a.bias_stride[:] = bias.stride()
+    if masked:
+        a.mask_stride[:] = mask.stride()
+    print("[fallback] N=%d masked=%s" % (N, masked), flush=True)
+    L.call("fpf_triattn_fwd", a, L.stream_ptr(DEV))
+    torch.cuda.synchronize()
+    rows = sorted(set([0, 1, 2, 5, 6, 7, 8, 9, N // 2, N // 2 + 1, N - 2, N - 1]))
+    idx = torch.tensor([16 * (kk // 16) + _VPERM.index(kk % 16) for kk in range(N)], device=DEV)
+    Vl = vt[0, rows].float()[..., idx].transpose(-1, -2)                   # [rows, H, key, D]
+    s = torch.einsum("ihqd,ihkd->ihqk", q[0, rows].float(), k[0, rows].float()) + bias[0].unsqueeze(0)
+    if masked:
+        km = mask[0, rows] != 0                                              # [rows, key]
+        dead = ~km.any(-1)
+        s = torch.where(km[:, None, None, :] | dead[:, None, None, None], s, torch.full_like(s, -float("inf")))
+        s = torch.where(dead[:, None, None, None], torch.zeros_like(s), s)
+    p = torch.exp2(s - s.amax(-1, keepdim=True))
+    ref = torch.einsum("ihqk,ihkd->ihqd", p / p.sum(-1, keepdim=True), Vl)
+    got = out[0, rows].float()
+    assert torch.isfinite(got).all(), "non-finite output"
+    assert_bf16_close(got, ref, "block-layout core N=%d masked=%s, extreme query tiles" % (N, masked))

@@ -203,9 +203,10 @@ __device__ __forceinline__ void rt_regroup_f32(const f32x16& acc, float (&out)[1
 // One 16-byte global -> LDS transfer per lane (global_load_lds_dwordx4): the wave's 64 chunks land at lds_base + 16 * lane.
 // Issued through inline assembly so that the only waits on it are the explicit s_waitcnt vmcnt of the slab ring (the
 // compiler would otherwise drain every outstanding transfer before each LDS read it cannot prove disjoint).  lds_base is
-// wave-uniform (it goes through M0).
+// wave-uniform (it goes through M0).  On this GPU family an LDS DMA that reads M0 right after a scalar write of M0 needs
+// one wait state (the s_nop): the compiler's hazard pass does not look inside inline assembly.
 __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base) : "memory");
 }
 // The lane index, computed where it is called (volatile: never hoisted, so values derived from it are not kept live
 // across a loop in registers the loop needs)
@@ -217,7 +218,7 @@ __device__ __forceinline__ int opaque_lane() {
 
 // The same transfer from a wave-uniform base plus a 32-bit per-lane byte offset (scalar base: no 64-bit address per lane).
 __device__ __forceinline__ void lds_dma16_s(uint32_t voff, const void* sbase, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "memory");
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);

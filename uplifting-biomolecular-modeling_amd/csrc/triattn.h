@@ -1,0 +1,92 @@
+// Definitions shared by the triangle-attention kernels (triattn.hip: the op core, the fused block's stages; triattn_pipe.hip:
+// the block-layout core and its keep-bit table).
+#pragma once
+#include "rowtile.h"
+
+namespace fpf {
+
+constexpr int TA_D = 32;
+constexpr int TA_R = 3;          // pair rows per workgroup sharing the bias tile (3: the register budget of 2 waves / SIMD)
+constexpr int TA_KT = 64;        // keys per staged tile (two MFMA sub-tiles of 32)
+constexpr int TA_KLD = 40;       // LDS pitch (bf16) of a K row: 80 B, conflict-free 16-byte reads
+constexpr int TA_VLD = 68;       // LDS pitch (bf16) of a V^T row: 136 B, conflict-free 8-byte reads
+constexpr int TA_MAXW = 128;     // block-layout core: keep-bit words per row held in LDS (S <= 8192)
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float TA_HEADROOM = 8.0f;   // log2 units the running max may lag the true one before O and l are rescaled
+static_assert(TA_R <= 4, "one wave computes the keep bits of one staged row");
+
+struct CoreParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t qs[5], ks[5], vs[5];   // v_t = 0: vs = [b, n, h, key, d] strides; v_t = 1: [b, n, h, d, key] (V stored transposed)
+  int v_t;
+  const void* bias;
+  int bias_bf16;
+  int bias_vec;                  // fp32 bias whose rows start 16-byte aligned: float4 loads
+  int64_t bs[4];
+  const void* mask;
+  int mask_f32;
+  int64_t ms[3];
+  uint16_t* out;
+  int64_t os[5];
+  int64_t B, N, H, S;
+  float scale;
+  const uint64_t* keep;          // block-layout core: keep table [B, N, keep_words(S)] of the mask, or NULL (every key kept)
+  uint32_t* redo;                // block-layout core: one flag per (work item, wave), written by the fast kernel
+};
+
+__device__ __forceinline__ bool mask_keep(const CoreParams& p, int64_t b, int64_t i, int64_t key) {
+  if (!p.mask) return true;
+  const int64_t o = b * p.ms[0] + i * p.ms[1] + key * p.ms[2];
+  return p.mask_f32 ? (static_cast<const float*>(p.mask)[o] != 0.0f) : (static_cast<const uint8_t*>(p.mask)[o] != 0);
+}
+
+__device__ __forceinline__ float bias_at(const CoreParams& p, int64_t off) {
+  return p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[off]) : static_cast<const float*>(p.bias)[off];
+}
+
+constexpr int TA_NB = 3;                                 // K / V^T tile buffers of the block-layout core
+constexpr int TA_DMA_WAVES = 8;                          // waves (32 queries each) per workgroup of the block-layout core:
+                                                         // 8 share each K / V^T tile among 256 queries (4 move K, 4 V^T)
+constexpr float TD_PS_MAX = 18446744073709551616.0f;     // 2^64: a sub-tile's partial row sum at or above it needs a reference
+constexpr float TD_PS_MIN = 2.3283064365386963e-10f;     // 2^-32: so does a query's first sub-tile with a kept key summing below it
+
+// 16 bytes at sbase + voff + IMM (scalar base, 32-bit per-lane byte offset) into registers, not waited for here
+template <int IMM>
+__device__ __forceinline__ f32x4 gload4_async(uint32_t voff, const void* sbase) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(v) : "v"(voff), "s"(sbase), "n"(IMM));
+  return v;
+}
+// The same load into registers that hold a live value until now ("+v": the previous value is an input), so the compiler
+// keeps that value in place up to the load instead of reusing its registers -- e.g. as the accumulator of an MFMA that reads
+// it last
+template <int IMM>
+__device__ __forceinline__ void gload4_into(f32x4& v, uint32_t voff, const void* sbase) {
+  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "+v"(v) : "v"(voff), "s"(sbase), "n"(IMM));
+}
+// waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
+// through the statement so nothing reads them earlier
+template <int N>
+__device__ __forceinline__ void vm_wait4(f32x4& a, f32x4& b, f32x4& c, f32x4& d) {
+  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// The block-layout core (v_layout 2) and its keep table (triattn_pipe.hip).  Keep table of a call: for each (b, attention row
+// i) keep_words(S) = S / 64 + 1 words: word 0 = row flags (TK_ALIVE: some key kept, TK_FULL: every key kept), word 1 + T = the
+// keep bits of keys 64 T .. 64 T + 63 (bit k = key 64 T + k); a row with no kept key has every bit set (it attends uniformly
+// to all keys).
+constexpr uint64_t TK_ALIVE = 1, TK_FULL = 2;
+__host__ __device__ inline int64_t keep_words(int64_t S) { return S / 64 + 1; }
+// Redo flags of a call (one 32-bit word per work item and wave; the 4-wave split has the most): B H ceil(N / TA_R) ceil(S / 128) 4.
+inline int64_t redo_words(int64_t B, int64_t N, int64_t H, int64_t S) { return B * H * cdiv(N, TA_R) * cdiv(S, 128) * 4; }
+int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, uint64_t* keep, hipStream_t st,
+                      char* err, size_t errlen);
+int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen);
+
+}  // namespace fpf

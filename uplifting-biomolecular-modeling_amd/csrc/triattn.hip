@@ -12,48 +12,10 @@
 // fp32 core (exact tier): one thread per query, LDS-staged K / V tiles, fp32 online softmax with expf.
 #include <algorithm>
 
-#include "rowtile.h"
+#include "triattn.h"
 
 namespace fpf {
 
-constexpr int TA_D = 32;
-constexpr int TA_R = 3;          // pair rows per workgroup sharing the bias tile (3: the register budget of 2 waves / SIMD)
-constexpr int TA_KT = 64;        // keys per staged tile (two MFMA sub-tiles of 32)
-constexpr int TA_KLD = 40;       // LDS pitch (bf16) of a K row: 80 B, conflict-free 16-byte reads
-constexpr int TA_VLD = 68;       // LDS pitch (bf16) of a V^T row: 136 B, conflict-free 8-byte reads
-constexpr int TA_MAXW = 128;     // block-layout core: keep-bit words per row held in LDS (S <= 8192)
-constexpr float LOG2E = 1.4426950408889634f;
-constexpr float TA_HEADROOM = 8.0f;   // log2 units the running max may lag the true one before O and l are rescaled
-static_assert(TA_R <= 4, "one wave computes the keep bits of one staged row");
-
-struct CoreParams {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  int64_t qs[5], ks[5], vs[5];   // v_t = 0: vs = [b, n, h, key, d] strides; v_t = 1: [b, n, h, d, key] (V stored transposed)
-  int v_t;
-  const void* bias;
-  int bias_bf16;
-  int bias_vec;                  // fp32 bias whose rows start 16-byte aligned: float4 loads
-  int64_t bs[4];
-  const void* mask;
-  int mask_f32;
-  int64_t ms[3];
-  uint16_t* out;
-  int64_t os[5];
-  int64_t B, N, H, S;
-  float scale;
-};
-
-__device__ __forceinline__ bool mask_keep(const CoreParams& p, int64_t b, int64_t i, int64_t key) {
-  if (!p.mask) return true;
-  const int64_t o = b * p.ms[0] + i * p.ms[1] + key * p.ms[2];
-  return p.mask_f32 ? (static_cast<const float*>(p.mask)[o] != 0.0f) : (static_cast<const uint8_t*>(p.mask)[o] != 0);
-}
-
-__device__ __forceinline__ float bias_at(const CoreParams& p, int64_t off) {
-  return p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[off]) : static_cast<const float*>(p.bias)[off];
-}
 
 // S^T tile of one pair row: keys of sub-tile `sub` (A = K rows from LDS) x this wave's 32 queries (B = Q^T), accumulated onto
 // the bias tile.
@@ -307,352 +269,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
   }
-  if (!qlive) return;
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    const int64_t i = i0 + r;
-    if (i >= p.N) continue;
-    const float lt = half_sum(lrow[r]);
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int d0 = 8 * qd + 4 * g;
-      *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------------------- bf16 core, block layout
-// The fused block's core: the work split of triattn_core_bf16 (a workgroup = TA_R pair rows x 128 queries of one (b, h); a
-// wave = 32 queries, lane n = query, lane group g = key half) on the operands the block's prologue lays out: q pre-multiplied
-// by scale * log2(e) and the fp32 bias by log2(e), so the S^T accumulator is already in log2 units; V^T with the keys of each
-// 16-key block stored {0-3, 8-11 | 4-7, 12-15}; S a multiple of 64.
-//   * Software pipeline over (sub-tile, row) steps.  A step turns the row's S^T tile into P (exp2, bf16, row sums), issues
-//     the row's P.V MFMAs and then the row's S^T MFMAs of the NEXT sub-tile, so the matrix core works through those while
-//     the wave computes the other rows' exponentials.  (A wave issues in order: with the S^T MFMAs of all rows issued
-//     together, its MFMA and VALU phases would alternate and only the second wave of the SIMD could fill the gaps.)
-//   * p = exp2(acc) with no per-element shift.  A row's reference max stays 0 while its logits stay inside +-TD_BAND (checked
-//     on the row's first live sub-tile) and each sub-tile's partial row sum stays below 2^64; otherwise the row moves its
-//     reference and from then on subtracts it.  Every value is relative to the reference, so its choice costs no precision.
-//   * K and V^T tiles (64 keys) go global -> LDS by DMA (global_load_lds_dwordx4) into a ring of TA_NB buffers, in
-//     XOR-swizzled 16-byte chunks so the MFMA fragment reads are conflict-free 16-byte reads (K: chunk c of key k at
-//     c ^ ((k >> 2) & 3); V^T: chunk c of row d at c ^ ((d >> 1) & 7)); the permuted key order makes a lane's V^T fragment
-//     one 16-byte chunk.  Three buffers let the barrier that publishes tile T + 1 come before the last reads of tile T.
-//   * the bias sub-tiles and the DMA are issued from inline assembly, every one unconditionally, and waited for with exact
-//     counts (the memory counter retires in order), so no wait covers a load that is not needed yet;
-//   * the keep bits of all keys of the TA_R rows are built once (LDS table), so the key loop reads no mask.
-constexpr int TA_NB = 3;                                 // K / V^T tile buffers of the block-layout core
-constexpr int TA_DMA_WAVES = 8;                          // waves (32 queries each) per workgroup of the block-layout core:
-                                                         // 8 share each K / V^T tile among 256 queries (4 move K, 4 V^T)
-constexpr float TD_PS_MAX = 18446744073709551616.0f;     // 2^64: a sub-tile's partial row sum at or above it moves the reference
-constexpr float TD_BAND = 32.0f;                         // first live sub-tile: a max outside +-TD_BAND (log2 units) sets it
-constexpr float TD_MOVE = 48.0f;                         // later sub-tiles: a max more than TD_MOVE above it moves it
-
-// 16 bytes at sbase + voff + IMM (scalar base, 32-bit per-lane byte offset) into registers, not waited for here
-template <int IMM>
-__device__ __forceinline__ f32x4 gload4_async(uint32_t voff, const void* sbase) {
-  f32x4 v;
-  asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(v) : "v"(voff), "s"(sbase), "n"(IMM));
-  return v;
-}
-// waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
-// through the statement so nothing reads them earlier
-template <int N>
-__device__ __forceinline__ void vm_wait4(f32x4& a, f32x4& b, f32x4& c, f32x4& d) {
-  asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "n"(N));
-}
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-template <int NW>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_dma(const CoreParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][TA_R][TA_KT * TA_D];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[TA_NB][TA_R][TA_D * TA_KT];
-  __shared__ uint64_t sKeepAll[TA_R][TA_MAXW];
-  __shared__ int sAlive[TA_R];
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  // the host checks that the grid fits 31 bits: the workgroup decode is 32-bit
-  const uint32_t nq = (uint32_t)cdiv(p.S, 32 * NW), nr = (uint32_t)cdiv(p.N, TA_R), H = (uint32_t)p.H;
-  const uint32_t total = (uint32_t)p.B * H * nr * nq;
-  const uint32_t per = (total + 7) / 8;
-  const uint32_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
-  if (w >= total) return;
-  const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
-  const int64_t b = bh / H, h = bh % H;
-  const int64_t i0 = (int64_t)rg * TA_R;
-  const int64_t q = (int64_t)qt * (32 * NW) + wave * 32 + n;
-  const bool qlive = q < p.S;
-
-  bf16x8 qf[TA_R][2];
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    const int64_t i = i0 + r;
-    const bool ok = i < p.N && qlive;
-    const uint16_t* qp = p.q + b * p.qs[0] + (ok ? i : 0) * p.qs[1] + h * p.qs[2] + (ok ? q : 0) * p.qs[3] + 8 * g;
-    qf[r][0] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0, 0, 0, 0});
-    qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
-  }
-
-
-  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
-  // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves); rows past N read row i0 (never stored).  Row bases are
-  // scalar, the in-tile byte offsets per lane are fixed.
-  const int wc = wave & 3;
-  const uint16_t* kb[TA_R];
-  const uint16_t* vb[TA_R];
-  uint32_t koff, voff;
-  {
-    const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
-    const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
-    koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
-    voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
-#pragma unroll
-    for (int r = 0; r < TA_R; ++r) {
-      const int64_t ii = i0 + r < p.N ? i0 + r : i0;
-      kb[r] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
-      vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
-    }
-  }
-  // LDS byte addresses of this wave's chunk block in buffer 0, row 0 (buffer / row steps are constants)
-  const uint32_t kl0 = lds_addr(&sK[0][0][512 * wc]), vl0 = lds_addr(&sV[0][0][512 * wc]);
-  constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
-  const bool v_mover = NW > 4 && wave >= 4;
-  auto dma_tile = [&](int64_t k0, int buf) {
-#pragma unroll
-    for (int r = 0; r < TA_R; ++r) {
-      if (NW == 4 || !v_mover) lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
-      if (NW == 4 || v_mover) lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
-    }
-  };
-  // The wait counts (vm_wait4<DMA_OPS + 4>, vm_wait4<4>) assume exactly DMA_OPS operations per dma_tile and 4 per
-  // bias_issue, every one issued unconditionally and in the order of the loop below: a wait that counted fewer operations
-  // than were issued after the load it guards would let that load land in registers already reused.
-  constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * TA_R;
-
-  const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
-  const uint32_t boff = (uint32_t)(((qlive ? q : 0) * p.bs[2] + 4 * g) * 4);
-  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
-  auto bias_issue = [&](int64_t kb, f32x4 (&dst)[4]) {
-    const float* sb = brow + kb;
-    dst[0] = gload4_async<0>(boff, sb);
-    dst[1] = gload4_async<32>(boff, sb);
-    dst[2] = gload4_async<64>(boff, sb);
-    dst[3] = gload4_async<96>(boff, sb);
-  };
-
-  f32x16 o[TA_R], s[TA_R];
-  float lrow[TA_R], mb[TA_R];
-  uint64_t unseen[TA_R];           // lanes whose `seen` is still false (a wave-uniform mask: the fast path tests it in scalar code)
-  bool seen[TA_R], sh[TA_R];       // seen: the row's first live sub-tile has set its reference (per lane, equal in l and
-                                   // l ^ 32; rows past N count as seen); sh: some lane of the row has a nonzero reference
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    o[r] = f32x16{};
-    lrow[r] = 0.f;
-    mb[r] = 0.f;
-    seen[r] = i0 + r >= p.N;
-    unseen[r] = seen[r] ? 0ull : ~0ull;
-    sh[r] = false;
-  }
-  // fragment offsets (bf16 elements) inside a row's K / V^T tile
-  const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile adds 32 keys
-  const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
-  const int vsw = (n >> 1) & 7;
-  auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
-    f32x16 bc;
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
-    return mfma32(as_bf8(k1f), qf[r][1], mfma32(as_bf8(k0f), qf[r][0], bc));
-  };
-  // P of one row step: bf16 pairs of exp2(s) and the sum of the bf16 values the P.V MFMA consumes
-  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8]) {
-    float ps0 = 0.f, ps1 = 0.f;
-#pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
-      if (v & 2) ps1 = dot2_bf16(pk[v >> 1], ps1);
-      else ps0 = dot2_bf16(pk[v >> 1], ps0);
-    }
-    return ps0 + ps1;
-  };
-
-  const int64_t nT = p.S / TA_KT;
-  f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
-  // issue order DMA(0), bias(0), bias(1), DMA(1): the loop's wait counts continue from it
-  dma_tile(0, 0);
-  bias_issue(0, bq[0]);
-  bias_issue(32, bq[1]);
-  dma_tile(nT > 1 ? TA_KT : 0, 1);
-  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys, all of the row's mask loads in flight together
-  // (overlapping the Q loads and the first tiles' transfers, issued above); a row with no kept key attends uniformly to
-  // every key (its words become all ones)
-  const int nw = (int)(p.S >> 6);
-  if (wave < TA_R) {
-    const int64_t i = i0 + wave;
-    const bool rowok = i < p.N;
-    auto build = [&](auto elt) {
-      using T = decltype(elt);
-      const T* mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + (rowok ? i : 0) * p.ms[1];
-      uint64_t any = 0;
-      if (sizeof(T) == 1 && p.mask && p.ms[2] == 1 && (reinterpret_cast<uintptr_t>(mrow) & 15) == 0) {
-        // contiguous u8 keys: lane l reads keys 16 l .. 16 l + 15 of each 1024-key block with one 16-byte load and writes
-        // their keep bits as the 16-bit piece l of the block's words (bit k of piece j = key 16 j + k, the ballot layout)
-        uint16_t* kw16 = reinterpret_cast<uint16_t*>(&sKeepAll[wave][0]);
-        uint32_t anyl = 0;
-        for (int c0 = 0; c0 < (int)p.S; c0 += 1024) {
-          const int key = c0 + 16 * l;
-          uint32_t bits = 0;
-          if (rowok && key < (int)p.S) {
-            const u32x4 m = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(mrow) + key);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              uint32_t t = m[e] | (m[e] >> 1);           // the low bit of each byte: byte != 0
-              t |= t >> 2;
-              t |= t >> 4;
-              t &= 0x01010101u;
-              bits |= ((t * 0x01020408u) >> 24 & 0xfu) << (4 * e);   // gathers the 4 byte flags, key order
-            }
-          }
-          if (key < (int)p.S) kw16[key >> 4] = (uint16_t)bits;
-          anyl |= bits;
-        }
-        any = __ballot(anyl != 0);
-      } else
-      for (int c0 = 0; c0 < nw; c0 += 16) {
-        T raw[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) raw[u] = (p.mask && c0 + u < nw) ? mrow[(int64_t)(64 * (c0 + u) + l) * p.ms[2]] : (T)1;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          if (c0 + u >= nw) break;
-          const uint64_t bal = __ballot(rowok && raw[u] != (T)0);
-          any |= bal;
-          if (l == 0) sKeepAll[wave][c0 + u] = bal;
-        }
-      }
-      if (rowok && any == 0)
-        for (int c = l; c < nw; c += 64) sKeepAll[wave][c] = ~0ull;
-      if (l == 0) sAlive[wave] = any != 0;
-    };
-    if (p.mask_f32) build(0.0f);
-    else build((uint8_t)0);
-  }
-  // the Q and mask loads complete here (and the older transfers with them: the counter retires in order); inside the key
-  // loop the only vector-memory operations are the counted ones
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
-  __syncthreads();
-  bool dead[TA_R];
-  bool dead_any = false;
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    dead[r] = (i0 + r < p.N) && !sAlive[r];
-    dead_any |= dead[r];
-  }
-  vm_wait4<4 + DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);    // tile 0 and bias 0 are in (bias 1, tile 1 may be pending)
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    const uint16_t* kt = &sK[0][r][0];
-    s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
-  }
-
-  int bt = 0;                      // buffer of tile T
-  for (int64_t T = 0; T < nT; ++T) {
-    const bool moreT = T + 1 < nT;
-    const int bn = bt == TA_NB - 1 ? 0 : bt + 1;      // buffer of tile T + 1
-    const int bf = bn == TA_NB - 1 ? 0 : bn + 1;      // buffer of tile T + 2: tile T - 1's, free once every wave is past it
-    const int64_t k0 = T * TA_KT;
-    bias_issue(moreT ? k0 + TA_KT : 0, bq[0]);         // sub-tile 2T + 2 (past the end: a valid re-read, the counts stay exact)
-    uint64_t kw[TA_R], kall = ~0ull, kany = 0;
-#pragma unroll
-    for (int r = 0; r < TA_R; ++r) {
-      const uint64_t wv = sKeepAll[r][T];                               // uniform: keep it in scalar registers
-      const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
-      const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);   // unsigned: no sign extension
-      kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
-      kall &= kw[r];
-      kany |= kw[r];
-    }
-    const bool full = (kall == ~0ull) && !dead_any;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      if (sub == 0) {
-        vm_wait4<DMA_OPS + 4>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);   // bias 2T + 1 (tile T + 1, bias 2T + 2 may be pending)
-      } else {
-        bias_issue(moreT ? k0 + TA_KT + 32 : 32, bq[1]);                 // sub-tile 2T + 3
-        vm_wait4<4>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);             // bias 2T + 2 and tile T + 1 are in
-        __builtin_amdgcn_s_barrier();                                     // every wave's part of tile T + 1 is in, and every
-        asm volatile("" ::: "memory");                                    // wave is done with tile T - 1
-        dma_tile((T + 2 < nT ? T + 2 : nT - 1) * TA_KT, bf);
-      }
-      const bool live_sub = (uint32_t)(kany >> (32 * sub)) != 0;
-      const bool next = sub == 0 || moreT;                                // the next sub-tile exists
-      const uint16_t* knext = sub == 0 ? &sK[bt][0][32 * TA_D] : &sK[bn][0][0];
-#pragma unroll
-      for (int r = 0; r < TA_R; ++r) {
-        // fragment reads first: V^T of this step, K of the row's next S^T
-        const uint16_t* vt = &sV[bt][r][n * TA_KT];
-        const u32x4 vf0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + g) ^ vsw));
-        const u32x4 vf1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + 2 + g) ^ vsw));
-        const uint16_t* kt = knext + r * (TA_KT * TA_D);
-        u32x4 kf0 = u32x4{0, 0, 0, 0}, kf1 = u32x4{0, 0, 0, 0};
-        if (next) {
-          kf0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
-          kf1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
-        }
-        if (live_sub) {
-          if (!full) {
-            const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const float sv = dead[r] ? 0.f : s[r][v];
-              s[r][v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? sv : -INFINITY;
-            }
-          }
-          if (sh[r]) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s[r][v] -= mb[r];
-          }
-          uint32_t pk[8];
-          float ps = expsum(s[r], pk);
-          if ((__builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX)) | unseen[r]) != 0) {
-            // set or move the reference of the queries that need it; the decision depends only on the sub-tile max over
-            // both key halves, so lanes l and l ^ 32 (one query) always agree
-            float m0 = s[r][0];
-#pragma unroll
-            for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, s[r][v]);
-            const float mt = half_max(m0);
-            const bool fin = mt > -INFINITY;
-            const float shift = !seen[r] ? ((fin && (mt > TD_BAND || mt < -TD_BAND)) ? mt : 0.f) : (mt > TD_MOVE ? mt : 0.f);
-            const float alpha = seen[r] && shift != 0.f ? fast_exp2(-shift) : 1.0f;   // before the first live sub-tile o, l are 0
-            lrow[r] *= alpha;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s[r][v] -= shift;
-            mb[r] += shift;
-            seen[r] = seen[r] || fin;
-            unseen[r] = __builtin_amdgcn_ballot_w64(!seen[r]);
-            sh[r] = __ballot(mb[r] != 0.f) != 0;
-            ps = expsum(s[r], pk);
-          }
-          lrow[r] += ps;
-          o[r] = mfma32(as_bf8(vf0), as_bf8(u32x4{pk[0], pk[1], pk[2], pk[3]}), o[r]);
-          o[r] = mfma32(as_bf8(vf1), as_bf8(u32x4{pk[4], pk[5], pk[6], pk[7]}), o[r]);
-        }
-        if (next) s[r] = qk(kf0, kf1, r, sub == 0 ? bq[1] : bq[0]);
-      }
-    }
-    bt = bn;
-  }
-  vm_wait<0>();                                         // no DMA may land after the wave ends
   if (!qlive) return;
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) {
@@ -1240,17 +856,14 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
       if (!p.bias_vec || p.S % TA_KT != 0 || p.S > 64 * TA_MAXW || p.vs[3] % 8 != 0)
         return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
       if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
-      // 8 waves share each K / V^T tile among 256 queries; they pay where S fills whole 256-query tiles and the grid still
-      // has at least 8 workgroups per CU (N = 768: 3072; N = 512: 1368, where 4 waves and twice the workgroups are faster)
-      const int64_t rows_heads = a->B * a->H * cdiv(a->N, TA_R);
-      if (p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * (int64_t)num_cus()) {
-        const int64_t total_w = rows_heads * (p.S / (32 * TA_DMA_WAVES));
-        hipLaunchKernelGGL(triattn_core_bf16_dma<TA_DMA_WAVES>, dim3((unsigned)(cdiv(total_w, 8) * 8)), dim3(64 * TA_DMA_WAVES), 0, st, p);
-      } else {
-        const int64_t total_w = rows_heads * cdiv(p.S, 128);
-        hipLaunchKernelGGL(triattn_core_bf16_dma<4>, dim3((unsigned)(cdiv(total_w, 8) * 8)), dim3(256), 0, st, p);
-      }
-      return launched(err, errlen, "triattn_core_bf16_dma");
+      if (p.mask && !a->keep)
+        return fail(err, errlen, FPF_E_ARGS, "v_layout 2 reads the mask as a keep-bit table (keep); the fused block builds it");
+      const size_t need = (size_t)redo_words(a->B, a->N, a->H, a->S) * 4;
+      if (!a->workspace || a->workspace_bytes < need)
+        return fail(err, errlen, FPF_E_WORKSPACE, "v_layout 2: workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
+      p.keep = a->keep;
+      p.redo = static_cast<uint32_t*>(a->workspace);
+      return pipe_core_launch(p, st, err, errlen);
     }
     if (p.v_t && p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<true, true>), grid, block, 0, st, p);
     else if (p.v_t) hipLaunchKernelGGL((triattn_core_bf16<true, false>), grid, block, 0, st, p);
@@ -1310,6 +923,11 @@ extern "C" int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err,
   if (a->mask && !(a->mask_dtype == FPF_DT_U8 || a->mask_dtype == FPF_DT_F32)) return fail(err, errlen, FPF_E_DTYPE, "mask_dtype %d", a->mask_dtype);
   if (!(a->scale > 0.f)) return fail(err, errlen, FPF_E_ARGS, "scale must be > 0");
   return core_launch(a, static_cast<hipStream_t>(stream), err, errlen);
+}
+
+extern "C" size_t fpf_triattn_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t S, int32_t v_layout) {
+  if (v_layout != 2 || B <= 0 || N <= 0 || H <= 0 || S <= 0) return 0;
+  return (size_t)fpf::redo_words(B, N, H, S) * 4;
 }
 
 namespace fpf {
@@ -1438,7 +1056,10 @@ extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_
   // padded to N rounded up to 32) + the full bias (H fp32 per pixel), 256-byte aligned regions
   const size_t r1 = ((size_t)B * rows * fpf::cdiv(N, 32) * 32 * HD * elt + 255) & ~(size_t)255;
   const size_t r2 = (pix * (size_t)H * 4 + 255) & ~(size_t)255;
-  return (dtype == FPF_DT_F32 ? 5 : 4) * r1 + r2;
+  // + the keep-bit table of the block-layout core's mask (B x rows attention rows, N / 64 + 1 words each) and its redo flags
+  const size_t r3 = ((size_t)B * rows * (size_t)fpf::keep_words(N) * 8 + 255) & ~(size_t)255;
+  const size_t r4 = ((size_t)fpf::redo_words(B, rows, H, N) * 4 + 255) & ~(size_t)255;
+  return (dtype == FPF_DT_F32 ? 5 : 4) * r1 + r2 + r3 + r4;
 }
 
 extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen) {
@@ -1501,6 +1122,8 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   const int regions = a->dtype == FPF_DT_F32 ? 5 : 4;  // q, k, v, o (+ g on the fp32 path)
   void *q = w, *k = w + r1, *v = w + 2 * r1, *o = w + 3 * r1, *g = regions == 5 ? w + 4 * r1 : nullptr;
   float* bias = a->bias_in ? const_cast<float*>(a->bias_in) : reinterpret_cast<float*>(w + regions * r1);
+  uint64_t* keep = reinterpret_cast<uint64_t*>(w + regions * r1 + (((size_t)B * N * N * H * 4 + 255) & ~(size_t)255));
+  void* redo = reinterpret_cast<char*>(keep) + (((size_t)B * R * (size_t)keep_words(N) * 8 + 255) & ~(size_t)255);
   const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)D);
   FpfTriattnArgs c{};
   c.abi_version = FPF_ABI_VERSION;
@@ -1541,6 +1164,13 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.mask = a->mask ? static_cast<const char*>(a->mask) + row0 * c.mask_stride[1] * (a->mask_dtype == FPF_DT_F32 ? 4 : 1) : nullptr;
   c.out = o;
   c.scale = dma_core ? 1.0f : scale;
+  c.workspace = redo;
+  c.workspace_bytes = (size_t)redo_words(B, R, H, N) * 4;
+  if (dma_core && c.mask) {                             // the block-layout core reads the mask as keep bits
+    const int rc = keep_table_launch(c.mask, c.mask_dtype == FPF_DT_F32, c.mask_stride, B, R, N, keep, st, err, errlen);
+    if (rc) return rc;
+    c.keep = keep;
+  }
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
   const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM : 0);
   int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,

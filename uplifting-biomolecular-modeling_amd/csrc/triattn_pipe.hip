@@ -1,0 +1,729 @@
+// Triangle attention: the fused block's core on the block's own operand layout (v_layout 2), and the keep-bit table it reads.
+// Replaces the core stage of common/opt_core/opt_core/attn/pair_fused.py:1391 (core_attention) inside tri_attn_block (:1500):
+// o = softmax_j(q.k + bias, -inf at masked keys) v per (b, attention row i, head h), kernels/triattn/__init__.py:3-8; a row with
+// no kept key is the uniform mean of v.
+//
+// Operands (written by the block's prologue): q [B, N, H, S, 32] already times scale * log2(e), k [B, N, H, S, 32], V^T
+// [B, N, H, 32, S] with the keys of every 16-key block stored 0-3, 8-11, 4-7, 12-15 (the order in which the S^T MFMA's output
+// registers hold P), fp32 bias [B, H, S, S] times log2(e): logits are in log2 units throughout.
+//
+// Work split: a workgroup = TA_R pair rows x 32 NW queries x one (b, h); a wave = 32 queries of the TA_R rows (lane n = query,
+// lane group g = key half).  The TA_R rows share the bias tile (it does not depend on i): each wave loads its 32 x 32 fp32
+// bias sub-tile once into registers and starts all TA_R rows' S^T = K Q^T accumulators (v_mfma_f32_32x32x16_bf16) from it.
+// K and V^T tiles of 64 keys go global -> LDS by DMA (global_load_lds_dwordx4) through a ring of TA_NB buffers, in
+// XOR-swizzled 16-byte chunks (K: chunk c of key k at c ^ ((k >> 2) & 3); V^T: chunk c of row d at c ^ ((d >> 1) & 7)), so
+// every fragment read is a conflict-free 16-byte read; all TA_R rows' tiles are shared by the NW waves.
+//
+// The step pipeline.  The key loop is a sequence of steps (t, r) over 32-key sub-tiles t and rows r.  Step (t, r) turns
+// the row's S^T sub-tile (already in registers) into P: p = exp2(s - m) rounded to bf16, and the partial row sum of those
+// bf16 values (v_dot2_f32_bf16).  In the same basic block it issues the MFMAs of the PREVIOUS step -- that row's O^T += V^T
+// P^T with the P computed one step earlier, and the same row's S^T of the next sub-tile -- so the matrix core works while the
+// wave computes exponentials (a wave issues in order: an MFMA right behind the exponentials it consumes would stall it).
+// The MFMAs and the softmax arithmetic are interleaved by sched_group_barrier.
+//
+// The reference max m of each query stays 0 while the logits are tame, so the common step has no max reduction and no
+// subtraction.  After each step one ballot checks the partial sum: at or above 2^64 (or not finite) the row's reference
+// moves up by the sub-tile's max, and a query without a reference (before its first live sub-tile) whose partial sum is
+// below 2^-32 (every logit below -32) takes that sub-tile's max; the check runs before the step's P.V is issued (one step
+// later), so the fix-up rescales O and l and recomputes P with nothing to undo.  Every value is relative to m, so its
+// choice costs no precision.  Tiles where every key of the TA_R rows is kept and no row is dead run a variant with no mask
+// code at all; the keep bits come from a table built once per call (triattn_keep_bits), so the key loop never reads the
+// mask.
+#include <algorithm>
+
+#include "triattn.h"
+
+namespace fpf {
+
+// ---------------------------------------------------------------------------------------------------------------- keep table
+// One wave per (b, attention row i): 64 keys per ballot, 16 mask loads in flight.  The table layout is in triattn.h.
+__global__ void __launch_bounds__(256) triattn_keep_bits(const void* __restrict__ mask, int mask_f32, int64_t ms0, int64_t ms1, int64_t ms2,
+                                                           int64_t B, int64_t N, int64_t S, uint64_t* __restrict__ keep) {
+  const int l = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= B * N) return;
+  const int64_t b = row / N, i = row - b * N;
+  const int nw = (int)(S >> 6);
+  uint64_t* out = keep + row * keep_words(S);
+  const int64_t base = b * ms0 + i * ms1;
+  uint64_t any = 0, all = ~0ull, mine0 = 0, mine1 = 0;   // words l and 64 + l of the row
+  for (int c0 = 0; c0 < nw; c0 += 16) {
+    bool k[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int64_t off = base + ((int64_t)64 * (c0 + u) + l) * ms2;
+      k[u] = c0 + u >= nw || (mask_f32 ? static_cast<const float*>(mask)[off] != 0.f : static_cast<const uint8_t*>(mask)[off] != 0);
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int c = c0 + u;
+      if (c >= nw) break;
+      const uint64_t bal = __ballot(k[u]);
+      any |= bal;
+      all &= bal;
+      if ((c & 63) == l) {
+        if (c < 64) mine0 = bal;
+        else mine1 = bal;
+      }
+    }
+  }
+  if (l < nw) out[1 + l] = any ? mine0 : ~0ull;
+  if (64 + l < nw) out[65 + l] = any ? mine1 : ~0ull;
+  if (l == 0) out[0] = (any ? TK_ALIVE : 0) | (all == ~0ull ? TK_FULL : 0);
+}
+
+// ---------------------------------------------------------------------------------------------------------------- core
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_pipe(const CoreParams p) {
+  constexpr int R = TA_R;
+  __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][R][TA_KT * TA_D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[TA_NB][R][TA_D * TA_KT];
+  __shared__ uint64_t sKeep[R][TA_MAXW + 1];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  // the host checks that the grid fits 31 bits: the workgroup decode is 32-bit.  Workgroup order is XCD-aware: consecutive
+  // work items (the query tiles of one row group, then the row groups of one head) run on one XCD, so a head's bias and a
+  // row group's K / V^T tiles stay in that XCD's L2.
+  const uint32_t nq = (uint32_t)cdiv(p.S, 32 * NW), nr = (uint32_t)cdiv(p.N, R), H = (uint32_t)p.H;
+  const uint32_t total = (uint32_t)p.B * H * nr * nq;
+  const uint32_t per = (total + 7) / 8;
+  const uint32_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (w >= total) return;
+  const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
+  const int64_t b = bh / H, h = bh % H;
+  const int64_t i0 = (int64_t)rg * R;
+  const int64_t q = (int64_t)qt * (32 * NW) + wave * 32 + n;
+  const bool qlive = q < p.S;
+
+  bf16x8 qf[R][2];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t i = i0 + r;
+    const bool ok = i < p.N && qlive;
+    const uint16_t* qp = p.q + b * p.qs[0] + (ok ? i : 0) * p.qs[1] + h * p.qs[2] + (ok ? q : 0) * p.qs[3] + 8 * g;
+    qf[r][0] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0, 0, 0, 0});
+    qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
+  }
+
+  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
+  // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves); rows past N read row i0 (never stored).
+  const int wc = wave & 3;
+  const uint16_t* kb[R];
+  const uint16_t* vb[R];
+  uint32_t koff, voff;
+  {
+    const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
+    const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+    koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
+    voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t ii = i0 + r < p.N ? i0 + r : i0;
+      kb[r] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
+      vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
+    }
+  }
+  const uint32_t kl0 = lds_addr(&sK[0][0][512 * wc]), vl0 = lds_addr(&sV[0][0][512 * wc]);
+  constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
+  const bool v_mover = NW > 4 && wave >= 4;
+  auto dma_tile = [&](int64_t k0, int buf) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (NW == 4 || !v_mover) lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * R + r) * TILE_B);
+      if (NW == 4 || v_mover) lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * R + r) * TILE_B);
+    }
+  };
+  // The wait counts below (vm_wait4<0>, vm_wait4<DMA_OPS>) assume exactly DMA_OPS operations per dma_tile and 4 per
+  // bias_issue, every one issued unconditionally and in the order of the loop: a wait counting fewer operations than were
+  // issued after the load it guards would let that load land in registers already in use.
+  constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * R;
+
+  const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
+  const uint32_t boff = (uint32_t)(((qlive ? q : 0) * p.bs[2] + 4 * g) * 4);
+  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
+  auto bias_issue = [&](int64_t k, f32x4 (&dst)[4]) {
+    const float* sb = brow + k;
+    gload4_into<0>(dst[0], boff, sb);
+    gload4_into<32>(dst[1], boff, sb);
+    gload4_into<64>(dst[2], boff, sb);
+    gload4_into<96>(dst[3], boff, sb);
+  };
+
+  const int nT = (int)(p.S / TA_KT);
+  f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) bq[x][qd] = f32x4{};
+  dma_tile(0, 0);
+  bias_issue(0, bq[0]);
+  bias_issue(32, bq[1]);
+  dma_tile(nT > 1 ? TA_KT : 0, 1);
+  // the TA_R rows' keep words (rows past N, or no mask: every key kept)
+  if (wave < R) {
+    const int64_t i = i0 + wave;
+    if (p.keep && i < p.N) {
+      const uint64_t* src = p.keep + (b * p.N + i) * keep_words(p.S);
+      for (int c = l; c <= nT; c += 64) sKeep[wave][c] = src[c];
+    } else {
+      for (int c = l; c <= nT; c += 64) sKeep[wave][c] = c == 0 ? (TK_ALIVE | TK_FULL) : ~0ull;
+    }
+  }
+  // every load issued so far completes here (Q, keep words, the first tiles and biases): inside the key loop the only
+  // vector-memory operations are the counted ones
+#pragma unroll
+  for (int r = 0; r < R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
+  __syncthreads();
+  bool dead[R];
+  bool dead_any = false, all_full = true;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t f = __builtin_amdgcn_readfirstlane((uint32_t)sKeep[r][0]);
+    dead[r] = !(f & TK_ALIVE);
+    dead_any |= dead[r];
+    all_full &= (f & TK_FULL) != 0;
+  }
+
+  f32x16 o[R], s[R];
+  float lrow[R];
+  uint64_t unseen[R];              // queries (lanes) of row r that have met no kept key yet (a wave-uniform mask)
+  uint64_t redo = 0;               // queries whose softmax needs a reference other than 0 (the work item goes to the fallback)
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    o[r] = f32x16{};
+    lrow[r] = 0.f;
+    unseen[r] = i0 + r < p.N ? ~0ull : 0ull;
+  }
+  const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile 1 adds 32 keys
+  const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
+  const int vsw = (n >> 1) & 7;
+  auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
+    f32x16 bc;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
+    return mfma32(as_bf8(k1f), qf[r][1], mfma32(as_bf8(k0f), qf[r][0], bc));
+  };
+  // P of one step: bf16 pairs of exp2(s) and the sum of the bf16 values the P.V MFMA consumes
+  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8]) {
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
+    float ps0 = dot2_bf16(pk[0], 0.f), ps1 = dot2_bf16(pk[1], 0.f);
+#pragma unroll
+    for (int j = 2; j < 8; j += 2) {
+      ps0 = dot2_bf16(pk[j], ps0);
+      ps1 = dot2_bf16(pk[j + 1], ps1);
+    }
+    return ps0 + ps1;
+  };
+  // S^T of sub-tile 0 for rows 0 .. R - 2 (row R - 1's is issued by the first step); P of "step -1" is zero, so the first
+  // step's P.V MFMAs add nothing
+  uint32_t P0[8], P1[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) P0[j] = 0u;
+#pragma unroll
+  for (int r = 0; r < R - 1; ++r) {
+    const uint16_t* kt = &sK[0][r][0];
+    s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
+  }
+
+  // MFMA fragments of a step, read from LDS one step ahead: V^T of (row, sub-tile vsub of buffer vbuf), K of (row, sub-tile
+  // ksub of buffer kbuf)
+  u32x4 fv0, fv1, fk0, fk1;
+  auto frags = [&](int vbuf, int vsub, int kbuf, int ksub, int row) {
+    const uint16_t* vt = &sV[vbuf][row][n * TA_KT];
+    fv0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * vsub + g) ^ vsw));
+    fv1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * vsub + 2 + g) ^ vsw));
+    const uint16_t* kt = &sK[kbuf][row][32 * ksub * TA_D];
+    fk0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
+    fk1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
+  };
+  frags(0, 1, 0, 0, R - 1);                            // step (0, 0) of tile 0
+
+  // one 64-key tile T (buffers: bt its own, bp tile T - 1's, bn tile T + 1's): six steps (sub, r); `fast`: every key of the
+  // TA_R rows in this tile is kept and no row is dead (no mask code)
+  auto tile = [&](bool fast, int T, int bt, int bp, int bn, const uint64_t (&kw)[R]) {
+    const int64_t k0 = (int64_t)T * TA_KT;
+    const bool moreT = T + 1 < nT;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (sub == 0 && r == 1) {
+          vm_wait4<0>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);        // bias 2T + 1 (the newest load) is in
+          bias_issue(moreT ? k0 + TA_KT : 0, bq[0]);                     // bias 2T + 2 (past the end: a valid re-read)
+        }
+        if (sub == 1 && r == 0) {
+          // every wave's part of tile T + 1 is in (each wave waited for it above), and every wave is past tile T - 1's
+          // last reads (step (0, 0)): its buffer takes tile T + 2
+          __builtin_amdgcn_s_barrier();
+          asm volatile("" ::: "memory");
+          dma_tile((T + 2 < nT ? T + 2 : nT - 1) * TA_KT, bp);
+        }
+        if (sub == 1 && r == 1) {
+          vm_wait4<DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);  // bias 2T + 2 is in (tile T + 2 may be pending)
+          bias_issue(moreT ? k0 + TA_KT + 32 : 32, bq[1]);              // bias 2T + 3
+        }
+        // the previous step's row pr and the sub-tile nsub of the S^T its MFMAs compute (tile-relative: -1 = tile T - 1's
+        // second sub-tile, 2 = tile T + 1's first); this step's fragments were read by the step before it
+        const int pr = r > 0 ? r - 1 : R - 1;
+        const int nsub = (r > 0 ? sub : sub - 1) + 1;
+        const bool even = ((3 * sub + r) & 1) == 0;
+        uint32_t(&pin)[8] = even ? P0 : P1;
+        uint32_t(&pout)[8] = even ? P1 : P0;
+        const u32x4 vf0 = fv0, vf1 = fv1, kf0 = fk0, kf1 = fk1;
+
+        f32x16& sv = s[r];               // S^T of this step; dead after it (the row's next S^T is written one step later)
+        if (!fast) {
+          const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float x = dead[r] ? 0.f : sv[v];
+            sv[v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? x : -INFINITY;
+          }
+        }
+        uint32_t pk[8];
+        float ps = expsum(sv, pk);
+        o[pr] = mfma32(as_bf8(vf0), as_bf8(u32x4{pin[0], pin[1], pin[2], pin[3]}), o[pr]);
+        o[pr] = mfma32(as_bf8(vf1), as_bf8(u32x4{pin[4], pin[5], pin[6], pin[7]}), o[pr]);
+        s[pr] = qk(kf0, kf1, pr, (nsub & 1) ? bq[1] : bq[0]);
+        // the next step's fragments: (sub, r + 1), else (1, 0), else tile T + 1's (0, 0) (V^T of this tile's second sub-tile,
+        // K of tile T + 1's first: published by this tile's barrier)
+        if (r + 1 < R) frags(bt, sub, sub == 0 ? bt : bn, sub == 0 ? 1 : 0, r);
+        else if (sub == 0) frags(bt, 0, bt, 1, R - 1);
+        else frags(bt, 1, bn, 0, R - 1);
+        // one MFMA every few softmax instructions, so neither unit waits on the other
+        __builtin_amdgcn_sched_group_barrier(0x402, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        // reference 0 is exact for this step unless a partial sum reached 2^64 (or is not finite), or a query's first sub-tile
+        // with a kept key sums below 2^-32 (every logit below about -32): such queries are marked for the fallback
+        uint64_t bad = __builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX));
+        if (unseen[r]) {
+          const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);
+          const uint64_t live = __builtin_amdgcn_ballot_w64(fast || dead[r] || (kbg & 0x0f0f0f0fu) != 0);
+          bad |= __builtin_amdgcn_ballot_w64(!(ps >= TD_PS_MIN)) & unseen[r] & live;
+          unseen[r] &= ~live;
+        }
+        redo |= bad;
+        lrow[r] += ps;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pout[j] = pk[j];
+      }
+    }
+  };
+
+  int bt = 0;
+  for (int T = 0; T < nT; ++T) {
+    const int bn = bt == TA_NB - 1 ? 0 : bt + 1;
+    const int bp = bn == TA_NB - 1 ? 0 : bn + 1;     // (T + 2) mod 3 = (T - 1) mod 3
+    uint64_t kw[R];
+    bool fast;
+    if (all_full) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) kw[r] = ~0ull;
+      fast = true;
+    } else {
+      uint64_t kall = ~0ull;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint64_t wv = sKeep[r][1 + T];
+        const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
+        const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);
+        kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
+        kall &= kw[r];
+      }
+      fast = kall == ~0ull && !dead_any;
+    }
+    tile(fast, T, bt, bp, bn, kw);
+    bt = bn;
+  }
+  // the last step's P.V: row R - 1 of the last sub-tile, with P0 and the V^T fragments the last step read ahead
+  o[R - 1] = mfma32(as_bf8(fv0), as_bf8(u32x4{P0[0], P0[1], P0[2], P0[3]}), o[R - 1]);
+  o[R - 1] = mfma32(as_bf8(fv1), as_bf8(u32x4{P0[4], P0[5], P0[6], P0[7]}), o[R - 1]);
+  vm_wait<0>();                                         // no DMA may land after the wave ends
+  // every wave writes its flag (no clearing needed); a flagged work item is recomputed whole by the fallback kernel
+  if (l == 0) p.redo[(size_t)w * NW + wave] = redo != 0;
+  if (!qlive || redo) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t i = i0 + r;
+    if (i >= p.N) continue;
+    const float lt = half_sum(lrow[r]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int d0 = 8 * qd + 4 * g;
+      *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- fallback core
+// The work items the fast kernel flagged (a query whose softmax needs a reference other than 0), recomputed whole with the
+// same operands and work split: the same MFMA / exp2 / bf16 / row-sum sequence per step, with a lazily moved per-query
+// reference max (log2 units) -- set on a query's first sub-tile with a kept key when that sub-tile's partial sum lies
+// outside [2^-32, 2^64), moved up by a later sub-tile's max when its partial sum reaches 2^64, O and l rescaled when it
+// moves.  One step per (row, 32-key sub-tile), the keep bits built in LDS from the mask, K / V^T tiles by DMA through the
+// same three-buffer ring.  Unflagged work items return at once (one flag read per wave of the item).
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_redo(const CoreParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][TA_R][TA_KT * TA_D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[TA_NB][TA_R][TA_D * TA_KT];
+  __shared__ uint64_t sKeepAll[TA_R][TA_MAXW];
+  __shared__ int sAlive[TA_R];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  // the host checks that the grid fits 31 bits: the workgroup decode is 32-bit
+  const uint32_t nq = (uint32_t)cdiv(p.S, 32 * NW), nr = (uint32_t)cdiv(p.N, TA_R), H = (uint32_t)p.H;
+  const uint32_t total = (uint32_t)p.B * H * nr * nq;
+  // the work items of this workgroup are blockIdx.x + k gridDim.x; 64 of them are checked per round (lane l reads item l's
+  // flags), and only the flagged ones are recomputed
+  for (uint32_t base = blockIdx.x; base < total; base += 64u * gridDim.x) {
+  uint64_t need;
+  {
+    const uint32_t wl = base + (uint32_t)l * gridDim.x;
+    uint32_t any = 0;
+    if (wl < total) {
+#pragma unroll
+      for (int v = 0; v < NW; ++v) any |= p.redo[(size_t)wl * NW + v];
+    }
+    need = __builtin_amdgcn_ballot_w64(any != 0);
+  }
+  while (need) {
+  const uint32_t w = base + (uint32_t)__builtin_ctzll(need) * gridDim.x;
+  need &= need - 1;
+  __syncthreads();                                 // every wave is done with the previous item's LDS
+  const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
+  const int64_t b = bh / H, h = bh % H;
+  const int64_t i0 = (int64_t)rg * TA_R;
+  const int64_t q = (int64_t)qt * (32 * NW) + wave * 32 + n;
+  const bool qlive = q < p.S;
+
+  bf16x8 qf[TA_R][2];
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    const bool ok = i < p.N && qlive;
+    const uint16_t* qp = p.q + b * p.qs[0] + (ok ? i : 0) * p.qs[1] + h * p.qs[2] + (ok ? q : 0) * p.qs[3] + 8 * g;
+    qf[r][0] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0, 0, 0, 0});
+    qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
+  }
+
+
+  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
+  // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves); rows past N read row i0 (never stored).  Row bases are
+  // scalar, the in-tile byte offsets per lane are fixed.
+  const int wc = wave & 3;
+  const uint16_t* kb[TA_R];
+  const uint16_t* vb[TA_R];
+  uint32_t koff, voff;
+  {
+    const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
+    const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+    koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
+    voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      const int64_t ii = i0 + r < p.N ? i0 + r : i0;
+      kb[r] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
+      vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
+    }
+  }
+  // LDS byte addresses of this wave's chunk block in buffer 0, row 0 (buffer / row steps are constants)
+  const uint32_t kl0 = lds_addr(&sK[0][0][512 * wc]), vl0 = lds_addr(&sV[0][0][512 * wc]);
+  constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
+  const bool v_mover = NW > 4 && wave >= 4;
+  auto dma_tile = [&](int64_t k0, int buf) {
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      if (NW == 4 || !v_mover) lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
+      if (NW == 4 || v_mover) lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
+    }
+  };
+  // The wait counts (vm_wait4<DMA_OPS + 4>, vm_wait4<4>) assume exactly DMA_OPS operations per dma_tile and 4 per
+  // bias_issue, every one issued unconditionally and in the order of the loop below: a wait that counted fewer operations
+  // than were issued after the load it guards would let that load land in registers already reused.
+  constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * TA_R;
+
+  const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
+  const uint32_t boff = (uint32_t)(((qlive ? q : 0) * p.bs[2] + 4 * g) * 4);
+  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
+  auto bias_issue = [&](int64_t kb, f32x4 (&dst)[4]) {
+    const float* sb = brow + kb;
+    dst[0] = gload4_async<0>(boff, sb);
+    dst[1] = gload4_async<32>(boff, sb);
+    dst[2] = gload4_async<64>(boff, sb);
+    dst[3] = gload4_async<96>(boff, sb);
+  };
+
+  f32x16 o[TA_R], s[TA_R];
+  float lrow[TA_R], mb[TA_R];
+  uint64_t unseen[TA_R];           // lanes whose `seen` is still false (a wave-uniform mask: the fast path tests it in scalar code)
+  bool seen[TA_R], sh[TA_R];       // seen: the row's first live sub-tile has set its reference (per lane, equal in l and
+                                   // l ^ 32; rows past N count as seen); sh: some lane of the row has a nonzero reference
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    o[r] = f32x16{};
+    lrow[r] = 0.f;
+    mb[r] = 0.f;
+    seen[r] = i0 + r >= p.N;
+    unseen[r] = seen[r] ? 0ull : ~0ull;
+    sh[r] = false;
+  }
+  // fragment offsets (bf16 elements) inside a row's K / V^T tile
+  const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile adds 32 keys
+  const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
+  const int vsw = (n >> 1) & 7;
+  auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
+    f32x16 bc;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
+    return mfma32(as_bf8(k1f), qf[r][1], mfma32(as_bf8(k0f), qf[r][0], bc));
+  };
+  // P of one row step: bf16 pairs of exp2(s) and the sum of the bf16 values the P.V MFMA consumes
+  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8]) {
+    float ps0 = 0.f, ps1 = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
+      if (v & 2) ps1 = dot2_bf16(pk[v >> 1], ps1);
+      else ps0 = dot2_bf16(pk[v >> 1], ps0);
+    }
+    return ps0 + ps1;
+  };
+
+  const int64_t nT = p.S / TA_KT;
+  f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
+  // issue order DMA(0), bias(0), bias(1), DMA(1): the loop's wait counts continue from it
+  dma_tile(0, 0);
+  bias_issue(0, bq[0]);
+  bias_issue(32, bq[1]);
+  dma_tile(nT > 1 ? TA_KT : 0, 1);
+  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys, all of the row's mask loads in flight together
+  // (overlapping the Q loads and the first tiles' transfers, issued above); a row with no kept key attends uniformly to
+  // every key (its words become all ones)
+  const int nw = (int)(p.S >> 6);
+  if (wave < TA_R) {
+    const int64_t i = i0 + wave;
+    const bool rowok = i < p.N;
+    auto build = [&](auto elt) {
+      using T = decltype(elt);
+      const T* mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + (rowok ? i : 0) * p.ms[1];
+      uint64_t any = 0;
+      if (sizeof(T) == 1 && p.mask && p.ms[2] == 1 && (reinterpret_cast<uintptr_t>(mrow) & 15) == 0) {
+        // contiguous u8 keys: lane l reads keys 16 l .. 16 l + 15 of each 1024-key block with one 16-byte load and writes
+        // their keep bits as the 16-bit piece l of the block's words (bit k of piece j = key 16 j + k, the ballot layout)
+        uint16_t* kw16 = reinterpret_cast<uint16_t*>(&sKeepAll[wave][0]);
+        uint32_t anyl = 0;
+        for (int c0 = 0; c0 < (int)p.S; c0 += 1024) {
+          const int key = c0 + 16 * l;
+          uint32_t bits = 0;
+          if (rowok && key < (int)p.S) {
+            const u32x4 m = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(mrow) + key);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              uint32_t t = m[e] | (m[e] >> 1);           // the low bit of each byte: byte != 0
+              t |= t >> 2;
+              t |= t >> 4;
+              t &= 0x01010101u;
+              bits |= ((t * 0x01020408u) >> 24 & 0xfu) << (4 * e);   // gathers the 4 byte flags, key order
+            }
+          }
+          if (key < (int)p.S) kw16[key >> 4] = (uint16_t)bits;
+          anyl |= bits;
+        }
+        any = __ballot(anyl != 0);
+      } else
+      for (int c0 = 0; c0 < nw; c0 += 16) {
+        T raw[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) raw[u] = (p.mask && c0 + u < nw) ? mrow[(int64_t)(64 * (c0 + u) + l) * p.ms[2]] : (T)1;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (c0 + u >= nw) break;
+          const uint64_t bal = __ballot(rowok && raw[u] != (T)0);
+          any |= bal;
+          if (l == 0) sKeepAll[wave][c0 + u] = bal;
+        }
+      }
+      if (rowok && any == 0)
+        for (int c = l; c < nw; c += 64) sKeepAll[wave][c] = ~0ull;
+      if (l == 0) sAlive[wave] = any != 0;
+    };
+    if (p.mask_f32) build(0.0f);
+    else build((uint8_t)0);
+  }
+  // the Q and mask loads complete here (and the older transfers with them: the counter retires in order); inside the key
+  // loop the only vector-memory operations are the counted ones
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
+  __syncthreads();
+  bool dead[TA_R];
+  bool dead_any = false;
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    dead[r] = (i0 + r < p.N) && !sAlive[r];
+    dead_any |= dead[r];
+  }
+  vm_wait4<4 + DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);    // tile 0 and bias 0 are in (bias 1, tile 1 may be pending)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const uint16_t* kt = &sK[0][r][0];
+    s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
+  }
+
+  int bt = 0;                      // buffer of tile T
+  for (int64_t T = 0; T < nT; ++T) {
+    const bool moreT = T + 1 < nT;
+    const int bn = bt == TA_NB - 1 ? 0 : bt + 1;      // buffer of tile T + 1
+    const int bf = bn == TA_NB - 1 ? 0 : bn + 1;      // buffer of tile T + 2: tile T - 1's, free once every wave is past it
+    const int64_t k0 = T * TA_KT;
+    bias_issue(moreT ? k0 + TA_KT : 0, bq[0]);         // sub-tile 2T + 2 (past the end: a valid re-read, the counts stay exact)
+    uint64_t kw[TA_R], kall = ~0ull, kany = 0;
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      const uint64_t wv = sKeepAll[r][T];                               // uniform: keep it in scalar registers
+      const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
+      const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);   // unsigned: no sign extension
+      kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
+      kall &= kw[r];
+      kany |= kw[r];
+    }
+    const bool full = (kall == ~0ull) && !dead_any;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      if (sub == 0) {
+        vm_wait4<DMA_OPS + 4>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);   // bias 2T + 1 (tile T + 1, bias 2T + 2 may be pending)
+      } else {
+        bias_issue(moreT ? k0 + TA_KT + 32 : 32, bq[1]);                 // sub-tile 2T + 3
+        vm_wait4<4>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);             // bias 2T + 2 and tile T + 1 are in
+        __builtin_amdgcn_s_barrier();                                     // every wave's part of tile T + 1 is in, and every
+        asm volatile("" ::: "memory");                                    // wave is done with tile T - 1
+        dma_tile((T + 2 < nT ? T + 2 : nT - 1) * TA_KT, bf);
+      }
+      const bool live_sub = (uint32_t)(kany >> (32 * sub)) != 0;
+      const bool next = sub == 0 || moreT;                                // the next sub-tile exists
+      const uint16_t* knext = sub == 0 ? &sK[bt][0][32 * TA_D] : &sK[bn][0][0];
+#pragma unroll
+      for (int r = 0; r < TA_R; ++r) {
+        // fragment reads first: V^T of this step, K of the row's next S^T
+        const uint16_t* vt = &sV[bt][r][n * TA_KT];
+        const u32x4 vf0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + g) ^ vsw));
+        const u32x4 vf1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + 2 + g) ^ vsw));
+        const uint16_t* kt = knext + r * (TA_KT * TA_D);
+        u32x4 kf0 = u32x4{0, 0, 0, 0}, kf1 = u32x4{0, 0, 0, 0};
+        if (next) {
+          kf0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
+          kf1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
+        }
+        if (live_sub) {
+          if (!full) {
+            const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const float sv = dead[r] ? 0.f : s[r][v];
+              s[r][v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? sv : -INFINITY;
+            }
+          }
+          if (sh[r]) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[r][v] -= mb[r];
+          }
+          uint32_t pk[8];
+          float ps = expsum(s[r], pk);
+          if ((__builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX)) | unseen[r]) != 0) {
+            // set or move the reference of the queries that need it; the decision depends only on the sub-tile max over
+            // both key halves, so lanes l and l ^ 32 (one query) always agree
+            float m0 = s[r][0];
+#pragma unroll
+            for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, s[r][v]);
+            const float mt = half_max(m0);
+            const bool fin = mt > -INFINITY;
+            // the fast kernel's thresholds: a query's first sub-tile with a kept key takes its max as the reference when its
+            // partial sum is below 2^-32 or at or above 2^64; later sub-tiles move it when their partial sum reaches 2^64.  A
+            // row the fast kernel finished (no flag) gets the same reference, 0, and so the same bits from both kernels.
+            const bool out = !(ps >= TD_PS_MIN && ps < TD_PS_MAX);
+            const float shift = !seen[r] ? ((fin && out) ? mt : 0.f) : (!(ps < TD_PS_MAX) ? mt : 0.f);
+            const float alpha = seen[r] && shift != 0.f ? fast_exp2(-shift) : 1.0f;   // before the first live sub-tile o, l are 0
+            lrow[r] *= alpha;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[r][v] -= shift;
+            mb[r] += shift;
+            seen[r] = seen[r] || fin;
+            unseen[r] = __builtin_amdgcn_ballot_w64(!seen[r]);
+            sh[r] = __ballot(mb[r] != 0.f) != 0;
+            ps = expsum(s[r], pk);
+          }
+          lrow[r] += ps;
+          o[r] = mfma32(as_bf8(vf0), as_bf8(u32x4{pk[0], pk[1], pk[2], pk[3]}), o[r]);
+          o[r] = mfma32(as_bf8(vf1), as_bf8(u32x4{pk[4], pk[5], pk[6], pk[7]}), o[r]);
+        }
+        if (next) s[r] = qk(kf0, kf1, r, sub == 0 ? bq[1] : bq[0]);
+      }
+    }
+    bt = bn;
+  }
+  vm_wait<0>();                                         // no DMA may land after the item ends
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) {
+    const int64_t i = i0 + r;
+    if (i >= p.N || !qlive) continue;
+    const float lt = half_sum(lrow[r]);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int d0 = 8 * qd + 4 * g;
+      *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
+    }
+  }
+  }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------- launchers
+int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, uint64_t* keep, hipStream_t st,
+                      char* err, size_t errlen) {
+  if (!mask || !keep) return fail(err, errlen, FPF_E_ARGS, "keep table: mask / table is NULL");
+  if (S % TA_KT != 0 || S > (int64_t)TA_KT * TA_MAXW) return fail(err, errlen, FPF_E_SHAPE, "keep table: S a multiple of 64 up to %d", TA_KT * TA_MAXW);
+  const int64_t blocks = cdiv(B * N, 4);
+  if (blocks > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "keep table: grid too large");
+  hipLaunchKernelGGL(triattn_keep_bits, dim3((unsigned)blocks), dim3(256), 0, st, mask, mask_f32, ms[0], ms[1], ms[2], B, N, S, keep);
+  return launched(err, errlen, "triattn_keep_bits");
+}
+
+// The caller has checked the layout: S a multiple of 64 up to 64 TA_MAXW, fp32 bias with 16-byte aligned rows, q / k / V^T
+// 16-byte aligned with strides in multiples of 8, scale 1, p.redo holding redo_words(B, N, H, S) words.  8 waves (256 queries)
+// share each K / V^T tile where S fills whole 256-query tiles and the grid still has 8 or more workgroups per CU; 4 waves (128
+// queries) elsewhere.  The fallback runs on the same stream right after the fast kernel, over the same grid.
+int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen) {
+  const int64_t rows_heads = p.B * p.H * cdiv(p.N, TA_R);
+  const bool wide = p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * (int64_t)num_cus();
+  const int64_t total = wide ? rows_heads * (p.S / (32 * TA_DMA_WAVES)) : rows_heads * cdiv(p.S, 128);
+  if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
+  const dim3 grid((unsigned)(cdiv(total, 8) * 8));
+  const dim3 redo_grid((unsigned)std::min<int64_t>(total, num_cus()));   // persistent: each workgroup scans its share of flags
+  if (wide) {
+    hipLaunchKernelGGL(triattn_core_bf16_pipe<TA_DMA_WAVES>, grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+    hipLaunchKernelGGL(triattn_core_bf16_redo<TA_DMA_WAVES>, redo_grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+  } else {
+    hipLaunchKernelGGL(triattn_core_bf16_pipe<4>, grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL(triattn_core_bf16_redo<4>, redo_grid, dim3(256), 0, st, p);
+  }
+  return launched(err, errlen, "triattn_core_bf16_pipe");
+}
+
+}  // namespace fpf

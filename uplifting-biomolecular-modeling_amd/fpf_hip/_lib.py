@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 DT_BF16, DT_F32, DT_U8 = 1, 2, 3
 TRIMUL_NOALLOC_SCRATCH_BYTES = 50331648          # include/fpf_hip.h FPF_TRIMUL_NOALLOC_SCRATCH_BYTES
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
@@ -40,7 +40,8 @@ class TriattnArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("H", i64), ("S", i64), ("D", i64),
                 ("q", vp), ("k", vp), ("v", vp), ("q_stride", i64 * 5), ("k_stride", i64 * 5), ("v_stride", i64 * 5), ("v_layout", i32),
                 ("bias", vp), ("bias_dtype", i32), ("bias_stride", i64 * 4), ("mask", vp), ("mask_dtype", i32),
-                ("mask_stride", i64 * 3), ("out", vp), ("out_stride", i64 * 5), ("scale", f32)]
+                ("mask_stride", i64 * 3), ("out", vp), ("out_stride", i64 * 5), ("scale", f32), ("keep", vp),
+                ("workspace", vp), ("workspace_bytes", sz)]
 
 
 class TriattnBlockArgs(C.Structure):
@@ -88,6 +89,7 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_trimul_fwd_noalloc": ([C.POINTER(TrimulArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_fwd": ([C.POINTER(TriattnArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_workspace_bytes": ([i64, i64, i64, i32, i32, i32, i32], sz),
+    "fpf_triattn_workspace_bytes": ([i64, i64, i64, i64, i32], sz),
     "fpf_triattn_bias_fwd": ([C.POINTER(TriattnBiasArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_fwd": ([C.POINTER(TriattnBlockArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_prologue_fwd": ([C.POINTER(TriattnPrologueArgs), vp, C.c_char_p, sz], C.c_int),
