@@ -66,6 +66,12 @@ template <int IMM>
 __device__ __forceinline__ void gload4_into(f32x4& v, uint32_t voff, const void* sbase) {
   asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "+v"(v) : "v"(voff), "s"(sbase), "n"(IMM));
 }
+// 8 bytes at a wave-uniform address through the scalar cache, waited for here (lgkmcnt also covers this wave's LDS reads)
+__device__ __forceinline__ uint64_t sload64(const uint64_t* a) {
+  uint64_t v;
+  asm volatile("s_load_dwordx2 %0, %1, 0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(a) : "memory");
+  return v;
+}
 // waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
 // through the statement so nothing reads them earlier
 template <int N>

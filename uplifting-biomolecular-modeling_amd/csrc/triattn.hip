@@ -858,6 +858,8 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
       if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
       if (p.mask && !a->keep)
         return fail(err, errlen, FPF_E_ARGS, "v_layout 2 reads the mask as a keep-bit table (keep); the fused block builds it");
+      if (p.os[3] != TA_D || ((p.os[0] | p.os[1] | p.os[2]) & 7) || !aligned16(a->out))
+        return fail(err, errlen, FPF_E_ALIGN, "v_layout 2 writes out rows of %d contiguous bf16, 16-byte aligned", TA_D);
       const size_t need = (size_t)redo_words(a->B, a->N, a->H, a->S) * 4;
       if (!a->workspace || a->workspace_bytes < need)
         return fail(err, errlen, FPF_E_WORKSPACE, "v_layout 2: workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);

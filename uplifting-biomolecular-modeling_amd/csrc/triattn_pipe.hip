@@ -73,129 +73,144 @@ __global__ void __launch_bounds__(256) triattn_keep_bits(const void* __restrict_
 }
 
 // ---------------------------------------------------------------------------------------------------------------- core
+constexpr int TA_OP = 40;        // LDS pitch (bf16) of the per-wave output staging rows (80 B: 16-byte aligned, few conflicts)
+
+// One work item: TA_R pair rows x 32 NW queries x one (b, h), and the addresses its loads use.  K / V^T row bases and the
+// bias plane are wave-uniform (scalar registers); q (the lane's query) and boff (its bias row offset) are per lane.
+struct PipeItem {
+  int64_t b, h, i0, q;
+  bool qlive;
+  const uint16_t* kb[TA_R];
+  const uint16_t* vb[TA_R];
+  const float* brow;
+  uint32_t boff;
+};
+
+// Persistent: a workgroup walks a contiguous range of work items (XCD x takes the x-th eighth of them, so one XCD works on one
+// head and keeps its bias in L2, and the query tiles of a row group run back to back).  The K / V^T DMA ring and the bias
+// double buffer run across item boundaries (the loads past an item's last tile fetch the next item's first tiles), the next
+// item's q is loaded during the item's second-to-last tile, and an item's output leaves through LDS as contiguous 16-byte
+// stores that drain while the next item computes.
 template <int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_pipe(const CoreParams p) {
   constexpr int R = TA_R;
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][R][TA_KT * TA_D];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_NB][R][TA_D * TA_KT];
-  __shared__ uint64_t sKeep[R][TA_MAXW + 1];
+  // output staging rows of the 8-wave split (the 4-wave split, two workgroups per CU, has no LDS left for them and stores
+  // straight from registers)
+  __shared__ __attribute__((aligned(16))) uint16_t sO[NW > 4 ? NW : 1][32 * TA_OP];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  // the host checks that the grid fits 31 bits: the workgroup decode is 32-bit.  Workgroup order is XCD-aware: consecutive
-  // work items (the query tiles of one row group, then the row groups of one head) run on one XCD, so a head's bias and a
-  // row group's K / V^T tiles stay in that XCD's L2.
+  // the host checks that the item count fits 31 bits: the decode is 32-bit
   const uint32_t nq = (uint32_t)cdiv(p.S, 32 * NW), nr = (uint32_t)cdiv(p.N, R), H = (uint32_t)p.H;
   const uint32_t total = (uint32_t)p.B * H * nr * nq;
-  const uint32_t per = (total + 7) / 8;
-  const uint32_t w = (blockIdx.x % 8) * per + blockIdx.x / 8;
-  if (w >= total) return;
-  const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
-  const int64_t b = bh / H, h = bh % H;
-  const int64_t i0 = (int64_t)rg * R;
-  const int64_t q = (int64_t)qt * (32 * NW) + wave * 32 + n;
-  const bool qlive = q < p.S;
-
-  bf16x8 qf[R][2];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t i = i0 + r;
-    const bool ok = i < p.N && qlive;
-    const uint16_t* qp = p.q + b * p.qs[0] + (ok ? i : 0) * p.qs[1] + h * p.qs[2] + (ok ? q : 0) * p.qs[3] + 8 * g;
-    qf[r][0] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp) : u32x4{0, 0, 0, 0});
-    qf[r][1] = as_bf8(ok ? *reinterpret_cast<const u32x4*>(qp + 16) : u32x4{0, 0, 0, 0});
+  const uint32_t xcd = blockIdx.x & 7, j = blockIdx.x >> 3, nwg = (gridDim.x - xcd + 7) >> 3;
+  const uint32_t lo = (uint32_t)((uint64_t)xcd * total / 8), hi = (uint32_t)((uint64_t)(xcd + 1) * total / 8);
+  const uint32_t w0 = lo + (uint32_t)((uint64_t)(hi - lo) * j / nwg), w1 = lo + (uint32_t)((uint64_t)(hi - lo) * (j + 1) / nwg);
+  if (w0 >= w1) return;
+  const int nT = (int)(p.S / TA_KT);
+  if (nT < 2) {                                    // a one-tile key range: every item goes to the fallback kernel
+    for (uint32_t w = w0; w < w1; ++w)
+      if (l == 0) p.redo[(size_t)w * NW + wave] = 1u;
+    return;
   }
 
-  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
-  // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves); rows past N read row i0 (never stored).
   const int wc = wave & 3;
-  const uint16_t* kb[R];
-  const uint16_t* vb[R];
   uint32_t koff, voff;
   {
     const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
     const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
     koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
     voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
+  }
+  auto item_of = [&](uint32_t w, PipeItem& it) {
+    const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
+    it.b = bh / H;
+    it.h = bh % H;
+    it.i0 = (int64_t)rg * R;
+    it.q = (int64_t)qt * (32 * NW) + wave * 32 + n;
+    it.qlive = it.q < p.S;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t ii = i0 + r < p.N ? i0 + r : i0;
-      kb[r] = p.k + b * p.ks[0] + ii * p.ks[1] + h * p.ks[2];
-      vb[r] = p.v + b * p.vs[0] + ii * p.vs[1] + h * p.vs[2];
+      const int64_t ii = it.i0 + r < p.N ? it.i0 + r : it.i0;         // rows past N read row i0 (never stored)
+      it.kb[r] = p.k + it.b * p.ks[0] + ii * p.ks[1] + it.h * p.ks[2];
+      it.vb[r] = p.v + it.b * p.vs[0] + ii * p.vs[1] + it.h * p.vs[2];
     }
-  }
+    it.brow = static_cast<const float*>(p.bias) + it.b * p.bs[0] + it.h * p.bs[1];
+    it.boff = (uint32_t)(((it.qlive ? it.q : 0) * p.bs[2] + 4 * g) * 4);
+  };
+  // q of an item (the lane's query in each of the TA_R rows; rows past N and queries past S read row i0 / query 0, whose
+  // results are never stored): 2 operations per row
+  auto q_issue = [&](const PipeItem& it, u32x4 (&dst)[R][2]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t i = it.i0 + r < p.N ? it.i0 + r : it.i0;
+      const uint16_t* qp = p.q + it.b * p.qs[0] + i * p.qs[1] + it.h * p.qs[2];        // scalar row base
+      const uint32_t qo = (uint32_t)(((it.qlive ? it.q : 0) * p.qs[3] + 8 * g) * 2);  // the lane's query (32-bit: host-checked)
+      asm volatile("global_load_dwordx4 %0, %1, %2 offset:0" : "+v"(dst[r][0]) : "v"(qo), "s"(qp));
+      asm volatile("global_load_dwordx4 %0, %1, %2 offset:32" : "+v"(dst[r][1]) : "v"(qo), "s"(qp));
+    }
+  };
+  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
+  // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves).  Row bases are scalar, the in-tile byte offsets per lane fixed.
   const uint32_t kl0 = lds_addr(&sK[0][0][512 * wc]), vl0 = lds_addr(&sV[0][0][512 * wc]);
   constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
   const bool v_mover = NW > 4 && wave >= 4;
-  auto dma_tile = [&](int64_t k0, int buf) {
+  auto dma_tile = [&](const PipeItem& it, int64_t k0, int buf) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (NW == 4 || !v_mover) lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * R + r) * TILE_B);
-      if (NW == 4 || v_mover) lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * R + r) * TILE_B);
+      if (NW == 4 || !v_mover) lds_dma16_s(koff, it.kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * R + r) * TILE_B);
+      if (NW == 4 || v_mover) lds_dma16_s(voff, it.vb[r] + k0, vl0 + (uint32_t)(buf * R + r) * TILE_B);
     }
   };
   // The wait counts below (vm_wait4<0>, vm_wait4<DMA_OPS>) assume exactly DMA_OPS operations per dma_tile and 4 per
-  // bias_issue, every one issued unconditionally and in the order of the loop: a wait counting fewer operations than were
-  // issued after the load it guards would let that load land in registers already in use.
+  // bias_issue, every one issued unconditionally and in the order of the loop (the q loads of the next item come after the
+  // last counted wait of a tile and before the next tile's vmcnt(0)): a wait counting fewer operations than were issued after
+  // the load it guards would let that load land in registers already in use.
   constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * R;
-
-  const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
-  const uint32_t boff = (uint32_t)(((qlive ? q : 0) * p.bs[2] + 4 * g) * 4);
-  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
-  auto bias_issue = [&](int64_t k, f32x4 (&dst)[4]) {
-    const float* sb = brow + k;
-    gload4_into<0>(dst[0], boff, sb);
-    gload4_into<32>(dst[1], boff, sb);
-    gload4_into<64>(dst[2], boff, sb);
-    gload4_into<96>(dst[3], boff, sb);
+  // bias of sub-tile keys k + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
+  auto bias_issue = [&](const PipeItem& it, int64_t k, f32x4 (&dst)[4]) {
+    const float* sb = it.brow + k;
+    gload4_into<0>(dst[0], it.boff, sb);
+    gload4_into<32>(dst[1], it.boff, sb);
+    gload4_into<64>(dst[2], it.boff, sb);
+    gload4_into<96>(dst[3], it.boff, sb);
+  };
+  // row flags / keep words of an item's TA_R rows (no mask: every key kept), read through the scalar cache: a vector load
+  // here would come with a compiler-placed vmcnt wait that drains the counted transfers in flight
+  auto row_flags = [&](const PipeItem& it, int r) -> uint32_t {
+    if (!p.keep || it.i0 + r >= p.N) return (uint32_t)(TK_ALIVE | TK_FULL);
+    return (uint32_t)sload64(p.keep + (it.b * p.N + it.i0 + r) * keep_words(p.S));
+  };
+  auto keep_word = [&](const PipeItem& it, int r, int T) -> uint64_t {
+    if (!p.keep || it.i0 + r >= p.N) return ~0ull;
+    return sload64(p.keep + (it.b * p.N + it.i0 + r) * keep_words(p.S) + 1 + T);
   };
 
-  const int nT = (int)(p.S / TA_KT);
+  PipeItem cur, nxt;
+  item_of(w0, cur);
+  item_of(w0 + 1 < w1 ? w0 + 1 : w0, nxt);
   f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
+  u32x4 qn[R][2];                  // q of the next item (loaded one tile ahead)
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) bq[x][qd] = f32x4{};
-  dma_tile(0, 0);
-  bias_issue(0, bq[0]);
-  bias_issue(32, bq[1]);
-  dma_tile(nT > 1 ? TA_KT : 0, 1);
-  // the TA_R rows' keep words (rows past N, or no mask: every key kept)
-  if (wave < R) {
-    const int64_t i = i0 + wave;
-    if (p.keep && i < p.N) {
-      const uint64_t* src = p.keep + (b * p.N + i) * keep_words(p.S);
-      for (int c = l; c <= nT; c += 64) sKeep[wave][c] = src[c];
-    } else {
-      for (int c = l; c <= nT; c += 64) sKeep[wave][c] = c == 0 ? (TK_ALIVE | TK_FULL) : ~0ull;
-    }
-  }
-  // every load issued so far completes here (Q, keep words, the first tiles and biases): inside the key loop the only
-  // vector-memory operations are the counted ones
 #pragma unroll
-  for (int r = 0; r < R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
+  for (int r = 0; r < R; ++r) qn[r][0] = qn[r][1] = u32x4{0, 0, 0, 0};
+  q_issue(cur, qn);
+  dma_tile(cur, 0, 0);
+  bias_issue(cur, 0, bq[0]);
+  bias_issue(cur, 32, bq[1]);
+  dma_tile(cur, TA_KT, 1);
+  vm_wait<0>();
+#pragma unroll
+  for (int r = 0; r < R; ++r) asm volatile("" : "+v"(qn[r][0]), "+v"(qn[r][1]));
   __syncthreads();
-  bool dead[R];
-  bool dead_any = false, all_full = true;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const uint32_t f = __builtin_amdgcn_readfirstlane((uint32_t)sKeep[r][0]);
-    dead[r] = !(f & TK_ALIVE);
-    dead_any |= dead[r];
-    all_full &= (f & TK_FULL) != 0;
-  }
 
-  f32x16 o[R], s[R];
-  float lrow[R];
-  uint64_t unseen[R];              // queries (lanes) of row r that have met no kept key yet (a wave-uniform mask)
-  uint64_t redo = 0;               // queries whose softmax needs a reference other than 0 (the work item goes to the fallback)
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    o[r] = f32x16{};
-    lrow[r] = 0.f;
-    unseen[r] = i0 + r < p.N ? ~0ull : 0ull;
-  }
   const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile 1 adds 32 keys
   const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
   const int vsw = (n >> 1) & 7;
+  bf16x8 qf[R][2];
   auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
     f32x16 bc;
 #pragma unroll
@@ -210,23 +225,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
     float ps0 = dot2_bf16(pk[0], 0.f), ps1 = dot2_bf16(pk[1], 0.f);
 #pragma unroll
-    for (int j = 2; j < 8; j += 2) {
-      ps0 = dot2_bf16(pk[j], ps0);
-      ps1 = dot2_bf16(pk[j + 1], ps1);
+    for (int jj = 2; jj < 8; jj += 2) {
+      ps0 = dot2_bf16(pk[jj], ps0);
+      ps1 = dot2_bf16(pk[jj + 1], ps1);
     }
     return ps0 + ps1;
   };
-  // S^T of sub-tile 0 for rows 0 .. R - 2 (row R - 1's is issued by the first step); P of "step -1" is zero, so the first
-  // step's P.V MFMAs add nothing
-  uint32_t P0[8], P1[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) P0[j] = 0u;
-#pragma unroll
-  for (int r = 0; r < R - 1; ++r) {
-    const uint16_t* kt = &sK[0][r][0];
-    s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
-  }
-
   // MFMA fragments of a step, read from LDS one step ahead: V^T of (row, sub-tile vsub of buffer vbuf), K of (row, sub-tile
   // ksub of buffer kbuf)
   u32x4 fv0, fv1, fk0, fk1;
@@ -238,132 +242,200 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     fk0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
     fk1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
   };
-  frags(0, 1, 0, 0, R - 1);                            // step (0, 0) of tile 0
 
-  // one 64-key tile T (buffers: bt its own, bp tile T - 1's, bn tile T + 1's): six steps (sub, r); `fast`: every key of the
-  // TA_R rows in this tile is kept and no row is dead (no mask code)
-  auto tile = [&](bool fast, int T, int bt, int bp, int bn, const uint64_t (&kw)[R]) {
-    const int64_t k0 = (int64_t)T * TA_KT;
-    const bool moreT = T + 1 < nT;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        if (sub == 0 && r == 1) {
-          vm_wait4<0>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);        // bias 2T + 1 (the newest load) is in
-          bias_issue(moreT ? k0 + TA_KT : 0, bq[0]);                     // bias 2T + 2 (past the end: a valid re-read)
-        }
-        if (sub == 1 && r == 0) {
-          // every wave's part of tile T + 1 is in (each wave waited for it above), and every wave is past tile T - 1's
-          // last reads (step (0, 0)): its buffer takes tile T + 2
-          __builtin_amdgcn_s_barrier();
-          asm volatile("" ::: "memory");
-          dma_tile((T + 2 < nT ? T + 2 : nT - 1) * TA_KT, bp);
-        }
-        if (sub == 1 && r == 1) {
-          vm_wait4<DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);  // bias 2T + 2 is in (tile T + 2 may be pending)
-          bias_issue(moreT ? k0 + TA_KT + 32 : 32, bq[1]);              // bias 2T + 3
-        }
-        // the previous step's row pr and the sub-tile nsub of the S^T its MFMAs compute (tile-relative: -1 = tile T - 1's
-        // second sub-tile, 2 = tile T + 1's first); this step's fragments were read by the step before it
-        const int pr = r > 0 ? r - 1 : R - 1;
-        const int nsub = (r > 0 ? sub : sub - 1) + 1;
-        const bool even = ((3 * sub + r) & 1) == 0;
-        uint32_t(&pin)[8] = even ? P0 : P1;
-        uint32_t(&pout)[8] = even ? P1 : P0;
-        const u32x4 vf0 = fv0, vf1 = fv1, kf0 = fk0, kf1 = fk1;
+  f32x16 o[R], s[R];
+  float lrow[R];
+  uint64_t unseen[R];              // queries (lanes) of row r that have met no kept key yet (a wave-uniform mask)
+  uint64_t redo = 0;               // queries whose softmax needs a reference other than 0 (the work item goes to the fallback)
+  bool dead[R];
+  bool dead_any = false, all_full = true;
+  uint32_t P0[8], P1[8];
+  int bt = 0;                      // ring buffer of the current tile
 
-        f32x16& sv = s[r];               // S^T of this step; dead after it (the row's next S^T is written one step later)
-        if (!fast) {
-          const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
+  for (uint32_t w = w0; w < w1; ++w) {
+    const bool has_next = w + 1 < w1;
+    // ---- item start: state, flags, q, S^T of sub-tile 0 for rows 0 .. R - 2 (row R - 1's is issued by the first step)
+    dead_any = false;
+    all_full = true;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float x = dead[r] ? 0.f : sv[v];
-            sv[v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? x : -INFINITY;
+    for (int r = 0; r < R; ++r) {
+      const uint32_t f = row_flags(cur, r);
+      dead[r] = !(f & TK_ALIVE);
+      dead_any |= dead[r];
+      all_full &= (f & TK_FULL) != 0;
+      o[r] = f32x16{};
+      lrow[r] = 0.f;
+      unseen[r] = cur.i0 + r < p.N ? ~0ull : 0ull;
+      qf[r][0] = as_bf8(qn[r][0]);
+      qf[r][1] = as_bf8(qn[r][1]);
+    }
+    redo = 0;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) P0[jj] = 0u;     // P of "step -1" is zero: the first step's P.V MFMAs add nothing
+#pragma unroll
+    for (int r = 0; r < R - 1; ++r) {
+      const uint16_t* kt = &sK[bt][r][0];
+      s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
+    }
+    frags(bt, 1, bt, 0, R - 1);                       // step (0, 0)
+
+    // one 64-key tile T (buffers: bt its own, bp tile T - 1's, bn tile T + 1's): six steps (sub, r); `fast`: every key of
+    // the TA_R rows in this tile is kept and no row is dead (no mask code)
+    auto tile = [&](bool fast, int T, int bp, int bn, const uint64_t (&kw)[R]) {
+      const int64_t k0 = (int64_t)T * TA_KT;
+      const bool moreT = T + 1 < nT;
+      const PipeItem& nb = moreT ? cur : nxt;         // the item whose sub-tiles 2T + 2, 2T + 3 follow
+      const int64_t kb2 = moreT ? k0 + TA_KT : 0;
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (sub == 0 && r == 1) {
+            vm_wait4<0>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);      // bias 2T + 1 (the newest load) is in, and the next
+#pragma unroll                                                          // item's q loaded in the tile before
+            for (int rr = 0; rr < R; ++rr) asm volatile("" : "+v"(qn[rr][0]), "+v"(qn[rr][1]));
+            bias_issue(nb, kb2, bq[0]);                                  // bias 2T + 2
           }
-        }
-        uint32_t pk[8];
-        float ps = expsum(sv, pk);
-        o[pr] = mfma32(as_bf8(vf0), as_bf8(u32x4{pin[0], pin[1], pin[2], pin[3]}), o[pr]);
-        o[pr] = mfma32(as_bf8(vf1), as_bf8(u32x4{pin[4], pin[5], pin[6], pin[7]}), o[pr]);
-        s[pr] = qk(kf0, kf1, pr, (nsub & 1) ? bq[1] : bq[0]);
-        // the next step's fragments: (sub, r + 1), else (1, 0), else tile T + 1's (0, 0) (V^T of this tile's second sub-tile,
-        // K of tile T + 1's first: published by this tile's barrier)
-        if (r + 1 < R) frags(bt, sub, sub == 0 ? bt : bn, sub == 0 ? 1 : 0, r);
-        else if (sub == 0) frags(bt, 0, bt, 1, R - 1);
-        else frags(bt, 1, bn, 0, R - 1);
-        // one MFMA every few softmax instructions, so neither unit waits on the other
-        __builtin_amdgcn_sched_group_barrier(0x402, 8, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-        __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        // reference 0 is exact for this step unless a partial sum reached 2^64 (or is not finite), or a query's first sub-tile
-        // with a kept key sums below 2^-32 (every logit below about -32): such queries are marked for the fallback
-        uint64_t bad = __builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX));
-        if (unseen[r]) {
-          const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);
-          const uint64_t live = __builtin_amdgcn_ballot_w64(fast || dead[r] || (kbg & 0x0f0f0f0fu) != 0);
-          bad |= __builtin_amdgcn_ballot_w64(!(ps >= TD_PS_MIN)) & unseen[r] & live;
-          unseen[r] &= ~live;
-        }
-        redo |= bad;
-        lrow[r] += ps;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pout[j] = pk[j];
-      }
-    }
-  };
+          if (sub == 1 && r == 0) {
+            // every wave's part of tile T + 1 is in (each wave waited for it above), and every wave is past tile T - 1's
+            // last reads (step (0, 0)): its buffer takes tile T + 2 (of this item, or of the next)
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (T + 2 < nT) dma_tile(cur, (int64_t)(T + 2) * TA_KT, bp);
+            else dma_tile(nxt, (int64_t)(T + 2 - nT) * TA_KT, bp);
+          }
+          if (sub == 1 && r == 1) {
+            vm_wait4<DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);  // bias 2T + 2 is in (tile T + 2 may be pending)
+            bias_issue(nb, kb2 + 32, bq[1]);                               // bias 2T + 3
+            if (T == nT - 2 && has_next) q_issue(nxt, qn);                 // waited by the last tile's vmcnt(0)
+          }
+          // the previous step's row pr and the sub-tile nsub of the S^T its MFMAs compute (tile-relative: -1 = tile T - 1's
+          // second sub-tile, 2 = tile T + 1's first); this step's fragments were read by the step before it
+          const int pr = r > 0 ? r - 1 : R - 1;
+          const int nsub = (r > 0 ? sub : sub - 1) + 1;
+          const bool even = ((3 * sub + r) & 1) == 0;
+          uint32_t(&pin)[8] = even ? P0 : P1;
+          uint32_t(&pout)[8] = even ? P1 : P0;
+          const u32x4 vf0 = fv0, vf1 = fv1, kf0 = fk0, kf1 = fk1;
 
-  int bt = 0;
-  for (int T = 0; T < nT; ++T) {
-    const int bn = bt == TA_NB - 1 ? 0 : bt + 1;
-    const int bp = bn == TA_NB - 1 ? 0 : bn + 1;     // (T + 2) mod 3 = (T - 1) mod 3
-    uint64_t kw[R];
-    bool fast;
-    if (all_full) {
+          f32x16& sv = s[r];               // S^T of this step; dead after it (the row's next S^T is written one step later)
+          if (!fast) {
+            const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
 #pragma unroll
-      for (int r = 0; r < R; ++r) kw[r] = ~0ull;
-      fast = true;
-    } else {
-      uint64_t kall = ~0ull;
+            for (int v = 0; v < 16; ++v) {
+              const float xv = dead[r] ? 0.f : sv[v];
+              sv[v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? xv : -INFINITY;
+            }
+          }
+          uint32_t pk[8];
+          float ps = expsum(sv, pk);
+          o[pr] = mfma32(as_bf8(vf0), as_bf8(u32x4{pin[0], pin[1], pin[2], pin[3]}), o[pr]);
+          o[pr] = mfma32(as_bf8(vf1), as_bf8(u32x4{pin[4], pin[5], pin[6], pin[7]}), o[pr]);
+          s[pr] = qk(kf0, kf1, pr, (nsub & 1) ? bq[1] : bq[0]);
+          // the next step's fragments: (sub, r + 1), else (1, 0), else tile T + 1's (0, 0) (V^T of this tile's second
+          // sub-tile, K of tile T + 1's first: published by this tile's barrier)
+          if (r + 1 < R) frags(bt, sub, sub == 0 ? bt : bn, sub == 0 ? 1 : 0, r);
+          else if (sub == 0) frags(bt, 0, bt, 1, R - 1);
+          else frags(bt, 1, bn, 0, R - 1);
+          // one MFMA every few softmax instructions, so neither unit waits on the other
+          __builtin_amdgcn_sched_group_barrier(0x402, 8, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          // reference 0 is exact for this step unless a partial sum reached 2^64 (or is not finite), or a query's first
+          // sub-tile with a kept key sums below 2^-32 (every logit below about -32): such queries are marked for the fallback
+          uint64_t bad = __builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX));
+          if (unseen[r]) {
+            const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);
+            const uint64_t live = __builtin_amdgcn_ballot_w64(fast || dead[r] || (kbg & 0x0f0f0f0fu) != 0);
+            bad |= __builtin_amdgcn_ballot_w64(!(ps >= TD_PS_MIN)) & unseen[r] & live;
+            unseen[r] &= ~live;
+          }
+          redo |= bad;
+          lrow[r] += ps;
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) pout[jj] = pk[jj];
+        }
+      }
+    };
+
+    for (int T = 0; T < nT; ++T) {
+      const int bn = bt == TA_NB - 1 ? 0 : bt + 1;
+      const int bp = bn == TA_NB - 1 ? 0 : bn + 1;     // (T + 2) mod 3 = (T - 1) mod 3
+      uint64_t kw[R];
+      bool fast;
+      if (all_full) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) kw[r] = ~0ull;
+        fast = true;
+      } else {
+        uint64_t kall = ~0ull;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          kw[r] = keep_word(cur, r, T);
+          kall &= kw[r];
+        }
+        fast = kall == ~0ull && !dead_any;
+      }
+      tile(fast, T, bp, bn, kw);
+      bt = bn;
+    }
+
+    // ---- item end: the last step's P.V (row R - 1 of the last sub-tile, with P0 and the V^T fragments the last step read
+    // ahead), the flag, and the normalised output through the wave's LDS staging rows as contiguous 16-byte stores
+    o[R - 1] = mfma32(as_bf8(fv0), as_bf8(u32x4{P0[0], P0[1], P0[2], P0[3]}), o[R - 1]);
+    o[R - 1] = mfma32(as_bf8(fv1), as_bf8(u32x4{P0[4], P0[5], P0[6], P0[7]}), o[R - 1]);
+    if (l == 0) p.redo[(size_t)w * NW + wave] = redo != 0;   // every wave writes its flag (no clearing needed)
+    if (!redo && NW == 4) {                                  // a flagged item is recomputed whole by the fallback kernel
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint64_t wv = sKeep[r][1 + T];
-        const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
-        const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);
-        kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
-        kall &= kw[r];
+        const int64_t i = cur.i0 + r;
+        if (i >= p.N || !cur.qlive) continue;
+        const float lt = half_sum(lrow[r]);
+        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+        uint16_t* op = p.out + cur.b * p.os[0] + i * p.os[1] + cur.h * p.os[2] + cur.q * p.os[3];
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int d0 = 8 * qd + 4 * g;
+          *reinterpret_cast<u32x2*>(op + d0) =
+              u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
+        }
       }
-      fast = kall == ~0ull && !dead_any;
+    } else if (!redo) {
+      uint16_t* so = &sO[wave][0];
+      const int64_t qbase = cur.q - n;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t i = cur.i0 + r;
+        if (i >= p.N) continue;
+        const float lt = half_sum(lrow[r]);
+        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+        rt_wave_lds_sync();                                 // the previous row's reads of the staging rows are done
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int d0 = 8 * qd + 4 * g;
+          *reinterpret_cast<u32x2*>(so + n * TA_OP + d0) =
+              u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
+        }
+        rt_wave_lds_sync();
+        uint16_t* ob = p.out + cur.b * p.os[0] + i * p.os[1] + cur.h * p.os[2];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int qq = 16 * half + (l >> 2), cc = 8 * (l & 3);            // lane: query qq, d cc .. cc + 7
+          const u32x4 v = *reinterpret_cast<const u32x4*>(so + qq * TA_OP + cc);
+          if (qbase + qq < p.S) *reinterpret_cast<u32x4*>(ob + (qbase + qq) * p.os[3] + cc) = v;
+        }
+      }
     }
-    tile(fast, T, bt, bp, bn, kw);
-    bt = bn;
+    cur = nxt;
+    item_of(w + 2 < w1 ? w + 2 : (w + 1 < w1 ? w + 1 : w), nxt);
   }
-  // the last step's P.V: row R - 1 of the last sub-tile, with P0 and the V^T fragments the last step read ahead
-  o[R - 1] = mfma32(as_bf8(fv0), as_bf8(u32x4{P0[0], P0[1], P0[2], P0[3]}), o[R - 1]);
-  o[R - 1] = mfma32(as_bf8(fv1), as_bf8(u32x4{P0[4], P0[5], P0[6], P0[7]}), o[R - 1]);
   vm_wait<0>();                                         // no DMA may land after the wave ends
-  // every wave writes its flag (no clearing needed); a flagged work item is recomputed whole by the fallback kernel
-  if (l == 0) p.redo[(size_t)w * NW + wave] = redo != 0;
-  if (!qlive || redo) return;
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int64_t i = i0 + r;
-    if (i >= p.N) continue;
-    const float lt = half_sum(lrow[r]);
-    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-    uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int d0 = 8 * qd + 4 * g;
-      *reinterpret_cast<u32x2*>(op + d0) = u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------- fallback core
@@ -507,7 +579,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   dma_tile(0, 0);
   bias_issue(0, bq[0]);
   bias_issue(32, bq[1]);
-  dma_tile(nT > 1 ? TA_KT : 0, 1);
+  if (nT > 1) dma_tile(TA_KT, 1);
   // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys, all of the row's mask loads in flight together
   // (overlapping the Q loads and the first tiles' transfers, issued above); a row with no kept key attends uniformly to
   // every key (its words become all ones)
@@ -706,7 +778,8 @@ int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64
 }
 
 // The caller has checked the layout: S a multiple of 64 up to 64 TA_MAXW, fp32 bias with 16-byte aligned rows, q / k / V^T
-// 16-byte aligned with strides in multiples of 8, scale 1, p.redo holding redo_words(B, N, H, S) words.  8 waves (256 queries)
+// 16-byte aligned with strides in multiples of 8, out rows of 32 contiguous, 16-byte aligned bf16 (out stride[3] = 32,
+// others multiples of 8), scale 1, p.redo holding redo_words(B, N, H, S) words.  8 waves (256 queries)
 // share each K / V^T tile where S fills whole 256-query tiles and the grid still has 8 or more workgroups per CU; 4 waves (128
 // queries) elsewhere.  The fallback runs on the same stream right after the fast kernel, over the same grid.
 int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen) {
@@ -714,8 +787,15 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   const bool wide = p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * (int64_t)num_cus();
   const int64_t total = wide ? rows_heads * (p.S / (32 * TA_DMA_WAVES)) : rows_heads * cdiv(p.S, 128);
   if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
-  const dim3 grid((unsigned)(cdiv(total, 8) * 8));
-  const dim3 redo_grid((unsigned)std::min<int64_t>(total, num_cus()));   // persistent: each workgroup scans its share of flags
+  // per-lane byte offsets from the scalar bases are 32-bit: q (query, d), bias (query), K (key row of a tile), V^T (d row)
+  const int64_t lim = 0x7fffffffLL;
+  if (p.qs[3] < 0 || p.bs[2] < 0 || p.ks[3] < 0 || p.vs[3] < 0 || (p.S - 1) * p.qs[3] * 2 + 64 > lim ||
+      (p.S - 1) * p.bs[2] * 4 + 512 > lim || TA_KT * p.ks[3] * 2 > lim || TA_D * p.vs[3] * 2 > lim)
+    return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v per-row offsets must fit 31 bits");
+  // persistent grids: one fast workgroup per CU walking a contiguous range of items (two per CU for the 4-wave split, whose
+  // LDS and registers fit twice); the fallback scans its share of the flags
+  const dim3 grid((unsigned)std::min<int64_t>(total, (wide ? 1 : 2) * (int64_t)num_cus()));
+  const dim3 redo_grid((unsigned)std::min<int64_t>(total, num_cus()));
   if (wide) {
     hipLaunchKernelGGL(triattn_core_bf16_pipe<TA_DMA_WAVES>, grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
     hipLaunchKernelGGL(triattn_core_bf16_redo<TA_DMA_WAVES>, redo_grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
