@@ -72,6 +72,22 @@ __device__ __forceinline__ uint64_t sload64(const uint64_t* a) {
   asm volatile("s_load_dwordx2 %0, %1, 0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(a) : "memory");
   return v;
 }
+// Fields of the CoreParams block of a kernel whose only argument it is (it starts the kernarg segment), reloaded through the
+// scalar cache where they are used, so that a loop running for the whole kernel holds none of them in registers.  Issue the
+// loads of one place with karg_issue, then pass every result through karg_wait before the first use.
+template <int OFF>
+__device__ __forceinline__ uint64_t karg_issue() {
+  uint64_t v;
+  asm volatile("s_load_dwordx2 %0, %1, %2" : "=s"(v) : "s"(__builtin_amdgcn_kernarg_segment_ptr()), "n"(OFF));
+  return v;
+}
+template <int K>
+__device__ __forceinline__ void karg_wait(uint64_t (&v)[K]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < K; ++i) asm volatile("" : "+s"(v[i]));
+}
+#define FPF_KARG(field) ::fpf::karg_issue<(int)offsetof(::fpf::CoreParams, field)>()
 // waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
 // through the statement so nothing reads them earlier
 template <int N>

@@ -75,15 +75,17 @@ __global__ void __launch_bounds__(256) triattn_keep_bits(const void* __restrict_
 // ---------------------------------------------------------------------------------------------------------------- core
 constexpr int TA_OP = 40;        // LDS pitch (bf16) of the per-wave output staging rows (80 B: 16-byte aligned, few conflicts)
 
-// One work item: TA_R pair rows x 32 NW queries x one (b, h), and the addresses its loads use.  K / V^T row bases and the
-// bias plane are wave-uniform (scalar registers); q (the lane's query) and boff (its bias row offset) are per lane.
+// One work item: TA_R pair rows x 32 NW queries x one (b, h), and the addresses its loads use.  The row-i0 bases of K, V^T
+// and q and the bias plane are wave-uniform (scalar registers; row r adds r times the row stride, rows past N read row i0);
+// q (the lane's query), qo and boff (its byte offsets in a q row and a bias plane) are per lane.
 struct PipeItem {
-  int64_t b, h, i0, q;
-  bool qlive;
-  const uint16_t* kb[TA_R];
-  const uint16_t* vb[TA_R];
+  const uint16_t* kb;
+  const uint16_t* vb;
+  const uint16_t* qb;
   const float* brow;
-  uint32_t boff;
+  int32_t b, h, i0, nrow;          // nrow: rows of the item below N (1 .. TA_R)
+  int32_t q;
+  uint32_t qo, boff;
 };
 
 // Persistent: a workgroup walks a contiguous range of work items (XCD x takes the x-th eighth of them, so one XCD works on one
@@ -108,6 +110,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   const uint32_t w0 = lo + (uint32_t)((uint64_t)(hi - lo) * j / nwg), w1 = lo + (uint32_t)((uint64_t)(hi - lo) * (j + 1) / nwg);
   if (w0 >= w1) return;
   const int nT = (int)(p.S / TA_KT);
+  const int32_t S = (int32_t)p.S, N = (int32_t)p.N;     // host-checked to fit 31 bits
   if (nT < 2) {                                    // a one-tile key range: every item goes to the fallback kernel
     for (uint32_t w = w0; w < w1; ++w)
       if (l == 0) p.redo[(size_t)w * NW + wave] = 1u;
@@ -122,32 +125,40 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
     voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
   }
+  // row r's byte offset from row i0, tile T's from tile 0 (32-bit: host-checked)
+  const uint32_t krow = (uint32_t)(p.ks[1] * 2), vrow = (uint32_t)(p.vs[1] * 2), qrow = (uint32_t)(p.qs[1] * 2);
+  const uint32_t ktile = (uint32_t)(TA_KT * p.ks[3] * 2);
+  auto row_at = [](const uint16_t* base, const PipeItem& it, int r, uint32_t stride) {
+    return reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) + (r < it.nrow ? r * stride : 0u));
+  };
   auto item_of = [&](uint32_t w, PipeItem& it) {
     const uint32_t qt = w % nq, rg = (w / nq) % nr, bh = w / (nq * nr);
-    it.b = bh / H;
-    it.h = bh % H;
-    it.i0 = (int64_t)rg * R;
-    it.q = (int64_t)qt * (32 * NW) + wave * 32 + n;
-    it.qlive = it.q < p.S;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t ii = it.i0 + r < p.N ? it.i0 + r : it.i0;         // rows past N read row i0 (never stored)
-      it.kb[r] = p.k + it.b * p.ks[0] + ii * p.ks[1] + it.h * p.ks[2];
-      it.vb[r] = p.v + it.b * p.vs[0] + ii * p.vs[1] + it.h * p.vs[2];
-    }
-    it.brow = static_cast<const float*>(p.bias) + it.b * p.bs[0] + it.h * p.bs[1];
-    it.boff = (uint32_t)(((it.qlive ? it.q : 0) * p.bs[2] + 4 * g) * 4);
+    it.b = (int32_t)(bh / H);
+    it.h = (int32_t)(bh % H);
+    it.i0 = (int32_t)(rg * R);
+    it.nrow = N - it.i0 < R ? N - it.i0 : R;
+    it.q = (int32_t)(qt * (32 * NW) + wave * 32 + n);
+    const int64_t qs = it.q < S ? it.q : 0;                            // queries past S read query 0 (never stored)
+    uint64_t a[17] = {FPF_KARG(k),     FPF_KARG(v),     FPF_KARG(q),     FPF_KARG(bias),  FPF_KARG(ks[0]), FPF_KARG(ks[1]),
+                      FPF_KARG(ks[2]), FPF_KARG(vs[0]), FPF_KARG(vs[1]), FPF_KARG(vs[2]), FPF_KARG(qs[0]), FPF_KARG(qs[1]),
+                      FPF_KARG(qs[2]), FPF_KARG(qs[3]), FPF_KARG(bs[0]), FPF_KARG(bs[1]), FPF_KARG(bs[2])};
+    karg_wait(a);
+    const int64_t b = it.b, h = it.h, i0 = it.i0;
+    it.kb = reinterpret_cast<const uint16_t*>(a[0]) + b * (int64_t)a[4] + i0 * (int64_t)a[5] + h * (int64_t)a[6];
+    it.vb = reinterpret_cast<const uint16_t*>(a[1]) + b * (int64_t)a[7] + i0 * (int64_t)a[8] + h * (int64_t)a[9];
+    it.qb = reinterpret_cast<const uint16_t*>(a[2]) + b * (int64_t)a[10] + i0 * (int64_t)a[11] + h * (int64_t)a[12];
+    it.brow = reinterpret_cast<const float*>(a[3]) + b * (int64_t)a[14] + h * (int64_t)a[15];
+    it.qo = (uint32_t)((qs * (int64_t)a[13] + 8 * g) * 2);
+    it.boff = (uint32_t)((qs * (int64_t)a[16] + 4 * g) * 4);
   };
-  // q of an item (the lane's query in each of the TA_R rows; rows past N and queries past S read row i0 / query 0, whose
-  // results are never stored): 2 operations per row
+  // q of an item (the lane's query in each of the TA_R rows; rows past N read row i0, whose results are never stored):
+  // 2 operations per row
   auto q_issue = [&](const PipeItem& it, u32x4 (&dst)[R][2]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t i = it.i0 + r < p.N ? it.i0 + r : it.i0;
-      const uint16_t* qp = p.q + it.b * p.qs[0] + i * p.qs[1] + it.h * p.qs[2];        // scalar row base
-      const uint32_t qo = (uint32_t)(((it.qlive ? it.q : 0) * p.qs[3] + 8 * g) * 2);  // the lane's query (32-bit: host-checked)
-      asm volatile("global_load_dwordx4 %0, %1, %2 offset:0" : "+v"(dst[r][0]) : "v"(qo), "s"(qp));
-      asm volatile("global_load_dwordx4 %0, %1, %2 offset:32" : "+v"(dst[r][1]) : "v"(qo), "s"(qp));
+      const uint16_t* qp = row_at(it.qb, it, r, qrow);
+      asm volatile("global_load_dwordx4 %0, %1, %2 offset:0" : "+v"(dst[r][0]) : "v"(it.qo), "s"(qp));
+      asm volatile("global_load_dwordx4 %0, %1, %2 offset:32" : "+v"(dst[r][1]) : "v"(it.qo), "s"(qp));
     }
   };
   // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
@@ -155,17 +166,20 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   const uint32_t kl0 = lds_addr(&sK[0][0][512 * wc]), vl0 = lds_addr(&sV[0][0][512 * wc]);
   constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
   const bool v_mover = NW > 4 && wave >= 4;
-  auto dma_tile = [&](const PipeItem& it, int64_t k0, int buf) {
+  auto dma_tile = [&](const PipeItem& it, int T, int buf) {
+    const uint32_t kt = (uint32_t)T * ktile, vt = (uint32_t)T * (TA_KT * 2);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (NW == 4 || !v_mover) lds_dma16_s(koff, it.kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * R + r) * TILE_B);
-      if (NW == 4 || v_mover) lds_dma16_s(voff, it.vb[r] + k0, vl0 + (uint32_t)(buf * R + r) * TILE_B);
+      if (NW == 4 || !v_mover)
+        lds_dma16_s(koff, row_at(it.kb, it, r, krow) + kt / 2, kl0 + (uint32_t)(buf * R + r) * TILE_B);
+      if (NW == 4 || v_mover)
+        lds_dma16_s(voff, row_at(it.vb, it, r, vrow) + vt / 2, vl0 + (uint32_t)(buf * R + r) * TILE_B);
     }
   };
   // The wait counts below (vm_wait4<0>, vm_wait4<DMA_OPS>) assume exactly DMA_OPS operations per dma_tile and 4 per
-  // bias_issue, every one issued unconditionally and in the order of the loop (the q loads of the next item come after the
-  // last counted wait of a tile and before the next tile's vmcnt(0)): a wait counting fewer operations than were issued after
-  // the load it guards would let that load land in registers already in use.
+  // bias_issue, every one issued unconditionally and in the order of the loop (the next item's q loads come after the last
+  // tile's last counted wait, and the item start waits for everything): a wait counting fewer operations than were issued
+  // after the load it guards would let that load land in registers already in use.
   constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * R;
   // bias of sub-tile keys k + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
   auto bias_issue = [&](const PipeItem& it, int64_t k, f32x4 (&dst)[4]) {
@@ -177,59 +191,60 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   };
   // row flags / keep words of an item's TA_R rows (no mask: every key kept), read through the scalar cache: a vector load
   // here would come with a compiler-placed vmcnt wait that drains the counted transfers in flight
+  const bool has_keep = p.keep != nullptr;
+  auto keep_row = [&](const PipeItem& it, int r) {
+    uint64_t a[1] = {FPF_KARG(keep)};
+    karg_wait(a);
+    return reinterpret_cast<const uint64_t*>(a[0]) + ((int64_t)it.b * N + it.i0 + r) * keep_words(S);
+  };
   auto row_flags = [&](const PipeItem& it, int r) -> uint32_t {
-    if (!p.keep || it.i0 + r >= p.N) return (uint32_t)(TK_ALIVE | TK_FULL);
-    return (uint32_t)sload64(p.keep + (it.b * p.N + it.i0 + r) * keep_words(p.S));
+    if (!has_keep || r >= it.nrow) return (uint32_t)(TK_ALIVE | TK_FULL);
+    return (uint32_t)sload64(keep_row(it, r));
   };
   auto keep_word = [&](const PipeItem& it, int r, int T) -> uint64_t {
-    if (!p.keep || it.i0 + r >= p.N) return ~0ull;
-    return sload64(p.keep + (it.b * p.N + it.i0 + r) * keep_words(p.S) + 1 + T);
+    if (!has_keep || r >= it.nrow) return ~0ull;
+    return sload64(keep_row(it, r) + 1 + T);
   };
 
   PipeItem cur, nxt;
   item_of(w0, cur);
   item_of(w0 + 1 < w1 ? w0 + 1 : w0, nxt);
   f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
-  u32x4 qn[R][2];                  // q of the next item (loaded one tile ahead)
+  u32x4 qf[R][2];                  // q of the item (the next item's is loaded in the last tile, after the last read of these)
 #pragma unroll
   for (int x = 0; x < 2; ++x)
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) bq[x][qd] = f32x4{};
 #pragma unroll
-  for (int r = 0; r < R; ++r) qn[r][0] = qn[r][1] = u32x4{0, 0, 0, 0};
-  q_issue(cur, qn);
+  for (int r = 0; r < R; ++r) qf[r][0] = qf[r][1] = u32x4{0, 0, 0, 0};
+  q_issue(cur, qf);
   dma_tile(cur, 0, 0);
   bias_issue(cur, 0, bq[0]);
   bias_issue(cur, 32, bq[1]);
-  dma_tile(cur, TA_KT, 1);
-  vm_wait<0>();
-#pragma unroll
-  for (int r = 0; r < R; ++r) asm volatile("" : "+v"(qn[r][0]), "+v"(qn[r][1]));
+  dma_tile(cur, 1, 1);
   __syncthreads();
 
   const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile 1 adds 32 keys
   const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
   const int vsw = (n >> 1) & 7;
-  bf16x8 qf[R][2];
   auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
     f32x16 bc;
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd)
 #pragma unroll
       for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
-    return mfma32(as_bf8(k1f), qf[r][1], mfma32(as_bf8(k0f), qf[r][0], bc));
+    return mfma32(as_bf8(k1f), as_bf8(qf[r][1]), mfma32(as_bf8(k0f), as_bf8(qf[r][0]), bc));
   };
-  // P of one step: bf16 pairs of exp2(s) and the sum of the bf16 values the P.V MFMA consumes
-  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8]) {
+  // P of one step: bf16 pairs of exp2(s), and the bf16 values the P.V MFMA consumes added to the row's two running sums
+  // (even pairs into a0, odd into a1, in order; the fallback kernel keeps the same order)
+  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8], float& a0, float& a1) {
 #pragma unroll
     for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
-    float ps0 = dot2_bf16(pk[0], 0.f), ps1 = dot2_bf16(pk[1], 0.f);
 #pragma unroll
-    for (int jj = 2; jj < 8; jj += 2) {
-      ps0 = dot2_bf16(pk[jj], ps0);
-      ps1 = dot2_bf16(pk[jj + 1], ps1);
+    for (int jj = 0; jj < 8; jj += 2) {
+      a0 = dot2_bf16(pk[jj], a0);
+      a1 = dot2_bf16(pk[jj + 1], a1);
     }
-    return ps0 + ps1;
   };
   // MFMA fragments of a step, read from LDS one step ahead: V^T of (row, sub-tile vsub of buffer vbuf), K of (row, sub-tile
   // ksub of buffer kbuf)
@@ -244,9 +259,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   };
 
   f32x16 o[R], s[R];
-  float lrow[R];
-  uint64_t unseen[R];              // queries (lanes) of row r that have met no kept key yet (a wave-uniform mask)
-  uint64_t redo = 0;               // queries whose softmax needs a reference other than 0 (the work item goes to the fallback)
+  float la[R][2];                  // running row sums (reference 0) of the lane's keys
   bool dead[R];
   bool dead_any = false, all_full = true;
   uint32_t P0[8], P1[8];
@@ -254,7 +267,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 
   for (uint32_t w = w0; w < w1; ++w) {
     const bool has_next = w + 1 < w1;
-    // ---- item start: state, flags, q, S^T of sub-tile 0 for rows 0 .. R - 2 (row R - 1's is issued by the first step)
+    // ---- item start: state, flags, q, S^T of sub-tile 0 for rows 0 .. R - 2 (row R - 1's is issued by the first step).
+    // The q loads (and every transfer before them) are in
+    vm_wait<0>();
+#pragma unroll
+    for (int r = 0; r < R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
     dead_any = false;
     all_full = true;
 #pragma unroll
@@ -264,12 +281,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       dead_any |= dead[r];
       all_full &= (f & TK_FULL) != 0;
       o[r] = f32x16{};
-      lrow[r] = 0.f;
-      unseen[r] = cur.i0 + r < p.N ? ~0ull : 0ull;
-      qf[r][0] = as_bf8(qn[r][0]);
-      qf[r][1] = as_bf8(qn[r][1]);
+      la[r][0] = la[r][1] = 0.f;
     }
-    redo = 0;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) P0[jj] = 0u;     // P of "step -1" is zero: the first step's P.V MFMAs add nothing
 #pragma unroll
@@ -291,9 +304,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           if (sub == 0 && r == 1) {
-            vm_wait4<0>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);      // bias 2T + 1 (the newest load) is in, and the next
-#pragma unroll                                                          // item's q loaded in the tile before
-            for (int rr = 0; rr < R; ++rr) asm volatile("" : "+v"(qn[rr][0]), "+v"(qn[rr][1]));
+            vm_wait4<0>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);      // bias 2T + 1 (the newest load) is in
             bias_issue(nb, kb2, bq[0]);                                  // bias 2T + 2
           }
           if (sub == 1 && r == 0) {
@@ -301,13 +312,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
             // last reads (step (0, 0)): its buffer takes tile T + 2 (of this item, or of the next)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            if (T + 2 < nT) dma_tile(cur, (int64_t)(T + 2) * TA_KT, bp);
-            else dma_tile(nxt, (int64_t)(T + 2 - nT) * TA_KT, bp);
+            if (T + 2 < nT) dma_tile(cur, T + 2, bp);
+            else dma_tile(nxt, T + 2 - nT, bp);
           }
           if (sub == 1 && r == 1) {
             vm_wait4<DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);  // bias 2T + 2 is in (tile T + 2 may be pending)
             bias_issue(nb, kb2 + 32, bq[1]);                               // bias 2T + 3
-            if (T == nT - 2 && has_next) q_issue(nxt, qn);                 // waited by the last tile's vmcnt(0)
+            // the next item's q: this item's last S^T (row R - 1, sub-tile 2 nT - 1) was issued by step (1, 0); the S^T
+            // that steps (1, 1) and (1, 2) of the last tile compute for the next item are recomputed at its start
+            if (T == nT - 1 && has_next) q_issue(nxt, qf);
           }
           // the previous step's row pr and the sub-tile nsub of the S^T its MFMAs compute (tile-relative: -1 = tile T - 1's
           // second sub-tile, 2 = tile T + 1's first); this step's fragments were read by the step before it
@@ -328,7 +341,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
             }
           }
           uint32_t pk[8];
-          float ps = expsum(sv, pk);
+          expsum(sv, pk, la[r][0], la[r][1]);
           o[pr] = mfma32(as_bf8(vf0), as_bf8(u32x4{pin[0], pin[1], pin[2], pin[3]}), o[pr]);
           o[pr] = mfma32(as_bf8(vf1), as_bf8(u32x4{pin[4], pin[5], pin[6], pin[7]}), o[pr]);
           s[pr] = qk(kf0, kf1, pr, (nsub & 1) ? bq[1] : bq[0]);
@@ -347,17 +360,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
           __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          // reference 0 is exact for this step unless a partial sum reached 2^64 (or is not finite), or a query's first
-          // sub-tile with a kept key sums below 2^-32 (every logit below about -32): such queries are marked for the fallback
-          uint64_t bad = __builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX));
-          if (unseen[r]) {
-            const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);
-            const uint64_t live = __builtin_amdgcn_ballot_w64(fast || dead[r] || (kbg & 0x0f0f0f0fu) != 0);
-            bad |= __builtin_amdgcn_ballot_w64(!(ps >= TD_PS_MIN)) & unseen[r] & live;
-            unseen[r] &= ~live;
-          }
-          redo |= bad;
-          lrow[r] += ps;
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) pout[jj] = pk[jj];
         }
@@ -387,18 +389,30 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     }
 
     // ---- item end: the last step's P.V (row R - 1 of the last sub-tile, with P0 and the V^T fragments the last step read
-    // ahead), the flag, and the normalised output through the wave's LDS staging rows as contiguous 16-byte stores
+    // ahead), the flag, and the normalised output through the wave's LDS staging rows as contiguous 16-byte stores.
+    // Reference 0 is exact for a query whose row sum lies in [2^-32, 2^64): no exp2 overflowed (every term is below the
+    // sum), and the largest term is at least 2^-45 (S <= 2^13 terms), so the terms that underflowed weigh below 2^-80 of
+    // it.  A query outside that range (or not finite) sends the work item to the fallback kernel.
     o[R - 1] = mfma32(as_bf8(fv0), as_bf8(u32x4{P0[0], P0[1], P0[2], P0[3]}), o[R - 1]);
     o[R - 1] = mfma32(as_bf8(fv1), as_bf8(u32x4{P0[4], P0[5], P0[6], P0[7]}), o[R - 1]);
-    if (l == 0) p.redo[(size_t)w * NW + wave] = redo != 0;   // every wave writes its flag (no clearing needed)
+    float lt[R];
+    bool redo = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      lt[r] = half_sum(la[r][0] + la[r][1]);
+      redo |= __builtin_amdgcn_ballot_w64(r < cur.nrow && cur.q < S && !(lt[r] >= TD_PS_MIN && lt[r] < TD_PS_MAX)) != 0;
+    }
+    uint64_t oa[6] = {FPF_KARG(redo), FPF_KARG(out), FPF_KARG(os[0]), FPF_KARG(os[1]), FPF_KARG(os[2]), FPF_KARG(os[3])};
+    karg_wait(oa);
+    // this item's output rows (row i0 of (b, h)); every wave writes its flag (no clearing needed)
+    uint16_t* const obase = reinterpret_cast<uint16_t*>(oa[1]) + cur.b * (int64_t)oa[2] + cur.i0 * (int64_t)oa[3] + cur.h * (int64_t)oa[4];
+    if (l == 0) reinterpret_cast<uint32_t*>(oa[0])[(size_t)w * NW + wave] = redo;
     if (!redo && NW == 4) {                                  // a flagged item is recomputed whole by the fallback kernel
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int64_t i = cur.i0 + r;
-        if (i >= p.N || !cur.qlive) continue;
-        const float lt = half_sum(lrow[r]);
-        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
-        uint16_t* op = p.out + cur.b * p.os[0] + i * p.os[1] + cur.h * p.os[2] + cur.q * p.os[3];
+        if (r >= cur.nrow || cur.q >= S) continue;
+        const float inv = lt[r] > 0.f ? 1.0f / lt[r] : 0.f;
+        uint16_t* op = obase + r * (int64_t)oa[3] + cur.q * (int64_t)oa[5];
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           const int d0 = 8 * qd + 4 * g;
@@ -408,13 +422,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       }
     } else if (!redo) {
       uint16_t* so = &sO[wave][0];
-      const int64_t qbase = cur.q - n;
+      const int64_t qbase = (int64_t)cur.q - n;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int64_t i = cur.i0 + r;
-        if (i >= p.N) continue;
-        const float lt = half_sum(lrow[r]);
-        const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+        if (r >= cur.nrow) continue;
+        const float inv = lt[r] > 0.f ? 1.0f / lt[r] : 0.f;
         rt_wave_lds_sync();                                 // the previous row's reads of the staging rows are done
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
@@ -423,12 +435,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
               u32x2{pack2(o[r][4 * qd] * inv, o[r][4 * qd + 1] * inv), pack2(o[r][4 * qd + 2] * inv, o[r][4 * qd + 3] * inv)};
         }
         rt_wave_lds_sync();
-        uint16_t* ob = p.out + cur.b * p.os[0] + i * p.os[1] + cur.h * p.os[2];
+        uint16_t* ob = obase + r * (int64_t)oa[3];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int qq = 16 * half + (l >> 2), cc = 8 * (l & 3);            // lane: query qq, d cc .. cc + 7
           const u32x4 v = *reinterpret_cast<const u32x4*>(so + qq * TA_OP + cc);
-          if (qbase + qq < p.S) *reinterpret_cast<u32x4*>(ob + (qbase + qq) * p.os[3] + cc) = v;
+          if (qbase + qq < S) *reinterpret_cast<u32x4*>(ob + (qbase + qq) * TA_D + cc) = v;   // out rows: 32 contiguous
         }
       }
     }
@@ -439,12 +451,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 }
 
 // ---------------------------------------------------------------------------------------------------------------- fallback core
-// The work items the fast kernel flagged (a query whose softmax needs a reference other than 0), recomputed whole with the
-// same operands and work split: the same MFMA / exp2 / bf16 / row-sum sequence per step, with a lazily moved per-query
-// reference max (log2 units) -- set on a query's first sub-tile with a kept key when that sub-tile's partial sum lies
-// outside [2^-32, 2^64), moved up by a later sub-tile's max when its partial sum reaches 2^64, O and l rescaled when it
-// moves.  One step per (row, 32-key sub-tile), the keep bits built in LDS from the mask, K / V^T tiles by DMA through the
-// same three-buffer ring.  Unflagged work items return at once (one flag read per wave of the item).
+// The work items the fast kernel flagged (a query whose reference-0 row sum lies outside [2^-32, 2^64)), recomputed whole
+// with the same operands and work split in two passes over the keys: the first repeats the fast kernel's row sums
+// (reference 0, the same MFMA / exp2 / bf16 / dot2 sequence) and takes each query's max; the second computes O and l with
+// reference 0 for the queries whose sum is in range -- the fast kernel's bits, whichever kernel finishes them -- and the
+// query's max for the others.  One step per (row, 32-key sub-tile), the keep bits built in LDS from the mask, K / V^T
+// tiles by DMA through the same three-buffer ring.  A workgroup reads the flags of 64 of its items at a time and skips
+// the unflagged ones.
 template <int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_redo(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][TA_R][TA_KT * TA_D];
@@ -535,20 +548,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     dst[3] = gload4_async<96>(boff, sb);
   };
 
-  f32x16 o[TA_R], s[TA_R];
-  float lrow[TA_R], mb[TA_R];
-  uint64_t unseen[TA_R];           // lanes whose `seen` is still false (a wave-uniform mask: the fast path tests it in scalar code)
-  bool seen[TA_R], sh[TA_R];       // seen: the row's first live sub-tile has set its reference (per lane, equal in l and
-                                   // l ^ 32; rows past N count as seen); sh: some lane of the row has a nonzero reference
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    o[r] = f32x16{};
-    lrow[r] = 0.f;
-    mb[r] = 0.f;
-    seen[r] = i0 + r >= p.N;
-    unseen[r] = seen[r] ? 0ull : ~0ull;
-    sh[r] = false;
-  }
   // fragment offsets (bf16 elements) inside a row's K / V^T tile
   const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile adds 32 keys
   const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
@@ -561,28 +560,20 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
     return mfma32(as_bf8(k1f), qf[r][1], mfma32(as_bf8(k0f), qf[r][0], bc));
   };
-  // P of one row step: bf16 pairs of exp2(s) and the sum of the bf16 values the P.V MFMA consumes
-  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8]) {
-    float ps0 = 0.f, ps1 = 0.f;
+  // P of one row step and the row's two running sums, in the fast kernel's order (even pairs into a0, odd into a1)
+  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8], float& a0, float& a1) {
 #pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
-      if (v & 2) ps1 = dot2_bf16(pk[v >> 1], ps1);
-      else ps0 = dot2_bf16(pk[v >> 1], ps0);
+    for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
+#pragma unroll
+    for (int jj = 0; jj < 8; jj += 2) {
+      a0 = dot2_bf16(pk[jj], a0);
+      a1 = dot2_bf16(pk[jj + 1], a1);
     }
-    return ps0 + ps1;
   };
 
   const int64_t nT = p.S / TA_KT;
-  f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
-  // issue order DMA(0), bias(0), bias(1), DMA(1): the loop's wait counts continue from it
-  dma_tile(0, 0);
-  bias_issue(0, bq[0]);
-  bias_issue(32, bq[1]);
-  if (nT > 1) dma_tile(TA_KT, 1);
-  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys, all of the row's mask loads in flight together
-  // (overlapping the Q loads and the first tiles' transfers, issued above); a row with no kept key attends uniformly to
-  // every key (its words become all ones)
+  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys; a row with no kept key attends uniformly to every
+  // key (its words become all ones)
   const int nw = (int)(p.S >> 6);
   if (wave < TA_R) {
     const int64_t i = i0 + wave;
@@ -634,8 +625,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     if (p.mask_f32) build(0.0f);
     else build((uint8_t)0);
   }
-  // the Q and mask loads complete here (and the older transfers with them: the counter retires in order); inside the key
-  // loop the only vector-memory operations are the counted ones
+  // the Q and mask loads complete here: inside the passes the only vector-memory operations are the counted ones
+  vm_wait<0>();
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
   __syncthreads();
@@ -646,114 +637,125 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     dead[r] = (i0 + r < p.N) && !sAlive[r];
     dead_any |= dead[r];
   }
-  vm_wait4<4 + DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);    // tile 0 and bias 0 are in (bias 1, tile 1 may be pending)
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-#pragma unroll
-  for (int r = 0; r < TA_R; ++r) {
-    const uint16_t* kt = &sK[0][r][0];
-    s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
-  }
 
-  int bt = 0;                      // buffer of tile T
-  for (int64_t T = 0; T < nT; ++T) {
-    const bool moreT = T + 1 < nT;
-    const int bn = bt == TA_NB - 1 ? 0 : bt + 1;      // buffer of tile T + 1
-    const int bf = bn == TA_NB - 1 ? 0 : bn + 1;      // buffer of tile T + 2: tile T - 1's, free once every wave is past it
-    const int64_t k0 = T * TA_KT;
-    bias_issue(moreT ? k0 + TA_KT : 0, bq[0]);         // sub-tile 2T + 2 (past the end: a valid re-read, the counts stay exact)
-    uint64_t kw[TA_R], kall = ~0ull, kany = 0;
+  f32x16 o[TA_R], s[TA_R];
+  float la[TA_R][2], mx[TA_R], ref[TA_R];
+  f32x4 bq[2][4];                  // bias of the even / odd sub-tiles
+#pragma unroll
+  for (int r = 0; r < TA_R; ++r) ref[r] = 0.f;
+  for (int pass = 0; pass < 2; ++pass) {
+    const bool stats = pass == 0;  // pass 0: row sums and maxima only; pass 1: O and l with the chosen references
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      const uint64_t wv = sKeepAll[r][T];                               // uniform: keep it in scalar registers
-      const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
-      const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);   // unsigned: no sign extension
-      kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
-      kall &= kw[r];
-      kany |= kw[r];
+      o[r] = f32x16{};
+      la[r][0] = la[r][1] = 0.f;
+      mx[r] = -INFINITY;
     }
-    const bool full = (kall == ~0ull) && !dead_any;
+    // issue order DMA(0), bias(0), bias(1), DMA(1) (a one-tile range re-reads tile 0: every operation is issued, so the
+    // counts stay exact)
+    dma_tile(0, 0);
+    bias_issue(0, bq[0]);
+    bias_issue(32, bq[1]);
+    dma_tile(nT > 1 ? TA_KT : 0, 1);
+    vm_wait4<4 + DMA_OPS>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);  // tile 0 and bias 0 are in (bias 1, tile 1 may be pending)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      if (sub == 0) {
-        vm_wait4<DMA_OPS + 4>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);   // bias 2T + 1 (tile T + 1, bias 2T + 2 may be pending)
-      } else {
-        bias_issue(moreT ? k0 + TA_KT + 32 : 32, bq[1]);                 // sub-tile 2T + 3
-        vm_wait4<4>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);             // bias 2T + 2 and tile T + 1 are in
-        __builtin_amdgcn_s_barrier();                                     // every wave's part of tile T + 1 is in, and every
-        asm volatile("" ::: "memory");                                    // wave is done with tile T - 1
-        dma_tile((T + 2 < nT ? T + 2 : nT - 1) * TA_KT, bf);
-      }
-      const bool live_sub = (uint32_t)(kany >> (32 * sub)) != 0;
-      const bool next = sub == 0 || moreT;                                // the next sub-tile exists
-      const uint16_t* knext = sub == 0 ? &sK[bt][0][32 * TA_D] : &sK[bn][0][0];
+    for (int r = 0; r < TA_R; ++r) {
+      const uint16_t* kt = &sK[0][r][0];
+      s[r] = qk(*reinterpret_cast<const u32x4*>(kt + kfo0), *reinterpret_cast<const u32x4*>(kt + kfo1), r, bq[0]);
+    }
+
+    int bt = 0;                    // buffer of tile T
+    for (int64_t T = 0; T < nT; ++T) {
+      const bool moreT = T + 1 < nT;
+      const int bn = bt == TA_NB - 1 ? 0 : bt + 1;      // buffer of tile T + 1
+      const int bf = bn == TA_NB - 1 ? 0 : bn + 1;      // buffer of tile T + 2: tile T - 1's, free once every wave is past it
+      const int64_t k0 = T * TA_KT;
+      bias_issue(moreT ? k0 + TA_KT : 0, bq[0]);         // sub-tile 2T + 2 (past the end: a valid re-read, the counts stay exact)
+      uint64_t kw[TA_R], kall = ~0ull, kany = 0;
 #pragma unroll
       for (int r = 0; r < TA_R; ++r) {
-        // fragment reads first: V^T of this step, K of the row's next S^T
-        const uint16_t* vt = &sV[bt][r][n * TA_KT];
-        const u32x4 vf0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + g) ^ vsw));
-        const u32x4 vf1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + 2 + g) ^ vsw));
-        const uint16_t* kt = knext + r * (TA_KT * TA_D);
-        u32x4 kf0 = u32x4{0, 0, 0, 0}, kf1 = u32x4{0, 0, 0, 0};
-        if (next) {
-          kf0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
-          kf1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
-        }
-        if (live_sub) {
-          if (!full) {
-            const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
+        const uint64_t wv = sKeepAll[r][T];                               // uniform: keep it in scalar registers
+        const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(wv >> 32));
+        const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)wv);   // unsigned: no sign extension
+        kw[r] = ((uint64_t)whi << 32) | (uint64_t)wlo;
+        kall &= kw[r];
+        kany |= kw[r];
+      }
+      const bool full = (kall == ~0ull) && !dead_any;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const float sv = dead[r] ? 0.f : s[r][v];
-              s[r][v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? sv : -INFINITY;
+      for (int sub = 0; sub < 2; ++sub) {
+        if (sub == 0) {
+          vm_wait4<DMA_OPS + 4>(bq[1][0], bq[1][1], bq[1][2], bq[1][3]);   // bias 2T + 1 (tile T + 1, bias 2T + 2 may be pending)
+        } else {
+          bias_issue(moreT ? k0 + TA_KT + 32 : 32, bq[1]);                 // sub-tile 2T + 3
+          vm_wait4<4>(bq[0][0], bq[0][1], bq[0][2], bq[0][3]);             // bias 2T + 2 and tile T + 1 are in
+          __builtin_amdgcn_s_barrier();                                     // every wave's part of tile T + 1 is in, and every
+          asm volatile("" ::: "memory");                                    // wave is done with tile T - 1
+          dma_tile((T + 2 < nT ? T + 2 : nT - 1) * TA_KT, bf);
+        }
+        const bool live_sub = (uint32_t)(kany >> (32 * sub)) != 0;
+        const bool next = sub == 0 || moreT;                                // the next sub-tile exists
+        const uint16_t* knext = sub == 0 ? &sK[bt][0][32 * TA_D] : &sK[bn][0][0];
+#pragma unroll
+        for (int r = 0; r < TA_R; ++r) {
+          // fragment reads first: V^T of this step, K of the row's next S^T
+          const uint16_t* vt = &sV[bt][r][n * TA_KT];
+          const u32x4 vf0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + g) ^ vsw));
+          const u32x4 vf1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + 2 + g) ^ vsw));
+          const uint16_t* kt = knext + r * (TA_KT * TA_D);
+          u32x4 kf0 = u32x4{0, 0, 0, 0}, kf1 = u32x4{0, 0, 0, 0};
+          if (next) {
+            kf0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
+            kf1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
+          }
+          if (live_sub) {          // a sub-tile with no kept key in any row adds exact zeros: skipped
+            if (!full) {
+              const uint32_t kbg = (uint32_t)(kw[r] >> (32 * sub)) >> (4 * g);   // bit c_row(v, g) - 4 g = 8 (v / 4) + v % 4
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const float sv = dead[r] ? 0.f : s[r][v];
+                s[r][v] = (kbg & (1u << (8 * (v >> 2) + (v & 3)))) ? sv : -INFINITY;
+              }
+            }
+            if (stats) {
+#pragma unroll
+              for (int v = 0; v < 16; ++v) mx[r] = fmaxf(mx[r], s[r][v]);
+            } else {
+#pragma unroll
+              for (int v = 0; v < 16; ++v) s[r][v] -= ref[r];     // ref +0: the values (and bits) are unchanged
+            }
+            uint32_t pk[8];
+            expsum(s[r], pk, la[r][0], la[r][1]);
+            if (!stats) {
+              o[r] = mfma32(as_bf8(vf0), as_bf8(u32x4{pk[0], pk[1], pk[2], pk[3]}), o[r]);
+              o[r] = mfma32(as_bf8(vf1), as_bf8(u32x4{pk[4], pk[5], pk[6], pk[7]}), o[r]);
             }
           }
-          if (sh[r]) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s[r][v] -= mb[r];
-          }
-          uint32_t pk[8];
-          float ps = expsum(s[r], pk);
-          if ((__builtin_amdgcn_ballot_w64(!(ps < TD_PS_MAX)) | unseen[r]) != 0) {
-            // set or move the reference of the queries that need it; the decision depends only on the sub-tile max over
-            // both key halves, so lanes l and l ^ 32 (one query) always agree
-            float m0 = s[r][0];
-#pragma unroll
-            for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, s[r][v]);
-            const float mt = half_max(m0);
-            const bool fin = mt > -INFINITY;
-            // the fast kernel's thresholds: a query's first sub-tile with a kept key takes its max as the reference when its
-            // partial sum is below 2^-32 or at or above 2^64; later sub-tiles move it when their partial sum reaches 2^64.  A
-            // row the fast kernel finished (no flag) gets the same reference, 0, and so the same bits from both kernels.
-            const bool out = !(ps >= TD_PS_MIN && ps < TD_PS_MAX);
-            const float shift = !seen[r] ? ((fin && out) ? mt : 0.f) : (!(ps < TD_PS_MAX) ? mt : 0.f);
-            const float alpha = seen[r] && shift != 0.f ? fast_exp2(-shift) : 1.0f;   // before the first live sub-tile o, l are 0
-            lrow[r] *= alpha;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[r][v] *= alpha;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) s[r][v] -= shift;
-            mb[r] += shift;
-            seen[r] = seen[r] || fin;
-            unseen[r] = __builtin_amdgcn_ballot_w64(!seen[r]);
-            sh[r] = __ballot(mb[r] != 0.f) != 0;
-            ps = expsum(s[r], pk);
-          }
-          lrow[r] += ps;
-          o[r] = mfma32(as_bf8(vf0), as_bf8(u32x4{pk[0], pk[1], pk[2], pk[3]}), o[r]);
-          o[r] = mfma32(as_bf8(vf1), as_bf8(u32x4{pk[4], pk[5], pk[6], pk[7]}), o[r]);
+          if (next) s[r] = qk(kf0, kf1, r, sub == 0 ? bq[1] : bq[0]);
         }
-        if (next) s[r] = qk(kf0, kf1, r, sub == 0 ? bq[1] : bq[0]);
+      }
+      bt = bn;
+    }
+    vm_wait<0>();                                       // no DMA may land after the pass ends
+    __syncthreads();                                    // every wave is done with the tiles before the next pass refills them
+    if (stats) {
+      // the fast kernel's test on the same sums: in range, reference 0; else the query's max (finite: a live row keeps a
+      // key, a dead row's logits are 0)
+#pragma unroll
+      for (int r = 0; r < TA_R; ++r) {
+        const float lt = half_sum(la[r][0] + la[r][1]);
+        const float m = half_max(mx[r]);
+        ref[r] = ((lt >= TD_PS_MIN && lt < TD_PS_MAX) || !(m > -INFINITY && m < INFINITY)) ? 0.f : m;
       }
     }
-    bt = bn;
   }
-  vm_wait<0>();                                         // no DMA may land after the item ends
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) {
     const int64_t i = i0 + r;
     if (i >= p.N || !qlive) continue;
-    const float lt = half_sum(lrow[r]);
+    const float lt = half_sum(la[r][0] + la[r][1]);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     uint16_t* op = p.out + b * p.os[0] + i * p.os[1] + h * p.os[2] + q * p.os[3];
 #pragma unroll
@@ -789,9 +791,11 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
   // per-lane byte offsets from the scalar bases are 32-bit: q (query, d), bias (query), K (key row of a tile), V^T (d row)
   const int64_t lim = 0x7fffffffLL;
-  if (p.qs[3] < 0 || p.bs[2] < 0 || p.ks[3] < 0 || p.vs[3] < 0 || (p.S - 1) * p.qs[3] * 2 + 64 > lim ||
-      (p.S - 1) * p.bs[2] * 4 + 512 > lim || TA_KT * p.ks[3] * 2 > lim || TA_D * p.vs[3] * 2 > lim)
-    return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v per-row offsets must fit 31 bits");
+  if (p.qs[3] < 0 || p.bs[2] < 0 || p.ks[3] < 0 || p.vs[3] < 0 || p.qs[1] < 0 || p.ks[1] < 0 || p.vs[1] < 0 ||
+      (p.S - 1) * p.qs[3] * 2 + 64 > lim || (p.S - 1) * p.bs[2] * 4 + 512 > lim || TA_KT * p.ks[3] * 2 > lim ||
+      TA_D * p.vs[3] * 2 > lim || (TA_R - 1) * std::max(p.qs[1], std::max(p.ks[1], p.vs[1])) * 2 > lim ||
+      p.B * p.N > lim || p.S > lim)
+    return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
   // persistent grids: one fast workgroup per CU walking a contiguous range of items (two per CU for the 4-wave split, whose
   // LDS and registers fit twice); the fallback scans its share of the flags
   const dim3 grid((unsigned)std::min<int64_t>(total, (wide ? 1 : 2) * (int64_t)num_cus()));
