@@ -66,6 +66,15 @@ template <int IMM>
 __device__ __forceinline__ void gload4_into(f32x4& v, uint32_t voff, const void* sbase) {
   asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "+v"(v) : "v"(voff), "s"(sbase), "n"(IMM));
 }
+// v_mfma_f32_32x32x16_bf16 into a new tuple (D and C distinct, no copy of C): the compiler's own selection copies C into
+// the accumulator when C stays live in other blocks.  Only a following MFMA accumulating onto the result may read it
+// next (the same instruction reading its exact D as C needs no wait states; nothing else reads it without the compiler
+// seeing an MFMA producer).
+__device__ __forceinline__ f32x16 mfma32_new(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  f32x16 d;
+  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
 // 8 bytes at a wave-uniform address through the scalar cache, waited for here (lgkmcnt also covers this wave's LDS reads)
 __device__ __forceinline__ uint64_t sload64(const uint64_t* a) {
   uint64_t v;

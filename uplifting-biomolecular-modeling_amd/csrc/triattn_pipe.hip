@@ -93,7 +93,8 @@ struct PipeItem {
 // double buffer run across item boundaries (the loads past an item's last tile fetch the next item's first tiles), the next
 // item's q is loaded during the item's second-to-last tile, and an item's output leaves through LDS as contiguous 16-byte
 // stores that drain while the next item computes.
-template <int NW>
+// MASKED: the call has a keep table (without one every key is kept and the kernel carries no mask code).
+template <int NW, bool MASKED>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_pipe(const CoreParams p) {
   constexpr int R = TA_R;
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][R][TA_KT * TA_D];
@@ -181,17 +182,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   // tile's last counted wait, and the item start waits for everything): a wait counting fewer operations than were issued
   // after the load it guards would let that load land in registers already in use.
   constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * R;
-  // bias of sub-tile keys k + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
+  // bias of sub-tile keys k + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations.  The previous value
+  // stays live up to here, so no S^T MFMA accumulates in place over it and its registers are free for the new tuple
   auto bias_issue = [&](const PipeItem& it, int64_t k, f32x4 (&dst)[4]) {
     const float* sb = it.brow + k;
-    gload4_into<0>(dst[0], it.boff, sb);
-    gload4_into<32>(dst[1], it.boff, sb);
-    gload4_into<64>(dst[2], it.boff, sb);
-    gload4_into<96>(dst[3], it.boff, sb);
+    asm volatile("" ::"v"(dst[0]), "v"(dst[1]), "v"(dst[2]), "v"(dst[3]));
+    dst[0] = gload4_async<0>(it.boff, sb);
+    dst[1] = gload4_async<32>(it.boff, sb);
+    dst[2] = gload4_async<64>(it.boff, sb);
+    dst[3] = gload4_async<96>(it.boff, sb);
   };
   // row flags / keep words of an item's TA_R rows (no mask: every key kept), read through the scalar cache: a vector load
   // here would come with a compiler-placed vmcnt wait that drains the counted transfers in flight
-  const bool has_keep = p.keep != nullptr;
+  const bool has_keep = MASKED && p.keep != nullptr;
   auto keep_row = [&](const PipeItem& it, int r) {
     uint64_t a[1] = {FPF_KARG(keep)};
     karg_wait(a);
@@ -222,24 +225,31 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   bias_issue(cur, 0, bq[0]);
   bias_issue(cur, 32, bq[1]);
   dma_tile(cur, 1, 1);
+  vm_wait<0>();                    // this wave's parts of tiles 0 and 1 are in; the barrier publishes every wave's
   __syncthreads();
 
   const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile 1 adds 32 keys
   const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
   const int vsw = (n >> 1) & 7;
+  // S^T of row r = bias + K q: the first MFMA writes a new tuple (the bias tuple serves all TA_R rows; the compiler would
+  // copy it into the accumulator instead), the second accumulates in place
   auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
     f32x16 bc;
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd)
 #pragma unroll
       for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
-    return mfma32(as_bf8(k1f), as_bf8(qf[r][1]), mfma32(as_bf8(k0f), as_bf8(qf[r][0]), bc));
+    return mfma32(as_bf8(k1f), as_bf8(qf[r][1]), mfma32_new(as_bf8(k0f), as_bf8(qf[r][0]), bc));
   };
   // P of one step: bf16 pairs of exp2(s), and the bf16 values the P.V MFMA consumes added to the row's two running sums
-  // (even pairs into a0, odd into a1, in order; the fallback kernel keeps the same order)
+  // (even pairs into a0, odd into a1, in order; the fallback kernel keeps the same order).  Every exp2 is issued before
+  // the first pack reads one (no transcendental-use wait state)
   auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8], float& a0, float& a1) {
+    float e[16];
 #pragma unroll
-    for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
+    for (int v = 0; v < 16; ++v) e[v] = fast_exp2(sv[v]);
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(e[v], e[v + 1]);
 #pragma unroll
     for (int jj = 0; jj < 8; jj += 2) {
       a0 = dot2_bf16(pk[jj], a0);
@@ -371,7 +381,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       const int bp = bn == TA_NB - 1 ? 0 : bn + 1;     // (T + 2) mod 3 = (T - 1) mod 3
       uint64_t kw[R];
       bool fast;
-      if (all_full) {
+      if (!MASKED || all_full) {
 #pragma unroll
         for (int r = 0; r < R; ++r) kw[r] = ~0ull;
         fast = true;
@@ -384,7 +394,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
         }
         fast = kall == ~0ull && !dead_any;
       }
-      tile(fast, T, bp, bn, kw);
+      if (MASKED) tile(fast, T, bp, bn, kw);
+      else tile(true, T, bp, bn, kw);
       bt = bn;
     }
 
@@ -801,10 +812,12 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   const dim3 grid((unsigned)std::min<int64_t>(total, (wide ? 1 : 2) * (int64_t)num_cus()));
   const dim3 redo_grid((unsigned)std::min<int64_t>(total, num_cus()));
   if (wide) {
-    hipLaunchKernelGGL(triattn_core_bf16_pipe<TA_DMA_WAVES>, grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+    if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, true>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+    else hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, false>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
     hipLaunchKernelGGL(triattn_core_bf16_redo<TA_DMA_WAVES>, redo_grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
   } else {
-    hipLaunchKernelGGL(triattn_core_bf16_pipe<4>, grid, dim3(256), 0, st, p);
+    if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<4, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((triattn_core_bf16_pipe<4, false>), grid, dim3(256), 0, st, p);
     hipLaunchKernelGGL(triattn_core_bf16_redo<4>, redo_grid, dim3(256), 0, st, p);
   }
   return launched(err, errlen, "triattn_core_bf16_pipe");
