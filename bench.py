@@ -183,7 +183,8 @@ def ln_args(x, y, w, b):
 
 def core_block_args(N, torch, dev, g):
     """Argument block of the triangle-attention core as the fused block launches it (v_layout 2: q already times scale *
-    log2(e), V^T [B, N, H, D, N] with the keys of each 16-key block in MFMA order, fp32 bias [B, H, N, N] in log2 units), with
+    log2(e), V^T [B, N, H, D, N] with the keys of each 16-key block in MFMA order, fp32 bias planes [B, H] of N x N in log2
+    units and 32 x 32 register-order blocks), with
     random contents and no mask (every key kept: the same all-kept tiles the block runs for a pair mask of ones, whose keep
     table flags every row full); plus the tensors it points at (kept alive by the caller)."""
     from fpf_hip import _lib as L
@@ -191,6 +192,8 @@ def core_block_args(N, torch, dev, g):
     q = (torch.randn(1, N, H, N, D, generator=g) / math.sqrt(D)).to(torch.bfloat16).to(dev)
     k = torch.randn(1, N, H, N, D, generator=g).to(torch.bfloat16).to(dev)
     vt = torch.randn(1, N, H, D, N, generator=g).to(torch.bfloat16).to(dev)
+    # fp32 bias planes in the core's 32 x 32 register-order blocks (csrc/triattn.h, bias_blk_off): random values, so only
+    # the shape and strides of a contiguous [1, H, N, N] tensor matter here
     bias = (torch.randn(1, H, N, N, generator=g) * 0.5).to(dev)
     out = torch.empty(1, N, H, N, D, dtype=torch.bfloat16, device=dev)
     ws = torch.empty(max(1, L.lib().fpf_triattn_workspace_bytes(1, N, H, N, 2)), dtype=torch.uint8, device=dev)

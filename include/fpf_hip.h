@@ -23,10 +23,12 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 6   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+#define FPF_ABI_VERSION 7   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
                                5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
                                6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
-                                  (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes) */
+                                  (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes);
+                               7: the v_layout 2 core's bias (and fpf_triattn_bias_fwd's output for such N) in 32 x 32
+                                  register-order blocks */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
 enum {
@@ -150,9 +152,12 @@ typedef struct {
   int64_t v_stride[5];     /* v_layout 0: strides of [B, N, H, S, D]; v_layout 1 / 2: strides of [B, N, H, D, S] (V stored transposed) */
   int32_t v_layout;        /* 0 | 1 | 2 (1, 2 bf16 only); the last stride must be 1.  2 is the fused block's internal layout: V^T
                               with the keys of every 16-key block stored in the order 0-3, 8-11, 4-7, 12-15, q already multiplied
-                              by scale * log2(e) (scale must be 1), fp32 bias times log2(e) with 16-byte aligned rows (logits in
-                              log2 units), S a multiple of 64 up to 8192 */
-  const void* bias;        /* [B, H, S, S] (the [B,1,H,S,S] operand without its unit axis) */
+                              by scale * log2(e) (scale must be 1), fp32 bias times log2(e) (logits in log2 units) in blocks (see
+                              bias), S a multiple of 64 up to 8192, out rows of 32 contiguous 16-byte aligned bf16 */
+  const void* bias;        /* [B, H, S, S] (the [B,1,H,S,S] operand without its unit axis).  v_layout 2: each (b, h) plane is
+                              S x S contiguous (bias_stride[2] = S, [3] = 1, 16-byte aligned) and holds 32 x 32 blocks (query
+                              block qb, key block kb) at element 1024 (qb S / 32 + kb), each block as 4 pieces (keys 8j .. 8j + 7)
+                              of 64 lanes (lane n + 32 g: query n, keys 8j + 4g .. 8j + 4g + 3) of 4 values */
   int32_t bias_dtype;      /* FPF_DT_F32 | FPF_DT_BF16 */
   int64_t bias_stride[4];  /* stride[3] must be 1 */
   const void* mask;        /* [B, N, S] or NULL, nonzero = attend */
@@ -228,8 +233,9 @@ typedef struct {
   const void* w_qkvg;      /* may be NULL (not read) */
   const void* w_b;         /* [H, C] */
   int32_t ending;
-  float* bias;             /* [B, H, N, N] fp32 out, in the units fpf_triattn_block_fwd's core takes: times log2(e) when N is
-                              a multiple of 64 up to 8192 (the v_layout 2 core), else as is */
+  float* bias;             /* [B, H, N, N] fp32 out, in the units and layout fpf_triattn_block_fwd's core takes: times log2(e)
+                              and in the v_layout 2 blocks when N is a multiple of 64 up to 8192 (the v_layout 2 core), else as
+                              is, row-major */
 } FpfTriattnBiasArgs;
 int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen);
 

@@ -289,6 +289,15 @@ def test_stages_fp32_exact():
 _VPERM = [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]      # stored position p of a 16-key block holds key _VPERM[p]
 
 
+def _bias_blocks(bias):
+    """[B, H, S, S] fp32 bias (query, key) -> the block-layout core's planes (csrc/triattn.h, bias_blk_off): 32 x 32 blocks
+    (query block, key block) in row-major block order, each as pieces j (keys 8j .. 8j+7) x lanes n + 32g (query n, keys
+    8j + 4g .. +3) x 4; returned with the shape and strides of a contiguous [B, H, S, S] tensor."""
+    B, H, S, _ = bias.shape
+    v = bias.reshape(B, H, S // 32, 32, S // 32, 4, 2, 4)                    # b, h, qt, n, kt, j, g, e
+    return v.permute(0, 1, 2, 4, 5, 6, 3, 7).contiguous().view(B, H, S, S)
+
+
 def _keep_table(mask):
     """The keep-bit table of the block-layout core (include/fpf_hip.h, FpfTriattnArgs.keep), built on the host from a [B, N, S]
     0/1 mask: per attention row, word 0 = flags (1 some key kept, 2 every key kept), word 1 + t = bits of keys 64 t .. 64 t + 63;
@@ -331,14 +340,15 @@ def test_block_layout_core_fallback_extreme_logits(N, masked):
         keep = _keep_table(mask)
     out = torch.full((1, N, H, N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
     ws = torch.empty(max(1, L.lib().fpf_triattn_workspace_bytes(1, N, H, N, 2)), dtype=torch.uint8, device=DEV)
+    bias_blk = _bias_blocks(bias)
     a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=1, N=N, H=H, S=N, D=D, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vt), v_layout=2,
-                      bias=L.ptr(bias), bias_dtype=L.DT_F32, mask=L.ptr(mask), mask_dtype=L.DT_F32, out=L.ptr(out), scale=1.0,
+                      bias=L.ptr(bias_blk), bias_dtype=L.DT_F32, mask=L.ptr(mask), mask_dtype=L.DT_F32, out=L.ptr(out), scale=1.0,
                       keep=None if keep is None else ctypes.c_void_p(keep.data_ptr()), workspace=L.ptr(ws), workspace_bytes=ws.numel())
     a.q_stride[:] = q.stride()
     a.k_stride[:] = k.stride()
     a.v_stride[:] = vt.stride()
     a.out_stride[:] = out.stride()
-    a.bias_stride[:] = bias.stride()
+    a.bias_stride[:] = bias_blk.stride()
     if masked:
         a.mask_stride[:] = mask.stride()
     print("[fallback] N=%d masked=%s" % (N, masked), flush=True)

@@ -46,6 +46,13 @@ __device__ __forceinline__ float bias_at(const CoreParams& p, int64_t off) {
   return p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[off]) : static_cast<const float*>(p.bias)[off];
 }
 
+// Bias plane of the block-layout core (v_layout 2): S x S fp32 (query q, key k) in 32 x 32 blocks, block (q / 32, k / 32) at
+// element ((q / 32) (S / 32) + k / 32) 1024, each block in the order one wave's S^T accumulator holds it -- piece j (keys
+// 8 j .. 8 j + 7) of 256 elements, lane n + 32 g (query n, keys 8 j + 4 g .. + 3) 4 elements each -- so a wave loads a
+// 32 x 32 sub-tile with four contiguous 1 KB reads.
+__host__ __device__ inline int64_t bias_blk_off(int64_t S, int64_t q, int64_t k) {
+  return (((q >> 5) * (S >> 5) + (k >> 5)) << 10) + (((k >> 3) & 3) << 8) + (((q & 31) + (((k >> 2) & 1) << 5)) << 2) + (k & 3);
+}
 constexpr int TA_NB = 3;                                 // K / V^T tile buffers of the block-layout core
 constexpr int TA_DMA_WAVES = 8;                          // waves (32 queries each) per workgroup of the block-layout core:
                                                          // 8 share each K / V^T tile among 256 queries (4 move K, 4 V^T)

@@ -412,7 +412,8 @@ constexpr int TP_C = 128, TP_HD = 128;
 // Outputs are selected by flags (PRO_QKV: q, k, v^T; PRO_G: g; PRO_BIAS: the full bias) and cover the attention rows
 // [row0, row0 + rows): q / k / v^T / g are indexed by the row within that range, the bias by the absolute row.  The `big`
 // chunked driver runs a bias-only pass over every row, then q / k / v^T per row chunk.
-enum { PRO_QKV = 1, PRO_G = 2, PRO_BIAS = 4, PRO_VPERM = 8 };  // VPERM: V^T keys in the core's 16-block order
+enum { PRO_QKV = 1, PRO_G = 2, PRO_BIAS = 4, PRO_VPERM = 8, PRO_BIAS_BLK = 16 };  // VPERM: V^T keys in the core's 16-block
+// order; BIAS_BLK: the bias planes in the block-layout core's 32 x 32 register-order blocks (bias_blk_off; fp32, N % 32 == 0)
 struct ProParams {
   const uint16_t* z;
   const float* ln_w;
@@ -502,11 +503,12 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
         *reinterpret_cast<u32x4*>(dst) = lo;
         *reinterpret_cast<u32x4*>(dst + 16) = hi;
       } else if (live) {                                  // bias: [B, H, I, bias_ld] fp32 | bf16, absolute row; head c_row(v, g)
+        const bool blk_bias = (p.flags & PRO_BIAS_BLK) != 0;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int hh = c_row(v, g);
           if (hh >= H) continue;
-          const int64_t o = ((b * H + hh) * N + i) * p.bias_ld + j;
+          const int64_t o = blk_bias ? (b * H + hh) * N * N + bias_blk_off(N, i, j) : ((b * H + hh) * N + i) * p.bias_ld + j;
           if (p.bias_bf16) reinterpret_cast<uint16_t*>(p.bias)[o] = f2bf(acc[v] * p.bias_scale);
           else p.bias[o] = acc[v] * p.bias_scale;
         }
@@ -855,6 +857,8 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     if (p.v_t == 2) {                  // the block layout (V^T keys permuted in 16-blocks, q times the scale): the DMA-staged core
       if (!p.bias_vec || p.S % TA_KT != 0 || p.S > 64 * TA_MAXW || p.vs[3] % 8 != 0)
         return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
+      if (p.bs[2] != p.S || p.bs[3] != 1)
+        return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 reads contiguous S x S bias planes in 32 x 32 register-order blocks (bias_stride[2] = S, [3] = 1)");
       if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
       if (p.mask && !a->keep)
         return fail(err, errlen, FPF_E_ARGS, "v_layout 2 reads the mask as a keep-bit table (keep); the fused block builds it");
@@ -965,6 +969,8 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
       return fail(err, errlen, FPF_E_ALIGN, "prologue operands must be 16-byte aligned");
     if ((flags & PRO_QKV) && (v_ld < cdiv(N, 32) * 32 || v_ld % 8))
       return fail(err, errlen, FPF_E_SHAPE, "v_ld %lld: V^T rows need N rounded up to 32", (long long)v_ld);
+    if ((flags & PRO_BIAS_BLK) && (N % 32 || bias_ld != N || bias_bf16))
+      return fail(err, errlen, FPF_E_SHAPE, "blocked bias: fp32, N a multiple of 32, contiguous planes");
     ProParams p{};
     p.z = (const uint16_t*)z;
     p.ln_w = ln_w;
@@ -1074,8 +1080,8 @@ extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, c
   if (rc) return rc;
   // the prologue kernel with only its bias output (the q|k|v|g weights are neither staged nor read)
   return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg ? a->w_qkvg : a->w_b, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending,
-                         nullptr, nullptr, nullptr, 0, nullptr, a->bias, static_cast<hipStream_t>(stream), err, errlen, PRO_BIAS, 0, -1, 1.0f,
-                         block_layout2(a->dtype, a->N) ? LOG2E : 1.0f);
+                         nullptr, nullptr, nullptr, 0, nullptr, a->bias, static_cast<hipStream_t>(stream), err, errlen,
+                         PRO_BIAS | (block_layout2(a->dtype, a->N) ? PRO_BIAS_BLK : 0), 0, -1, 1.0f, block_layout2(a->dtype, a->N) ? LOG2E : 1.0f);
 }
 
 extern "C" int fpf_apb_bias_fwd(const FpfApbBiasArgs* a, void* stream, char* err, size_t errlen) {
@@ -1174,7 +1180,7 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
     c.keep = keep;
   }
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
-  const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM : 0);
+  const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM | PRO_BIAS_BLK : 0);
   int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
                            bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f, -1, 0, a->b_g);
   if (rc) return rc;

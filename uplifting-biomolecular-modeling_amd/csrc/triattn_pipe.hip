@@ -5,30 +5,31 @@
 //
 // Operands (written by the block's prologue): q [B, N, H, S, 32] already times scale * log2(e), k [B, N, H, S, 32], V^T
 // [B, N, H, 32, S] with the keys of every 16-key block stored 0-3, 8-11, 4-7, 12-15 (the order in which the S^T MFMA's output
-// registers hold P), fp32 bias [B, H, S, S] times log2(e): logits are in log2 units throughout.
+// registers hold P), fp32 bias planes [B, H] of S x S times log2(e) in 32 x 32 register-order blocks (bias_blk_off):
+// logits are in log2 units throughout.
 //
-// Work split: a workgroup = TA_R pair rows x 32 NW queries x one (b, h); a wave = 32 queries of the TA_R rows (lane n = query,
-// lane group g = key half).  The TA_R rows share the bias tile (it does not depend on i): each wave loads its 32 x 32 fp32
-// bias sub-tile once into registers and starts all TA_R rows' S^T = K Q^T accumulators (v_mfma_f32_32x32x16_bf16) from it.
-// K and V^T tiles of 64 keys go global -> LDS by DMA (global_load_lds_dwordx4) through a ring of TA_NB buffers, in
-// XOR-swizzled 16-byte chunks (K: chunk c of key k at c ^ ((k >> 2) & 3); V^T: chunk c of row d at c ^ ((d >> 1) & 7)), so
-// every fragment read is a conflict-free 16-byte read; all TA_R rows' tiles are shared by the NW waves.
+// Work split: a work item = TA_R pair rows x 32 NW queries x one (b, h); a wave = 32 queries of the TA_R rows (lane n = query,
+// lane group g = key half).  The TA_R rows share the bias (it does not depend on i): each wave loads its 32 x 32 fp32 bias
+// sub-tile once into registers (four contiguous 1 KB reads) and starts all TA_R rows' S^T = K Q^T accumulators
+// (v_mfma_f32_32x32x16_bf16) from it.  K and V^T tiles of 64 keys go global -> LDS by DMA (global_load_lds_dwordx4) through
+// a ring of TA_NB buffers, in XOR-swizzled 16-byte chunks (K: chunk c of key k at c ^ ((k >> 2) & 3); V^T: chunk c of row d
+// at c ^ ((d >> 1) & 7)), so every fragment read is a conflict-free 16-byte read; all TA_R rows' tiles are shared by the NW
+// waves.  Workgroups are persistent and walk contiguous ranges of items (the next item's first tiles, bias and q are
+// fetched during the current item's last tiles).
 //
 // The step pipeline.  The key loop is a sequence of steps (t, r) over 32-key sub-tiles t and rows r.  Step (t, r) turns
-// the row's S^T sub-tile (already in registers) into P: p = exp2(s - m) rounded to bf16, and the partial row sum of those
-// bf16 values (v_dot2_f32_bf16).  In the same basic block it issues the MFMAs of the PREVIOUS step -- that row's O^T += V^T
-// P^T with the P computed one step earlier, and the same row's S^T of the next sub-tile -- so the matrix core works while the
-// wave computes exponentials (a wave issues in order: an MFMA right behind the exponentials it consumes would stall it).
-// The MFMAs and the softmax arithmetic are interleaved by sched_group_barrier.
+// the row's S^T sub-tile (already in registers) into P = exp2(s) rounded to bf16 and adds those bf16 values to the row's
+// running sums (v_dot2_f32_bf16).  In the same basic block it issues the MFMAs of the PREVIOUS step -- that row's O^T +=
+// V^T P^T with the P computed one step earlier, and the same row's S^T of the next sub-tile -- so the matrix core works
+// while the wave computes exponentials (a wave issues in order: an MFMA right behind the exponentials it consumes would
+// stall it).  The MFMAs and the softmax arithmetic are interleaved by sched_group_barrier.
 //
-// The reference max m of each query stays 0 while the logits are tame, so the common step has no max reduction and no
-// subtraction.  After each step one ballot checks the partial sum: at or above 2^64 (or not finite) the row's reference
-// moves up by the sub-tile's max, and a query without a reference (before its first live sub-tile) whose partial sum is
-// below 2^-32 (every logit below -32) takes that sub-tile's max; the check runs before the step's P.V is issued (one step
-// later), so the fix-up rescales O and l and recomputes P with nothing to undo.  Every value is relative to m, so its
-// choice costs no precision.  Tiles where every key of the TA_R rows is kept and no row is dead run a variant with no mask
-// code at all; the keep bits come from a table built once per call (triattn_keep_bits), so the key loop never reads the
-// mask.
+// The softmax reference (the max subtracted before exp2) is 0: exact whenever a query's row sum lies in [2^-32, 2^64),
+// which one test per query at the end of the item checks.  A work item with a query outside that range is recomputed by
+// the fallback kernel, which repeats the sums in a first pass and uses the query's max as the reference where they are
+// out of range (and 0 elsewhere, so both kernels produce the same bits for every other query).  Tiles where every key of
+// the TA_R rows is kept and no row is dead run with no mask code at all; the keep bits come from a table built once per
+// call (triattn_keep_bits), so the key loop never reads the mask.
 #include <algorithm>
 
 #include "triattn.h"
@@ -76,16 +77,16 @@ __global__ void __launch_bounds__(256) triattn_keep_bits(const void* __restrict_
 constexpr int TA_OP = 40;        // LDS pitch (bf16) of the per-wave output staging rows (80 B: 16-byte aligned, few conflicts)
 
 // One work item: TA_R pair rows x 32 NW queries x one (b, h), and the addresses its loads use.  The row-i0 bases of K, V^T
-// and q and the bias plane are wave-uniform (scalar registers; row r adds r times the row stride, rows past N read row i0);
-// q (the lane's query), qo and boff (its byte offsets in a q row and a bias plane) are per lane.
+// and q and the wave's row of bias blocks are wave-uniform (scalar registers; row r adds r times the row stride, rows past N
+// read row i0); q (the lane's query) and qo (its byte offset in a q row) are per lane.
 struct PipeItem {
   const uint16_t* kb;
   const uint16_t* vb;
   const uint16_t* qb;
-  const float* brow;
+  const float* brow;               // bias block (wave's 32 queries, keys 0 .. 31); key sub-tile s adds 1024 s
   int32_t b, h, i0, nrow;          // nrow: rows of the item below N (1 .. TA_R)
   int32_t q;
-  uint32_t qo, boff;
+  uint32_t qo;
 };
 
 // Persistent: a workgroup walks a contiguous range of work items (XCD x takes the x-th eighth of them, so one XCD works on one
@@ -140,17 +141,17 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     it.nrow = N - it.i0 < R ? N - it.i0 : R;
     it.q = (int32_t)(qt * (32 * NW) + wave * 32 + n);
     const int64_t qs = it.q < S ? it.q : 0;                            // queries past S read query 0 (never stored)
-    uint64_t a[17] = {FPF_KARG(k),     FPF_KARG(v),     FPF_KARG(q),     FPF_KARG(bias),  FPF_KARG(ks[0]), FPF_KARG(ks[1]),
+    uint64_t a[16] = {FPF_KARG(k),     FPF_KARG(v),     FPF_KARG(q),     FPF_KARG(bias),  FPF_KARG(ks[0]), FPF_KARG(ks[1]),
                       FPF_KARG(ks[2]), FPF_KARG(vs[0]), FPF_KARG(vs[1]), FPF_KARG(vs[2]), FPF_KARG(qs[0]), FPF_KARG(qs[1]),
-                      FPF_KARG(qs[2]), FPF_KARG(qs[3]), FPF_KARG(bs[0]), FPF_KARG(bs[1]), FPF_KARG(bs[2])};
+                      FPF_KARG(qs[2]), FPF_KARG(qs[3]), FPF_KARG(bs[0]), FPF_KARG(bs[1])};
     karg_wait(a);
     const int64_t b = it.b, h = it.h, i0 = it.i0;
     it.kb = reinterpret_cast<const uint16_t*>(a[0]) + b * (int64_t)a[4] + i0 * (int64_t)a[5] + h * (int64_t)a[6];
     it.vb = reinterpret_cast<const uint16_t*>(a[1]) + b * (int64_t)a[7] + i0 * (int64_t)a[8] + h * (int64_t)a[9];
     it.qb = reinterpret_cast<const uint16_t*>(a[2]) + b * (int64_t)a[10] + i0 * (int64_t)a[11] + h * (int64_t)a[12];
-    it.brow = reinterpret_cast<const float*>(a[3]) + b * (int64_t)a[14] + h * (int64_t)a[15];
+    const int64_t qw = (int64_t)(it.q - n) < S ? (it.q - n) >> 5 : 0;   // the wave's query block (a wave past S reads block 0)
+    it.brow = reinterpret_cast<const float*>(a[3]) + b * (int64_t)a[14] + h * (int64_t)a[15] + qw * (S >> 5) * 1024;
     it.qo = (uint32_t)((qs * (int64_t)a[13] + 8 * g) * 2);
-    it.boff = (uint32_t)((qs * (int64_t)a[16] + 4 * g) * 4);
   };
   // q of an item (the lane's query in each of the TA_R rows; rows past N read row i0, whose results are never stored):
   // 2 operations per row
@@ -182,15 +183,17 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   // tile's last counted wait, and the item start waits for everything): a wait counting fewer operations than were issued
   // after the load it guards would let that load land in registers already in use.
   constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * R;
-  // bias of sub-tile keys k + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations.  The previous value
-  // stays live up to here, so no S^T MFMA accumulates in place over it and its registers are free for the new tuple
+  // bias of the key sub-tile starting at k (keys k + 8 qd + 4 g + 0..3: D-layout rows of the S^T accumulator), four
+  // contiguous 1 KB reads of its register-order block.  The previous value stays live up to here, so no S^T MFMA
+  // accumulates in place over it and its registers are free for the new tuple
+  const uint32_t boff = (uint32_t)l * 16;
   auto bias_issue = [&](const PipeItem& it, int64_t k, f32x4 (&dst)[4]) {
-    const float* sb = it.brow + k;
+    const float* sb = it.brow + (k >> 5) * 1024;
     asm volatile("" ::"v"(dst[0]), "v"(dst[1]), "v"(dst[2]), "v"(dst[3]));
-    dst[0] = gload4_async<0>(it.boff, sb);
-    dst[1] = gload4_async<32>(it.boff, sb);
-    dst[2] = gload4_async<64>(it.boff, sb);
-    dst[3] = gload4_async<96>(it.boff, sb);
+    dst[0] = gload4_async<0>(boff, sb);
+    dst[1] = gload4_async<1024>(boff, sb);
+    dst[2] = gload4_async<2048>(boff, sb);
+    dst[3] = gload4_async<3072>(boff, sb);
   };
   // row flags / keep words of an item's TA_R rows (no mask: every key kept), read through the scalar cache: a vector load
   // here would come with a compiler-placed vmcnt wait that drains the counted transfers in flight
@@ -548,15 +551,17 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   // than were issued after the load it guards would let that load land in registers already reused.
   constexpr int DMA_OPS = (NW == 4 ? 2 : 1) * TA_R;
 
-  const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1];
-  const uint32_t boff = (uint32_t)(((qlive ? q : 0) * p.bs[2] + 4 * g) * 4);
-  // bias of sub-tile keys kb + 8 qd + 4 g + 0..3 (D-layout rows of the S^T accumulator): 4 operations
+  // the wave's row of register-order bias blocks (a wave past S reads block row 0, never stored)
+  const int64_t qw = q - n < p.S ? (q - n) >> 5 : 0;
+  const float* brow = static_cast<const float*>(p.bias) + b * p.bs[0] + h * p.bs[1] + qw * (p.S >> 5) * 1024;
+  const uint32_t boff = (uint32_t)l * 16;
+  // bias of the key sub-tile starting at kb (keys kb + 8 qd + 4 g + 0..3: D-layout rows of the S^T accumulator): 4 operations
   auto bias_issue = [&](int64_t kb, f32x4 (&dst)[4]) {
-    const float* sb = brow + kb;
+    const float* sb = brow + (kb >> 5) * 1024;
     dst[0] = gload4_async<0>(boff, sb);
-    dst[1] = gload4_async<32>(boff, sb);
-    dst[2] = gload4_async<64>(boff, sb);
-    dst[3] = gload4_async<96>(boff, sb);
+    dst[1] = gload4_async<1024>(boff, sb);
+    dst[2] = gload4_async<2048>(boff, sb);
+    dst[3] = gload4_async<3072>(boff, sb);
   };
 
   // fragment offsets (bf16 elements) inside a row's K / V^T tile
@@ -803,7 +808,7 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   // per-lane byte offsets from the scalar bases are 32-bit: q (query, d), bias (query), K (key row of a tile), V^T (d row)
   const int64_t lim = 0x7fffffffLL;
   if (p.qs[3] < 0 || p.bs[2] < 0 || p.ks[3] < 0 || p.vs[3] < 0 || p.qs[1] < 0 || p.ks[1] < 0 || p.vs[1] < 0 ||
-      (p.S - 1) * p.qs[3] * 2 + 64 > lim || (p.S - 1) * p.bs[2] * 4 + 512 > lim || TA_KT * p.ks[3] * 2 > lim ||
+      (p.S - 1) * p.qs[3] * 2 + 64 > lim || TA_KT * p.ks[3] * 2 > lim ||
       TA_D * p.vs[3] * 2 > lim || (TA_R - 1) * std::max(p.qs[1], std::max(p.ks[1], p.vs[1])) * 2 > lim ||
       p.B * p.N > lim || p.S > lim)
     return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
