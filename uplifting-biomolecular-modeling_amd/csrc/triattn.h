@@ -82,6 +82,23 @@ __device__ __forceinline__ f32x16 mfma32_new(const bf16x8& a, const bf16x8& b, c
   asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
 }
+// One softmax step of the block-layout core (both of its kernels, so they produce the same bits): exp2 of the 16 logits,
+// packed to the bf16 pairs the P.V MFMA consumes, and those bf16 values added to the row's two running sums (even pairs
+// into a0, odd into a1, in order; v_dot2_f32_bf16 against (1, 1)).  The sums hold exactly the weights O accumulates, so
+// each query's weights sum to 1 after the normalisation (summing the unrounded fp32 terms with v_add_f32 is cheaper
+// but measurably less accurate at block level).  Every exp2 is issued before the first pack reads one.
+__device__ __forceinline__ void softmax_step(const f32x16& sv, uint32_t (&pk)[8], float& a0, float& a1) {
+  float e[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) e[v] = fast_exp2(sv[v]);
+#pragma unroll
+  for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(e[v], e[v + 1]);
+#pragma unroll
+  for (int jj = 0; jj < 8; jj += 2) {
+    a0 = dot2_bf16(pk[jj], a0);
+    a1 = dot2_bf16(pk[jj + 1], a1);
+  }
+}
 // 8 bytes at a wave-uniform address through the scalar cache, waited for here (lgkmcnt also covers this wave's LDS reads)
 __device__ __forceinline__ uint64_t sload64(const uint64_t* a) {
   uint64_t v;

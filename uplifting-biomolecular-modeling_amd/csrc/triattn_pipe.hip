@@ -19,7 +19,7 @@
 //
 // The step pipeline.  The key loop is a sequence of steps (t, r) over 32-key sub-tiles t and rows r.  Step (t, r) turns
 // the row's S^T sub-tile (already in registers) into P = exp2(s) rounded to bf16 and adds those bf16 values to the row's
-// running sums (v_dot2_f32_bf16).  In the same basic block it issues the MFMAs of the PREVIOUS step -- that row's O^T +=
+// running sums (softmax_step).  In the same basic block it issues the MFMAs of the PREVIOUS step -- that row's O^T +=
 // V^T P^T with the P computed one step earlier, and the same row's S^T of the next sub-tile -- so the matrix core works
 // while the wave computes exponentials (a wave issues in order: an MFMA right behind the exponentials it consumes would
 // stall it).  The MFMAs and the softmax arithmetic are interleaved by sched_group_barrier.
@@ -244,21 +244,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
     return mfma32(as_bf8(k1f), as_bf8(qf[r][1]), mfma32_new(as_bf8(k0f), as_bf8(qf[r][0]), bc));
   };
-  // P of one step: bf16 pairs of exp2(s), and the bf16 values the P.V MFMA consumes added to the row's two running sums
-  // (even pairs into a0, odd into a1, in order; the fallback kernel keeps the same order).  Every exp2 is issued before
-  // the first pack reads one (no transcendental-use wait state)
-  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8], float& a0, float& a1) {
-    float e[16];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) e[v] = fast_exp2(sv[v]);
-#pragma unroll
-    for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(e[v], e[v + 1]);
-#pragma unroll
-    for (int jj = 0; jj < 8; jj += 2) {
-      a0 = dot2_bf16(pk[jj], a0);
-      a1 = dot2_bf16(pk[jj + 1], a1);
-    }
-  };
   // MFMA fragments of a step, read from LDS one step ahead: V^T of (row, sub-tile vsub of buffer vbuf), K of (row, sub-tile
   // ksub of buffer kbuf)
   u32x4 fv0, fv1, fk0, fk1;
@@ -354,7 +339,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
             }
           }
           uint32_t pk[8];
-          expsum(sv, pk, la[r][0], la[r][1]);
+          softmax_step(sv, pk, la[r][0], la[r][1]);
           o[pr] = mfma32(as_bf8(vf0), as_bf8(u32x4{pin[0], pin[1], pin[2], pin[3]}), o[pr]);
           o[pr] = mfma32(as_bf8(vf1), as_bf8(u32x4{pin[4], pin[5], pin[6], pin[7]}), o[pr]);
           s[pr] = qk(kf0, kf1, pr, (nsub & 1) ? bq[1] : bq[0]);
@@ -576,16 +561,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       for (int e = 0; e < 4; ++e) bc[4 * qd + e] = bb[qd][e];
     return mfma32(as_bf8(k1f), qf[r][1], mfma32(as_bf8(k0f), qf[r][0], bc));
   };
-  // P of one row step and the row's two running sums, in the fast kernel's order (even pairs into a0, odd into a1)
-  auto expsum = [&](const f32x16& sv, uint32_t (&pk)[8], float& a0, float& a1) {
-#pragma unroll
-    for (int v = 0; v < 16; v += 2) pk[v >> 1] = pack2(fast_exp2(sv[v]), fast_exp2(sv[v + 1]));
-#pragma unroll
-    for (int jj = 0; jj < 8; jj += 2) {
-      a0 = dot2_bf16(pk[jj], a0);
-      a1 = dot2_bf16(pk[jj + 1], a1);
-    }
-  };
 
   const int64_t nT = p.S / TA_KT;
   // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys; a row with no kept key attends uniformly to every
@@ -743,7 +718,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
               for (int v = 0; v < 16; ++v) s[r][v] -= ref[r];     // ref +0: the values (and bits) are unchanged
             }
             uint32_t pk[8];
-            expsum(s[r], pk, la[r][0], la[r][1]);
+            softmax_step(s[r], pk, la[r][0], la[r][1]);
             if (!stats) {
               o[r] = mfma32(as_bf8(vf0), as_bf8(u32x4{pk[0], pk[1], pk[2], pk[3]}), o[r]);
               o[r] = mfma32(as_bf8(vf1), as_bf8(u32x4{pk[4], pk[5], pk[6], pk[7]}), o[r]);
