@@ -2,7 +2,7 @@
 """bench.py -- one Pairformer pair block (the hot path) on one MI355X: ms, TFLOP/s and fraction of the bf16 MFMA roofline.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--n 768] [--no-cpu]
-    python bench.py --probe triattn_core|copy [--n 768] [--steps 5]     (launch-only runs for rocprofv3 --pmc passes)
+    python bench.py --probe triattn_core|trimul|transition|pair_block|copy [--n 768] [--steps 5]   (launch-only runs for rocprofv3)
 
 Step = one pair block on a resident z [1, N, N, 128] bf16, in place, in the reference order (trimul outgoing, trimul incoming,
 tri-att starting node, tri-att ending node, transition 4x): 13 launches of libfpf_hip on torch's current stream.  Synthetic
@@ -210,7 +210,9 @@ def core_block_args(N, torch, dev, g):
 
 def probe(kind, N, reps):
     """Launch-only runs for hardware-counter passes (rocprofv3 --pmc): `triattn_core` = the core at the block's shape, reps
-    times; `copy` = a device copy of a known byte count (the calibration kernel for FETCH_SIZE / WRITE_SIZE)."""
+    times; `trimul` = both triangle multiplications, `transition` = the transition, `pair_block` = whole blocks, on a
+    resident z, reps times; `copy` = a device copy of a known byte count (the calibration kernel for FETCH_SIZE /
+    WRITE_SIZE)."""
     import torch
     from fpf_hip.kernels import triattn as TA
     dev = torch.device("cuda:0")
@@ -221,13 +223,28 @@ def probe(kind, N, reps):
         a, keep = core_block_args(N, torch, dev, g)
         for _ in range(reps):
             L.call("fpf_triattn_fwd", a, L.stream_ptr(dev))
+    elif kind in ("trimul", "transition", "pair_block"):
+        from fpf_hip import pairformer as PFM
+        from fpf_hip.kernels import transition as TR
+        from fpf_hip.kernels import trimul as TM
+        blk = PFM.PairBlock(PFM.random_params(seed=0), dev, torch.bfloat16)
+        z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(dev)
+        mask = torch.ones(1, N, N, device=dev)
+        for _ in range(reps):
+            if kind == "trimul":
+                TM.triangle_multiplication(z, mask, direction="outgoing", weights=blk.tmo, word="fast", residual=True, cache=blk.cache_o, out=z)
+                TM.triangle_multiplication(z, mask, direction="incoming", weights=blk.tmi, word="fast", residual=True, cache=blk.cache_i, out=z)
+            elif kind == "transition":
+                TR.transition(z, blk.tr, word="fast", residual=True, out=z)
+            else:
+                PFM.pair_block(z, mask, blk)
     elif kind == "copy":
         x = torch.randn(N * N * 128, generator=g).to(torch.bfloat16).to(dev)
         y = torch.empty_like(x)
         for _ in range(reps):
             y.copy_(x)
     else:
-        raise SystemExit("unknown probe %r (triattn_core | copy)" % kind)
+        raise SystemExit("unknown probe %r (triattn_core | trimul | transition | pair_block | copy)" % kind)
     torch.cuda.synchronize()
     print("probe %s N=%d reps=%d done" % (kind, N, reps), flush=True)
 
@@ -268,7 +285,7 @@ def main():
     ap.add_argument("--trunk-layers", type=int, default=48, help="BASELINE config-3 trunk leg (0: skip)")
     ap.add_argument("--stack-layers", type=int, default=48, help="the north star's pair stack at N (0: skip)")
     ap.add_argument("--no-configs", action="store_true", help="skip the config-1 (tri-att N = 384) and config-4 (big, N = 2048) legs")
-    ap.add_argument("--probe", default=None, help="launch-only run for counter passes: triattn_core | copy")
+    ap.add_argument("--probe", default=None, help="launch-only run for counter passes: triattn_core | trimul | transition | pair_block | copy")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this build runs the pair stack on a single MI355X (multi-GPU row sharding is a design "
