@@ -23,12 +23,14 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 7   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+#define FPF_ABI_VERSION 8   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
                                5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
                                6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
                                   (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes);
                                7: the v_layout 2 core's bias (and fpf_triattn_bias_fwd's output for such N) in 32 x 32
-                                  register-order blocks */
+                                  register-order blocks;
+                               8: the trimul rows mode (FpfTrimulArgs.row0 / rows / fixed_in, fpf_trimul_fixed_fwd,
+                                  fpf_trimul_fixed_bytes, fpf_trimul_rows_workspace_bytes) */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
 enum {
@@ -122,9 +124,25 @@ typedef struct {
   float eps;
   void* workspace;
   size_t workspace_bytes;
+  /* The rows mode (bf16; common/opt_core/opt_core/mem/chunk.py:526 triangle_multiplication_chunked, mode "rows"): both
+     operand planes are computed whole once from the input z (fpf_trimul_fixed_fwd into a caller buffer), then each call
+     produces the output rows [row0, row0 + rows), holding only that row block's product plane
+     (fpf_trimul_rows_workspace_bytes) instead of the whole one.  The operands never see an updated row, so out may be z
+     (residual in place) in both directions, and every output element is the same arithmetic in the same order as in the
+     whole op: the rows bitwise equal the whole op's.  rows = 0, row0 = 0, fixed_in = NULL: the whole op. */
+  int64_t row0;
+  int64_t rows;
+  const void* fixed_in;    /* the A | B planes from fpf_trimul_fixed_fwd (same z, mask, weights, direction) */
 } FpfTrimulArgs;
 size_t fpf_trimul_workspace_bytes(int64_t batch, int64_t n, int32_t c_z, int32_t c_h, int32_t dtype);
 int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, size_t errlen);
+/* The rows mode's operands: the A and B planes of the whole op (K1; bf16, fpf_trimul_fixed_bytes bytes, 16-byte aligned) into
+   fixed_out; the workspace and row fields of `a` are not used.  No counterpart of its own in the reference (its rows mode
+   builds the fixed operand inside the chunked driver, mem/chunk.py:526). */
+size_t fpf_trimul_fixed_bytes(int64_t batch, int64_t n, int32_t c_h, int32_t dtype);
+int fpf_trimul_fixed_fwd(const FpfTrimulArgs* a, void* fixed_out, void* stream, char* err, size_t errlen);
+/* Workspace of a rows-mode call of `rows` rows: the product plane of the row block's cover by contraction tiles. */
+size_t fpf_trimul_rows_workspace_bytes(int64_t batch, int64_t n, int64_t rows, int32_t c_h, int32_t dtype);
 
 /* The same triangle multiplication without a caller workspace.  No counterpart in the reference: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The workspace

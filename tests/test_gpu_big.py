@@ -1,8 +1,10 @@
-"""The memory-lean `big` line (common/opt_core/opt_core/mem/chunk.py:424, the row-chunked triangle attention) on the GPU.
+"""The memory-lean `big` line (common/opt_core/opt_core/mem/chunk.py: row-chunked triangle attention :424, triangle
+multiplication in the rows mode :526, pair transition :370) on the GPU.
 
 Two bars:
   * chunked == whole-tensor, bit for bit: every attention row's arithmetic is independent of the others (per-lane running max,
-    per-row softmax, per-pixel projections), so the chunk size may not change one bit of the result;
+    per-row softmax, per-pixel projections), every trimul output row is the whole op's contraction over the whole shared axis,
+    the transition is per position: the chunk size may not change one bit of the result;
   * config 4 of the benchmark set (N = 2048, ragged mask of chains 900 + 700 + 300 and 148 padded positions, one pair block in
     `big` mode): equal to the `fast` line bitwise, and sampled rows of every site against the fp32 oracle restated per row.
 Byte offsets past 2^31 (N = 3072, a 2.4 GB pair tensor) are exercised on the per-pixel kernels (LayerNorm, transition).
@@ -110,6 +112,71 @@ def test_chunked_block_against_oracle():
         assert_bf16_close(u, ref, "chunked block ending=%s" % ending)
 
 
+# ------------------------------------------------------------------------------------------------ chunked trimul / transition
+def _asym_mask(B, N, keep_rows, seed):
+    """The ragged mask (the last N - keep_rows positions padded) times a random keep pattern: not symmetric, so a rows-mode
+    block that took the other operand's rows would show."""
+    g = torch.Generator().manual_seed(seed)
+    valid = torch.zeros(N)
+    valid[:keep_rows] = 1
+    return torch.outer(valid, valid).expand(B, N, N) * (torch.rand(B, N, N, generator=g) > 0.1).float()
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("B,N,chunk", [(1, 403, 256), (1, 403, 100), (1, 300, 64), (2, 130, 50)])
+def test_trimul_chunked_bitwise_equals_whole(direction, B, N, chunk):
+    """Rows mode (chunk.py:526): N = 403 pads to 512 planes (the 256-tile contraction; 100-row blocks straddle its tiles),
+    N = 300 to 384 (the 128-tile contraction; the last block holds 44 rows), batch 2.  Out of place, in place (out = z: the
+    incoming operand reads columns every later block would see updated) and the bare update, each equal to the whole op."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import trimul as TM
+    blk = PFM.PairBlock(PFM.random_params(seed=3), DEV, torch.bfloat16)
+    w = blk.tmo if direction == "outgoing" else blk.tmi
+    z = torch.randn(B, N, N, 128, generator=torch.Generator().manual_seed(N + chunk)).to(torch.bfloat16).to(DEV)
+    mask = _asym_mask(B, N, N - 3, N).to(DEV)
+    print("[big] trimul chunked %s B=%d N=%d chunk=%d" % (direction, B, N, chunk), flush=True)
+    for residual in (True, False):
+        whole = TM.triangle_multiplication(z, mask, direction=direction, weights=w, word="fast", residual=residual)
+        got = TM.triangle_multiplication_chunked(z, mask, direction=direction, weights=w, chunk=chunk, residual=residual)
+        torch.cuda.synchronize()
+        assert torch.equal(whole, got), "residual=%s: max diff %.3e" % (residual, (whole.float() - got.float()).abs().max().item())
+    z2 = z.clone()
+    TM.triangle_multiplication_chunked(z2, mask, direction=direction, weights=w, chunk=chunk, residual=True, out=z2)
+    torch.cuda.synchronize()
+    assert torch.equal(z2, TM.triangle_multiplication(z, mask, direction=direction, weights=w, word="fast", residual=True))
+
+
+def test_trimul_chunked_refusals():
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import trimul as TM
+    blk = PFM.PairBlock(PFM.random_params(seed=3), DEV, torch.bfloat16)
+    z = torch.randn(1, 64, 64, 128).to(torch.bfloat16).to(DEV)
+    with pytest.raises(TM.Refusal):
+        TM.triangle_multiplication_chunked(z, None, direction="outgoing", weights=blk.tmo, chunk=32, mode="channels")
+    with pytest.raises(TM.Refusal):
+        TM.triangle_multiplication_chunked(z, None, direction="outgoing", weights=blk.tmo, chunk=32, residual=False, out=z)
+    with pytest.raises(ValueError):
+        TM.triangle_multiplication_chunked(z, None, direction="outgoing", weights=blk.tmo, chunk=0)
+
+
+def test_transition_chunked_bitwise_equals_whole():
+    """Row blocks (chunk.py:370) of a batch-2 pair tensor with a per-position mask, out of place and in place."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import transition as TR
+    blk = PFM.PairBlock(PFM.random_params(seed=5), DEV, torch.bfloat16)
+    z = torch.randn(2, 130, 130, 128, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(DEV)
+    mask = _asym_mask(2, 130, 120, 8).to(DEV)
+    whole, _ = TR.transition(z, blk.tr, word="fast", residual=True, mask=mask)
+    got, sel = TR.pair_transition_chunked(z, blk.tr, chunk=50, residual=True, mask=mask)
+    torch.cuda.synchronize()
+    assert sel.row == "hip_gfx950"
+    assert torch.equal(whole, got)
+    z2 = z.clone()
+    TR.pair_transition_chunked(z2, blk.tr, chunk=33, residual=True, mask=mask, out=z2)
+    torch.cuda.synchronize()
+    assert torch.equal(whole, z2)
+
+
 def test_chunked_block_refuses_bad_chunk():
     from fpf_hip.attn import pair_fused as PF
     W = _ta_pack(_ta_weights(5))
@@ -170,9 +237,12 @@ def test_config4_trimul_sampled_rows(big_case, direction):
     params, blk, z, mask = big_case
     site = "tmo" if direction == "outgoing" else "tmi"
     w = blk.tmo if direction == "outgoing" else blk.tmi
-    print("[big] config4 trimul %s" % direction, flush=True)
-    u = TM.triangle_multiplication(z.to(DEV), mask.to(DEV), direction=direction, weights=w, word="big", residual=False)
+    print("[big] config4 trimul %s (rows mode, 256-row blocks)" % direction, flush=True)
+    u = TM.triangle_multiplication_chunked(z.to(DEV), mask.to(DEV), direction=direction, weights=w, chunk=256, word="big", residual=False)
+    whole = TM.triangle_multiplication(z.to(DEV), mask.to(DEV), direction=direction, weights=w, word="fast", residual=False)
     torch.cuda.synchronize()
+    assert torch.equal(u, whole), "chunked != whole: max diff %.3e" % (u.float() - whole.float()).abs().max().item()
+    del whole
     got = u[0, SAMPLE].cpu()
     wf = {k: (v.to(torch.bfloat16).float() if k.startswith("w_") else v) for k, v in params[site].items()}
     ref = S.trimul_rows(z[0].float(), mask[0], SAMPLE, direction=direction, weights=wf, dtype=torch.float32)

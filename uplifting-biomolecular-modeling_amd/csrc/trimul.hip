@@ -23,11 +23,14 @@ constexpr int TM_TILE = 128;         // contraction tile and plane padding
 // values form one contiguous 8 KB block, and the blocks of one column block follow each other row by row.  K1 writes a
 // 32-pixel tile as whole blocks and K3 reads one as 1 KB-contiguous loads; the contraction reads 64-byte runs of k along
 // rows 8 KB apart (TL_ROW) and steps one column block (TL_KBLK(Np)) per 32-wide k slab.
+// A plane of Rp rows (the rows mode's slices: Rp < Np rows, all Np columns) has the same layout with Rp rows per column
+// block: ((b (Np / 32) + Q / 32) Rp + P) 4096 + 32 c + Q % 32.
 constexpr int64_t TL_ROW = 4096;
-__device__ __forceinline__ int64_t tl_kblk(int64_t Np) { return Np * 4096; }
-__device__ __forceinline__ int64_t tl_off(int64_t b, int64_t c, int64_t P, int64_t Q, int64_t Np) {
-  return ((b * (Np >> 5) + (Q >> 5)) * Np + P) * 4096 + c * 32 + (Q & 31);
+__device__ __forceinline__ int64_t tl_kblk(int64_t Rp) { return Rp * 4096; }
+__host__ __device__ __forceinline__ int64_t tl_off_r(int64_t b, int64_t c, int64_t P, int64_t Q, int64_t Np, int64_t Rp) {
+  return ((b * (Np >> 5) + (Q >> 5)) * Rp + P) * 4096 + c * 32 + (Q & 31);
 }
+__device__ __forceinline__ int64_t tl_off(int64_t b, int64_t c, int64_t P, int64_t Q, int64_t Np) { return tl_off_r(b, c, P, Q, Np, Np); }
 
 // ---------------------------------------------------------------------------------------------------------------- K1 (bf16)
 // Persistent: the four [128 x 128] projection weights live in LDS (139 KB) for the workgroup's lifetime; each wave walks
@@ -121,14 +124,17 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
 constexpr int CT_BK = 64;
 constexpr int CT_LD = CT_BK + 8;     // 144-byte LDS rows: conflict-free 16-byte fragment reads
 
+// Rows a0 .. a0 + Ra - 1 of the A plane (whose layout holds La rows per column block: Np for the whole plane) against the
+// whole B plane, into an X plane of Ra rows (local row = plane row - a0); X rows at or past nrows (local) and columns at or
+// past N are not written.  The whole op: La = Ra = Np, a0 = 0.
 __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X,
-                                                            int64_t Np, int64_t N, int64_t nbatch) {
+                                                            int64_t Np, int64_t N, int64_t nbatch, int64_t La, int64_t a0, int64_t Ra, int64_t nrows) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[TM_TILE * CT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t sB[TM_TILE * CT_LD];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
   // XCD-aware order: the hardware deals workgroups round-robin over 8 XCDs; give each XCD a contiguous run of (plane, tile)
   // work so the 36-ish tiles of one plane share that XCD's L2.
-  const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE);
+  const int64_t tiles = (Ra / TM_TILE) * (Np / TM_TILE);
   const int64_t total = tiles * nbatch;
   const int64_t L = blockIdx.x;
   const int64_t per = (total + 7) / 8;
@@ -136,9 +142,9 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
   if (w >= total) return;
   const int64_t bc = w / tiles, t = w % tiles;
   const int64_t ti = t / (Np / TM_TILE), tj = t % (Np / TM_TILE);
-  const int64_t pb_ = bc / TM_C, pc = bc % TM_C, rstride = TL_ROW, kstride = tl_kblk(Np);   // tiled planes
-  const uint16_t* a0 = A + tl_off(pb_, pc, ti * TM_TILE, 0, Np);
-  const uint16_t* b0 = Bm + tl_off(pb_, pc, tj * TM_TILE, 0, Np);
+  const int64_t pb_ = bc / TM_C, pc = bc % TM_C, rstride = TL_ROW, kstride_a = tl_kblk(La), kstride_b = tl_kblk(Np);   // tiled planes
+  const uint16_t* ap = A + tl_off_r(pb_, pc, a0 + ti * TM_TILE, 0, Np, La);
+  const uint16_t* bp = Bm + tl_off(pb_, pc, tj * TM_TILE, 0, Np);
   const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;     // the wave's 64 x 64 sub-tile
   f32x16 acc[2][2] = {};
   // global -> register prefetch: 128 rows x 64 k = 1024 16-byte chunks per operand, 4 per thread
@@ -147,9 +153,9 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int i = tid + 256 * it, r = i >> 3, ch = i & 7;
-      const int64_t kk = k0 + ch * 8, o = r * rstride + (kk >> 5) * kstride + (kk & 31);
-      ra[it] = *reinterpret_cast<const u32x4*>(a0 + o);
-      rb[it] = *reinterpret_cast<const u32x4*>(b0 + o);
+      const int64_t kk = k0 + ch * 8, o = r * rstride + (kk & 31);
+      ra[it] = *reinterpret_cast<const u32x4*>(ap + o + (kk >> 5) * kstride_a);
+      rb[it] = *reinterpret_cast<const u32x4*>(bp + o + (kk >> 5) * kstride_b);
     }
   };
   gload(0);
@@ -186,7 +192,7 @@ __global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __re
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t i = ti * TM_TILE + wr + 32 * si + c_row(v, g);
-        if (i < N && j < N) X[tl_off(pb_, pc, i, j, Np)] = f2bf(acc[si][sj][v]);
+        if (i < nrows && j < N) X[tl_off_r(pb_, pc, i, j, Np, Ra)] = f2bf(acc[si][sj][v]);
       }
     }
 }
@@ -220,17 +226,18 @@ __device__ __forceinline__ void cb_wait(int p, bool stores) {
 }
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t nbatch) {
+trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t nbatch,
+                         int64_t La, int64_t a0, int64_t Ra) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[CB_NBUF][CB_T * CB_K];
   __shared__ __attribute__((aligned(16))) uint16_t sB[CB_NBUF][CB_T * CB_K];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t tpd = Np / CB_T, tiles = tpd * tpd, total = tiles * nbatch;
+  const int64_t tpd = Np / CB_T, tiles = (Ra / CB_T) * tpd, total = tiles * nbatch;   // A rows a0 .. a0 + Ra - 1, B whole
   const int64_t per = (total + 7) / 8, g8 = gridDim.x / 8;     // the host launches a multiple of 8 workgroups
   const int64_t x0 = (blockIdx.x % 8) * per, first = x0 + blockIdx.x / 8, end = total < x0 + per ? total : x0 + per;
   if (first >= end) return;
   const int ntile = (int)((end - first + g8 - 1) / g8);       // tiles first, first + g8, ... below end
   const int nk = (int)(Np / CB_K), U = ntile * nk;             // slabs per tile, slabs of this workgroup (host: U < 2^31)
-  const int64_t kstride = tl_kblk(Np);
+  const int64_t kstride_a = tl_kblk(La), kstride_b = tl_kblk(Np);
   auto tile_of = [&](int r, int64_t& bc, int64_t& ti, int64_t& tj) {
     const int64_t w = first + (int64_t)r * g8, t = w % tiles;
     bc = w / tiles;
@@ -251,16 +258,16 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   auto set_bases = [&](int r) {
     int64_t bc, ti, tj;
     tile_of(r, bc, ti, tj);
-    ia0 = A + tl_off(bc / TM_C, bc % TM_C, ti * CB_T, 0, Np);
+    ia0 = A + tl_off_r(bc / TM_C, bc % TM_C, a0 + ti * CB_T, 0, Np, La);
     ib0 = Bm + tl_off(bc / TM_C, bc % TM_C, tj * CB_T, 0, Np);
   };
   set_bases(0);
   auto issue_next = [&](int buf) {
-    const int64_t ko = (int64_t)ikt * kstride;
+    const int64_t koa = (int64_t)ikt * kstride_a, kob = (int64_t)ikt * kstride_b;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      lds_dma16(ia0 + goff[q] + ko, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
-      lds_dma16(ib0 + goff[q] + ko, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16(ia0 + goff[q] + koa, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16(ib0 + goff[q] + kob, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
     }
     if (++ikt == nk) {
       ikt = 0;
@@ -343,7 +350,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
       for (int sj = 0; sj < 4; ++sj) {
         u32x4 lo, hi;
         rt_pack16(acc[si][sj], lo, hi);
-        uint16_t* xp = X + tl_off(pb_, pc, ti * CB_T + wr + 32 * si, tj * CB_T + wc + 32 * sj, Np) + lane_el;
+        uint16_t* xp = X + tl_off_r(pb_, pc, ti * CB_T + wr + 32 * si, tj * CB_T + wc + 32 * sj, Np, Ra) + lane_el;
         *reinterpret_cast<u32x4*>(xp) = lo;
         *reinterpret_cast<u32x4*>(xp + 16) = hi;
         __builtin_amdgcn_sched_barrier(0);               // one accumulator at a time (bounded VGPR use)
@@ -352,6 +359,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
 }
 
 // ---------------------------------------------------------------------------------------------------------------- K3 (bf16)
+// Output rows i0 .. i0 + rows - 1 (the whole op: 0 .. N - 1), X read from a plane of Rx rows whose row 0 is plane row x0.
 // Persistent: W_o and W_og live in LDS (70 KB; with the per-wave X slots one workgroup of 8 waves per CU, so registers up
 // to 256 cost no occupancy).  Each wave scatters its X tile X[c][i][j0 .. j0+31] (channel-major, 128 rows of 64 B, loaded
 // during the previous tile) pixel-major into a private LDS slot, so the LN_out / B-operand reads are 16-byte rows, issues
@@ -363,7 +371,7 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
                                                       const float* __restrict__ ln_in_w, const float* __restrict__ ln_in_b,
                                                       const float* __restrict__ ln_out_w, const float* __restrict__ ln_out_b, float eps,
                                                       const uint16_t* __restrict__ w_o, const uint16_t* __restrict__ w_og,
-                                                      int64_t N, int64_t Np, int64_t B, int residual) {
+                                                      int64_t N, int64_t Np, int64_t B, int residual, int64_t i0, int64_t rows, int64_t x0, int64_t Rx) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[2 * RT_C * RT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t sX[RT_WAVES][32 * K3_XLD];
   __shared__ __attribute__((aligned(16))) float sLNo[2 * RT_C];
@@ -374,21 +382,21 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
   rt_stage_weights(sW, w_o, RT_C, RT_C, tid, 512);
   rt_stage_weights(sW + RT_C * RT_LD, w_og, RT_C, RT_C, tid, 512);
   __syncthreads();
-  const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)N * tpr, total = (uint32_t)B * per_b;
+  const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)rows * tpr, total = (uint32_t)B * per_b;
   const uint32_t stride = gridDim.x * RT_WAVES;
   uint16_t* sx = sX[wave];
   uint32_t t = blockIdx.x * RT_WAVES + wave;
   u32x4 rx[8], rz[8];
   auto fetch_x = [&](uint32_t tt) {                       // the tile's 8 KB X block (rows padded to Np: in bounds)
     const RtTile tl = rt_tile(tt, per_b, tpr);
-    const uint16_t* xs = X + tl_off(tl.b, 0, tl.r, tl.c * 32, Np);
+    const uint16_t* xs = X + tl_off_r(tl.b, 0, i0 + tl.r - x0, tl.c * 32, Np, Rx);
 #pragma unroll
     for (int it = 0; it < 8; ++it) rx[it] = *reinterpret_cast<const u32x4*>(xs + 8 * (l + 64 * it));   // channel q >> 2, chunk q & 3
   };
   if (t < total) fetch_x(t);
   for (; t < total; t += stride) {
     const RtTile tl = rt_tile(t, per_b, tpr);
-    const int64_t b = tl.b, i = tl.r, j = tl.c * 32 + n;
+    const int64_t b = tl.b, i = i0 + tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
     const int64_t pix = (b * N + i) * N + j;
     rt_load(zin + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
@@ -623,8 +631,86 @@ __global__ void __launch_bounds__(256) trimul_k3_f32(const float* zin, float* ou
 }
 
 static int64_t padded(int64_t n) { return cdiv(n, TM_TILE) * TM_TILE; }
+// The contraction tile of n (256 when the padded planes take the 256-tile kernel, else 128).
+static int64_t ctile(int64_t n) { return padded(n) % CB_T == 0 ? CB_T : TM_TILE; }
+
+// Contraction -> K3 of the bf16 path for output rows [row0, row0 + rows), from whole A and B planes: A rows a0 .. a0 + Ra - 1
+// (the tile-aligned cover of the row block) into an X plane of Ra rows.  The whole op is row0 = 0, rows = N, Ra = Np.
+static int bf16_rows(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* pa, const uint16_t* pb, uint16_t* X, int64_t row0, int64_t rows,
+                     char* err, size_t errlen) {
+  const int64_t N = a->n, Np = padded(N), B = a->batch, T = ctile(N);
+  const int64_t a0 = row0 / T * T, Ra = cdiv(row0 + rows, T) * T - a0;   // a0 + Ra <= Np: Np is a multiple of T
+  const int64_t k3_tiles = B * rows * cdiv(N, 32);
+  if (!rt_tiles_ok(k3_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
+  int rc;
+  if (T == CB_T) {
+    const int64_t tiles = (Ra / CB_T) * (Np / CB_T) * B * TM_C;
+    const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;    // persistent, a multiple of 8
+    if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
+    hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * TM_C, Np, a0, Ra);
+    rc = launched(err, errlen, "trimul_contract_bf16_256");
+  } else {
+    const int64_t tiles = (Ra / TM_TILE) * (Np / TM_TILE) * B * TM_C;
+    hipLaunchKernelGGL(trimul_contract_bf16, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, N, B * TM_C, Np, a0, Ra,
+                       std::min<int64_t>(Ra, N - a0));
+    rc = launched(err, errlen, "trimul_contract_bf16");
+  }
+  if (rc) return rc;
+  const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
+  hipLaunchKernelGGL(trimul_k3_bf16, dim3(k3_grid), dim3(512), 0, st, (const uint16_t*)a->z, (uint16_t*)a->out, X, a->ln_in_w, a->ln_in_b,
+                     a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np, B, a->residual, row0, rows, a0, Ra);
+  return launched(err, errlen, "trimul_k3_bf16");
+}
+
+// K1: both planes, whole (LN_in + four gated projections + mask), into pa / pb.
+static int bf16_planes(const FpfTrimulArgs* a, hipStream_t st, uint16_t* pa, uint16_t* pb, char* err, size_t errlen) {
+  const int64_t N = a->n, Np = padded(N), B = a->batch;
+  const int64_t k1_tiles = B * Np * (Np / 32);
+  if (!rt_tiles_ok(k1_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
+  const unsigned k1_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k1_tiles, RT_WAVES));
+  hipLaunchKernelGGL(trimul_k1_bf16, dim3(k1_grid), dim3(512), 0, st, (const uint16_t*)a->z, a->mask, a->ln_in_w, a->ln_in_b, a->eps,
+                     (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B,
+                     a->outgoing);
+  return launched(err, errlen, "trimul_k1_bf16");
+}
+
+static int bf16_checks(const FpfTrimulArgs* a, char* err, size_t errlen) {
+  if (a->c_z != TM_C || a->c_h != TM_C) return fail(err, errlen, FPF_E_SHAPE, "bf16 trimul serves c_z = c_h = 128 (got %d, %d)", a->c_z, a->c_h);
+  if (!aligned16(a->z) || !aligned16(a->out) || !aligned16(a->w_ag) || !aligned16(a->w_ap) || !aligned16(a->w_bg) || !aligned16(a->w_bp) ||
+      !aligned16(a->w_o) || !aligned16(a->w_og))
+    return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
+  return FPF_OK;
+}
 
 }  // namespace fpf
+
+extern "C" size_t fpf_trimul_fixed_bytes(int64_t batch, int64_t n, int32_t c_h, int32_t dtype) {
+  const int64_t Np = fpf::padded(n);
+  return dtype == FPF_DT_BF16 ? (size_t)2 * (size_t)batch * (size_t)c_h * (size_t)Np * (size_t)Np * 2 : 0;
+}
+
+extern "C" size_t fpf_trimul_rows_workspace_bytes(int64_t batch, int64_t n, int64_t rows, int32_t c_h, int32_t dtype) {
+  if (dtype != FPF_DT_BF16 || rows <= 0 || n <= 0) return 0;
+  // the X plane of a row block's tile-aligned cover: at most rows rounded up to the tile, plus one tile, capped at the plane
+  const int64_t Np = fpf::padded(n), T = fpf::ctile(n), Ra = std::min<int64_t>(fpf::cdiv(std::min(rows, n), T) * T + T, Np);
+  return (size_t)batch * (size_t)c_h * (size_t)Ra * (size_t)Np * 2;
+}
+
+extern "C" int fpf_trimul_fixed_fwd(const FpfTrimulArgs* a, void* fixed_out, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->z || !a->ln_in_w || !a->ln_in_b || !a->w_ag || !a->w_ap || !a->w_bg || !a->w_bp || !fixed_out)
+    return fail(err, errlen, FPF_E_ARGS, "z / ln_in / the four projection weights / fixed_out is NULL");
+  if (a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_DTYPE, "the rows mode serves the bf16 trimul");
+  if (a->batch <= 0 || a->n <= 0) return a->batch == 0 || a->n == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "batch / n negative");
+  if (a->batch > 65535) return fail(err, errlen, FPF_E_SHAPE, "batch above 65535");
+  if (a->c_z != TM_C || a->c_h != TM_C) return fail(err, errlen, FPF_E_SHAPE, "bf16 trimul serves c_z = c_h = 128 (got %d, %d)", a->c_z, a->c_h);
+  if (!aligned16(a->z) || !aligned16(fixed_out) || !aligned16(a->w_ag) || !aligned16(a->w_ap) || !aligned16(a->w_bg) || !aligned16(a->w_bp))
+    return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
+  const int64_t Np = padded(a->n);
+  uint16_t* pa = static_cast<uint16_t*>(fixed_out);
+  return bf16_planes(a, static_cast<hipStream_t>(stream), pa, pa + a->batch * TM_C * Np * Np, err, errlen);
+}
 
 extern "C" size_t fpf_trimul_workspace_bytes(int64_t batch, int64_t n, int32_t c_z, int32_t c_h, int32_t dtype) {
   (void)c_z;
@@ -640,44 +726,36 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
       !a->w_o || !a->w_og)
     return fail(err, errlen, FPF_E_ARGS, "a required pointer is NULL (z, out, the ten weights)");
   if (a->batch <= 0 || a->n <= 0) return a->batch == 0 || a->n == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "batch / n negative");
-  const size_t need = fpf_trimul_workspace_bytes(a->batch, a->n, a->c_z, a->c_h, a->dtype);
-  if (!a->workspace || a->workspace_bytes < need)
-    return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t N = a->n, Np = padded(N), B = a->batch;
   if (B > 65535) return fail(err, errlen, FPF_E_SHAPE, "batch above 65535");
+  if (a->rows != 0 || a->row0 != 0 || a->fixed_in) {    // rows mode: output rows [row0, row0 + rows) from the planes in fixed_in
+    if (a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_DTYPE, "the rows mode serves the bf16 trimul");
+    if (a->rows <= 0 || a->row0 < 0 || a->row0 + a->rows > N)
+      return fail(err, errlen, FPF_E_SHAPE, "rows [%lld, %lld) outside [0, %lld)", (long long)a->row0, (long long)(a->row0 + a->rows), (long long)N);
+    if (!a->fixed_in) return fail(err, errlen, FPF_E_ARGS, "the rows mode takes the A | B planes in fixed_in (fpf_trimul_fixed_fwd)");
+    int rc = bf16_checks(a, err, errlen);
+    if (rc) return rc;
+    const size_t need = fpf_trimul_rows_workspace_bytes(B, N, a->rows, a->c_h, a->dtype);
+    if (!a->workspace || a->workspace_bytes < need)
+      return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
+    if (!aligned16(a->workspace) || !aligned16(a->fixed_in)) return fail(err, errlen, FPF_E_ALIGN, "workspace / fixed_in must be 16-byte aligned");
+    const uint16_t* pa = static_cast<const uint16_t*>(a->fixed_in);
+    return bf16_rows(a, st, pa, pa + B * TM_C * Np * Np, static_cast<uint16_t*>(a->workspace), a->row0, a->rows, err, errlen);
+  }
+  const size_t need = fpf_trimul_workspace_bytes(a->batch, a->n, a->c_z, a->c_h, a->dtype);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
   if (a->dtype == FPF_DT_BF16) {
-    if (a->c_z != TM_C || a->c_h != TM_C) return fail(err, errlen, FPF_E_SHAPE, "bf16 trimul serves c_z = c_h = 128 (got %d, %d)", a->c_z, a->c_h);
-    if (!aligned16(a->z) || !aligned16(a->out) || !aligned16(a->workspace) || !aligned16(a->w_ag) || !aligned16(a->w_ap) ||
-        !aligned16(a->w_bg) || !aligned16(a->w_bp) || !aligned16(a->w_o) || !aligned16(a->w_og))
-      return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
+    int rc = bf16_checks(a, err, errlen);
+    if (rc) return rc;
+    if (!aligned16(a->workspace)) return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
     uint16_t* pa = static_cast<uint16_t*>(a->workspace);
     uint16_t* pb = pa + B * TM_C * Np * Np;
     uint16_t* X = pb + B * TM_C * Np * Np;
-    const int64_t k1_tiles = B * Np * (Np / 32), k3_tiles = B * N * cdiv(N, 32);
-    if (!rt_tiles_ok(k1_tiles) || !rt_tiles_ok(k3_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
-    const unsigned k1_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k1_tiles, RT_WAVES));
-    hipLaunchKernelGGL(trimul_k1_bf16, dim3(k1_grid), dim3(512), 0, st, (const uint16_t*)a->z, a->mask, a->ln_in_w, a->ln_in_b, a->eps,
-                       (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B,
-                       a->outgoing);
-    int rc = launched(err, errlen, "trimul_k1_bf16");
+    rc = bf16_planes(a, st, pa, pb, err, errlen);
     if (rc) return rc;
-    if (Np % CB_T == 0) {
-      const int64_t tiles = (Np / CB_T) * (Np / CB_T) * B * TM_C;
-      const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;    // persistent, a multiple of 8
-      if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
-      hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * TM_C);
-      rc = launched(err, errlen, "trimul_contract_bf16_256");
-    } else {
-      const int64_t tiles = (Np / TM_TILE) * (Np / TM_TILE) * B * TM_C;
-      hipLaunchKernelGGL(trimul_contract_bf16, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, N, B * TM_C);
-      rc = launched(err, errlen, "trimul_contract_bf16");
-    }
-    if (rc) return rc;
-    const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
-    hipLaunchKernelGGL(trimul_k3_bf16, dim3(k3_grid), dim3(512), 0, st, (const uint16_t*)a->z, (uint16_t*)a->out, X, a->ln_in_w, a->ln_in_b,
-                       a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np, B, a->residual);
-    return launched(err, errlen, "trimul_k3_bf16");
+    return bf16_rows(a, st, pa, pb, X, 0, N, err, errlen);
   }
   if (a->dtype == FPF_DT_F32) {
     if (a->c_z > F_CM || a->c_h > F_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 trimul serves c_z, c_h <= %d", F_CM);
@@ -736,6 +814,7 @@ extern "C" int fpf_trimul_fwd_noalloc(const FpfTrimulArgs* a, void* stream, char
   FPF_CHECK_VERSION(a);
   if (a->workspace || a->workspace_bytes)
     return fail(err, errlen, FPF_E_ARGS, "the no-allocation entry uses the library's static scratch: pass workspace NULL, workspace_bytes 0");
+  if (a->rows || a->row0 || a->fixed_in) return fail(err, errlen, FPF_E_ARGS, "the no-allocation entry runs the whole op (rows mode: fpf_trimul_fwd)");
   if (a->batch < 0 || a->n < 0) return fail(err, errlen, FPF_E_SHAPE, "batch / n negative");
   const size_t need = fpf_trimul_workspace_bytes(a->batch, a->n, a->c_z, a->c_h, a->dtype);
   if (need > (size_t)FPF_TRIMUL_NOALLOC_SCRATCH_BYTES)

@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 DT_BF16, DT_F32, DT_U8 = 1, 2, 3
 TRIMUL_NOALLOC_SCRATCH_BYTES = 50331648          # include/fpf_hip.h FPF_TRIMUL_NOALLOC_SCRATCH_BYTES
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
@@ -33,7 +33,7 @@ class TrimulArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("c_z", i32), ("c_h", i32), ("batch", i64), ("n", i64), ("z", vp), ("out", vp),
                 ("mask", vp), ("ln_in_w", vp), ("ln_in_b", vp), ("ln_out_w", vp), ("ln_out_b", vp), ("w_ag", vp), ("w_ap", vp),
                 ("w_bg", vp), ("w_bp", vp), ("w_o", vp), ("w_og", vp), ("outgoing", i32), ("residual", i32), ("eps", f32),
-                ("workspace", vp), ("workspace_bytes", sz)]
+                ("workspace", vp), ("workspace_bytes", sz), ("row0", i64), ("rows", i64), ("fixed_in", vp)]
 
 
 class TriattnArgs(C.Structure):
@@ -87,6 +87,9 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_trimul_workspace_bytes": ([i64, i64, i32, i32, i32], sz),
     "fpf_trimul_fwd": ([C.POINTER(TrimulArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_trimul_fwd_noalloc": ([C.POINTER(TrimulArgs), vp, C.c_char_p, sz], C.c_int),
+    "fpf_trimul_fixed_fwd": ([C.POINTER(TrimulArgs), vp, vp, C.c_char_p, sz], C.c_int),
+    "fpf_trimul_fixed_bytes": ([i64, i64, i32, i32], sz),
+    "fpf_trimul_rows_workspace_bytes": ([i64, i64, i64, i32, i32], sz),
     "fpf_triattn_fwd": ([C.POINTER(TriattnArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_workspace_bytes": ([i64, i64, i64, i32, i32, i32, i32], sz),
     "fpf_triattn_workspace_bytes": ([i64, i64, i64, i64, i32], sz),
@@ -153,13 +156,13 @@ def stream_ptr(device=None):
     return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
-def call(name, args, stream):
-    """Invoke an entry point; raise LibError on refusal."""
+def call(name, args, *rest):
+    """Invoke an entry point ``name(&args, *rest, err, errlen)`` (``rest`` ends with the stream); raise LibError on refusal."""
     err = C.create_string_buffer(512)
     fn = getattr(lib(), name, None)
     if fn is None:
         raise LibraryMissing("libfpf_hip.so does not export %s: rebuild" % name)
-    rc = fn(C.byref(args), stream, err, 512)
+    rc = fn(C.byref(args), *rest, err, 512)
     if rc != 0:
         raise LibError(name, rc, err.value.decode(errors="replace"))
 

@@ -122,3 +122,47 @@ def transition(x, W, *, word, residual=False, x_ln=None, mask=None, binary_mask=
                          w_o=L.ptr(wo), row_mask=L.ptr(m), residual=1 if residual else 0)
     L.call("fpf_transition_fwd", a, L.stream_ptr(x.device))
     return out, sel
+
+
+def pair_transition_chunked(x, W, *, chunk, row_dim=-3, word="big", residual=False, mask=None, out=None, fp32="passthrough", selection=None):
+    """Row-chunked pair transition (common/opt_core/opt_core/mem/chunk.py:370 ``pair_transition_chunked``): ``transition`` on
+    blocks of ``chunk`` rows of ``x [..., I, J, C]`` (``row_dim`` = the I axis, the only one served), one ``fpf_transition_fwd``
+    launch per block and leading index -> (y, Selection).  The statement is per position, so the result equals the unchunked
+    transition's bitwise; the kernel keeps the 4c hidden on chip, so a block bounds nothing but the launch extent (the
+    reference's blocks bound its [.., I, J, 4C] intermediates).  ``residual`` / ``out`` (x itself for in place) / ``mask`` (one
+    value per position, [..., I, J]) as in ``transition``.  An fp32 x runs unchunked for ``fp32`` = ``"passthrough"`` (the
+    reference's guard) or ``"band"`` (the unchunked result meets it) and is refused for ``"refuse"``."""
+    if str(fp32) not in ("passthrough", "band", "refuse"):
+        raise ValueError("fp32 must be passthrough | band | refuse (got %r)" % (fp32,))
+    chunk = int(chunk)
+    if chunk <= 0:
+        raise ValueError("chunk must be positive (got %d)" % chunk)
+    if x.dim() < 3:
+        raise Refusal("not_pair_shaped", F.word_base(word), F.ROW_STOCK, "x has rank %d, expected [..., I, J, C]" % x.dim())
+    if int(row_dim) not in (-3, x.dim() - 3):
+        raise Refusal("row_dim:%s" % row_dim, F.word_base(word), F.ROW_STOCK, "the row blocks run along the I axis (row_dim -3)")
+    sel = selection or select(word, c=int(x.shape[-1]), hidden=W.hidden, n_tokens=int(x.shape[-2]), dtype=x.dtype, cc=x, residual=residual,
+                              mask=mask is not None)
+    if sel.row != F.ROW_FAST:
+        if str(fp32) == "refuse":
+            raise Refusal("fp32_site", sel.row, F.ROW_STOCK, "an fp32 transition is not chunked (fp32='refuse')")
+        return transition(x, W, word=word, residual=residual, mask=mask, out=out, selection=sel)
+    if not x.is_contiguous():
+        raise Refusal("stride", sel.row, F.ROW_STOCK, "x must be contiguous")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+        raise Refusal("out", sel.row, F.ROW_STOCK, "out must be contiguous, x's shape and dtype")
+    I, J, C = (int(s) for s in x.shape[-3:])
+    x3, o3 = x.view(-1, I, J, C), out.view(-1, I, J, C)
+    m3 = None
+    if mask is not None:
+        if mask.numel() != x.numel() // C:
+            raise Refusal("mask_rows", sel.row, F.ROW_STOCK, "one mask value per position")
+        m3 = mask.reshape(-1, I, J)
+    for l in range(x3.shape[0]):
+        for i0 in range(0, I, chunk):
+            i1 = min(i0 + chunk, I)
+            transition(x3[l, i0:i1], W, word=word, residual=residual, mask=None if m3 is None else m3[l, i0:i1], out=o3[l, i0:i1],
+                       selection=sel)
+    return out, sel

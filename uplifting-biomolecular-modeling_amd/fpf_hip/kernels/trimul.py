@@ -142,11 +142,80 @@ def triangle_multiplication(z, mask=None, *, direction, weights, word=None, sele
     dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
     need = L.lib().fpf_trimul_workspace_bytes(B, N, Cz, Ch, dt)
     ws = F.scratch(z.device, need)
-    a = L.TrimulArgs(abi_version=L.ABI_VERSION, dtype=dt, c_z=Cz, c_h=Ch, batch=B, n=N, z=L.ptr(z4), out=L.ptr(out), mask=L.ptr(m),
-                     ln_in_w=L.ptr(p["ln_in_w"]), ln_in_b=L.ptr(p["ln_in_b"]), ln_out_w=L.ptr(p["ln_out_w"]), ln_out_b=L.ptr(p["ln_out_b"]),
-                     w_ag=L.ptr(p["w_ag"]), w_ap=L.ptr(p["w_ap"]), w_bg=L.ptr(p["w_bg"]), w_bp=L.ptr(p["w_bp"]), w_o=L.ptr(p["w_o"]),
-                     w_og=L.ptr(p["w_og"]), outgoing=1 if d == "outgoing" else 0, residual=1 if residual else 0, eps=float(eps),
-                     workspace=L.ptr(ws), workspace_bytes=ws.numel())
+    a = _args(z4, out, m, p, d, residual, eps, dt, Cz, Ch, ws)
     L.call("fpf_trimul_fwd", a, L.stream_ptr(z.device))
+    cache["_last"] = sel
+    return out
+
+
+def _args(z4, out, m, p, d, residual, eps, dt, Cz, Ch, ws):
+    B, N = int(z4.shape[0]), int(z4.shape[1])
+    return L.TrimulArgs(abi_version=L.ABI_VERSION, dtype=dt, c_z=Cz, c_h=Ch, batch=B, n=N, z=L.ptr(z4), out=L.ptr(out), mask=L.ptr(m),
+                        ln_in_w=L.ptr(p["ln_in_w"]), ln_in_b=L.ptr(p["ln_in_b"]), ln_out_w=L.ptr(p["ln_out_w"]), ln_out_b=L.ptr(p["ln_out_b"]),
+                        w_ag=L.ptr(p["w_ag"]), w_ap=L.ptr(p["w_ap"]), w_bg=L.ptr(p["w_bg"]), w_bp=L.ptr(p["w_bp"]), w_o=L.ptr(p["w_o"]),
+                        w_og=L.ptr(p["w_og"]), outgoing=1 if d == "outgoing" else 0, residual=1 if residual else 0, eps=float(eps),
+                        workspace=L.ptr(ws), workspace_bytes=0 if ws is None else ws.numel())
+
+
+def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, mode="rows", word="big", residual=False, out=None, cache=None,
+                                    eps=1e-5, fp32="passthrough", selection=None, prefer=None, residency=None):
+    """Row-chunked triangle multiplication (common/opt_core/opt_core/mem/chunk.py:526 ``triangle_multiplication_chunked``, mode
+    ``rows``): both operand planes are built whole once from z (``fpf_trimul_fixed_fwd``), then each block of ``chunk`` output
+    rows runs the contraction over the whole shared axis and the output stage for those rows only (``fpf_trimul_fwd`` in its
+    rows mode), so the product plane is held for one block instead of all N rows.  Every output element is the whole op's
+    arithmetic in the whole op's order: the result equals ``triangle_multiplication`` bitwise.  Since the operands are built
+    before any row is written, ``out`` may be z (``residual=True``) in both directions -- the reference's incoming free operand
+    reads z columns per block, which an in-place update of earlier blocks would change.
+
+    ``mode="channels"`` (the reference's channel-block operands with a full product) is refused by name: the whole-op kernels
+    already never hold a channel-split plane.  An fp32 call (row hip_gfx950_f32) runs the whole op when ``fp32`` is
+    ``"passthrough"`` or ``"band"`` (the result is the whole op's, which meets either label) and is refused for ``"refuse"``."""
+    if str(mode) != "rows":
+        raise Refusal("mode:%s" % mode, F.word_base(word), F.ROW_STOCK, "the chunked trimul serves mode rows")
+    if str(fp32) not in ("passthrough", "band", "refuse"):
+        raise ValueError("fp32 must be passthrough | band | refuse (got %r)" % (fp32,))
+    chunk = int(chunk)
+    if chunk <= 0:
+        raise ValueError("chunk must be positive (got %d)" % chunk)
+    cache = {} if cache is None else cache
+    z4 = z if z.dim() == 4 else z.unsqueeze(0)
+    B, N, N2, Cz = z4.shape
+    if N != N2:
+        raise ValueError("z must be [B,N,N,c] or [N,N,c] (got %s)" % (tuple(z.shape),))
+    d = direction_word(direction)
+    Ch = int(weights["w_ap"].shape[0])
+    sel = selection or select(z, z.dtype, Cz, Ch, N, d, word=word, residency=residency, prefer=prefer, batch=B)
+    if sel.row != F.ROW_FAST:
+        if str(fp32) == "refuse":
+            raise Refusal("fp32_site", sel.row, F.ROW_STOCK, "an fp32 trimul is not chunked (fp32='refuse')")
+        return triangle_multiplication(z, mask, direction=d, weights=weights, selection=sel, residual=residual, cache=cache, eps=eps, out=out)
+    if not z4.is_contiguous():
+        raise Refusal("stride", sel.row, F.ROW_STOCK, "z must be contiguous")
+    F.check_device("trimul", sel.row, z.device, out=out)
+    p = _pack(weights, z.dtype, z.device, cache)
+    m = None
+    if mask is not None:
+        m = mask if mask.dim() == 3 else mask.unsqueeze(0)
+        if tuple(m.shape) != (B, N, N):
+            raise Refusal("mask_shape", sel.row, F.ROW_STOCK, str(tuple(mask.shape)))
+        m = m.to(device=z.device, dtype=torch.float32).contiguous()
+    if out is None:
+        out = torch.empty_like(z)
+    elif out.shape != z.shape or out.dtype != z.dtype or not out.is_contiguous():
+        raise Refusal("out", sel.row, F.ROW_STOCK, "out must be contiguous with z's shape and dtype")
+    if out.data_ptr() == z.data_ptr() and not residual:
+        raise Refusal("out_aliases_z", sel.row, F.ROW_STOCK, "out may alias z only for the residual form")
+    if B * N == 0:
+        return out
+    lib, st = L.lib(), L.stream_ptr(z.device)
+    rows = min(chunk, N)
+    planes = F.scratch(z.device, lib.fpf_trimul_fixed_bytes(B, N, Ch, L.DT_BF16), kind="trimul_planes")
+    ws = F.scratch(z.device, lib.fpf_trimul_rows_workspace_bytes(B, N, rows, Ch, L.DT_BF16))
+    a = _args(z4, out, m, p, d, residual, eps, L.DT_BF16, Cz, Ch, None)
+    L.call("fpf_trimul_fixed_fwd", a, L.ptr(planes), st)
+    a.workspace, a.workspace_bytes, a.fixed_in = L.ptr(ws), ws.numel(), L.ptr(planes)
+    for r0 in range(0, N, rows):
+        a.row0, a.rows = r0, min(rows, N - r0)
+        L.call("fpf_trimul_fwd", a, st)
     cache["_last"] = sel
     return out

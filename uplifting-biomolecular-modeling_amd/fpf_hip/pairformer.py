@@ -52,19 +52,23 @@ class PairBlock(object):
 def pair_block(z, mask, blk, *, word="fast", rows=256):
     """z [B,N,N,C] (or [N,N,C]) updated in place by the five sites; returns z.  mask [B,N,N] / [N,N] (0/1) or None.
 
-    ``word="big"`` is the memory-lean line of common/opt_core/opt_core/mem/chunk.py (the `big` levers): the triangle-attention
-    blocks run row-chunked (``rows`` attention rows per launch; a bias pass over every pixel first), bitwise equal to the
-    whole-tensor blocks.  The transition needs no chunking here (its 4c hidden never leaves the chip, so there is no per-row
-    transient to bound) and triangle multiplication keeps its whole-plane contraction (3 c_h N^2 bf16 of workspace: 3.2 GB at
-    N = 2048, far inside one MI355X's 288 GB)."""
-    TM.triangle_multiplication(z, mask, direction="outgoing", weights=blk.tmo, word=word, residual=True, cache=blk.cache_o, out=z)
-    TM.triangle_multiplication(z, mask, direction="incoming", weights=blk.tmi, word=word, residual=True, cache=blk.cache_i, out=z)
+    ``word="big"`` is the memory-lean line of common/opt_core/opt_core/mem/chunk.py (the `big` levers), every site on blocks of
+    ``rows`` rows, each bitwise equal to its whole-tensor form: the triangle multiplications in the rows mode (operand planes
+    whole, the product plane for one row block: chunk.py:526), the triangle-attention blocks row-chunked after a bias pass over
+    every pixel (chunk.py:424) and the transition in row blocks (chunk.py:370; its 4c hidden never leaves the chip either way)."""
     if word == "big":
+        TM.triangle_multiplication_chunked(z, mask, direction="outgoing", weights=blk.tmo, chunk=rows, word=word, residual=True,
+                                           cache=blk.cache_o, out=z)
+        TM.triangle_multiplication_chunked(z, mask, direction="incoming", weights=blk.tmi, chunk=rows, word=word, residual=True,
+                                           cache=blk.cache_i, out=z)
         PF.tri_attn_block_chunked(z, blk.ta["tas"], mask, ending=False, residual=True, chunk=rows, word=word)
         PF.tri_attn_block_chunked(z, blk.ta["tae"], mask, ending=True, residual=True, chunk=rows, word=word)
-    else:
-        PF.tri_attn_block(z, blk.ta["tas"], mask, ending=False, residual=True, word=word)
-        PF.tri_attn_block(z, blk.ta["tae"], mask, ending=True, residual=True, word=word)
+        TR.pair_transition_chunked(z, blk.tr, chunk=rows, word=word, residual=True, out=z)
+        return z
+    TM.triangle_multiplication(z, mask, direction="outgoing", weights=blk.tmo, word=word, residual=True, cache=blk.cache_o, out=z)
+    TM.triangle_multiplication(z, mask, direction="incoming", weights=blk.tmi, word=word, residual=True, cache=blk.cache_i, out=z)
+    PF.tri_attn_block(z, blk.ta["tas"], mask, ending=False, residual=True, word=word)
+    PF.tri_attn_block(z, blk.ta["tae"], mask, ending=True, residual=True, word=word)
     TR.transition(z, blk.tr, word=word, residual=True, out=z)
     return z
 
