@@ -102,3 +102,22 @@ def test_transition_fp32_exact(rows):
     assert sel.row == "hip_gfx950_f32"
     ref = S.transition(x, wa, wb, wo, lw, lb, dtype=torch.float64)
     assert_f32_close(y, ref, "transition fp32")
+
+
+@pytest.mark.parametrize("affine", [True, False])
+def test_transition_fp32_exact_residual_mask(affine):
+    """The fp32 matrix-core kernel (c = 128) with the residual, a row mask of arbitrary values and with / without the
+    LayerNorm affine, hidden 256 (8 chunks); a ragged last tile (1000 rows)."""
+    from fpf_hip.kernels import transition as T
+    c, hidden, rows = 128, 256, 1000
+    wa, wb, wo, lw, lb = _tr_weights(c, hidden, 14, torch.float32)
+    if not affine:
+        lw = lb = None
+    x = torch.randn(rows, c, generator=_g(3))
+    m = torch.rand(rows, generator=_g(4)) * (torch.rand(rows, generator=_g(5)) > 0.2).float()
+    W = T.pack(w_a=wa.to(DEV), w_b=wb.to(DEV), w_o=wo.to(DEV), ln_w=None if lw is None else lw.to(DEV), ln_b=None if lb is None else lb.to(DEV))
+    y, sel = T.transition(x.to(DEV), W, word="exact", residual=True, mask=m.to(DEV))
+    torch.cuda.synchronize()
+    assert sel.row == "hip_gfx950_f32"
+    upd = S.transition(x, wa, wb, wo, lw, lb, dtype=torch.float64)
+    assert_f32_close(y, x.double() + m.double()[:, None] * upd, "transition fp32 residual mask affine=%s" % affine)

@@ -261,6 +261,161 @@ __global__ void __launch_bounds__(256) transition_f32_kernel(const float* x, flo
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------- fp32, c = 128 (exact tier)
+// The bf16 kernel's structure on the fp32 matrix core (v_mfma_f32_32x32x2_f32: fp32 operands, fp32 products and sums).  One
+// wave owns 32 pixel rows; lane (n, g) holds pixel n's LayerNorm'd channels 64 g .. 64 g + 63, so k-step s of GEMM 1 pairs
+// channels s (g = 0) and 64 + s (g = 1) -- each lane's weight fragment is then 4 consecutive k-steps in one 16-byte LDS
+// read.  GEMM 1 is computed transposed (a^T = W_a n^T: lane = pixel, 16 hidden rows per lane), and k-step t of GEMM 2
+// pairs the hidden rows register t holds in the two lane halves, so h = silu(a) * b feeds GEMM 2 from the registers it was
+// computed in.  Weights stream through two LDS buffers in 32-hidden chunks shared by the 8 waves (the next chunk's global
+// loads are issued before the current chunk's MFMAs and stored after them; one barrier per chunk).
+constexpr int TX_HB = 32;             // hidden rows per chunk
+constexpr int TX_NW = 8;              // waves per workgroup
+constexpr int TX_WP = TR_C + 4;       // LDS pitch (floats) of a W_a / W_b chunk row: 16 consecutive rows on distinct banks
+constexpr int TX_OP = TX_HB + 4;      // LDS pitch of a W_o chunk row (one output channel)
+
+__device__ __forceinline__ f32x16 mfma32f(float a, float b, const f32x16& c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
+
+__global__ void __launch_bounds__(64 * TX_NW) transition_f32_mfma(const float* x, float* out, const float* __restrict__ ln_w,
+                                                                  const float* __restrict__ ln_b, float eps, const float* __restrict__ wa,
+                                                                  const float* __restrict__ wb, const float* __restrict__ wo,
+                                                                  const float* __restrict__ mask, int residual, int64_t rows, int hidden) {
+  __shared__ __attribute__((aligned(16))) float sWa[2][TX_HB * TX_WP];
+  __shared__ __attribute__((aligned(16))) float sWb[2][TX_HB * TX_WP];
+  __shared__ __attribute__((aligned(16))) float sWo[2][TR_C * TX_OP];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t pix = ((int64_t)blockIdx.x * TX_NW + wave) * 32 + n;
+  const bool live = pix < rows;
+  // chunk hb: W_a / W_b rows hb 32 .. + 31 (1024 float4 each) and W_o columns hb 32 .. + 31 of all 128 rows (1024 float4);
+  // thread tid moves float4 tid and tid + 512 of each
+  f32x4 stage[6];
+  auto gload = [&](int hb) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = tid + 64 * TX_NW * q;
+      const int64_t wrow = (int64_t)(hb * TX_HB + (i >> 5)) * TR_C + (i & 31) * 4;
+      stage[q] = *reinterpret_cast<const f32x4*>(wa + wrow);
+      stage[2 + q] = *reinterpret_cast<const f32x4*>(wb + wrow);
+      stage[4 + q] = *reinterpret_cast<const f32x4*>(wo + (int64_t)(i >> 3) * hidden + hb * TX_HB + (i & 7) * 4);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = tid + 64 * TX_NW * q;
+      *reinterpret_cast<f32x4*>(&sWa[buf][(i >> 5) * TX_WP + (i & 31) * 4]) = stage[q];
+      *reinterpret_cast<f32x4*>(&sWb[buf][(i >> 5) * TX_WP + (i & 31) * 4]) = stage[2 + q];
+      *reinterpret_cast<f32x4*>(&sWo[buf][(i >> 3) * TX_OP + (i & 7) * 4]) = stage[4 + q];
+    }
+  };
+  const int nhb = hidden / TX_HB;
+  gload(0);
+  // LayerNorm of the lane's pixel (two-pass, the halves' partial sums exchanged across the wave's two halves)
+  float xn[64];
+  {
+    const float* xr = x + (live ? pix : 0) * TR_C + 64 * g;
+#pragma unroll
+    for (int s4 = 0; s4 < 16; ++s4) {
+      const f32x4 v = live ? *reinterpret_cast<const f32x4*>(xr + 4 * s4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xn[4 * s4 + e] = v[e];
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 64; ++k) s += xn[k];
+    s += __shfl_xor(s, 32);
+    const float mean = s / (float)TR_C;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < 64; ++k) {
+      const float d = xn[k] - mean;
+      q += d * d;
+    }
+    q += __shfl_xor(q, 32);
+    const float rstd = 1.0f / sqrtf(q / (float)TR_C + eps);
+#pragma unroll
+    for (int k = 0; k < 64; ++k) xn[k] = (xn[k] - mean) * rstd;
+    if (ln_w) {                                   // the affine, when given (16-byte aligned: checked by the launcher)
+#pragma unroll
+      for (int s4 = 0; s4 < 16; ++s4) {
+        const f32x4 w = *reinterpret_cast<const f32x4*>(ln_w + 64 * g + 4 * s4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xn[4 * s4 + e] *= w[e];
+      }
+    }
+    if (ln_b) {
+#pragma unroll
+      for (int s4 = 0; s4 < 16; ++s4) {
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(ln_b + 64 * g + 4 * s4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xn[4 * s4 + e] += bb[e];
+      }
+    }
+  }
+  lstore(0);
+  __syncthreads();
+  f32x16 acc[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x16{};
+  for (int hb = 0; hb < nhb; ++hb) {
+    const int buf = hb & 1;
+    if (hb + 1 < nhb) gload(hb + 1);
+    f32x16 a = f32x16{}, b = f32x16{};
+    const float* ra = &sWa[buf][n * TX_WP + 64 * g];
+    const float* rb = &sWb[buf][n * TX_WP + 64 * g];
+    f32x4 fa = *reinterpret_cast<const f32x4*>(ra), fb = *reinterpret_cast<const f32x4*>(rb);
+#pragma unroll
+    for (int s4 = 0; s4 < 16; ++s4) {
+      const f32x4 ca = fa, cb_ = fb;
+      if (s4 + 1 < 16) {                          // one 4-step group of fragment lookahead
+        fa = *reinterpret_cast<const f32x4*>(ra + 4 * s4 + 4);
+        fb = *reinterpret_cast<const f32x4*>(rb + 4 * s4 + 4);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a = mfma32f(ca[e], xn[4 * s4 + e], a);
+        b = mfma32f(cb_[e], xn[4 * s4 + e], b);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // h = silu(a) * b in place of a; register t holds hidden row 8 (t / 4) + 4 g + t % 4 of the chunk
+#pragma unroll
+    for (int v = 0; v < 16; ++v) a[v] = a[v] / (1.0f + expf(-a[v])) * b[v];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f32x4 fo[4];
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) fo[cb] = *reinterpret_cast<const f32x4*>(&sWo[buf][(32 * cb + n) * TX_OP + 4 * g + 8 * q]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = mfma32f(fo[cb][e], a[4 * q + e], acc[cb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (hb + 1 < nhb) {
+      lstore(buf ^ 1);                           // its previous chunk (hb - 1) was read by every wave before the last barrier
+      __syncthreads();
+    }
+  }
+  if (!live) return;
+  const float m = mask ? mask[pix] : 1.0f;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t o = pix * TR_C + 32 * cb + 8 * q + 4 * g;      // channels of registers 4 q .. 4 q + 3
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = acc[cb][4 * q + e] * m;
+      if (residual) {
+        const f32x4 r = *reinterpret_cast<const f32x4*>(x + o);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] += r[e];
+      }
+      *reinterpret_cast<f32x4*>(out + o) = y;
+    }
+}
+
 }  // namespace fpf
 
 extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char* err, size_t errlen) {
@@ -283,6 +438,13 @@ extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char
   }
   if (a->dtype == FPF_DT_F32) {
     if (a->c > TF_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 transition serves c <= %d (got %d)", TF_CM, a->c);
+    if (a->c == TR_C && a->hidden % TX_HB == 0 && aligned16(a->x) && aligned16(a->out) && aligned16(a->w_a) && aligned16(a->w_b) &&
+        aligned16(a->w_o) && (!a->ln_w || aligned16(a->ln_w)) && (!a->ln_b || aligned16(a->ln_b))) {   // the matrix-core kernel
+      const dim3 grid((unsigned)cdiv(a->rows, 32 * TX_NW)), block(64 * TX_NW);
+      hipLaunchKernelGGL(transition_f32_mfma, grid, block, 0, st, (const float*)a->x, (float*)a->out, a->ln_w, a->ln_b, a->eps,
+                         (const float*)a->w_a, (const float*)a->w_b, (const float*)a->w_o, a->row_mask, a->residual, a->rows, a->hidden);
+      return launched(err, errlen, "fpf_transition_fwd(f32 mfma)");
+    }
     const dim3 grid((unsigned)cdiv(a->rows, TF_R)), block(256);
     if (a->c <= 128)
       hipLaunchKernelGGL(transition_f32_kernel<128>, grid, block, 0, st, (const float*)a->x, (float*)a->out, a->ln_w, a->ln_b, a->eps,
