@@ -143,3 +143,34 @@ def test_trimul_fp32_exact(direction, N, masked):
     torch.cuda.synchronize()
     ref = S.trimul(z, mask, direction=direction, weights=w, dtype=torch.float64)
     assert_f32_close(out, ref, "trimul fp32 %s N%d" % (direction, N))
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_fp32_exact_batch_residual_ragged(direction):
+    """The fp32 matrix-core kernels past one contraction tile: batch 2, N = 300 (planes of 384: 3 x 3 tiles of 128, the last
+    one ragged), residual, a mask with padded tail rows / columns and random holes."""
+    from fpf_hip.kernels import trimul as TM
+    N = 300
+    w = _weights(128, 9, torch.float32)
+    g = torch.Generator().manual_seed(11)
+    z = torch.randn(2, N, N, 128, generator=g)
+    valid = torch.ones(N)
+    valid[N - 7:] = 0
+    mask = torch.outer(valid, valid).expand(2, N, N) * (torch.rand(2, N, N, generator=g) > 0.05).float()
+    print("[case] trimul fp32 %s B=2 N=%d residual" % (direction, N), flush=True)
+    out = TM.triangle_multiplication(z.to(DEV), mask.to(DEV), direction=direction, weights=_dev(w), word="hip_gfx950_f32", residual=True)
+    torch.cuda.synchronize()
+    ref = S.trimul(z, mask, direction=direction, weights=w, residual=True, dtype=torch.float64)
+    assert_f32_close(out, ref, "trimul fp32 %s B2 N%d residual" % (direction, N))
+
+
+def test_trimul_fp32_narrow_channels_scalar_path():
+    """c_z = c_h = 64 is served by the scalar fp32 kernels (the matrix-core form is built for 128)."""
+    from fpf_hip.kernels import trimul as TM
+    N = 40
+    w = _weights(64, 10, torch.float32)
+    z = torch.randn(N, N, 64, generator=torch.Generator().manual_seed(12))
+    out = TM.triangle_multiplication(z.to(DEV), None, direction="incoming", weights=_dev(w), word="hip_gfx950_f32", residual=True)
+    torch.cuda.synchronize()
+    ref = S.trimul(z, None, direction="incoming", weights=w, residual=True, dtype=torch.float64)
+    assert_f32_close(out, ref, "trimul fp32 c64")

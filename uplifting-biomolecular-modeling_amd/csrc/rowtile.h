@@ -232,4 +232,102 @@ __device__ __forceinline__ void rt_wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// ---------------------------------------------------------------------------------------------------------------- fp32 row tiles
+// The exact tier's form of the 32-pixel tile on the fp32 matrix core (v_mfma_f32_32x32x2_f32: fp32 operands, products and
+// sums).  Lane (n, g) holds pixel n's channels 64 g .. 64 g + 63, and k-step s pairs channel s (g = 0) with 64 + s (g = 1),
+// so one 16-byte LDS read gives a lane the weights of 4 consecutive k-steps.  D = W x^T: lane (n, g) holds pixel n and the
+// 16 output rows c_row(v, g) = 8 (v / 4) + 4 g + v % 4 of a 32-row block, as in the bf16 form.
+constexpr int RTF_WP = RT_C + 4;     // LDS pitch (floats) of a 128-wide fp32 weight row: 16 consecutive rows on distinct banks
+
+__device__ __forceinline__ f32x16 mfma32f(float a, float b, const f32x16& c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
+
+// LayerNorm of the lane's half of a 128-channel fp32 pixel row (row = the pixel's channel 0; zeros when !live): two-pass
+// statistics over both halves (exchanged with lane n ^ 32), then the affine (either pointer may be NULL; 16-byte aligned).
+// rtf_norm: the same on values already in registers.
+__device__ __forceinline__ void rtf_norm(int g, const float* __restrict__ w, const float* __restrict__ b, float eps, float (&xn)[64]) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 64; ++k) s += xn[k];
+  s += __shfl_xor(s, 32);
+  const float mean = s / (float)RT_C;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < 64; ++k) {
+    const float d = xn[k] - mean;
+    q += d * d;
+  }
+  q += __shfl_xor(q, 32);
+  const float rstd = 1.0f / sqrtf(q / (float)RT_C + eps);
+#pragma unroll
+  for (int k = 0; k < 64; ++k) xn[k] = (xn[k] - mean) * rstd;
+  if (w) {
+#pragma unroll
+    for (int s4 = 0; s4 < 16; ++s4) {
+      const f32x4 wv = *reinterpret_cast<const f32x4*>(w + 64 * g + 4 * s4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xn[4 * s4 + e] *= wv[e];
+    }
+  }
+  if (b) {
+#pragma unroll
+    for (int s4 = 0; s4 < 16; ++s4) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(b + 64 * g + 4 * s4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xn[4 * s4 + e] += bv[e];
+    }
+  }
+}
+__device__ __forceinline__ void rtf_ln(const float* row, bool live, int g, const float* __restrict__ w, const float* __restrict__ b,
+                                       float eps, float (&xn)[64]) {
+#pragma unroll
+  for (int s4 = 0; s4 < 16; ++s4) {
+    const f32x4 v = live ? *reinterpret_cast<const f32x4*>(row + 64 * g + 4 * s4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) xn[4 * s4 + e] = v[e];
+  }
+  rtf_norm(g, w, b, eps, xn);
+}
+
+// acc[m] += W_m x^T over 128 channels for K weight blocks of 32 rows held in LDS (w[m] = &block_m[n * RTF_WP + 64 g]), the
+// K accumulation chains interleaved, one 4-step group of fragment lookahead.
+template <int K>
+__device__ __forceinline__ void rtf_gemm(const float* const (&w)[K], const float (&xn)[64], f32x16 (&acc)[K]) {
+  f32x4 f[K];
+#pragma unroll
+  for (int m = 0; m < K; ++m) f[m] = *reinterpret_cast<const f32x4*>(w[m]);
+#pragma unroll
+  for (int s4 = 0; s4 < 16; ++s4) {
+    f32x4 c[K];
+#pragma unroll
+    for (int m = 0; m < K; ++m) {
+      c[m] = f[m];
+      if (s4 + 1 < 16) f[m] = *reinterpret_cast<const f32x4*>(w[m] + 4 * s4 + 4);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int m = 0; m < K; ++m) acc[m] = mfma32f(c[m][e], xn[4 * s4 + e], acc[m]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Rows r0 .. r0 + 31 of a [rows][128] fp32 matrix (16-byte aligned) into LDS at pitch RTF_WP, through registers: rtf_fetch
+// issues the global loads (NT threads, 1024 / NT float4 each), rtf_put stores them.
+template <int NT>
+__device__ __forceinline__ void rtf_fetch(const float* __restrict__ m, int64_t r0, int tid, f32x4 (&st)[1024 / NT]) {
+#pragma unroll
+  for (int q = 0; q < 1024 / NT; ++q) {
+    const int i = tid + NT * q;
+    st[q] = *reinterpret_cast<const f32x4*>(m + (r0 + (i >> 5)) * RT_C + (i & 31) * 4);
+  }
+}
+template <int NT>
+__device__ __forceinline__ void rtf_put(float* lds, int tid, const f32x4 (&st)[1024 / NT]) {
+#pragma unroll
+  for (int q = 0; q < 1024 / NT; ++q) {
+    const int i = tid + NT * q;
+    *reinterpret_cast<f32x4*>(lds + (i >> 5) * RTF_WP + (i & 31) * 4) = st[q];
+  }
+}
+
 }  // namespace fpf

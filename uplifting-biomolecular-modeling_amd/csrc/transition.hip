@@ -7,7 +7,7 @@
 // out^T = W_o h^T once the hidden index of each k-step is permuted the same way in W_o: the 4c hidden never leaves the
 // registers.  Weights stream through double-buffered LDS in 32-hidden chunks shared by the 8 waves of a workgroup (the next
 // chunk's global loads are in flight while the current one feeds the MFMAs; one barrier per chunk).
-// fp32 path (exact tier): LDS-tiled scalar FMA, fp32 throughout.
+// fp32 path (exact tier): c = 128 on the fp32 matrix core (transition_f32_mfma), other widths LDS-tiled scalar FMA.
 #include "rowtile.h"
 
 namespace fpf {
@@ -271,10 +271,8 @@ __global__ void __launch_bounds__(256) transition_f32_kernel(const float* x, flo
 // loads are issued before the current chunk's MFMAs and stored after them; one barrier per chunk).
 constexpr int TX_HB = 32;             // hidden rows per chunk
 constexpr int TX_NW = 8;              // waves per workgroup
-constexpr int TX_WP = TR_C + 4;       // LDS pitch (floats) of a W_a / W_b chunk row: 16 consecutive rows on distinct banks
+constexpr int TX_WP = RTF_WP;         // LDS pitch (floats) of a W_a / W_b chunk row: 16 consecutive rows on distinct banks
 constexpr int TX_OP = TX_HB + 4;      // LDS pitch of a W_o chunk row (one output channel)
-
-__device__ __forceinline__ f32x16 mfma32f(float a, float b, const f32x16& c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
 
 __global__ void __launch_bounds__(64 * TX_NW) transition_f32_mfma(const float* x, float* out, const float* __restrict__ ln_w,
                                                                   const float* __restrict__ ln_b, float eps, const float* __restrict__ wa,
@@ -310,48 +308,8 @@ __global__ void __launch_bounds__(64 * TX_NW) transition_f32_mfma(const float* x
   };
   const int nhb = hidden / TX_HB;
   gload(0);
-  // LayerNorm of the lane's pixel (two-pass, the halves' partial sums exchanged across the wave's two halves)
-  float xn[64];
-  {
-    const float* xr = x + (live ? pix : 0) * TR_C + 64 * g;
-#pragma unroll
-    for (int s4 = 0; s4 < 16; ++s4) {
-      const f32x4 v = live ? *reinterpret_cast<const f32x4*>(xr + 4 * s4) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xn[4 * s4 + e] = v[e];
-    }
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < 64; ++k) s += xn[k];
-    s += __shfl_xor(s, 32);
-    const float mean = s / (float)TR_C;
-    float q = 0.f;
-#pragma unroll
-    for (int k = 0; k < 64; ++k) {
-      const float d = xn[k] - mean;
-      q += d * d;
-    }
-    q += __shfl_xor(q, 32);
-    const float rstd = 1.0f / sqrtf(q / (float)TR_C + eps);
-#pragma unroll
-    for (int k = 0; k < 64; ++k) xn[k] = (xn[k] - mean) * rstd;
-    if (ln_w) {                                   // the affine, when given (16-byte aligned: checked by the launcher)
-#pragma unroll
-      for (int s4 = 0; s4 < 16; ++s4) {
-        const f32x4 w = *reinterpret_cast<const f32x4*>(ln_w + 64 * g + 4 * s4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xn[4 * s4 + e] *= w[e];
-      }
-    }
-    if (ln_b) {
-#pragma unroll
-      for (int s4 = 0; s4 < 16; ++s4) {
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(ln_b + 64 * g + 4 * s4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xn[4 * s4 + e] += bb[e];
-      }
-    }
-  }
+  float xn[64];                                  // the lane's LayerNorm'd half of its pixel row
+  rtf_ln(x + (live ? pix : 0) * TR_C, live, g, ln_w, ln_b, eps, xn);
   lstore(0);
   __syncthreads();
   f32x16 acc[4];
@@ -360,24 +318,11 @@ __global__ void __launch_bounds__(64 * TX_NW) transition_f32_mfma(const float* x
   for (int hb = 0; hb < nhb; ++hb) {
     const int buf = hb & 1;
     if (hb + 1 < nhb) gload(hb + 1);
-    f32x16 a = f32x16{}, b = f32x16{};
-    const float* ra = &sWa[buf][n * TX_WP + 64 * g];
-    const float* rb = &sWb[buf][n * TX_WP + 64 * g];
-    f32x4 fa = *reinterpret_cast<const f32x4*>(ra), fb = *reinterpret_cast<const f32x4*>(rb);
-#pragma unroll
-    for (int s4 = 0; s4 < 16; ++s4) {
-      const f32x4 ca = fa, cb_ = fb;
-      if (s4 + 1 < 16) {                          // one 4-step group of fragment lookahead
-        fa = *reinterpret_cast<const f32x4*>(ra + 4 * s4 + 4);
-        fb = *reinterpret_cast<const f32x4*>(rb + 4 * s4 + 4);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        a = mfma32f(ca[e], xn[4 * s4 + e], a);
-        b = mfma32f(cb_[e], xn[4 * s4 + e], b);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    f32x16 ab[2] = {f32x16{}, f32x16{}};
+    const float* const wab[2] = {&sWa[buf][n * TX_WP + 64 * g], &sWb[buf][n * TX_WP + 64 * g]};
+    rtf_gemm<2>(wab, xn, ab);
+    f32x16& a = ab[0];
+    const f32x16& b = ab[1];
     // h = silu(a) * b in place of a; register t holds hidden row 8 (t / 4) + 4 g + t % 4 of the chunk
 #pragma unroll
     for (int v = 0; v < 16; ++v) a[v] = a[v] / (1.0f + expf(-a[v])) * b[v];

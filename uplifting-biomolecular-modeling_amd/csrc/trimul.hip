@@ -630,6 +630,219 @@ __global__ void __launch_bounds__(256) trimul_k3_f32(const float* zin, float* ou
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------- fp32 on the matrix core
+// The exact tier at c_z = c_h = 128 (v_mfma_f32_32x32x2_f32: fp32 operands, products and sums), on the fp32 path's
+// row-major planes [B 128][Np][Np].  K1 and K3 take one 32-pixel tile per wave (the fp32 row-tile form of rowtile.h), the
+// weights of one 32-channel output block at a time in LDS (two buffers, the next block's global loads in flight while the
+// current one feeds the MFMAs); the contraction takes 128 x 128 tiles of X per workgroup of 4 waves (64 x 64 each), k in
+// slabs of 16 through two LDS buffers.
+constexpr int FM_NW = 8;                    // waves per workgroup of K1 / K3
+constexpr int FC_T = 128, FC_K = 16, FC_P = FC_K + 4;   // contraction tile, k-slab, LDS pitch (floats) of a slab row
+
+// K1: tile = plane row P, columns Q0 .. Q0 + 31 (pixel (P, Q) outgoing, (Q, P) incoming); every plane element is written,
+// padding (P or Q >= N) as 0 (the mask factor of a pixel outside the image is 0).
+__global__ void __launch_bounds__(64 * FM_NW) trimul_k1_f32m(const float* __restrict__ z, const float* __restrict__ mask,
+                                                             const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
+                                                             const float* __restrict__ w_ap, const float* __restrict__ w_ag,
+                                                             const float* __restrict__ w_bp, const float* __restrict__ w_bg,
+                                                             float* __restrict__ pa, float* __restrict__ pb, int64_t N, int64_t Np, int outgoing) {
+  __shared__ __attribute__((aligned(16))) float sW[2][4][32 * RTF_WP];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t b = blockIdx.y, tpr = Np / 32, tile = (int64_t)blockIdx.x * FM_NW + wave;
+  const int64_t P = tile / tpr, Q = (tile % tpr) * 32 + n;
+  const bool inb = P < Np;                           // always, for Np a multiple of 128; kept for the stores
+  const bool live = inb && P < N && Q < N;
+  const int64_t pix = outgoing ? (b * N + P) * N + Q : (b * N + Q) * N + P;
+  const float* const W[4] = {w_ap, w_ag, w_bp, w_bg};
+  f32x4 st[2][1024 / (64 * FM_NW)];                  // staging of two of the four matrices at a time
+  float xn[64];
+  rtf_ln(z + (live ? pix : 0) * RT_C, live, g, ln_w, ln_b, eps, xn);
+  const float mk = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) rtf_fetch<64 * FM_NW>(W[2 * h + m], 0, tid, st[m]);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) rtf_put<64 * FM_NW>(sW[0][2 * h + m], tid, st[m]);
+  }
+  __syncthreads();
+  const int64_t plane = Np * Np;
+  for (int cb = 0; cb < 4; ++cb) {
+    const int buf = cb & 1;
+    // block cb + 1 goes to buffer buf ^ 1 (block cb - 1, read by every wave before the last barrier): W_ap / W_ag loads in
+    // flight during the MFMAs, W_bp / W_bg during the stores
+    if (cb + 1 < 4) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) rtf_fetch<64 * FM_NW>(W[m], 32 * (cb + 1), tid, st[m]);
+    }
+    f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
+    const float* const w[4] = {&sW[buf][0][n * RTF_WP + 64 * g], &sW[buf][1][n * RTF_WP + 64 * g], &sW[buf][2][n * RTF_WP + 64 * g],
+                               &sW[buf][3][n * RTF_WP + 64 * g]};
+    rtf_gemm<4>(w, xn, acc);
+    if (cb + 1 < 4) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) rtf_put<64 * FM_NW>(sW[buf ^ 1][m], tid, st[m]);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) rtf_fetch<64 * FM_NW>(W[2 + m], 32 * (cb + 1), tid, st[m]);
+    }
+    if (inb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t c = 32 * cb + 8 * (v >> 2) + 4 * g + (v & 3);
+        const int64_t o = (b * RT_C + c) * plane + P * Np + Q;
+        pa[o] = mk * sigmoid_exact(acc[1][v]) * acc[0][v];
+        pb[o] = mk * sigmoid_exact(acc[3][v]) * acc[2][v];
+      }
+    }
+    if (cb + 1 < 4) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) rtf_put<64 * FM_NW>(sW[buf ^ 1][2 + m], tid, st[m]);
+      __syncthreads();
+    }
+  }
+}
+
+// X[bc][i][j] = sum_k A[bc][i][k] B[bc][j][k] for a 128 x 128 tile; X rows / columns at or past N are not written.  k-step s
+// of a slab pairs k = s (g = 0) with 8 + s (g = 1), so each lane's 8 slab values of a row are two 16-byte LDS reads.
+__global__ void __launch_bounds__(256) trimul_contract_f32m(const float* __restrict__ A, const float* __restrict__ Bm, float* __restrict__ X,
+                                                            int64_t Np, int64_t N) {
+  __shared__ __attribute__((aligned(16))) float sA[2][FC_T * FC_P];
+  __shared__ __attribute__((aligned(16))) float sB[2][FC_T * FC_P];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t bc = blockIdx.z, plane = Np * Np;
+  const float* a0 = A + bc * plane + (int64_t)blockIdx.y * FC_T * Np;
+  const float* b0 = Bm + bc * plane + (int64_t)blockIdx.x * FC_T * Np;
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  f32x4 sta[2], stb[2];
+  auto fetch = [&](int64_t k0) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = tid + 256 * q, r = i >> 2, c4 = i & 3;
+      sta[q] = *reinterpret_cast<const f32x4*>(a0 + r * Np + k0 + 4 * c4);
+      stb[q] = *reinterpret_cast<const f32x4*>(b0 + r * Np + k0 + 4 * c4);
+    }
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int i = tid + 256 * q, r = i >> 2, c4 = i & 3;
+      *reinterpret_cast<f32x4*>(&sA[buf][r * FC_P + 4 * c4]) = sta[q];
+      *reinterpret_cast<f32x4*>(&sB[buf][r * FC_P + 4 * c4]) = stb[q];
+    }
+  };
+  f32x16 acc[2][2] = {{f32x16{}, f32x16{}}, {f32x16{}, f32x16{}}};
+  const int nk = (int)(Np / FC_K);
+  fetch(0);
+  put(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) fetch((int64_t)(kt + 1) * FC_K);
+    f32x4 fa[2][2], fb[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        fa[s][h] = *reinterpret_cast<const f32x4*>(&sA[buf][(wr + 32 * s + n) * FC_P + 8 * g + 4 * h]);
+        fb[s][h] = *reinterpret_cast<const f32x4*>(&sB[buf][(wc + 32 * s + n) * FC_P + 8 * g + 4 * h]);
+      }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int si = 0; si < 2; ++si)
+#pragma unroll
+          for (int sj = 0; sj < 2; ++sj) acc[si][sj] = mfma32f(fa[si][h][e], fb[sj][h][e], acc[si][sj]);
+    if (kt + 1 < nk) {                               // buffer buf ^ 1 held slab kt - 1, read by every wave before the last barrier
+      put(buf ^ 1);
+      __syncthreads();
+    }
+  }
+  const int64_t i0 = (int64_t)blockIdx.y * FC_T + wr, j0 = (int64_t)blockIdx.x * FC_T + wc;
+#pragma unroll
+  for (int si = 0; si < 2; ++si)
+#pragma unroll
+    for (int sj = 0; sj < 2; ++sj) {
+      const int64_t j = j0 + 32 * sj + n;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t i = i0 + 32 * si + 8 * (v >> 2) + 4 * g + (v & 3);
+        if (i < N && j < N) X[bc * plane + i * Np + j] = acc[si][sj][v];
+      }
+    }
+}
+
+// K3: tile = output row i, columns j0 .. j0 + 31: LayerNorm of X's 128 channels and of z's, then out = sigmoid(W_og
+// LN(z)) * (W_o LN(X)) [+ z], the two GEMMs' chains interleaved.
+__global__ void __launch_bounds__(64 * FM_NW) trimul_k3_f32m(const float* zin, float* out, const float* __restrict__ X,
+                                                             const float* __restrict__ ln_in_w, const float* __restrict__ ln_in_b,
+                                                             const float* __restrict__ ln_out_w, const float* __restrict__ ln_out_b, float eps,
+                                                             const float* __restrict__ w_o, const float* __restrict__ w_og, int64_t N, int64_t Np,
+                                                             int residual) {
+  __shared__ __attribute__((aligned(16))) float sW[2][2][32 * RTF_WP];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
+  const int64_t b = blockIdx.y, tpr = cdiv(N, 32), tile = (int64_t)blockIdx.x * FM_NW + wave;
+  const int64_t i = tile / tpr, j = (tile % tpr) * 32 + n;
+  const bool live = i < N && j < N;
+  const int64_t pix = (b * N + i) * N + j, plane = Np * Np;
+  f32x4 st[2][1024 / (64 * FM_NW)];
+  rtf_fetch<64 * FM_NW>(w_o, 0, tid, st[0]);
+  rtf_fetch<64 * FM_NW>(w_og, 0, tid, st[1]);
+  float xo[64], zn[64];
+  {
+    const float* xp = X + (b * RT_C + 64 * g) * plane + (live ? i * Np + j : 0);
+#pragma unroll
+    for (int k = 0; k < 64; ++k) xo[k] = live ? xp[k * plane] : 0.0f;
+  }
+  rtf_norm(g, ln_out_w, ln_out_b, eps, xo);
+  rtf_ln(zin + (live ? pix : 0) * RT_C, live, g, ln_in_w, ln_in_b, eps, zn);
+  rtf_put<64 * FM_NW>(sW[0][0], tid, st[0]);
+  rtf_put<64 * FM_NW>(sW[0][1], tid, st[1]);
+  __syncthreads();
+  for (int cb = 0; cb < 4; ++cb) {
+    const int buf = cb & 1;
+    if (cb + 1 < 4) {
+      rtf_fetch<64 * FM_NW>(w_o, 32 * (cb + 1), tid, st[0]);
+      rtf_fetch<64 * FM_NW>(w_og, 32 * (cb + 1), tid, st[1]);
+    }
+    const float* wo_r = &sW[buf][0][n * RTF_WP + 64 * g];
+    const float* wg_r = &sW[buf][1][n * RTF_WP + 64 * g];
+    f32x16 o = f32x16{}, gt = f32x16{};
+#pragma unroll
+    for (int s4 = 0; s4 < 16; ++s4) {
+      const f32x4 fo = *reinterpret_cast<const f32x4*>(wo_r + 4 * s4);
+      const f32x4 fg = *reinterpret_cast<const f32x4*>(wg_r + 4 * s4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o = mfma32f(fo[e], xo[4 * s4 + e], o);
+        gt = mfma32f(fg[e], zn[4 * s4 + e], gt);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (live) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t oo = pix * RT_C + 32 * cb + 8 * q + 4 * g;     // channels of registers 4 q .. 4 q + 3
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = sigmoid_exact(gt[4 * q + e]) * o[4 * q + e];
+        if (residual) {
+          const f32x4 r = *reinterpret_cast<const f32x4*>(zin + oo);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] += r[e];
+        }
+        *reinterpret_cast<f32x4*>(out + oo) = y;
+      }
+    }
+    if (cb + 1 < 4) {
+      rtf_put<64 * FM_NW>(sW[buf ^ 1][0], tid, st[0]);
+      rtf_put<64 * FM_NW>(sW[buf ^ 1][1], tid, st[1]);
+      __syncthreads();
+    }
+  }
+}
+
 static int64_t padded(int64_t n) { return cdiv(n, TM_TILE) * TM_TILE; }
 // The contraction tile of n (256 when the padded planes take the 256-tile kernel, else 128).
 static int64_t ctile(int64_t n) { return padded(n) % CB_T == 0 ? CB_T : TM_TILE; }
@@ -762,6 +975,24 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
     float* pa = static_cast<float*>(a->workspace);
     float* pb = pa + B * a->c_h * Np * Np;
     float* X = pb + B * a->c_h * Np * Np;
+    if (a->c_z == TM_C && a->c_h == TM_C && aligned16(a->z) && aligned16(a->out) && aligned16(a->workspace) && aligned16(a->w_ap) &&
+        aligned16(a->w_ag) && aligned16(a->w_bp) && aligned16(a->w_bg) && aligned16(a->w_o) && aligned16(a->w_og) &&
+        (!a->ln_in_w || aligned16(a->ln_in_w)) && (!a->ln_in_b || aligned16(a->ln_in_b)) && (!a->ln_out_w || aligned16(a->ln_out_w)) &&
+        (!a->ln_out_b || aligned16(a->ln_out_b))) {   // the matrix-core kernels
+      hipLaunchKernelGGL(trimul_k1_f32m, dim3((unsigned)(Np * (Np / 32) / FM_NW), (unsigned)B), dim3(64 * FM_NW), 0, st, (const float*)a->z,
+                         a->mask, a->ln_in_w, a->ln_in_b, a->eps, (const float*)a->w_ap, (const float*)a->w_ag, (const float*)a->w_bp,
+                         (const float*)a->w_bg, pa, pb, N, Np, a->outgoing);
+      int rc = launched(err, errlen, "trimul_k1_f32m");
+      if (rc) return rc;
+      hipLaunchKernelGGL(trimul_contract_f32m, dim3((unsigned)(Np / FC_T), (unsigned)(Np / FC_T), (unsigned)(B * TM_C)), dim3(256), 0, st, pa,
+                         pb, X, Np, N);
+      rc = launched(err, errlen, "trimul_contract_f32m");
+      if (rc) return rc;
+      hipLaunchKernelGGL(trimul_k3_f32m, dim3((unsigned)cdiv(N * cdiv(N, 32), FM_NW), (unsigned)B), dim3(64 * FM_NW), 0, st, (const float*)a->z,
+                         (float*)a->out, X, a->ln_in_w, a->ln_in_b, a->ln_out_w, a->ln_out_b, a->eps, (const float*)a->w_o,
+                         (const float*)a->w_og, N, Np, a->residual);
+      return launched(err, errlen, "trimul_k3_f32m");
+    }
     hipLaunchKernelGGL(trimul_k1_f32, dim3((unsigned)(Np * Np / F_R), (unsigned)B), dim3(256), 0, st, (const float*)a->z, a->mask, a->ln_in_w,
                        a->ln_in_b, a->eps, (const float*)a->w_ap, (const float*)a->w_ag, (const float*)a->w_bp, (const float*)a->w_bg, pa, pb, N,
                        Np, a->c_z, a->c_h, a->outgoing);

@@ -95,7 +95,8 @@ def measure(sizes, reps, dev):
             c["exact"] = row if ms_stock >= ms_row else F.ROW_STOCK   # measured >= x1.00 over the stock op, else the stock op
 
     for N in sizes:
-        for dt, word, row in ((torch.bfloat16, "fast", F.ROW_FAST), (torch.float32, "exact", F.ROW_F32)):
+        # each row is named directly (a tier word would resolve through the table being rebuilt)
+        for dt, word, row in ((torch.bfloat16, F.ROW_FAST, F.ROW_FAST), (torch.float32, F.ROW_F32, F.ROW_F32)):
             dw = F.dtype_word(dt)
             # triangle attention op
             shp = (1, N, 4, N, 32)
