@@ -155,8 +155,23 @@ def step_times(fn, reps, torch):
     return [ev[i].elapsed_time(ev[i + 1]) for i in range(reps)]
 
 
+def warm_up(fn, torch, seconds=0.03):
+    """Calls fn() back to back for about `seconds` of GPU time (at least 3 calls): the first ~10 ms of a kernel stream after
+    host-side set-up run measurably slower on the box (the core at N = 768 took a median of 427 us over its first 30 calls
+    and 363-367 us afterwards), so a leg's timed calls start once the clocks have settled."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < 3 or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def time_events(fn, reps, torch):
-    """Median ms per call of fn() over max(reps, 20) calls (median of >= 20 after warm-up)."""
+    """Median ms per call of fn() over max(reps, 20) calls after warm_up (median of >= 20 after warm-up)."""
+    warm_up(fn, torch)
     return statistics.median(step_times(fn, max(reps, 20), torch))
 
 
