@@ -166,6 +166,55 @@ def test_pair_block_same_class(N):
     assert_same_class(zd.float(), ref, S.pair_block_autocast(z, mask, params), "pair block N=%d" % N)
 
 
+def test_pair_block_per_site_budget():
+    """Where the block's error comes from, on the smoke's inputs (N = 48, 4 padded residues, seed-1 weights): each site alone,
+    fed the same bf16 input (the fp32 chain's state rounded to bf16), its update against the fp32 statement of that site, next
+    to the bf16-autocast statement's update on the same input -- each held to SAME_CLASS -- and the share of the block error
+    that the bf16 residual stream alone causes (the fp32 chain with z rounded to bf16 after every site: the resident-z
+    composition rounds there, the autocast statement keeps z in fp32)."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.attn import pair_fused as PF
+    from fpf_hip.kernels import transition as TR
+    from fpf_hip.kernels import trimul as TM
+    N = 48
+    params = _bf16_weights(PFM.random_params(seed=1))
+    z = torch.randn(1, N, N, 128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).float()
+    mask = torch.ones(1, N, N)
+    mask[:, N - 4:, :] = 0
+    mask[:, :, N - 4:] = 0
+    blk = PFM.PairBlock(params, DEV, torch.bfloat16)
+    t = params["tr"]
+    sites = [
+        ("trimul_out", lambda x: S.trimul(x, mask, direction="outgoing", weights=params["tmo"], dtype=torch.float32),
+         lambda x: S.trimul_autocast(x, mask, direction="outgoing", weights=params["tmo"]),
+         lambda xd: TM.triangle_multiplication(xd, mask.to(DEV), direction="outgoing", weights=blk.tmo, word="fast", cache=blk.cache_o)),
+        ("trimul_in", lambda x: S.trimul(x, mask, direction="incoming", weights=params["tmi"], dtype=torch.float32),
+         lambda x: S.trimul_autocast(x, mask, direction="incoming", weights=params["tmi"]),
+         lambda xd: TM.triangle_multiplication(xd, mask.to(DEV), direction="incoming", weights=blk.tmi, word="fast", cache=blk.cache_i)),
+        ("tri_att_start", lambda x: S.tri_attn(x, params["tas"], mask, ending=False, dtype=torch.float32),
+         lambda x: S.tri_attn_autocast(x, params["tas"], mask, ending=False),
+         lambda xd: PF.tri_attn_block(xd, blk.ta["tas"], mask.to(DEV), ending=False)),
+        ("tri_att_end", lambda x: S.tri_attn(x, params["tae"], mask, ending=True, dtype=torch.float32),
+         lambda x: S.tri_attn_autocast(x, params["tae"], mask, ending=True),
+         lambda xd: PF.tri_attn_block(xd, blk.ta["tae"], mask.to(DEV), ending=True)),
+        ("transition", lambda x: S.transition(x, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"], dtype=torch.float32),
+         lambda x: S.transition_autocast(x, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"]),
+         lambda xd: TR.transition(xd, blk.tr, word="fast")[0]),
+    ]
+    x32 = z.clone()          # the fp32 chain
+    xr = z.clone()           # the fp32 chain with the residual stream rounded to bf16 after every site
+    for name, f32, ac, hip in sites:
+        xin = x32.to(torch.bfloat16).float()                           # the site's input, bf16-representable
+        ref = f32(xin)
+        u = hip(xin.to(torch.bfloat16).to(DEV))
+        torch.cuda.synchronize()
+        assert_same_class(u.float().cpu(), ref, ac(xin), "site %s" % name)
+        x32 = x32 + f32(x32)
+        xr = (xr + f32(xr)).to(torch.bfloat16).float()
+    ma, rl = max_abs(xr, x32), rel_l2(xr, x32)
+    print("[same-class] block: the bf16 residual stream alone (exact sites) max_abs=%.3e rel_l2=%.3e vs the fp32 chain" % (ma, rl))
+
+
 # ------------------------------------------------------------------------------------------------------------------ biases
 @pytest.mark.parametrize("ending", [False, True])
 def test_block_gate_and_output_biases(ending):
