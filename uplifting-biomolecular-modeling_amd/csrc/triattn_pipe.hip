@@ -340,7 +340,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
           }
           uint32_t pk[8];
           softmax_step(sv, pk, la[r][0], la[r][1]);
-          o[pr] = mfma32(as_bf8(vf0), as_bf8(u32x4{pin[0], pin[1], pin[2], pin[3]}), o[pr]);
+          // the sums are taken in this step, between its MFMAs (left free, the compiler sinks every step's v_dot2 to the end
+          // of the tile: 40 more live registers and a VALU burst the matrix core cannot overlap)
+          asm volatile("" : "+v"(la[r][0]), "+v"(la[r][1]));
+          o[pr] =mfma32(as_bf8(vf0), as_bf8(u32x4{pin[0], pin[1], pin[2], pin[3]}), o[pr]);
           o[pr] = mfma32(as_bf8(vf1), as_bf8(u32x4{pin[4], pin[5], pin[6], pin[7]}), o[pr]);
           s[pr] = qk(kf0, kf1, pr, (nsub & 1) ? bq[1] : bq[0]);
           // the next step's fragments: (sub, r + 1), else (1, 0), else tile T + 1's (0, 0) (V^T of this tile's second
