@@ -5,8 +5,8 @@
 // B operand of v_mfma_f32_32x32x16_bf16 (lane n%32 = pixel, channels 64*(lane/32) + 8t .. +7 for k-step t).  GEMM 1 is
 // computed transposed, a^T = W_a n^T, so its D layout (lane = pixel, 16 hidden values) IS the B operand of GEMM 2
 // out^T = W_o h^T once the hidden index of each k-step is permuted the same way in W_o: the 4c hidden never leaves the
-// registers.  Weights stream through double-buffered LDS in 32-hidden chunks shared by the 8 waves of a workgroup (the next
-// chunk's global loads are in flight while the current one feeds the MFMAs; one barrier per chunk).
+// registers.  Weights stream through a 3-buffer LDS ring in 32-hidden chunks shared by the 4 waves of a workgroup (the next
+// two chunks' transfers are in flight while the current one feeds the MFMAs; one barrier per chunk).
 // fp32 path (exact tier): c = 128 on the fp32 matrix core (transition_f32_mfma), other widths LDS-tiled scalar FMA.
 #include "rowtile.h"
 
@@ -15,11 +15,14 @@ namespace fpf {
 constexpr int TR_C = 128;
 constexpr int TR_KS = TR_C / 16;      // k-steps of GEMM 1
 constexpr int TR_HB = 32;             // hidden rows per chunk
-constexpr int TR_PW = 1, TR_NW = 8;   // 32-row tiles per wave, waves per workgroup (2 per SIMD; measured faster than 2 tiles x 1 wave per SIMD)
-constexpr int TR_NBUF = 4;            // weight-chunk ring: 3 chunks in flight
+// 32-row tiles per wave and waves per workgroup: 4 waves (one per SIMD) and two workgroups per CU, whose waves share a SIMD
+// without sharing a barrier, so one can run its MFMAs while the other evaluates its activation (measured 9-10 % faster than
+// 8 waves in one workgroup, and than 2 tiles x 1 wave per SIMD)
+constexpr int TR_PW = 1, TR_NW = 4;
+constexpr int TR_NBUF = 3;            // weight-chunk ring: 2 chunks in flight (73 KB of LDS per workgroup: two fit a CU)
 
 template <int PW, int NW>
-__global__ void __launch_bounds__(64 * NW) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
                                                               const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ wa,
                                                               const uint16_t* __restrict__ wb, const uint16_t* __restrict__ wo,
                                                               const float* __restrict__ mask, int residual, int64_t rows, int hidden) {
@@ -129,15 +132,14 @@ __global__ void __launch_bounds__(64 * NW) transition_bf16_kernel(const uint16_t
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (hb + 1 < nhb) {                          // chunk hb + 1 landed: only the later chunks' transfers may be outstanding
+    if (hb + 1 < nhb) {                          // chunk hb + 1 landed: only chunk hb + 2's transfers (3 NQ) may be outstanding
+      static_assert(TR_NBUF == 3, "the waits below count one chunk in flight behind the awaited one");
       if constexpr (NQ == 1) {
-        if (hb + 3 < nhb) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-        else if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+        if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       } else {
         static_assert(NQ == 2, "4 or 8 waves");
-        if (hb + 3 < nhb) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-        else if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       __builtin_amdgcn_s_barrier();
