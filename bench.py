@@ -2,7 +2,7 @@
 """bench.py -- one Pairformer pair block (the hot path) on one MI355X: ms, TFLOP/s and fraction of the bf16 MFMA roofline.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--n 768] [--no-cpu]
-    python bench.py --probe triattn_core|trimul|transition|pair_block|copy [--n 768] [--steps 5]   (launch-only runs for rocprofv3)
+    python bench.py --probe triattn_core|trimul|transition|pair_block|trunk|big|copy [--n 768] [--steps 5]   (runs for rocprofv3)
 
 Step = one pair block on a resident z [1, N, N, 128] bf16, in place, in the reference order (trimul outgoing, trimul incoming,
 tri-att starting node, tri-att ending node, transition 4x): 13 launches of libfpf_hip on torch's current stream.  Synthetic
@@ -47,7 +47,7 @@ def single_flops(N, c_s=384, c_z=128, heads=16, factor=4):
 def trunk(torch, dev, layers, N=512, reps=2):
     """BASELINE config 3: a Pairformer trunk of ``layers`` layers at N tokens (pair track bf16, c_z = 128, 4 x 32 triangle heads;
     single track fp32, c_s = 384, 16 heads x 24), random-init weights per layer (seeds 1000 + l), s, z ~ N(0, 1), masks all ones.
-    One warm-up pass, then the mean of ``reps`` passes, HIP events on the current stream."""
+    One warm-up pass, then the median of ``reps`` passes, HIP events on the current stream."""
     from fpf_hip import pairformer as PFM
     stack = [(PFM.PairBlock(PFM.random_params(seed=1000 + l), dev, torch.bfloat16),
               PFM.SingleBlock(PFM.random_single_params(seed=2000 + l), dev)) for l in range(layers)]
@@ -117,6 +117,15 @@ def configs_legs(torch, dev, big_blocks=4):
         t = time_events(fn, 20, torch)
         legs["c1_triatt_%s" % name] = {"N": N, "ms": round(t, 4), "tflops": round(f / (t * 1e-3) / 1e12, 1)}
     del z
+    legs["c4_big"] = big_leg(torch, dev, blk, big_blocks)
+    return legs
+
+
+def big_leg(torch, dev, blk, blocks):
+    """Config 4: `blocks` pair blocks of the `big` line at N = 2048 (256-row chunks), after one untimed block; the peak is this
+    leg's own (the shared scratch is released first)."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip import _face as F
     F.release_scratch()                                     # the big leg's peak is its own: no scratch left from earlier legs
     torch.cuda.empty_cache()
     torch.cuda.reset_peak_memory_stats()
@@ -129,17 +138,17 @@ def configs_legs(torch, dev, big_blocks=4):
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(big_blocks):
+    for _ in range(blocks):
         PFM.pair_block(zb, mb, blk, word="big", rows=256)
     e.record()
     torch.cuda.synchronize()
     ms = s.elapsed_time(e)
-    fb = block_flops(N)["block"] * big_blocks
-    legs["c4_big"] = {"N": N, "blocks": big_blocks, "rows_per_chunk": 256, "ms": round(ms, 2), "ms_per_block": round(ms / big_blocks, 2),
-                      "tflops": round(fb / (ms * 1e-3) / 1e12, 1), "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
-                      "peak_note": "this leg alone: z 1.07 GB + the shared scratch of its largest call"}
+    fb = block_flops(N)["block"] * blocks
+    leg = {"N": N, "blocks": blocks, "rows_per_chunk": 256, "ms": round(ms, 2), "ms_per_block": round(ms / blocks, 2),
+           "tflops": round(fb / (ms * 1e-3) / 1e12, 1), "peak_gb": round(torch.cuda.max_memory_allocated() / 1e9, 2),
+           "peak_note": "this leg alone: z 1.07 GB + the shared scratch of its largest call"}
     del zb
-    return legs
+    return leg
 
 
 def step_times(fn, reps, torch):
@@ -253,13 +262,19 @@ def probe(kind, N, reps):
                 TR.transition(z, blk.tr, word="fast", residual=True, out=z)
             else:
                 PFM.pair_block(z, mask, blk)
+    elif kind == "trunk":                                  # BASELINE config 3 alone: 48 layers at N = 512, 1 warm-up + 2 timed passes
+        print(json.dumps(trunk(torch, dev, 48)), flush=True)
+    elif kind == "big":                                    # BASELINE config 4 alone: 1 warm-up + 4 timed `big` blocks at N = 2048
+        from fpf_hip import pairformer as PFM
+        blk = PFM.PairBlock(PFM.random_params(seed=0), dev, torch.bfloat16)
+        print(json.dumps(big_leg(torch, dev, blk, 4)), flush=True)
     elif kind == "copy":
         x = torch.randn(N * N * 128, generator=g).to(torch.bfloat16).to(dev)
         y = torch.empty_like(x)
         for _ in range(reps):
             y.copy_(x)
     else:
-        raise SystemExit("unknown probe %r (triattn_core | trimul | transition | pair_block | copy)" % kind)
+        raise SystemExit("unknown probe %r (triattn_core | trimul | transition | pair_block | trunk | big | copy)" % kind)
     torch.cuda.synchronize()
     print("probe %s N=%d reps=%d done" % (kind, N, reps), flush=True)
 
@@ -300,7 +315,7 @@ def main():
     ap.add_argument("--trunk-layers", type=int, default=48, help="BASELINE config-3 trunk leg (0: skip)")
     ap.add_argument("--stack-layers", type=int, default=48, help="the north star's pair stack at N (0: skip)")
     ap.add_argument("--no-configs", action="store_true", help="skip the config-1 (tri-att N = 384) and config-4 (big, N = 2048) legs")
-    ap.add_argument("--probe", default=None, help="launch-only run for counter passes: triattn_core | trimul | transition | pair_block | copy")
+    ap.add_argument("--probe", default=None, help="a run for rocprofv3: triattn_core | trimul | transition | pair_block | trunk | big | copy")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: this build runs the pair stack on a single MI355X (multi-GPU row sharding is a design "
