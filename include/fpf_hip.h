@@ -9,7 +9,9 @@
  *     never synchronises the host, so calls are capture-safe and reentrant across host threads and streams;
  *   - shapes are 64-bit; strides are in ELEMENTS;
  *   - dtype codes: FPF_DT_BF16 = bf16 storage with fp32 accumulation and softmax (the "fast" tier), FPF_DT_F32 = fp32
- *     storage and fp32 arithmetic throughout (the "exact" tier).
+ *     storage and fp32 arithmetic throughout (the "exact" tier), FPF_DT_F32Z_BF16 (the triangle multiplication only) = fp32
+ *     z and out with bf16 operands: the reference's f32z_bf16 class (kernels/trimul/__init__.py:219, an fp32 pair tensor
+ *     under bf16 autocast), whose fused rows read z rounded once to bf16 (compute_input, :1248).
  *
  * The reference interface each entry point replaces is cited on its declaration (paths under the reference tree).
  */
@@ -23,16 +25,17 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 8   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+#define FPF_ABI_VERSION 9   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
                                5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
                                6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
                                   (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes);
                                7: the v_layout 2 core's bias (and fpf_triattn_bias_fwd's output for such N) in 32 x 32
                                   register-order blocks;
                                8: the trimul rows mode (FpfTrimulArgs.row0 / rows / fixed_in, fpf_trimul_fixed_fwd,
-                                  fpf_trimul_fixed_bytes, fpf_trimul_rows_workspace_bytes) */
+                                  fpf_trimul_fixed_bytes, fpf_trimul_rows_workspace_bytes);
+                               9: FPF_DT_F32Z_BF16 for the trimul (fp32 z / out, bf16 operands and planes) */
 
-enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3 };
+enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3, FPF_DT_F32Z_BF16 = 4 };
 enum {
   FPF_OK = 0,
   FPF_E_VERSION = 1,   /* abi_version mismatch */
@@ -101,7 +104,8 @@ int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char* err, size
  * transposed), the batched contraction over k, K3 (LN_out + W_o + output gate + residual). */
 typedef struct {
   int32_t abi_version;
-  int32_t dtype;           /* FPF_DT_BF16 (z, out, w_* bf16) | FPF_DT_F32 */
+  int32_t dtype;           /* FPF_DT_BF16 (z, out, w_* bf16) | FPF_DT_F32 | FPF_DT_F32Z_BF16 (z, out fp32; w_* bf16; the LayerNorm
+                              and the gate read z rounded to bf16, the residual adds the fp32 z; whole op only, no rows mode) */
   int32_t c_z;             /* bf16: 128 */
   int32_t c_h;             /* bf16: 128 */
   int64_t batch;

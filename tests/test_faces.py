@@ -221,9 +221,11 @@ def test_select_keywords_are_served_or_refused_by_name():
     assert TA.admits("hip_gfx950", (9, 5), "bf16", 32, 4, 768) == (True, "ok")
     assert TA.admits("hip_gfx950", (9, 5), "bf16", 16, 4, 768) == (False, "no_row:head_dim16")
     assert TA.admits("cuda_sm90a", (9, 5), "bf16", 32, 4, 768)[0] is False
-    with pytest.raises(TM.Refusal) as e:
-        TM.select((9, 5), "bf16", 128, 128, 400, "outgoing", word="fast", residency="fp32")
-    assert e.value.kind.startswith("precision:f32z_bf16") or e.value.kind == "precision:f32z_bf16"
+    # the f32z_bf16 class (an fp32 pair tensor under bf16 autocast) is served by the bf16 row (fp32 z / out, bf16 operands)
+    assert TM.select((9, 5), "bf16", 128, 128, 400, "outgoing", word="fast", residency="fp32").row == "hip_gfx950"
+    assert TM.admits("hip_gfx950", (9, 5), "bf16", 128, 128, 400, residency="fp32") is None
+    assert TM.call_precision(torch.zeros(2, 2, 2, 128))[0] == "fp32"
+    assert TM.call_precision(torch.zeros(2, 2, 2, 128, dtype=torch.bfloat16)) == ("bf16", torch.bfloat16)
 
 
 def test_kit_transition_select_and_ln_given_refusal():

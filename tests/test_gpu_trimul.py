@@ -164,6 +164,49 @@ def test_trimul_fp32_exact_batch_residual_ragged(direction):
     assert_f32_close(out, ref, "trimul fp32 %s B2 N%d residual" % (direction, N))
 
 
+# ---------------------------------------------------------------------------------------------------------- the f32z_bf16 class
+def test_trimul_f32z_reference_case_under_autocast():
+    """The reference-held case c128x128_n400_out_f32z_res1_mnone_fast (tests/golden/trimul_cases.json): an fp32 z and fp32
+    weights under bf16 autocast -- the f32z_bf16 class, served by the bf16 row with fp32 z / out -- against the fp64
+    statement, next to the reference's recorded numbers for its fast row."""
+    from fpf_hip.kernels import trimul as TM
+    case = [c for c in TRIMUL if c["id"] == "c128x128_n400_out_f32z_res1_mnone_fast"][0]
+    z, mask, w = V.trimul_inputs(case)
+    assert z.dtype == torch.float32 and mask is None
+    print("[case] %s" % case["id"], flush=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = TM.triangle_multiplication(z.to(DEV), None, direction=case["direction"], weights=_dev(w), word="fast", residual=True)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    ref = S.trimul(z, None, direction=case["direction"], weights=w, residual=True, dtype=torch.float64)
+    assert_bf16_close(out, ref, case["id"])
+    rec = case["expected"]["sm80"]["numerics"]
+    print("[parity] %s ours max_abs=%.3e rel_rms=%.3e | reference fast row (sm80) max_abs=%.3e rel_rms=%.3e" % (
+        case["id"], max_abs(out, ref), rel_l2(out, ref), rec["max_abs_fp64"], rec["rel_rms_fp64"]))
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_f32z_update_is_the_bf16_update_of_the_rounded_z(direction):
+    """The f32z_bf16 kernels read z rounded once to bf16 (the reference's compute_input): their fp32 update, rounded to bf16,
+    is the bf16 row's update on z.to(bfloat16) bit for bit; the residual form adds the fp32 z.  Ragged mask, N = 300."""
+    from fpf_hip.kernels import trimul as TM
+    N = 300
+    w = _weights(128, 21, torch.bfloat16)
+    g = torch.Generator().manual_seed(22)
+    z = torch.randn(N, N, 128, generator=g).to(DEV)
+    mask = torch.ones(N, N)
+    mask[N - 5:, :] = 0
+    mask = mask.to(DEV)
+    sel = TM.select((9, 5), "bf16", 128, 128, N, direction, word="fast", residency="fp32")
+    u32 = TM.triangle_multiplication(z, mask, direction=direction, weights=_dev(w), selection=sel)
+    u16 = TM.triangle_multiplication(z.to(torch.bfloat16), mask, direction=direction, weights=_dev(w), word="fast")
+    r32 = TM.triangle_multiplication(z, mask, direction=direction, weights=_dev(w), selection=sel, residual=True)
+    torch.cuda.synchronize()
+    assert u32.dtype == torch.float32 and u16.dtype == torch.bfloat16
+    assert torch.equal(u32.to(torch.bfloat16), u16)
+    assert torch.equal(r32, z + u32)
+
+
 def test_trimul_fp32_narrow_channels_scalar_path():
     """c_z = c_h = 64 is served by the scalar fp32 kernels (the matrix-core form is built for 128)."""
     from fpf_hip.kernels import trimul as TM

@@ -37,6 +37,17 @@ __device__ __forceinline__ void rt_load(const uint16_t* __restrict__ row, bool l
   for (int t = 0; t < 8; ++t) raw[t] = live ? *reinterpret_cast<const u32x4*>(row + 8 * rt_chunk(t, g)) : u32x4{0, 0, 0, 0};
 }
 
+// The same half row read from fp32 storage and rounded to bf16 (round to nearest even), the compute input of the
+// fp32-resident form: a kernel reading it sees exactly the bf16 copy of the row.
+__device__ __forceinline__ void rt_load_f32(const float* __restrict__ row, bool live, int g, u32x4 (&raw)[8]) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const f32x4 a = live ? *reinterpret_cast<const f32x4*>(row + 8 * rt_chunk(t, g)) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 b = live ? *reinterpret_cast<const f32x4*>(row + 8 * rt_chunk(t, g) + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    raw[t] = u32x4{pack2(a[0], a[1]), pack2(a[2], a[3]), pack2(b[0], b[1]), pack2(b[2], b[3])};
+  }
+}
+
 // LayerNorm over the 128 channels split across lanes n and n + 32 (fp32 statistics, two-pass variance), packed to bf16
 // B-operand fragments.  gb = the affine parameters staged in LDS as fp32 [gamma 128 | beta 128] (rt_stage_affine).
 __device__ __forceinline__ void rt_ln(const u32x4 (&raw)[8], int g, const float* __restrict__ gb, float eps, bf16x8 (&xb)[8]) {

@@ -35,7 +35,9 @@ __device__ __forceinline__ int64_t tl_off(int64_t b, int64_t c, int64_t P, int64
 // ---------------------------------------------------------------------------------------------------------------- K1 (bf16)
 // Persistent: the four [128 x 128] projection weights live in LDS (139 KB) for the workgroup's lifetime; each wave walks
 // 32-column plane tiles (plane row P, columns Q0 .. Q0+31), prefetching the next tile's 32 z rows while it computes.
-__global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict__ z, const float* __restrict__ mask,
+// ZF32: z is fp32 (the fp32-resident form); each tile's rows are read and rounded to bf16 at the start of its iteration.
+template <bool ZF32>
+__global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z, const float* __restrict__ mask,
                                                       const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
                                                       const uint16_t* __restrict__ w_ap, const uint16_t* __restrict__ w_ag,
                                                       const uint16_t* __restrict__ w_bp, const uint16_t* __restrict__ w_bg,
@@ -60,10 +62,12 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
     const int64_t b = tl.b, P = tl.r, Q = tl.c * 32 + n;
     const bool live = P < N && Q < N;
     const int64_t pix = (b * N + (outgoing ? P : Q)) * N + (outgoing ? Q : P);
-    rt_load(z + (live ? pix : 0) * RT_C, live, g, raw);
+    if constexpr (ZF32) rt_load_f32(static_cast<const float*>(z) + (live ? pix : 0) * RT_C, live, g, raw);
+    else rt_load(static_cast<const uint16_t*>(z) + (live ? pix : 0) * RT_C, live, g, raw);
   };
-  if (t < total) fetch(t);
+  if (!ZF32 && t < total) fetch(t);
   for (; t < total; t += stride) {
+    if constexpr (ZF32) fetch(t);
     const RtTile tl = rt_tile(t, per_b, tpr);
     const int64_t b = tl.b, P = tl.r, Q = tl.c * 32 + n;
     const bool live = P < N && Q < N;
@@ -72,7 +76,7 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const uint16_t* __restrict
     const bool ones = __builtin_amdgcn_ballot_w64(m != 1.0f) == 0;   // every pixel of the tile kept: no mask products
     bf16x8 xb[8];
     rt_ln(raw, g, sLN, eps, xb);
-    if (t + stride < total) fetch(t + stride);
+    if (!ZF32 && t + stride < total) fetch(t + stride);
     // the swapped products put the channel on the lanes and 16 pixels of the tile in the registers: the pixel masks come back
     // from LDS in that order (pixels c_row(v, g) = four runs of 4), and after the lane exchange each lane stores two runs of 8
     // consecutive plane columns
@@ -367,7 +371,10 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
 // LayerNorm read).
 constexpr int K3_XLD = RT_C + 8;     // LDS pitch of the staged X tile, pixel-major [32 pixels][128 channels]
 
-__global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint16_t* out, const uint16_t* __restrict__ X,
+// ZF32: z and out are fp32 (the fp32-resident form): LN_in reads the bf16 copy of each row, the residual adds the fp32 z
+// and the result is stored in fp32.
+template <bool ZF32>
+__global__ void __launch_bounds__(512) trimul_k3_bf16(const void* zin, void* out, const uint16_t* __restrict__ X,
                                                       const float* __restrict__ ln_in_w, const float* __restrict__ ln_in_b,
                                                       const float* __restrict__ ln_out_w, const float* __restrict__ ln_out_b, float eps,
                                                       const uint16_t* __restrict__ w_o, const uint16_t* __restrict__ w_og,
@@ -399,7 +406,8 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
     const int64_t b = tl.b, i = i0 + tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
     const int64_t pix = (b * N + i) * N + j;
-    rt_load(zin + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
+    if constexpr (ZF32) rt_load_f32(static_cast<const float*>(zin) + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
+    else rt_load(static_cast<const uint16_t*>(zin) + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, rz);
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
       const int q = l + 64 * it, c = q >> 2, p0 = (q & 3) * 8;
@@ -434,16 +442,32 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const uint16_t* zin, uint1
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
         const int64_t c0 = pix * RT_C + cb * 32 + 16 * h2 + 8 * g;
-        if (residual) {
-          const u32x4 r = rz[2 * cb + h2];                  // z rows chunk 2cb + h2: channels cb*32 + 16 h2 + 8g .. +7
+        if constexpr (ZF32) {
+          float* of = static_cast<float*>(out) + c0;
+          if (residual) {
+            const float* zf = static_cast<const float*>(zin) + c0;
+            const f32x4 r0 = *reinterpret_cast<const f32x4*>(zf), r1 = *reinterpret_cast<const f32x4*>(zf + 4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            y[8 * h2 + 2 * e] += lo_bf(r[e]);
-            y[8 * h2 + 2 * e + 1] += hi_bf(r[e]);
+            for (int e = 0; e < 4; ++e) {
+              y[8 * h2 + e] += r0[e];
+              y[8 * h2 + 4 + e] += r1[e];
+            }
           }
+          *reinterpret_cast<f32x4*>(of) = f32x4{y[8 * h2], y[8 * h2 + 1], y[8 * h2 + 2], y[8 * h2 + 3]};
+          *reinterpret_cast<f32x4*>(of + 4) = f32x4{y[8 * h2 + 4], y[8 * h2 + 5], y[8 * h2 + 6], y[8 * h2 + 7]};
+        } else {
+          if (residual) {
+            const u32x4 r = rz[2 * cb + h2];                  // z rows chunk 2cb + h2: channels cb*32 + 16 h2 + 8g .. +7
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              y[8 * h2 + 2 * e] += lo_bf(r[e]);
+              y[8 * h2 + 2 * e + 1] += hi_bf(r[e]);
+            }
+          }
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + c0) =
+              u32x4{pack2(y[8 * h2], y[8 * h2 + 1]), pack2(y[8 * h2 + 2], y[8 * h2 + 3]), pack2(y[8 * h2 + 4], y[8 * h2 + 5]),
+                    pack2(y[8 * h2 + 6], y[8 * h2 + 7])};
         }
-        *reinterpret_cast<u32x4*>(out + c0) = u32x4{pack2(y[8 * h2], y[8 * h2 + 1]), pack2(y[8 * h2 + 2], y[8 * h2 + 3]),
-                                                    pack2(y[8 * h2 + 4], y[8 * h2 + 5]), pack2(y[8 * h2 + 6], y[8 * h2 + 7])};
       }
     }
   }
@@ -870,8 +894,9 @@ static int bf16_rows(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* pa,
   }
   if (rc) return rc;
   const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
-  hipLaunchKernelGGL(trimul_k3_bf16, dim3(k3_grid), dim3(512), 0, st, (const uint16_t*)a->z, (uint16_t*)a->out, X, a->ln_in_w, a->ln_in_b,
-                     a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np, B, a->residual, row0, rows, a0, Ra);
+  hipLaunchKernelGGL(a->dtype == FPF_DT_F32Z_BF16 ? trimul_k3_bf16<true> : trimul_k3_bf16<false>, dim3(k3_grid), dim3(512), 0, st, a->z, a->out, X,
+                     a->ln_in_w, a->ln_in_b, a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np, B,
+                     a->residual, row0, rows, a0, Ra);
   return launched(err, errlen, "trimul_k3_bf16");
 }
 
@@ -881,7 +906,8 @@ static int bf16_planes(const FpfTrimulArgs* a, hipStream_t st, uint16_t* pa, uin
   const int64_t k1_tiles = B * Np * (Np / 32);
   if (!rt_tiles_ok(k1_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
   const unsigned k1_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k1_tiles, RT_WAVES));
-  hipLaunchKernelGGL(trimul_k1_bf16, dim3(k1_grid), dim3(512), 0, st, (const uint16_t*)a->z, a->mask, a->ln_in_w, a->ln_in_b, a->eps,
+  hipLaunchKernelGGL(a->dtype == FPF_DT_F32Z_BF16 ? trimul_k1_bf16<true> : trimul_k1_bf16<false>, dim3(k1_grid), dim3(512), 0, st, a->z,
+                     a->mask, a->ln_in_w, a->ln_in_b, a->eps,
                      (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B,
                      a->outgoing);
   return launched(err, errlen, "trimul_k1_bf16");
@@ -959,7 +985,7 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
   const size_t need = fpf_trimul_workspace_bytes(a->batch, a->n, a->c_z, a->c_h, a->dtype);
   if (!a->workspace || a->workspace_bytes < need)
     return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
-  if (a->dtype == FPF_DT_BF16) {
+  if (a->dtype == FPF_DT_BF16 || a->dtype == FPF_DT_F32Z_BF16) {    // bf16 planes; z / out bf16, or fp32 (the fp32-resident form)
     int rc = bf16_checks(a, err, errlen);
     if (rc) return rc;
     if (!aligned16(a->workspace)) return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");

@@ -41,8 +41,23 @@ def precision_word(dtype, residency=None, tf32=None):
 
 
 def _class_of(prec):
-    """precision class -> the dtype word the row resolution keys on ('tf32' is served by the fp32 row: it meets that class)."""
-    return {"bf16": "bf16", "fp32": "fp32", "tf32": "fp32"}.get(prec)
+    """precision class -> the dtype word the row resolution keys on ('tf32' is served by the fp32 row: it meets that class;
+    'f32z_bf16' by the bf16 row, which reads the fp32 z rounded to bf16 and writes fp32)."""
+    return {"bf16": "bf16", "f32z_bf16": "bf16", "fp32": "fp32", "tf32": "fp32"}.get(prec)
+
+
+def call_precision(z, residency=None):
+    """(precision word, compute dtype) of a live call (common/opt_core/opt_core/kernels/trimul/__init__.py:1293): an fp32 z under
+    bf16 autocast on its device -- or with ``residency="fp32"`` and a bf16 compute request made through ``select`` -- is the
+    f32z_bf16 class; else z's own dtype (fp32 with TF32 matmuls allowed is tf32)."""
+    if z.dtype == torch.float32:
+        dev = z.device.type
+        ac = torch.is_autocast_enabled(dev) and torch.get_autocast_dtype(dev) == torch.bfloat16 if dev == "cuda" else False
+        if ac:
+            return "f32z_bf16", torch.bfloat16
+        tf = bool(torch.backends.cuda.matmul.allow_tf32) or torch.get_float32_matmul_precision() != "highest"
+        return ("tf32" if tf else "fp32"), torch.float32
+    return precision_word(z.dtype, residency), z.dtype
 
 
 def admits(row, cc, dtype, c_z, c_hidden, n_tokens, *, residency=None, backward=False, residual=None, batch=1, abi=None, has_cueq=None,
@@ -119,14 +134,29 @@ def triangle_multiplication(z, mask=None, *, direction, weights, word=None, sele
         raise ValueError("z must be [B,N,N,c] or [N,N,c] (got %s)" % (tuple(z.shape),))
     d = direction_word(direction)
     Ch = int(weights["w_ap"].shape[0])
-    sel = selection or select(z, z.dtype, Cz, Ch, N, d, word=word, residency=residency, prefer=prefer, config=config, form=form, batch=B)
+    prec, cdt = call_precision(z4)
+    if selection is None:
+        f32z = prec == "f32z_bf16"
+        sel = select(z, "bf16" if f32z else z.dtype, Cz, Ch, N, d, word=word, residency="fp32" if f32z else residency, prefer=prefer,
+                     config=config, form=form, batch=B, tf32=prec == "tf32")
+    else:
+        sel = selection
     if (sel.row == F.ROW_FAST and str(contract) != "bf16") or str(contract) not in ("bf16", "fp32", "f32", "tf32"):
         raise Refusal("contract:%s" % contract, sel.row, F.ROW_F32 if sel.row == F.ROW_FAST else F.ROW_STOCK,
                       "row %s contracts in %s" % (sel.row, "bf16" if sel.row == F.ROW_FAST else "fp32"))
     if not z4.is_contiguous():
         raise Refusal("stride", sel.row, F.ROW_STOCK, "z must be contiguous")
     F.check_device("trimul", sel.row, z.device, out=out)
-    p = _pack(weights, z.dtype, z.device, cache)
+    # the bf16 row on an fp32 z is the f32z_bf16 class (bf16 operands, fp32 z / out); the fp32 row takes fp32 z only
+    if sel.row == F.ROW_FAST and z.dtype == torch.float32:
+        dt, wdt = L.DT_F32Z_BF16, torch.bfloat16
+    elif sel.row == F.ROW_FAST and z.dtype == torch.bfloat16:
+        dt, wdt = L.DT_BF16, torch.bfloat16
+    elif sel.row == F.ROW_F32 and z.dtype == torch.float32:
+        dt, wdt = L.DT_F32, torch.float32
+    else:
+        raise Refusal("precision:%s" % F.dtype_of(z.dtype), sel.row, F.ROW_STOCK, "row %s does not serve a %s z" % (sel.row, z.dtype))
+    p = _pack(weights, wdt, z.device, cache)
     m = None
     if mask is not None:
         m = mask if mask.dim() == 3 else mask.unsqueeze(0)
@@ -139,7 +169,6 @@ def triangle_multiplication(z, mask=None, *, direction, weights, word=None, sele
         raise Refusal("out", sel.row, F.ROW_STOCK, "out must be contiguous with z's shape and dtype")
     if out.data_ptr() == z.data_ptr() and not residual:
         raise Refusal("out_aliases_z", sel.row, F.ROW_STOCK, "out may alias z only for the residual form")
-    dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
     need = L.lib().fpf_trimul_workspace_bytes(B, N, Cz, Ch, dt)
     ws = F.scratch(z.device, need)
     a = _args(z4, out, m, p, d, residual, eps, dt, Cz, Ch, ws)
@@ -169,7 +198,8 @@ def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, 
 
     ``mode="channels"`` (the reference's channel-block operands with a full product) is refused by name: the whole-op kernels
     already never hold a channel-split plane.  An fp32 call (row hip_gfx950_f32) runs the whole op when ``fp32`` is
-    ``"passthrough"`` or ``"band"`` (the result is the whole op's, which meets either label) and is refused for ``"refuse"``."""
+    ``"passthrough"`` or ``"band"`` (the result is the whole op's, which meets either label) and is refused for ``"refuse"``;
+    an fp32 z under bf16 autocast (the f32z_bf16 class) runs the whole op."""
     if str(mode) != "rows":
         raise Refusal("mode:%s" % mode, F.word_base(word), F.ROW_STOCK, "the chunked trimul serves mode rows")
     if str(fp32) not in ("passthrough", "band", "refuse"):
@@ -184,15 +214,29 @@ def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, 
         raise ValueError("z must be [B,N,N,c] or [N,N,c] (got %s)" % (tuple(z.shape),))
     d = direction_word(direction)
     Ch = int(weights["w_ap"].shape[0])
-    sel = selection or select(z, z.dtype, Cz, Ch, N, d, word=word, residency=residency, prefer=prefer, batch=B)
-    if sel.row != F.ROW_FAST:
+    prec, _ = call_precision(z4)
+    f32z = prec == "f32z_bf16"
+    sel = selection or select(z, "bf16" if f32z else z.dtype, Cz, Ch, N, d, word=word, residency="fp32" if f32z else residency, prefer=prefer,
+                              batch=B, tf32=prec == "tf32")
+    if sel.row != F.ROW_FAST or z.dtype != torch.bfloat16:      # fp32 and the f32z_bf16 class: the whole op
+        if sel.row == F.ROW_FAST:
+            return triangle_multiplication(z, mask, direction=d, weights=weights, selection=sel, residual=residual, cache=cache, eps=eps, out=out)
         if str(fp32) == "refuse":
             raise Refusal("fp32_site", sel.row, F.ROW_STOCK, "an fp32 trimul is not chunked (fp32='refuse')")
         return triangle_multiplication(z, mask, direction=d, weights=weights, selection=sel, residual=residual, cache=cache, eps=eps, out=out)
     if not z4.is_contiguous():
         raise Refusal("stride", sel.row, F.ROW_STOCK, "z must be contiguous")
     F.check_device("trimul", sel.row, z.device, out=out)
-    p = _pack(weights, z.dtype, z.device, cache)
+    # the bf16 row on an fp32 z is the f32z_bf16 class (bf16 operands, fp32 z / out); the fp32 row takes fp32 z only
+    if sel.row == F.ROW_FAST and z.dtype == torch.float32:
+        dt, wdt = L.DT_F32Z_BF16, torch.bfloat16
+    elif sel.row == F.ROW_FAST and z.dtype == torch.bfloat16:
+        dt, wdt = L.DT_BF16, torch.bfloat16
+    elif sel.row == F.ROW_F32 and z.dtype == torch.float32:
+        dt, wdt = L.DT_F32, torch.float32
+    else:
+        raise Refusal("precision:%s" % F.dtype_of(z.dtype), sel.row, F.ROW_STOCK, "row %s does not serve a %s z" % (sel.row, z.dtype))
+    p = _pack(weights, wdt, z.device, cache)
     m = None
     if mask is not None:
         m = mask if mask.dim() == 3 else mask.unsqueeze(0)
