@@ -601,3 +601,23 @@ def test_single_track_with_zero_outputs_is_identity():
     g = torch.Generator().manual_seed(11)
     s = torch.randn(1, 5, 48, generator=g, dtype=torch.float64)
     assert torch.equal(S.single_track(s, torch.randn(1, 5, 5, 128, generator=g), torch.ones(1, 5), P), s)
+
+
+def test_single_track_one_token_closed_form():
+    """One token: the attention over its single key is sigmoid(s_n W_g^T) * (s_n W_v^T), projected by W_o, with s_n the
+    LayerNorm of s (library routine), so the sequence stack is s1 = s + that, then s1 + transition(s1).  A wiring that
+    attends over s instead of s_n, or applies the transition to s or s_n instead of s1, fails here (the transition is
+    pinned by its own vectors)."""
+    P = _single_params(4)
+    a, t = P["apb"], P["trs"]
+    g = torch.Generator().manual_seed(12)
+    s = torch.randn(1, 1, 48, generator=g, dtype=torch.float64)
+    z = torch.randn(1, 1, 1, 128, generator=g, dtype=torch.float64)
+    sn = torch.nn.functional.layer_norm(s, (48,), a["ln_s_w"].double(), a["ln_s_b"].double(), 1e-5)
+    att = (torch.sigmoid(sn @ a["w_g"].double().t()) * (sn @ a["w_v"].double().t())) @ a["w_o"].double().t()
+    s1 = s + att
+    want = s1 + S.transition(s1, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"])
+    got = S.single_track(s, z, torch.ones(1, 1), P)
+    assert torch.allclose(got, want, atol=1e-12)
+    wrong = s1 + S.transition(s, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"])
+    assert not torch.allclose(got, wrong, atol=1e-6)
