@@ -91,6 +91,7 @@ def test_integration_stub_sends_the_header_version():
     assert hdr == L.ABI_VERSION
     txt = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     lits = [int(x) for x in re.findall(r"abi_version\s*=\s*(\d+)", txt)] + [int(x) for x in re.findall(r"fpf_abi_version\(\)\s*==\s*(\d+)", txt)]
+    lits += [int(x) for x in re.findall(r"\((\d+) for this header\)", txt)]
     assert all(v == hdr for v in lits), lits
     assert "abi_version=ABI" in txt and "fpf_abi_version()" in txt
 
