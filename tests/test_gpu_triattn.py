@@ -204,6 +204,31 @@ def test_block_bf16_mask_frames_asymmetric_mask(ending, N):
 
 
 @pytest.mark.parametrize("ending", [False, True])
+def test_block_keep_table_builders_agree(ending):
+    """The keep table's two builders -- 16-byte loads for a contiguous u8 mask (attention frame), one byte per lane for an
+    fp32 or strided mask (z frame) -- give the same block output bit for bit at N = 1088 (keys past 1024: a second load
+    round), with a dead row (no key kept: uniform attention) and a fully kept row next to a random pattern."""
+    from fpf_hip import _lib as L
+    P = _block_weights(torch.bfloat16, seed=5)
+    W = _pack(P, torch.bfloat16)
+    N = 1088
+    g = torch.Generator().manual_seed(11)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16)
+    mask = (torch.rand(1, N, N, generator=g) > 0.25).float()
+    mask[:, 7, :] = 0                                    # row 7: no key kept
+    mask[:, 9, :] = 1                                    # row 9: every key kept
+    mask[:, :, N - 70:] = 0                              # the last keys (the second load round) off
+    print("[case] keep builders ending=%s N=%d" % (ending, N), flush=True)
+    zd, md = z.to(DEV), mask.to(DEV)
+    att = (md.transpose(1, 2) if ending else md) != 0
+    u_a8 = _block_abi(zd, W, att.view(torch.uint8).contiguous(), L.DT_U8, 1, ending)
+    u_zf = _block_abi(zd, W, md.contiguous(), L.DT_F32, 0, ending)
+    torch.cuda.synchronize()
+    assert torch.equal(u_a8, u_zf), "the u8 and fp32 keep-table builders differ"
+    assert torch.isfinite(u_a8.float()).all()
+
+
+@pytest.mark.parametrize("ending", [False, True])
 def test_block_fp32_exact(ending):
     from fpf_hip.attn import pair_fused as PF
     P = _block_weights(torch.float32, seed=1)

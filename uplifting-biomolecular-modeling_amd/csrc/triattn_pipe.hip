@@ -29,7 +29,7 @@
 // the fallback kernel, which repeats the sums in a first pass and uses the query's max as the reference where they are
 // out of range (and 0 elsewhere, so both kernels produce the same bits for every other query).  Tiles where every key of
 // the TA_R rows is kept and no row is dead run with no mask code at all; the keep bits come from a table built once per
-// call (triattn_keep_bits), so the key loop never reads the mask.
+// call (triattn_keep_bits_u8 / triattn_keep_bits), so the key loop never reads the mask.
 #include <algorithm>
 
 #include "triattn.h"
@@ -71,6 +71,39 @@ __global__ void __launch_bounds__(256) triattn_keep_bits(const void* __restrict_
   if (l < nw) out[1 + l] = any ? mine0 : ~0ull;
   if (64 + l < nw) out[65 + l] = any ? mine1 : ~0ull;
   if (l == 0) out[0] = (any ? TK_ALIVE : 0) | (all == ~0ull ? TK_FULL : 0);
+}
+
+// The same table from a u8 mask with contiguous keys and 16-byte aligned rows: lane l loads keys 1024 c + 16 l .. +15 in one
+// 16-byte load, turns each byte into its keep bit with word arithmetic, and lanes 4 T .. 4 T + 3 assemble word T.
+__device__ __forceinline__ uint32_t kb_nibble(uint32_t w) {    // bit e = (byte e of w != 0), e = 0 .. 3
+  const uint32_t hi = (((w & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | w) & 0x80808080u;   // bit 8 e + 7: byte e is nonzero
+  return ((hi >> 7) * 0x10204080u) >> 28;                   // bits 0, 8, 16, 24 gathered to 28 .. 31 (no two products meet)
+}
+__global__ void __launch_bounds__(256) triattn_keep_bits_u8(const uint8_t* __restrict__ mask, int64_t ms0, int64_t ms1, int64_t B, int64_t N,
+                                                              int64_t S, uint64_t* __restrict__ keep) {
+  const int l = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= B * N) return;
+  const int64_t b = row / N, i = row - b * N;
+  const uint8_t* src = mask + b * ms0 + i * ms1;
+  uint64_t* out = keep + row * keep_words(S);
+  bool any = false, all = true;
+  for (int64_t c0 = 0; c0 < S; c0 += 1024) {
+    const int64_t k0 = c0 + 16 * l;
+    const bool valid = k0 < S;
+    const u32x4 v = valid ? *reinterpret_cast<const u32x4*>(src + k0) : u32x4{0, 0, 0, 0};
+    const uint32_t piece = kb_nibble(v[0]) | (kb_nibble(v[1]) << 4) | (kb_nibble(v[2]) << 8) | (kb_nibble(v[3]) << 12);
+    any |= __builtin_amdgcn_ballot_w64(valid && piece != 0) != 0;
+    all &= __builtin_amdgcn_ballot_w64(valid && piece != 0xFFFFu) == 0;
+    // lanes 4 T + 1 .. 4 T + 3 hand their pieces to lane 4 T (keys 64 T + 16 .. 64 T + 63)
+    const uint32_t p1 = __shfl_down(piece, 1), p2 = __shfl_down(piece, 2), p3 = __shfl_down(piece, 3);
+    if ((l & 3) == 0 && valid)
+      out[1 + (c0 >> 6) + (l >> 2)] = (uint64_t)(piece | (p1 << 16)) | ((uint64_t)(p2 | (p3 << 16)) << 32);
+  }
+  if (!any) {                                               // no kept key: every bit set (the row attends uniformly)
+    for (int64_t w = l; w < S / 64; w += 64) out[1 + w] = ~0ull;
+  }
+  if (l == 0) out[0] = (any ? TK_ALIVE : 0) | (all ? TK_FULL : 0);
 }
 
 // ---------------------------------------------------------------------------------------------------------------- core
@@ -769,6 +802,10 @@ int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64
   if (S % TA_KT != 0 || S > (int64_t)TA_KT * TA_MAXW) return fail(err, errlen, FPF_E_SHAPE, "keep table: S a multiple of 64 up to %d", TA_KT * TA_MAXW);
   const int64_t blocks = cdiv(B * N, 4);
   if (blocks > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "keep table: grid too large");
+  if (!mask_f32 && ms[2] == 1 && aligned16(mask) && ms[0] % 16 == 0 && ms[1] % 16 == 0) {
+    hipLaunchKernelGGL(triattn_keep_bits_u8, dim3((unsigned)blocks), dim3(256), 0, st, static_cast<const uint8_t*>(mask), ms[0], ms[1], B, N, S, keep);
+    return launched(err, errlen, "triattn_keep_bits_u8");
+  }
   hipLaunchKernelGGL(triattn_keep_bits, dim3((unsigned)blocks), dim3(256), 0, st, mask, mask_f32, ms[0], ms[1], ms[2], B, N, S, keep);
   return launched(err, errlen, "triattn_keep_bits");
 }
