@@ -6,7 +6,10 @@
 // computed transposed, a^T = W_a n^T, so its D layout (lane = pixel, 16 hidden values) IS the B operand of GEMM 2
 // out^T = W_o h^T once the hidden index of each k-step is permuted the same way in W_o: the 4c hidden never leaves the
 // registers.  Weights stream through a 3-buffer LDS ring in 32-hidden chunks shared by the 4 waves of a workgroup (the next
-// two chunks' transfers are in flight while the current one feeds the MFMAs; one barrier per chunk).
+// two chunks' transfers are in flight while the current one feeds the MFMAs; one barrier per chunk).  The grid is persistent
+// (two workgroups per CU, each walking every grid-th 128-pixel tile) and the ring runs across tiles, so the weight stream
+// starts once per workgroup; the kernel holds 241 VGPRs without spills (a workgroup per tile spilled 23 of them, whose
+// scratch traffic doubled the kernel's HBM bytes).
 // fp32 path (exact tier): c = 128 on the fp32 matrix core (transition_f32_mfma), other widths LDS-tiled scalar FMA.
 #include "rowtile.h"
 
@@ -34,11 +37,14 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   __shared__ __attribute__((aligned(16))) uint16_t sWb[TR_NBUF][TR_HB * TR_C];
   __shared__ __attribute__((aligned(16))) uint16_t sWo[TR_NBUF][TR_C * TR_HB];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t pix0 = ((int64_t)blockIdx.x * NW + wave) * (32 * PW);
   // DMA map: slot sl = tid + 64 NW q of each 512-slot matrix chunk (each wave instruction fills 64 contiguous slots)
   constexpr int NQ = 512 / (64 * NW);
-  auto issue = [&](int hb) {
-    const int buf = hb % TR_NBUF;
+  const int nhb = hidden / TR_HB;
+  const int64_t ntiles = cdiv(rows, (int64_t)32 * PW * NW);
+  const int nkt = (int)((ntiles - blockIdx.x + gridDim.x - 1) / gridDim.x);   // tiles of this workgroup (the grid is <= ntiles)
+  const int U = nkt * nhb;                                                     // weight chunks it streams
+  static_assert(TR_NBUF == 3, "the ring indices below step through 3 buffers");
+  auto issue = [&](int buf, int hb) {   // chunk hb of the hidden into ring buffer buf
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int sl = tid + 64 * NW * q;
@@ -52,11 +58,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   };
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
   rt_stage_affine(sLN, ln_w, ln_b, tid, 64 * NW);
-  const int nhb = hidden / TR_HB;
-#pragma unroll
-  for (int q = 0; q < TR_NBUF - 1; ++q)
-    if (q < nhb) issue(q);
+  issue(0, 0);
+  if (U > 1) issue(1, nhb > 1 ? 1 : 0);
+  int buf = 0;                                         // ring buffer of chunk u (u mod 3)
   __syncthreads();                                     // sLN visible
+  for (int kt = 0; kt < nkt; ++kt) {
+  const int64_t pix0 = ((int64_t)(blockIdx.x + (int64_t)kt * gridDim.x) * NW + wave) * (32 * PW);
   bf16x8 xb[PW][TR_KS];
 #pragma unroll
   for (int p = 0; p < PW; ++p) {
@@ -65,17 +72,22 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     rt_load(x + (pix < rows ? pix : 0) * TR_C, pix < rows, g, raw);
     rt_ln(raw, g, sLN, eps, xb[p]);
   }
-  // chunk 0 landed (the row loads above are younger and may still be counted), then published
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+  if (kt == 0) {
+    // chunk 0 landed (the row loads above are younger and may still be counted), then published
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
   f32x16 acc[PW][4];
 #pragma unroll
   for (int p = 0; p < PW; ++p)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) acc[p][cb] = f32x16{};
   for (int hb = 0; hb < nhb; ++hb) {
-    const int buf = hb % TR_NBUF;
-    if (hb + TR_NBUF - 1 < nhb) issue(hb + TR_NBUF - 1);  // its buffer held chunk hb - 1, finished before the last barrier
+    const int u = kt * nhb + hb;
+    if (u + 2 < U) {                                   // chunk u + 2: its buffer held chunk u - 1, finished before the last barrier
+      const int h2 = hb + 2;
+      issue(buf == 0 ? 2 : buf - 1, h2 < nhb ? h2 : (h2 - nhb < nhb ? h2 - nhb : 0));
+    }
     f32x16 a[PW], b[PW];
 #pragma unroll
     for (int p = 0; p < PW; ++p) {
@@ -132,18 +144,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (hb + 1 < nhb) {                          // chunk hb + 1 landed: only chunk hb + 2's transfers (3 NQ) may be outstanding
+    if (u + 1 < U) {                             // chunk u + 1 landed: only chunk u + 2's transfers (3 NQ) may be outstanding
       static_assert(TR_NBUF == 3, "the waits below count one chunk in flight behind the awaited one");
       if constexpr (NQ == 1) {
-        if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+        if (u + 2 < U) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       } else {
         static_assert(NQ == 2, "4 or 8 waves");
-        if (hb + 2 < nhb) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        if (u + 2 < U) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
       __builtin_amdgcn_s_barrier();
     }
+    buf = buf == 2 ? 0 : buf + 1;
   }
   // epilogue: lane (pixel n, half g) holds c_out = 32 cb + c_row(v, g); after the lane exchange it holds channels
   // 32 cb + 8g .. +7 and 32 cb + 16 + 8g .. +7, stored (with mask and residual) in 16-byte pieces
@@ -174,6 +187,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
         *reinterpret_cast<u32x4*>(out + c0) = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
       }
     }
+  }
   }
 }
 
@@ -378,7 +392,7 @@ extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char
         (a->ln_w && !aligned16(a->ln_w)) || (a->ln_b && !aligned16(a->ln_b)))
       return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
     constexpr int PW = TR_PW, NW = TR_NW;
-    const dim3 grid((unsigned)cdiv(a->rows, 32 * NW * PW)), block(64 * NW);
+    const dim3 grid((unsigned)std::min<int64_t>(cdiv(a->rows, 32 * NW * PW), 2 * (int64_t)num_cus())), block(64 * NW);
     hipLaunchKernelGGL((transition_bf16_kernel<PW, NW>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b, a->eps,
                        (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows, a->hidden);
     return launched(err, errlen, "fpf_transition_fwd(bf16)");
