@@ -46,6 +46,30 @@ def _ragged_mask(N, chains, pad):
 
 # ------------------------------------------------------------------------------------------------------- chunked == whole
 @pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("chunk", [125, 1])
+def test_chunked_block_tiny_chunks_on_the_block_core(ending, chunk):
+    """N = 128 takes the block-layout core; a chunk of 3 rows or fewer has fewer work items (4 heads x 1 row group x 1
+    query tile) than XCDs, so the persistent grid must still give every XCD's item range a workgroup (with a grid of one
+    workgroup per item, the items of XCDs 4 .. 7 were skipped, and only a stale nonzero fallback flag hid it): chunked ==
+    whole."""
+    from fpf_hip import _face as F
+    from fpf_hip.attn import pair_fused as PF
+    N = 128
+    W = _ta_pack(_ta_weights(5))
+    g = torch.Generator().manual_seed(37)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(DEV)
+    mask = (torch.rand(1, N, N, generator=g) > 0.2).float().to(DEV)      # the last rows live: their outputs are not masked out
+    print("[big] tiny chunks N=%d chunk=%d ending=%s" % (N, chunk, ending), flush=True)
+    u1 = PF.tri_attn_block(z, W, mask, ending=ending, residual=False)
+    # a zeroed workspace (the whole block's, which the chunks reuse): an item the core skipped would keep a zero fallback flag
+    # and a zero output instead of being recomputed from whatever the buffer held
+    F.scratch(DEV, 1).zero_()
+    u2 = PF.tri_attn_block_chunked(z, W, mask, ending=ending, residual=False, chunk=chunk)
+    torch.cuda.synchronize()
+    assert torch.equal(u1, u2), "chunked != whole: max diff %.3e" % (u1.float() - u2.float()).abs().max().item()
+
+
+@pytest.mark.parametrize("ending", [False, True])
 @pytest.mark.parametrize("residual", [False, True])
 @pytest.mark.parametrize("chunk", [64, 7])
 @pytest.mark.parametrize("asym", [False, True])

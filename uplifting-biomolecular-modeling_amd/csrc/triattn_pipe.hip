@@ -830,8 +830,9 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
       p.B * p.N > lim || p.S > lim)
     return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
   // persistent grids: one fast workgroup per CU walking every nwg-th item of its XCD's range (two per CU for the 4-wave
-  // split, whose LDS and registers fit twice); the fallback scans its share of the flags
-  const dim3 grid((unsigned)std::min<int64_t>(total, (wide ? 1 : 2) * (int64_t)num_cus()));
+  // split, whose LDS and registers fit twice), and at least 8 workgroups, so that every XCD's range has one (with fewer
+  // than 8 items some of them have none to do); the fallback scans its share of the flags
+  const dim3 grid((unsigned)std::max<int64_t>(8, std::min<int64_t>(total, (wide ? 1 : 2) * (int64_t)num_cus())));
   const dim3 redo_grid((unsigned)std::min<int64_t>(total, num_cus()));
   if (wide) {
     if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, true>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
