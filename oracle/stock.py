@@ -1,7 +1,9 @@
 """The stock PyTorch statements of the pair-stack hot path, restated on the CPU -- TEST INFRASTRUCTURE ONLY.
 
 Every function evaluates in ``dtype`` (float64 by default; float32 for the fp32 yardstick the BASELINE tolerances are stated
-against) on CPU tensors and returns a tensor of that dtype.  They are the checker of the HIP path and the timed CPU baseline of
+against) on CPU tensors and returns a tensor of that dtype.  The pair-block statements also accept device tensors (inputs and
+parameters on one device; the results are allocated there): the N = 768 stack checks evaluate the same fp32 statements on the
+GPU, where the CPU would take minutes per block.  They are the checker of the HIP path and the timed CPU baseline of
 ``bench.py``; nothing in the product imports them.
 
 Reference statements followed (paths under the reference tree):
@@ -60,7 +62,7 @@ def triangle_attention_op(q, k, v, bias, mask=None, scale=None, dtype=torch.floa
     invariance, brute force (tests/test_oracle.py)."""
     B, N, H, S, D = q.shape
     sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
-    out = torch.empty(B, N, H, S, D, dtype=dtype)
+    out = torch.empty(B, N, H, S, D, dtype=dtype, device=q.device)
     bias_ = bias.to(dtype)
     for n0 in range(0, N, rows_per_step):
         n1 = min(N, n0 + rows_per_step)
@@ -90,7 +92,7 @@ def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_ste
     B, N, _, C = z4.shape
     H, D = int(P["H"]), int(P["D"])
     x = z4.to(dtype)
-    m = torch.ones(B, N, N, dtype=dtype) if mask is None else (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(dtype)
+    m = torch.ones(B, N, N, dtype=dtype, device=z4.device) if mask is None else (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(dtype)
     if ending:
         x = x.transpose(1, 2)
         m = m.transpose(1, 2)
@@ -100,7 +102,7 @@ def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_ste
     bg = None if P.get("b_g") is None else P["b_g"].to(dtype)
     bo = None if P.get("b_o") is None else P["b_o"].to(dtype)
     tri_bias = torch.matmul(x, wb.t()).permute(0, 3, 1, 2).unsqueeze(1)          # [B, 1, H, I, J]
-    out = torch.empty(B, N, N, wo.shape[0], dtype=dtype)
+    out = torch.empty(B, N, N, wo.shape[0], dtype=dtype, device=x.device)
     for i0 in range(0, N, rows_per_step):
         i1 = min(N, i0 + rows_per_step)
         xi = x[:, i0:i1]                                                            # [B, r, J, C]
@@ -302,12 +304,12 @@ def tri_attn_autocast(z, P, mask=None, *, ending=False, inf=1e9, rows_per_step=6
     B, N, _, C = z4.shape
     H, D = int(P["H"]), int(P["D"])
     x = z4.to(torch.float32)
-    m = torch.ones(B, N, N) if mask is None else (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(torch.float32)
+    m = torch.ones(B, N, N, device=z4.device) if mask is None else (mask if mask.dim() == 3 else mask.unsqueeze(0)).to(torch.float32)
     if ending:
         x, m = x.transpose(1, 2), m.transpose(1, 2)
     x = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
     tri_bias = _lin_ac(x, P["w_b"], rnd).permute(0, 3, 1, 2).unsqueeze(1)            # [B, 1, H, I, J]
-    out = torch.empty(B, N, N, P["w_o"].shape[0])
+    out = torch.empty(B, N, N, P["w_o"].shape[0], device=z4.device)
     for i0 in range(0, N, rows_per_step):
         i1 = min(N, i0 + rows_per_step)
         xi = x[:, i0:i1]

@@ -329,3 +329,20 @@ def test_shared_scratch_is_one_buffer_per_stream_sized_by_the_largest_call():
     for N, cap in ((512, 3e9), (768, 3e9)):                  # 48 layers x (2 trimul + 2 tri-att): one buffer of the largest need
         need = max(lib.fpf_trimul_workspace_bytes(1, N, 128, 128, L.DT_BF16), lib.fpf_triattn_block_workspace_bytes(1, N, 0, 128, 4, 32, L.DT_BF16))
         assert need < cap, (N, need)
+
+
+def test_shared_scratch_keeps_an_outgrown_buffer_a_captured_call_used():
+    """A buffer handed out under graph capture is marked; when a larger call outgrows it, it stays allocated (a graph replays with
+    its address), while unmarked buffers go back to the allocator; release_scratch drops both."""
+    from fpf_hip import _face as F
+    F.release_scratch()
+    t = F.scratch("cpu", 100)
+    t._fpf_captured = True                       # what a call under capture leaves on the buffer it was handed
+    t2 = F.scratch("cpu", 300)
+    assert t2.numel() >= 300 and t2.data_ptr() != t.data_ptr()
+    assert any(c is t for c in F._CAPTURED)
+    F.scratch("cpu", 600)                        # t2 was never captured: not kept
+    assert not any(c is t2 for c in F._CAPTURED)
+    assert F.reserve_scratch("cpu", 50).numel() >= 600
+    F.release_scratch()
+    assert F._CAPTURED == [] and F.scratch_bytes() == 0

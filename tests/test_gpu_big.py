@@ -98,28 +98,72 @@ def test_chunked_block_bitwise_equals_whole(ending, residual, chunk, asym):
     assert torch.equal(u1, u2), "chunked != whole: max diff %.3e" % (u1.float() - u2.float()).abs().max().item()
 
 
+def _n768_case(band):
+    """z and the asymmetric mask of the N = 768 chunk cases: a random 75 % keep pattern (seed 61), and with ``band`` a masked key
+    band 600:650 on one side only."""
+    N = 768
+    g = torch.Generator().manual_seed(61)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16)
+    mask = (torch.rand(1, N, N, generator=g) > 0.25).float()
+    if band:
+        mask[:, :, 600:650] = 0
+    return z, mask
+
+
 @pytest.mark.parametrize("ending", [False, True])
 @pytest.mark.parametrize("chunk", [256, 100])
-def test_chunked_block_bitwise_equals_whole_n768(ending, chunk):
+@pytest.mark.parametrize("band", [True, False])
+def test_chunked_block_bitwise_equals_whole_n768(ending, chunk, band):
     """The metric size: the whole block takes the 8-wave block-layout core, 256-row chunks the 4-wave one (fewer workgroups),
-    100-row chunks ranges that are not a multiple of the core's 3-row groups; with an asymmetric mask (a random keep pattern and a
-    masked key band on one side only) both must equal the whole block bit for bit."""
+    100-row chunks ranges that are not a multiple of the core's 3-row groups; with an asymmetric mask (a random keep pattern, with
+    and without a masked key band on one side only) both must be finite and equal the whole block bit for bit (torch.equal alone
+    would accept matching infinities)."""
     from fpf_hip.attn import pair_fused as PF
-    N = 768
-    P = _ta_weights(6)
-    W = _ta_pack(P)
-    g = torch.Generator().manual_seed(61)
-    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(DEV)
-    mask = (torch.rand(1, N, N, generator=g) > 0.25).float()
-    mask[:, :, 600:650] = 0
-    mask = mask.to(DEV)
-    print("[big] N=%d chunk=%d ending=%s asym" % (N, chunk, ending), flush=True)
+    W = _ta_pack(_ta_weights(6))
+    z, mask = _n768_case(band)
+    z, mask = z.to(DEV), mask.to(DEV)
+    print("[big] N=768 chunk=%d ending=%s band=%s asym" % (chunk, ending, band), flush=True)
     z1, z2 = z.clone(), z.clone()
     PF.tri_attn_block(z1, W, mask, ending=ending, residual=True)
     PF.tri_attn_block_chunked(z2, W, mask, ending=ending, residual=True, chunk=chunk)
     torch.cuda.synchronize()
+    assert torch.isfinite(z1.float()).all(), "whole block: non-finite output"
+    assert torch.isfinite(z2.float()).all(), "chunked block: non-finite output"
     assert torch.equal(z1, z2), "chunked != whole: max diff %.3e" % (z1.float() - z2.float()).abs().max().item()
     assert not torch.equal(z1, z)
+
+
+@pytest.mark.parametrize("ending", [True, False])
+def test_whole_block_n768_random_mask_finite_oracle_and_repeatable(ending):
+    """Regression for a non-finite whole-block output once seen at N = 768 on exactly this input (ending node, seed 61, a random
+    75 % keep mask with no key band, residual in place; the 256-row chunked block was finite): the 8-wave persistent core then
+    issued its LDS DMA right after the scalar write of M0 with no wait state, so a transfer could land in the ring buffer of the
+    previous M0 value and another wave read stale K / V^T.  The output must be finite, its sampled rows must match the fp32
+    statement restated per row at the bf16 bars, and 20 consecutive whole-block calls must be bitwise equal."""
+    from fpf_hip.attn import pair_fused as PF
+    N = 768
+    P = _ta_weights(6)
+    W = _ta_pack(P)
+    z, mask = _n768_case(False)
+    zd, md = z.to(DEV), mask.to(DEV)
+    print("[big] N=768 regression ending=%s no band x 20" % ending, flush=True)
+    first = zd.clone()
+    PF.tri_attn_block(first, W, md, ending=ending, residual=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(first.float()).all(), "non-finite pixels: %d" % int((~torch.isfinite(first.float())).any(-1).sum())
+    for rep in range(1, 20):
+        zr = zd.clone()
+        PF.tri_attn_block(zr, W, md, ending=ending, residual=True)
+        assert torch.equal(zr, first), "call %d differs from call 0" % rep
+    rows = [0, 1, 288, 295, 485, 488, 600, 767]
+    got = first[0].cpu()
+    base = z[0]
+    if ending:
+        got, base = got[:, rows].transpose(0, 1), base[:, rows].transpose(0, 1)
+    else:
+        got, base = got[rows], base[rows]
+    ref = base.float() + S.tri_attn_rows(z[0].float(), P, mask[0], rows, ending=ending, dtype=torch.float32)
+    assert_bf16_residual_close(got, ref, "N=768 regression ending=%s rows %s" % (ending, rows))
 
 
 def test_chunked_block_against_oracle():

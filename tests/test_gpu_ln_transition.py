@@ -121,3 +121,53 @@ def test_transition_fp32_exact_residual_mask(affine):
     assert sel.row == "hip_gfx950_f32"
     upd = S.transition(x, wa, wb, wo, lw, lb, dtype=torch.float64)
     assert_f32_close(y, x.double() + m.double()[:, None] * upd, "transition fp32 residual mask affine=%s" % affine)
+
+
+# ------------------------------------------------------------------------------------------------ the block-glue transition face
+@pytest.mark.parametrize("split", [("a", "b"), ("b", "a")])
+def test_pair_fused_transition_face(split):
+    """pair_fused.transition over pack_transition_weights (common/opt_core/opt_core/attn/pair_fused.py:1519-1585, :744-780) on a
+    pair tensor [1, 96, 96, 128]: the fused w_ab in both ab_split orders (rows of each half named by the split), a per-position mask
+    with zero and fractional values, the residual, and in place (out = x).  Against the fp32 statement at the bf16 bars (the
+    residual form with the half-ulp allowance), masked positions equal to x bit for bit, and in place equal to out of place."""
+    from fpf_hip.attn import pair_fused as PF
+    c, hidden, n = 128, 512, 96
+    wa, wb, wo, lw, lb = _tr_weights(c, hidden, 21, torch.bfloat16)
+    halves = {"a": wa, "b": wb}
+    w_ab = torch.cat([halves[split[0]], halves[split[1]]], 0).to(DEV)
+    T = PF.pack_transition_weights(w_out=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV), w_ab=w_ab, ab_split=split)
+    assert (T.C, T.NH, T.n) == (c, hidden, 4)
+    x = torch.randn(1, n, n, c, generator=_g(22)).to(torch.bfloat16)
+    m = (torch.rand(1, n, n, generator=_g(23)) > 0.2).float()
+    m[0, 3, :] = 0.5
+    print("[C3] pair_fused.transition split=%s" % (split,), flush=True)
+    xd, md = x.to(DEV), m.to(DEV)
+    y = PF.transition(xd, T, residual=True, mask=md)
+    xi = xd.clone()
+    yi = PF.transition(xi, T, residual=True, mask=md, out=xi)
+    u = PF.transition(xd, T, residual=False)
+    torch.cuda.synchronize()
+    assert yi.data_ptr() == xi.data_ptr() and torch.equal(yi, y), "in place != out of place"
+    assert torch.equal(xd.cpu(), x), "out of place must leave x untouched"
+    ref_u = S.transition(x.float(), wa.float(), wb.float(), wo.float(), lw, lb, dtype=torch.float32)
+    assert_bf16_close(u, ref_u, "C3 update split=%s" % (split,))
+    ref = S.transition(x.float(), wa.float(), wb.float(), wo.float(), lw, lb, residual=True, mask=m, dtype=torch.float32)
+    assert_bf16_residual_close(y, ref, "C3 residual + mask split=%s" % (split,))
+    assert torch.equal(y.cpu()[m == 0], x[m == 0]), "masked positions must equal x bit for bit"
+
+
+def test_pair_fused_transition_face_matches_the_kernel_face():
+    """The glue face and kernels.transition.transition run the same kernel on the same pack: bitwise the same result, both ab_split
+    orders naming the same halves included."""
+    from fpf_hip.attn import pair_fused as PF
+    from fpf_hip.kernels import transition as TRK
+    wa, wb, wo, lw, lb = _tr_weights(128, 512, 24, torch.bfloat16)
+    x = torch.randn(1, 64, 64, 128, generator=_g(25)).to(torch.bfloat16).to(DEV)
+    T1 = PF.pack_transition_weights(w_out=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV), w_a=wa.to(DEV), w_b=wb.to(DEV))
+    T2 = PF.pack_transition_weights(w_out=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV), w_ab=torch.cat([wb, wa], 0).to(DEV), ab_split=("b", "a"))
+    K = TRK.pack(w_a=wa.to(DEV), w_b=wb.to(DEV), w_o=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV))
+    y1 = PF.transition(x, T1, residual=True)
+    y2 = PF.transition(x, T2, residual=True)
+    y3, _ = TRK.transition(x, K, word="fast", residual=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(y1, y3)

@@ -77,3 +77,19 @@ def test_noalloc_refusals_launch_nothing():
     torch.cuda.synchronize()
     assert torch.count_nonzero(out) == 0
     assert L.TRIMUL_NOALLOC_SCRATCH_BYTES == 3 * 128 * 256 * 256 * 2
+
+
+def test_noalloc_on_a_side_stream_of_the_current_device():
+    """The entry checks that the caller's stream belongs to the current device (the scratch address is per device; a stream of
+    another device is refused before any launch).  A side stream of the current device passes the check and gives the same bits as
+    the null-stream call; on a one-GPU box the refusal itself cannot be provoked."""
+    from fpf_hip import _lib as L
+    z, mask, w = _case(96, 5, True)
+    out0, out1 = torch.empty_like(z), torch.empty_like(z)
+    L.call("fpf_trimul_fwd_noalloc", _args(z, mask, w, out0, True, True), L.stream_ptr(DEV))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(side):
+        L.call("fpf_trimul_fwd_noalloc", _args(z, mask, w, out1, True, True), ctypes.c_void_p(side.cuda_stream))
+    side.synchronize()
+    assert torch.equal(out0, out1)

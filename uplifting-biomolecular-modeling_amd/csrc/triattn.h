@@ -140,8 +140,9 @@ constexpr uint64_t TK_ALIVE = 1, TK_FULL = 2;
 __host__ __device__ inline int64_t keep_words(int64_t S) { return S / 64 + 1; }
 // Redo flags of a call (one 32-bit word per work item and wave; the 4-wave split has the most): B H ceil(N / TA_R) ceil(S / 128) 4.
 inline int64_t redo_words(int64_t B, int64_t N, int64_t H, int64_t S) { return B * H * cdiv(N, TA_R) * cdiv(S, 128) * 4; }
+// dry = true: every check of the launch, nothing launched (callers that must refuse before their first launch)
 int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, uint64_t* keep, hipStream_t st,
-                      char* err, size_t errlen);
-int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen);
+                      char* err, size_t errlen, bool dry = false);
+int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry = false);
 
 }  // namespace fpf

@@ -819,7 +819,8 @@ __global__ void __launch_bounds__(256) triattn_epilogue_f32(const float* __restr
   }
 }
 
-static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen) {
+// dry = true: every check, nothing launched
+static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen, bool dry = false) {
   if (a->dtype == FPF_DT_BF16) {
     if (a->D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 core serves head_dim 32 (got %lld)", (long long)a->D);
     CoreParams p{};
@@ -871,8 +872,9 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
         return fail(err, errlen, FPF_E_WORKSPACE, "v_layout 2: workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
       p.keep = a->keep;
       p.redo = static_cast<uint32_t*>(a->workspace);
-      return pipe_core_launch(p, st, err, errlen);
+      return pipe_core_launch(p, st, err, errlen, dry);
     }
+    if (dry) return FPF_OK;
     if (p.v_t && p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<true, true>), grid, block, 0, st, p);
     else if (p.v_t) hipLaunchKernelGGL((triattn_core_bf16<true, false>), grid, block, 0, st, p);
     else if (p.bias_vec) hipLaunchKernelGGL((triattn_core_bf16<false, true>), grid, block, 0, st, p);
@@ -905,6 +907,8 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     p.scale = a->scale;
     const int64_t blocks = a->B * a->N * a->H * cdiv(a->S, TF_QT);
     if (blocks > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
+    if (a->D != 16 && a->D != 32 && a->D != 64) return fail(err, errlen, FPF_E_SHAPE, "fp32 core serves head_dim 16 | 32 | 64 (got %lld)", (long long)a->D);
+    if (dry) return FPF_OK;
 #define FPF_TF(DD)                                                                                       \
   if (a->D == DD) {                                                                                      \
     hipLaunchKernelGGL(triattn_core_f32<DD>, dim3((unsigned)blocks), dim3(TF_QT), 0, st, p);             \
@@ -962,7 +966,7 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
                            int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f, int64_t bias_ld = -1, int bias_bf16 = 0,
-                           const float* b_g = nullptr) {
+                           const float* b_g = nullptr, bool dry = false) {
   if (rows < 0) rows = N;
   if (bias_ld < 0) bias_ld = N;
   if (dtype == FPF_DT_BF16) {
@@ -999,12 +1003,14 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.bias_bf16 = bias_bf16;
     p.b_g = b_g;
     if (!rt_tiles_ok(B * rows * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "prologue: 2^31 or more 32-pixel tiles");
+    if (dry) return FPF_OK;
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
   if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS) || q_scale != 1.0f || bias_scale != 1.0f || bias_ld != N || bias_bf16)
     return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output, q unscaled)");
+  if (dry) return FPF_OK;
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
                      (const float*)w_b, C, H, D, (float*)q, (float*)k, (float*)v, (float*)g, bias, N, ending, b_g);
@@ -1012,16 +1018,18 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
 }
 
 static int epilogue_launch(int dtype, const void* o, const void* g, const void* w_o, const float* b_o, int64_t B, int64_t N, int C, int H,
-                           int D, int ending, int residual, void* out, hipStream_t st, char* err, size_t errlen) {
+                           int D, int ending, int residual, void* out, hipStream_t st, char* err, size_t errlen, bool dry = false) {
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(o) || !aligned16(g) || !aligned16(w_o) || !aligned16(out))
       return fail(err, errlen, FPF_E_ALIGN, "epilogue operands must be 16-byte aligned");
     if (!rt_tiles_ok(B * N * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "epilogue: 2^31 or more 32-pixel tiles");
+    if (dry) return FPF_OK;
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * N * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_epilogue_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)o, (const uint16_t*)g, (const uint16_t*)w_o, b_o,
                        H, (uint16_t*)out, N, B, ending, residual);
     return launched(err, errlen, "triattn_epilogue_bf16");
   }
+  if (dry) return FPF_OK;
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_epilogue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)o, (const float*)g, (const float*)w_o, b_o, C,
                      H, D, (float*)out, N, ending, residual);
@@ -1176,26 +1184,34 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.scale = dma_core ? 1.0f : scale;
   c.workspace = redo;
   c.workspace_bytes = (size_t)redo_words(B, R, H, N) * 4;
-  if (dma_core && c.mask) {                             // the block-layout core reads the mask as keep bits
-    const int rc = keep_table_launch(c.mask, c.mask_dtype == FPF_DT_F32, c.mask_stride, B, R, N, keep, st, err, errlen);
-    if (rc) return rc;
-    c.keep = keep;
-  }
+  if (dma_core && c.mask) c.keep = keep;                // the block-layout core reads the mask as keep bits
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
   const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM | PRO_BIAS_BLK : 0);
-  int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp, g,
-                           bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f, -1, 0, a->b_g);
-  if (rc) return rc;
-  rc = core_launch(&c, st, err, errlen);
-  if (rc) return rc;
-  if (fused_gate) {
-    if (!aligned16(a->out)) return fail(err, errlen, FPF_E_ALIGN, "out must be 16-byte aligned");
-    if (!rt_tiles_ok(B * R * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "epilogue: 2^31 or more 32-pixel tiles");
+  // two passes over the stages: the first runs every check and launches nothing, so a refusal leaves the stream untouched
+  for (int pass = 0; pass < 2; ++pass) {
+    const bool dry = pass == 0;
+    if (c.keep) {
+      const int rc = keep_table_launch(c.mask, c.mask_dtype == FPF_DT_F32, c.mask_stride, B, R, N, keep, st, err, errlen, dry);
+      if (rc) return rc;
+    }
+    int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp,
+                             g, bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f, -1, 0, a->b_g, dry);
+    if (rc) return rc;
+    rc = core_launch(&c, st, err, errlen, dry);
+    if (rc) return rc;
+    if (fused_gate) {
+      if (!aligned16(a->out)) return fail(err, errlen, FPF_E_ALIGN, "out must be 16-byte aligned");
+      if (!rt_tiles_ok(B * R * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "epilogue: 2^31 or more 32-pixel tiles");
+    } else {
+      rc = epilogue_launch(a->dtype, o, g, a->w_o, a->b_o, B, N, a->C, (int)H, (int)D, a->ending, a->residual, a->out, st, err, errlen, dry);
+      if (rc || !dry) return rc;
+    }
+  }
+  {
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * R * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_epilogue_gate_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w, a->ln_b,
                        a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, a->b_g, a->b_o, (uint16_t*)a->out, N, B, row0,
                        R, a->ending, a->residual);
     return launched(err, errlen, "triattn_epilogue_gate_bf16");
   }
-  return epilogue_launch(a->dtype, o, g, a->w_o, a->b_o, B, N, a->C, (int)H, (int)D, a->ending, a->residual, a->out, st, err, errlen);
 }

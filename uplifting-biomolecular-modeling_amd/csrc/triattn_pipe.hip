@@ -799,11 +799,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 
 // ---------------------------------------------------------------------------------------------------------------- launchers
 int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, uint64_t* keep, hipStream_t st,
-                      char* err, size_t errlen) {
+                      char* err, size_t errlen, bool dry) {
   if (!mask || !keep) return fail(err, errlen, FPF_E_ARGS, "keep table: mask / table is NULL");
   if (S % TA_KT != 0 || S > (int64_t)TA_KT * TA_MAXW) return fail(err, errlen, FPF_E_SHAPE, "keep table: S a multiple of 64 up to %d", TA_KT * TA_MAXW);
   const int64_t blocks = cdiv(B * N, 4);
   if (blocks > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "keep table: grid too large");
+  if (dry) return FPF_OK;
   if (!mask_f32 && ms[2] == 1 && aligned16(mask) && ms[0] % 16 == 0 && ms[1] % 16 == 0) {
     hipLaunchKernelGGL(triattn_keep_bits_u8, dim3((unsigned)blocks), dim3(256), 0, st, static_cast<const uint8_t*>(mask), ms[0], ms[1], B, N, S, keep);
     return launched(err, errlen, "triattn_keep_bits_u8");
@@ -817,7 +818,7 @@ int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64
 // others multiples of 8), scale 1, p.redo holding redo_words(B, N, H, S) words.  8 waves (256 queries)
 // share each K / V^T tile where S fills whole 256-query tiles and the grid still has 8 or more workgroups per CU; 4 waves (128
 // queries) elsewhere.  The fallback runs on the same stream right after the fast kernel, over the same grid.
-int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen) {
+int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry) {
   const int64_t rows_heads = p.B * p.H * cdiv(p.N, TA_R);
   const bool wide = p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * (int64_t)num_cus();
   const int64_t total = wide ? rows_heads * (p.S / (32 * TA_DMA_WAVES)) : rows_heads * cdiv(p.S, 128);
@@ -829,6 +830,7 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
       TA_D * p.vs[3] * 2 > lim || (TA_R - 1) * std::max(p.qs[1], std::max(p.ks[1], p.vs[1])) * 2 > lim ||
       p.B * p.N > lim || p.S > lim)
     return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
+  if (dry) return FPF_OK;
   // persistent grids: one fast workgroup per CU walking every nwg-th item of its XCD's range (two per CU for the 4-wave
   // split, whose LDS and registers fit twice), and at least 8 workgroups, so that every XCD's range has one (with fewer
   // than 8 items some of them have none to do); the fallback scans its share of the flags

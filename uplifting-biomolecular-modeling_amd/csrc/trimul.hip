@@ -1077,6 +1077,17 @@ extern "C" int fpf_trimul_fwd_noalloc(const FpfTrimulArgs* a, void* stream, char
   if (need > (size_t)FPF_TRIMUL_NOALLOC_SCRATCH_BYTES)
     return fail(err, errlen, FPF_E_WORKSPACE, "needs %zu workspace bytes, above the %zu-byte static scratch (bf16, B = 1: N <= 256)", need,
                 (size_t)FPF_TRIMUL_NOALLOC_SCRATCH_BYTES);
+  // the scratch address is the current device's: a stream of another device would run the kernels there with this device's
+  // address, so such a stream is refused before anything is launched (the null stream is the current device's)
+  if (stream) {
+    int cur = 0;
+    hipDevice_t sdev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess) e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return fail(err, errlen, FPF_E_ARGS, "the stream's device could not be read: %s", hipGetErrorString(e));
+    if ((int)sdev != cur)
+      return fail(err, errlen, FPF_E_ARGS, "the stream belongs to device %d but device %d is current: make the stream's device current", (int)sdev, cur);
+  }
   FpfTrimulArgs b = *a;
   const int rc = scratch_address(&b.workspace, err, errlen);
   if (rc) return rc;

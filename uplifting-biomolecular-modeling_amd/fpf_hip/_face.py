@@ -191,6 +191,7 @@ def narrow(sel, word, prefer, exclude=None):
 
 # ---------------------------------------------------------------------------------------------------------------- scratch
 _SCRATCH = {}
+_CAPTURED = []      # outgrown buffers that a captured call used: a graph replays with their addresses, so they stay allocated
 
 
 def scratch(device, nbytes, kind="ws"):
@@ -198,16 +199,32 @@ def scratch(device, nbytes, kind="ws"):
     its workspace only between its own launches on the current stream, so the next call on the same stream may reuse it, and
     a stack of layers holds ONE workspace sized by its largest call instead of one per layer.  Calls on other streams get
     their own buffers.  ``kind`` separates buffers one call needs at the same time (the chunked triangle attention holds a
-    workspace and a full bias)."""
+    workspace and a full bias).
+
+    Graph capture: a buffer handed to a call while its stream is capturing is marked, and when a later, larger call outgrows
+    it, the marked buffer is kept allocated (not returned to torch's caching allocator), so a graph that recorded its address
+    never replays into memory torch has handed to another tensor.  ``reserve_scratch`` sizes the buffer up front instead, so
+    that no captured call sees a buffer that is later outgrown; ``release_scratch`` drops everything, marked buffers included,
+    and must not run while such a graph is still replayed."""
     import torch
     dev = torch.device(device)
     key = (str(dev), torch.cuda.current_stream(dev).cuda_stream if dev.type == "cuda" else 0, kind)
     t = _SCRATCH.get(key)
     if t is None or t.numel() < nbytes:
-        _SCRATCH.pop(key, None)
-        del t                                                # the old buffer goes back to the caching allocator first
+        old = _SCRATCH.pop(key, None)
+        if old is not None and getattr(old, "_fpf_captured", False):
+            _CAPTURED.append(old)
+        del old, t                                           # an unmarked buffer goes back to the caching allocator first
         t = _SCRATCH[key] = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    if dev.type == "cuda" and not getattr(t, "_fpf_captured", False) and torch.cuda.is_current_stream_capturing():
+        t._fpf_captured = True
     return t
+
+
+def reserve_scratch(device, nbytes, kind="ws"):
+    """Size the current stream's shared buffer of ``kind`` to at least ``nbytes`` now (before capturing a graph whose calls
+    should never see it outgrown)."""
+    return scratch(device, nbytes, kind)
 
 
 def scratch_bytes(device=None):
@@ -216,5 +233,7 @@ def scratch_bytes(device=None):
 
 
 def release_scratch():
-    """Drop every shared scratch buffer (their memory returns to torch's caching allocator)."""
+    """Drop every shared scratch buffer, the outgrown ones a captured call used included (their memory returns to torch's caching
+    allocator): no graph that captured a call of these faces may be replayed afterwards."""
     _SCRATCH.clear()
+    del _CAPTURED[:]

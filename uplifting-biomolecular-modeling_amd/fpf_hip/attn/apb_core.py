@@ -1,7 +1,8 @@
 """Attention with a pair bias over libfpf_hip (``fpf_apb_fwd``; the producer ``fpf_apb_bias_fwd``): the Pairformer single track's
 AttentionPairBias and the token attention of a sample batch sharing one bias.
 
-Mirrors common/opt_core/opt_core/attn/apb_core.py: ``Unsupported(event, detail)`` (:45), ``census()`` (:63) and
+Serves the face of common/opt_core/opt_core/attn/apb_core.py -- the refusal type with its ``event`` / ``detail`` (:45), the
+per-process ``census()`` (:63) and
 
     out = pair_bias_attention(q, k, v, pair_bias, key_mask=None, *, gate=None, num_samples=None, num_heads=None, layout="rows",
                               out=None, scale=None, inf=1e9)                                                              (:89)
@@ -20,6 +21,7 @@ Also here: ``pair_bias_producer`` (the kernels/apb "producer" boundary: bias = L
 pass over bf16 z) and ``attention_pair_bias_module`` (the whole AttentionPairBias module, attentionv2.py:62-111: the q|k|v|g and
 output projections are plain GEMMs through torch, the core and the producer are the HIP kernels).
 """
+import collections
 import math
 import threading
 
@@ -29,139 +31,175 @@ from .. import _lib as L
 
 LAYOUTS = ("rows", "shnd")
 HEAD_DIMS = (16, 24, 32, 48, 64)
-CENSUS = {"served": 0, "refused": {}, "by_shape": {}}
-_LOCK = threading.Lock()
 
 
 class Unsupported(Exception):
-    """An input outside the served domain, refused by name before any work (``.event``, ``.detail``)."""
+    """Raised before anything is launched when a call falls outside what the HIP core serves.  ``event`` is the census word
+    (``layout:<name>``, ``shape:<operand>``, ``dtype:<operand>``, ``stride:<operand>``, ``head_dim:<n>``, ``device:<type>``,
+    ``rank``, ``nonfinite:inf_or_scale``, ``lib:<kind>``); ``detail`` says what was found."""
 
     def __init__(self, event, detail=""):
-        Exception.__init__(self, "%s: %s" % (event, detail) if detail else event)
         self.event, self.detail = event, detail
+        Exception.__init__(self, event + (": " + detail if detail else ""))
 
 
-def _book(event, key=None):
-    with _LOCK:
-        if event is None:
-            CENSUS["served"] += 1
-            if key is not None and (key in CENSUS["by_shape"] or len(CENSUS["by_shape"]) < 32):
-                CENSUS["by_shape"][key] = CENSUS["by_shape"].get(key, 0) + 1
-        else:
-            CENSUS["refused"][event] = CENSUS["refused"].get(event, 0) + 1
+class _Ledger(object):
+    """Per-process counts of this face's calls: served calls (in all and per problem shape) and refusals per event word.  At most
+    SHAPES distinct shapes are named; calls of further shapes are counted under "other"."""
+    SHAPES = 32
+
+    def __init__(self):
+        self._mu = threading.Lock()
+        self.served = 0
+        self.refused = collections.Counter()
+        self.by_shape = collections.Counter()
+
+    def serve(self, shape):
+        with self._mu:
+            self.served += 1
+            self.by_shape[shape if shape in self.by_shape or len(self.by_shape) < self.SHAPES else "other"] += 1
+
+    def refuse(self, event):
+        with self._mu:
+            self.refused[event] += 1
+
+    def snapshot(self):
+        with self._mu:
+            return {"served": self.served, "refused": dict(self.refused), "by_shape": dict(self.by_shape)}
+
+
+LEDGER = _Ledger()
 
 
 def census():
-    """This process's served calls (by shape, capped at 32 keys) and refusals by event."""
-    with _LOCK:
-        return {k: (dict(v) if isinstance(v, dict) else v) for k, v in CENSUS.items()}
+    """{"served": n, "refused": {event: n}, "by_shape": {"S..H..N..D..": n}} for this process."""
+    return LEDGER.snapshot()
 
 
-def _dt(t, what):
-    if t.dtype == torch.float32:
-        return L.DT_F32
-    if t.dtype == torch.bfloat16:
-        return L.DT_BF16
-    raise Unsupported("dtype:%s" % what, str(t.dtype))
+def _require(ok, event, detail=""):
+    if not ok:
+        raise Unsupported(event, detail)
+
+
+def _heads_view(t, S, n, H, D):
+    """[S*n, H*D] row block (unit column stride, any row stride) -> its [S, n, H, D] view."""
+    r = t.stride(0)
+    return t.as_strided((S, n, H, D), (n * r, r, D, 1), t.storage_offset())
+
+
+class _Problem(object):
+    """The operands of one call as [S, N|NK, H, D] views plus the result tensor handed back to the caller."""
+    __slots__ = ("S", "N", "NK", "H", "D", "q", "k", "v", "gate", "o", "result")
+
+
+def _rows_problem(q, k, v, gate, out, num_samples, num_heads):
+    """Layout "rows": every operand a 2-D row block [S*rows, H*D] with unit column stride, e.g. column slices of one fused
+    q|k|v|g projection output."""
+    _require(num_samples is not None and num_heads is not None, "layout:rows_needs_S_H", "num_samples and num_heads are required")
+    P = _Problem()
+    P.S, P.H = int(num_samples), int(num_heads)
+    named = [("q", q), ("k", k), ("v", v)] + ([("gate", gate)] if gate is not None else [])
+    for name, t in named:
+        _require(t.dim() == 2 and t.stride(1) == 1 and t.shape[0] % P.S == 0 and t.shape[1] % P.H == 0, "shape:" + name,
+                 "%s is %s with strides %s; a 2-D block of S*rows x H*D with unit column stride is needed"
+                 % (name, tuple(t.shape), tuple(t.stride())))
+    P.N, P.D = int(q.shape[0]) // P.S, int(q.shape[1]) // P.H
+    P.NK = int(k.shape[0]) // P.S
+    _require(int(k.shape[1]) == P.H * P.D and tuple(v.shape) == tuple(k.shape), "shape:kv",
+             "k %s and v %s must both be [S*NK, %d]" % (tuple(k.shape), tuple(v.shape), P.H * P.D))
+    _require(gate is None or tuple(gate.shape) == (P.S * P.N, P.H * P.D), "shape:gate",
+             "gate %s, query rows need %s" % (None if gate is None else tuple(gate.shape), (P.S * P.N, P.H * P.D)))
+    res = out if out is not None else torch.empty((P.S * P.N, P.H * P.D), dtype=q.dtype, device=q.device)
+    _require(res.dim() == 2 and tuple(res.shape) == (P.S * P.N, P.H * P.D) and res.stride(1) == 1, "shape:out",
+             "out %s; a [%d, %d] block with unit column stride is needed" % (tuple(res.shape), P.S * P.N, P.H * P.D))
+    P.q, P.k, P.v = _heads_view(q, P.S, P.N, P.H, P.D), _heads_view(k, P.S, P.NK, P.H, P.D), _heads_view(v, P.S, P.NK, P.H, P.D)
+    P.gate = None if gate is None else _heads_view(gate, P.S, P.N, P.H, P.D)
+    P.o, P.result = _heads_view(res, P.S, P.N, P.H, P.D), res
+    return P
+
+
+def _shnd_problem(q, k, v, gate, out, num_samples):
+    """Layout "shnd": q, k, v [S, H, rows, D] (innermost stride 1, served through their strides), gate [S, N, H*D] or
+    [S, N, H, D]."""
+    _require(q.dim() == 4, "rank", "q has shape %s; [S, H, N, D] expected" % (tuple(q.shape),))
+    P = _Problem()
+    P.S, P.H, P.N, P.D = (int(x) for x in q.shape)
+    P.NK = int(k.shape[2]) if k.dim() == 4 else -1
+    _require(num_samples is None or int(num_samples) == P.S, "shape:num_samples", "num_samples=%s, q holds %d samples" % (num_samples, P.S))
+    _require(tuple(k.shape) == (P.S, P.H, P.NK, P.D) and tuple(v.shape) == tuple(k.shape), "shape:kv",
+             "k %s, v %s; both [%d, %d, NK, %d] expected" % (tuple(k.shape), tuple(v.shape), P.S, P.H, P.D))
+    P.q, P.k, P.v = (t.permute(0, 2, 1, 3) for t in (q, k, v))          # [S, rows, H, D] views
+    P.gate = None
+    if gate is not None:
+        g4 = None
+        if gate.dim() == 3 and tuple(gate.shape) == (P.S, P.N, P.H * P.D) and gate.stride(-1) == 1:
+            g4 = gate.as_strided((P.S, P.N, P.H, P.D), (gate.stride(0), gate.stride(1), P.D, 1), gate.storage_offset())
+        elif gate.dim() == 4 and tuple(gate.shape) == (P.S, P.N, P.H, P.D) and gate.stride(-1) == 1:
+            g4 = gate
+        _require(g4 is not None, "shape:gate", "gate %s; [S, N, H*D] or [S, N, H, D] with unit innermost stride expected" % (tuple(gate.shape),))
+        P.gate = g4
+    res = out if out is not None else torch.empty((P.S, P.N, P.H * P.D), dtype=q.dtype, device=q.device)
+    _require(tuple(res.shape) == (P.S, P.N, P.H * P.D) and res.stride(-1) == 1, "shape:out",
+             "out %s; [%d, %d, %d] with unit column stride expected" % (tuple(res.shape), P.S, P.N, P.H * P.D))
+    P.o = res.as_strided((P.S, P.N, P.H, P.D), (res.stride(0), res.stride(1), P.D, 1), res.storage_offset())
+    P.result = res
+    return P
+
+
+def _drop_unit_dims(t, keep):
+    """``t`` without leading size-1 dimensions beyond its last ``keep`` ones."""
+    while t.dim() > keep and int(t.shape[0]) == 1:
+        t = t.squeeze(0)
+    return t
+
+
+def _storage_code(t, what):
+    codes = {torch.float32: L.DT_F32, torch.bfloat16: L.DT_BF16}
+    _require(t.dtype in codes, "dtype:" + what, "%s is %s; fp32 or bf16 storage is served" % (what, t.dtype))
+    return codes[t.dtype]
 
 
 def pair_bias_attention(q, k, v, pair_bias, key_mask=None, *, gate=None, num_samples=None, num_heads=None, layout="rows", out=None,
                         scale=None, inf=1e9, config=None):
     """See the module docstring.  Returns [S*N, H*D] (layout rows) or [S, N, H*D] (layout shnd), or ``out``."""
     try:
-        if not math.isfinite(float(inf)) or (scale is not None and not math.isfinite(float(scale))):
-            raise Unsupported("nonfinite:inf_or_scale", "inf and scale must be finite (inf=%r scale=%r)" % (inf, scale))
-        if not q.is_cuda:
-            raise Unsupported("device:%s" % q.device.type, "the HIP core serves device tensors")
-        if layout == "shnd":
-            if q.dim() != 4:
-                raise Unsupported("rank", "layout shnd wants q/k/v [S,H,N,D], got %s" % (tuple(q.shape),))
-            S, H, N, D = (int(x) for x in q.shape)
-            NK = int(k.shape[2])
-            if num_samples is not None and int(num_samples) != S:
-                raise Unsupported("shape:num_samples", "num_samples=%s but q has S=%d" % (num_samples, S))
-            if tuple(k.shape) != (S, H, NK, D) or tuple(v.shape) != (S, H, NK, D):
-                raise Unsupported("shape:kv", "k / v must be [S,H,NK,D] = %s" % ((S, H, NK, D),))
-            q4 = q.permute(0, 2, 1, 3)                   # [S, N, H, D] views, no copy
-            k4 = k.permute(0, 2, 1, 3)
-            v4 = v.permute(0, 2, 1, 3)
-            g4 = None
-            if gate is not None:
-                g4 = gate if gate.dim() == 4 else gate.reshape(S, N, H, D) if gate.stride(-1) == 1 else None
-                if g4 is None or tuple(g4.shape) != (S, N, H, D):
-                    raise Unsupported("shape:gate", "layout shnd wants gate [S,N,H*D] or [S,N,H,D]")
-            res = out if out is not None else torch.empty((S, N, H * D), dtype=q.dtype, device=q.device)
-            if tuple(res.shape) != (S, N, H * D) or res.stride(-1) != 1:
-                raise Unsupported("shape:out", "layout shnd wants out [S,N,H*D] with unit column stride")
-            o4 = res.as_strided((S, N, H, D), (res.stride(0), res.stride(1), D, 1), res.storage_offset())
-        elif layout == "rows":
-            if num_samples is None or num_heads is None:
-                raise Unsupported("layout:rows_needs_S_H", "layout rows needs num_samples and num_heads")
-            S, H = int(num_samples), int(num_heads)
-            for name, t in (("q", q), ("k", k), ("v", v)) + ((("gate", gate),) if gate is not None else ()):
-                if t.dim() != 2 or t.shape[0] % S or t.shape[1] % H or t.stride(1) != 1:
-                    raise Unsupported("shape:%s" % name, "layout rows wants %s 2-D [S*N, H*D] with unit column stride, got %s strides %s"
-                                      % (name, tuple(t.shape), tuple(t.stride())))
-            N, D = int(q.shape[0]) // S, int(q.shape[1]) // H
-            NK = int(k.shape[0]) // S
-            if tuple(v.shape) != tuple(k.shape) or int(k.shape[1]) != H * D:
-                raise Unsupported("shape:kv", "layout rows wants k / v [S*NK, H*D]")
-            if gate is not None and tuple(gate.shape) != (S * N, H * D):
-                raise Unsupported("shape:gate", "layout rows wants gate [S*N, H*D] = %s, got %s" % ((S * N, H * D), tuple(gate.shape)))
-
-            def as4(t, n):                               # [S*n, H*D] rows -> [S, n, H, D] view (no copy)
-                rs = t.stride(0)
-                return t.as_strided((S, n, H, D), (n * rs, rs, D, 1), t.storage_offset())
-            q4, k4, v4 = as4(q, N), as4(k, NK), as4(v, NK)
-            g4 = None if gate is None else as4(gate, N)
-            res = out if out is not None else torch.empty((S * N, H * D), dtype=q.dtype, device=q.device)
-            if res.dim() != 2 or tuple(res.shape) != (S * N, H * D) or res.stride(1) != 1:
-                raise Unsupported("shape:out", "layout rows wants out [S*N, H*D] with unit column stride, got %s" % (tuple(res.shape),))
-            o4 = as4(res, N)
+        _require(math.isfinite(float(inf)) and (scale is None or math.isfinite(float(scale))), "nonfinite:inf_or_scale",
+                 "a masked key is dropped by name, so inf and scale must be finite numbers (inf=%r, scale=%r)" % (inf, scale))
+        _require(q.is_cuda, "device:%s" % q.device.type, "q is on %s; the HIP core reads device memory" % q.device)
+        if layout == "rows":
+            P = _rows_problem(q, k, v, gate, out, num_samples, num_heads)
+        elif layout == "shnd":
+            P = _shnd_problem(q, k, v, gate, out, num_samples)
         else:
-            raise Unsupported("layout:%s" % layout, "known layouts: " + ", ".join(LAYOUTS))
-        if D not in HEAD_DIMS:
-            raise Unsupported("head_dim:%d" % D, "served head dims: %s" % (HEAD_DIMS,))
-        dt = _dt(q, "q")
-        for name, t in (("k", k), ("v", v)) + ((("gate", gate),) if gate is not None else ()) + (("out", res),):
-            if t.dtype != q.dtype:
-                raise Unsupported("dtype:mix", "%s is %s, q is %s" % (name, t.dtype, q.dtype))
-        pb = pair_bias
-        while pb.dim() > 4 and int(pb.shape[0]) == 1:
-            pb = pb[0]
-        if pb.dim() == 3:
-            pb = pb.unsqueeze(0)
-        if pb.dim() != 4 or int(pb.shape[0]) not in (1, S) or tuple(pb.shape[1:]) != (H, N, NK):
-            raise Unsupported("shape:pair_bias", "pair_bias must be [H,N,NK] or [S|1,H,N,NK], got %s" % (tuple(pair_bias.shape),))
-        if pb.stride(-1) != 1:
-            raise Unsupported("stride:pair_bias", "pair_bias needs a unit key stride")
-        bdt = _dt(pb, "pair_bias")
-        km, mdt = None, L.DT_U8
+            raise Unsupported("layout:%s" % (layout,), "served layouts: %s" % (", ".join(LAYOUTS),))
+        _require(P.D in HEAD_DIMS, "head_dim:%d" % P.D, "head dims with a compiled kernel: %s" % (HEAD_DIMS,))
+        dt = _storage_code(q, "q")
+        for name, t in (("k", k), ("v", v), ("gate", gate), ("out", P.result)):
+            _require(t is None or t.dtype == q.dtype, "dtype:mix", "%s is %s while q is %s" % (name, None if t is None else t.dtype, q.dtype))
+        pb = _drop_unit_dims(pair_bias, 4)
+        pb = pb.unsqueeze(0) if pb.dim() == 3 else pb
+        _require(pb.dim() == 4 and int(pb.shape[0]) in (1, P.S) and tuple(pb.shape[1:]) == (P.H, P.N, P.NK), "shape:pair_bias",
+                 "pair_bias %s; [H, N, NK] or [1 | S, H, N, NK] with H=%d N=%d NK=%d expected" % (tuple(pair_bias.shape), P.H, P.N, P.NK))
+        _require(pb.stride(-1) == 1, "stride:pair_bias", "the key axis of pair_bias must have unit stride")
+        bias_code = _storage_code(pb, "pair_bias")
+        km, mask_code = None, L.DT_U8
         if key_mask is not None:
-            km = key_mask
-            while km.dim() > 2 and int(km.shape[0]) == 1:
-                km = km[0]
-            if km.dim() == 1:
-                km = km[None, :]
-            if km.dim() != 2 or int(km.shape[0]) not in (1, S) or int(km.shape[1]) != NK:
-                raise Unsupported("shape:mask", "key_mask must be [NK], [1,NK] or [S,NK], got %s" % (tuple(key_mask.shape),))
+            km = _drop_unit_dims(key_mask, 2)
+            km = km.unsqueeze(0) if km.dim() == 1 else km
+            _require(km.dim() == 2 and int(km.shape[0]) in (1, P.S) and int(km.shape[1]) == P.NK, "shape:mask",
+                     "key_mask %s; [NK], [1, NK] or [S, NK] with NK=%d expected" % (tuple(key_mask.shape), P.NK))
             if km.dtype == torch.float32:
-                mdt = L.DT_F32
-            elif km.dtype in (torch.bool, torch.uint8):
-                km = km.view(torch.uint8)
+                mask_code = L.DT_F32
             else:
-                km = (km != 0).view(torch.uint8)
-        a = L.ApbArgs(abi_version=L.ABI_VERSION, dtype=dt, S=S, N=N, NK=NK, H=H, D=D, q=L.ptr(q4), k=L.ptr(k4), v=L.ptr(v4),
-                      gate=L.ptr(g4), bias=L.ptr(pb), bias_dtype=bdt, key_mask=L.ptr(km), mask_dtype=mdt, out=L.ptr(o4),
-                      scale=(1.0 / math.sqrt(D)) if scale is None else float(scale))
-        a.q_stride[:] = list(q4.stride())
-        a.k_stride[:] = list(k4.stride())
-        a.v_stride[:] = list(v4.stride())
-        a.out_stride[:] = list(o4.stride())
-        if g4 is not None:
-            a.gate_stride[:] = list(g4.stride())
-        bs = list(pb.stride())
-        a.bias_stride[:] = [0 if int(pb.shape[0]) == 1 else bs[0], bs[1], bs[2], bs[3]]
+                km = (km if km.dtype in (torch.bool, torch.uint8) else km != 0).view(torch.uint8)
+        a = L.ApbArgs(abi_version=L.ABI_VERSION, dtype=dt, S=P.S, N=P.N, NK=P.NK, H=P.H, D=P.D, q=L.ptr(P.q), k=L.ptr(P.k),
+                      v=L.ptr(P.v), gate=L.ptr(P.gate), bias=L.ptr(pb), bias_dtype=bias_code, key_mask=L.ptr(km), mask_dtype=mask_code,
+                      out=L.ptr(P.o), scale=(1.0 / math.sqrt(P.D)) if scale is None else float(scale))
+        for field, t in (("q_stride", P.q), ("k_stride", P.k), ("v_stride", P.v), ("out_stride", P.o), ("gate_stride", P.gate)):
+            if t is not None:
+                getattr(a, field)[:] = list(t.stride())
+        shared = int(pb.shape[0]) == 1
+        a.bias_stride[:] = [0 if shared else pb.stride(0)] + list(pb.stride()[1:])
         if km is not None:
             a.mask_stride[:] = [0 if int(km.shape[0]) == 1 else km.stride(0), km.stride(1)]
         try:
@@ -169,10 +207,10 @@ def pair_bias_attention(q, k, v, pair_bias, key_mask=None, *, gate=None, num_sam
         except L.LibError as e:
             raise Unsupported("lib:%s" % e.kind, e.msg)
     except Unsupported as e:
-        _book(e.event)
+        LEDGER.refuse(e.event)
         raise
-    _book(None, "S%dH%dN%dD%d" % (S, H, N, D))
-    return res
+    LEDGER.serve("S%dH%dN%dD%d" % (P.S, P.H, P.N, P.D))
+    return P.result
 
 
 def pair_bias_producer(z, w_z, ln_w=None, ln_b=None, *, eps=1e-5, dtype=torch.float32, out=None):
@@ -193,7 +231,7 @@ def pair_bias_producer(z, w_z, ln_w=None, ln_b=None, *, eps=1e-5, dtype=torch.fl
     lw = None if ln_w is None else ln_w.to(device=z.device, dtype=torch.float32).contiguous()
     lb = None if ln_b is None else ln_b.to(device=z.device, dtype=torch.float32).contiguous()
     a = L.ApbBiasArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=C, H=H, z=L.ptr(z4), ln_w=L.ptr(lw), ln_b=L.ptr(lb),
-                      eps=float(eps), w_z=L.ptr(wz), bias=L.ptr(out), bias_dtype=_dt(out, "bias"), bias_ld=int(out.stride(2)))
+                      eps=float(eps), w_z=L.ptr(wz), bias=L.ptr(out), bias_dtype=_storage_code(out, "bias"), bias_ld=int(out.stride(2)))
     try:
         L.call("fpf_apb_bias_fwd", a, L.stream_ptr(z.device))
     except L.LibError as e:

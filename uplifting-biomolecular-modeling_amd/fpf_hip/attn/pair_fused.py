@@ -48,6 +48,25 @@ class TriAttnWeights(object):
         self._packs = {}
 
 
+def _matrix(reason, t, rows=None, cols=None):
+    """Refuse (by ``reason``) unless ``t`` is a 2-D weight with ``rows`` rows and ``cols`` columns (None: any)."""
+    got = None if t is None else tuple(t.shape)
+    if got is None or len(got) != 2 or (rows is not None and got[0] != rows) or (cols is not None and got[1] != cols):
+        raise Unsupported(reason, "weight of shape %s where [%s, %s] is needed" % (got, "*" if rows is None else rows, "*" if cols is None else cols))
+    return t
+
+
+def _vector(reason, t, n):
+    if t is not None and tuple(t.shape) != (n,):
+        raise Unsupported(reason, "bias of shape %s where [%d] is needed" % (tuple(t.shape), n))
+    return t
+
+
+def _named_blocks(w, order, block_rows):
+    """The row blocks of a fused weight, keyed by the names of ``order`` (block i = rows i*block_rows .. (i+1)*block_rows - 1)."""
+    return dict((name, w[i * block_rows:(i + 1) * block_rows]) for i, name in enumerate(order))
+
+
 def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=None, w_k=None, w_v=None, w_g=None, w_b=None, w_qkvg=None,
                          qkvg_split=("q", "k", "v", "g"), b_g=None, b_o=None, eps=1e-5, device=None):
     """Pack once per module.  w_q / w_k / w_v / w_g [H*D, C] or w_qkvg [4*H*D, C] (row blocks in ``qkvg_split`` order); w_b [H, C];
@@ -57,26 +76,19 @@ def pack_triattn_weights(*, w_o, n_heads, head_dim, ln_w=None, ln_b=None, w_q=No
     H, D = int(n_heads), int(head_dim)
     HD = H * D
     if w_qkvg is not None:
-        if int(w_qkvg.shape[0]) != 4 * HD:
-            raise Unsupported("w_qkvg-shape", str(tuple(w_qkvg.shape)))
-        blocks = {nm: w_qkvg[i * HD:(i + 1) * HD] for i, nm in enumerate(qkvg_split)}
-        w_q, w_k, w_v, w_g = blocks["q"], blocks["k"], blocks["v"], blocks["g"]
+        blocks = _named_blocks(_matrix("w_qkvg-shape", w_qkvg, 4 * HD), qkvg_split, HD)
+        w_q, w_k, w_v, w_g = (blocks[n] for n in ("q", "k", "v", "g"))
     if w_g is None:
-        raise Unsupported("gate:none")
+        raise Unsupported("gate:none", "attention without a gate projection is not served")
     if w_b is None:
-        raise Unsupported("bias:none")
-    for nm, t in (("w_q", w_q), ("w_k", w_k), ("w_v", w_v), ("w_g", w_g)):
-        if t is None or t.dim() != 2 or int(t.shape[0]) != HD:
-            raise Unsupported(nm + "-shape", str(None if t is None else tuple(t.shape)))
-    C = int(w_q.shape[1])
-    if tuple(w_b.shape) != (H, C):
-        raise Unsupported("w_b-shape", str(tuple(w_b.shape)))
-    if w_o.dim() != 2 or int(w_o.shape[1]) != HD:
-        raise Unsupported("w_o-shape", str(tuple(w_o.shape)))
-    if b_g is not None and tuple(b_g.shape) != (HD,):
-        raise Unsupported("b_g-shape", str(tuple(b_g.shape)))
-    if b_o is not None and tuple(b_o.shape) != (int(w_o.shape[0]),):
-        raise Unsupported("b_o-shape", str(tuple(b_o.shape)))
+        raise Unsupported("bias:none", "the triangle bias projection w_b is required")
+    C = None if w_q is None or w_q.dim() != 2 else int(w_q.shape[1])
+    for reason, t in (("w_q-shape", w_q), ("w_k-shape", w_k), ("w_v-shape", w_v), ("w_g-shape", w_g)):
+        _matrix(reason, t, HD, C)
+    _matrix("w_b-shape", w_b, H, C)
+    _matrix("w_o-shape", w_o, None, HD)
+    _vector("b_g-shape", b_g, HD)
+    _vector("b_o-shape", b_o, int(w_o.shape[0]))
     W = TriAttnWeights()
     dev = device if device is not None else w_o.device
     W.C, W.H, W.D, W.C_out, W.eps, W.dev = C, H, D, int(w_o.shape[0]), float(eps), dev
@@ -383,17 +395,16 @@ class TransitionWeights(object):
 
 
 def pack_transition_weights(*, w_out, ln_w=None, ln_b=None, w_a=None, w_b=None, w_ab=None, ab_split=("a", "b"), eps=1e-5, device=None):
-    C, NH = int(w_out.shape[0]), int(w_out.shape[1])
+    """SwiGLU transition weights: w_a / w_b [n*C, C] (silu branch, linear branch) or the fused w_ab [2*n*C, C] with its row blocks
+    named in ``ab_split`` order; w_out [C, n*C]; LayerNorm ln_w / ln_b [C] or None."""
+    C, NH = (int(x) for x in _matrix("w_out-shape", w_out).shape)
     if w_ab is not None:
-        if tuple(w_ab.shape) != (2 * NH, C):
-            raise Unsupported("w_ab-shape", str(tuple(w_ab.shape)))
-        blocks = {nm: w_ab[i * NH:(i + 1) * NH] for i, nm in enumerate(ab_split)}
+        blocks = _named_blocks(_matrix("w_ab-shape", w_ab, 2 * NH, C), ab_split, NH)
         w_a, w_b = blocks["a"], blocks["b"]
-    for nm, t in (("w_a", w_a), ("w_b", w_b)):
-        if t is None or tuple(t.shape) != (NH, C):
-            raise Unsupported(nm + "-shape", str(None if t is None else tuple(t.shape)))
-    if NH % C != 0:
-        raise Unsupported("hidden", "n*C hidden expected, got C=%d hidden=%d" % (C, NH))
+    _matrix("w_a-shape", w_a, NH, C)
+    _matrix("w_b-shape", w_b, NH, C)
+    if NH % C:
+        raise Unsupported("hidden", "hidden width %d is not a whole multiple of the %d channels" % (NH, C))
     return TransitionWeights(_TR.pack(w_o=w_out, w_a=w_a, w_b=w_b, ln_w=ln_w, ln_b=ln_b, eps=eps, device=device))
 
 

@@ -46,6 +46,11 @@ def _class_of(prec):
     return {"bf16": "bf16", "f32z_bf16": "bf16", "fp32": "fp32", "tf32": "fp32"}.get(prec)
 
 
+def _reduced_fp32_matmul():
+    """torch may run this process's fp32 matmuls in a reduced-precision (TF32-class) mode."""
+    return torch.get_float32_matmul_precision() in ("high", "medium") or torch.backends.cuda.matmul.allow_tf32
+
+
 def call_precision(z, residency=None):
     """(precision word, compute dtype) of a live call (common/opt_core/opt_core/kernels/trimul/__init__.py:1293): an fp32 z under
     bf16 autocast on its device -- or with ``residency="fp32"`` and a bf16 compute request made through ``select`` -- is the
@@ -55,8 +60,7 @@ def call_precision(z, residency=None):
         ac = torch.is_autocast_enabled(dev) and torch.get_autocast_dtype(dev) == torch.bfloat16 if dev == "cuda" else False
         if ac:
             return "f32z_bf16", torch.bfloat16
-        tf = bool(torch.backends.cuda.matmul.allow_tf32) or torch.get_float32_matmul_precision() != "highest"
-        return ("tf32" if tf else "fp32"), torch.float32
+        return ("tf32" if _reduced_fp32_matmul() else "fp32"), torch.float32
     return precision_word(z.dtype, residency), z.dtype
 
 
