@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 9   /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+#define FPF_ABI_VERSION 10  /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
                                5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
                                6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
                                   (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes);
@@ -33,7 +33,10 @@ extern "C" {
                                   register-order blocks;
                                8: the trimul rows mode (FpfTrimulArgs.row0 / rows / fixed_in, fpf_trimul_fixed_fwd,
                                   fpf_trimul_fixed_bytes, fpf_trimul_rows_workspace_bytes);
-                               9: FPF_DT_F32Z_BF16 for the trimul (fp32 z / out, bf16 operands and planes) */
+                               9: FPF_DT_F32Z_BF16 for the trimul (fp32 z / out, bf16 operands and planes);
+                               10: the bf16 block runs the v_layout 2 core for every N up to 8192 (its J axis padded to 64:
+                                   fpf_triattn_bias_bytes sizes fpf_triattn_bias_fwd's output); fpf_triattn_stage_bytes and the
+                                   staged route of fpf_triattn_fwd onto that core */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3, FPF_DT_F32Z_BF16 = 4 };
 enum {
@@ -193,13 +196,20 @@ typedef struct {
                               for a row with no kept key), or NULL with mask NULL (every key kept).  The fused block builds it from
                               its pair mask in its workspace; v_layout 2 with a mask and no table is refused (FPF_E_ARGS).  Other
                               layouts read `mask` and ignore this field. */
-  void* workspace;         /* v_layout 2 only: device memory of fpf_triattn_workspace_bytes(B, N, H, S, 2) bytes (per work item a
-                              flag the fast kernel writes and its fallback reads); other layouts ignore it */
+  void* workspace;         /* v_layout 2: device memory of fpf_triattn_workspace_bytes(B, N, H, S, 2) bytes (per work item a flag the
+                              fast kernel writes and its fallback reads).  v_layout 0 / 1: NULL, or fpf_triattn_stage_bytes(B, N,
+                              H, S, D, dtype) bytes or more, which runs a bf16 call with head_dim 32 on the block-layout core (q, v,
+                              the bias and the mask restaged there; q / k / v rows and out rows of 32 contiguous 16-byte aligned
+                              bf16, out_stride[3] = 32); a call that does not meet those conditions runs the op core as without */
   size_t workspace_bytes;
 } FpfTriattnArgs;
 int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err, size_t errlen);
 /* Workspace of fpf_triattn_fwd for this layout (0 for v_layout 0 / 1). */
 size_t fpf_triattn_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t S, int32_t v_layout);
+/* Staging workspace that puts a v_layout 0 / 1 call on the block-layout core: bf16, head_dim 32, S a multiple of 64 or at least
+ * 128, up to 8192; 0 when the call's class has no staged route.  No counterpart in the reference (its op face routes S ranges
+ * to tuned members, kernels/triattn/triattn_native/DESIGN.md:27-40; here the route is this workspace). */
+size_t fpf_triattn_stage_bytes(int64_t B, int64_t N, int64_t H, int64_t S, int64_t D, int32_t dtype);
 
 /* ---------------------------------------------------------------------------------------------------------------- triangle attention (block)
  * The fused block: prologue (LN -> q|k|v|g and the pair-bias projection, reading z or z^T by address) -> core -> epilogue
@@ -228,8 +238,8 @@ typedef struct {
   size_t workspace_bytes;
   int64_t row0;            /* attention rows [row0, row0 + rows) only (bf16; the `big` row-chunked driver); rows <= 0: all N */
   int64_t rows;
-  const float* bias_in;    /* NULL: the block computes the bias; else the full [B, H, N, N] fp32 bias of fpf_triattn_bias_fwd
-                              (required with a row range: every attention row needs the bias of every pair) */
+  const float* bias_in;    /* NULL: the block computes the bias; else the full bias of fpf_triattn_bias_fwd (fpf_triattn_bias_bytes
+                              bytes; required with a row range: every attention row needs the bias of every pair) */
   int32_t mask_frame;      /* 0: mask in z's frame (the ending node reads its columns); 1: mask already in the attention
                               frame (for the ending node the transposed pair mask, so every key row is contiguous); other values:
                               FPF_E_ARGS */
@@ -255,11 +265,14 @@ typedef struct {
   const void* w_qkvg;      /* may be NULL (not read) */
   const void* w_b;         /* [H, C] */
   int32_t ending;
-  float* bias;             /* [B, H, N, N] fp32 out, in the units and layout fpf_triattn_block_fwd's core takes: times log2(e)
-                              and in the v_layout 2 blocks when N is a multiple of 64 up to 8192 (the v_layout 2 core), else as
-                              is, row-major */
+  float* bias;             /* fp32 out, fpf_triattn_bias_bytes(B, N, H, dtype) bytes, in the units and layout fpf_triattn_block_fwd's
+                              core takes: for the bf16 block up to N = 8192 (the v_layout 2 core) [B, H, Np, Np] with Np = N
+                              rounded up to 64, times log2(e), in the 32 x 32 register-order blocks (the padding rows and
+                              columns are not written); else [B, H, N, N] as is, row-major */
 } FpfTriattnBiasArgs;
 int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen);
+/* Bytes of fpf_triattn_bias_fwd's output (no counterpart in the reference: its bias is a torch tensor the driver allocates). */
+size_t fpf_triattn_bias_bytes(int64_t B, int64_t N, int32_t H, int32_t dtype);
 
 /* ---------------------------------------------------------------------------------------------------------------- triangle attention (block stages)
  * The block's prologue and epilogue as separate calls, for callers that run their own core between them.

@@ -119,6 +119,33 @@ def test_metric_tri_attn_n768_sampled_rows_asymmetric_mask(ending):
     assert_bf16_close(got, ref, "metric tri-att ending=%s rows %s" % (ending, rows))
 
 
+@pytest.mark.parametrize("N", [800, 450, 97])
+@pytest.mark.parametrize("ending", [False, True])
+def test_tri_attn_any_n_sampled_rows(N, ending):
+    """N not a multiple of 64: from N = 128 the block-layout core on a key axis padded to a multiple of 64 (the padding keys
+    masked by the keep table, the padding queries never stored; N = 800 is the N <= 800 bucket's measured size), below it (97)
+    the op core; with an asymmetric mask (a random keep pattern, a masked key band, a fully masked row) and no mask at all, on
+    sampled attention rows against the statement restated per row; the whole output finite."""
+    from fpf_hip.attn import pair_fused as PF
+    P = _ta_weights(23)
+    W = _ta_pack(P)
+    g = torch.Generator().manual_seed(24)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16)
+    mask = (torch.rand(1, N, N, generator=g) > 0.2).float()
+    mask[:, :, N - 40:N - 25] = 0
+    mask[:, 7, :] = 0
+    rows = sorted(set([0, 7, N // 3, N // 2, N - 65, N - 64, N - 2, N - 1]))
+    for m in (mask, None):
+        print("[any-N] tri-att N=%d ending=%s mask=%s" % (N, ending, m is not None), flush=True)
+        u = PF.tri_attn_block(z.to(DEV), W, None if m is None else m.to(DEV), ending=ending, residual=False)
+        torch.cuda.synchronize()
+        assert torch.isfinite(u.float()).all()
+        u = u[0].cpu()
+        got = u[:, rows].transpose(0, 1) if ending else u[rows]
+        ref = S.tri_attn_rows(z[0].float(), P, None if m is None else m[0], rows, ending=ending, dtype=torch.float32)
+        assert_bf16_close(got, ref, "any-N tri-att N=%d ending=%s mask=%s rows %s" % (N, ending, m is not None, rows))
+
+
 # ------------------------------------------------------------------------------------------------------------------ configs[3]
 def test_config3_pairformer_layer_n512():
     """BASELINE configs[3]'s layer: N = 512, c_z = 128, c_s = 384, pair track bf16 (4 x 32 triangle heads), single track fp32

@@ -97,6 +97,50 @@ def test_core_bf16_key_padding_is_bitwise_the_cropped_problem():
     assert torch.equal(full[..., :L, :], crop)
 
 
+@pytest.mark.parametrize("S_,vt", [(800, False), (768, False), (456, True), (130, False)])
+def test_op_face_staged_route_against_the_op_core_and_the_oracle(S_, vt):
+    """The op face's staged route (bf16, head_dim 32, S a multiple of 64 or at least 128: q, V^T, bias and mask restaged for the
+    block-layout core, S padded to a multiple of 64) against the same call without a workspace (the op core) and the fp32
+    oracle, with a random keep mask, a dead row and a masked band; V given in [.., S, D] and transposed ([.., D, S] storage)."""
+    from fpf_hip import _lib as L
+    from fpf_hip.kernels import triattn as TA
+    B, N, H, D = 1, 7, 4, 32
+    q, k, v, bias = _rand_op(B, N, H, S_, D, 11, torch.bfloat16)
+    g = torch.Generator().manual_seed(12)
+    mask = torch.rand(B, N, 1, 1, S_, generator=g) > 0.2
+    mask[0, 3] = False
+    mask[0, 5, ..., S_ // 2:S_ // 2 + 40] = False
+    assert L.lib().fpf_triattn_stage_bytes(B, N, H, S_, D, L.DT_BF16) > 0
+    vd = v.to(DEV)
+    if vt:
+        vd = v.transpose(-1, -2).contiguous().to(DEV).transpose(-1, -2)          # V^T storage [B, N, H, D, S]
+    print("[op staged] S=%d vt=%s" % (S_, vt), flush=True)
+    staged = TA.triangle_attention(q.to(DEV), k.to(DEV), vd, bias.to(DEV), mask.to(DEV), word="fast")
+    # the same call through the C ABI with no workspace: the op core
+    out = torch.empty_like(staged)
+    m8 = mask.reshape(B, N, S_).to(DEV).view(torch.uint8)
+    qd, kd, bd = q.to(DEV), k.to(DEV), bias.to(DEV)
+    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, H=H, S=S_, D=D, q=L.ptr(qd), k=L.ptr(kd), v=L.ptr(vd),
+                      bias=L.ptr(bd), bias_dtype=L.DT_F32, mask=L.ptr(m8), mask_dtype=L.DT_U8, out=L.ptr(out), scale=1.0 / D ** 0.5)
+    a.q_stride[:] = list(qd.stride())
+    a.k_stride[:] = list(kd.stride())
+    vs = list(vd.stride())
+    a.v_stride[:] = [vs[0], vs[1], vs[2], vs[4], vs[3]] if vt else vs
+    a.v_layout = 1 if vt else 0
+    a.out_stride[:] = list(out.stride())
+    bs = list(bd.stride())
+    a.bias_stride[:] = [bs[0], bs[2], bs[3], bs[4]]
+    a.mask_stride[:] = list(m8.stride())
+    L.call("fpf_triattn_fwd", a, L.stream_ptr(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(staged.float()).all()
+    ref = S.triangle_attention_op(q, k, v, bias, mask, dtype=torch.float32)
+    assert_bf16_close(staged, ref, "staged S=%d vt=%s" % (S_, vt))
+    assert_bf16_close(out, ref, "op core S=%d vt=%s" % (S_, vt))
+    mean = v[0, 3].float().mean(dim=-2, keepdim=True).expand(H, S_, D)
+    assert max_abs(staged[0, 3].cpu(), mean) <= 2 ** -8 * max(1.0, mean.abs().max().item())
+
+
 def test_core_bf16_run_to_run_bitwise():
     from fpf_hip.kernels import triattn as TA
     q, k, v, bias = (t.to(DEV) for t in _rand_op(1, 8, 4, 200, 32, 3, torch.bfloat16))

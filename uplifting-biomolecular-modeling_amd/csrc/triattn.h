@@ -34,6 +34,8 @@ struct CoreParams {
   float scale;
   const uint64_t* keep;          // block-layout core: keep table [B, N, keep_words(S)] of the mask, or NULL (every key kept)
   uint32_t* redo;                // block-layout core: one flag per (work item, wave), written by the fast kernel
+  int64_t Sv;                    // block-layout core: the real keys / queries (<= S); keys Sv .. S - 1 pad the key axis to a
+                                 // multiple of 64 and are masked by the keep table, queries past Sv are never stored
 };
 
 __device__ __forceinline__ bool mask_keep(const CoreParams& p, int64_t b, int64_t i, int64_t key) {
@@ -133,16 +135,54 @@ __device__ __forceinline__ void vm_wait() {
 }
 
 // The block-layout core (v_layout 2) and its keep table (triattn_pipe.hip).  Keep table of a call: for each (b, attention row
-// i) keep_words(S) = S / 64 + 1 words: word 0 = row flags (TK_ALIVE: some key kept, TK_FULL: every key kept), word 1 + T = the
-// keep bits of keys 64 T .. 64 T + 63 (bit k = key 64 T + k); a row with no kept key has every bit set (it attends uniformly
-// to all keys).
+// i) keep_words(S) = S / 64 + 1 words: word 0 = row flags (TK_ALIVE: some key kept, TK_FULL: every one of the S keys kept),
+// word 1 + T = the keep bits of keys 64 T .. 64 T + 63 (bit k = key 64 T + k).  Keys at or past Sv (the padding of the key
+// axis to a multiple of 64) have bit 0 in every row; a row with no kept key has the bits of all Sv real keys set (it attends
+// uniformly to them).
 constexpr uint64_t TK_ALIVE = 1, TK_FULL = 2;
 __host__ __device__ inline int64_t keep_words(int64_t S) { return S / 64 + 1; }
-// Redo flags of a call (one 32-bit word per work item and wave; the 4-wave split has the most): B H ceil(N / TA_R) ceil(S / 128) 4.
-inline int64_t redo_words(int64_t B, int64_t N, int64_t H, int64_t S) { return B * H * cdiv(N, TA_R) * cdiv(S, 128) * 4; }
+// Redo flags of a call (one 32-bit word per work item and wave), enough for either split: B H ceil(N / TA_R) times the larger of
+// ceil(S / 128) 4 (4 waves of 32 queries per item) and ceil(S / 256) 8 (8 waves; larger when S is an odd multiple of 64 ... 128
+// past a multiple of 256).
+inline int64_t redo_words(int64_t B, int64_t N, int64_t H, int64_t S) {
+  return B * H * cdiv(N, TA_R) * std::max<int64_t>(cdiv(S, 128) * 4, cdiv(S, 256) * 8);
+}
 // dry = true: every check of the launch, nothing launched (callers that must refuse before their first launch)
-int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, uint64_t* keep, hipStream_t st,
-                      char* err, size_t errlen, bool dry = false);
+// mask NULL: every real key kept (a table that only masks the padding keys Sv .. S - 1)
+int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, int64_t Sv, uint64_t* keep,
+                      hipStream_t st, char* err, size_t errlen, bool dry = false);
 int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry = false);
+
+// N a multiple of 64, or any N from 128, up to 8192: the J axis of q / k / V^T / o and of the bias planes is padded to Np = N
+// rounded up to 64 (block_np), the padding keys masked by the keep table, the padding queries never stored.  Below 128 keys a
+// padded call keeps the op core: with few keys the extra bf16 rounding of q * scale * log2(e) no longer averages out (N = 97
+// measured rel-L2 5.0e-3 on the block core against the 5e-3 bar).
+inline bool block_layout2(int dtype, int64_t N) {
+  return dtype == FPF_DT_BF16 && cdiv(N, TA_KT) * TA_KT <= 64 * TA_MAXW && (N % TA_KT == 0 || N >= 2 * TA_KT);
+}
+inline int64_t block_np(int dtype, int64_t N) { return block_layout2(dtype, N) ? cdiv(N, TA_KT) * TA_KT : N; }
+
+// The op face's operands restaged into the block-layout core's layout (triattn_pipe.hip): q2 = q * qmul and k2 = k as
+// [B, N, H, Sp, 32], v2 = V^T [B, N, H, 32, Sp] with each 16-key block in the order 0-3, 8-11, 4-7, 12-15, bias2 = bias * log2(e)
+// as [B, H, Sp, Sp] in 32 x 32 register-order blocks (bias_blk_off), Sp = S rounded up to 64, every padding element zero.  v is
+// read as [B, N, H, S, 32] (v_t = 0) or transposed as [B, N, H, 32, S] (v_t = 1); k2 NULL: k is not copied (the core reads it in
+// place).  The caller has checked: head_dim rows of 32 contiguous, 16-byte aligned bf16 (strides multiples of 8 elements).
+struct StageParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t qs[4], ks[4], vs[4];   // strides of b, n, h, s (v_t = 1: of b, n, h, d)
+  int v_t;
+  const void* bias;
+  int bias_bf16;
+  int64_t bs[3];                 // strides of b, h, query (the key stride is 1)
+  uint16_t* q2;
+  uint16_t* k2;
+  uint16_t* v2;
+  float* bias2;
+  int64_t B, N, H, S, Sp;
+  float qmul;
+};
+int op_stage_launch(const StageParams& p, hipStream_t st, char* err, size_t errlen, bool dry = false);
 
 }  // namespace fpf

@@ -434,6 +434,9 @@ struct ProParams {
   int64_t bias_ld;               // elements between bias rows (>= N)
   int bias_bf16;                 // bias stored as bf16 (else fp32)
   const float* b_g;              // [HD] gate projection bias added to g, or NULL
+  int64_t Np;                    // J extent of the q / k rows and of the blocked bias planes: N, or N padded to 64 for the
+                                 // block-layout core (then every 32-pixel tile up to Np is computed, so V^T's padding keys hold
+                                 // finite values; the padding rows of q / k and of the bias are never written)
 };
 
 __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
@@ -445,8 +448,8 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
   rt_stage_weights(sW + 4 * TP_HD * RT_LD, p.w_b, 32, p.H, tid, 512);
   __syncthreads();
   const int H = p.H, D = TP_HD / H;
-  const int64_t N = p.N, Jp = p.Jp, R = p.rows;
-  const uint32_t tpr = (uint32_t)cdiv(N, 32), per_b = (uint32_t)R * tpr, total = (uint32_t)p.B * per_b;
+  const int64_t N = p.N, Jp = p.Jp, R = p.rows, Np = p.Np;
+  const uint32_t tpr = (uint32_t)cdiv(Np, 32), per_b = (uint32_t)R * tpr, total = (uint32_t)p.B * per_b;
   const uint32_t stride = gridDim.x * RT_WAVES;
   u32x4 raw[8];                                         // the next tile's pixel rows, loaded while this tile computes
   // the lane index is re-read per tile (opaque_lane): lane-dependent address parts kept live across the tile loop would
@@ -500,7 +503,7 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
         u32x4 lo, hi;
         rt_pack16(acc, lo, hi);
         if (!live) continue;
-        uint16_t* dst = blk < 8 ? (blk < 4 ? p.q : p.k) + (((b * R + ii) * H + (blk & 3)) * N + j) * D + 8 * g   // [B, R, H, J, D]
+        uint16_t* dst = blk < 8 ? (blk < 4 ? p.q : p.k) + (((b * R + ii) * H + (blk & 3)) * Np + j) * D + 8 * g  // [B, R, H, Np, D]
                                 : p.g + ((b * R + ii) * N + j) * TP_HD + (blk - 12) * 32 + 8 * g;             // [B, R, J, HD]
         *reinterpret_cast<u32x4*>(dst) = lo;
         *reinterpret_cast<u32x4*>(dst + 16) = hi;
@@ -510,7 +513,7 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
         for (int v = 0; v < 16; ++v) {
           const int hh = c_row(v, g);
           if (hh >= H) continue;
-          const int64_t o = blk_bias ? (b * H + hh) * N * N + bias_blk_off(N, i, j) : ((b * H + hh) * N + i) * p.bias_ld + j;
+          const int64_t o = blk_bias ? (b * H + hh) * Np * Np + bias_blk_off(Np, i, j) : ((b * H + hh) * N + i) * p.bias_ld + j;
           if (p.bias_bf16) reinterpret_cast<uint16_t*>(p.bias)[o] = f2bf(acc[v] * p.bias_scale);
           else p.bias[o] = acc[v] * p.bias_scale;
         }
@@ -597,7 +600,7 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
                                                                   const uint16_t* __restrict__ w_g, const uint16_t* __restrict__ w_o,
                                                                   const float* __restrict__ b_g, const float* __restrict__ b_o,
                                                                   uint16_t* zout, int64_t N, int64_t B, int64_t row0, int64_t rows, int ending,
-                                                                  int residual) {
+                                                                  int residual, int64_t Jo) {
   __shared__ __attribute__((aligned(16))) uint16_t sWg[RT_C * RT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t sWo[RT_C * RT_LD];   // columns permuted to the k-step order above
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
@@ -638,14 +641,14 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
     const int64_t zpix = zpix_of(t, live);
     // o of all four heads for this tile, issued before the LayerNorm
     u32x2 ov2[4][2][2];
-    const uint16_t* op = o + (((b * rows + ii) * H) * N + (live ? j : 0)) * TA_D + 4 * g;   // o rows of this range
+    const uint16_t* op = o + (((b * rows + ii) * H) * Jo + (live ? j : 0)) * TA_D + 4 * g;   // o rows of this range (J extent Jo)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
       for (int half = 0; half < 2; ++half)
 #pragma unroll
         for (int e = 0; e < 2; ++e)
-          ov2[cb][half][e] = live ? *reinterpret_cast<const u32x2*>(op + (int64_t)cb * N * TA_D + 16 * half + 8 * e) : u32x2{0, 0};
+          ov2[cb][half][e] = live ? *reinterpret_cast<const u32x2*>(op + (int64_t)cb * Jo * TA_D + 16 * half + 8 * e) : u32x2{0, 0};
     bf16x8 xb[8];
     rt_ln(raw, g, sLN, eps, xb);
     f32x16 acc[4];
@@ -820,7 +823,8 @@ __global__ void __launch_bounds__(256) triattn_epilogue_f32(const float* __restr
 }
 
 // dry = true: every check, nothing launched
-static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen, bool dry = false) {
+// Sv: the real keys / queries of a v_layout 2 call whose key axis is padded (S = Sv rounded up to 64); -1 = S.
+static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen, bool dry = false, int64_t Sv = -1) {
   if (a->dtype == FPF_DT_BF16) {
     if (a->D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 core serves head_dim 32 (got %lld)", (long long)a->D);
     CoreParams p{};
@@ -845,6 +849,7 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     p.H = a->H;
     p.S = a->S;
     p.scale = a->scale;
+    p.Sv = Sv < 0 ? a->S : Sv;
     p.v_t = a->v_layout;
     if (!(p.v_t == 0 || p.v_t == 1 || p.v_t == 2)) return fail(err, errlen, FPF_E_ARGS, "v_layout %d", a->v_layout);
     for (int t = 0; t < 4; ++t)
@@ -921,7 +926,99 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
   return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);
 }
 
+// The op face on the block-layout core: a bf16 call with head_dim 32 and S the block core serves (a multiple of 64, or at
+// least 128, up to 8192), given a workspace of fpf_triattn_stage_bytes, is restaged (op_stage_launch: q times scale * log2(e),
+// V^T in the core's key order, the bias in blocks, every operand padded to Sp = S rounded up to 64), its mask (and the padding)
+// becomes a keep table, and the persistent core writes the caller's out directly.  k is read in place when no padding is needed
+// and its rows are 16-byte aligned.  Workspace regions: q2 | k2 | v2 (each B N H Sp 32 bf16) | bias2 (B H Sp^2 fp32) | keep | redo.
+struct OpStage {
+  size_t k2, v2, bias2, keep, redo, total;
+};
+static OpStage op_stage_layout(int64_t B, int64_t N, int64_t H, int64_t S) {
+  const int64_t Sp = block_np(FPF_DT_BF16, S);
+  const auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  const size_t r = al((size_t)B * N * H * Sp * TA_D * 2), rb = al((size_t)B * H * Sp * Sp * 4);
+  const size_t rk = al((size_t)B * N * keep_words(Sp) * 8), rr = al((size_t)redo_words(B, N, H, Sp) * 4);
+  return {r, 2 * r, 3 * r, 3 * r + rb, 3 * r + rb + rk, 3 * r + rb + rk + rr};
+}
+static bool op_staged_shape(int dtype, int64_t D, int64_t S) { return dtype == FPF_DT_BF16 && D == TA_D && block_layout2(dtype, S); }
+static bool rows32_ok(const void* p, const int64_t* st4) {     // rows of 32 contiguous bf16, 16-byte aligned, for strides [0..3]
+  return aligned16(p) && ((st4[0] | st4[1] | st4[2] | st4[3]) & 7) == 0;
+}
+
+static int op_staged(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen) {
+  const int64_t B = a->B, N = a->N, H = a->H, S = a->S, Sp = block_np(FPF_DT_BF16, S);
+  const OpStage L = op_stage_layout(B, N, H, S);
+  char* w = static_cast<char*>(a->workspace);
+  const bool k_in_place = Sp == S && rows32_ok(a->k, a->k_stride);
+  StageParams sp{};
+  sp.q = (const uint16_t*)a->q;
+  sp.k = (const uint16_t*)a->k;
+  sp.v = (const uint16_t*)a->v;
+  for (int t = 0; t < 4; ++t) {
+    sp.qs[t] = a->q_stride[t];
+    sp.ks[t] = a->k_stride[t];
+    sp.vs[t] = a->v_stride[t];
+  }
+  sp.v_t = a->v_layout;
+  sp.bias = a->bias;
+  sp.bias_bf16 = a->bias_dtype == FPF_DT_BF16;
+  for (int t = 0; t < 3; ++t) sp.bs[t] = a->bias_stride[t];
+  sp.q2 = reinterpret_cast<uint16_t*>(w);
+  sp.k2 = k_in_place ? nullptr : reinterpret_cast<uint16_t*>(w + L.k2);
+  sp.v2 = reinterpret_cast<uint16_t*>(w + L.v2);
+  sp.bias2 = reinterpret_cast<float*>(w + L.bias2);
+  sp.B = B;
+  sp.N = N;
+  sp.H = H;
+  sp.S = S;
+  sp.Sp = Sp;
+  sp.qmul = a->scale * LOG2E;
+  uint64_t* keep = reinterpret_cast<uint64_t*>(w + L.keep);
+  FpfTriattnArgs c = *a;
+  c.v_layout = 2;
+  c.S = Sp;
+  c.q = sp.q2;
+  const int64_t qs5[5] = {N * H * Sp * TA_D, H * Sp * TA_D, Sp * TA_D, TA_D, 1};
+  const int64_t vs5[5] = {N * H * TA_D * Sp, H * TA_D * Sp, TA_D * Sp, Sp, 1};
+  for (int t = 0; t < 5; ++t) {
+    c.q_stride[t] = qs5[t];
+    c.v_stride[t] = vs5[t];
+    if (!k_in_place) c.k_stride[t] = qs5[t];
+  }
+  if (!k_in_place) c.k = sp.k2;
+  c.v = sp.v2;
+  c.bias = sp.bias2;
+  c.bias_dtype = FPF_DT_F32;
+  c.bias_stride[0] = H * Sp * Sp;
+  c.bias_stride[1] = Sp * Sp;
+  c.bias_stride[2] = Sp;
+  c.bias_stride[3] = 1;
+  c.scale = 1.0f;
+  c.keep = (a->mask || Sp != S) ? keep : nullptr;
+  c.workspace = w + L.redo;
+  c.workspace_bytes = L.total - L.redo;
+  for (int pass = 0; pass < 2; ++pass) {            // every check of every stage before the first launch
+    const bool dry = pass == 0;
+    int rc = op_stage_launch(sp, st, err, errlen, dry);
+    if (rc) return rc;
+    if (c.keep) {
+      rc = keep_table_launch(a->mask, a->mask_dtype == FPF_DT_F32, a->mask_stride, B, N, Sp, S, keep, st, err, errlen, dry);
+      if (rc) return rc;
+    }
+    rc = core_launch(&c, st, err, errlen, dry, S);
+    if (rc || !dry) return rc;
+  }
+  return FPF_OK;
+}
+
 }  // namespace fpf
+
+extern "C" size_t fpf_triattn_stage_bytes(int64_t B, int64_t N, int64_t H, int64_t S, int64_t D, int32_t dtype) {
+  using namespace fpf;
+  if (B <= 0 || N <= 0 || H <= 0 || !op_staged_shape(dtype, D, S)) return 0;
+  return op_stage_layout(B, N, H, S).total;
+}
 
 extern "C" int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err, size_t errlen) {
   using namespace fpf;
@@ -934,6 +1031,11 @@ extern "C" int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err,
   if (!(a->bias_dtype == FPF_DT_F32 || a->bias_dtype == FPF_DT_BF16)) return fail(err, errlen, FPF_E_DTYPE, "bias_dtype %d", a->bias_dtype);
   if (a->mask && !(a->mask_dtype == FPF_DT_U8 || a->mask_dtype == FPF_DT_F32)) return fail(err, errlen, FPF_E_DTYPE, "mask_dtype %d", a->mask_dtype);
   if (!(a->scale > 0.f)) return fail(err, errlen, FPF_E_ARGS, "scale must be > 0");
+  if ((a->v_layout == 0 || a->v_layout == 1) && a->workspace && op_staged_shape(a->dtype, a->D, a->S) &&
+      a->workspace_bytes >= op_stage_layout(a->B, a->N, a->H, a->S).total && rows32_ok(a->q, a->q_stride) &&
+      rows32_ok(a->k, a->k_stride) && rows32_ok(a->v, a->v_stride) && aligned16(a->out) && a->out_stride[3] == TA_D &&
+      ((a->out_stride[0] | a->out_stride[1] | a->out_stride[2]) & 7) == 0)
+    return op_staged(a, static_cast<hipStream_t>(stream), err, errlen);
   return core_launch(a, static_cast<hipStream_t>(stream), err, errlen);
 }
 
@@ -960,23 +1062,26 @@ static int block_shape_check(int dtype, int64_t B, int C, int64_t H, int64_t D, 
 
 // The bf16 block with N a multiple of 64 (up to 8192) runs the block-layout core (v_layout 2): its q carries scale * log2(e),
 // its bias (computed in the block or by fpf_triattn_bias_fwd for bias_in) log2(e).
-static bool block_layout2(int dtype, int64_t N) { return dtype == FPF_DT_BF16 && N % TA_KT == 0 && N <= 64 * TA_MAXW; }
+
 
 static int prologue_launch(int dtype, const void* z, const float* ln_w, const float* ln_b, float eps, const void* w_qkvg, const void* w_b,
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
                            int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f, int64_t bias_ld = -1, int bias_bf16 = 0,
-                           const float* b_g = nullptr, bool dry = false) {
+                           const float* b_g = nullptr, bool dry = false, int64_t Np = -1) {
   if (rows < 0) rows = N;
   if (bias_ld < 0) bias_ld = N;
+  if (Np < 0) Np = N;
+  if (Np != N && (dtype != FPF_DT_BF16 || !(flags & PRO_BIAS_BLK) || (flags & PRO_G) || Np % 64 || Np < N))
+    return fail(err, errlen, FPF_E_SHAPE, "a padded J extent (%lld for N = %lld) serves the bf16 block layout only", (long long)Np, (long long)N);
   if (dtype == FPF_DT_BF16) {
     if (!aligned16(z) || !aligned16(w_qkvg) || !aligned16(w_b) || ((flags & PRO_QKV) && (!aligned16(q) || !aligned16(k) || !aligned16(v))) ||
         ((flags & PRO_G) && !aligned16(g)) || ((flags & PRO_BIAS) && !aligned16(bias)))
       return fail(err, errlen, FPF_E_ALIGN, "prologue operands must be 16-byte aligned");
-    if ((flags & PRO_QKV) && (v_ld < cdiv(N, 32) * 32 || v_ld % 8))
-      return fail(err, errlen, FPF_E_SHAPE, "v_ld %lld: V^T rows need N rounded up to 32", (long long)v_ld);
-    if ((flags & PRO_BIAS_BLK) && (N % 32 || bias_ld != N || bias_bf16))
-      return fail(err, errlen, FPF_E_SHAPE, "blocked bias: fp32, N a multiple of 32, contiguous planes");
+    if ((flags & PRO_QKV) && (v_ld < cdiv(Np, 32) * 32 || v_ld % 8))
+      return fail(err, errlen, FPF_E_SHAPE, "v_ld %lld: V^T rows need %lld rounded up to 32", (long long)v_ld, (long long)Np);
+    if ((flags & PRO_BIAS_BLK) && (Np % 32 || bias_ld != N || bias_bf16))
+      return fail(err, errlen, FPF_E_SHAPE, "blocked bias: fp32, a J extent that is a multiple of 32, contiguous planes");
     ProParams p{};
     p.z = (const uint16_t*)z;
     p.ln_w = ln_w;
@@ -992,6 +1097,7 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.bias = bias;
     p.N = N;
     p.Jp = v_ld;
+    p.Np = Np;
     p.B = B;
     p.row0 = row0;
     p.rows = rows;
@@ -1002,9 +1108,9 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.bias_ld = bias_ld;
     p.bias_bf16 = bias_bf16;
     p.b_g = b_g;
-    if (!rt_tiles_ok(B * rows * cdiv(N, 32))) return fail(err, errlen, FPF_E_SHAPE, "prologue: 2^31 or more 32-pixel tiles");
+    if (!rt_tiles_ok(B * rows * cdiv(Np, 32))) return fail(err, errlen, FPF_E_SHAPE, "prologue: 2^31 or more 32-pixel tiles");
     if (dry) return FPF_OK;
-    const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(N, 32), RT_WAVES));
+    const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(Np, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
@@ -1068,16 +1174,23 @@ extern "C" size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_
   (void)C;
   if (rows <= 0 || rows > N) rows = N;
   const size_t elt = dtype == FPF_DT_F32 ? 4 : 2;
-  const size_t pix = (size_t)B * (size_t)N * (size_t)N;
+  const int64_t Np = fpf::block_np(dtype, N), Jp = fpf::block_layout2(dtype, N) ? Np : fpf::cdiv(N, 32) * 32;
   const size_t HD = (size_t)H * (size_t)D;
-  // q, k, v, o (and g for fp32: the bf16 epilogue recomputes the gate) of `rows` attention rows (HD per pixel each; V^T rows
-  // padded to N rounded up to 32) + the full bias (H fp32 per pixel), 256-byte aligned regions
-  const size_t r1 = ((size_t)B * rows * fpf::cdiv(N, 32) * 32 * HD * elt + 255) & ~(size_t)255;
-  const size_t r2 = (pix * (size_t)H * 4 + 255) & ~(size_t)255;
-  // + the keep-bit table of the block-layout core's mask (B x rows attention rows, N / 64 + 1 words each) and its redo flags
-  const size_t r3 = ((size_t)B * rows * (size_t)fpf::keep_words(N) * 8 + 255) & ~(size_t)255;
-  const size_t r4 = ((size_t)fpf::redo_words(B, rows, H, N) * 4 + 255) & ~(size_t)255;
+  // q, k, v, o (and g for fp32: the bf16 epilogue recomputes the gate) of `rows` attention rows (HD per position each, Jp
+  // positions: N rounded up to 64 for the block-layout core, to 32 otherwise) + the full bias (H fp32 planes of Np x Np),
+  // 256-byte aligned regions
+  const size_t r1 = ((size_t)B * rows * Jp * HD * elt + 255) & ~(size_t)255;
+  const size_t r2 = ((size_t)B * (size_t)Np * (size_t)Np * (size_t)H * 4 + 255) & ~(size_t)255;
+  // + the keep-bit table of the block-layout core (B x rows attention rows, Np / 64 + 1 words each) and its redo flags
+  const size_t r3 = ((size_t)B * rows * (size_t)fpf::keep_words(Np) * 8 + 255) & ~(size_t)255;
+  const size_t r4 = ((size_t)fpf::redo_words(B, rows, H, Np) * 4 + 255) & ~(size_t)255;
   return (dtype == FPF_DT_F32 ? 5 : 4) * r1 + r2 + r3 + r4;
+}
+
+extern "C" size_t fpf_triattn_bias_bytes(int64_t B, int64_t N, int32_t H, int32_t dtype) {
+  if (B <= 0 || N <= 0 || H <= 0) return 0;
+  const int64_t Np = fpf::block_np(dtype, N);
+  return (size_t)B * (size_t)H * (size_t)Np * (size_t)Np * 4;
 }
 
 extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, char* err, size_t errlen) {
@@ -1091,7 +1204,8 @@ extern "C" int fpf_triattn_bias_fwd(const FpfTriattnBiasArgs* a, void* stream, c
   // the prologue kernel with only its bias output (the q|k|v|g weights are neither staged nor read)
   return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg ? a->w_qkvg : a->w_b, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending,
                          nullptr, nullptr, nullptr, 0, nullptr, a->bias, static_cast<hipStream_t>(stream), err, errlen,
-                         PRO_BIAS | (block_layout2(a->dtype, a->N) ? PRO_BIAS_BLK : 0), 0, -1, 1.0f, block_layout2(a->dtype, a->N) ? LOG2E : 1.0f);
+                         PRO_BIAS | (block_layout2(a->dtype, a->N) ? PRO_BIAS_BLK : 0), 0, -1, 1.0f, block_layout2(a->dtype, a->N) ? LOG2E : 1.0f, -1, 0,
+                         nullptr, false, block_np(a->dtype, a->N));
 }
 
 extern "C" int fpf_apb_bias_fwd(const FpfApbBiasArgs* a, void* stream, char* err, size_t errlen) {
@@ -1134,14 +1248,17 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const size_t elt = a->dtype == FPF_DT_F32 ? 4 : 2;
-  const int64_t Jp = cdiv(N, 32) * 32;
+  // bf16 up to N = 8192: the block-layout core, fed q times scale * log2(e), the bias times log2(e) and V^T keys in its
+  // 16-block order, on a J axis of Np = N rounded up to 64 (the padding keys masked, the padding queries not stored)
+  const bool dma_core = block_layout2(a->dtype, N);
+  const int64_t Np = block_np(a->dtype, N), Jp = dma_core ? Np : cdiv(N, 32) * 32;
   const size_t r1 = ((size_t)B * R * Jp * HD * elt + 255) & ~(size_t)255;
   char* w = static_cast<char*>(a->workspace);
   const int regions = a->dtype == FPF_DT_F32 ? 5 : 4;  // q, k, v, o (+ g on the fp32 path)
   void *q = w, *k = w + r1, *v = w + 2 * r1, *o = w + 3 * r1, *g = regions == 5 ? w + 4 * r1 : nullptr;
   float* bias = a->bias_in ? const_cast<float*>(a->bias_in) : reinterpret_cast<float*>(w + regions * r1);
-  uint64_t* keep = reinterpret_cast<uint64_t*>(w + regions * r1 + (((size_t)B * N * N * H * 4 + 255) & ~(size_t)255));
-  void* redo = reinterpret_cast<char*>(keep) + (((size_t)B * R * (size_t)keep_words(N) * 8 + 255) & ~(size_t)255);
+  uint64_t* keep = reinterpret_cast<uint64_t*>(w + regions * r1 + (((size_t)B * Np * Np * H * 4 + 255) & ~(size_t)255));
+  void* redo = reinterpret_cast<char*>(keep) + (((size_t)B * R * (size_t)keep_words(Np) * 8 + 255) & ~(size_t)255);
   const float scale = a->scale > 0.f ? a->scale : 1.0f / sqrtf((float)D);
   FpfTriattnArgs c{};
   c.abi_version = FPF_ABI_VERSION;
@@ -1149,16 +1266,13 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.B = B;
   c.N = R;                                       // the attention rows of this call
   c.H = H;
-  c.S = N;
+  c.S = Np;
   c.D = D;
   c.q = q;
   c.k = k;
   c.v = v;
-  const int64_t st5[5] = {R * H * N * D, H * N * D, N * D, D, 1};
+  const int64_t st5[5] = {R * H * Np * D, H * Np * D, Np * D, D, 1};
   for (int t = 0; t < 5; ++t) c.q_stride[t] = c.k_stride[t] = c.v_stride[t] = c.out_stride[t] = st5[t];
-  // bf16 with N a multiple of 64 (up to 8192): the block-layout core, fed q times scale * log2(e), the bias times log2(e)
-  // and V^T keys in its 16-block order
-  const bool dma_core = block_layout2(a->dtype, N);
   if (a->dtype == FPF_DT_BF16) {               // the bf16 prologue writes V transposed: [B, R, H, D, Jp]
     c.v_layout = dma_core ? 2 : 1;
     c.v_stride[0] = R * H * D * Jp;
@@ -1169,9 +1283,9 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   }
   c.bias = bias;
   c.bias_dtype = FPF_DT_F32;
-  c.bias_stride[0] = H * N * N;
-  c.bias_stride[1] = N * N;
-  c.bias_stride[2] = N;
+  c.bias_stride[0] = H * Np * Np;
+  c.bias_stride[1] = Np * Np;
+  c.bias_stride[2] = Np;
   c.bias_stride[3] = 1;
   // key mask of attention row i: z-frame pair mask row i (starting) / column i (ending), rows from row0
   c.mask_dtype = a->mask_dtype;
@@ -1183,21 +1297,22 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   c.out = o;
   c.scale = dma_core ? 1.0f : scale;
   c.workspace = redo;
-  c.workspace_bytes = (size_t)redo_words(B, R, H, N) * 4;
-  if (dma_core && c.mask) c.keep = keep;                // the block-layout core reads the mask as keep bits
+  c.workspace_bytes = (size_t)redo_words(B, R, H, Np) * 4;
+  if (dma_core && (c.mask || Np != N)) c.keep = keep;   // the block-layout core reads the mask (and the padding) as keep bits
   const bool fused_gate = a->dtype == FPF_DT_BF16;      // bf16: g is recomputed in the epilogue instead of stored
   const int flags = PRO_QKV | (fused_gate ? 0 : PRO_G) | (a->bias_in ? 0 : PRO_BIAS) | (dma_core ? PRO_VPERM | PRO_BIAS_BLK : 0);
   // two passes over the stages: the first runs every check and launches nothing, so a refusal leaves the stream untouched
   for (int pass = 0; pass < 2; ++pass) {
     const bool dry = pass == 0;
     if (c.keep) {
-      const int rc = keep_table_launch(c.mask, c.mask_dtype == FPF_DT_F32, c.mask_stride, B, R, N, keep, st, err, errlen, dry);
+      const int rc = keep_table_launch(c.mask, c.mask_dtype == FPF_DT_F32, c.mask_stride, B, R, Np, N, keep, st, err, errlen, dry);
       if (rc) return rc;
     }
     int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp,
-                             g, bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f, -1, 0, a->b_g, dry);
+                             g, bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f, -1, 0, a->b_g, dry,
+                             Np);
     if (rc) return rc;
-    rc = core_launch(&c, st, err, errlen, dry);
+    rc = core_launch(&c, st, err, errlen, dry, N);
     if (rc) return rc;
     if (fused_gate) {
       if (!aligned16(a->out)) return fail(err, errlen, FPF_E_ALIGN, "out must be 16-byte aligned");
@@ -1211,7 +1326,7 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * R * cdiv(N, 32), RT_WAVES));
     hipLaunchKernelGGL(triattn_epilogue_gate_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w, a->ln_b,
                        a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, a->b_g, a->b_o, (uint16_t*)a->out, N, B, row0,
-                       R, a->ending, a->residual);
+                       R, a->ending, a->residual, Np);
     return launched(err, errlen, "triattn_epilogue_gate_bf16");
   }
 }

@@ -39,7 +39,7 @@ namespace fpf {
 // ---------------------------------------------------------------------------------------------------------------- keep table
 // One wave per (b, attention row i): 64 keys per ballot, 16 mask loads in flight.  The table layout is in triattn.h.
 __global__ void __launch_bounds__(256) triattn_keep_bits(const void* __restrict__ mask, int mask_f32, int64_t ms0, int64_t ms1, int64_t ms2,
-                                                           int64_t B, int64_t N, int64_t S, uint64_t* __restrict__ keep) {
+                                                           int64_t B, int64_t N, int64_t S, int64_t Sv, uint64_t* __restrict__ keep) {
   const int l = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= B * N) return;
@@ -47,29 +47,31 @@ __global__ void __launch_bounds__(256) triattn_keep_bits(const void* __restrict_
   const int nw = (int)(S >> 6);
   uint64_t* out = keep + row * keep_words(S);
   const int64_t base = b * ms0 + i * ms1;
-  uint64_t any = 0, all = ~0ull, mine0 = 0, mine1 = 0;   // words l and 64 + l of the row
+  uint64_t any = 0, all = ~0ull, mine0 = 0, mine1 = 0, real0 = 0, real1 = 0;   // words l and 64 + l of the row (and of real keys)
   for (int c0 = 0; c0 < nw; c0 += 16) {
     bool k[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const int64_t off = base + ((int64_t)64 * (c0 + u) + l) * ms2;
-      k[u] = c0 + u >= nw || (mask_f32 ? static_cast<const float*>(mask)[off] != 0.f : static_cast<const uint8_t*>(mask)[off] != 0);
+      const int64_t key = (int64_t)64 * (c0 + u) + l;
+      const int64_t off = base + (key < Sv ? key : 0) * ms2;
+      k[u] = key < Sv && (!mask || (mask_f32 ? static_cast<const float*>(mask)[off] != 0.f : static_cast<const uint8_t*>(mask)[off] != 0));
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int c = c0 + u;
       if (c >= nw) break;
       const uint64_t bal = __ballot(k[u]);
+      const uint64_t real = __ballot((int64_t)64 * c + l < Sv);
       any |= bal;
       all &= bal;
       if ((c & 63) == l) {
-        if (c < 64) mine0 = bal;
-        else mine1 = bal;
+        if (c < 64) mine0 = bal, real0 = real;
+        else mine1 = bal, real1 = real;
       }
     }
   }
-  if (l < nw) out[1 + l] = any ? mine0 : ~0ull;
-  if (64 + l < nw) out[65 + l] = any ? mine1 : ~0ull;
+  if (l < nw) out[1 + l] = any ? mine0 : real0;
+  if (64 + l < nw) out[65 + l] = any ? mine1 : real1;
   if (l == 0) out[0] = (any ? TK_ALIVE : 0) | (all == ~0ull ? TK_FULL : 0);
 }
 
@@ -79,29 +81,33 @@ __device__ __forceinline__ uint32_t kb_nibble(uint32_t w) {    // bit e = (byte 
   const uint32_t hi = (((w & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | w) & 0x80808080u;   // bit 8 e + 7: byte e is nonzero
   return ((hi >> 7) * 0x10204080u) >> 28;                   // bits 0, 8, 16, 24 gathered to 28 .. 31 (no two products meet)
 }
+// Sv is a multiple of 16 here (the launcher's condition), so no 16-byte load straddles the end of the real keys.
 __global__ void __launch_bounds__(256) triattn_keep_bits_u8(const uint8_t* __restrict__ mask, int64_t ms0, int64_t ms1, int64_t B, int64_t N,
-                                                              int64_t S, uint64_t* __restrict__ keep) {
+                                                              int64_t S, int64_t Sv, uint64_t* __restrict__ keep) {
   const int l = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= B * N) return;
   const int64_t b = row / N, i = row - b * N;
   const uint8_t* src = mask + b * ms0 + i * ms1;
   uint64_t* out = keep + row * keep_words(S);
-  bool any = false, all = true;
+  bool any = false, all = Sv == S;                          // a padded row is never FULL
   for (int64_t c0 = 0; c0 < S; c0 += 1024) {
     const int64_t k0 = c0 + 16 * l;
-    const bool valid = k0 < S;
-    const u32x4 v = valid ? *reinterpret_cast<const u32x4*>(src + k0) : u32x4{0, 0, 0, 0};
+    const bool real = k0 < Sv, inrow = k0 < S;
+    const u32x4 v = real ? *reinterpret_cast<const u32x4*>(src + k0) : u32x4{0, 0, 0, 0};
     const uint32_t piece = kb_nibble(v[0]) | (kb_nibble(v[1]) << 4) | (kb_nibble(v[2]) << 8) | (kb_nibble(v[3]) << 12);
-    any |= __builtin_amdgcn_ballot_w64(valid && piece != 0) != 0;
-    all &= __builtin_amdgcn_ballot_w64(valid && piece != 0xFFFFu) == 0;
+    any |= __builtin_amdgcn_ballot_w64(real && piece != 0) != 0;
+    all &= __builtin_amdgcn_ballot_w64(real && piece != 0xFFFFu) == 0;
     // lanes 4 T + 1 .. 4 T + 3 hand their pieces to lane 4 T (keys 64 T + 16 .. 64 T + 63)
     const uint32_t p1 = __shfl_down(piece, 1), p2 = __shfl_down(piece, 2), p3 = __shfl_down(piece, 3);
-    if ((l & 3) == 0 && valid)
+    if ((l & 3) == 0 && inrow)
       out[1 + (c0 >> 6) + (l >> 2)] = (uint64_t)(piece | (p1 << 16)) | ((uint64_t)(p2 | (p3 << 16)) << 32);
   }
-  if (!any) {                                               // no kept key: every bit set (the row attends uniformly)
-    for (int64_t w = l; w < S / 64; w += 64) out[1 + w] = ~0ull;
+  if (!any) {                                               // no kept key: every real key's bit set (the row attends uniformly)
+    for (int64_t w = l; w < S / 64; w += 64) {
+      const int64_t nreal = Sv - 64 * w;
+      out[1 + w] = nreal >= 64 ? ~0ull : nreal > 0 ? (1ull << nreal) - 1 : 0ull;
+    }
   }
   if (l == 0) out[0] = (any ? TK_ALIVE : 0) | (all ? TK_FULL : 0);
 }
@@ -147,7 +153,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   const uint32_t w0 = lo + j;
   if (w0 >= hi) return;
   const int nT = (int)(p.S / TA_KT);
-  const int32_t S = (int32_t)p.S, N = (int32_t)p.N;     // host-checked to fit 31 bits
+  const int32_t S = (int32_t)p.S, N = (int32_t)p.N, Sv = (int32_t)p.Sv;   // host-checked to fit 31 bits
   if (nT < 2) {                                    // a one-tile key range: every item goes to the fallback kernel
     for (uint32_t w = w0; w < hi; w += nwg)
       if (l == 0) p.redo[(size_t)w * NW + wave] = 1u;
@@ -437,7 +443,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       lt[r] = half_sum(la[r][0] + la[r][1]);
-      redo |= __builtin_amdgcn_ballot_w64(r < cur.nrow && cur.q < S && !(lt[r] >= TD_PS_MIN && lt[r] < TD_PS_MAX)) != 0;
+      redo |= __builtin_amdgcn_ballot_w64(r < cur.nrow && cur.q < Sv && !(lt[r] >= TD_PS_MIN && lt[r] < TD_PS_MAX)) != 0;
     }
     uint64_t oa[6] = {FPF_KARG(redo), FPF_KARG(out), FPF_KARG(os[0]), FPF_KARG(os[1]), FPF_KARG(os[2]), FPF_KARG(os[3])};
     karg_wait(oa);
@@ -447,7 +453,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     if (!redo && NW == 4) {                                  // a flagged item is recomputed whole by the fallback kernel
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        if (r >= cur.nrow || cur.q >= S) continue;
+        if (r >= cur.nrow || cur.q >= Sv) continue;
         const float inv = lt[r] > 0.f ? 1.0f / lt[r] : 0.f;
         uint16_t* op = obase + r * (int64_t)oa[3] + cur.q * (int64_t)oa[5];
 #pragma unroll
@@ -477,7 +483,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
         for (int half = 0; half < 2; ++half) {
           const int qq = 16 * half + (l >> 2), cc = 8 * (l & 3);            // lane: query qq, d cc .. cc + 7
           const u32x4 v = *reinterpret_cast<const u32x4*>(so + qq * TA_OP + cc);
-          if (qbase + qq < S) *reinterpret_cast<u32x4*>(ob + (qbase + qq) * TA_D + cc) = v;   // out rows: 32 contiguous
+          if (qbase + qq < Sv) *reinterpret_cast<u32x4*>(ob + (qbase + qq) * TA_D + cc) = v;   // out rows: 32 contiguous
         }
       }
     }
@@ -526,7 +532,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   const int64_t b = bh / H, h = bh % H;
   const int64_t i0 = (int64_t)rg * TA_R;
   const int64_t q = (int64_t)qt * (32 * NW) + wave * 32 + n;
-  const bool qlive = q < p.S;
+  const bool qlive = q < p.Sv;
 
   bf16x8 qf[TA_R][2];
 #pragma unroll
@@ -601,60 +607,17 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   };
 
   const int64_t nT = p.S / TA_KT;
-  // keep table: wave r < TA_R builds row i0 + r, one ballot per 64 keys; a row with no kept key attends uniformly to every
-  // key (its words become all ones)
+  // keep words of rows i0 .. i0 + TA_R - 1 from the call's keep table (the fast kernel's, so both kernels mask the same keys);
+  // without a table every key is kept.  Rows past N: no key, not dead (never stored)
   const int nw = (int)(p.S >> 6);
   if (wave < TA_R) {
     const int64_t i = i0 + wave;
     const bool rowok = i < p.N;
-    auto build = [&](auto elt) {
-      using T = decltype(elt);
-      const T* mrow = static_cast<const T*>(p.mask) + b * p.ms[0] + (rowok ? i : 0) * p.ms[1];
-      uint64_t any = 0;
-      if (sizeof(T) == 1 && p.mask && p.ms[2] == 1 && (reinterpret_cast<uintptr_t>(mrow) & 15) == 0) {
-        // contiguous u8 keys: lane l reads keys 16 l .. 16 l + 15 of each 1024-key block with one 16-byte load and writes
-        // their keep bits as the 16-bit piece l of the block's words (bit k of piece j = key 16 j + k, the ballot layout)
-        uint16_t* kw16 = reinterpret_cast<uint16_t*>(&sKeepAll[wave][0]);
-        uint32_t anyl = 0;
-        for (int c0 = 0; c0 < (int)p.S; c0 += 1024) {
-          const int key = c0 + 16 * l;
-          uint32_t bits = 0;
-          if (rowok && key < (int)p.S) {
-            const u32x4 m = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(mrow) + key);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              uint32_t t = m[e] | (m[e] >> 1);           // the low bit of each byte: byte != 0
-              t |= t >> 2;
-              t |= t >> 4;
-              t &= 0x01010101u;
-              bits |= ((t * 0x01020408u) >> 24 & 0xfu) << (4 * e);   // gathers the 4 byte flags, key order
-            }
-          }
-          if (key < (int)p.S) kw16[key >> 4] = (uint16_t)bits;
-          anyl |= bits;
-        }
-        any = __ballot(anyl != 0);
-      } else
-      for (int c0 = 0; c0 < nw; c0 += 16) {
-        T raw[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) raw[u] = (p.mask && c0 + u < nw) ? mrow[(int64_t)(64 * (c0 + u) + l) * p.ms[2]] : (T)1;
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          if (c0 + u >= nw) break;
-          const uint64_t bal = __ballot(rowok && raw[u] != (T)0);
-          any |= bal;
-          if (l == 0) sKeepAll[wave][c0 + u] = bal;
-        }
-      }
-      if (rowok && any == 0)
-        for (int c = l; c < nw; c += 64) sKeepAll[wave][c] = ~0ull;
-      if (l == 0) sAlive[wave] = any != 0;
-    };
-    if (p.mask_f32) build(0.0f);
-    else build((uint8_t)0);
+    const uint64_t* kr = p.keep ? p.keep + (b * p.N + (rowok ? i : 0)) * keep_words(p.S) : nullptr;
+    for (int c = l; c < nw; c += 64) sKeepAll[wave][c] = !rowok ? 0ull : kr ? kr[1 + c] : ~0ull;
+    if (l == 0) sAlive[wave] = rowok && (!kr || (kr[0] & TK_ALIVE) != 0);
   }
-  // the Q and mask loads complete here: inside the passes the only vector-memory operations are the counted ones
+  // the Q and keep-table loads complete here: inside the passes the only vector-memory operations are the counted ones
   vm_wait<0>();
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
@@ -797,19 +760,133 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------- op staging
+// The op face (kernels/triattn/__init__.py:1094) hands q, k, v [B, N, H, S, 32] and a [B, 1, H, S, S] bias in its own layout; the
+// block-layout core wants them as the block's prologue writes them.  One wave per (b, n, h, 64-position tile): lane = position s
+// for q and k (a 64-byte row each, q scaled by scale * log2(e) in fp32 and rounded once), and for V the tile goes through the
+// wave's LDS rows so each lane stores 32 consecutive positions of one V^T row in the core's 16-block key order.
+__device__ __forceinline__ int vperm16(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }   // swaps bits 2 and 3
+
+constexpr int ST_VLD = 64 + 8;    // LDS pitch (bf16) of a staged V^T row: 144 B
+
+__global__ void __launch_bounds__(256) triattn_stage_qkv(const StageParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t sV[4][32 * ST_VLD];
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int64_t tiles = p.Sp / 64, total = p.B * p.N * p.H * tiles;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
+  if (unit >= total) return;                                  // whole waves leave: only wave-level synchronisation below
+  const int64_t tile = unit % tiles, bnh = unit / tiles, h = bnh % p.H, bn = bnh / p.H, n = bn % p.N, b = bn / p.N;
+  // the tile's 64 positions x 64 bytes as 256 16-byte chunks; load / store i moves chunk l + 64 i (position (l + 64 i) / 4, head-dim
+  // chunk l % 4), so each instruction touches 1 KB of consecutive q2 / k2 rows (and of the caller's rows when they are contiguous)
+  const int dc = l & 3;
+  uint16_t* q2 = p.q2 + (((b * p.N + n) * p.H + h) * p.Sp + tile * 64) * 32;
+  const uint16_t* qb = p.q + b * p.qs[0] + n * p.qs[1] + h * p.qs[2];
+  const uint16_t* kb = p.k + b * p.ks[0] + n * p.ks[1] + h * p.ks[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ps = (l >> 2) + 16 * i;
+    const int64_t s = tile * 64 + ps;
+    const bool live = s < p.S;
+    const u32x4 r = live ? *reinterpret_cast<const u32x4*>(qb + s * p.qs[3] + 8 * dc) : u32x4{0, 0, 0, 0};
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = pack2(lo_bf(r[e]) * p.qmul, hi_bf(r[e]) * p.qmul);
+    *reinterpret_cast<u32x4*>(q2 + ps * 32 + 8 * dc) = w;
+    if (p.k2) {
+      uint16_t* k2 = p.k2 + (((b * p.N + n) * p.H + h) * p.Sp + tile * 64) * 32;
+      *reinterpret_cast<u32x4*>(k2 + ps * 32 + 8 * dc) = live ? *reinterpret_cast<const u32x4*>(kb + s * p.ks[3] + 8 * dc) : u32x4{0, 0, 0, 0};
+    }
+  }
+  uint16_t* sv = sV[wave];
+  uint16_t* vdst = p.v2 + ((b * p.N + n) * p.H + h) * 32 * p.Sp + tile * 64;      // V^T row 0 of this tile
+  const uint16_t* vb = p.v + b * p.vs[0] + n * p.vs[1] + h * p.vs[2];
+  if (!p.v_t) {
+    // chunk (position ps, dims 8 dc .. 8 dc + 7) goes to column vperm16(ps) of LDS rows 8 dc .. 8 dc + 7
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ps = (l >> 2) + 16 * i;
+      const int64_t s = tile * 64 + ps;
+      const u32x4 r = s < p.S ? *reinterpret_cast<const u32x4*>(vb + s * p.vs[3] + 8 * dc) : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sv[(8 * dc + 2 * e) * ST_VLD + vperm16(ps)] = (uint16_t)(r[e] & 0xffff);
+        sv[(8 * dc + 2 * e + 1) * ST_VLD + vperm16(ps)] = (uint16_t)(r[e] >> 16);
+      }
+    }
+    rt_wave_lds_sync();
+    // V^T tile: 32 rows x 128 bytes; store i moves row (l + 64 i) / 8, chunk l % 8: each instruction writes 8 whole 128-byte row
+    // segments
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = (l >> 3) + 8 * i, c = l & 7;
+      *reinterpret_cast<u32x4*>(vdst + d * p.Sp + 8 * c) = *reinterpret_cast<const u32x4*>(sv + d * ST_VLD + 8 * c);
+    }
+  } else {
+    // V^T given: row d's 64 keys as 4 blocks of 16; lane (d, block) reads one block, and in it the 8-byte halves 4-7 and 8-11
+    // trade places
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int d = (l >> 2) + 16 * i, blk = l & 3;
+      const uint16_t* vr = vb + d * p.vs[3];
+      const int64_t k0 = tile * 64 + 16 * blk;
+      u32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+      if (k0 + 16 <= p.S) {
+        c0 = *reinterpret_cast<const u32x4*>(vr + k0);
+        c1 = *reinterpret_cast<const u32x4*>(vr + k0 + 8);
+      } else {
+        uint16_t t[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) t[e] = k0 + e < p.S ? vr[k0 + e] : (uint16_t)0;
+        c0 = u32x4{t[0] | (uint32_t)t[1] << 16, t[2] | (uint32_t)t[3] << 16, t[4] | (uint32_t)t[5] << 16, t[6] | (uint32_t)t[7] << 16};
+        c1 = u32x4{t[8] | (uint32_t)t[9] << 16, t[10] | (uint32_t)t[11] << 16, t[12] | (uint32_t)t[13] << 16, t[14] | (uint32_t)t[15] << 16};
+      }
+      uint16_t* dst = vdst + d * p.Sp + 16 * blk;
+      *reinterpret_cast<u32x4*>(dst) = u32x4{c0[0], c0[1], c1[0], c1[1]};
+      *reinterpret_cast<u32x4*>(dst + 8) = u32x4{c0[2], c0[3], c1[2], c1[3]};
+    }
+  }
+}
+
+// bias2 block (qb, kb) of plane (b, h): one wave, piece j = 256 consecutive floats, lane (n, g) = query qb 32 + n, keys kb 32 + 8j +
+// 4g .. + 3 (the register order of the core's S^T accumulator); values past S are zero.
+__global__ void __launch_bounds__(256) triattn_stage_bias(const StageParams p) {
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, n = l & 31, g = l >> 5;
+  const int64_t nb = p.Sp / 32, total = p.B * p.H * nb * nb;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
+  if (unit >= total) return;
+  const int64_t kb = unit % nb, qb = (unit / nb) % nb, bh = unit / (nb * nb), h = bh % p.H, b = bh / p.H;
+  const int64_t qi = qb * 32 + n;
+  const int64_t rowoff = b * p.bs[0] + h * p.bs[1] + (qi < p.S ? qi : 0) * p.bs[2];
+  float* dst = p.bias2 + bh * p.Sp * p.Sp + ((qb * nb + kb) << 10) + l * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t key = kb * 32 + 8 * j + 4 * g + e;
+      float x = 0.f;
+      if (qi < p.S && key < p.S)
+        x = p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[rowoff + key]) : static_cast<const float*>(p.bias)[rowoff + key];
+      w[e] = x * LOG2E;
+    }
+    *reinterpret_cast<f32x4*>(dst + 256 * j) = w;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------- launchers
-int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, uint64_t* keep, hipStream_t st,
-                      char* err, size_t errlen, bool dry) {
-  if (!mask || !keep) return fail(err, errlen, FPF_E_ARGS, "keep table: mask / table is NULL");
+int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, int64_t Sv, uint64_t* keep,
+                      hipStream_t st, char* err, size_t errlen, bool dry) {
+  if (!keep) return fail(err, errlen, FPF_E_ARGS, "keep table: table is NULL");
   if (S % TA_KT != 0 || S > (int64_t)TA_KT * TA_MAXW) return fail(err, errlen, FPF_E_SHAPE, "keep table: S a multiple of 64 up to %d", TA_KT * TA_MAXW);
+  if (Sv <= 0 || Sv > S) return fail(err, errlen, FPF_E_SHAPE, "keep table: real keys %lld outside (0, %lld]", (long long)Sv, (long long)S);
   const int64_t blocks = cdiv(B * N, 4);
   if (blocks > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "keep table: grid too large");
   if (dry) return FPF_OK;
-  if (!mask_f32 && ms[2] == 1 && aligned16(mask) && ms[0] % 16 == 0 && ms[1] % 16 == 0) {
-    hipLaunchKernelGGL(triattn_keep_bits_u8, dim3((unsigned)blocks), dim3(256), 0, st, static_cast<const uint8_t*>(mask), ms[0], ms[1], B, N, S, keep);
+  if (mask && !mask_f32 && ms[2] == 1 && aligned16(mask) && ms[0] % 16 == 0 && ms[1] % 16 == 0 && Sv % 16 == 0) {
+    hipLaunchKernelGGL(triattn_keep_bits_u8, dim3((unsigned)blocks), dim3(256), 0, st, static_cast<const uint8_t*>(mask), ms[0], ms[1], B, N, S, Sv, keep);
     return launched(err, errlen, "triattn_keep_bits_u8");
   }
-  hipLaunchKernelGGL(triattn_keep_bits, dim3((unsigned)blocks), dim3(256), 0, st, mask, mask_f32, ms[0], ms[1], ms[2], B, N, S, keep);
+  hipLaunchKernelGGL(triattn_keep_bits, dim3((unsigned)blocks), dim3(256), 0, st, mask, mask_f32, ms[0], ms[1], ms[2], B, N, S, Sv, keep);
   return launched(err, errlen, "triattn_keep_bits");
 }
 
@@ -820,8 +897,12 @@ int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64
 // queries) elsewhere.  The fallback runs on the same stream right after the fast kernel, over the same grid.
 int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry) {
   const int64_t rows_heads = p.B * p.H * cdiv(p.N, TA_R);
-  const bool wide = p.S % (32 * TA_DMA_WAVES) == 0 && rows_heads * (p.S / (32 * TA_DMA_WAVES)) >= 8 * (int64_t)num_cus();
-  const int64_t total = wide ? rows_heads * (p.S / (32 * TA_DMA_WAVES)) : rows_heads * cdiv(p.S, 128);
+  // 8 waves share each K / V^T tile among 256 queries; where S is not a multiple of 256 the last query tile is partly padding.
+  // They are taken when that padding costs less than a fifth over the 4-wave split's own (an item of 128 queries per 4 waves)
+  // and the grid holds 8 or more workgroups per CU (measured: the 8-wave split 11-15 % slower at S = 384, where it pads a third)
+  const int64_t q8 = cdiv(p.S, 32 * TA_DMA_WAVES), q4 = cdiv(p.S, 128);
+  const bool wide = 5 * q8 * (32 * TA_DMA_WAVES) < 6 * q4 * 128 && rows_heads * q8 >= 8 * (int64_t)num_cus();
+  const int64_t total = wide ? rows_heads * q8 : rows_heads * q4;
   if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
   // per-lane byte offsets from the scalar bases are 32-bit: q (query, d), bias (query), K (key row of a tile), V^T (d row)
   const int64_t lim = 0x7fffffffLL;
@@ -830,6 +911,8 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
       TA_D * p.vs[3] * 2 > lim || (TA_R - 1) * std::max(p.qs[1], std::max(p.ks[1], p.vs[1])) * 2 > lim ||
       p.B * p.N > lim || p.S > lim)
     return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
+  if (p.Sv <= 0 || p.Sv > p.S || (p.Sv < p.S && !p.keep))
+    return fail(err, errlen, FPF_E_ARGS, "v_layout 2: %lld real keys of %lld need a keep table masking the padding", (long long)p.Sv, (long long)p.S);
   if (dry) return FPF_OK;
   // persistent grids: one fast workgroup per CU walking every nwg-th item of its XCD's range (two per CU for the 4-wave
   // split, whose LDS and registers fit twice), and at least 8 workgroups, so that every XCD's range has one (with fewer
@@ -846,6 +929,16 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
     hipLaunchKernelGGL(triattn_core_bf16_redo<4>, redo_grid, dim3(256), 0, st, p);
   }
   return launched(err, errlen, "triattn_core_bf16_pipe");
+}
+
+int op_stage_launch(const StageParams& p, hipStream_t st, char* err, size_t errlen, bool dry) {
+  if (p.Sp % 64 || p.Sp < p.S || p.S <= 0) return fail(err, errlen, FPF_E_SHAPE, "staging: Sp %lld for S %lld", (long long)p.Sp, (long long)p.S);
+  const int64_t u1 = p.B * p.N * p.H * (p.Sp / 64), u2 = p.B * p.H * (p.Sp / 32) * (p.Sp / 32);
+  if (cdiv(u1, 4) > 0x7fffffffLL || cdiv(u2, 4) > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "staging: grid too large");
+  if (dry) return FPF_OK;
+  hipLaunchKernelGGL(triattn_stage_qkv, dim3((unsigned)cdiv(u1, 4)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(triattn_stage_bias, dim3((unsigned)cdiv(u2, 4)), dim3(256), 0, st, p);
+  return launched(err, errlen, "triattn_stage_qkv / triattn_stage_bias");
 }
 
 }  // namespace fpf

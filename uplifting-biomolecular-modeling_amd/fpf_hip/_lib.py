@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 DT_BF16, DT_F32, DT_U8, DT_F32Z_BF16 = 1, 2, 3, 4
 TRIMUL_NOALLOC_SCRATCH_BYTES = 50331648          # include/fpf_hip.h FPF_TRIMUL_NOALLOC_SCRATCH_BYTES
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
@@ -92,6 +92,8 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_trimul_rows_workspace_bytes": ([i64, i64, i64, i32, i32], sz),
     "fpf_triattn_fwd": ([C.POINTER(TriattnArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_workspace_bytes": ([i64, i64, i64, i32, i32, i32, i32], sz),
+    "fpf_triattn_bias_bytes": ([i64, i64, i32, i32], sz),
+    "fpf_triattn_stage_bytes": ([i64, i64, i64, i64, i64, i32], sz),
     "fpf_triattn_workspace_bytes": ([i64, i64, i64, i64, i32], sz),
     "fpf_triattn_bias_fwd": ([C.POINTER(TriattnBiasArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_fwd": ([C.POINTER(TriattnBlockArgs), vp, C.c_char_p, sz], C.c_int),

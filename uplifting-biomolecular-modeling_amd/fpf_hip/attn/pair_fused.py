@@ -372,7 +372,7 @@ def tri_attn_block_chunked(z, W, mask=None, *, ending=False, residual=False, chu
     rows = min(chunk, N)
     lib = L.lib()
     ws = F.scratch(z.device, lib.fpf_triattn_block_workspace_bytes(B, N, rows, W.C, W.H, W.D, L.DT_BF16))
-    bias = F.scratch(z.device, B * W.H * N * N * 4, kind="bias")
+    bias = F.scratch(z.device, lib.fpf_triattn_bias_bytes(B, N, W.H, L.DT_BF16), kind="bias")
     ab = L.TriattnBiasArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), ln_w=L.ptr(W.ln_w),
                            ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wp[0]), w_b=L.ptr(wp[1]), ending=1 if ending else 0, bias=L.ptr(bias))
     _launch("fpf_triattn_bias_fwd", ab, z.device)

@@ -109,9 +109,14 @@ def triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, prefer=Non
     elif tuple(out.shape) != (B, N, H, S, D) or out.dtype != q.dtype or out.stride(-1) != 1:
         raise Refusal("out", sel.row, F.ROW_STOCK, "out must be [B,N,H,S,D] in q's dtype with a contiguous head_dim")
     sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
-    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if q.dtype == torch.bfloat16 else L.DT_F32, B=B, N=N, H=H, S=S, D=D,
+    dt = L.DT_BF16 if q.dtype == torch.bfloat16 else L.DT_F32
+    # bf16 at head_dim 32: a workspace of the staging size routes the call onto the block-layout core (q, V^T, bias and mask
+    # restaged into its layout; the library keeps the op core when the strides do not allow it)
+    stage = L.lib().fpf_triattn_stage_bytes(B, N, H, S, D, dt)
+    ws = F.scratch(q.device, stage, kind="op") if stage else None
+    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=dt, B=B, N=N, H=H, S=S, D=D,
                       q=L.ptr(q), k=L.ptr(k), v=L.ptr(v), bias=L.ptr(bias), bias_dtype=L.DT_F32 if bias.dtype == torch.float32 else L.DT_BF16,
-                      mask=L.ptr(m), mask_dtype=mdt, out=L.ptr(out), scale=sc)
+                      mask=L.ptr(m), mask_dtype=mdt, out=L.ptr(out), scale=sc, workspace=L.ptr(ws), workspace_bytes=0 if ws is None else ws.numel())
     for name, t in (("q_stride", q), ("k_stride", k), ("v_stride", v), ("out_stride", out)):
         getattr(a, name)[:] = _strides(t, 5)
     if v_t:
