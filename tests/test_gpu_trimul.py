@@ -5,7 +5,7 @@ import os
 import pytest
 import torch
 
-from _util import assert_bf16_close, assert_bf16_residual_close, assert_f32_close, max_abs, rel_l2
+from _util import assert_bf16_close, assert_bf16_residual_close, assert_bf16_ulp_close, assert_f32_close, max_abs, rel_l2
 from conftest import GOLDEN
 from oracle import stock as S
 from oracle import vectors as V
@@ -48,11 +48,14 @@ def test_trimul_bf16(direction, B, N, masked):
 
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
-@pytest.mark.parametrize("N", [512, 768])
+@pytest.mark.parametrize("N", [512, 768, 800, 600])
 def test_trimul_bf16_256_tiles_sampled_rows(direction, N):
-    """Planes padded to a multiple of 256 take the persistent 256 x 256 contraction, whose slab ring runs across tile
-    boundaries (N = 512: two tiles per workgroup; N = 768, the bench shape: four or five).  Sampled rows on both sides of
-    every tile boundary against the fp32 oracle, with a ragged mask; a second call is bitwise the first."""
+    """The persistent 256 x 256 contraction, whose slab ring runs across tile boundaries (N = 512: two tiles per workgroup;
+    N = 768, the bench shape: four or five), also on planes padded to an odd multiple of 128 (N = 800 -> 896, N = 600 -> 640),
+    whose last tile row and column are half inside the plane.  Sampled rows on both sides of every tile boundary against the
+    fp32 oracle, with a ragged mask, at the bf16 bars with max-abs counted above the output's half-ulp (these updates reach
+    |value| of a few units, where a bf16 output's own rounding is up to 1.6e-2: the max-abs measures 1.6-2.0e-2 at every N, with
+    rel-L2 4.4-4.5e-3); a second call is bitwise the first."""
     from fpf_hip.kernels import trimul as TM
     w = _weights(128, 11, torch.bfloat16)
     g = torch.Generator().manual_seed(N + 1)
@@ -66,10 +69,10 @@ def test_trimul_bf16_256_tiles_sampled_rows(direction, N):
     u2 = TM.triangle_multiplication(zd, md, direction=direction, weights=wd, word="fast")
     torch.cuda.synchronize()
     assert torch.equal(u1, u2)
-    rows = [0, 1, 130, 255, 256, 383, N // 2 + 3, N - 256, N - 8, N - 1]
+    rows = sorted(set([0, 1, 130, 255, 256, 383, N // 2 + 3, N - 256, N - 130, N - 8, N - 1]))
     got = u1[rows].cpu()
     ref = S.trimul_rows(z.float(), mask, rows, direction=direction, weights={k: v.float() for k, v in w.items()}, dtype=torch.float32)
-    assert_bf16_close(got, ref, "trimul256 %s N%d rows %s" % (direction, N, rows))
+    assert_bf16_ulp_close(got, ref, "trimul256 %s N%d rows %s" % (direction, N, rows))
 
 
 def test_trimul_bf16_residual_in_place_equals_out_of_place():

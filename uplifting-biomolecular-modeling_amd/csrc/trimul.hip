@@ -124,86 +124,11 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z
   }
 }
 
-// ---------------------------------------------------------------------------------------------------------------- contraction (bf16)
-constexpr int CT_BK = 64;
-constexpr int CT_LD = CT_BK + 8;     // 144-byte LDS rows: conflict-free 16-byte fragment reads
-
-// Rows a0 .. a0 + Ra - 1 of the A plane (whose layout holds La rows per column block: Np for the whole plane) against the
-// whole B plane, into an X plane of Ra rows (local row = plane row - a0); X rows at or past nrows (local) and columns at or
-// past N are not written.  The whole op: La = Ra = Np, a0 = 0.
-__global__ void __launch_bounds__(256) trimul_contract_bf16(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X,
-                                                            int64_t Np, int64_t N, int64_t nbatch, int64_t La, int64_t a0, int64_t Ra, int64_t nrows) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[TM_TILE * CT_LD];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[TM_TILE * CT_LD];
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  // XCD-aware order: the hardware deals workgroups round-robin over 8 XCDs; give each XCD a contiguous run of (plane, tile)
-  // work so the 36-ish tiles of one plane share that XCD's L2.
-  const int64_t tiles = (Ra / TM_TILE) * (Np / TM_TILE);
-  const int64_t total = tiles * nbatch;
-  const int64_t L = blockIdx.x;
-  const int64_t per = (total + 7) / 8;
-  const int64_t w = (L % 8) * per + L / 8;
-  if (w >= total) return;
-  const int64_t bc = w / tiles, t = w % tiles;
-  const int64_t ti = t / (Np / TM_TILE), tj = t % (Np / TM_TILE);
-  const int64_t pb_ = bc / TM_C, pc = bc % TM_C, rstride = TL_ROW, kstride_a = tl_kblk(La), kstride_b = tl_kblk(Np);   // tiled planes
-  const uint16_t* ap = A + tl_off_r(pb_, pc, a0 + ti * TM_TILE, 0, Np, La);
-  const uint16_t* bp = Bm + tl_off(pb_, pc, tj * TM_TILE, 0, Np);
-  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;     // the wave's 64 x 64 sub-tile
-  f32x16 acc[2][2] = {};
-  // global -> register prefetch: 128 rows x 64 k = 1024 16-byte chunks per operand, 4 per thread
-  u32x4 ra[4], rb[4];
-  auto gload = [&](int64_t k0) {
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int i = tid + 256 * it, r = i >> 3, ch = i & 7;
-      const int64_t kk = k0 + ch * 8, o = r * rstride + (kk & 31);
-      ra[it] = *reinterpret_cast<const u32x4*>(ap + o + (kk >> 5) * kstride_a);
-      rb[it] = *reinterpret_cast<const u32x4*>(bp + o + (kk >> 5) * kstride_b);
-    }
-  };
-  gload(0);
-  for (int64_t k0 = 0; k0 < Np; k0 += CT_BK) {
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int i = tid + 256 * it, r = i >> 3, ch = i & 7;
-      *reinterpret_cast<u32x4*>(&sA[r * CT_LD + ch * 8]) = ra[it];
-      *reinterpret_cast<u32x4*>(&sB[r * CT_LD + ch * 8]) = rb[it];
-    }
-    __syncthreads();
-    if (k0 + CT_BK < Np) gload(k0 + CT_BK);
-#pragma unroll
-    for (int ks = 0; ks < CT_BK / 16; ++ks) {
-      bf16x8 fa[2], fb[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        fa[s] = as_bf8(*reinterpret_cast<const u32x4*>(&sA[(wr + 32 * s + n) * CT_LD + 16 * ks + 8 * g]));
-        fb[s] = as_bf8(*reinterpret_cast<const u32x4*>(&sB[(wc + 32 * s + n) * CT_LD + 16 * ks + 8 * g]));
-      }
-#pragma unroll
-      for (int si = 0; si < 2; ++si)
-#pragma unroll
-        for (int sj = 0; sj < 2; ++sj) acc[si][sj] = mfma32(fa[si], fb[sj], acc[si][sj]);
-    }
-  }
-  // D layout: row i = 8(v/4) + 4g + v%4 of the sub-tile, column j = n
-#pragma unroll
-  for (int si = 0; si < 2; ++si)
-#pragma unroll
-    for (int sj = 0; sj < 2; ++sj) {
-      const int64_t j = tj * TM_TILE + wc + 32 * sj + n;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t i = ti * TM_TILE + wr + 32 * si + c_row(v, g);
-        if (i < nrows && j < N) X[tl_off_r(pb_, pc, i, j, Np, Ra)] = f2bf(acc[si][sj][v]);
-      }
-    }
-}
-
 // ---------------------------------------------------------------------------------------------------------------- contraction, 256 x 256 tiles
-// For planes padded to a multiple of 256: a workgroup (4 waves, one per SIMD) computes 256 x 256 tiles of X, each wave a
-// 128 x 128 quarter in 16 accumulators.  The grid is persistent (one workgroup per CU): workgroup b runs on XCD b % 8
+// Planes padded to a multiple of 128: a workgroup (4 waves, one per SIMD) computes 256 x 256 tiles of X, each wave a 128 x 128
+// quarter in 16 accumulators.  Where the rows (or columns) end 128 into a tile (a padded extent of an odd multiple of 128),
+// that tile's upper 128 rows of the operand re-read its lower 128 (the DMA addresses of slots 512 .. 1023 step back 128 rows),
+// so nothing is read past the plane; the duplicated quarters are computed and not stored.  The grid is persistent (one workgroup per CU): workgroup b runs on XCD b % 8
 // (round-robin dispatch), XCD x owns the contiguous tile range [x per, (x + 1) per) and its workgroups take every
 // (grid / 8)-th tile of it, so the tiles that share A rows / B rows of one plane are computed by one XCD at the same time.
 // The A and B k-slabs (256 rows x 32 k each) go straight from global memory into LDS (global_load_lds_dwordx4: no VGPR
@@ -235,7 +160,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   __shared__ __attribute__((aligned(16))) uint16_t sA[CB_NBUF][CB_T * CB_K];
   __shared__ __attribute__((aligned(16))) uint16_t sB[CB_NBUF][CB_T * CB_K];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
-  const int64_t tpd = Np / CB_T, tiles = (Ra / CB_T) * tpd, total = tiles * nbatch;   // A rows a0 .. a0 + Ra - 1, B whole
+  const int64_t tpd = cdiv(Np, CB_T), tiles = cdiv(Ra, CB_T) * tpd, total = tiles * nbatch;   // A rows a0 .. a0 + Ra - 1, B whole
   const int64_t per = (total + 7) / 8, g8 = gridDim.x / 8;     // the host launches a multiple of 8 workgroups
   const int64_t x0 = (blockIdx.x % 8) * per, first = x0 + blockIdx.x / 8, end = total < x0 + per ? total : x0 + per;
   if (first >= end) return;
@@ -256,22 +181,25 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
     const int sl = 256 * q + tid, r = sl >> 2, c = (sl & 3) ^ ((r >> 2) & 3);
     goff[q] = (uint32_t)(r * TL_ROW + 8 * c);
   }
-  // issue cursor: the next slab to load is slab ikt of tile ir (operand bases ia0 / ib0)
+  // issue cursor: the next slab to load is slab ikt of tile ir (operand bases ia0 / ib0 of slots 0 .. 511, rows 0 .. 127 of the
+  // tile; ia1 / ib1 of slots 512 .. 1023, rows 128 .. 255, or rows 0 .. 127 again where the tile is half inside)
   int ir = 0, ikt = 0;
-  const uint16_t *ia0, *ib0;
+  const uint16_t *ia0, *ib0, *ia1, *ib1;
   auto set_bases = [&](int r) {
     int64_t bc, ti, tj;
     tile_of(r, bc, ti, tj);
     ia0 = A + tl_off_r(bc / TM_C, bc % TM_C, a0 + ti * CB_T, 0, Np, La);
     ib0 = Bm + tl_off(bc / TM_C, bc % TM_C, tj * CB_T, 0, Np);
+    ia1 = ti * CB_T + CB_T > Ra ? ia0 - 128 * TL_ROW : ia0;
+    ib1 = tj * CB_T + CB_T > Np ? ib0 - 128 * TL_ROW : ib0;
   };
   set_bases(0);
   auto issue_next = [&](int buf) {
     const int64_t koa = (int64_t)ikt * kstride_a, kob = (int64_t)ikt * kstride_b;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      lds_dma16(ia0 + goff[q] + koa, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
-      lds_dma16(ib0 + goff[q] + kob, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16((q < 2 ? ia0 : ia1) + goff[q] + koa, lds_addr(&sA[buf][(256 * q + 64 * wave) * 8]));
+      lds_dma16((q < 2 ? ib0 : ib1) + goff[q] + kob, lds_addr(&sB[buf][(256 * q + 64 * wave) * 8]));
     }
     if (++ikt == nk) {
       ikt = 0;
@@ -335,7 +263,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
 #pragma unroll
       for (int sj = 0; sj < 4; ++sj) acc[si][sj] = f32x16{};
     const int u0 = r * nk;
-    slab(r > 0, u0, f0a, f0b, f1a, f1b);                 // nk is even: Np is a multiple of 256
+    slab(r > 0, u0, f0a, f0b, f1a, f1b);                 // nk is even: Np is a multiple of 128
     slab(r > 0, u0 + 1, f1a, f1b, f0a, f0b);
     for (int kt = 2; kt < nk; kt += 2) {
       slab(false, u0 + kt, f0a, f0b, f1a, f1b);
@@ -348,6 +276,8 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
     // the loop needs): row n of each 32-row block, 8 g columns in
     const uint32_t lane = (uint32_t)opaque_lane();
     const uint32_t lane_el = (lane & 31) * (uint32_t)TL_ROW + 8 * (lane >> 5);
+    // a quarter past the rows (or columns) of a half-inside tile holds duplicates: not stored (wave-uniform)
+    const bool keep_r = ti * CB_T + wr < Ra, keep_c = tj * CB_T + wc < Np;
 #pragma unroll
     for (int si = 0; si < 4; ++si)
 #pragma unroll
@@ -355,8 +285,10 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
         u32x4 lo, hi;
         rt_pack16(acc[si][sj], lo, hi);
         uint16_t* xp = X + tl_off_r(pb_, pc, ti * CB_T + wr + 32 * si, tj * CB_T + wc + 32 * sj, Np, Ra) + lane_el;
-        *reinterpret_cast<u32x4*>(xp) = lo;
-        *reinterpret_cast<u32x4*>(xp + 16) = hi;
+        if (keep_r && keep_c) {
+          *reinterpret_cast<u32x4*>(xp) = lo;
+          *reinterpret_cast<u32x4*>(xp + 16) = hi;
+        }
         __builtin_amdgcn_sched_barrier(0);               // one accumulator at a time (bounded VGPR use)
       }
   }
@@ -868,30 +800,23 @@ __global__ void __launch_bounds__(64 * FM_NW) trimul_k3_f32m(const float* zin, f
 }
 
 static int64_t padded(int64_t n) { return cdiv(n, TM_TILE) * TM_TILE; }
-// The contraction tile of n (256 when the padded planes take the 256-tile kernel, else 128).
-static int64_t ctile(int64_t n) { return padded(n) % CB_T == 0 ? CB_T : TM_TILE; }
+// The contraction tile: 256 at every n (a padded extent of an odd multiple of 128 ends with half-inside tiles).
+static int64_t ctile(int64_t n) { (void)n; return CB_T; }
 
 // Contraction -> K3 of the bf16 path for output rows [row0, row0 + rows), from whole A and B planes: A rows a0 .. a0 + Ra - 1
 // (the tile-aligned cover of the row block) into an X plane of Ra rows.  The whole op is row0 = 0, rows = N, Ra = Np.
 static int bf16_rows(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* pa, const uint16_t* pb, uint16_t* X, int64_t row0, int64_t rows,
                      char* err, size_t errlen) {
   const int64_t N = a->n, Np = padded(N), B = a->batch, T = ctile(N);
-  const int64_t a0 = row0 / T * T, Ra = cdiv(row0 + rows, T) * T - a0;   // a0 + Ra <= Np: Np is a multiple of T
+  // the row block's cover by contraction tiles, capped at the plane (Np, a multiple of 128, may end half way into a tile)
+  const int64_t a0 = row0 / T * T, Ra = std::min<int64_t>(cdiv(row0 + rows, T) * T, Np) - a0;
   const int64_t k3_tiles = B * rows * cdiv(N, 32);
   if (!rt_tiles_ok(k3_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
-  int rc;
-  if (T == CB_T) {
-    const int64_t tiles = (Ra / CB_T) * (Np / CB_T) * B * TM_C;
-    const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;    // persistent, a multiple of 8
-    if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
-    hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * TM_C, Np, a0, Ra);
-    rc = launched(err, errlen, "trimul_contract_bf16_256");
-  } else {
-    const int64_t tiles = (Ra / TM_TILE) * (Np / TM_TILE) * B * TM_C;
-    hipLaunchKernelGGL(trimul_contract_bf16, dim3((unsigned)(cdiv(tiles, 8) * 8)), dim3(256), 0, st, pa, pb, X, Np, N, B * TM_C, Np, a0, Ra,
-                       std::min<int64_t>(Ra, N - a0));
-    rc = launched(err, errlen, "trimul_contract_bf16");
-  }
+  const int64_t tiles = cdiv(Ra, CB_T) * cdiv(Np, CB_T) * B * TM_C;
+  const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;    // persistent, a multiple of 8
+  if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
+  hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * TM_C, Np, a0, Ra);
+  int rc = launched(err, errlen, "trimul_contract_bf16_256");
   if (rc) return rc;
   const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
   hipLaunchKernelGGL(a->dtype == FPF_DT_F32Z_BF16 ? trimul_k3_bf16<true> : trimul_k3_bf16<false>, dim3(k3_grid), dim3(512), 0, st, a->z, a->out, X,
