@@ -120,3 +120,17 @@ def test_apb_refusals_need_no_device():
     with pytest.raises(L.LibError) as e:
         L.call("fpf_apb_bias_fwd", b, None)
     assert e.value.kind == "args"
+
+
+def test_build_reads_kernel_resource_usage_and_refuses_vgpr_spills():
+    """The build reads the compiler's kernel-resource-usage remarks per kernel (a kernel that spills vector registers is refused:
+    its reloads' waits would drain the transfers in flight inside its loops)."""
+    from fpf_hip import _build
+    txt = ("a.hip:1:1: remark: Function Name: _Zk1 [-Rpass-analysis=kernel-resource-usage]\n"
+           "a.hip:1:1: remark:     VGPRs: 200 [-Rpass-analysis=kernel-resource-usage]\n"
+           "a.hip:1:1: remark:     VGPRs Spill: 0 [-Rpass-analysis=kernel-resource-usage]\n"
+           "a.hip:1:1: remark:     Occupancy [waves/SIMD]: 2 [-Rpass-analysis=kernel-resource-usage]\n"
+           "a.hip:9:1: remark: Function Name: _Zk2 [-Rpass-analysis=kernel-resource-usage]\n"
+           "a.hip:9:1: remark:     VGPRs Spill: 12 [-Rpass-analysis=kernel-resource-usage]\n")
+    ru = _build.resource_usage(txt)
+    assert ru == {"_Zk1": {"VGPRs": 200, "VGPRs Spill": 0, "Occupancy": 2}, "_Zk2": {"VGPRs Spill": 12}}

@@ -276,21 +276,21 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
     // the loop needs): row n of each 32-row block, 8 g columns in
     const uint32_t lane = (uint32_t)opaque_lane();
     const uint32_t lane_el = (lane & 31) * (uint32_t)TL_ROW + 8 * (lane >> 5);
-    // a quarter past the rows (or columns) of a half-inside tile holds duplicates: not stored (wave-uniform)
-    const bool keep_r = ti * CB_T + wr < Ra, keep_c = tj * CB_T + wc < Np;
+    // a quarter past the rows (or columns) of a half-inside tile holds duplicates: not stored (a wave-uniform branch around the
+    // whole store sequence, so the accumulators are still packed and stored one at a time)
+    if (ti * CB_T + wr < Ra && tj * CB_T + wc < Np) {
 #pragma unroll
-    for (int si = 0; si < 4; ++si)
+      for (int si = 0; si < 4; ++si)
 #pragma unroll
-      for (int sj = 0; sj < 4; ++sj) {
-        u32x4 lo, hi;
-        rt_pack16(acc[si][sj], lo, hi);
-        uint16_t* xp = X + tl_off_r(pb_, pc, ti * CB_T + wr + 32 * si, tj * CB_T + wc + 32 * sj, Np, Ra) + lane_el;
-        if (keep_r && keep_c) {
+        for (int sj = 0; sj < 4; ++sj) {
+          u32x4 lo, hi;
+          rt_pack16(acc[si][sj], lo, hi);
+          uint16_t* xp = X + tl_off_r(pb_, pc, ti * CB_T + wr + 32 * si, tj * CB_T + wc + 32 * sj, Np, Ra) + lane_el;
           *reinterpret_cast<u32x4*>(xp) = lo;
           *reinterpret_cast<u32x4*>(xp + 16) = hi;
+          __builtin_amdgcn_sched_barrier(0);             // one accumulator at a time (bounded VGPR use)
         }
-        __builtin_amdgcn_sched_barrier(0);               // one accumulator at a time (bounded VGPR use)
-      }
+    }
   }
 }
 

@@ -2,7 +2,9 @@
 parallel, then one link.  ``python -m fpf_hip._build`` or ``__graft_entry__.build()``."""
 import concurrent.futures as cf
 import glob
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -18,17 +20,32 @@ ARCH = os.environ.get("FPF_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 # packed fp32 VALU forms are disabled: the kernels' fp32 arithmetic must stay on the scalar-lane VALU forms
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-         "-I" + INCLUDE, "-I" + CSRC, "-Wno-unused-result"]
+         "-I" + INCLUDE, "-I" + CSRC, "-Wno-unused-result", "-Rpass-analysis=kernel-resource-usage"]
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|VGPRs Spill|SGPRs Spill|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]|LDS Size \[bytes/block\]):\s*(\S+)")
+
+
+def resource_usage(text):
+    """{kernel: {field: value}} from the compiler's kernel-resource-usage remarks (one block per kernel, starting at its name)."""
+    out, cur = {}, None
+    for m in _REMARK.finditer(text):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[key.split(" [")[0]] = int(val) if val.isdigit() else val
+    return out
 
 
 def _compile(src):
     obj = os.path.join(OBJ_DIR, os.path.basename(src).replace(".hip", ".o"))
     cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(ln for ln in r.stdout.splitlines() if "packed-fp32-ops" not in ln)   # host pass: feature unknown there, harmless
+    res = resource_usage(r.stdout)
+    out = "\n".join(ln for ln in r.stdout.splitlines() if "packed-fp32-ops" not in ln and "kernel-resource-usage" not in ln
+                    and not ln.lstrip().startswith(("|", "^")) and not re.match(r"^\s*\d+\s*\|", ln))
     if r.returncode != 0:
         raise RuntimeError("hipcc failed on %s:\n%s" % (src, out))
-    return obj, out
+    return obj, out, res
 
 
 def build(verbose=False):
@@ -38,11 +55,20 @@ def build(verbose=False):
         raise RuntimeError("no HIP sources under %s" % CSRC)
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         res = list(ex.map(_compile, srcs))
-    for obj, out in res:
+    usage = {}
+    for obj, out, ru in res:
+        usage.update(ru)
         if verbose and out.strip():
             print(out)
+    # a kernel that spills vector registers reloads them inside its loops, and each reload's wait drains the
+    # loads and DMA transfers in flight: refuse to build one
+    spilled = sorted(k for k, v in usage.items() if v.get("VGPRs Spill", 0))
+    if spilled:
+        raise RuntimeError("kernels spill vector registers to scratch: %s" % ", ".join("%s (%s)" % (k, usage[k]) for k in spilled))
+    with open(os.path.join(OBJ_DIR, "resources.json"), "w") as f:
+        json.dump(usage, f, indent=1, sort_keys=True)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + [o for o, _ in res]
+    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + [o for o, _, _ in res]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout)
