@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 10  /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+#define FPF_ABI_VERSION 11  /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
                                5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
                                6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
                                   (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes);
@@ -36,7 +36,9 @@ extern "C" {
                                9: FPF_DT_F32Z_BF16 for the trimul (fp32 z / out, bf16 operands and planes);
                                10: the bf16 block runs the v_layout 2 core for every N up to 8192 (its J axis padded to 64:
                                    fpf_triattn_bias_bytes sizes fpf_triattn_bias_fwd's output); fpf_triattn_stage_bytes and the
-                                   staged route of fpf_triattn_fwd onto that core */
+                                   staged route of fpf_triattn_fwd onto that core;
+                               11: x_ln (the caller's own LayerNorm output, ln="stock") appended to FpfTriattnBlockArgs,
+                                   FpfTriattnPrologueArgs and FpfTransitionArgs */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3, FPF_DT_F32Z_BF16 = 4 };
 enum {
@@ -94,6 +96,9 @@ typedef struct {
   const void* w_o;         /* [c, hidden] */
   const float* row_mask;   /* [rows] or NULL: the update is multiplied by it before the residual add */
   int32_t residual;        /* 1: out = x + update */
+  const void* x_ln;        /* bf16 only: [rows, c] contiguous, the caller's own LayerNorm output of x, projected in place of LN(x)
+                              (the exact-candidate construction, pair_fused.py:1089-1094 ln="stock"); the residual still adds x; NULL:
+                              LN in the kernel */
 } FpfTransitionArgs;
 int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char* err, size_t errlen);
 
@@ -245,6 +250,9 @@ typedef struct {
                               FPF_E_ARGS */
   const float* b_g;        /* [H*D] gate projection bias (g = x_ln W_g^T + b_g, before the sigmoid) or NULL; pair_fused.py:731-736 */
   const float* b_o;        /* [C] output projection bias (u = (sigmoid(g) o) W_o^T + b_o) or NULL; pair_fused.py:738 */
+  const void* x_ln;        /* bf16 whole block only: [B, N, N, C] contiguous, the caller's LayerNorm output in the attention frame
+                              (LN(z), or LN(z^T) for the ending node), projected in place of the in-kernel LayerNorm for q, k, v, the
+                              bias and the gate (pair_fused.py:1019-1029, :1151-1160 ln="stock"); the residual still updates z */
 } FpfTriattnBlockArgs;
 /* Workspace for `rows` attention rows (rows <= 0: all N). */
 size_t fpf_triattn_block_workspace_bytes(int64_t B, int64_t N, int64_t rows, int32_t C, int32_t H, int32_t D, int32_t dtype);
@@ -300,6 +308,8 @@ typedef struct {
   void* g;                 /* [B, I, J, H*D] pre-sigmoid */
   float* bias;             /* [B, H, I, J] fp32 (the [B,1,H,I,J] operand without its unit axis) */
   const float* b_g;        /* [H*D] gate projection bias added to g, or NULL */
+  const void* x_ln;        /* bf16 only: [B, N, N, C] contiguous, the caller's LayerNorm output in the attention frame, projected in
+                              place of the in-kernel LayerNorm (ln="stock"); NULL: LN in the kernel */
 } FpfTriattnPrologueArgs;
 int fpf_triattn_prologue_fwd(const FpfTriattnPrologueArgs* a, void* stream, char* err, size_t errlen);
 

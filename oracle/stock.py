@@ -80,11 +80,12 @@ def _as4(z):
     return (z, False) if z.dim() == 4 else (z.unsqueeze(0), True)
 
 
-def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_step=64, inf=1e9):
+def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_step=64, inf=1e9, x_ln=None):
     """Stock TriangleAttention{Starting,Ending}Node forward -> the update in z's frame ([B,N,N,C] or [N,N,C]).
     P: dict ln_w, ln_b [C], w_q, w_k, w_v, w_g [H*D, C], w_b [H, C], w_o [C, H*D], plus ints H, D; optional b_g [H*D] (linear_g
     bias) and b_o [C] (linear_o bias), the Linear biases of primitives.py:259-270 where a kit's module carries them.
-    The ending node transposes z (and the mask) in and the update out (attention.py:140-142, :175-176).
+    The ending node transposes z (and the mask) in and the update out (attention.py:140-142, :175-176).  ``x_ln``: the caller's
+    own LayerNorm output in the attention frame, used in place of LN(x) (pair_fused.py:1151-1160, ln="stock").
     Pinned by: scalar loops over the published equations (starting and ending node each in its own index form), ending(z) ==
     starting(z^T)^T, the op form (triangle_attention_op) on the same projections, and the BASELINE config-1 block
     (tests/test_oracle.py)."""
@@ -96,7 +97,7 @@ def tri_attn(z, P, mask=None, *, ending=False, dtype=torch.float64, rows_per_ste
     if ending:
         x = x.transpose(1, 2)
         m = m.transpose(1, 2)
-    x = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
+    x = layer_norm(x, P["ln_w"], P["ln_b"], 1e-5) if x_ln is None else _as4(x_ln)[0].to(dtype)
     wq, wk, wv, wg = (P[n].to(dtype) for n in ("w_q", "w_k", "w_v", "w_g"))
     wb, wo = P["w_b"].to(dtype), P["w_o"].to(dtype)
     bg = None if P.get("b_g") is None else P["b_g"].to(dtype)
@@ -231,12 +232,13 @@ def tri_attn_rows(z, P, mask, rows, *, ending=False, dtype=torch.float32):
     return triatt_epilogue(o, g.unsqueeze(0), P, dtype=dtype)[0]
 
 
-def transition(x, w_a, w_b, w_o, ln_w=None, ln_b=None, *, eps=1e-5, mask=None, residual=False, dtype=torch.float64):
-    """y = W_o(silu(W_a n) * (W_b n)), n = LayerNorm(x); optional row mask (y * mask) and residual (x + y).
+def transition(x, w_a, w_b, w_o, ln_w=None, ln_b=None, *, eps=1e-5, mask=None, residual=False, dtype=torch.float64, x_ln=None):
+    """y = W_o(silu(W_a n) * (W_b n)), n = LayerNorm(x) (or the caller's own ``x_ln``: pair_fused.py:1089-1094, ln="stock"); optional
+    row mask (y * mask) and residual (x + y).
     Pinned by: the reference's H100 stock bytes at c = 256 (tests/golden/transition_*), W_o = 0 -> identity residual, row
     independence (tests/test_oracle.py)."""
     xx = x.to(dtype)
-    n = layer_norm(xx, ln_w, ln_b, eps)
+    n = layer_norm(xx, ln_w, ln_b, eps) if x_ln is None else x_ln.to(dtype)
     a = torch.matmul(n, w_a.to(dtype).t())
     h = a * torch.sigmoid(a) * torch.matmul(n, w_b.to(dtype).t())
     y = torch.matmul(h, w_o.to(dtype).t())

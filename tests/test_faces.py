@@ -228,15 +228,17 @@ def test_select_keywords_are_served_or_refused_by_name():
     assert TM.call_precision(torch.zeros(2, 2, 2, 128, dtype=torch.bfloat16)) == ("bf16", torch.bfloat16)
 
 
-def test_kit_transition_select_and_ln_given_refusal():
+def test_kit_transition_select_and_ln_given():
     """boltz2/opt/boltz2_opt/transition.py:149: select(word, c=, hidden=, n_tokens=, dtype="bf16", family=, residual=, mask=, cc=,
-    stack=, rows_count=, ln_given=)."""
+    stack=, rows_count=, ln_given=); the caller's own LayerNorm output (ln_given) is served by the bf16 row and refused by name on
+    the fp32 row."""
     from fpf_hip.kernels import transition as KT
     sel = KT.select("fast", c=128, hidden=512, n_tokens=768, dtype="bf16", family="pair", residual=False, mask=False, cc=(9, 5), stack=None,
                     rows_count=768 * 768, ln_given=False)
     assert sel.row == "hip_gfx950"
+    assert KT.select("fast", c=128, hidden=512, n_tokens=768, dtype="bf16", cc=(9, 5), ln_given=True).row == "hip_gfx950"
     with pytest.raises(KT.Refusal) as e:
-        KT.select("fast", c=128, hidden=512, n_tokens=768, dtype="bf16", cc=(9, 5), ln_given=True)
+        KT.select("exact", c=128, hidden=512, n_tokens=768, dtype="fp32", cc=(9, 5), ln_given=True)
     assert e.value.kind == "ln_given"
     with pytest.raises(KT.Refusal) as e:
         KT.select("fast", c=128, hidden=512, dtype="bf16", cc=(9, 5), form="geglu")
@@ -250,8 +252,9 @@ def _pack_small():
 
 
 @pytest.mark.parametrize("kw,reason", [
-    (dict(ln="stock", x_ln=torch.zeros(1, 8, 8, 128)), "ln:stock"),
-    (dict(x_ln=torch.zeros(1, 8, 8, 128)), "ln:stock"),
+    (dict(ln="stock"), "ln:stock-needs-x_ln"),
+    (dict(x_ln=torch.zeros(1, 8, 8, 128)), "x_ln:ln_fused"),
+    (dict(ln="layer"), "ln:layer"),
     (dict(impl="torch"), "impl:torch"),
     (dict(core="flash_triattn"), "core:flash_triattn"),
     (dict(core="k2b"), "core:k2b"),
@@ -268,8 +271,11 @@ def test_block_keywords_not_served_are_refused_by_name(kw, reason):
     assert e.value.reason == reason
     T = PF.pack_transition_weights(w_out=torch.randn(128, 512), w_a=torch.randn(512, 128), w_b=torch.randn(512, 128))
     with pytest.raises(PF.Unsupported) as e:
+        PF.transition(torch.randn(1, 8, 8, 128), T, ln="stock")
+    assert e.value.reason == "ln:stock-needs-x_ln"
+    with pytest.raises(PF.Unsupported) as e:                  # x_ln must be bf16 of x's shape
         PF.transition(torch.randn(1, 8, 8, 128), T, ln="stock", x_ln=torch.randn(1, 8, 8, 128))
-    assert e.value.reason == "ln:stock"
+    assert e.value.reason == "x_ln-shape"
     with pytest.raises(PF.Unsupported) as e:
         PF.transition(torch.randn(1, 8, 8, 128), T, variant="v1")
     assert e.value.reason == "variant:v1"

@@ -171,3 +171,30 @@ def test_pair_fused_transition_face_matches_the_kernel_face():
     y3, _ = TRK.transition(x, K, word="fast", residual=True)
     torch.cuda.synchronize()
     assert torch.equal(y1, y2) and torch.equal(y1, y3)
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_transition_bf16_x_ln(residual):
+    """The caller's own LayerNorm output x_ln (pair_fused.py:1089-1094, ln="stock"; kernels.transition's x_ln) is projected in place
+    of the in-kernel LayerNorm and the residual adds x: x_ln = bf16(LN(x) * 1.05 + 0.02), against the statement with that x_ln,
+    through both faces, in place as well."""
+    from fpf_hip.attn import pair_fused as PF
+    from fpf_hip.kernels import transition as T
+    wa, wb, wo, lw, lb = _tr_weights(128, 512, 31, torch.bfloat16)
+    x = torch.randn(1, 40, 50, 128, generator=_g(32)).to(torch.bfloat16)
+    xl = (S.layer_norm(x.float(), lw, lb, 1e-5) * 1.05 + 0.02).to(torch.bfloat16).contiguous()
+    W = T.pack(w_a=wa.to(DEV), w_b=wb.to(DEV), w_o=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV))
+    TW = PF.pack_transition_weights(w_out=wo.to(DEV), ln_w=lw.to(DEV), ln_b=lb.to(DEV), w_a=wa.to(DEV), w_b=wb.to(DEV))
+    xd, xld = x.to(DEV), xl.to(DEV)
+    print("[x_ln] transition residual=%s" % residual, flush=True)
+    y, sel = T.transition(xd, W, word="fast", residual=residual, x_ln=xld)
+    y2 = PF.transition(xd, TW, residual=residual, ln="stock", x_ln=xld)
+    xi = xd.clone()
+    y3 = PF.transition(xi, TW, residual=residual, ln="stock", x_ln=xld, out=xi)
+    plain, _ = T.transition(xd, W, word="fast", residual=residual)
+    torch.cuda.synchronize()
+    assert sel.row == "hip_gfx950"
+    assert torch.equal(y, y2) and torch.equal(y, y3)
+    ref = S.transition(x.float(), wa.float(), wb.float(), wo.float(), lw, lb, residual=residual, dtype=torch.float32, x_ln=xl.float())
+    (assert_bf16_residual_close if residual else assert_bf16_close)(y, ref, "transition x_ln residual=%s" % residual)
+    assert (y.float() - plain.float()).abs().max().item() > 0.05, "x_ln was not taken"

@@ -437,3 +437,49 @@ def test_block_layout_core_fallback_extreme_logits(N, masked):
     got = out[0, rows].float()
     assert torch.isfinite(got).all(), "non-finite output"
     assert_bf16_close(got, ref, "block-layout core N=%d masked=%s, extreme query tiles" % (N, masked))
+
+
+def _xln_weights(seed):
+    P = S.make_block_params(c_z=128, heads=4, head_dim=32, seed=seed)["tas"]
+    g = torch.Generator().manual_seed(seed + 100)
+    P["ln_w"] = 1 + 0.1 * torch.randn(128, generator=g)
+    P["ln_b"] = 0.1 * torch.randn(128, generator=g)
+    for n in ("w_q", "w_k", "w_v", "w_g", "w_b", "w_o"):
+        P[n] = P[n].to(torch.bfloat16).float()
+    return P
+
+
+@pytest.mark.parametrize("ending", [False, True])
+@pytest.mark.parametrize("N,residual", [(96, False), (300, True)])
+def test_block_bf16_ln_stock_x_ln(ending, N, residual):
+    """ln="stock" with x_ln (pair_fused.py:1019-1029, :1151-1160): the caller's own LayerNorm output in the attention frame is
+    projected for q, k, v, the bias and the gate instead of the in-kernel LayerNorm of z, and the residual still updates z.  Here
+    x_ln = bf16(LN(x) * 1.05 + 0.02), so a kernel that normalised z itself would be caught; against the statement with that x_ln,
+    through the fused block and through the staged route (a callable core between the prologue and the epilogue)."""
+    from fpf_hip.attn import pair_fused as PF
+    P = _xln_weights(81)
+    W = PF.pack_triattn_weights(w_o=P["w_o"].to(DEV, torch.bfloat16), n_heads=4, head_dim=32, ln_w=P["ln_w"].to(DEV), ln_b=P["ln_b"].to(DEV),
+                                w_q=P["w_q"].to(DEV, torch.bfloat16), w_k=P["w_k"].to(DEV, torch.bfloat16),
+                                w_v=P["w_v"].to(DEV, torch.bfloat16), w_g=P["w_g"].to(DEV, torch.bfloat16), w_b=P["w_b"].to(DEV, torch.bfloat16))
+    g = torch.Generator().manual_seed(82)
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16)
+    mask = torch.ones(1, N, N)
+    mask[:, :, N - 9:] = 0
+    x = z.transpose(1, 2) if ending else z
+    xl = (S.layer_norm(x.float(), P["ln_w"], P["ln_b"], 1e-5) * 1.05 + 0.02).to(torch.bfloat16).contiguous()
+    print("[x_ln] block N=%d ending=%s residual=%s" % (N, ending, residual), flush=True)
+    zd, md, xd = z.to(DEV), mask.to(DEV), xl.to(DEV)
+    u = PF.tri_attn_block(zd.clone(), W, md, ending=ending, residual=residual, ln="stock", x_ln=xd)
+    fused = PF.tri_attn_block(zd.clone(), W, md, ending=ending, residual=residual)
+
+    def torch_core(q, k, v, bias, m5, scale):
+        o = S.triangle_attention_op(q.cpu(), k.cpu(), v.cpu(), bias.cpu(), None if m5 is None else m5.cpu(), scale, dtype=torch.float32)
+        return o.to(q.device, q.dtype)
+    staged = PF.tri_attn_block(zd.clone(), W, md, ending=ending, residual=residual, ln="stock", x_ln=xd, core=torch_core)
+    torch.cuda.synchronize()
+    ref = S.tri_attn(z.float(), P, mask, ending=ending, dtype=torch.float32, x_ln=xl.float())
+    check = assert_bf16_residual_close if residual else assert_bf16_close
+    want = z.float() + ref if residual else ref
+    check(u, want, "x_ln block N=%d ending=%s" % (N, ending))
+    check(staged, want, "x_ln staged N=%d ending=%s" % (N, ending))
+    assert max_abs(u, fused) > 0.05, "x_ln was not taken"

@@ -621,3 +621,28 @@ def test_single_track_one_token_closed_form():
     assert torch.allclose(got, want, atol=1e-12)
     wrong = s1 + S.transition(s, t["w_a"], t["w_b"], t["w_o"], t["ln_w"], t["ln_b"])
     assert not torch.allclose(got, wrong, atol=1e-6)
+
+
+def test_x_ln_replaces_exactly_the_layer_norm_output():
+    """The statements' ``x_ln`` (the caller's own LayerNorm output, ln="stock") takes the place of LN(x) and nothing else:
+    passing LN(x) itself (the attention frame for the ending node) gives the default result bit for bit, and any other x_ln
+    changes it."""
+    g = torch.Generator().manual_seed(71)
+    N, C = 10, 16
+    P = S.make_block_params(c_z=C, heads=2, head_dim=4, seed=3)["tas"]
+    P["ln_w"] = 1 + 0.1 * torch.randn(C, generator=g, dtype=torch.float64)
+    P["ln_b"] = 0.1 * torch.randn(C, generator=g, dtype=torch.float64)
+    z = torch.randn(1, N, N, C, generator=g, dtype=torch.float64)
+    mask = (torch.rand(1, N, N, generator=g) > 0.2).double()
+    for ending in (False, True):
+        x = z.transpose(1, 2) if ending else z
+        xl = S.layer_norm(x, P["ln_w"], P["ln_b"], 1e-5)
+        ref = S.tri_attn(z, P, mask, ending=ending)
+        assert torch.equal(S.tri_attn(z, P, mask, ending=ending, x_ln=xl), ref)
+        assert not torch.allclose(S.tri_attn(z, P, mask, ending=ending, x_ln=xl * 1.1), ref)
+    t = S.make_block_params(c_z=C, heads=2, head_dim=4, seed=4)["tr"]
+    ln_w, ln_b = P["ln_w"], P["ln_b"]
+    xl = S.layer_norm(z, ln_w, ln_b, 1e-5)
+    ref = S.transition(z, t["w_a"], t["w_b"], t["w_o"], ln_w, ln_b, residual=True)
+    assert torch.equal(S.transition(z, t["w_a"], t["w_b"], t["w_o"], ln_w, ln_b, residual=True, x_ln=xl), ref)
+    assert not torch.allclose(S.transition(z, t["w_a"], t["w_b"], t["w_o"], ln_w, ln_b, residual=True, x_ln=xl + 0.1), ref)

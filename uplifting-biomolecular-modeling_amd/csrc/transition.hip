@@ -24,11 +24,13 @@ constexpr int TR_HB = 32;             // hidden rows per chunk
 constexpr int TR_PW = 1, TR_NW = 4;
 constexpr int TR_NBUF = 3;            // weight-chunk ring: 2 chunks in flight (73 KB of LDS per workgroup: two fit a CU)
 
-template <int PW, int NW>
+// XLN: the GEMM input rows come from xln (the caller's own LayerNorm output of x) as they are; the residual reads x.
+template <int PW, int NW, bool XLN>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
                                                               const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ wa,
                                                               const uint16_t* __restrict__ wb, const uint16_t* __restrict__ wo,
-                                                              const float* __restrict__ mask, int residual, int64_t rows, int hidden) {
+                                                              const float* __restrict__ mask, int residual, int64_t rows, int hidden,
+                                                              const uint16_t* __restrict__ xln) {
   // weight chunk hb = W_a / W_b rows hb*32 .. +31 (all 128 inputs) and W_o columns hb*32 .. +31 (all 128 outputs), 24 KB,
   // streamed by DMA (global_load_lds_dwordx4, no VGPR staging) through a ring of TR_NBUF buffers, TR_NBUF - 1 chunks in
   // flight.  W_a / W_b rows are 16 chunks of 16 bytes stored at position c ^ (row & 15) (conflict-free fragment reads of 16
@@ -69,8 +71,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   for (int p = 0; p < PW; ++p) {
     const int64_t pix = pix0 + 32 * p + n;
     u32x4 raw[8];
-    rt_load(x + (pix < rows ? pix : 0) * TR_C, pix < rows, g, raw);
-    rt_ln(raw, g, sLN, eps, xb[p]);
+    rt_load((XLN ? xln : x) + (pix < rows ? pix : 0) * TR_C, pix < rows, g, raw);
+    if constexpr (XLN) {
+#pragma unroll
+      for (int c = 0; c < TR_KS; ++c) xb[p][c] = as_bf8(raw[c]);
+    } else {
+      rt_ln(raw, g, sLN, eps, xb[p]);
+    }
   }
   if (kt == 0) {
     // chunk 0 landed (the row loads above are younger and may still be counted), then published
@@ -391,13 +398,21 @@ extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char
     if (!aligned16(a->x) || !aligned16(a->out) || !aligned16(a->w_a) || !aligned16(a->w_b) || !aligned16(a->w_o) ||
         (a->ln_w && !aligned16(a->ln_w)) || (a->ln_b && !aligned16(a->ln_b)))
       return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
+    if (a->x_ln && !aligned16(a->x_ln)) return fail(err, errlen, FPF_E_ALIGN, "x_ln must be 16-byte aligned");
     constexpr int PW = TR_PW, NW = TR_NW;
     const dim3 grid((unsigned)std::min<int64_t>(cdiv(a->rows, 32 * NW * PW), 2 * (int64_t)num_cus())), block(64 * NW);
-    hipLaunchKernelGGL((transition_bf16_kernel<PW, NW>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b, a->eps,
-                       (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows, a->hidden);
+    if (a->x_ln)
+      hipLaunchKernelGGL((transition_bf16_kernel<PW, NW, true>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b,
+                         a->eps, (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows,
+                         a->hidden, (const uint16_t*)a->x_ln);
+    else
+      hipLaunchKernelGGL((transition_bf16_kernel<PW, NW, false>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b,
+                         a->eps, (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows,
+                         a->hidden, nullptr);
     return launched(err, errlen, "fpf_transition_fwd(bf16)");
   }
   if (a->dtype == FPF_DT_F32) {
+    if (a->x_ln) return fail(err, errlen, FPF_E_DTYPE, "x_ln serves the bf16 transition");
     if (a->c > TF_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 transition serves c <= %d (got %d)", TF_CM, a->c);
     if (a->c == TR_C && a->hidden % TX_HB == 0 && aligned16(a->x) && aligned16(a->out) && aligned16(a->w_a) && aligned16(a->w_b) &&
         aligned16(a->w_o) && (!a->ln_w || aligned16(a->ln_w)) && (!a->ln_b || aligned16(a->ln_b))) {   // the matrix-core kernel

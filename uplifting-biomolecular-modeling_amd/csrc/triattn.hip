@@ -434,11 +434,14 @@ struct ProParams {
   int64_t bias_ld;               // elements between bias rows (>= N)
   int bias_bf16;                 // bias stored as bf16 (else fp32)
   const float* b_g;              // [HD] gate projection bias added to g, or NULL
+  const uint16_t* xln;           // the caller's LayerNorm output [B, N, N, 128] bf16 in the attention frame (XLN instance), or NULL
   int64_t Np;                    // J extent of the q / k rows and of the blocked bias planes: N, or N padded to 64 for the
                                  // block-layout core (then every 32-pixel tile up to Np is computed, so V^T's padding keys hold
                                  // finite values; the padding rows of q / k and of the bias are never written)
 };
 
+// XLN: the rows come from p.xln (the caller's own LayerNorm output, attention frame) and are projected as they are.
+template <bool XLN>
 __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[(4 * TP_HD + 32) * RT_LD];
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
@@ -459,8 +462,12 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
     const RtTile tl = rt_tile(tt, per_b, tpr);
     const int64_t b = tl.b, i = p.row0 + tl.r, j = tl.c * 32 + n;
     const bool live = j < N;
-    const int64_t zpix = p.ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
-    rt_load(p.z + zpix * RT_C, live, g, raw);
+    if constexpr (XLN) {
+      rt_load(p.xln + ((b * N + i) * N + (live ? j : 0)) * RT_C, live, g, raw);
+    } else {
+      const int64_t zpix = p.ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
+      rt_load(p.z + zpix * RT_C, live, g, raw);
+    }
   };
   if (blockIdx.x * RT_WAVES + wave < total) fetch(blockIdx.x * RT_WAVES + wave);
   for (uint32_t t = blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
@@ -469,7 +476,12 @@ __global__ void __launch_bounds__(512) triattn_prologue_bf16(const ProParams p) 
     const int64_t b = tl.b, ii = tl.r, i = p.row0 + ii, j = tl.c * 32 + n;
     const bool live = j < N;
     bf16x8 xb[8];
-    rt_ln(raw, g, sLN, p.eps, xb);
+    if constexpr (XLN) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) xb[c] = as_bf8(raw[c]);
+    } else {
+      rt_ln(raw, g, sLN, p.eps, xb);
+    }
     if (t + stride < total) fetch(t + stride);
     // two output blocks per iteration: the second block's MFMA chain is issued while the first one's results are packed and
     // stored (one block at a time left the matrix core idle during each store phase: 156 -> 148 us at N = 768)
@@ -595,12 +607,14 @@ __global__ void __launch_bounds__(512) triattn_epilogue_bf16(const uint16_t* __r
 // by the same lane).  The g GEMM's output fragments are used directly as the B operand of the W_o GEMM: k-step s = 2 cb +
 // half takes, in lane half g, the channels cb*32 + 16 half + {4g .. 4g+3, 8+4g .. 8+4g+3} that the D layout leaves there,
 // and W_o's columns are permuted identically when staged.
+// XLN: the gate's input rows come from xln (the caller's LayerNorm output, attention frame) as they are; the residual reads z.
+template <bool XLN>
 __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t* zin, const uint16_t* __restrict__ o,
                                                                   const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
                                                                   const uint16_t* __restrict__ w_g, const uint16_t* __restrict__ w_o,
                                                                   const float* __restrict__ b_g, const float* __restrict__ b_o,
                                                                   uint16_t* zout, int64_t N, int64_t B, int64_t row0, int64_t rows, int ending,
-                                                                  int residual, int64_t Jo) {
+                                                                  int residual, int64_t Jo, const uint16_t* __restrict__ xln) {
   __shared__ __attribute__((aligned(16))) uint16_t sWg[RT_C * RT_LD];
   __shared__ __attribute__((aligned(16))) uint16_t sWo[RT_C * RT_LD];   // columns permuted to the k-step order above
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
@@ -629,11 +643,19 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
     live = j < N;
     return ending ? (b * N + (live ? j : 0)) * N + i : (b * N + i) * N + (live ? j : 0);
   };
-  if (blockIdx.x * RT_WAVES + wave < total) {
+  // the rows the gate reads: z (its LayerNorm is taken here), or the caller's x_ln at the attention-frame pixel
+  auto in_rows = [&](uint32_t tt) {
     bool lv;
-    const int64_t zp0 = zpix_of(blockIdx.x * RT_WAVES + wave, lv);
-    rt_load(zin + zp0 * RT_C, lv, g, raw);
-  }
+    const int64_t zp = zpix_of(tt, lv);
+    if constexpr (XLN) {
+      const RtTile tl = rt_tile(tt, per_b, tpr);
+      const int64_t j = tl.c * 32 + n;
+      rt_load(xln + ((tl.b * N + row0 + tl.r) * N + (lv ? j : 0)) * RT_C, lv, g, raw);
+    } else {
+      rt_load(zin + zp * RT_C, lv, g, raw);
+    }
+  };
+  if (blockIdx.x * RT_WAVES + wave < total) in_rows(blockIdx.x * RT_WAVES + wave);
   for (uint32_t t = blockIdx.x * RT_WAVES + wave; t < total; t += stride) {
     const RtTile tl = rt_tile(t, per_b, tpr);
     const int64_t b = tl.b, ii = tl.r, j = tl.c * 32 + n;
@@ -650,7 +672,12 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
         for (int e = 0; e < 2; ++e)
           ov2[cb][half][e] = live ? *reinterpret_cast<const u32x2*>(op + (int64_t)cb * Jo * TA_D + 16 * half + 8 * e) : u32x2{0, 0};
     bf16x8 xb[8];
-    rt_ln(raw, g, sLN, eps, xb);
+    if constexpr (XLN) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) xb[c] = as_bf8(raw[c]);
+    } else {
+      rt_ln(raw, g, sLN, eps, xb);
+    }
     f32x16 acc[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) acc[k] = f32x16{};
@@ -692,7 +719,9 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
       for (int h2 = 0; h2 < 2; ++h2) {
         u32x4 w;
         if (residual) {
-          const u32x4 r = raw[2 * blk + h2];                     // channels blk*32 + 16 h2 + 8g .. +7 of this pixel
+          // channels blk*32 + 16 h2 + 8g .. +7 of this pixel: the z rows already held, or (x_ln read) z itself, read by the lane
+          // that writes it
+          const u32x4 r = XLN ? *reinterpret_cast<const u32x4*>(zin + zpix * RT_C + blk * 32 + 16 * h2 + 8 * g) : raw[2 * blk + h2];
 #pragma unroll
           for (int e = 0; e < 4; ++e) w[e] = pack2(y[8 * h2 + 2 * e] + lo_bf(r[e]), y[8 * h2 + 2 * e + 1] + hi_bf(r[e]));
         } else {
@@ -702,11 +731,7 @@ __global__ void __launch_bounds__(512) triattn_epilogue_gate_bf16(const uint16_t
         *reinterpret_cast<u32x4*>(zp + blk * 32 + 16 * h2) = w;
       }
     }
-    if (t + stride < total) {
-      bool lvn;
-      const int64_t zpn = zpix_of(t + stride, lvn);
-      rt_load(zin + zpn * RT_C, lvn, g, raw);
-    }
+    if (t + stride < total) in_rows(t + stride);
   }
 }
 
@@ -1068,7 +1093,7 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
                            int64_t B, int64_t N, int C, int H, int D, int ending, void* q, void* k, void* v, int64_t v_ld, void* g, float* bias,
                            hipStream_t st, char* err, size_t errlen, int flags = PRO_QKV | PRO_G | PRO_BIAS, int64_t row0 = 0,
                            int64_t rows = -1, float q_scale = 1.0f, float bias_scale = 1.0f, int64_t bias_ld = -1, int bias_bf16 = 0,
-                           const float* b_g = nullptr, bool dry = false, int64_t Np = -1) {
+                           const float* b_g = nullptr, bool dry = false, int64_t Np = -1, const void* xln = nullptr) {
   if (rows < 0) rows = N;
   if (bias_ld < 0) bias_ld = N;
   if (Np < 0) Np = N;
@@ -1109,13 +1134,17 @@ static int prologue_launch(int dtype, const void* z, const float* ln_w, const fl
     p.bias_bf16 = bias_bf16;
     p.b_g = b_g;
     if (!rt_tiles_ok(B * rows * cdiv(Np, 32))) return fail(err, errlen, FPF_E_SHAPE, "prologue: 2^31 or more 32-pixel tiles");
+    if (xln && !aligned16(xln)) return fail(err, errlen, FPF_E_ALIGN, "x_ln must be 16-byte aligned");
+    p.xln = static_cast<const uint16_t*>(xln);
     if (dry) return FPF_OK;
     const unsigned grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(B * rows * cdiv(Np, 32), RT_WAVES));
-    hipLaunchKernelGGL(triattn_prologue_bf16, dim3(grid), dim3(512), 0, st, p);
+    if (xln) hipLaunchKernelGGL(triattn_prologue_bf16<true>, dim3(grid), dim3(512), 0, st, p);
+    else hipLaunchKernelGGL(triattn_prologue_bf16<false>, dim3(grid), dim3(512), 0, st, p);
     return launched(err, errlen, "triattn_prologue_bf16");
   }
   if (row0 != 0 || rows != N || flags != (PRO_QKV | PRO_G | PRO_BIAS) || q_scale != 1.0f || bias_scale != 1.0f || bias_ld != N || bias_bf16)
     return fail(err, errlen, FPF_E_SHAPE, "the fp32 prologue serves whole tensors (no row range, every output, q unscaled)");
+  if (xln) return fail(err, errlen, FPF_E_DTYPE, "x_ln serves the bf16 prologue");
   if (dry) return FPF_OK;
   const unsigned grid = (unsigned)(N * cdiv(N, PF_R));
   hipLaunchKernelGGL(triattn_prologue_f32, dim3(grid, (unsigned)B), dim3(256), 0, st, (const float*)z, ln_w, ln_b, eps, (const float*)w_qkvg,
@@ -1155,7 +1184,7 @@ extern "C" int fpf_triattn_prologue_fwd(const FpfTriattnPrologueArgs* a, void* s
   if (rc) return rc;
   return prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, a->B, a->N, a->C, a->H, a->D, a->ending, a->q, a->k, a->v,
                          a->v_ld, a->g, a->bias, static_cast<hipStream_t>(stream), err, errlen, PRO_QKV | PRO_G | PRO_BIAS, 0, -1, 1.0f, 1.0f, -1, 0,
-                         a->b_g);
+                         a->b_g, false, -1, a->x_ln);
 }
 
 extern "C" int fpf_triattn_epilogue_fwd(const FpfTriattnEpilogueArgs* a, void* stream, char* err, size_t errlen) {
@@ -1240,6 +1269,9 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   if (ranged && a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_SHAPE, "the fp32 block serves whole tensors (no row range)");
   if (ranged && !a->bias_in) return fail(err, errlen, FPF_E_ARGS, "a row range needs bias_in (the full bias from fpf_triattn_bias_fwd)");
   if (a->bias_in && a->dtype != FPF_DT_BF16) return fail(err, errlen, FPF_E_DTYPE, "bias_in serves the bf16 block");
+  if (a->x_ln && (a->dtype != FPF_DT_BF16 || ranged || a->bias_in))
+    return fail(err, errlen, FPF_E_ARGS, "x_ln serves the whole bf16 block (no row range, no bias_in: the bias comes from x_ln)");
+  if (a->x_ln && !aligned16(a->x_ln)) return fail(err, errlen, FPF_E_ALIGN, "x_ln must be 16-byte aligned");
   const size_t need = fpf_triattn_block_workspace_bytes(B, N, R, a->C, a->H, a->D, a->dtype);
   if (!a->workspace || a->workspace_bytes < need) return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
   {
@@ -1310,7 +1342,7 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
     }
     int rc = prologue_launch(a->dtype, a->z, a->ln_w, a->ln_b, a->eps, a->w_qkvg, a->w_b, B, N, a->C, (int)H, (int)D, a->ending, q, k, v, Jp,
                              g, bias, st, err, errlen, flags, row0, R, dma_core ? scale * LOG2E : 1.0f, dma_core ? LOG2E : 1.0f, -1, 0, a->b_g, dry,
-                             Np);
+                             Np, a->x_ln);
     if (rc) return rc;
     rc = core_launch(&c, st, err, errlen, dry, N);
     if (rc) return rc;
@@ -1324,9 +1356,14 @@ extern "C" int fpf_triattn_block_fwd(const FpfTriattnBlockArgs* a, void* stream,
   }
   {
     const unsigned grid = (unsigned)std::min<int64_t>(2 * num_cus(), cdiv(B * R * cdiv(N, 32), RT_WAVES));
-    hipLaunchKernelGGL(triattn_epilogue_gate_bf16, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w, a->ln_b,
-                       a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, a->b_g, a->b_o, (uint16_t*)a->out, N, B, row0,
-                       R, a->ending, a->residual, Np);
+    if (a->x_ln)
+      hipLaunchKernelGGL(triattn_epilogue_gate_bf16<true>, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w,
+                         a->ln_b, a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, a->b_g, a->b_o, (uint16_t*)a->out, N,
+                         B, row0, R, a->ending, a->residual, Np, (const uint16_t*)a->x_ln);
+    else
+      hipLaunchKernelGGL(triattn_epilogue_gate_bf16<false>, dim3(grid), dim3(512), 0, st, (const uint16_t*)a->z, (const uint16_t*)o, a->ln_w,
+                         a->ln_b, a->eps, (const uint16_t*)a->w_qkvg + 3 * HD * a->C, (const uint16_t*)a->w_o, a->b_g, a->b_o, (uint16_t*)a->out, N,
+                         B, row0, R, a->ending, a->residual, Np, nullptr);
     return launched(err, errlen, "triattn_epilogue_gate_bf16");
   }
 }

@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 DT_BF16, DT_F32, DT_U8, DT_F32Z_BF16 = 1, 2, 3, 4
 TRIMUL_NOALLOC_SCRATCH_BYTES = 50331648          # include/fpf_hip.h FPF_TRIMUL_NOALLOC_SCRATCH_BYTES
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
@@ -26,7 +26,8 @@ class LnArgs(C.Structure):
 
 class TransitionArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("c", i32), ("hidden", i32), ("rows", i64), ("x", vp), ("out", vp),
-                ("ln_w", vp), ("ln_b", vp), ("eps", f32), ("w_a", vp), ("w_b", vp), ("w_o", vp), ("row_mask", vp), ("residual", i32)]
+                ("ln_w", vp), ("ln_b", vp), ("eps", f32), ("w_a", vp), ("w_b", vp), ("w_o", vp), ("row_mask", vp), ("residual", i32),
+                ("x_ln", vp)]
 
 
 class TrimulArgs(C.Structure):
@@ -48,7 +49,7 @@ class TriattnBlockArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp),
                 ("mask", vp), ("mask_dtype", i32), ("ln_w", vp), ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("w_o", vp),
                 ("ending", i32), ("residual", i32), ("out", vp), ("scale", f32), ("workspace", vp), ("workspace_bytes", sz),
-                ("row0", i64), ("rows", i64), ("bias_in", vp), ("mask_frame", i32), ("b_g", vp), ("b_o", vp)]
+                ("row0", i64), ("rows", i64), ("bias_in", vp), ("mask_frame", i32), ("b_g", vp), ("b_o", vp), ("x_ln", vp)]
 
 
 class TriattnBiasArgs(C.Structure):
@@ -59,7 +60,7 @@ class TriattnBiasArgs(C.Structure):
 class TriattnPrologueArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("B", i64), ("N", i64), ("C", i32), ("H", i32), ("D", i32), ("z", vp), ("ln_w", vp),
                 ("ln_b", vp), ("eps", f32), ("w_qkvg", vp), ("w_b", vp), ("ending", i32), ("q", vp), ("k", vp), ("v", vp), ("v_ld", i64),
-                ("g", vp), ("bias", vp), ("b_g", vp)]
+                ("g", vp), ("bias", vp), ("b_g", vp), ("x_ln", vp)]
 
 
 class TriattnEpilogueArgs(C.Structure):

@@ -15,7 +15,9 @@ x = z^T: the prologue reads z^T by address (no copy) and the epilogue writes the
 Served: ``ln="fused"`` (LayerNorm in-kernel); ``impl`` "fpf" (the fused kernels; also "hip"); ``core`` "default",
 "tier:<word>", a row name of kernels.triattn, or a callable core(q, k, v, bias, mask, scale) (run between this package's
 prologue and epilogue stages); ``bias_frame`` "x" or "z" (the same numbers; "z" only changes the strides of the bias the
-prologue returns for the ending node).  Refused by name: ``ln="stock"`` / ``x_ln`` (the caller's own LayerNorm output),
+prologue returns for the ending node); ``ln="stock"`` with ``x_ln`` (the caller's own LayerNorm output, the exact-candidate
+construction) on the bf16 rows, projected in place of the in-kernel LayerNorm.  Refused by name: ``x_ln`` with ``ln="fused"`` or
+on the fp32 rows,
 ``impl`` "torch" / "lnl", cores "flash_triattn" / "k2b" (Triton members of the reference), ``write_x``, transition variants
 other than the in-place folded one, ``silu`` other than swiglu / liger.
 """
@@ -161,11 +163,28 @@ def _block_check(z, W, word, face):
     return z4, sel
 
 
-def _check_ln(ln, x_ln):
-    if ln == "stock" or x_ln is not None:
-        raise Unsupported("ln:stock", "the caller's own LayerNorm output (x_ln) is not taken: the kernels normalise z in-kernel")
-    if ln != "fused":
+def _check_ln(ln, x_ln, like=None):
+    """``ln="fused"``: the kernels normalise in-kernel (no x_ln).  ``ln="stock"``: x_ln, the caller's own LayerNorm output (the
+    attention frame for the triangle attention), is projected in place of the in-kernel LayerNorm -- the exact-candidate
+    construction of pair_fused.py:1151-1160; it must be a contiguous bf16 tensor of ``like``'s shape on its device.  Returns
+    the x_ln to pass (4-D when ``like`` is), or None."""
+    if ln == "fused":
+        if x_ln is not None:
+            raise Unsupported("x_ln:ln_fused", "x_ln is projected with ln='stock'; ln='fused' normalises in-kernel")
+        return None
+    if ln != "stock":
         raise Unsupported("ln:%s" % ln)
+    if x_ln is None:
+        raise Unsupported("ln:stock-needs-x_ln", "ln='stock' projects the caller's own LayerNorm output x_ln")
+    if like is None:
+        return x_ln
+    x4 = x_ln.unsqueeze(0) if x_ln.dim() + 1 == like.dim() else x_ln
+    if tuple(x4.shape) != tuple(like.shape) or x4.dtype != torch.bfloat16 or not x4.is_contiguous() or x4.device != like.device:
+        raise Unsupported("x_ln-shape", "a contiguous bf16 tensor of shape %s on %s, got %s %s on %s"
+                          % (tuple(like.shape), like.device, tuple(x_ln.shape), x_ln.dtype, x_ln.device))
+    if like.dtype != torch.bfloat16:
+        raise Unsupported("x_ln:%s" % F.dtype_word(like.dtype), "x_ln is served on the bf16 rows (the fp32 rows normalise in-kernel)")
+    return x4
 
 
 def _check_impl(impl):
@@ -224,6 +243,7 @@ def prologue(z, W, *, ending=False, ln="fused", x_ln=None, impl="fpf", bias_fram
     _check_impl(impl)
     _check_bias_frame(bias_frame)
     z4, sel = _block_check(z, W, word, "prologue")
+    x4 = _check_ln(ln, x_ln, z4)
     B, N = int(z4.shape[0]), int(z4.shape[1])
     H, D = W.H, W.D
     wqkvg, wb, _wo, bg, _bo = _wpack(W, z.dtype, z.device)
@@ -238,7 +258,7 @@ def prologue(z, W, *, ending=False, ln="fused", x_ln=None, impl="fpf", bias_fram
     a = L.TriattnPrologueArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if bf else L.DT_F32, B=B, N=N, C=W.C, H=H, D=D, z=L.ptr(z4),
                               ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb),
                               ending=1 if ending else 0, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vs), v_ld=jp if bf else 0, g=L.ptr(g),
-                              bias=L.ptr(bias), b_g=L.ptr(bg))
+                              bias=L.ptr(bias), b_g=L.ptr(bg), x_ln=L.ptr(x4))
     _launch("fpf_triattn_prologue_fwd", a, z.device)
     v = vs[..., :N].transpose(-1, -2) if bf else vs
     if bias_frame == "z" and ending:
@@ -304,14 +324,14 @@ def epilogue(o, g, W, z=None, *, ending=False, residual=False, impl="fpf", o_lay
     return dst.transpose(1, 2) if ending else dst
 
 
-def _block_args(z4, W, m, mdt, mframe, ending, residual, out, scale, ws, dt, wpack, row0=0, rows=0, bias_in=None):
+def _block_args(z4, W, m, mdt, mframe, ending, residual, out, scale, ws, dt, wpack, row0=0, rows=0, bias_in=None, x_ln=None):
     wqkvg, wb, wo, bg, bo = wpack
     B, N = int(z4.shape[0]), int(z4.shape[1])
     return L.TriattnBlockArgs(abi_version=L.ABI_VERSION, dtype=dt, B=B, N=N, C=W.C, H=W.H, D=W.D, z=L.ptr(z4), mask=L.ptr(m), mask_dtype=mdt,
                               ln_w=L.ptr(W.ln_w), ln_b=L.ptr(W.ln_b), eps=W.eps, w_qkvg=L.ptr(wqkvg), w_b=L.ptr(wb), w_o=L.ptr(wo),
                               ending=1 if ending else 0, residual=1 if residual else 0, out=L.ptr(out), scale=float(scale or 0.0),
                               workspace=L.ptr(ws), workspace_bytes=ws.numel(), row0=row0, rows=rows, bias_in=L.ptr(bias_in),
-                              mask_frame=mframe, b_g=L.ptr(bg), b_o=L.ptr(bo))
+                              mask_frame=mframe, b_g=L.ptr(bg), b_o=L.ptr(bo), x_ln=L.ptr(x_ln))
 
 
 def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, impl="fpf", core=DEFAULT_CORE, ln="fused", x_ln=None, scale=None,
@@ -326,8 +346,9 @@ def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, impl="fpf",
         raise Unsupported("variant:%s" % (variant,), "the block has one variant")
     cw = _core_word(core)
     z4, sel = _block_check(z, W, word, "tri_attn_block")
+    x4 = _check_ln(ln, x_ln, z4)
     if cw is None:                                    # the caller's core between this package's stages
-        q, k, v, g, bias = prologue(z, W, ending=ending, word=word)
+        q, k, v, g, bias = prologue(z, W, ending=ending, ln=ln, x_ln=x4, word=word)
         o = core_attention(q, k, v, bias, _key_mask(mask, z, ending), core=core, scale=scale)
         if residual:
             return epilogue(o.contiguous(), g, W, z, ending=ending, residual=True, word=word)
@@ -346,7 +367,7 @@ def tri_attn_block(z, W, mask=None, *, ending=False, residual=False, impl="fpf",
     dt = L.DT_BF16 if z.dtype == torch.bfloat16 else L.DT_F32
     ws = F.scratch(z.device, L.lib().fpf_triattn_block_workspace_bytes(B, N, 0, W.C, W.H, W.D, dt))
     out = z4 if residual else torch.empty_like(z4)
-    _launch("fpf_triattn_block_fwd", _block_args(z4, W, m, mdt, mframe, ending, residual, out, scale, ws, dt, wp), z.device)
+    _launch("fpf_triattn_block_fwd", _block_args(z4, W, m, mdt, mframe, ending, residual, out, scale, ws, dt, wp, x_ln=x4), z.device)
     if residual:
         return z
     return out if z.dim() == 4 else out[0]
@@ -419,7 +440,7 @@ def transition(x, T, *, residual=False, ln="fused", x_ln=None, impl="fpf", varia
     h = silu(a) * b is formed from fp32 a, b and rounded to bf16 once, the 'liger' form; ``silu='swiglu'`` (which rounds
     silu(a) first) is served by the same kernel: the two differ by one bf16 rounding of the hidden, inside the fast tier's
     tolerance."""
-    _check_ln(ln, x_ln)
+    x_ln = _check_ln(ln, x_ln, x)
     _check_impl(impl)
     if variant is not None and variant not in TRANSITION_VARIANTS:
         raise Unsupported("variant:%s" % (variant,), "served: %s" % (TRANSITION_VARIANTS,))
@@ -428,7 +449,7 @@ def transition(x, T, *, residual=False, ln="fused", x_ln=None, impl="fpf", varia
     if silu not in ("swiglu", "liger"):
         raise Unsupported("silu:%s" % silu)
     try:
-        y, _sel = _TR.transition(x, T.W, word=word, residual=residual, mask=mask, binary_mask=binary_mask, out=out)
+        y, _sel = _TR.transition(x, T.W, word=word, residual=residual, mask=mask, binary_mask=binary_mask, out=out, x_ln=x_ln)
     except F.Refusal as e:
         raise Unsupported(e.kind, e.detail) from None
     return y

@@ -5,7 +5,8 @@ Mirrors common/opt_core/opt_core/kernels/transition/__init__.py: ``pack(*, w_o, 
 ln_b=None, eps=1e-5, device=None) -> Weights`` (:1011), ``Weights`` (:928; operand packs built once per weight set and dtype)
 ``select(word, *, c, hidden, n_tokens=None, dtype="bf16", ...)`` (:509) and ``transition(x, W, *, word, residual=False, x_ln=None,
 mask=None, binary_mask=None, out=None, n_tokens=None, family="pair", ...) -> (y, Selection)`` (:1074).  ``out`` may be ``x`` itself
-(in place).  ``x_ln`` (the caller's own LayerNorm output) is refused by name: the kernels always normalise.
+(in place).  ``x_ln`` (the caller's own LayerNorm output of x, the exact-candidate construction) is projected in place of the
+in-kernel LayerNorm on the bf16 row; the fp32 row refuses it by name.
 """
 import torch
 
@@ -66,16 +67,14 @@ def select(word, *, c, hidden, n_tokens=None, dtype="bf16", direction="fwd", tim
            cc=None, device=None, stack=None, capture=False, rows_count=None, ln_given=False, form="swiglu"):
     """Pure: the row serving a transition of this class, or Refusal by name (common/opt_core/opt_core/kernels/transition/__init__.py:509).
     ``cc`` / ``device`` name the card (the current device when both are None); ``n_tokens`` (the pair tensor's N) names the
-    measured cell.  ``ln_given`` (the caller's own LayerNorm output, the exact-candidate construction) and any ``form`` other than
-    swiglu are refused by name; ``timing`` / ``capture`` / ``stack`` / ``rows_count`` / ``residual`` / ``mask`` do not change the
+    measured cell.  ``ln_given`` (the caller's own LayerNorm output, the exact-candidate construction) is served by the bf16 row
+    and refused by name on the fp32 row; any ``form`` other than swiglu is refused by name; ``timing`` / ``capture`` / ``stack`` / ``rows_count`` / ``residual`` / ``mask`` do not change the
     answer (the kernel folds the residual and the row mask and is capture-safe)."""
     w = F.word_base(word)
     if str(direction) not in ("fwd", "forward"):
         raise Refusal("no_backward", w, F.ROW_STOCK, "forward only")
     if form != "swiglu":
         raise Refusal("form:%s" % form, w, F.ROW_STOCK, "the kernel computes the SwiGLU transition")
-    if ln_given:
-        raise Refusal("ln_given", w, F.ROW_STOCK, "the HIP rows normalise in-kernel; the caller's x_ln is not taken")
     dw = F.dtype_of(dtype)
     c, hidden = int(c), int(hidden)
     cell = "%s|%s|%s_c%d_n%d|eager|fwd" % (CELLS.CC, dw, family, c, hidden // max(c, 1))
@@ -86,6 +85,8 @@ def select(word, *, c, hidden, n_tokens=None, dtype="bf16", direction="fwd", tim
         raise Refusal("shape:c%dh%d" % (c, hidden), sel.row, F.ROW_F32, "the bf16 kernel serves c = 128, hidden % 32 == 0")
     if sel.row == F.ROW_F32 and c > 384:
         raise Refusal("shape:c%d" % c, sel.row, F.ROW_STOCK, "the fp32 kernel serves c <= 384")
+    if ln_given and sel.row != F.ROW_FAST:
+        raise Refusal("ln_given", sel.row, F.ROW_STOCK, "the fp32 row normalises in-kernel; the caller's x_ln is taken by the bf16 row")
     return sel
 
 
@@ -116,10 +117,12 @@ def transition(x, W, *, word, residual=False, x_ln=None, mask=None, binary_mask=
         if m.numel() != rows:
             raise Refusal("mask_rows", sel.row, F.ROW_STOCK, "one mask value per row")
         m = m.to(device=x.device, dtype=torch.float32).contiguous()
+    if x_ln is not None and (x_ln.shape != x.shape or x_ln.dtype != torch.bfloat16 or not x_ln.is_contiguous() or x_ln.device != x.device):
+        raise Refusal("x_ln", sel.row, F.ROW_STOCK, "x_ln must be a contiguous bf16 tensor of x's shape on x's device")
     wa, wb, wo, lw, lb = W.pack_for(x.dtype, x.device)
     a = L.TransitionArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if x.dtype == torch.bfloat16 else L.DT_F32, c=c, hidden=W.hidden,
                          rows=rows, x=L.ptr(x), out=L.ptr(out), ln_w=L.ptr(lw), ln_b=L.ptr(lb), eps=W.eps, w_a=L.ptr(wa), w_b=L.ptr(wb),
-                         w_o=L.ptr(wo), row_mask=L.ptr(m), residual=1 if residual else 0)
+                         w_o=L.ptr(wo), row_mask=L.ptr(m), residual=1 if residual else 0, x_ln=L.ptr(x_ln))
     L.call("fpf_transition_fwd", a, L.stream_ptr(x.device))
     return out, sel
 
