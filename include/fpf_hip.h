@@ -113,7 +113,7 @@ int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char* err, size
 typedef struct {
   int32_t abi_version;
   int32_t dtype;           /* FPF_DT_BF16 (z, out, w_* bf16) | FPF_DT_F32 | FPF_DT_F32Z_BF16 (z, out fp32; w_* bf16; the LayerNorm
-                              and the gate read z rounded to bf16, the residual adds the fp32 z; whole op only, no rows mode) */
+                              and the gate read z rounded to bf16, the residual adds the fp32 z; the whole op and the channels mode, no rows mode) */
   int32_t c_z;             /* bf16: 128 */
   int32_t c_h;             /* bf16: 128 */
   int64_t batch;
@@ -155,6 +155,15 @@ size_t fpf_trimul_fixed_bytes(int64_t batch, int64_t n, int32_t c_h, int32_t dty
 int fpf_trimul_fixed_fwd(const FpfTrimulArgs* a, void* fixed_out, void* stream, char* err, size_t errlen);
 /* Workspace of a rows-mode call of `rows` rows: the product plane of the row block's cover by contraction tiles. */
 size_t fpf_trimul_rows_workspace_bytes(int64_t batch, int64_t n, int64_t rows, int32_t c_h, int32_t dtype);
+/* The channels mode (FPF_DT_BF16 or FPF_DT_F32Z_BF16, c_h = 128; common/opt_core/opt_core/mem/chunk.py:542-552,
+   triangle_multiplication_chunked mode "channels"): the operand planes are built per block of `chunk` hidden channels (32, 64
+   or 128: the largest not above chunk, 32 below that) and each block's products are written into the one full product
+   plane, then the output stage runs over all rows.  The full plane is held because the output LayerNorm normalises over all
+   hidden channels of a pixel.  The result equals fpf_trimul_fwd's bitwise; out may be z (residual).  The row fields of `a`
+   must be 0 / NULL; the workspace (fpf_trimul_channels_workspace_bytes: the product plane + two planes of the block's
+   channels) is a->workspace. */
+size_t fpf_trimul_channels_workspace_bytes(int64_t batch, int64_t n, int64_t chunk, int32_t c_h, int32_t dtype);
+int fpf_trimul_channels_fwd(const FpfTrimulArgs* a, int64_t chunk, void* stream, char* err, size_t errlen);
 
 /* The same triangle multiplication without a caller workspace.  No counterpart in the reference: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The workspace

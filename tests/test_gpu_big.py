@@ -193,8 +193,8 @@ def _asym_mask(B, N, keep_rows, seed):
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 @pytest.mark.parametrize("B,N,chunk", [(1, 403, 256), (1, 403, 100), (1, 300, 64), (2, 130, 50)])
 def test_trimul_chunked_bitwise_equals_whole(direction, B, N, chunk):
-    """Rows mode (chunk.py:526): N = 403 pads to 512 planes (the 256-tile contraction; 100-row blocks straddle its tiles),
-    N = 300 to 384 (the 128-tile contraction; the last block holds 44 rows), batch 2.  Out of place, in place (out = z: the
+    """Rows mode (chunk.py:526): N = 403 pads to 512 planes (100-row blocks straddle the 256-row contraction tiles), N = 300 to
+    384 (an odd multiple of 128: the last tile row is half inside; the last block holds 44 rows), batch 2.  Out of place, in place (out = z: the
     incoming operand reads columns every later block would see updated) and the bare update, each equal to the whole op."""
     from fpf_hip import pairformer as PFM
     from fpf_hip.kernels import trimul as TM
@@ -214,13 +214,62 @@ def test_trimul_chunked_bitwise_equals_whole(direction, B, N, chunk):
     assert torch.equal(z2, TM.triangle_multiplication(z, mask, direction=direction, weights=w, word="fast", residual=True))
 
 
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("B,N,chunk", [(1, 403, 32), (1, 300, 96), (2, 130, 64), (1, 200, 20), (1, 256, 128)])
+def test_trimul_channels_bitwise_equals_whole(direction, B, N, chunk):
+    """Channels mode (chunk.py:542-552): the operand planes per block of chunk hidden channels (96: blocks of 64; 20: of 32), each block's products into the one full product plane, then the output stage over all rows.  Out of place,
+    in place and the bare update, each equal to the whole op bitwise."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import trimul as TM
+    blk = PFM.PairBlock(PFM.random_params(seed=4), DEV, torch.bfloat16)
+    w = blk.tmo if direction == "outgoing" else blk.tmi
+    z = torch.randn(B, N, N, 128, generator=torch.Generator().manual_seed(N + 7 * chunk)).to(torch.bfloat16).to(DEV)
+    mask = _asym_mask(B, N, N - 5, N + 1).to(DEV)
+    print("[big] trimul channels %s B=%d N=%d chunk=%d" % (direction, B, N, chunk), flush=True)
+    for residual in (True, False):
+        whole = TM.triangle_multiplication(z, mask, direction=direction, weights=w, word="fast", residual=residual)
+        got = TM.triangle_multiplication_chunked(z, mask, direction=direction, weights=w, chunk=chunk, mode="channels", hidden=128,
+                                                 row_block=64, residual=residual)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(whole, got), "residual=%s: max diff %.3e" % (residual, (whole.float() - got.float()).abs().max().item())
+    z2 = z.clone()
+    TM.triangle_multiplication_chunked(z2, mask, direction=direction, weights=w, chunk=chunk, mode="channels", hidden=128, residual=True,
+                                       out=z2)
+    torch.cuda.synchronize()
+    assert torch.equal(z2, TM.triangle_multiplication(z, mask, direction=direction, weights=w, word="fast", residual=True))
+
+
+def test_trimul_channels_f32z_bitwise_equals_whole():
+    """The channels mode on an fp32 z under bf16 autocast (the f32z_bf16 class: bf16 operands, fp32 z and out) equals the whole
+    op of that class bitwise."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import trimul as TM
+    blk = PFM.PairBlock(PFM.random_params(seed=6), DEV, torch.bfloat16)
+    z = torch.randn(1, 200, 200, 128, generator=torch.Generator().manual_seed(11)).to(DEV)
+    mask = _asym_mask(1, 200, 190, 12).to(DEV)
+    print("[big] trimul channels f32z N=200", flush=True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        whole = TM.triangle_multiplication(z, mask, direction="incoming", weights=blk.tmi, word="fast", residual=True)
+        got = TM.triangle_multiplication_chunked(z, mask, direction="incoming", weights=blk.tmi, chunk=64, mode="channels", hidden=128,
+                                                 residual=True)
+    torch.cuda.synchronize()
+    assert whole.dtype == torch.float32 and got.dtype == torch.float32
+    assert torch.equal(whole, got)
+
+
 def test_trimul_chunked_refusals():
     from fpf_hip import pairformer as PFM
     from fpf_hip.kernels import trimul as TM
     blk = PFM.PairBlock(PFM.random_params(seed=3), DEV, torch.bfloat16)
     z = torch.randn(1, 64, 64, 128).to(torch.bfloat16).to(DEV)
-    with pytest.raises(TM.Refusal):
-        TM.triangle_multiplication_chunked(z, None, direction="outgoing", weights=blk.tmo, chunk=32, mode="channels")
+    for kw, kind in ((dict(mode="cols"), "mode:cols"), (dict(mode="channels"), "bad_hidden"), (dict(mode="channels", hidden=True), "bad_hidden"),
+                     (dict(mode="channels", hidden=64), "operand_output_shape")):
+        with pytest.raises(TM.Refusal) as ei:
+            TM.triangle_multiplication_chunked(z, None, direction="outgoing", weights=blk.tmo, chunk=32, **kw)
+        assert ei.value.kind == kind
+    with pytest.raises(ValueError):
+        TM.triangle_multiplication_chunked(z, None, direction="outgoing", weights=blk.tmo, chunk=32, row_block=0)
     with pytest.raises(TM.Refusal):
         TM.triangle_multiplication_chunked(z, None, direction="outgoing", weights=blk.tmo, chunk=32, residual=False, out=z)
     with pytest.raises(ValueError):

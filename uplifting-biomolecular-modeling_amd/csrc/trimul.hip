@@ -24,11 +24,15 @@ constexpr int TM_TILE = 128;         // contraction tile and plane padding
 // 32-pixel tile as whole blocks and K3 reads one as 1 KB-contiguous loads; the contraction reads 64-byte runs of k along
 // rows 8 KB apart (TL_ROW) and steps one column block (TL_KBLK(Np)) per 32-wide k slab.
 // A plane of Rp rows (the rows mode's slices: Rp < Np rows, all Np columns) has the same layout with Rp rows per column
-// block: ((b (Np / 32) + Q / 32) Rp + P) 4096 + 32 c + Q % 32.
+// block: ((b (Np / 32) + Q / 32) Rp + P) 4096 + 32 c + Q % 32.  The channels mode's operand planes hold a block of cpl
+// channels (cpl a multiple of 32) in the same order: ((b (Np / 32) + Q / 32) Rp + P) 32 cpl + 32 c + Q % 32.
 constexpr int64_t TL_ROW = 4096;
 __device__ __forceinline__ int64_t tl_kblk(int64_t Rp) { return Rp * 4096; }
+__host__ __device__ __forceinline__ int64_t tl_off_rc(int64_t b, int64_t c, int64_t P, int64_t Q, int64_t Np, int64_t Rp, int64_t cpl) {
+  return ((b * (Np >> 5) + (Q >> 5)) * Rp + P) * (32 * cpl) + c * 32 + (Q & 31);
+}
 __host__ __device__ __forceinline__ int64_t tl_off_r(int64_t b, int64_t c, int64_t P, int64_t Q, int64_t Np, int64_t Rp) {
-  return ((b * (Np >> 5) + (Q >> 5)) * Rp + P) * 4096 + c * 32 + (Q & 31);
+  return tl_off_rc(b, c, P, Q, Np, Rp, TM_C);
 }
 __device__ __forceinline__ int64_t tl_off(int64_t b, int64_t c, int64_t P, int64_t Q, int64_t Np) { return tl_off_r(b, c, P, Q, Np, Np); }
 
@@ -36,13 +40,14 @@ __device__ __forceinline__ int64_t tl_off(int64_t b, int64_t c, int64_t P, int64
 // Persistent: the four [128 x 128] projection weights live in LDS (139 KB) for the workgroup's lifetime; each wave walks
 // 32-column plane tiles (plane row P, columns Q0 .. Q0+31), prefetching the next tile's 32 z rows while it computes.
 // ZF32: z is fp32 (the fp32-resident form); each tile's rows are read and rounded to bf16 at the start of its iteration.
-template <bool ZF32>
+// NCB: the 32-channel blocks computed (4: the whole op; fewer: one block of the channels mode, from channel 32 cb0).
+template <bool ZF32, int NCB>
 __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z, const float* __restrict__ mask,
                                                       const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
                                                       const uint16_t* __restrict__ w_ap, const uint16_t* __restrict__ w_ag,
                                                       const uint16_t* __restrict__ w_bp, const uint16_t* __restrict__ w_bg,
                                                       uint16_t* __restrict__ pa, uint16_t* __restrict__ pb, int64_t N, int64_t Np, int64_t B,
-                                                      int outgoing) {
+                                                      int outgoing, int cb0) {
   __shared__ __attribute__((aligned(16))) uint16_t sW[4 * RT_C * RT_LD];
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
   __shared__ __attribute__((aligned(16))) float sM[RT_WAVES][32];
@@ -90,14 +95,15 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z
       for (int e = 0; e < 4; ++e) mv[4 * q + e] = m4[e];
     }
     rt_wave_lds_sync();
-    const int64_t Q0 = Q - n;
-    uint16_t* oa = pa + tl_off(b, 0, P, Q0, Np) + 8 * g;
-    uint16_t* ob = pb + tl_off(b, 0, P, Q0, Np) + 8 * g;
+    // channel blocks cb0 .. cb0 + NCB - 1 (32 channels each) into planes of 32 NCB channels (the whole op: 0 .. 3 into 128)
+    const int64_t Q0 = Q - n, cpl = 32 * NCB;
+    uint16_t* oa = pa + tl_off_rc(b, 0, P, Q0, Np, Np, cpl) + 8 * g;
+    uint16_t* ob = pb + tl_off_rc(b, 0, P, Q0, Np, Np, cpl) + 8 * g;
 #pragma unroll 1
-    for (int cb = 0; cb < 4; ++cb) {
+    for (int cb = 0; cb < NCB; ++cb) {
       const uint16_t* const ws[4] = {sW, sW + 1 * RT_C * RT_LD, sW + 2 * RT_C * RT_LD, sW + 3 * RT_C * RT_LD};
       f32x16 acc[4];
-      rt_gemm32_multi_xw<4>(ws, cb * 32, n, g, xb, acc);
+      rt_gemm32_multi_xw<4>(ws, (cb0 + cb) * 32, n, g, xb, acc);
       f32x16 va, vb;
       if (ones) {
 #pragma unroll
@@ -154,9 +160,13 @@ __device__ __forceinline__ void cb_wait(int p, bool stores) {
   }
 }
 
+// CPL: the channels the operand planes hold (128: the whole op; 32 / 64: one block of the channels mode, whose channel c is
+// channel cx0 + c of X).
+template <int CPL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t nbatch,
-                         int64_t La, int64_t a0, int64_t Ra) {
+                         int64_t La, int64_t a0, int64_t Ra, int cx0) {
+  constexpr int64_t cpl = CPL;
   __shared__ __attribute__((aligned(16))) uint16_t sA[CB_NBUF][CB_T * CB_K];
   __shared__ __attribute__((aligned(16))) uint16_t sB[CB_NBUF][CB_T * CB_K];
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, n = l & 31, g = l >> 5;
@@ -166,7 +176,10 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   if (first >= end) return;
   const int ntile = (int)((end - first + g8 - 1) / g8);       // tiles first, first + g8, ... below end
   const int nk = (int)(Np / CB_K), U = ntile * nk;             // slabs per tile, slabs of this workgroup (host: U < 2^31)
-  const int64_t kstride_a = tl_kblk(La), kstride_b = tl_kblk(Np);
+  // the operand planes hold cpl channels (128: the whole op; the channels mode's block otherwise), batch index bc = b cpl + c;
+  // X holds all 128, this call's channel c at cx0 + c
+  constexpr int64_t orow = 32 * cpl;
+  const int64_t kstride_a = La * orow, kstride_b = Np * orow;
   auto tile_of = [&](int r, int64_t& bc, int64_t& ti, int64_t& tj) {
     const int64_t w = first + (int64_t)r * g8, t = w % tiles;
     bc = w / tiles;
@@ -179,7 +192,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int sl = 256 * q + tid, r = sl >> 2, c = (sl & 3) ^ ((r >> 2) & 3);
-    goff[q] = (uint32_t)(r * TL_ROW + 8 * c);
+    goff[q] = (uint32_t)(r * orow + 8 * c);
   }
   // issue cursor: the next slab to load is slab ikt of tile ir (operand bases ia0 / ib0 of slots 0 .. 511, rows 0 .. 127 of the
   // tile; ia1 / ib1 of slots 512 .. 1023, rows 128 .. 255, or rows 0 .. 127 again where the tile is half inside)
@@ -188,10 +201,10 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   auto set_bases = [&](int r) {
     int64_t bc, ti, tj;
     tile_of(r, bc, ti, tj);
-    ia0 = A + tl_off_r(bc / TM_C, bc % TM_C, a0 + ti * CB_T, 0, Np, La);
-    ib0 = Bm + tl_off(bc / TM_C, bc % TM_C, tj * CB_T, 0, Np);
-    ia1 = ti * CB_T + CB_T > Ra ? ia0 - 128 * TL_ROW : ia0;
-    ib1 = tj * CB_T + CB_T > Np ? ib0 - 128 * TL_ROW : ib0;
+    ia0 = A + tl_off_rc(bc / cpl, bc % cpl, a0 + ti * CB_T, 0, Np, La, cpl);
+    ib0 = Bm + tl_off_rc(bc / cpl, bc % cpl, tj * CB_T, 0, Np, Np, cpl);
+    ia1 = ti * CB_T + CB_T > Ra ? ia0 - 128 * orow : ia0;
+    ib1 = tj * CB_T + CB_T > Np ? ib0 - 128 * orow : ib0;
   };
   set_bases(0);
   auto issue_next = [&](int buf) {
@@ -271,7 +284,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
     }
     int64_t bc, ti, tj;
     tile_of(r, bc, ti, tj);
-    const int64_t pb_ = bc / TM_C, pc = bc % TM_C;
+    const int64_t pb_ = bc / cpl, pc = cx0 + bc % cpl;
     // the lane's part of the store offsets, recomputed per tile (kept live across the slab loop it would take registers
     // the loop needs): row n of each 32-row block, 8 g columns in
     const uint32_t lane = (uint32_t)opaque_lane();
@@ -800,11 +813,27 @@ __global__ void __launch_bounds__(64 * FM_NW) trimul_k3_f32m(const float* zin, f
 }
 
 static int64_t padded(int64_t n) { return cdiv(n, TM_TILE) * TM_TILE; }
+
+// The contraction of operand planes holding cpl channels (A rows a0 .. a0 + Ra - 1 of a plane of La rows, B whole) into X
+// (Ra rows, all 128 channels; these planes' channel c at cx0 + c): persistent, a multiple of 8 workgroups.
+static int contract_launch(hipStream_t st, const uint16_t* pa, const uint16_t* pb, uint16_t* X, int64_t Np, int64_t B, int cpl, int64_t La,
+                           int64_t a0, int64_t Ra, int cx0, char* err, size_t errlen) {
+  if (cpl != 32 && cpl != 64 && cpl != TM_C) return fail(err, errlen, FPF_E_ARGS, "operand planes of %d channels (32, 64 or 128)", cpl);
+  const int64_t tiles = cdiv(Ra, CB_T) * cdiv(Np, CB_T) * B * cpl;
+  const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;
+  if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
+  auto kern = cpl == 32 ? trimul_contract_bf16_256<32> : cpl == 64 ? trimul_contract_bf16_256<64> : trimul_contract_bf16_256<TM_C>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * cpl, La, a0, Ra, cx0);
+  return launched(err, errlen, "trimul_contract_bf16_256");
+}
 // The contraction tile: 256 at every n (a padded extent of an odd multiple of 128 ends with half-inside tiles).
 static int64_t ctile(int64_t n) { (void)n; return CB_T; }
 
 // Contraction -> K3 of the bf16 path for output rows [row0, row0 + rows), from whole A and B planes: A rows a0 .. a0 + Ra - 1
 // (the tile-aligned cover of the row block) into an X plane of Ra rows.  The whole op is row0 = 0, rows = N, Ra = Np.
+static int k3_launch(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* X, int64_t row0, int64_t rows, int64_t a0, int64_t Ra, char* err,
+                     size_t errlen);
+
 static int bf16_rows(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* pa, const uint16_t* pb, uint16_t* X, int64_t row0, int64_t rows,
                      char* err, size_t errlen) {
   const int64_t N = a->n, Np = padded(N), B = a->batch, T = ctile(N);
@@ -812,12 +841,16 @@ static int bf16_rows(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* pa,
   const int64_t a0 = row0 / T * T, Ra = std::min<int64_t>(cdiv(row0 + rows, T) * T, Np) - a0;
   const int64_t k3_tiles = B * rows * cdiv(N, 32);
   if (!rt_tiles_ok(k3_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
-  const int64_t tiles = cdiv(Ra, CB_T) * cdiv(Np, CB_T) * B * TM_C;
-  const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;    // persistent, a multiple of 8
-  if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
-  hipLaunchKernelGGL(trimul_contract_bf16_256, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * TM_C, Np, a0, Ra);
-  int rc = launched(err, errlen, "trimul_contract_bf16_256");
+  int rc = contract_launch(st, pa, pb, X, Np, B, TM_C, Np, a0, Ra, 0, err, errlen);
   if (rc) return rc;
+  return k3_launch(a, st, X, row0, rows, a0, Ra, err, errlen);
+}
+
+// K3 (LN_out(X) + W_o x sigmoid(gate) + residual) on output rows row0 .. row0 + rows - 1, from X's rows a0 .. a0 + Ra - 1
+static int k3_launch(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* X, int64_t row0, int64_t rows, int64_t a0, int64_t Ra, char* err,
+                     size_t errlen) {
+  const int64_t N = a->n, Np = padded(N), B = a->batch;
+  const int64_t k3_tiles = B * rows * cdiv(N, 32);
   const unsigned k3_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k3_tiles, RT_WAVES));
   hipLaunchKernelGGL(a->dtype == FPF_DT_F32Z_BF16 ? trimul_k3_bf16<true> : trimul_k3_bf16<false>, dim3(k3_grid), dim3(512), 0, st, a->z, a->out, X,
                      a->ln_in_w, a->ln_in_b, a->ln_out_w, a->ln_out_b, a->eps, (const uint16_t*)a->w_o, (const uint16_t*)a->w_og, N, Np, B,
@@ -825,16 +858,19 @@ static int bf16_rows(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* pa,
   return launched(err, errlen, "trimul_k3_bf16");
 }
 
-// K1: both planes, whole (LN_in + four gated projections + mask), into pa / pb.
-static int bf16_planes(const FpfTrimulArgs* a, hipStream_t st, uint16_t* pa, uint16_t* pb, char* err, size_t errlen) {
+// K1: both planes (LN_in + four gated projections + mask), into pa / pb: channel blocks cb0 .. cb0 + ncb - 1 (32 channels
+// each) as planes of 32 ncb channels; the whole op: all four into planes of 128.
+static int bf16_planes(const FpfTrimulArgs* a, hipStream_t st, uint16_t* pa, uint16_t* pb, char* err, size_t errlen, int cb0 = 0, int ncb = 4) {
   const int64_t N = a->n, Np = padded(N), B = a->batch;
   const int64_t k1_tiles = B * Np * (Np / 32);
   if (!rt_tiles_ok(k1_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
+  if (ncb != 1 && ncb != 2 && ncb != 4) return fail(err, errlen, FPF_E_ARGS, "K1 writes 1, 2 or 4 channel blocks (got %d)", ncb);
   const unsigned k1_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k1_tiles, RT_WAVES));
-  hipLaunchKernelGGL(a->dtype == FPF_DT_F32Z_BF16 ? trimul_k1_bf16<true> : trimul_k1_bf16<false>, dim3(k1_grid), dim3(512), 0, st, a->z,
-                     a->mask, a->ln_in_w, a->ln_in_b, a->eps,
-                     (const uint16_t*)a->w_ap, (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B,
-                     a->outgoing);
+  const bool f = a->dtype == FPF_DT_F32Z_BF16;
+  auto kern = ncb == 4 ? (f ? trimul_k1_bf16<true, 4> : trimul_k1_bf16<false, 4>)
+                       : ncb == 2 ? (f ? trimul_k1_bf16<true, 2> : trimul_k1_bf16<false, 2>) : (f ? trimul_k1_bf16<true, 1> : trimul_k1_bf16<false, 1>);
+  hipLaunchKernelGGL(kern, dim3(k1_grid), dim3(512), 0, st, a->z, a->mask, a->ln_in_w, a->ln_in_b, a->eps, (const uint16_t*)a->w_ap,
+                     (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B, a->outgoing, cb0);
   return launched(err, errlen, "trimul_k1_bf16");
 }
 
@@ -959,6 +995,54 @@ extern "C" int fpf_trimul_fwd(const FpfTrimulArgs* a, void* stream, char* err, s
     return launched(err, errlen, "trimul_k3_f32");
   }
   return fail(err, errlen, FPF_E_DTYPE, "dtype %d", a->dtype);
+}
+
+// ---------------------------------------------------------------------------------------------------------------- channels mode
+// The product plane X is built channel block by channel block (common/opt_core/opt_core/mem/chunk.py:542-552, mode
+// "channels"): per block of `chunk` hidden channels, K1 writes the A / B planes of those channels only (LN_in recomputed,
+// the block's projection columns), and the contraction writes those channels of the one full X; K3 then runs over all rows.
+// Each channel of X is computed by the same instructions on the same values as in the whole op (K1's 32-channel blocks
+// and the contraction's per-channel products are independent of one another), so the result equals fpf_trimul_fwd bitwise.
+// Held: X (all channels) + two planes of `chunk` channels, against the whole op's three 128-channel planes.
+namespace fpf {
+static int64_t channel_block(int64_t chunk) { return chunk >= TM_C ? TM_C : chunk >= 64 ? 64 : 32; }
+}  // namespace fpf
+
+extern "C" size_t fpf_trimul_channels_workspace_bytes(int64_t batch, int64_t n, int64_t chunk, int32_t c_h, int32_t dtype) {
+  if ((dtype != FPF_DT_BF16 && dtype != FPF_DT_F32Z_BF16) || c_h != fpf::TM_C || chunk <= 0 || n <= 0 || batch <= 0) return 0;
+  const int64_t Np = fpf::padded(n), cpl = fpf::channel_block(chunk);
+  return (size_t)batch * (size_t)(fpf::TM_C + 2 * cpl) * (size_t)Np * (size_t)Np * 2;
+}
+
+extern "C" int fpf_trimul_channels_fwd(const FpfTrimulArgs* a, int64_t chunk, void* stream, char* err, size_t errlen) {
+  using namespace fpf;
+  FPF_CHECK_VERSION(a);
+  if (!a->z || !a->out || !a->ln_in_w || !a->ln_in_b || !a->ln_out_w || !a->ln_out_b || !a->w_ag || !a->w_ap || !a->w_bg || !a->w_bp ||
+      !a->w_o || !a->w_og)
+    return fail(err, errlen, FPF_E_ARGS, "a required pointer is NULL (z, out, the ten weights)");
+  if (a->rows || a->row0 || a->fixed_in) return fail(err, errlen, FPF_E_ARGS, "the channels mode runs every row (rows mode: fpf_trimul_fwd)");
+  if (a->dtype != FPF_DT_BF16 && a->dtype != FPF_DT_F32Z_BF16) return fail(err, errlen, FPF_E_DTYPE, "the channels mode serves the bf16 trimul");
+  if (chunk <= 0) return fail(err, errlen, FPF_E_ARGS, "chunk %lld: a positive channel count", (long long)chunk);
+  if (a->batch <= 0 || a->n <= 0) return a->batch == 0 || a->n == 0 ? FPF_OK : fail(err, errlen, FPF_E_SHAPE, "batch / n negative");
+  if (a->batch > 65535) return fail(err, errlen, FPF_E_SHAPE, "batch above 65535");
+  int rc = bf16_checks(a, err, errlen);
+  if (rc) return rc;
+  const size_t need = fpf_trimul_channels_workspace_bytes(a->batch, a->n, chunk, a->c_h, a->dtype);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(err, errlen, FPF_E_WORKSPACE, "workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
+  if (!aligned16(a->workspace)) return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t N = a->n, Np = padded(N), B = a->batch, cpl = channel_block(chunk);
+  uint16_t* X = static_cast<uint16_t*>(a->workspace);
+  uint16_t* pa = X + B * TM_C * Np * Np;
+  uint16_t* pb = pa + B * cpl * Np * Np;
+  for (int64_t c0 = 0; c0 < TM_C; c0 += cpl) {
+    rc = bf16_planes(a, st, pa, pb, err, errlen, (int)(c0 / 32), (int)(cpl / 32));
+    if (rc) return rc;
+    rc = contract_launch(st, pa, pb, X, Np, B, (int)cpl, Np, 0, Np, (int)c0, err, errlen);
+    if (rc) return rc;
+  }
+  return k3_launch(a, st, X, 0, N, 0, Np, err, errlen);
 }
 
 // ---------------------------------------------------------------------------------------------------------------- no-allocation entry

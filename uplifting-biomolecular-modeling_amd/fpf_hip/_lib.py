@@ -91,6 +91,8 @@ ENTRY_POINTS = {                     # name -> (argtypes, restype); every symbol
     "fpf_trimul_fixed_fwd": ([C.POINTER(TrimulArgs), vp, vp, C.c_char_p, sz], C.c_int),
     "fpf_trimul_fixed_bytes": ([i64, i64, i32, i32], sz),
     "fpf_trimul_rows_workspace_bytes": ([i64, i64, i64, i32, i32], sz),
+    "fpf_trimul_channels_fwd": ([C.POINTER(TrimulArgs), i64, vp, C.c_char_p, sz], C.c_int),
+    "fpf_trimul_channels_workspace_bytes": ([i64, i64, i64, i32, i32], sz),
     "fpf_triattn_fwd": ([C.POINTER(TriattnArgs), vp, C.c_char_p, sz], C.c_int),
     "fpf_triattn_block_workspace_bytes": ([i64, i64, i64, i32, i32, i32, i32], sz),
     "fpf_triattn_bias_bytes": ([i64, i64, i32, i32], sz),

@@ -190,8 +190,8 @@ def _args(z4, out, m, p, d, residual, eps, dt, Cz, Ch, ws):
                         workspace=L.ptr(ws), workspace_bytes=0 if ws is None else ws.numel())
 
 
-def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, mode="rows", word="big", residual=False, out=None, cache=None,
-                                    eps=1e-5, fp32="passthrough", selection=None, prefer=None, residency=None):
+def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, mode="rows", hidden=None, row_block=None, word="big", residual=False,
+                                    out=None, cache=None, eps=1e-5, fp32="passthrough", selection=None, prefer=None, residency=None):
     """Row-chunked triangle multiplication (common/opt_core/opt_core/mem/chunk.py:526 ``triangle_multiplication_chunked``, mode
     ``rows``): both operand planes are built whole once from z (``fpf_trimul_fixed_fwd``), then each block of ``chunk`` output
     rows runs the contraction over the whole shared axis and the output stage for those rows only (``fpf_trimul_fwd`` in its
@@ -200,12 +200,29 @@ def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, 
     before any row is written, ``out`` may be z (``residual=True``) in both directions -- the reference's incoming free operand
     reads z columns per block, which an in-place update of earlier blocks would change.
 
-    ``mode="channels"`` (the reference's channel-block operands with a full product) is refused by name: the whole-op kernels
-    already never hold a channel-split plane.  An fp32 call (row hip_gfx950_f32) runs the whole op when ``fp32`` is
-    ``"passthrough"`` or ``"band"`` (the result is the whole op's, which meets either label) and is refused for ``"refuse"``;
-    an fp32 z under bf16 autocast (the f32z_bf16 class) runs the whole op."""
-    if str(mode) != "rows":
-        raise Refusal("mode:%s" % mode, F.word_base(word), F.ROW_STOCK, "the chunked trimul serves mode rows")
+    ``mode="channels"`` (mem/chunk.py:542-552; ``hidden`` = the hidden channel count, ``chunk`` = channels per block):
+    ``fpf_trimul_channels_fwd`` builds both operand planes per block of ``chunk`` hidden channels (32, 64 or 128: the largest
+    not above ``chunk``, 32 below that) and writes each block's products into ONE full product plane, then the output stage runs over all rows --
+    the output LayerNorm normalises over every hidden channel of a pixel, so a channel chunk bounds the operands, not the
+    product.  Held: the product plane + two planes of ``chunk`` channels.  Each channel is the whole op's arithmetic: the result
+    equals ``triangle_multiplication`` bitwise.  ``row_block`` (the reference's row block of its operand and finish passes) is
+    validated and changes nothing here: the kernels stream rows and hold no per-row transients.  The channels mode also serves
+    the f32z_bf16 class (fp32 z under bf16 autocast) through the same entry.
+
+    An fp32 call (row hip_gfx950_f32) runs the whole op when ``fp32`` is ``"passthrough"`` or ``"band"`` (the result is the whole
+    op's, which meets either label) and is refused for ``"refuse"``; an fp32 z under bf16 autocast (the f32z_bf16 class) runs the
+    whole op in rows mode."""
+    mode = str(mode)
+    if mode not in ("rows", "channels"):
+        raise Refusal("mode:%s" % mode, F.word_base(word), F.ROW_STOCK, "the chunked trimul serves mode rows | channels")
+    if mode == "channels":
+        if not isinstance(hidden, int) or isinstance(hidden, bool) or hidden < 1:
+            raise Refusal("bad_hidden", F.word_base(word), F.ROW_STOCK, "hidden=%r is not a positive int (the hidden channel count)" % (hidden,))
+        if int(weights["w_ap"].shape[0]) != hidden:
+            raise Refusal("operand_output_shape", F.word_base(word), F.ROW_STOCK,
+                          "the operand projections give %d hidden channels, hidden=%d" % (int(weights["w_ap"].shape[0]), hidden))
+    if row_block is not None and (not isinstance(row_block, int) or isinstance(row_block, bool) or row_block < 1):
+        raise ValueError("row_block must be a positive int (got %r)" % (row_block,))
     if str(fp32) not in ("passthrough", "band", "refuse"):
         raise ValueError("fp32 must be passthrough | band | refuse (got %r)" % (fp32,))
     chunk = int(chunk)
@@ -222,7 +239,8 @@ def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, 
     f32z = prec == "f32z_bf16"
     sel = selection or select(z, "bf16" if f32z else z.dtype, Cz, Ch, N, d, word=word, residency="fp32" if f32z else residency, prefer=prefer,
                               batch=B, tf32=prec == "tf32")
-    if sel.row != F.ROW_FAST or z.dtype != torch.bfloat16:      # fp32 and the f32z_bf16 class: the whole op
+    channels_f32z = mode == "channels" and sel.row == F.ROW_FAST and z.dtype == torch.float32
+    if (sel.row != F.ROW_FAST or z.dtype != torch.bfloat16) and not channels_f32z:   # fp32, and the f32z_bf16 class in rows mode: the whole op
         if sel.row == F.ROW_FAST:
             return triangle_multiplication(z, mask, direction=d, weights=weights, selection=sel, residual=residual, cache=cache, eps=eps, out=out)
         if str(fp32) == "refuse":
@@ -256,6 +274,12 @@ def triangle_multiplication_chunked(z, mask=None, *, direction, weights, chunk, 
     if B * N == 0:
         return out
     lib, st = L.lib(), L.stream_ptr(z.device)
+    if mode == "channels":
+        ws = F.scratch(z.device, lib.fpf_trimul_channels_workspace_bytes(B, N, chunk, Ch, dt))
+        a = _args(z4, out, m, p, d, residual, eps, dt, Cz, Ch, ws)
+        L.call("fpf_trimul_channels_fwd", a, chunk, st)
+        cache["_last"] = sel
+        return out
     rows = min(chunk, N)
     planes = F.scratch(z.device, lib.fpf_trimul_fixed_bytes(B, N, Ch, L.DT_BF16), kind="trimul_planes")
     ws = F.scratch(z.device, lib.fpf_trimul_rows_workspace_bytes(B, N, rows, Ch, L.DT_BF16))
