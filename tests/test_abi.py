@@ -134,3 +134,6 @@ def test_build_reads_kernel_resource_usage_and_refuses_vgpr_spills():
            "a.hip:9:1: remark:     VGPRs Spill: 12 [-Rpass-analysis=kernel-resource-usage]\n")
     ru = _build.resource_usage(txt)
     assert ru == {"_Zk1": {"VGPRs": 200, "VGPRs Spill": 0, "Occupancy": 2}, "_Zk2": {"VGPRs Spill": 12}}
+    # a register array in scratch memory (no counted spill) is refused too; a few SGPR-spill slots are not
+    usage = dict(ru, _Zk3={"VGPRs Spill": 0, "ScratchSize": 1088}, _Zk4={"VGPRs Spill": 0, "SGPRs Spill": 53, "ScratchSize": 36})
+    assert _build.refused(usage) == ["_Zk2", "_Zk3"]

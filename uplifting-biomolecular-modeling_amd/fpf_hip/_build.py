@@ -21,6 +21,14 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 # packed fp32 VALU forms are disabled: the kernels' fp32 arithmetic must stay on the scalar-lane VALU forms
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I" + INCLUDE, "-I" + CSRC, "-Wno-unused-result", "-Rpass-analysis=kernel-resource-usage"]
+def refused(usage):
+    """Kernels the build refuses: a VGPR spill, or more scratch than a few SGPR-spill slots (a register array the compiler
+    placed in scratch memory, e.g. one captured by a lambda it did not inline).  Either reloads registers from memory inside
+    the kernel's loops, and each reload's wait drains the loads and DMA transfers in flight."""
+    return sorted(k for k, v in usage.items() if v.get("VGPRs Spill", 0) or v.get("ScratchSize", 0) > SCRATCH_LIMIT)
+
+
+SCRATCH_LIMIT = 64          # bytes per lane: the SGPR-spill slots some kernels keep; a spilled register array is far larger
 _REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|VGPRs Spill|SGPRs Spill|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]|LDS Size \[bytes/block\]):\s*(\S+)")
 
 
@@ -60,9 +68,7 @@ def build(verbose=False):
         usage.update(ru)
         if verbose and out.strip():
             print(out)
-    # a kernel that spills vector registers reloads them inside its loops, and each reload's wait drains the
-    # loads and DMA transfers in flight: refuse to build one
-    spilled = sorted(k for k, v in usage.items() if v.get("VGPRs Spill", 0))
+    spilled = refused(usage)
     if spilled:
         raise RuntimeError("kernels spill vector registers to scratch: %s" % ", ".join("%s (%s)" % (k, usage[k]) for k in spilled))
     with open(os.path.join(OBJ_DIR, "resources.json"), "w") as f:
