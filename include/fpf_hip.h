@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 11  /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+#define FPF_ABI_VERSION 12  /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
                                5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
                                6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
                                   (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes);
@@ -38,7 +38,9 @@ extern "C" {
                                    fpf_triattn_bias_bytes sizes fpf_triattn_bias_fwd's output); fpf_triattn_stage_bytes and the
                                    staged route of fpf_triattn_fwd onto that core;
                                11: x_ln (the caller's own LayerNorm output, ln="stock") appended to FpfTriattnBlockArgs,
-                                   FpfTriattnPrologueArgs and FpfTransitionArgs */
+                                   FpfTriattnPrologueArgs and FpfTransitionArgs;
+                               12: the single track's pair bias projected from the transition's written rows (FpfTransitionArgs
+                                   w_z .. z_bias_ld) */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3, FPF_DT_F32Z_BF16 = 4 };
 enum {
@@ -99,6 +101,21 @@ typedef struct {
   const void* x_ln;        /* bf16 only: [rows, c] contiguous, the caller's own LayerNorm output of x, projected in place of LN(x)
                               (the exact-candidate construction, pair_fused.py:1089-1094 ln="stock"); the residual still adds x; NULL:
                               LN in the kernel */
+  /* The single track's pair bias from the rows this call writes (bf16, c = 128; rows = B * pair_n * pair_n, a pair tensor
+     [B, N, N, 128]): z_bias[b, h, i, j] = LN(out[b, i, j, :]) . w_z[h, :] (fp32 LayerNorm statistics, the normalised row
+     rounded to bf16, fp32 accumulation) -- fpf_apb_bias_fwd's values on the written z, bitwise, without another pass over
+     it.  The pass the reference runs separately on the resident z after the pair stack (the sequence pair bias of
+     boltz2/opt/forward/pairfuse/bz_pairfuse.py:18-20, proj_z of boltz2/stock/src/boltz/model/layers/attentionv2.py:53-58)
+     folded into the stack's last site.  w_z NULL: no bias. */
+  const void* w_z;         /* [z_heads, 128] bf16 */
+  const float* z_ln_w;     /* [128] or NULL (1) */
+  const float* z_ln_b;     /* [128] or NULL (0) */
+  float z_eps;
+  int32_t z_heads;         /* 1 .. 32 */
+  int64_t pair_n;          /* N */
+  void* z_bias;            /* [B, z_heads, N, z_bias_ld] */
+  int32_t z_bias_dtype;    /* FPF_DT_F32 | FPF_DT_BF16 */
+  int64_t z_bias_ld;       /* >= N; <= 0 means N */
 } FpfTransitionArgs;
 int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char* err, size_t errlen);
 

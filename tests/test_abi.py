@@ -109,6 +109,26 @@ def test_version_mismatch_is_refused_before_any_launch():
     assert e.value.kind == "args"
 
 
+def test_transition_pair_bias_gate_needs_no_device():
+    """The transition's pair-bias fields are checked before any launch: w_z without a bias buffer (and the reverse), heads outside
+    1 .. 32, rows that are not B N N pixels, an fp32 call (placeholder addresses: nothing is dereferenced)."""
+    from fpf_hip import _lib as L
+    p = 0x10000
+
+    def args(**kw):
+        base = dict(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, c=128, hidden=512, rows=2 * 8 * 8, x=p, out=p, w_a=p, w_b=p, w_o=p,
+                    w_z=p, z_heads=4, pair_n=8, z_bias=p, z_bias_dtype=L.DT_F32)
+        base.update(kw)
+        return L.TransitionArgs(**base)
+    for kw, kind, text in ((dict(z_bias=None), "args", "without z_bias"), (dict(w_z=None), "args", "without w_z"),
+                           (dict(z_heads=33), "shape", "z_heads"), (dict(pair_n=7), "shape", "rows = B N N"),
+                           (dict(z_bias_dtype=L.DT_U8), "dtype", "z_bias_dtype"), (dict(z_bias_ld=5), "shape", "z_bias_ld"),
+                           (dict(dtype=L.DT_F32), "dtype", "bf16 transition")):
+        with pytest.raises(L.LibError) as e:
+            L.call("fpf_transition_fwd", args(**kw), None)
+        assert e.value.kind == kind and text in e.value.msg, (kw, e.value.kind, e.value.msg)
+
+
 def test_apb_refusals_need_no_device():
     """The attention-with-pair-bias gate refuses NULL operands and unserved head dims by name (nothing is launched)."""
     from fpf_hip import _lib as L

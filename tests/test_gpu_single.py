@@ -107,6 +107,55 @@ def test_pair_bias_producer(out_dtype, pad):
         assert torch.isnan(store[..., N:].float()).all()                            # the row padding is never written
 
 
+@pytest.mark.parametrize("B,N,H,out_dtype,pad,masked", [(1, 96, 16, torch.float32, 0, False), (2, 130, 16, torch.bfloat16, 8, True),
+                                                       (1, 768, 16, torch.float32, 0, True), (1, 37, 5, torch.float32, 3, False)])
+def test_transition_pair_bias_equals_the_producer_on_the_written_z(B, N, H, out_dtype, pad, masked):
+    """The pair bias projected by the transition kernel from the rows it writes (the single track's proj_z folded into the pair
+    stack's last site) equals the producer's pass over the written z bitwise, and the written z equals the transition's without
+    the bias: in place with the residual, a row mask, fp32 and bf16 bias with a padded row pitch, H below a 32-row block."""
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.attn import apb_core as APB
+    from fpf_hip.kernels import transition as TR
+    g = torch.Generator().manual_seed(N + H)
+    blk = PFM.PairBlock(PFM.random_params(seed=N), DEV, torch.bfloat16)
+    z = torch.randn(B, N, N, 128, generator=g).to(torch.bfloat16).to(DEV)
+    m = (torch.rand(B, N, N, generator=g) > 0.3).float().to(DEV) if masked else None
+    wz = (torch.randn(H, 128, generator=g) / math.sqrt(128)).to(torch.bfloat16).to(DEV)
+    lw, lb = (1 + 0.1 * torch.randn(128, generator=g)).to(DEV), (0.1 * torch.randn(128, generator=g)).to(DEV)
+    print("[pair-bias] transition B=%d N=%d H=%d %s pad %d mask %s" % (B, N, H, out_dtype, pad, masked), flush=True)
+    store = torch.full((B, H, N, N + pad), float("nan"), dtype=out_dtype, device=DEV)
+    z1 = z.clone()
+    TR.transition(z1, blk.tr, word="fast", residual=True, out=z1, mask=m,
+                  pair_bias=dict(w_z=wz, ln_w=lw, ln_b=lb, eps=1e-5, out=store[..., :N]))
+    z2 = z.clone()
+    TR.transition(z2, blk.tr, word="fast", residual=True, out=z2, mask=m)
+    ref = APB.pair_bias_producer(z2, wz, lw, lb, dtype=out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(z1, z2), "the bias changed the written z"
+    assert torch.equal(store[..., :N], ref), "max diff %.3e" % (store[..., :N].float() - ref.float()).abs().max().item()
+    if pad:
+        assert torch.isnan(store[..., N:].float()).all()                            # the row padding is never written
+
+
+def test_transition_pair_bias_refusals():
+    from fpf_hip import pairformer as PFM
+    from fpf_hip.kernels import transition as TR
+    blk = PFM.PairBlock(PFM.random_params(seed=1), DEV, torch.bfloat16)
+    z = torch.randn(1, 16, 16, 128, device=DEV).to(torch.bfloat16)
+    wz = torch.randn(4, 128, device=DEV).to(torch.bfloat16)
+    good = torch.empty(1, 4, 16, 16, device=DEV)
+    cases = [(dict(w_z=wz), "pair_bias:args"), (dict(w_z=torch.randn(40, 128, device=DEV), out=good), "pair_bias:w_z"),
+             (dict(w_z=wz, out=torch.empty(1, 4, 16, 15, device=DEV)), "pair_bias:out"),
+             (dict(w_z=wz, out=good.transpose(2, 3)), "pair_bias:out")]
+    for pb, kind in cases:
+        with pytest.raises(TR.Refusal) as e:
+            TR.transition(z, blk.tr, word="fast", pair_bias=pb)
+        assert e.value.kind == kind
+    with pytest.raises(TR.Refusal) as e:
+        TR.transition(z[0, :, :8].contiguous(), blk.tr, word="fast", pair_bias=dict(w_z=wz, out=good))
+    assert e.value.kind == "pair_bias:not_pair"
+
+
 def _layer(seed, N, c_s=384, heads=16):
     from fpf_hip import pairformer as PFM
     sp = PFM.random_single_params(c_s=c_s, heads=heads, seed=seed)

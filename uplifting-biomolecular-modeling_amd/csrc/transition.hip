@@ -24,13 +24,27 @@ constexpr int TR_HB = 32;             // hidden rows per chunk
 constexpr int TR_PW = 1, TR_NW = 4;
 constexpr int TR_NBUF = 3;            // weight-chunk ring: 2 chunks in flight (73 KB of LDS per workgroup: two fit a CU)
 
+// The single track's pair bias projected from the written rows (BIAS instances): bias[b, h, i, j] = LN(out row) . w[h, :]
+// for out rows of a pair tensor [B, n, n, 128], by the same instructions as the bias output of the tri-att prologue
+// (rt_ln on the stored bf16 values, then D = W x^T on the matrix core), so the values equal fpf_apb_bias_fwd's bitwise.
+struct TrBias {
+  const uint16_t* w;         // [H, 128] bf16
+  const float* ln_w;         // [128] or NULL
+  const float* ln_b;
+  float eps;
+  int H;
+  int bf16;                  // the bias stored as bf16 (else fp32)
+  void* out;                 // [B, H, n, ld]
+  int64_t n, ld;
+};
+
 // XLN: the GEMM input rows come from xln (the caller's own LayerNorm output of x) as they are; the residual reads x.
-template <int PW, int NW, bool XLN>
+template <int PW, int NW, bool XLN, bool BIAS>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) transition_bf16_kernel(const uint16_t* x, uint16_t* out, const float* __restrict__ ln_w,
                                                               const float* __restrict__ ln_b, float eps, const uint16_t* __restrict__ wa,
                                                               const uint16_t* __restrict__ wb, const uint16_t* __restrict__ wo,
                                                               const float* __restrict__ mask, int residual, int64_t rows, int hidden,
-                                                              const uint16_t* __restrict__ xln) {
+                                                              const uint16_t* __restrict__ xln, const TrBias zb) {
   // weight chunk hb = W_a / W_b rows hb*32 .. +31 (all 128 inputs) and W_o columns hb*32 .. +31 (all 128 outputs), 24 KB,
   // streamed by DMA (global_load_lds_dwordx4, no VGPR staging) through a ring of TR_NBUF buffers, TR_NBUF - 1 chunks in
   // flight.  W_a / W_b rows are 16 chunks of 16 bytes stored at position c ^ (row & 15) (conflict-free fragment reads of 16
@@ -59,7 +73,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     }
   };
   __shared__ __attribute__((aligned(16))) float sLN[2 * RT_C];
+  __shared__ __attribute__((aligned(16))) float sLNz[BIAS ? 2 * RT_C : 4];
   rt_stage_affine(sLN, ln_w, ln_b, tid, 64 * NW);
+  if constexpr (BIAS) rt_stage_affine(sLNz, zb.ln_w, zb.ln_b, tid, 64 * NW);
   issue(0, 0);
   if (U > 1) issue(1, nhb > 1 ? 1 : 0);
   int buf = 0;                                         // ring buffer of chunk u (u mod 3)
@@ -172,11 +188,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     const int64_t pix = pix0 + 32 * p + n;
     const bool live = pix < rows;
     const float m = (mask && live) ? mask[pix] : 1.0f;
+    u32x4 zo[8];                                       // the written row, chunk 2 cb + h2 = channels 32 cb + 16 h2 + 8 g .. +7
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
       float y[16];
       rt_regroup_f32(acc[p][cb], y);
-      if (!live) continue;
+      if (!live) {
+        zo[2 * cb] = zo[2 * cb + 1] = u32x4{0, 0, 0, 0};
+        continue;
+      }
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
         const int64_t c0 = pix * TR_C + 32 * cb + 16 * h2 + 8 * g;
@@ -191,7 +211,39 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
             v[2 * e + 1] += hi_bf(r[e]);
           }
         }
-        *reinterpret_cast<u32x4*>(out + c0) = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+        const u32x4 w = u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7])};
+        *reinterpret_cast<u32x4*>(out + c0) = w;
+        zo[2 * cb + h2] = w;
+      }
+    }
+    if constexpr (BIAS) {
+      // chunk 2 cb + h2 of the lane is rt_chunk(2 cb + h2, g): zo is the row in the order rt_load gives the prologue.  The
+      // lane index is re-read here (opaque_lane): weight addresses derived from it and hoisted out of the tile loop would
+      // hold registers the chunk loop needs
+      __builtin_amdgcn_sched_barrier(0);               // the output stores above are issued; nothing of this moves above them
+      const int ol = opaque_lane(), on = ol & 31;
+      bf16x8 xn[8];
+      rt_ln(zo, g, sLNz, zb.eps, xn);
+      f32x16 bacc = {};
+      const uint16_t* wrow = zb.w + on * TR_C + 8 * g;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const u32x4 wv = on < zb.H ? *reinterpret_cast<const u32x4*>(wrow + 16 * t) : u32x4{0, 0, 0, 0};
+        bacc = mfma32(as_bf8(wv), xn[t], bacc);
+      }
+      if (live) {
+        // head c_row(v, g) of pixel (b, i, j): offset base + head * (n ld); the head rows come from the re-read lane index
+        const int64_t nn = zb.n * zb.n, b = pix / nn, rem = pix - b * nn, i = rem / zb.n, j = rem - i * zb.n;
+        const int64_t hs = zb.n * zb.ld, base = (b * zb.H * zb.n + i) * zb.ld + j;
+        const int og = ol >> 5;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int hh = c_row(v, og);
+          if (hh >= zb.H) continue;
+          const int64_t o = base + hh * hs;
+          if (zb.bf16) reinterpret_cast<uint16_t*>(zb.out)[o] = f2bf(bacc[v] * 1.0f);
+          else reinterpret_cast<float*>(zb.out)[o] = bacc[v] * 1.0f;
+        }
       }
     }
   }
@@ -399,20 +451,33 @@ extern "C" int fpf_transition_fwd(const FpfTransitionArgs* a, void* stream, char
         (a->ln_w && !aligned16(a->ln_w)) || (a->ln_b && !aligned16(a->ln_b)))
       return fail(err, errlen, FPF_E_ALIGN, "operands must be 16-byte aligned");
     if (a->x_ln && !aligned16(a->x_ln)) return fail(err, errlen, FPF_E_ALIGN, "x_ln must be 16-byte aligned");
+    TrBias zb = {};
+    if (a->w_z) {
+      if (!a->z_bias) return fail(err, errlen, FPF_E_ARGS, "w_z given without z_bias");
+      if (a->z_heads < 1 || a->z_heads > 32) return fail(err, errlen, FPF_E_SHAPE, "z_heads %d outside 1 .. 32", a->z_heads);
+      if (a->pair_n <= 0 || a->rows % (a->pair_n * a->pair_n) != 0)
+        return fail(err, errlen, FPF_E_SHAPE, "the pair bias needs rows = B N N (rows %lld, pair_n %lld)", (long long)a->rows, (long long)a->pair_n);
+      if (!(a->z_bias_dtype == FPF_DT_F32 || a->z_bias_dtype == FPF_DT_BF16)) return fail(err, errlen, FPF_E_DTYPE, "z_bias_dtype %d", a->z_bias_dtype);
+      const int64_t ld = a->z_bias_ld > 0 ? a->z_bias_ld : a->pair_n;
+      if (ld < a->pair_n) return fail(err, errlen, FPF_E_SHAPE, "z_bias_ld %lld < N %lld", (long long)ld, (long long)a->pair_n);
+      if (!aligned16(a->w_z) || (a->z_ln_w && !aligned16(a->z_ln_w)) || (a->z_ln_b && !aligned16(a->z_ln_b)))
+        return fail(err, errlen, FPF_E_ALIGN, "w_z / z_ln_w / z_ln_b must be 16-byte aligned");
+      zb = TrBias{(const uint16_t*)a->w_z, a->z_ln_w, a->z_ln_b, a->z_eps, a->z_heads, a->z_bias_dtype == FPF_DT_BF16, a->z_bias, a->pair_n, ld};
+    } else if (a->z_bias) {
+      return fail(err, errlen, FPF_E_ARGS, "z_bias given without w_z");
+    }
     constexpr int PW = TR_PW, NW = TR_NW;
     const dim3 grid((unsigned)std::min<int64_t>(cdiv(a->rows, 32 * NW * PW), 2 * (int64_t)num_cus())), block(64 * NW);
-    if (a->x_ln)
-      hipLaunchKernelGGL((transition_bf16_kernel<PW, NW, true>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b,
-                         a->eps, (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows,
-                         a->hidden, (const uint16_t*)a->x_ln);
-    else
-      hipLaunchKernelGGL((transition_bf16_kernel<PW, NW, false>), grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b,
-                         a->eps, (const uint16_t*)a->w_a, (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows,
-                         a->hidden, nullptr);
+    const bool xl = a->x_ln != nullptr, bz = a->w_z != nullptr;
+    auto k = xl ? (bz ? transition_bf16_kernel<PW, NW, true, true> : transition_bf16_kernel<PW, NW, true, false>)
+                : (bz ? transition_bf16_kernel<PW, NW, false, true> : transition_bf16_kernel<PW, NW, false, false>);
+    hipLaunchKernelGGL(k, grid, block, 0, st, (const uint16_t*)a->x, (uint16_t*)a->out, a->ln_w, a->ln_b, a->eps, (const uint16_t*)a->w_a,
+                       (const uint16_t*)a->w_b, (const uint16_t*)a->w_o, a->row_mask, a->residual, a->rows, a->hidden, (const uint16_t*)a->x_ln, zb);
     return launched(err, errlen, "fpf_transition_fwd(bf16)");
   }
   if (a->dtype == FPF_DT_F32) {
     if (a->x_ln) return fail(err, errlen, FPF_E_DTYPE, "x_ln serves the bf16 transition");
+    if (a->w_z || a->z_bias) return fail(err, errlen, FPF_E_DTYPE, "the pair bias serves the bf16 transition");
     if (a->c > TF_CM) return fail(err, errlen, FPF_E_SHAPE, "fp32 transition serves c <= %d (got %d)", TF_CM, a->c);
     if (a->c == TR_C && a->hidden % TX_HB == 0 && aligned16(a->x) && aligned16(a->out) && aligned16(a->w_a) && aligned16(a->w_b) &&
         aligned16(a->w_o) && (!a->ln_w || aligned16(a->ln_w)) && (!a->ln_b || aligned16(a->ln_b))) {   // the matrix-core kernel

@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 DT_BF16, DT_F32, DT_U8, DT_F32Z_BF16 = 1, 2, 3, 4
 TRIMUL_NOALLOC_SCRATCH_BYTES = 50331648          # include/fpf_hip.h FPF_TRIMUL_NOALLOC_SCRATCH_BYTES
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
@@ -27,7 +27,8 @@ class LnArgs(C.Structure):
 class TransitionArgs(C.Structure):
     _fields_ = [("abi_version", i32), ("dtype", i32), ("c", i32), ("hidden", i32), ("rows", i64), ("x", vp), ("out", vp),
                 ("ln_w", vp), ("ln_b", vp), ("eps", f32), ("w_a", vp), ("w_b", vp), ("w_o", vp), ("row_mask", vp), ("residual", i32),
-                ("x_ln", vp)]
+                ("x_ln", vp), ("w_z", vp), ("z_ln_w", vp), ("z_ln_b", vp), ("z_eps", f32), ("z_heads", i32), ("pair_n", i64), ("z_bias", vp),
+                ("z_bias_dtype", i32), ("z_bias_ld", i64)]
 
 
 class TrimulArgs(C.Structure):

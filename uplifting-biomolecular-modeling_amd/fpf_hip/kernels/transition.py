@@ -91,10 +91,15 @@ def select(word, *, c, hidden, n_tokens=None, dtype="bf16", direction="fwd", tim
 
 
 def transition(x, W, *, word, residual=False, x_ln=None, mask=None, binary_mask=None, out=None, n_tokens=None, family="pair", timing="eager",
-               capture=False, stack=None, form="swiglu", cc=None, selection=None):
+               capture=False, stack=None, form="swiglu", cc=None, selection=None, pair_bias=None):
     """y = W_o(silu(W_a n) * (W_b n)), n = LayerNorm(x) in-kernel -> (y, Selection); x + y when ``residual``; ``mask`` one value
     per row of x (any values: the update is multiplied by it before the residual add, so ``binary_mask`` changes nothing);
-    ``out`` may be x (in place).  The hidden is fp32 and rounded to bf16 once (silu(a) * b) before the output projection."""
+    ``out`` may be x (in place).  The hidden is fp32 and rounded to bf16 once (silu(a) * b) before the output projection.
+
+    ``pair_bias`` (bf16 pair tensor x [B, N, N, 128] or [N, N, 128]): a dict ``w_z`` [H, 128] (H <= 32), ``out`` [B, H, N, N] fp32 |
+    bf16 (unit key stride, one row pitch), optional ``ln_w`` / ``ln_b`` [128] and ``eps`` -- the single track's pair bias
+    LN(row) . w_z[h] of the rows this call writes, computed in the same kernel (boltz2/opt/forward/pairfuse/bz_pairfuse.py:18-20
+    runs it as its own pass over the resident z; the values equal ``attn.apb_core.pair_bias_producer`` on the written z)."""
     c = int(x.shape[-1])
     if c != W.c:
         raise Refusal("c:%d!=%d" % (c, W.c), word, F.ROW_STOCK)
@@ -123,8 +128,37 @@ def transition(x, W, *, word, residual=False, x_ln=None, mask=None, binary_mask=
     a = L.TransitionArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16 if x.dtype == torch.bfloat16 else L.DT_F32, c=c, hidden=W.hidden,
                          rows=rows, x=L.ptr(x), out=L.ptr(out), ln_w=L.ptr(lw), ln_b=L.ptr(lb), eps=W.eps, w_a=L.ptr(wa), w_b=L.ptr(wb),
                          w_o=L.ptr(wo), row_mask=L.ptr(m), residual=1 if residual else 0, x_ln=L.ptr(x_ln))
+    keep = _pair_bias_args(a, x, pair_bias, sel) if pair_bias is not None else None
     L.call("fpf_transition_fwd", a, L.stream_ptr(x.device))
+    del keep
     return out, sel
+
+
+def _pair_bias_args(a, x, pb, sel):
+    """Fills the pair-bias fields of ``a`` from the ``pair_bias`` dict; returns the device tensors the call reads (kept alive by
+    the caller until the launch)."""
+    if x.dtype != torch.bfloat16 or sel.row != F.ROW_FAST:
+        raise Refusal("pair_bias:precision", sel.row, F.ROW_STOCK, "the pair bias is projected by the bf16 transition")
+    x4 = x if x.dim() == 4 else x.unsqueeze(0)
+    if x4.dim() != 4 or int(x4.shape[1]) != int(x4.shape[2]) or int(x4.shape[3]) != 128:
+        raise Refusal("pair_bias:not_pair", sel.row, F.ROW_STOCK, "x must be a pair tensor [B, N, N, 128] (got %s)" % (tuple(x.shape),))
+    B, N = int(x4.shape[0]), int(x4.shape[1])
+    w_z, bias = pb.get("w_z"), pb.get("out")
+    if w_z is None or bias is None:
+        raise Refusal("pair_bias:args", sel.row, F.ROW_STOCK, "pair_bias needs w_z and out")
+    H = int(w_z.shape[0])
+    if w_z.dim() != 2 or int(w_z.shape[1]) != 128 or not 1 <= H <= 32:
+        raise Refusal("pair_bias:w_z", sel.row, F.ROW_STOCK, "w_z [H <= 32, 128] (got %s)" % (tuple(w_z.shape),))
+    if (tuple(bias.shape) != (B, H, N, N) or bias.dtype not in (torch.float32, torch.bfloat16) or bias.device != x.device
+            or bias.stride(3) != 1 or bias.stride(1) != N * bias.stride(2) or bias.stride(0) != H * bias.stride(1)):
+        raise Refusal("pair_bias:out", sel.row, F.ROW_STOCK, "out must be an fp32 | bf16 [B, H, N, N] on x's device with rows of one pitch")
+    wz = w_z.to(device=x.device, dtype=torch.bfloat16).contiguous()
+    lw = None if pb.get("ln_w") is None else pb["ln_w"].to(device=x.device, dtype=torch.float32).contiguous()
+    lb = None if pb.get("ln_b") is None else pb["ln_b"].to(device=x.device, dtype=torch.float32).contiguous()
+    a.w_z, a.z_ln_w, a.z_ln_b, a.z_eps, a.z_heads = L.ptr(wz), L.ptr(lw), L.ptr(lb), float(pb.get("eps", 1e-5)), H
+    a.pair_n, a.z_bias, a.z_bias_ld = N, L.ptr(bias), int(bias.stride(2))
+    a.z_bias_dtype = L.DT_F32 if bias.dtype == torch.float32 else L.DT_BF16
+    return wz, lw, lb
 
 
 def pair_transition_chunked(x, W, *, chunk, row_dim=-3, word="big", residual=False, mask=None, out=None, fp32="passthrough", selection=None):

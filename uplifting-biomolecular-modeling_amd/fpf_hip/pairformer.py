@@ -49,8 +49,10 @@ class PairBlock(object):
         self.tr = TR.pack(w_o=t(p["w_o"]), w_a=t(p["w_a"]), w_b=t(p["w_b"]), ln_w=t(p["ln_w"], True), ln_b=t(p["ln_b"], True))
 
 
-def pair_block(z, mask, blk, *, word="fast", rows=256):
+def pair_block(z, mask, blk, *, word="fast", rows=256, pair_bias=None):
     """z [B,N,N,C] (or [N,N,C]) updated in place by the five sites; returns z.  mask [B,N,N] / [N,N] (0/1) or None.
+    ``pair_bias`` (the transition face's dict: w_z, out, ln_w, ln_b, eps): the single track's pair bias of the updated z, written
+    to ``out`` by the transition kernel (word fast) or by the producer pass after the chunked transition (word big).
 
     ``word="big"`` is the memory-lean line of common/opt_core/opt_core/mem/chunk.py (the `big` levers), every site on blocks of
     ``rows`` rows, each bitwise equal to its whole-tensor form: the triangle multiplications in the rows mode (operand planes
@@ -64,12 +66,15 @@ def pair_block(z, mask, blk, *, word="fast", rows=256):
         PF.tri_attn_block_chunked(z, blk.ta["tas"], mask, ending=False, residual=True, chunk=rows, word=word)
         PF.tri_attn_block_chunked(z, blk.ta["tae"], mask, ending=True, residual=True, chunk=rows, word=word)
         TR.pair_transition_chunked(z, blk.tr, chunk=rows, word=word, residual=True, out=z)
+        if pair_bias is not None:
+            APB.pair_bias_producer(z, pair_bias["w_z"], pair_bias.get("ln_w"), pair_bias.get("ln_b"), eps=pair_bias.get("eps", 1e-5),
+                                   out=pair_bias["out"])
         return z
     TM.triangle_multiplication(z, mask, direction="outgoing", weights=blk.tmo, word=word, residual=True, cache=blk.cache_o, out=z)
     TM.triangle_multiplication(z, mask, direction="incoming", weights=blk.tmi, word=word, residual=True, cache=blk.cache_i, out=z)
     PF.tri_attn_block(z, blk.ta["tas"], mask, ending=False, residual=True, word=word)
     PF.tri_attn_block(z, blk.ta["tae"], mask, ending=True, residual=True, word=word)
-    TR.transition(z, blk.tr, word=word, residual=True, out=z)
+    TR.transition(z, blk.tr, word=word, residual=True, out=z, pair_bias=pair_bias)
     return z
 
 
@@ -99,13 +104,14 @@ class SingleBlock(object):
         self.w_o_t = f(t["w_o"]).t().contiguous()                                       # [hidden, c_s]
 
 
-def single_block(s, z, mask, sb):
+def single_block(s, z, mask, sb, bias=None):
     """The sequence stack of one Pairformer layer (boltz2/stock/src/boltz/model/layers/pairformer.py:104-111, autocast off, post
     norm = identity): s_n = LN_s(s); s = s + AttentionPairBias(s_n, z, mask, k_in = s_n); s = s + transition_s(s).  s [B, N, c_s]
-    fp32, z the bf16 pair tensor (already updated by this layer's pair stack), mask [B, N] token mask (or None).  Returns a new s."""
+    fp32, z the bf16 pair tensor (already updated by this layer's pair stack), mask [B, N] token mask (or None), ``bias`` the pair
+    bias of z when already produced (``pair_block(..., pair_bias=...)``).  Returns a new s."""
     c_s = s.shape[-1]
     s_n, _ = LN.layer_norm(s, c_s, sb.ln_s_w, sb.ln_s_b, 1e-5, word="exact")
-    s = s + APB.attention_pair_bias_module(s_n, z, mask, sb.apb)
+    s = s + APB.attention_pair_bias_module(s_n, z, mask, sb.apb, bias=bias)
     # transition_s on N rows (transition.py:47-78): the LayerNorm kernel, then fc1 | fc2 in one library GEMM, silu * gate, fc3
     # and the residual add (plain GEMMs: N token rows are far too few for the fused transition kernels, built for N^2 pair rows)
     x_n, _ = LN.layer_norm(s, c_s, sb.tr.ln_w, sb.tr.ln_b, sb.tr.eps, word="exact")
@@ -115,10 +121,15 @@ def single_block(s, z, mask, sb):
 
 
 def pairformer_layer(s, z, mask, pair_mask, blk, sb, *, word="fast", rows=256):
-    """One Pairformer layer (pairformer.py:64-113): the pair stack updates z in place, then the single track reads it.
-    Returns (s, z)."""
-    pair_block(z, pair_mask, blk, word=word, rows=rows)
-    return single_block(s, z, mask, sb), z
+    """One Pairformer layer (pairformer.py:64-113): the pair stack updates z in place, then the single track reads it.  The
+    single track's pair bias is projected from z by the pair stack's last site (the transition) as it writes z, not by another
+    pass over z.  Returns (s, z)."""
+    z4 = z if z.dim() == 4 else z.unsqueeze(0)
+    B, N = int(z4.shape[0]), int(z4.shape[1])
+    bias = torch.empty((B, sb.apb.H, N, N), dtype=torch.float32, device=z.device)
+    pb = dict(w_z=sb.apb.w_z, ln_w=sb.apb.ln_z_w, ln_b=sb.apb.ln_z_b, eps=1e-5, out=bias)
+    pair_block(z, pair_mask, blk, word=word, rows=rows, pair_bias=pb)
+    return single_block(s, z, mask, sb, bias=bias), z
 
 
 def pairformer_trunk(s, z, mask, pair_mask, layers, *, word="fast", rows=256):
