@@ -148,8 +148,10 @@ constexpr int CB_T = 256, CB_K = 32, CB_NBUF = 4, CB_IF = CB_NBUF - 1;
 // waits until at most p slabs (8 transfers of this wave each) are outstanding, plus the 32 stores of the previous tile when
 // they were issued after the awaited slab (the vector-memory counter retires loads and stores in issue order)
 __device__ __forceinline__ void cb_wait(int p, bool stores) {
+  static_assert(CB_IF <= 4, "the waits below count at most 4 slabs in flight");
   if (stores) {
-    if (p >= 2) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+    if (p >= 3) asm volatile("s_waitcnt vmcnt(56)" ::: "memory");
+    else if (p == 2) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
     else if (p == 1) asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
   } else {
@@ -238,8 +240,9 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   // ring: slab u lives in buffer u % CB_NBUF, CB_IF slabs in flight.  Slab u issues slab u + CB_IF (its buffer held slab
   // u - 1, whose fragments every wave read before slab u - 1's barrier), runs 8 of its 32 MFMAs, waits for slab u + 1 at
   // the barrier (the matrix core keeps working), then reads slab u + 1's 16 fragments ahead of the other 24 MFMAs.  A
-  // tile's stores are issued after the DMA of the next tile's slabs 0 .. 2 and before that of slab 3, so the waits for
-  // slabs 1 and 2 of every tile but the first count them.
+  // tile's stores are issued after the DMA of the next tile's slabs 0 .. CB_IF - 1 and before that of slab CB_IF, so the
+  // waits for slabs 1 .. CB_IF - 1 of the next tile count them -- in the waves that stored (a wave whose quarter of a
+  // half-inside tile is a duplicate issues none, and counting stores it never issued would end its wait early).
   for (int s = 0; s < CB_IF && s < U; ++s) issue_next(s);
   cb_wait((U < CB_IF ? U : CB_IF) - 1, false);
   __builtin_amdgcn_s_barrier();
@@ -247,8 +250,11 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   // MFMAs still read would hold the wave until those MFMAs start)
   bf16x8 f0a[2][4], f0b[2][4], f1a[2][4], f1b[2][4];
   read_frags(0, f0a, f0b);
+  // ring buffers of the next slab to issue (slab u + CB_IF) and of the next slab to read (u + 1), stepped once per slab
+  int bi = CB_IF % CB_NBUF, br = 1 % CB_NBUF;
   auto slab = [&](bool stores, int u, const bf16x8 (&fa)[2][4], const bf16x8 (&fb)[2][4], bf16x8 (&na)[2][4], bf16x8 (&nb)[2][4]) {
-    if (u + CB_IF < U) issue_next((u + CB_IF) % CB_NBUF);
+    if (u + CB_IF < U) issue_next(bi);
+    bi = bi == CB_NBUF - 1 ? 0 : bi + 1;
 #pragma unroll
     for (int si = 0; si < 4; ++si)
 #pragma unroll
@@ -259,7 +265,8 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
       __builtin_amdgcn_s_barrier();
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (u + 1 < U) read_frags((u + 1) % CB_NBUF, na, nb);
+    if (u + 1 < U) read_frags(br, na, nb);
+    br = br == CB_NBUF - 1 ? 0 : br + 1;
 #pragma unroll
     for (int si = 0; si < 4; ++si)
 #pragma unroll
@@ -270,17 +277,20 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
       for (int sj = 0; sj < 4; ++sj) acc[si][sj] = mfma32(fb[1][sj], fa[1][si], acc[si][sj]);
     __builtin_amdgcn_sched_barrier(0);
   };
+  bool stored = false;                                   // this wave issued the previous tile's 32 stores
   for (int r = 0; r < ntile; ++r) {
 #pragma unroll
     for (int si = 0; si < 4; ++si)
 #pragma unroll
       for (int sj = 0; sj < 4; ++sj) acc[si][sj] = f32x16{};
     const int u0 = r * nk;
-    slab(r > 0, u0, f0a, f0b, f1a, f1b);                 // nk is even: Np is a multiple of 128
-    slab(r > 0, u0 + 1, f1a, f1b, f0a, f0b);
+    // the previous tile's stores were issued after this tile's slabs 0 .. CB_IF - 1: the waits for slabs 1 .. CB_IF - 1 (in slabs
+    // 0 .. CB_IF - 2) count them
+    slab(stored, u0, f0a, f0b, f1a, f1b);                // nk is even: Np is a multiple of 128
+    slab(stored, u0 + 1, f1a, f1b, f0a, f0b);
     for (int kt = 2; kt < nk; kt += 2) {
-      slab(false, u0 + kt, f0a, f0b, f1a, f1b);
-      slab(false, u0 + kt + 1, f1a, f1b, f0a, f0b);
+      slab(stored && kt <= CB_IF - 2, u0 + kt, f0a, f0b, f1a, f1b);
+      slab(stored && kt + 1 <= CB_IF - 2, u0 + kt + 1, f1a, f1b, f0a, f0b);
     }
     int64_t bc, ti, tj;
     tile_of(r, bc, ti, tj);
@@ -291,7 +301,8 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
     const uint32_t lane_el = (lane & 31) * (uint32_t)TL_ROW + 8 * (lane >> 5);
     // a quarter past the rows (or columns) of a half-inside tile holds duplicates: not stored (a wave-uniform branch around the
     // whole store sequence, so the accumulators are still packed and stored one at a time)
-    if (ti * CB_T + wr < Ra && tj * CB_T + wc < Np) {
+    stored = ti * CB_T + wr < Ra && tj * CB_T + wc < Np;
+    if (stored) {
 #pragma unroll
       for (int si = 0; si < 4; ++si)
 #pragma unroll
