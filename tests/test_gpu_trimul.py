@@ -220,3 +220,25 @@ def test_trimul_fp32_narrow_channels_scalar_path():
     torch.cuda.synchronize()
     ref = S.trimul(z, None, direction="incoming", weights=w, residual=True, dtype=torch.float64)
     assert_f32_close(out, ref, "trimul fp32 c64")
+
+
+@pytest.mark.parametrize("N", [800, 600])
+def test_trimul_half_inside_tiles_repeat_bitwise(N):
+    """Planes padded to an odd multiple of 128 (N = 800 -> 896, N = 600 -> 640) end half way into the contraction's 256-row
+    tiles: the waves whose quarter of such a tile is a duplicate store nothing, and their next tile's slab waits must not
+    count stores they never issued.  20 calls in a row on one input, both directions, with a mask: all finite and bitwise
+    equal to the first."""
+    from fpf_hip.kernels import trimul as TM
+    g = torch.Generator().manual_seed(N + 3)
+    w = _dev(_weights(128, 5, torch.bfloat16))
+    z = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(DEV)
+    mask = (torch.rand(1, N, N, generator=g) > 0.2).float().to(DEV)
+    for d in ("outgoing", "incoming"):
+        print("[trimul] half-inside tiles N=%d %s x 20" % (N, d), flush=True)
+        cache = {}
+        first = TM.triangle_multiplication(z, mask, direction=d, weights=w, word="fast", cache=cache)
+        torch.cuda.synchronize()
+        assert torch.isfinite(first.float()).all()
+        for rep in range(1, 20):
+            out = TM.triangle_multiplication(z, mask, direction=d, weights=w, word="fast", cache=cache)
+            assert torch.equal(out, first), "%s run %d differs from run 0" % (d, rep)
