@@ -898,10 +898,12 @@ int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64
 int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry) {
   const int64_t rows_heads = p.B * p.H * cdiv(p.N, TA_R);
   // 8 waves share each K / V^T tile among 256 queries; where S is not a multiple of 256 the last query tile is partly padding.
-  // They are taken when that padding costs less than a fifth over the 4-wave split's own (an item of 128 queries per 4 waves)
-  // and the grid holds 8 or more workgroups per CU (measured: the 8-wave split 11-15 % slower at S = 384, where it pads a third)
+  // A query slot of the 8-wave split costs about 95 % of one of the 4-wave split (items of 128 queries per 4 waves): the
+  // 8-wave split is taken when its slots at that rate cost less, and the grid holds 8 or more workgroups per CU (measured,
+  // op / block at the starting node: S = 768 8-wave 0.447 / 0.603 ms against 0.473 / 0.622; S = 800 (832 padded) 4-wave
+  // 0.692 / 0.783 against 0.710 / 0.813; S = 640 4-wave 0.297 / 0.426 against 0.326 / 0.447; S = 384 8-wave 11-15 % slower)
   const int64_t q8 = cdiv(p.S, 32 * TA_DMA_WAVES), q4 = cdiv(p.S, 128);
-  const bool wide = 5 * q8 * (32 * TA_DMA_WAVES) < 6 * q4 * 128 && rows_heads * q8 >= 8 * (int64_t)num_cus();
+  const bool wide = 19 * q8 * (32 * TA_DMA_WAVES) < 20 * q4 * 128 && rows_heads * q8 >= 8 * (int64_t)num_cus();
   const int64_t total = wide ? rows_heads * q8 : rows_heads * q4;
   if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
   // per-lane byte offsets from the scalar bases are 32-bit: q (query, d), bias (query), K (key row of a tile), V^T (d row)

@@ -7,7 +7,8 @@ torch statement of the same op (the same dtype, on the same device: what the ref
 written out in torch because the reference's stock libraries do not exist on this platform), median of ``reps`` calls
 after one warm-up, with HIP events.  Shapes: triangle attention B = 1, H = 4, D = 32, S = N rows and keys, fp32 bias, mask
 all ones; triangle multiplication B = 1, c_z = c_hidden = 128, both directions, mask all ones; transition c = 128, 4x
-hidden, N^2 rows.  Inputs ~ N(0, 1), weights ~ N(0, 1/fan_in), seed 0.
+hidden, N^2 rows.  Inputs ~ N(0, 1), weights ~ N(0, 1/fan_in), seed 0.  Each timing follows at least 30 ms of untimed calls
+(the torch statements: one call when a single call takes longer).
 
 A cell's `fast` is this package's bf16 row; its `exact` follows the reference's exact rule (TRIATTN_CELLS.json
 `exact_rule`): the fp32 row where it measured at least as fast as the fp32 torch statement, else "stock" -- the caller's own
@@ -27,9 +28,15 @@ from . import BUCKETS, CC, TABLE, transition_key, triattn_key, trimul_key
 from .. import _face as F
 
 
-def _median_ms(fn, reps):
+def _median_ms(fn, reps, warm_s=0.03):
+    """Median of ``reps`` timed calls after at least ``warm_s`` seconds of untimed calls (the first ~10 ms of a kernel stream
+    after host-side set-up run slower than the steady state a stack of layers sees)."""
     fn()
     torch.cuda.synchronize()
+    t0 = time.time()
+    while time.time() - t0 < warm_s:
+        fn()
+        torch.cuda.synchronize()
     ts = []
     for _ in range(reps):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
