@@ -179,7 +179,8 @@ def warm_up(fn, torch, seconds=0.03):
 
 
 def time_events(fn, reps, torch):
-    """Median ms per call of fn() over max(reps, 20) calls after warm_up (median of >= 20 after warm-up)."""
+    """Median ms per call of fn() over max(reps, 20) calls after warm_up (the baseline's convention: a median of at least 20
+    calls after a warm-up)."""
     warm_up(fn, torch)
     return statistics.median(step_times(fn, max(reps, 20), torch))
 

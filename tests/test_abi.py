@@ -84,7 +84,7 @@ def test_workspace_queries_need_no_device():
 
 
 def test_integration_stub_sends_the_header_version():
-    """The ctypes stubs in INTEGRATION.md must not pin an ABI version other than the header's: every literal
+    """The ctypes stubs of the integration notes must not pin an ABI version other than the header's: every literal
     abi_version / fpf_abi_version() comparison there equals FPF_ABI_VERSION, which equals the binding's ABI_VERSION."""
     from fpf_hip import _lib as L
     hdr = int(re.search(r"#define FPF_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
