@@ -352,3 +352,27 @@ def test_shared_scratch_keeps_an_outgrown_buffer_a_captured_call_used():
     assert F.reserve_scratch("cpu", 50).numel() >= 600
     F.release_scratch()
     assert F._CAPTURED == [] and F.scratch_bytes() == 0
+
+
+def test_block_mask_all_ones_is_handed_on_as_no_mask():
+    """The block face converts a pair mask once per tensor (object and version); one that keeps every pixel is handed on as no
+    mask (bz_pairfuse.py:46-50: a trivial mask goes to the providers as None), in both frames; a mask with a masked pixel, a
+    mask changed in place and an inference-mode mask (converted per call) are handed on as u8."""
+    from fpf_hip import _lib as L
+    from fpf_hip.attn import pair_fused as PF
+    z4 = torch.zeros(1, 8, 8, 128, dtype=torch.bfloat16)
+    ones = torch.ones(1, 8, 8)
+    for ending in (False, True):
+        for _ in range(2):                                           # the conversion and the cached answer
+            assert PF._pair_mask(ones, z4, ending) == (None, L.DT_U8, 0)
+    part = torch.ones(1, 8, 8)
+    part[0, 3, 5] = 0
+    m, dt, frame = PF._pair_mask(part, z4, True)
+    assert frame == 1 and dt == L.DT_U8 and m.dtype == torch.uint8 and int(m[0, 5, 3]) == 0 and int(m.sum()) == 63
+    ones[0, 1, 2] = 0                                                # in place: a new version, converted again
+    m, _, frame = PF._pair_mask(ones, z4, False)
+    assert frame == 1 and int(m[0, 1, 2]) == 0
+    with torch.inference_mode():
+        inf = torch.ones(1, 8, 8)
+        m, _, frame = PF._pair_mask(inf, z4, False)
+    assert frame == 1 and int(m.sum()) == 64

@@ -126,7 +126,10 @@ def _pair_mask(mask, z4, ending=False):
     node gets the transposed mask, mask_frame 1, so each attention row's keys are contiguous) -> (tensor, dtype, mask_frame).
     The copies are made once and kept while the same tensor (same object, same version counter) comes back -- a pair stack
     passes one mask to every block.  Inference tensors carry no version counter, so a mask made under torch.inference_mode()
-    is converted on every call instead."""
+    is converted on every call instead.  A cached mask that keeps every pixel is handed on as no mask (the reference's pairfuse
+    driver does the same, boltz2/opt/forward/pairfuse/bz_pairfuse.py:46-50): the block then builds no keep table and runs the
+    mask-free core, whose arithmetic is the masked core's on fully kept tiles (the same bits).  Deciding that reads one flag
+    back from the device once per mask tensor (not while the stream is capturing a graph, and not for inference tensors)."""
     if mask is None:
         return None, L.DT_U8, 0
     B, N = z4.shape[0], z4.shape[1]
@@ -137,12 +140,14 @@ def _pair_mask(mask, z4, ending=False):
     key = ("t" if ending else "m", z4.device)
     hit = _MASK_U8.get(key)
     if version is not None and hit is not None and hit[0] is mask and hit[1] == version:
-        return hit[2], L.DT_U8, 1
+        return hit[2], L.DT_U8, (0 if hit[2] is None else 1)
     mm = m.transpose(1, 2) if ending else m
     u8 = (mm.to(z4.device) != 0).contiguous().view(torch.uint8)
     if version is not None:
+        if u8.device.type != "meta" and not (u8.is_cuda and torch.cuda.is_current_stream_capturing()) and bool(u8.all()):
+            u8 = None                                 # every pixel kept: no mask
         _MASK_U8[key] = (mask, version, u8)          # holding the tensor keeps its storage from being reused
-    return u8, L.DT_U8, 1
+    return u8, L.DT_U8, (0 if u8 is None else 1)
 
 
 def _block_check(z, W, word, face):
