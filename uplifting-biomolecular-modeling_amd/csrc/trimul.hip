@@ -326,6 +326,10 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
 // the next tile's X loads, then LN_out(X) W_o^T * sigmoid(LN_in(z) W_og^T) [+ z] (the residual reuses the z rows the
 // LayerNorm read).
 constexpr int K3_XLD = RT_C + 8;     // LDS pitch of the staged X tile, pixel-major [32 pixels][128 channels]
+// Channel c of pixel p sits at column c ^ k3_swz(p): the 2-byte scatter writes pixels p0 + 2e, p0 = 0, 8, 16, 24, in one
+// instruction, rows that any 16-byte-aligned pitch puts on the same banks; the XOR moves them 0 / 8 / 16 / 24 dwords apart,
+// and every 8-channel chunk stays contiguous for the 16-byte fragment reads
+__device__ __forceinline__ int k3_swz(int p) { return 16 * ((p >> 3) & 3); }
 
 // ZF32: z and out are fp32 (the fp32-resident form): LN_in reads the bf16 copy of each row, the residual adds the fp32 z
 // and the result is stored in fp32.
@@ -369,15 +373,15 @@ __global__ void __launch_bounds__(512) trimul_k3_bf16(const void* zin, void* out
       const int q = l + 64 * it, c = q >> 2, p0 = (q & 3) * 8;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        sx[(p0 + 2 * e) * K3_XLD + c] = (uint16_t)(rx[it][e] & 0xffff);
-        sx[(p0 + 2 * e + 1) * K3_XLD + c] = (uint16_t)(rx[it][e] >> 16);
+        sx[(p0 + 2 * e) * K3_XLD + (c ^ k3_swz(p0 + 2 * e))] = (uint16_t)(rx[it][e] & 0xffff);
+        sx[(p0 + 2 * e + 1) * K3_XLD + (c ^ k3_swz(p0 + 2 * e + 1))] = (uint16_t)(rx[it][e] >> 16);
       }
     }
     rt_wave_lds_sync();
     if (t + stride < total) fetch_x(t + stride);            // the next tile's X lands while this one computes
     u32x4 xr[8];
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) xr[tt] = *reinterpret_cast<const u32x4*>(&sx[n * K3_XLD + 8 * rt_chunk(tt, g)]);
+    for (int tt = 0; tt < 8; ++tt) xr[tt] = *reinterpret_cast<const u32x4*>(&sx[n * K3_XLD + ((8 * rt_chunk(tt, g)) ^ k3_swz(n))]);
     rt_wave_lds_sync();
     bf16x8 xo[8], xi[8];
     rt_ln(xr, g, sLNo, eps, xo);
