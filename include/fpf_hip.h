@@ -229,9 +229,10 @@ typedef struct {
                               layouts read `mask` and ignore this field. */
   void* workspace;         /* v_layout 2: device memory of fpf_triattn_workspace_bytes(B, N, H, S, 2) bytes (per work item a flag the
                               fast kernel writes and its fallback reads).  v_layout 0 / 1: NULL, or fpf_triattn_stage_bytes(B, N,
-                              H, S, D, dtype) bytes or more, which runs a bf16 call with head_dim 32 on the block-layout core (q, v,
-                              the bias and the mask restaged there; q / k / v rows and out rows of 32 contiguous 16-byte aligned
-                              bf16, out_stride[3] = 32); a call that does not meet those conditions runs the op core as without */
+                              H, S, D, dtype) bytes or more, which runs a bf16 call with head_dim 32 on the block-layout core (v,
+                              the bias and the mask restaged there, q and k read in place; q / k / v rows and out rows of 32
+                              contiguous 16-byte aligned bf16, out_stride[3] = 32, q / k offsets within a (b, h) plane below 2^31
+                              bytes); a call that does not meet those conditions runs the op core as without */
   size_t workspace_bytes;
 } FpfTriattnArgs;
 int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err, size_t errlen);

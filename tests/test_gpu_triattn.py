@@ -367,16 +367,18 @@ def _bias_blocks(bias):
     return v.permute(0, 1, 2, 4, 5, 6, 3, 7).contiguous().view(B, H, S, S)
 
 
-def _keep_table(mask):
+def _keep_table(mask, real=None):
     """The keep-bit table of the block-layout core (include/fpf_hip.h, FpfTriattnArgs.keep), built on the host from a [B, N, S]
     0/1 mask: per attention row, word 0 = flags (1 some key kept, 2 every key kept), word 1 + t = bits of keys 64 t .. 64 t + 63;
-    a row with no kept key has every bit set."""
+    a row with no kept key has the bit of every real key (the first `real`, default all) set."""
     B, N, S = mask.shape
+    real = S if real is None else real
     m = (mask != 0).cpu().numpy().reshape(B, N, S // 64, 64).astype(np.uint64)
     words = (m << np.arange(64, dtype=np.uint64)).sum(axis=-1, dtype=np.uint64)
     alive = m.reshape(B, N, S).any(axis=-1)
     full = m.reshape(B, N, S).all(axis=-1)
-    words[~alive] = np.uint64(0xFFFFFFFFFFFFFFFF)
+    r = (np.arange(S) < real).astype(np.uint64).reshape(S // 64, 64)
+    words[~alive] = (r << np.arange(64, dtype=np.uint64)).sum(axis=-1, dtype=np.uint64)
     flags = alive.astype(np.uint64) | (full.astype(np.uint64) << np.uint64(1))
     table = np.concatenate([flags[..., None], words], axis=-1)
     return torch.from_numpy(table.view(np.int64).copy()).to(DEV)
@@ -437,6 +439,65 @@ def test_block_layout_core_fallback_extreme_logits(N, masked):
     got = out[0, rows].float()
     assert torch.isfinite(got).all(), "non-finite output"
     assert_bf16_close(got, ref, "block-layout core N=%d masked=%s, extreme query tiles" % (N, masked))
+
+
+@pytest.mark.parametrize("S_,layout,N", [(456, "contig", 7), (800, "contig", 7), (768, "endstrided", 7), (130, "endstrided", 7),
+                                         (720, "contig", 512)])
+def test_op_face_in_place_route_equals_the_block_core_on_restaged_operands(S_, layout, N):
+    """The op face's route onto the block-layout core reads q and k in place -- q times scale * log2(e) in registers, the
+    padding keys of the last tile re-reading the last real key row under the keep table's mask -- and restages only V^T and the
+    bias.  Its output equals, bit for bit, the block-layout core (v_layout 2) given every operand restaged on the host:
+    q2 = bf16(q * fp32(scale * log2(e))), k and V^T padded with zeros to Sp = S rounded up to 64 (V^T in the 16-block key
+    order), the bias times log2(e) in register-order blocks, the keep table with the padding keys masked.  A random mask with a
+    dead row; `endstrided`: q and k as transposed views of [B, S, H, N, D] storage (the ending node's layout).  N = 7 runs the
+    4-wave split, N = 512 at S = 720 (padded to 768) the 8-wave one."""
+    import ctypes
+    from fpf_hip import _lib as L
+    from fpf_hip.kernels import triattn as TA
+    B, H, D = 1, 4, 32
+    Sp = -(-S_ // 64) * 64
+    q, k, v, bias = _rand_op(B, N, H, S_, D, 31 + S_, torch.bfloat16)
+    g = torch.Generator().manual_seed(32 + S_)
+    mask = torch.rand(B, N, 1, 1, S_, generator=g) > 0.2
+    mask[0, 3] = False
+    if layout == "endstrided":
+        qd, kd = (t.transpose(1, 3).contiguous().to(DEV).transpose(1, 3) for t in (q, k))
+    else:
+        qd, kd = q.to(DEV), k.to(DEV)
+    print("[op in place] S=%d %s N=%d" % (S_, layout, N), flush=True)
+    got = TA.triangle_attention(qd, kd, v.to(DEV), bias.to(DEV), mask.to(DEV), word="fast")
+    # every operand restaged on the host, for the core's own layout
+    qmul = float(np.float32(np.float32(1.0 / np.sqrt(D)) * np.float32(1.4426950408889634)))
+    q2 = torch.zeros(B, N, H, Sp, D, dtype=torch.bfloat16)
+    q2[..., :S_, :] = (q.float() * qmul).to(torch.bfloat16)
+    k2 = torch.zeros(B, N, H, Sp, D, dtype=torch.bfloat16)
+    k2[..., :S_, :] = k
+    vT = torch.zeros(B, N, H, D, Sp, dtype=torch.bfloat16)
+    vT[..., :S_] = v.transpose(-1, -2)
+    perm = torch.tensor([16 * (p // 16) + _VPERM[p % 16] for p in range(Sp)])
+    v2 = vT[..., perm].contiguous()
+    b2 = torch.zeros(B, H, Sp, Sp)
+    b2[:, :, :S_, :S_] = bias[:, 0].float() * float(np.float32(1.4426950408889634))
+    b2 = _bias_blocks(b2).to(DEV)
+    m2 = torch.zeros(B, N, Sp)
+    m2[..., :S_] = mask.reshape(B, N, S_).float()
+    keep = _keep_table(m2, real=S_)
+    q2, k2, v2 = q2.to(DEV), k2.to(DEV), v2.to(DEV)
+    out = torch.full((B, N, H, Sp, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    ws = torch.empty(max(1, L.lib().fpf_triattn_workspace_bytes(B, N, H, Sp, 2)), dtype=torch.uint8, device=DEV)
+    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=B, N=N, H=H, S=Sp, D=D, q=L.ptr(q2), k=L.ptr(k2), v=L.ptr(v2),
+                      v_layout=2, bias=L.ptr(b2), bias_dtype=L.DT_F32, out=L.ptr(out), scale=1.0,
+                      keep=ctypes.c_void_p(keep.data_ptr()), workspace=L.ptr(ws), workspace_bytes=ws.numel())
+    a.q_stride[:] = q2.stride()
+    a.k_stride[:] = k2.stride()
+    a.v_stride[:] = v2.stride()
+    a.out_stride[:] = out.stride()
+    a.bias_stride[:] = b2.stride()
+    L.call("fpf_triattn_fwd", a, L.stream_ptr(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, out[..., :S_, :]), "in-place route differs from the restaged core: max |d| %g" % max_abs(
+        got.float().cpu(), out[..., :S_, :].float().cpu())
 
 
 def _xln_weights(seed):

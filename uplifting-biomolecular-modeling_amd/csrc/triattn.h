@@ -36,6 +36,11 @@ struct CoreParams {
   uint32_t* redo;                // block-layout core: one flag per (work item, wave), written by the fast kernel
   int64_t Sv;                    // block-layout core: the real keys / queries (<= S); keys Sv .. S - 1 pad the key axis to a
                                  // multiple of 64 and are masked by the keep table, queries past Sv are never stored
+  int64_t Sqk;                   // block-layout core: the query / key rows q and k hold (S - 64 < Sqk <= S); queries past it read
+                                 // query 0 (never stored), the last K tile's rows past it re-read row Sqk - 1 (keys the keep
+                                 // table masks)
+  float qmul;                    // block-layout core: the factor q is multiplied by in registers, each product rounded to bf16
+                                 // once (1: q comes already multiplied)
 };
 
 __device__ __forceinline__ bool mask_keep(const CoreParams& p, int64_t b, int64_t i, int64_t key) {
@@ -46,6 +51,15 @@ __device__ __forceinline__ bool mask_keep(const CoreParams& p, int64_t b, int64_
 
 __device__ __forceinline__ float bias_at(const CoreParams& p, int64_t off) {
   return p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[off]) : static_cast<const float*>(p.bias)[off];
+}
+
+// eight bf16 of q times m, each product rounded to bf16 once (the op face's staging and the block-layout core's in-register
+// scaling compute the same bits)
+__device__ __forceinline__ u32x4 scale_bf8(const u32x4& x, float m) {
+  u32x4 w;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) w[e] = pack2(lo_bf(x[e]) * m, hi_bf(x[e]) * m);
+  return w;
 }
 
 // Bias plane of the block-layout core (v_layout 2): S x S fp32 (query q, key k) in 32 x 32 blocks, block (q / 32, k / 32) at
@@ -123,6 +137,7 @@ __device__ __forceinline__ void karg_wait(uint64_t (&v)[K]) {
   for (int i = 0; i < K; ++i) asm volatile("" : "+s"(v[i]));
 }
 #define FPF_KARG(field) ::fpf::karg_issue<(int)offsetof(::fpf::CoreParams, field)>()
+static_assert(offsetof(CoreParams, qmul) + 8 <= sizeof(CoreParams), "a reload of qmul reads 8 bytes inside the block");
 // waits until at most N vector-memory operations of this wave are outstanding; the registers of the sub-tile's bias pass
 // through the statement so nothing reads them earlier
 template <int N>
@@ -151,6 +166,7 @@ inline int64_t redo_words(int64_t B, int64_t N, int64_t H, int64_t S) {
 // mask NULL: every real key kept (a table that only masks the padding keys Sv .. S - 1)
 int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, int64_t Sv, uint64_t* keep,
                       hipStream_t st, char* err, size_t errlen, bool dry = false);
+bool pipe_offsets_fit(int64_t S, const int64_t* qs, const int64_t* ks, const int64_t* vs);
 int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry = false);
 
 // N a multiple of 64, or any N from 128, up to 8192: the J axis of q / k / V^T / o and of the bias planes is padded to Np = N
@@ -162,26 +178,21 @@ inline bool block_layout2(int dtype, int64_t N) {
 }
 inline int64_t block_np(int dtype, int64_t N) { return block_layout2(dtype, N) ? cdiv(N, TA_KT) * TA_KT : N; }
 
-// The op face's operands restaged into the block-layout core's layout (triattn_pipe.hip): q2 = q * qmul and k2 = k as
-// [B, N, H, Sp, 32], v2 = V^T [B, N, H, 32, Sp] with each 16-key block in the order 0-3, 8-11, 4-7, 12-15, bias2 = bias * log2(e)
-// as [B, H, Sp, Sp] in 32 x 32 register-order blocks (bias_blk_off), Sp = S rounded up to 64, every padding element zero.  v is
-// read as [B, N, H, S, 32] (v_t = 0) or transposed as [B, N, H, 32, S] (v_t = 1); k2 NULL: k is not copied (the core reads it in
-// place).  The caller has checked: head_dim rows of 32 contiguous, 16-byte aligned bf16 (strides multiples of 8 elements).
+// The op face's V and bias restaged into the block-layout core's layout (triattn_pipe.hip): v2 = V^T [B, N, H, 32, Sp] with each
+// 16-key block in the order 0-3, 8-11, 4-7, 12-15, bias2 = bias * log2(e) as [B, H, Sp, Sp] in 32 x 32 register-order blocks
+// (bias_blk_off), Sp = S rounded up to 64, every padding element zero (q and k the core reads in place).  v is read as
+// [B, N, H, S, 32] (v_t = 0) or transposed as [B, N, H, 32, S] (v_t = 1).  The caller has checked: head_dim rows of 32
+// contiguous, 16-byte aligned bf16 (strides multiples of 8 elements).
 struct StageParams {
-  const uint16_t* q;
-  const uint16_t* k;
   const uint16_t* v;
-  int64_t qs[4], ks[4], vs[4];   // strides of b, n, h, s (v_t = 1: of b, n, h, d)
+  int64_t vs[4];                 // strides of b, n, h, s (v_t = 1: of b, n, h, d)
   int v_t;
   const void* bias;
   int bias_bf16;
   int64_t bs[3];                 // strides of b, h, query (the key stride is 1)
-  uint16_t* q2;
-  uint16_t* k2;
   uint16_t* v2;
   float* bias2;
   int64_t B, N, H, S, Sp;
-  float qmul;
 };
 int op_stage_launch(const StageParams& p, hipStream_t st, char* err, size_t errlen, bool dry = false);
 

@@ -11,6 +11,7 @@
 // folded into one FMA.  A row whose keys are all masked attends uniformly to every key (the op's convention).
 // fp32 core (exact tier): one thread per query, LDS-staged K / V tiles, fp32 online softmax with expf.
 #include <algorithm>
+#include <cmath>
 
 #include "triattn.h"
 
@@ -849,7 +850,11 @@ __global__ void __launch_bounds__(256) triattn_epilogue_f32(const float* __restr
 
 // dry = true: every check, nothing launched
 // Sv: the real keys / queries of a v_layout 2 call whose key axis is padded (S = Sv rounded up to 64); -1 = S.
-static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen, bool dry = false, int64_t Sv = -1) {
+// Sv: the real keys / queries of a padded block-layout call (-1: S).  qmul > 0: a block-layout call whose q and k hold only the
+// Sv real rows, q not yet multiplied by the scale -- the core multiplies q by qmul in registers and re-reads the last real key
+// row for the padding keys (the op face's in-place route); 0: q and k hold S rows, q already multiplied.
+static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen, bool dry = false, int64_t Sv = -1,
+                       float qmul = 0.0f) {
   if (a->dtype == FPF_DT_BF16) {
     if (a->D != TA_D) return fail(err, errlen, FPF_E_SHAPE, "bf16 core serves head_dim 32 (got %lld)", (long long)a->D);
     CoreParams p{};
@@ -875,6 +880,8 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     p.S = a->S;
     p.scale = a->scale;
     p.Sv = Sv < 0 ? a->S : Sv;
+    p.qmul = qmul > 0.f ? qmul : 1.0f;
+    p.Sqk = qmul > 0.f ? p.Sv : a->S;
     p.v_t = a->v_layout;
     if (!(p.v_t == 0 || p.v_t == 1 || p.v_t == 2)) return fail(err, errlen, FPF_E_ARGS, "v_layout %d", a->v_layout);
     for (int t = 0; t < 4; ++t)
@@ -893,6 +900,8 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
       if (p.bs[2] != p.S || p.bs[3] != 1)
         return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 reads contiguous S x S bias planes in 32 x 32 register-order blocks (bias_stride[2] = S, [3] = 1)");
       if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
+      if (!(p.qmul > 0.f) || !std::isfinite(p.qmul) || p.Sqk <= p.S - TA_KT || p.Sqk > p.S)
+        return fail(err, errlen, FPF_E_ARGS, "v_layout 2: q / k rows %lld of %lld, q factor %g", (long long)p.Sqk, (long long)p.S, (double)p.qmul);
       if (p.mask && !a->keep)
         return fail(err, errlen, FPF_E_ARGS, "v_layout 2 reads the mask as a keep-bit table (keep); the fused block builds it");
       if (p.os[3] != TA_D || ((p.os[0] | p.os[1] | p.os[2]) & 7) || !aligned16(a->out))
@@ -952,66 +961,57 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
 }
 
 // The op face on the block-layout core: a bf16 call with head_dim 32 and S the block core serves (a multiple of 64, or at
-// least 128, up to 8192), given a workspace of fpf_triattn_stage_bytes, is restaged (op_stage_launch: q times scale * log2(e),
-// V^T in the core's key order, the bias in blocks, every operand padded to Sp = S rounded up to 64), its mask (and the padding)
-// becomes a keep table, and the persistent core writes the caller's out directly.  k is read in place when no padding is needed
-// and its rows are 16-byte aligned.  Workspace regions: q2 | k2 | v2 (each B N H Sp 32 bf16) | bias2 (B H Sp^2 fp32) | keep | redo.
+// least 128, up to 8192), given a workspace of fpf_triattn_stage_bytes, has V^T and the bias restaged (op_stage_launch: V^T in
+// the core's key order, the bias times log2(e) in blocks, both padded to Sp = S rounded up to 64), its mask (and the padding)
+// becomes a keep table, and the persistent core reads the caller's q and k in place -- q multiplied by scale * log2(e) in
+// registers, the padding keys re-reading the last real key row, masked -- and writes the caller's out directly.
+// Workspace regions: v2 (B N H 32 Sp bf16) | bias2 (B H Sp^2 fp32) | keep | redo.
 struct OpStage {
-  size_t k2, v2, bias2, keep, redo, total;
+  size_t bias2, keep, redo, total;
 };
 static OpStage op_stage_layout(int64_t B, int64_t N, int64_t H, int64_t S) {
   const int64_t Sp = block_np(FPF_DT_BF16, S);
   const auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
   const size_t r = al((size_t)B * N * H * Sp * TA_D * 2), rb = al((size_t)B * H * Sp * Sp * 4);
   const size_t rk = al((size_t)B * N * keep_words(Sp) * 8), rr = al((size_t)redo_words(B, N, H, Sp) * 4);
-  return {r, 2 * r, 3 * r, 3 * r + rb, 3 * r + rb + rk, 3 * r + rb + rk + rr};
+  return {r, r + rb, r + rb + rk, r + rb + rk + rr};
 }
 static bool op_staged_shape(int dtype, int64_t D, int64_t S) { return dtype == FPF_DT_BF16 && D == TA_D && block_layout2(dtype, S); }
 static bool rows32_ok(const void* p, const int64_t* st4) {     // rows of 32 contiguous bf16, 16-byte aligned, for strides [0..3]
   return aligned16(p) && ((st4[0] | st4[1] | st4[2] | st4[3]) & 7) == 0;
 }
 
+// the caller's q and k strides (and the staged V^T's) within the block-layout core's 32-bit in-item offsets
+static bool op_in_place_fits(const FpfTriattnArgs* a) {
+  const int64_t Sp = block_np(FPF_DT_BF16, a->S);
+  const int64_t vs5[5] = {a->N * a->H * TA_D * Sp, a->H * TA_D * Sp, TA_D * Sp, Sp, 1};
+  return pipe_offsets_fit(Sp, a->q_stride, a->k_stride, vs5);
+}
+
 static int op_staged(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen) {
   const int64_t B = a->B, N = a->N, H = a->H, S = a->S, Sp = block_np(FPF_DT_BF16, S);
   const OpStage L = op_stage_layout(B, N, H, S);
   char* w = static_cast<char*>(a->workspace);
-  const bool k_in_place = Sp == S && rows32_ok(a->k, a->k_stride);
   StageParams sp{};
-  sp.q = (const uint16_t*)a->q;
-  sp.k = (const uint16_t*)a->k;
   sp.v = (const uint16_t*)a->v;
-  for (int t = 0; t < 4; ++t) {
-    sp.qs[t] = a->q_stride[t];
-    sp.ks[t] = a->k_stride[t];
-    sp.vs[t] = a->v_stride[t];
-  }
+  for (int t = 0; t < 4; ++t) sp.vs[t] = a->v_stride[t];
   sp.v_t = a->v_layout;
   sp.bias = a->bias;
   sp.bias_bf16 = a->bias_dtype == FPF_DT_BF16;
   for (int t = 0; t < 3; ++t) sp.bs[t] = a->bias_stride[t];
-  sp.q2 = reinterpret_cast<uint16_t*>(w);
-  sp.k2 = k_in_place ? nullptr : reinterpret_cast<uint16_t*>(w + L.k2);
-  sp.v2 = reinterpret_cast<uint16_t*>(w + L.v2);
+  sp.v2 = reinterpret_cast<uint16_t*>(w);
   sp.bias2 = reinterpret_cast<float*>(w + L.bias2);
   sp.B = B;
   sp.N = N;
   sp.H = H;
   sp.S = S;
   sp.Sp = Sp;
-  sp.qmul = a->scale * LOG2E;
   uint64_t* keep = reinterpret_cast<uint64_t*>(w + L.keep);
   FpfTriattnArgs c = *a;
   c.v_layout = 2;
   c.S = Sp;
-  c.q = sp.q2;
-  const int64_t qs5[5] = {N * H * Sp * TA_D, H * Sp * TA_D, Sp * TA_D, TA_D, 1};
   const int64_t vs5[5] = {N * H * TA_D * Sp, H * TA_D * Sp, TA_D * Sp, Sp, 1};
-  for (int t = 0; t < 5; ++t) {
-    c.q_stride[t] = qs5[t];
-    c.v_stride[t] = vs5[t];
-    if (!k_in_place) c.k_stride[t] = qs5[t];
-  }
-  if (!k_in_place) c.k = sp.k2;
+  for (int t = 0; t < 5; ++t) c.v_stride[t] = vs5[t];
   c.v = sp.v2;
   c.bias = sp.bias2;
   c.bias_dtype = FPF_DT_F32;
@@ -1031,7 +1031,7 @@ static int op_staged(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t 
       rc = keep_table_launch(a->mask, a->mask_dtype == FPF_DT_F32, a->mask_stride, B, N, Sp, S, keep, st, err, errlen, dry);
       if (rc) return rc;
     }
-    rc = core_launch(&c, st, err, errlen, dry, S);
+    rc = core_launch(&c, st, err, errlen, dry, S, a->scale * LOG2E);
     if (rc || !dry) return rc;
   }
   return FPF_OK;
@@ -1059,7 +1059,8 @@ extern "C" int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err,
   if ((a->v_layout == 0 || a->v_layout == 1) && a->workspace && op_staged_shape(a->dtype, a->D, a->S) &&
       a->workspace_bytes >= op_stage_layout(a->B, a->N, a->H, a->S).total && rows32_ok(a->q, a->q_stride) &&
       rows32_ok(a->k, a->k_stride) && rows32_ok(a->v, a->v_stride) && aligned16(a->out) && a->out_stride[3] == TA_D &&
-      ((a->out_stride[0] | a->out_stride[1] | a->out_stride[2]) & 7) == 0)
+      ((a->out_stride[0] | a->out_stride[1] | a->out_stride[2]) & 7) == 0 &&
+      op_in_place_fits(a))
     return op_staged(a, static_cast<hipStream_t>(stream), err, errlen);
   return core_launch(a, static_cast<hipStream_t>(stream), err, errlen);
 }

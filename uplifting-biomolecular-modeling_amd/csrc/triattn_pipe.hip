@@ -161,11 +161,14 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   }
 
   const int wc = wave & 3;
-  uint32_t koff, voff;
+  // koffL: the last tile's, whose key rows past Sqk re-read row Sqk - 1 (keys the keep table masks)
+  uint32_t koff, koffL, voff;
   {
     const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
     const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+    const int kl = (int)p.Sqk - 1 - TA_KT * (nT - 1);
     koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
+    koffL = (uint32_t)(((kk < kl ? kk : kl) * p.ks[3] + 8 * kc) * 2);
     voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
   }
   // row r's byte offset from row i0, tile T's from tile 0 (32-bit: host-checked)
@@ -181,11 +184,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     it.i0 = (int32_t)(rg * R);
     it.nrow = N - it.i0 < R ? N - it.i0 : R;
     it.q = (int32_t)(qt * (32 * NW) + wave * 32 + n);
-    const int64_t qs = it.q < S ? it.q : 0;                            // queries past S read query 0 (never stored)
-    uint64_t a[16] = {FPF_KARG(k),     FPF_KARG(v),     FPF_KARG(q),     FPF_KARG(bias),  FPF_KARG(ks[0]), FPF_KARG(ks[1]),
+    uint64_t a[17] = {FPF_KARG(k),     FPF_KARG(v),     FPF_KARG(q),     FPF_KARG(bias),  FPF_KARG(ks[0]), FPF_KARG(ks[1]),
                       FPF_KARG(ks[2]), FPF_KARG(vs[0]), FPF_KARG(vs[1]), FPF_KARG(vs[2]), FPF_KARG(qs[0]), FPF_KARG(qs[1]),
-                      FPF_KARG(qs[2]), FPF_KARG(qs[3]), FPF_KARG(bs[0]), FPF_KARG(bs[1])};
+                      FPF_KARG(qs[2]), FPF_KARG(qs[3]), FPF_KARG(bs[0]), FPF_KARG(bs[1]), FPF_KARG(Sqk)};
     karg_wait(a);
+    const int64_t qs = it.q < (int32_t)a[16] ? it.q : 0;               // queries past q's rows read query 0 (never stored)
     const int64_t b = it.b, h = it.h, i0 = it.i0;
     it.kb = reinterpret_cast<const uint16_t*>(a[0]) + b * (int64_t)a[4] + i0 * (int64_t)a[5] + h * (int64_t)a[6];
     it.vb = reinterpret_cast<const uint16_t*>(a[1]) + b * (int64_t)a[7] + i0 * (int64_t)a[8] + h * (int64_t)a[9];
@@ -214,7 +217,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (NW == 4 || !v_mover)
-        lds_dma16_s(koff, row_at(it.kb, it, r, krow) + kt / 2, kl0 + (uint32_t)(buf * R + r) * TILE_B);
+        lds_dma16_s(T == nT - 1 ? koffL : koff, row_at(it.kb, it, r, krow) + kt / 2, kl0 + (uint32_t)(buf * R + r) * TILE_B);
       if (NW == 4 || v_mover)
         lds_dma16_s(voff, row_at(it.vb, it, r, vrow) + vt / 2, vl0 + (uint32_t)(buf * R + r) * TILE_B);
     }
@@ -311,6 +314,18 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
     vm_wait<0>();
 #pragma unroll
     for (int r = 0; r < R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
+    {
+      uint64_t m[1] = {FPF_KARG(qmul)};
+      karg_wait(m);
+      const float qmul = __uint_as_float((uint32_t)m[0]);
+      if (qmul != 1.0f) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          qf[r][0] = scale_bf8(qf[r][0], qmul);
+          qf[r][1] = scale_bf8(qf[r][1], qmul);
+        }
+      }
+    }
     dead_any = false;
     all_full = true;
 #pragma unroll
@@ -532,7 +547,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   const int64_t b = bh / H, h = bh % H;
   const int64_t i0 = (int64_t)rg * TA_R;
   const int64_t q = (int64_t)qt * (32 * NW) + wave * 32 + n;
-  const bool qlive = q < p.Sv;
+  const bool qlive = q < p.Sv;                     // (Sv <= Sqk: a live query's row is in q)
 
   bf16x8 qf[TA_R][2];
 #pragma unroll
@@ -551,11 +566,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   const int wc = wave & 3;
   const uint16_t* kb[TA_R];
   const uint16_t* vb[TA_R];
-  uint32_t koff, voff;
+  uint32_t koff, koffL, voff;
   {
     const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
     const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+    const int64_t kl = p.Sqk - 1 - (p.S - TA_KT);   // the last tile's key rows past Sqk re-read row Sqk - 1 (masked keys)
     koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
+    koffL = (uint32_t)(((kk < kl ? kk : kl) * p.ks[3] + 8 * kc) * 2);
     voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
@@ -571,7 +588,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   auto dma_tile = [&](int64_t k0, int buf) {
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
-      if (NW == 4 || !v_mover) lds_dma16_s(koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
+      if (NW == 4 || !v_mover) lds_dma16_s(k0 + TA_KT == p.S ? koffL : koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
       if (NW == 4 || v_mover) lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
     }
   };
@@ -621,6 +638,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   vm_wait<0>();
 #pragma unroll
   for (int r = 0; r < TA_R; ++r) asm volatile("" : "+v"(qf[r][0]), "+v"(qf[r][1]));
+  if (p.qmul != 1.0f) {
+#pragma unroll
+    for (int r = 0; r < TA_R; ++r) {
+      qf[r][0] = as_bf8(scale_bf8(__builtin_bit_cast(u32x4, qf[r][0]), p.qmul));
+      qf[r][1] = as_bf8(scale_bf8(__builtin_bit_cast(u32x4, qf[r][1]), p.qmul));
+    }
+  }
   __syncthreads();
   bool dead[TA_R];
   bool dead_any = false;
@@ -762,41 +786,23 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 
 // ---------------------------------------------------------------------------------------------------------------- op staging
 // The op face (kernels/triattn/__init__.py:1094) hands q, k, v [B, N, H, S, 32] and a [B, 1, H, S, S] bias in its own layout; the
-// block-layout core wants them as the block's prologue writes them.  One wave per (b, n, h, 64-position tile): lane = position s
-// for q and k (a 64-byte row each, q scaled by scale * log2(e) in fp32 and rounded once), and for V the tile goes through the
-// wave's LDS rows so each lane stores 32 consecutive positions of one V^T row in the core's 16-block key order.
+// block-layout core reads q and k in place and wants V^T and the bias as the block's prologue writes them.  One wave per (b, n, h,
+// 64-position tile): the tile goes through the wave's LDS rows so each lane stores 32 consecutive positions of one V^T row in the
+// core's 16-block key order.
 __device__ __forceinline__ int vperm16(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }   // swaps bits 2 and 3
 
 constexpr int ST_VLD = 64 + 8;    // LDS pitch (bf16) of a staged V^T row: 144 B
 
-__global__ void __launch_bounds__(256) triattn_stage_qkv(const StageParams p) {
+__global__ void __launch_bounds__(256) triattn_stage_v(const StageParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sV[4][32 * ST_VLD];
   const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
   const int64_t tiles = p.Sp / 64, total = p.B * p.N * p.H * tiles;
   const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
   if (unit >= total) return;                                  // whole waves leave: only wave-level synchronisation below
   const int64_t tile = unit % tiles, bnh = unit / tiles, h = bnh % p.H, bn = bnh / p.H, n = bn % p.N, b = bn / p.N;
-  // the tile's 64 positions x 64 bytes as 256 16-byte chunks; load / store i moves chunk l + 64 i (position (l + 64 i) / 4, head-dim
-  // chunk l % 4), so each instruction touches 1 KB of consecutive q2 / k2 rows (and of the caller's rows when they are contiguous)
+  // the tile's 64 positions x 64 bytes as 256 16-byte chunks: load i moves chunk l + 64 i (position (l + 64 i) / 4, head-dim chunk
+  // l % 4), so each instruction reads 1 KB of the caller's rows when they are contiguous
   const int dc = l & 3;
-  uint16_t* q2 = p.q2 + (((b * p.N + n) * p.H + h) * p.Sp + tile * 64) * 32;
-  const uint16_t* qb = p.q + b * p.qs[0] + n * p.qs[1] + h * p.qs[2];
-  const uint16_t* kb = p.k + b * p.ks[0] + n * p.ks[1] + h * p.ks[2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int ps = (l >> 2) + 16 * i;
-    const int64_t s = tile * 64 + ps;
-    const bool live = s < p.S;
-    const u32x4 r = live ? *reinterpret_cast<const u32x4*>(qb + s * p.qs[3] + 8 * dc) : u32x4{0, 0, 0, 0};
-    u32x4 w;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) w[e] = pack2(lo_bf(r[e]) * p.qmul, hi_bf(r[e]) * p.qmul);
-    *reinterpret_cast<u32x4*>(q2 + ps * 32 + 8 * dc) = w;
-    if (p.k2) {
-      uint16_t* k2 = p.k2 + (((b * p.N + n) * p.H + h) * p.Sp + tile * 64) * 32;
-      *reinterpret_cast<u32x4*>(k2 + ps * 32 + 8 * dc) = live ? *reinterpret_cast<const u32x4*>(kb + s * p.ks[3] + 8 * dc) : u32x4{0, 0, 0, 0};
-    }
-  }
   uint16_t* sv = sV[wave];
   uint16_t* vdst = p.v2 + ((b * p.N + n) * p.H + h) * 32 * p.Sp + tile * 64;      // V^T row 0 of this tile
   const uint16_t* vb = p.v + b * p.vs[0] + n * p.vs[1] + h * p.vs[2];
@@ -895,6 +901,15 @@ int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64
 // others multiples of 8), scale 1, p.redo holding redo_words(B, N, H, S) words.  8 waves (256 queries)
 // share each K / V^T tile where S fills whole 256-query tiles and the grid still has 8 or more workgroups per CU; 4 waves (128
 // queries) elsewhere.  The fallback runs on the same stream right after the fast kernel, over the same grid.
+// The block-layout core's per-lane byte offsets from its scalar bases are 32-bit: q (query, d), K (key row of a tile, and the
+// tile's offset from tile 0), V^T (d row), and a row's from the item's first row.
+bool pipe_offsets_fit(int64_t S, const int64_t* qs, const int64_t* ks, const int64_t* vs) {
+  const int64_t lim = 0x7fffffffLL;
+  return qs[3] >= 0 && ks[3] >= 0 && vs[3] >= 0 && qs[1] >= 0 && ks[1] >= 0 && vs[1] >= 0 && S <= lim &&
+         (S - 1) * qs[3] * 2 + 64 <= lim && S * ks[3] * 2 <= lim && TA_D * vs[3] * 2 <= lim &&
+         (TA_R - 1) * std::max(qs[1], std::max(ks[1], vs[1])) * 2 <= lim;
+}
+
 int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry) {
   const int64_t rows_heads = p.B * p.H * cdiv(p.N, TA_R);
   // 8 waves share each K / V^T tile among 256 queries; where S is not a multiple of 256 the last query tile is partly padding.
@@ -906,12 +921,7 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   const bool wide = 19 * q8 * (32 * TA_DMA_WAVES) < 20 * q4 * 128 && rows_heads * q8 >= 8 * (int64_t)num_cus();
   const int64_t total = wide ? rows_heads * q8 : rows_heads * q4;
   if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
-  // per-lane byte offsets from the scalar bases are 32-bit: q (query, d), bias (query), K (key row of a tile), V^T (d row)
-  const int64_t lim = 0x7fffffffLL;
-  if (p.qs[3] < 0 || p.bs[2] < 0 || p.ks[3] < 0 || p.vs[3] < 0 || p.qs[1] < 0 || p.ks[1] < 0 || p.vs[1] < 0 ||
-      (p.S - 1) * p.qs[3] * 2 + 64 > lim || TA_KT * p.ks[3] * 2 > lim ||
-      TA_D * p.vs[3] * 2 > lim || (TA_R - 1) * std::max(p.qs[1], std::max(p.ks[1], p.vs[1])) * 2 > lim ||
-      p.B * p.N > lim || p.S > lim)
+  if (p.bs[2] < 0 || !pipe_offsets_fit(p.S, p.qs, p.ks, p.vs) || p.B * p.N > 0x7fffffffLL)
     return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
   if (p.Sv <= 0 || p.Sv > p.S || (p.Sv < p.S && !p.keep))
     return fail(err, errlen, FPF_E_ARGS, "v_layout 2: %lld real keys of %lld need a keep table masking the padding", (long long)p.Sv, (long long)p.S);
@@ -938,9 +948,9 @@ int op_stage_launch(const StageParams& p, hipStream_t st, char* err, size_t errl
   const int64_t u1 = p.B * p.N * p.H * (p.Sp / 64), u2 = p.B * p.H * (p.Sp / 32) * (p.Sp / 32);
   if (cdiv(u1, 4) > 0x7fffffffLL || cdiv(u2, 4) > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "staging: grid too large");
   if (dry) return FPF_OK;
-  hipLaunchKernelGGL(triattn_stage_qkv, dim3((unsigned)cdiv(u1, 4)), dim3(256), 0, st, p);
+  hipLaunchKernelGGL(triattn_stage_v, dim3((unsigned)cdiv(u1, 4)), dim3(256), 0, st, p);
   hipLaunchKernelGGL(triattn_stage_bias, dim3((unsigned)cdiv(u2, 4)), dim3(256), 0, st, p);
-  return launched(err, errlen, "triattn_stage_qkv / triattn_stage_bias");
+  return launched(err, errlen, "triattn_stage_v / triattn_stage_bias");
 }
 
 }  // namespace fpf

@@ -110,8 +110,8 @@ def triangle_attention(q, k, v, bias, mask=None, scale=None, *, word, prefer=Non
         raise Refusal("out", sel.row, F.ROW_STOCK, "out must be [B,N,H,S,D] in q's dtype with a contiguous head_dim")
     sc = (1.0 / math.sqrt(D)) if scale is None else float(scale)
     dt = L.DT_BF16 if q.dtype == torch.bfloat16 else L.DT_F32
-    # bf16 at head_dim 32: a workspace of the staging size routes the call onto the block-layout core (q, V^T, bias and mask
-    # restaged into its layout; the library keeps the op core when the strides do not allow it)
+    # bf16 at head_dim 32: a workspace of the staging size routes the call onto the block-layout core (V^T, bias and mask
+    # restaged into its layout, q and k read in place; the library keeps the op core when the strides do not allow it)
     stage = L.lib().fpf_triattn_stage_bytes(B, N, H, S, D, dt)
     ws = F.scratch(q.device, stage, kind="op") if stage else None
     a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=dt, B=B, N=N, H=H, S=S, D=D,
