@@ -77,6 +77,22 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z
     const int64_t b = tl.b, P = tl.r, Q = tl.c * 32 + n;
     const bool live = P < N && Q < N;
     const int64_t pix = (b * N + (outgoing ? P : Q)) * N + (outgoing ? Q : P);
+    const int64_t Q0 = Q - n, cpl = 32 * NCB;
+    uint16_t* oa = pa + tl_off_rc(b, 0, P, Q0, Np, Np, cpl) + 8 * g;
+    uint16_t* ob = pb + tl_off_rc(b, 0, P, Q0, Np, Np, cpl) + 8 * g;
+    if (P >= N || Q0 >= N) {             // wave-uniform: a tile of plane padding only, whose products are zero
+      if (!ZF32 && t + stride < total) fetch(t + stride);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const int64_t c = cb * 32 + n;
+        const u32x4 zero = {0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(oa + c * 32) = zero;
+        *reinterpret_cast<u32x4*>(oa + c * 32 + 16) = zero;
+        *reinterpret_cast<u32x4*>(ob + c * 32) = zero;
+        *reinterpret_cast<u32x4*>(ob + c * 32 + 16) = zero;
+      }
+      continue;
+    }
     const float m = live ? (mask ? mask[pix] : 1.0f) : 0.0f;
     const bool ones = __builtin_amdgcn_ballot_w64(m != 1.0f) == 0;   // every pixel of the tile kept: no mask products
     bf16x8 xb[8];
@@ -96,9 +112,6 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z
     }
     rt_wave_lds_sync();
     // channel blocks cb0 .. cb0 + NCB - 1 (32 channels each) into planes of 32 NCB channels (the whole op: 0 .. 3 into 128)
-    const int64_t Q0 = Q - n, cpl = 32 * NCB;
-    uint16_t* oa = pa + tl_off_rc(b, 0, P, Q0, Np, Np, cpl) + 8 * g;
-    uint16_t* ob = pb + tl_off_rc(b, 0, P, Q0, Np, Np, cpl) + 8 * g;
 #pragma unroll 1
     for (int cb = 0; cb < NCB; ++cb) {
       const uint16_t* const ws[4] = {sW, sW + 1 * RT_C * RT_LD, sW + 2 * RT_C * RT_LD, sW + 3 * RT_C * RT_LD};
@@ -166,8 +179,8 @@ __device__ __forceinline__ void cb_wait(int p, bool stores) {
 // channel cx0 + c of X).
 template <int CPL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t nbatch,
-                         int64_t La, int64_t a0, int64_t Ra, int cx0) {
+trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bm, uint16_t* __restrict__ X, int64_t Np, int64_t Nk,
+                         int64_t nbatch, int64_t La, int64_t a0, int64_t Ra, int cx0) {
   constexpr int64_t cpl = CPL;
   __shared__ __attribute__((aligned(16))) uint16_t sA[CB_NBUF][CB_T * CB_K];
   __shared__ __attribute__((aligned(16))) uint16_t sB[CB_NBUF][CB_T * CB_K];
@@ -177,7 +190,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
   const int64_t x0 = (blockIdx.x % 8) * per, first = x0 + blockIdx.x / 8, end = total < x0 + per ? total : x0 + per;
   if (first >= end) return;
   const int ntile = (int)((end - first + g8 - 1) / g8);       // tiles first, first + g8, ... below end
-  const int nk = (int)(Np / CB_K), U = ntile * nk;             // slabs per tile, slabs of this workgroup (host: U < 2^31)
+  const int nk = (int)(Nk / CB_K), U = ntile * nk;             // slabs per tile, slabs of this workgroup (host: U < 2^31)
   // the operand planes hold cpl channels (128: the whole op; the channels mode's block otherwise), batch index bc = b cpl + c;
   // X holds all 128, this call's channel c at cx0 + c
   constexpr int64_t orow = 32 * cpl;
@@ -286,7 +299,7 @@ trimul_contract_bf16_256(const uint16_t* __restrict__ A, const uint16_t* __restr
     const int u0 = r * nk;
     // the previous tile's stores were issued after this tile's slabs 0 .. CB_IF - 1: the waits for slabs 1 .. CB_IF - 1 (in slabs
     // 0 .. CB_IF - 2) count them
-    slab(stored, u0, f0a, f0b, f1a, f1b);                // nk is even: Np is a multiple of 128
+    slab(stored, u0, f0a, f0b, f1a, f1b);                // nk is even: Nk is a multiple of 64
     slab(stored, u0 + 1, f1a, f1b, f0a, f0b);
     for (int kt = 2; kt < nk; kt += 2) {
       slab(stored && kt <= CB_IF - 2, u0 + kt, f0a, f0b, f1a, f1b);
@@ -828,17 +841,21 @@ __global__ void __launch_bounds__(64 * FM_NW) trimul_k3_f32m(const float* zin, f
 }
 
 static int64_t padded(int64_t n) { return cdiv(n, TM_TILE) * TM_TILE; }
+// The contraction's depth: the pair axis rounded up to 64 (two 32-deep slabs per step of its loop); the planes are zero from N
+// to Np along it, so the slabs past the depth would add only zero products.
+static int64_t depth(int64_t n) { return cdiv(n, 64) * 64; }
 
 // The contraction of operand planes holding cpl channels (A rows a0 .. a0 + Ra - 1 of a plane of La rows, B whole) into X
 // (Ra rows, all 128 channels; these planes' channel c at cx0 + c): persistent, a multiple of 8 workgroups.
-static int contract_launch(hipStream_t st, const uint16_t* pa, const uint16_t* pb, uint16_t* X, int64_t Np, int64_t B, int cpl, int64_t La,
+static int contract_launch(hipStream_t st, const uint16_t* pa, const uint16_t* pb, uint16_t* X, int64_t Np, int64_t Nk, int64_t B, int cpl, int64_t La,
                            int64_t a0, int64_t Ra, int cx0, char* err, size_t errlen) {
   if (cpl != 32 && cpl != 64 && cpl != TM_C) return fail(err, errlen, FPF_E_ARGS, "operand planes of %d channels (32, 64 or 128)", cpl);
   const int64_t tiles = cdiv(Ra, CB_T) * cdiv(Np, CB_T) * B * cpl;
   const int64_t grid = std::min<int64_t>(cdiv(tiles, 8), std::max(num_cus() / 8, 1)) * 8;
-  if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Np / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
+  if (Nk <= 0 || Nk % 64 || Nk > Np) return fail(err, errlen, FPF_E_ARGS, "contraction depth %lld of a %lld plane", (long long)Nk, (long long)Np);
+  if ((cdiv(cdiv(tiles, 8), grid / 8) + 1) * (Nk / CB_K) >= (int64_t(1) << 31)) return fail(err, errlen, FPF_E_SHAPE, "contraction slab count above 2^31");
   auto kern = cpl == 32 ? trimul_contract_bf16_256<32> : cpl == 64 ? trimul_contract_bf16_256<64> : trimul_contract_bf16_256<TM_C>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, B * cpl, La, a0, Ra, cx0);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, st, pa, pb, X, Np, Nk, B * cpl, La, a0, Ra, cx0);
   return launched(err, errlen, "trimul_contract_bf16_256");
 }
 // The contraction tile: 256 at every n (a padded extent of an odd multiple of 128 ends with half-inside tiles).
@@ -856,7 +873,7 @@ static int bf16_rows(const FpfTrimulArgs* a, hipStream_t st, const uint16_t* pa,
   const int64_t a0 = row0 / T * T, Ra = std::min<int64_t>(cdiv(row0 + rows, T) * T, Np) - a0;
   const int64_t k3_tiles = B * rows * cdiv(N, 32);
   if (!rt_tiles_ok(k3_tiles)) return fail(err, errlen, FPF_E_SHAPE, "2^31 or more 32-pixel tiles");
-  int rc = contract_launch(st, pa, pb, X, Np, B, TM_C, Np, a0, Ra, 0, err, errlen);
+  int rc = contract_launch(st, pa, pb, X, Np, depth(N), B, TM_C, Np, a0, Ra, 0, err, errlen);
   if (rc) return rc;
   return k3_launch(a, st, X, row0, rows, a0, Ra, err, errlen);
 }
@@ -1054,7 +1071,7 @@ extern "C" int fpf_trimul_channels_fwd(const FpfTrimulArgs* a, int64_t chunk, vo
   for (int64_t c0 = 0; c0 < TM_C; c0 += cpl) {
     rc = bf16_planes(a, st, pa, pb, err, errlen, (int)(c0 / 32), (int)(cpl / 32));
     if (rc) return rc;
-    rc = contract_launch(st, pa, pb, X, Np, B, (int)cpl, Np, 0, Np, (int)c0, err, errlen);
+    rc = contract_launch(st, pa, pb, X, Np, depth(N), B, (int)cpl, Np, 0, Np, (int)c0, err, errlen);
     if (rc) return rc;
   }
   return k3_launch(a, st, X, 0, N, 0, Np, err, errlen);
