@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define FPF_ABI_VERSION 12  /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
+#define FPF_ABI_VERSION 13  /* 3: v_layout 2 logits in log2 units; fpf_apb_fwd, fpf_apb_bias_fwd; 4: block mask_frame;
                                5: gate / output projection biases b_g, b_o on the tri-att block and its stages;
                                6: the v_layout 2 core reads the mask as a keep-bit table and takes a workspace
                                   (FpfTriattnArgs.keep / workspace / workspace_bytes, fpf_triattn_workspace_bytes);
@@ -40,7 +40,9 @@ extern "C" {
                                11: x_ln (the caller's own LayerNorm output, ln="stock") appended to FpfTriattnBlockArgs,
                                    FpfTriattnPrologueArgs and FpfTransitionArgs;
                                12: the single track's pair bias projected from the transition's written rows (FpfTransitionArgs
-                                   w_z .. z_bias_ld) */
+                                   w_z .. z_bias_ld);
+                               13: v_layout 3 (the block-layout core reading V as key rows); the op face's staged route reads
+                                   q, k and v in place */
 
 enum { FPF_DT_BF16 = 1, FPF_DT_F32 = 2, FPF_DT_U8 = 3, FPF_DT_F32Z_BF16 = 4 };
 enum {
@@ -205,12 +207,14 @@ typedef struct {
   const void* v;
   int64_t q_stride[5];     /* [B, N, H, S, D] element strides; stride[4] must be 1 */
   int64_t k_stride[5];
-  int64_t v_stride[5];     /* v_layout 0: strides of [B, N, H, S, D]; v_layout 1 / 2: strides of [B, N, H, D, S] (V stored transposed) */
-  int32_t v_layout;        /* 0 | 1 | 2 (1, 2 bf16 only); the last stride must be 1.  2 is the fused block's internal layout: V^T
-                              with the keys of every 16-key block stored in the order 0-3, 8-11, 4-7, 12-15, q already multiplied
-                              by scale * log2(e) (scale must be 1), fp32 bias times log2(e) (logits in log2 units) in blocks (see
-                              bias), S a multiple of 64 up to 8192, out rows of 32 contiguous 16-byte aligned bf16 */
-  const void* bias;        /* [B, H, S, S] (the [B,1,H,S,S] operand without its unit axis).  v_layout 2: each (b, h) plane is
+  int64_t v_stride[5];     /* v_layout 0 / 3: strides of [B, N, H, S, D]; v_layout 1 / 2: strides of [B, N, H, D, S] (V stored
+                              transposed) */
+  int32_t v_layout;        /* 0 | 1 | 2 | 3 (1, 2, 3 bf16 only); the last stride must be 1.  2 is the fused block's internal layout:
+                              V^T with the keys of every 16-key block stored in the order 0-3, 8-11, 4-7, 12-15, q already
+                              multiplied by scale * log2(e) (scale must be 1), fp32 bias times log2(e) (logits in log2 units) in
+                              blocks (see bias), S a multiple of 64 up to 8192, out rows of 32 contiguous 16-byte aligned bf16.
+                              3 is the same core with V as plain key rows [B, N, H, S, D] (keys in order) */
+  const void* bias;        /* [B, H, S, S] (the [B,1,H,S,S] operand without its unit axis).  v_layout 2 / 3: each (b, h) plane is
                               S x S contiguous (bias_stride[2] = S, [3] = 1, 16-byte aligned) and holds 32 x 32 blocks (query
                               block qb, key block kb) at element 1024 (qb S / 32 + kb), each block as 4 pieces (keys 8j .. 8j + 7)
                               of 64 lanes (lane n + 32 g: query n, keys 8j + 4g .. 8j + 4g + 3) of 4 values */
@@ -222,21 +226,22 @@ typedef struct {
   void* out;
   int64_t out_stride[5];   /* stride[4] must be 1 */
   float scale;
-  const uint64_t* keep;    /* v_layout 2 only: the mask as a keep-bit table [B, N, S / 64 + 1] (per attention row: word 0 = flags,
+  const uint64_t* keep;    /* v_layout 2 / 3 only: the mask as a keep-bit table [B, N, S / 64 + 1] (per attention row: word 0 = flags,
                               bit 0 some key kept, bit 1 every key kept; word 1 + t = keep bits of keys 64 t .. 64 t + 63, all set
                               for a row with no kept key), or NULL with mask NULL (every key kept).  The fused block builds it from
-                              its pair mask in its workspace; v_layout 2 with a mask and no table is refused (FPF_E_ARGS).  Other
+                              its pair mask in its workspace; v_layout 2 / 3 with a mask and no table is refused (FPF_E_ARGS).  Other
                               layouts read `mask` and ignore this field. */
-  void* workspace;         /* v_layout 2: device memory of fpf_triattn_workspace_bytes(B, N, H, S, 2) bytes (per work item a flag the
-                              fast kernel writes and its fallback reads).  v_layout 0 / 1: NULL, or fpf_triattn_stage_bytes(B, N,
-                              H, S, D, dtype) bytes or more, which runs a bf16 call with head_dim 32 on the block-layout core (v,
-                              the bias and the mask restaged there, q and k read in place; q / k / v rows and out rows of 32
-                              contiguous 16-byte aligned bf16, out_stride[3] = 32, q / k offsets within a (b, h) plane below 2^31
-                              bytes); a call that does not meet those conditions runs the op core as without */
+  void* workspace;         /* v_layout 2 / 3: device memory of fpf_triattn_workspace_bytes(B, N, H, S, v_layout) bytes (per work item
+                              a flag the fast kernel writes and its fallback reads).  v_layout 0 / 1: NULL, or
+                              fpf_triattn_stage_bytes(B, N, H, S, D, dtype) bytes or more, which runs a bf16 call with head_dim 32
+                              on the block-layout core (the bias and the mask restaged there, v_layout 1's V^T too; q, k and
+                              v_layout 0's v read in place; q / k / v rows and out rows of 32 contiguous 16-byte aligned bf16,
+                              out_stride[3] = 32, q / k / v offsets within a (b, h) plane below 2^31 bytes); a call that does not
+                              meet those conditions runs the op core as without */
   size_t workspace_bytes;
 } FpfTriattnArgs;
 int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err, size_t errlen);
-/* Workspace of fpf_triattn_fwd for this layout (0 for v_layout 0 / 1). */
+/* Workspace of fpf_triattn_fwd for this layout (0 for v_layout 0 / 1; v_layout 2 and 3 take the same). */
 size_t fpf_triattn_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t S, int32_t v_layout);
 /* Staging workspace that puts a v_layout 0 / 1 call on the block-layout core: bf16, head_dim 32, S a multiple of 64 or at least
  * 128, up to 8192; 0 when the call's class has no staged route.  No counterpart in the reference (its op face routes S ranges

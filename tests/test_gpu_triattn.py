@@ -385,13 +385,14 @@ def _keep_table(mask, real=None):
 
 
 @pytest.mark.parametrize("N", [256, 768])
-@pytest.mark.parametrize("masked", [False, True])
-def test_block_layout_core_fallback_extreme_logits(N, masked):
+@pytest.mark.parametrize("masked,vrows", [(False, False), (True, False), (True, True)])
+def test_block_layout_core_fallback_extreme_logits(N, masked, vrows):
     """The block's own core layout (v_layout 2, logits in log2 units) with query tiles whose logits need a reference max other
     than 0: bias +150 on queries 64..127 (a partial row sum far above 2^64) and -120 on queries 192..255 (every logit of a
     query's first sub-tile below -32), next to ordinary query tiles.  The fast kernel flags the work items of the extreme
     tiles and the fallback recomputes them; every sampled row is held to the bf16 bars against a max-subtracted fp32 softmax.
-    N = 256 takes the 4-wave split, N = 768 the 8-wave one; `masked` adds a random keep pattern with dead rows (uniform mean)."""
+    N = 256 takes the 4-wave split, N = 768 the 8-wave one; `masked` adds a random keep pattern with dead rows (uniform mean);
+    `vrows` hands V as key rows (v_layout 3) instead of V^T in the core's key order (v_layout 2)."""
     import ctypes
     from fpf_hip import _lib as L
     H, D = 4, 32
@@ -412,21 +413,23 @@ def test_block_layout_core_fallback_extreme_logits(N, masked):
     out = torch.full((1, N, H, N, D), float("nan"), dtype=torch.bfloat16, device=DEV)
     ws = torch.empty(max(1, L.lib().fpf_triattn_workspace_bytes(1, N, H, N, 2)), dtype=torch.uint8, device=DEV)
     bias_blk = _bias_blocks(bias)
-    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=1, N=N, H=H, S=N, D=D, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vt), v_layout=2,
-                      bias=L.ptr(bias_blk), bias_dtype=L.DT_F32, mask=L.ptr(mask), mask_dtype=L.DT_F32, out=L.ptr(out), scale=1.0,
-                      keep=None if keep is None else ctypes.c_void_p(keep.data_ptr()), workspace=L.ptr(ws), workspace_bytes=ws.numel())
+    idx = torch.tensor([16 * (kk // 16) + _VPERM.index(kk % 16) for kk in range(N)], device=DEV)
+    vin = vt[..., idx].transpose(-1, -2).contiguous() if vrows else vt           # key rows [1, N, H, key, D]
+    a = L.TriattnArgs(abi_version=L.ABI_VERSION, dtype=L.DT_BF16, B=1, N=N, H=H, S=N, D=D, q=L.ptr(q), k=L.ptr(k), v=L.ptr(vin),
+                      v_layout=3 if vrows else 2, bias=L.ptr(bias_blk), bias_dtype=L.DT_F32, mask=L.ptr(mask), mask_dtype=L.DT_F32,
+                      out=L.ptr(out), scale=1.0, keep=None if keep is None else ctypes.c_void_p(keep.data_ptr()),
+                      workspace=L.ptr(ws), workspace_bytes=ws.numel())
     a.q_stride[:] = q.stride()
     a.k_stride[:] = k.stride()
-    a.v_stride[:] = vt.stride()
+    a.v_stride[:] = vin.stride()
     a.out_stride[:] = out.stride()
     a.bias_stride[:] = bias_blk.stride()
     if masked:
         a.mask_stride[:] = mask.stride()
-    print("[fallback] N=%d masked=%s" % (N, masked), flush=True)
+    print("[fallback] N=%d masked=%s vrows=%s" % (N, masked, vrows), flush=True)
     L.call("fpf_triattn_fwd", a, L.stream_ptr(DEV))
     torch.cuda.synchronize()
     rows = sorted(set([0, 1, 2, 5, 6, 7, 8, 9, N // 2, N // 2 + 1, N - 2, N - 1]))
-    idx = torch.tensor([16 * (kk // 16) + _VPERM.index(kk % 16) for kk in range(N)], device=DEV)
     Vl = vt[0, rows].float()[..., idx].transpose(-1, -2)                   # [rows, H, key, D]
     s = torch.einsum("ihqd,ihkd->ihqk", q[0, rows].float(), k[0, rows].float()) + bias[0].unsqueeze(0)
     if masked:
@@ -438,18 +441,19 @@ def test_block_layout_core_fallback_extreme_logits(N, masked):
     ref = torch.einsum("ihqk,ihkd->ihqd", p / p.sum(-1, keepdim=True), Vl)
     got = out[0, rows].float()
     assert torch.isfinite(got).all(), "non-finite output"
-    assert_bf16_close(got, ref, "block-layout core N=%d masked=%s, extreme query tiles" % (N, masked))
+    assert_bf16_close(got, ref, "block-layout core N=%d masked=%s vrows=%s, extreme query tiles" % (N, masked, vrows))
 
 
 @pytest.mark.parametrize("S_,layout,N", [(456, "contig", 7), (800, "contig", 7), (768, "endstrided", 7), (130, "endstrided", 7),
                                          (720, "contig", 512)])
 def test_op_face_in_place_route_equals_the_block_core_on_restaged_operands(S_, layout, N):
-    """The op face's route onto the block-layout core reads q and k in place -- q times scale * log2(e) in registers, the
-    padding keys of the last tile re-reading the last real key row under the keep table's mask -- and restages only V^T and the
-    bias.  Its output equals, bit for bit, the block-layout core (v_layout 2) given every operand restaged on the host:
+    """The op face's route onto the block-layout core reads q, k and v in place -- q times scale * log2(e) in registers, V's
+    key rows through LDS transpose reads, the padding keys of the last tile re-reading the last real key row under the keep
+    table's mask -- and restages only the bias.  Its output equals, bit for bit, the block-layout core with V^T in its key
+    order (v_layout 2) given every operand restaged on the host:
     q2 = bf16(q * fp32(scale * log2(e))), k and V^T padded with zeros to Sp = S rounded up to 64 (V^T in the 16-block key
     order), the bias times log2(e) in register-order blocks, the keep table with the padding keys masked.  A random mask with a
-    dead row; `endstrided`: q and k as transposed views of [B, S, H, N, D] storage (the ending node's layout).  N = 7 runs the
+    dead row; `endstrided`: q, k and v as transposed views of [B, S, H, N, D] storage (the ending node's layout).  N = 7 runs the
     4-wave split, N = 512 at S = 720 (padded to 768) the 8-wave one."""
     import ctypes
     from fpf_hip import _lib as L
@@ -461,11 +465,11 @@ def test_op_face_in_place_route_equals_the_block_core_on_restaged_operands(S_, l
     mask = torch.rand(B, N, 1, 1, S_, generator=g) > 0.2
     mask[0, 3] = False
     if layout == "endstrided":
-        qd, kd = (t.transpose(1, 3).contiguous().to(DEV).transpose(1, 3) for t in (q, k))
+        qd, kd, vd = (t.transpose(1, 3).contiguous().to(DEV).transpose(1, 3) for t in (q, k, v))
     else:
-        qd, kd = q.to(DEV), k.to(DEV)
+        qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     print("[op in place] S=%d %s N=%d" % (S_, layout, N), flush=True)
-    got = TA.triangle_attention(qd, kd, v.to(DEV), bias.to(DEV), mask.to(DEV), word="fast")
+    got = TA.triangle_attention(qd, kd, vd, bias.to(DEV), mask.to(DEV), word="fast")
     # every operand restaged on the host, for the core's own layout
     qmul = float(np.float32(np.float32(1.0 / np.sqrt(D)) * np.float32(1.4426950408889634)))
     q2 = torch.zeros(B, N, H, Sp, D, dtype=torch.bfloat16)

@@ -41,6 +41,8 @@ struct CoreParams {
                                  // table masks)
   float qmul;                    // block-layout core: the factor q is multiplied by in registers, each product rounded to bf16
                                  // once (1: q comes already multiplied)
+  int v_rows;                    // block-layout core: V as key rows [b, n, h, key, d] (vs its strides; the last tile's rows past
+                                 // Sqk re-read row Sqk - 1, like K), else V^T [b, n, h, d, key] with keys in the 16-block order
 };
 
 __device__ __forceinline__ bool mask_keep(const CoreParams& p, int64_t b, int64_t i, int64_t key) {
@@ -60,6 +62,27 @@ __device__ __forceinline__ u32x4 scale_bf8(const u32x4& x, float m) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) w[e] = pack2(lo_bf(x[e]) * m, hi_bf(x[e]) * m);
   return w;
+}
+
+// V of the block-layout core as key rows (v_rows): a 64-key tile in LDS holds key k's 32 values as four 16-byte chunks, chunk c
+// at position c ^ ((k >> 2) & 3), as the K tile does.  The P.V product's A operand -- lane (n, g): d = n and the keys
+// kb + 4 g + 0..3, kb + 8 + 4 g + 0..3 of a 16-key step -- comes from two ds_read_b64_tr_b16: within each group of 16 lanes,
+// lane 4 e + q reads 4 values (d0 + 4 q .. + 3) of key row k0 + e, and lane j receives the values of d0 + j in rows
+// k0 .. k0 + 3.  vrows_off: lane l's byte offset in a tile for the read at key base 0 (S2 = 0) or 8 (S2 = 2) of a step.
+__device__ __forceinline__ uint32_t vrows_off(int l, int S2) {
+  const int h16 = l >> 4, il = l & 15, e = il >> 2, q = il & 3, g = h16 >> 1;
+  const int c = 2 * (h16 & 1) + (q >> 1);
+  return (uint32_t)((4 * g + e) * 64 + (c ^ (g + S2)) * 16 + (q & 1) * 8);
+}
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+// the A-operand fragment of the 16-key step starting at key kb (a multiple of 16) of a V-rows tile
+__device__ __forceinline__ u32x4 vrows_frag(const uint16_t* tile, int kb, uint32_t vo0, uint32_t vo2) {
+  typedef __attribute__((address_space(3))) v4i16_t lds_v4;
+  char* t = const_cast<char*>(reinterpret_cast<const char*>(tile));
+  const v4i16_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(t + kb * 64 + vo0));
+  const v4i16_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4*)(t + (kb + 8) * 64 + vo2));
+  const u32x2 a2 = __builtin_bit_cast(u32x2, a), b2 = __builtin_bit_cast(u32x2, b);
+  return u32x4{a2[0], a2[1], b2[0], b2[1]};
 }
 
 // Bias plane of the block-layout core (v_layout 2): S x S fp32 (query q, key k) in 32 x 32 blocks, block (q / 32, k / 32) at
@@ -166,7 +189,7 @@ inline int64_t redo_words(int64_t B, int64_t N, int64_t H, int64_t S) {
 // mask NULL: every real key kept (a table that only masks the padding keys Sv .. S - 1)
 int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64_t B, int64_t N, int64_t S, int64_t Sv, uint64_t* keep,
                       hipStream_t st, char* err, size_t errlen, bool dry = false);
-bool pipe_offsets_fit(int64_t S, const int64_t* qs, const int64_t* ks, const int64_t* vs);
+bool pipe_offsets_fit(int64_t S, const int64_t* qs, const int64_t* ks, const int64_t* vs, bool v_rows);
 int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errlen, bool dry = false);
 
 // N a multiple of 64, or any N from 128, up to 8192: the J axis of q / k / V^T / o and of the bias planes is padded to Np = N
@@ -181,8 +204,9 @@ inline int64_t block_np(int dtype, int64_t N) { return block_layout2(dtype, N) ?
 // The op face's V and bias restaged into the block-layout core's layout (triattn_pipe.hip): v2 = V^T [B, N, H, 32, Sp] with each
 // 16-key block in the order 0-3, 8-11, 4-7, 12-15, bias2 = bias * log2(e) as [B, H, Sp, Sp] in 32 x 32 register-order blocks
 // (bias_blk_off), Sp = S rounded up to 64, every padding element zero (q and k the core reads in place).  v is read as
-// [B, N, H, S, 32] (v_t = 0) or transposed as [B, N, H, 32, S] (v_t = 1).  The caller has checked: head_dim rows of 32
-// contiguous, 16-byte aligned bf16 (strides multiples of 8 elements).
+// [B, N, H, S, 32] (v_t = 0) or transposed as [B, N, H, 32, S] (v_t = 1); v2 NULL: V is not copied (the core reads its key
+// rows in place).  The caller has checked: head_dim rows of 32 contiguous, 16-byte aligned bf16 (strides multiples of 8
+// elements).
 struct StageParams {
   const uint16_t* v;
   int64_t vs[4];                 // strides of b, n, h, s (v_t = 1: of b, n, h, d)

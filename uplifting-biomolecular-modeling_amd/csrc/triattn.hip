@@ -883,7 +883,8 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     p.qmul = qmul > 0.f ? qmul : 1.0f;
     p.Sqk = qmul > 0.f ? p.Sv : a->S;
     p.v_t = a->v_layout;
-    if (!(p.v_t == 0 || p.v_t == 1 || p.v_t == 2)) return fail(err, errlen, FPF_E_ARGS, "v_layout %d", a->v_layout);
+    if (!(p.v_t >= 0 && p.v_t <= 3)) return fail(err, errlen, FPF_E_ARGS, "v_layout %d", a->v_layout);
+    p.v_rows = p.v_t == 3;
     for (int t = 0; t < 4; ++t)
       if ((p.qs[t] | p.ks[t] | p.vs[t]) & 7) return fail(err, errlen, FPF_E_ALIGN, "bf16 core: q / k / v strides must be multiples of 8 elements");
     for (int t = 0; t < 4; ++t)
@@ -894,7 +895,8 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     const int64_t total = a->B * a->H * cdiv(a->N, TA_R) * cdiv(a->S, 128);
     if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
     const dim3 grid((unsigned)(cdiv(total, 8) * 8)), block(256);
-    if (p.v_t == 2) {                  // the block layout (V^T keys permuted in 16-blocks, q times the scale): the DMA-staged core
+    if (p.v_t >= 2) {                  // the block layout (q times the scale; V^T keys permuted in 16-blocks, or V as key rows):
+                                       // the DMA-staged core
       if (!p.bias_vec || p.S % TA_KT != 0 || p.S > 64 * TA_MAXW || p.vs[3] % 8 != 0)
         return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
       if (p.bs[2] != p.S || p.bs[3] != 1)
@@ -961,11 +963,11 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
 }
 
 // The op face on the block-layout core: a bf16 call with head_dim 32 and S the block core serves (a multiple of 64, or at
-// least 128, up to 8192), given a workspace of fpf_triattn_stage_bytes, has V^T and the bias restaged (op_stage_launch: V^T in
-// the core's key order, the bias times log2(e) in blocks, both padded to Sp = S rounded up to 64), its mask (and the padding)
-// becomes a keep table, and the persistent core reads the caller's q and k in place -- q multiplied by scale * log2(e) in
-// registers, the padding keys re-reading the last real key row, masked -- and writes the caller's out directly.
-// Workspace regions: v2 (B N H 32 Sp bf16) | bias2 (B H Sp^2 fp32) | keep | redo.
+// least 128, up to 8192), given a workspace of fpf_triattn_stage_bytes, has the bias restaged (op_stage_launch: times log2(e)
+// in blocks, padded to Sp = S rounded up to 64), its mask (and the padding) becomes a keep table, and the persistent core
+// reads the caller's q, k and v in place -- q multiplied by scale * log2(e) in registers, the padding keys re-reading the last
+// real key row, masked -- and writes the caller's out directly.  V given transposed (v_layout 1) is restaged as V^T in the
+// core's key order.  Workspace regions: v2 (B N H 32 Sp bf16, V^T only) | bias2 (B H Sp^2 fp32) | keep | redo.
 struct OpStage {
   size_t bias2, keep, redo, total;
 };
@@ -984,14 +986,16 @@ static bool rows32_ok(const void* p, const int64_t* st4) {     // rows of 32 con
 // the caller's q and k strides (and the staged V^T's) within the block-layout core's 32-bit in-item offsets
 static bool op_in_place_fits(const FpfTriattnArgs* a) {
   const int64_t Sp = block_np(FPF_DT_BF16, a->S);
+  if (a->v_layout == 0) return pipe_offsets_fit(Sp, a->q_stride, a->k_stride, a->v_stride, true);
   const int64_t vs5[5] = {a->N * a->H * TA_D * Sp, a->H * TA_D * Sp, TA_D * Sp, Sp, 1};
-  return pipe_offsets_fit(Sp, a->q_stride, a->k_stride, vs5);
+  return pipe_offsets_fit(Sp, a->q_stride, a->k_stride, vs5, false);
 }
 
 static int op_staged(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen) {
   const int64_t B = a->B, N = a->N, H = a->H, S = a->S, Sp = block_np(FPF_DT_BF16, S);
   const OpStage L = op_stage_layout(B, N, H, S);
   char* w = static_cast<char*>(a->workspace);
+  const bool v_rows = a->v_layout == 0;            // V as key rows, read in place (V^T: restaged)
   StageParams sp{};
   sp.v = (const uint16_t*)a->v;
   for (int t = 0; t < 4; ++t) sp.vs[t] = a->v_stride[t];
@@ -999,7 +1003,7 @@ static int op_staged(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t 
   sp.bias = a->bias;
   sp.bias_bf16 = a->bias_dtype == FPF_DT_BF16;
   for (int t = 0; t < 3; ++t) sp.bs[t] = a->bias_stride[t];
-  sp.v2 = reinterpret_cast<uint16_t*>(w);
+  sp.v2 = v_rows ? nullptr : reinterpret_cast<uint16_t*>(w);
   sp.bias2 = reinterpret_cast<float*>(w + L.bias2);
   sp.B = B;
   sp.N = N;
@@ -1008,11 +1012,13 @@ static int op_staged(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t 
   sp.Sp = Sp;
   uint64_t* keep = reinterpret_cast<uint64_t*>(w + L.keep);
   FpfTriattnArgs c = *a;
-  c.v_layout = 2;
+  c.v_layout = v_rows ? 3 : 2;
   c.S = Sp;
-  const int64_t vs5[5] = {N * H * TA_D * Sp, H * TA_D * Sp, TA_D * Sp, Sp, 1};
-  for (int t = 0; t < 5; ++t) c.v_stride[t] = vs5[t];
-  c.v = sp.v2;
+  if (!v_rows) {
+    const int64_t vs5[5] = {N * H * TA_D * Sp, H * TA_D * Sp, TA_D * Sp, Sp, 1};
+    for (int t = 0; t < 5; ++t) c.v_stride[t] = vs5[t];
+    c.v = sp.v2;
+  }
   c.bias = sp.bias2;
   c.bias_dtype = FPF_DT_F32;
   c.bias_stride[0] = H * Sp * Sp;
@@ -1066,7 +1072,7 @@ extern "C" int fpf_triattn_fwd(const FpfTriattnArgs* a, void* stream, char* err,
 }
 
 extern "C" size_t fpf_triattn_workspace_bytes(int64_t B, int64_t N, int64_t H, int64_t S, int32_t v_layout) {
-  if (v_layout != 2 || B <= 0 || N <= 0 || H <= 0 || S <= 0) return 0;
+  if ((v_layout != 2 && v_layout != 3) || B <= 0 || N <= 0 || H <= 0 || S <= 0) return 0;
   return (size_t)fpf::redo_words(B, N, H, S) * 4;
 }
 

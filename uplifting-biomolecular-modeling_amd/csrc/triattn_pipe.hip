@@ -136,7 +136,7 @@ struct PipeItem {
 // item's q is loaded during the item's second-to-last tile, and an item's output leaves through LDS as contiguous 16-byte
 // stores that drain while the next item computes.
 // MASKED: the call has a keep table (without one every key is kept and the kernel carries no mask code).
-template <int NW, bool MASKED>
+template <int NW, bool MASKED, bool VROWS>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_pipe(const CoreParams p) {
   constexpr int R = TA_R;
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][R][TA_KT * TA_D];
@@ -161,19 +161,25 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   }
 
   const int wc = wave & 3;
-  // koffL: the last tile's, whose key rows past Sqk re-read row Sqk - 1 (keys the keep table masks)
-  uint32_t koff, koffL, voff;
+  // koffL: the last tile's, whose key rows past Sqk re-read row Sqk - 1 (keys the keep table masks); V as key rows moves
+  // like K (voffL the same for its last tile), V^T by rows of d
+  uint32_t koff, koffL, voff, voffL;
   {
     const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
-    const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
     const int kl = (int)p.Sqk - 1 - TA_KT * (nT - 1);
     koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
     koffL = (uint32_t)(((kk < kl ? kk : kl) * p.ks[3] + 8 * kc) * 2);
-    voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
+    if constexpr (VROWS) {
+      voff = (uint32_t)((kk * p.vs[3] + 8 * kc) * 2);
+      voffL = (uint32_t)(((kk < kl ? kk : kl) * p.vs[3] + 8 * kc) * 2);
+    } else {
+      const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+      voff = voffL = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
+    }
   }
   // row r's byte offset from row i0, tile T's from tile 0 (32-bit: host-checked)
   const uint32_t krow = (uint32_t)(p.ks[1] * 2), vrow = (uint32_t)(p.vs[1] * 2), qrow = (uint32_t)(p.qs[1] * 2);
-  const uint32_t ktile = (uint32_t)(TA_KT * p.ks[3] * 2);
+  const uint32_t ktile = (uint32_t)(TA_KT * p.ks[3] * 2), vtile = (uint32_t)(VROWS ? TA_KT * p.vs[3] * 2 : TA_KT * 2);
   auto row_at = [](const uint16_t* base, const PipeItem& it, int r, uint32_t stride) {
     return reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) + (r < it.nrow ? r * stride : 0u));
   };
@@ -213,13 +219,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   constexpr uint32_t TILE_B = TA_KT * TA_D * 2;
   const bool v_mover = NW > 4 && wave >= 4;
   auto dma_tile = [&](const PipeItem& it, int T, int buf) {
-    const uint32_t kt = (uint32_t)T * ktile, vt = (uint32_t)T * (TA_KT * 2);
+    const uint32_t kt = (uint32_t)T * ktile, vt = (uint32_t)T * vtile;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (NW == 4 || !v_mover)
         lds_dma16_s(T == nT - 1 ? koffL : koff, row_at(it.kb, it, r, krow) + kt / 2, kl0 + (uint32_t)(buf * R + r) * TILE_B);
       if (NW == 4 || v_mover)
-        lds_dma16_s(voff, row_at(it.vb, it, r, vrow) + vt / 2, vl0 + (uint32_t)(buf * R + r) * TILE_B);
+        lds_dma16_s(VROWS && T == nT - 1 ? voffL : voff, row_at(it.vb, it, r, vrow) + vt / 2, vl0 + (uint32_t)(buf * R + r) * TILE_B);
     }
   };
   // The wait counts below (vm_wait4<0>, vm_wait4<DMA_OPS>) assume exactly DMA_OPS operations per dma_tile and 4 per
@@ -291,10 +297,17 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   // MFMA fragments of a step, read from LDS one step ahead: V^T of (row, sub-tile vsub of buffer vbuf), K of (row, sub-tile
   // ksub of buffer kbuf)
   u32x4 fv0, fv1, fk0, fk1;
+  const uint32_t vo0 = VROWS ? vrows_off(l, 0) : 0u, vo2 = VROWS ? vrows_off(l, 2) : 0u;
   auto frags = [&](int vbuf, int vsub, int kbuf, int ksub, int row) {
-    const uint16_t* vt = &sV[vbuf][row][n * TA_KT];
-    fv0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * vsub + g) ^ vsw));
-    fv1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * vsub + 2 + g) ^ vsw));
+    if constexpr (VROWS) {
+      const uint16_t* vt = &sV[vbuf][row][0];
+      fv0 = vrows_frag(vt, 32 * vsub, vo0, vo2);
+      fv1 = vrows_frag(vt, 32 * vsub + 16, vo0, vo2);
+    } else {
+      const uint16_t* vt = &sV[vbuf][row][n * TA_KT];
+      fv0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * vsub + g) ^ vsw));
+      fv1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * vsub + 2 + g) ^ vsw));
+    }
     const uint16_t* kt = &sK[kbuf][row][32 * ksub * TA_D];
     fk0 = *reinterpret_cast<const u32x4*>(kt + kfo0);
     fk1 = *reinterpret_cast<const u32x4*>(kt + kfo1);
@@ -516,7 +529,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 // query's max for the others.  One step per (row, 32-key sub-tile), the keep bits built in LDS from the mask, K / V^T
 // tiles by DMA through the same three-buffer ring.  A workgroup reads the flags of 64 of its items at a time and skips
 // the unflagged ones.
-template <int NW>
+template <int NW, bool VROWS>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2))) triattn_core_bf16_redo(const CoreParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[TA_NB][TA_R][TA_KT * TA_D];
   __shared__ __attribute__((aligned(16))) uint16_t sV[TA_NB][TA_R][TA_D * TA_KT];
@@ -560,20 +573,25 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   }
 
 
-  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V^T tile (rows 8c .. 8c + 7) is moved by wave
-  // c (4 waves: both) or by waves c (K) and 4 + c (V^T) (8 waves); rows past N read row i0 (never stored).  Row bases are
-  // scalar, the in-tile byte offsets per lane are fixed.
+  // DMA: chunk block c (1 KB) of each row's K tile (keys 16c .. 16c + 15) and V tile (V rows: keys 16c .. 16c + 15 as for K;
+  // V^T: rows 8c .. 8c + 7) is moved by wave c (4 waves: both) or by waves c (K) and 4 + c (V) (8 waves); rows past N read row
+  // i0 (never stored).  Row bases are scalar, the in-tile byte offsets per lane are fixed.
   const int wc = wave & 3;
   const uint16_t* kb[TA_R];
   const uint16_t* vb[TA_R];
-  uint32_t koff, koffL, voff;
+  uint32_t koff, koffL, voff, voffL;
   {
     const int kk = 16 * wc + (l >> 2), kc = (l & 3) ^ ((kk >> 2) & 3);
-    const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
     const int64_t kl = p.Sqk - 1 - (p.S - TA_KT);   // the last tile's key rows past Sqk re-read row Sqk - 1 (masked keys)
     koff = (uint32_t)((kk * p.ks[3] + 8 * kc) * 2);
     koffL = (uint32_t)(((kk < kl ? kk : kl) * p.ks[3] + 8 * kc) * 2);
-    voff = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
+    if constexpr (VROWS) {
+      voff = (uint32_t)((kk * p.vs[3] + 8 * kc) * 2);
+      voffL = (uint32_t)(((kk < kl ? kk : kl) * p.vs[3] + 8 * kc) * 2);
+    } else {
+      const int vd = 8 * wc + (l >> 3), vc = (l & 7) ^ ((vd >> 1) & 7);
+      voff = voffL = (uint32_t)((vd * p.vs[3] + 8 * vc) * 2);
+    }
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
       const int64_t ii = i0 + r < p.N ? i0 + r : i0;
@@ -589,7 +607,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int r = 0; r < TA_R; ++r) {
       if (NW == 4 || !v_mover) lds_dma16_s(k0 + TA_KT == p.S ? koffL : koff, kb[r] + k0 * p.ks[3], kl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
-      if (NW == 4 || v_mover) lds_dma16_s(voff, vb[r] + k0, vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
+      if (NW == 4 || v_mover)
+        lds_dma16_s(k0 + TA_KT == p.S ? voffL : voff, vb[r] + (VROWS ? k0 * p.vs[3] : k0), vl0 + (uint32_t)(buf * TA_R + r) * TILE_B);
     }
   };
   // The wait counts (vm_wait4<DMA_OPS + 4>, vm_wait4<4>) assume exactly DMA_OPS operations per dma_tile and 4 per
@@ -614,6 +633,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
   const int kfo0 = n * TA_D + 8 * ((g) ^ ((n >> 2) & 3));            // key n, chunk g (k-step 0); sub-tile adds 32 keys
   const int kfo1 = n * TA_D + 8 * ((g + 2) ^ ((n >> 2) & 3));        // chunk g + 2 (k-step 1)
   const int vsw = (n >> 1) & 7;
+  const uint32_t vo0 = VROWS ? vrows_off(l, 0) : 0u, vo2 = VROWS ? vrows_off(l, 2) : 0u;
   auto qk = [&](const u32x4& k0f, const u32x4& k1f, int r, const f32x4 (&bb)[4]) {
     f32x16 bc;
 #pragma unroll
@@ -717,9 +737,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
         for (int r = 0; r < TA_R; ++r) {
           // fragment reads first: V^T of this step, K of the row's next S^T
-          const uint16_t* vt = &sV[bt][r][n * TA_KT];
-          const u32x4 vf0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + g) ^ vsw));
-          const u32x4 vf1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + 2 + g) ^ vsw));
+          u32x4 vf0, vf1;
+          if constexpr (VROWS) {
+            vf0 = vrows_frag(&sV[bt][r][0], 32 * sub, vo0, vo2);
+            vf1 = vrows_frag(&sV[bt][r][0], 32 * sub + 16, vo0, vo2);
+          } else {
+            const uint16_t* vt = &sV[bt][r][n * TA_KT];
+            vf0 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + g) ^ vsw));
+            vf1 = *reinterpret_cast<const u32x4*>(vt + 8 * ((4 * sub + 2 + g) ^ vsw));
+          }
           const uint16_t* kt = knext + r * (TA_KT * TA_D);
           u32x4 kf0 = u32x4{0, 0, 0, 0}, kf1 = u32x4{0, 0, 0, 0};
           if (next) {
@@ -903,10 +929,10 @@ int keep_table_launch(const void* mask, int mask_f32, const int64_t ms[3], int64
 // queries) elsewhere.  The fallback runs on the same stream right after the fast kernel, over the same grid.
 // The block-layout core's per-lane byte offsets from its scalar bases are 32-bit: q (query, d), K (key row of a tile, and the
 // tile's offset from tile 0), V^T (d row), and a row's from the item's first row.
-bool pipe_offsets_fit(int64_t S, const int64_t* qs, const int64_t* ks, const int64_t* vs) {
+bool pipe_offsets_fit(int64_t S, const int64_t* qs, const int64_t* ks, const int64_t* vs, bool v_rows) {
   const int64_t lim = 0x7fffffffLL;
   return qs[3] >= 0 && ks[3] >= 0 && vs[3] >= 0 && qs[1] >= 0 && ks[1] >= 0 && vs[1] >= 0 && S <= lim &&
-         (S - 1) * qs[3] * 2 + 64 <= lim && S * ks[3] * 2 <= lim && TA_D * vs[3] * 2 <= lim &&
+         (S - 1) * qs[3] * 2 + 64 <= lim && S * ks[3] * 2 <= lim && (v_rows ? S : TA_D) * vs[3] * 2 <= lim &&
          (TA_R - 1) * std::max(qs[1], std::max(ks[1], vs[1])) * 2 <= lim;
 }
 
@@ -921,7 +947,7 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   const bool wide = 19 * q8 * (32 * TA_DMA_WAVES) < 20 * q4 * 128 && rows_heads * q8 >= 8 * (int64_t)num_cus();
   const int64_t total = wide ? rows_heads * q8 : rows_heads * q4;
   if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
-  if (p.bs[2] < 0 || !pipe_offsets_fit(p.S, p.qs, p.ks, p.vs) || p.B * p.N > 0x7fffffffLL)
+  if (p.bs[2] < 0 || !pipe_offsets_fit(p.S, p.qs, p.ks, p.vs, p.v_rows != 0) || p.B * p.N > 0x7fffffffLL)
     return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
   if (p.Sv <= 0 || p.Sv > p.S || (p.Sv < p.S && !p.keep))
     return fail(err, errlen, FPF_E_ARGS, "v_layout 2: %lld real keys of %lld need a keep table masking the padding", (long long)p.Sv, (long long)p.S);
@@ -931,14 +957,24 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   // than 8 items some of them have none to do); the fallback scans its share of the flags
   const dim3 grid((unsigned)std::max<int64_t>(8, std::min<int64_t>(total, (wide ? 1 : 2) * (int64_t)num_cus())));
   const dim3 redo_grid((unsigned)std::min<int64_t>(total, num_cus()));
-  if (wide) {
-    if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, true>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
-    else hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, false>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
-    hipLaunchKernelGGL(triattn_core_bf16_redo<TA_DMA_WAVES>, redo_grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+  if (p.v_rows) {
+    if (wide) {
+      if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, true, true>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+      else hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, false, true>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+      hipLaunchKernelGGL((triattn_core_bf16_redo<TA_DMA_WAVES, true>), redo_grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+    } else {
+      if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<4, true, true>), grid, dim3(256), 0, st, p);
+      else hipLaunchKernelGGL((triattn_core_bf16_pipe<4, false, true>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((triattn_core_bf16_redo<4, true>), redo_grid, dim3(256), 0, st, p);
+    }
+  } else if (wide) {
+    if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, true, false>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+    else hipLaunchKernelGGL((triattn_core_bf16_pipe<TA_DMA_WAVES, false, false>), grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
+    hipLaunchKernelGGL((triattn_core_bf16_redo<TA_DMA_WAVES, false>), redo_grid, dim3(64 * TA_DMA_WAVES), 0, st, p);
   } else {
-    if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<4, true>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((triattn_core_bf16_pipe<4, false>), grid, dim3(256), 0, st, p);
-    hipLaunchKernelGGL(triattn_core_bf16_redo<4>, redo_grid, dim3(256), 0, st, p);
+    if (p.keep) hipLaunchKernelGGL((triattn_core_bf16_pipe<4, true, false>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((triattn_core_bf16_pipe<4, false, false>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((triattn_core_bf16_redo<4, false>), redo_grid, dim3(256), 0, st, p);
   }
   return launched(err, errlen, "triattn_core_bf16_pipe");
 }
@@ -948,7 +984,7 @@ int op_stage_launch(const StageParams& p, hipStream_t st, char* err, size_t errl
   const int64_t u1 = p.B * p.N * p.H * (p.Sp / 64), u2 = p.B * p.H * (p.Sp / 32) * (p.Sp / 32);
   if (cdiv(u1, 4) > 0x7fffffffLL || cdiv(u2, 4) > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "staging: grid too large");
   if (dry) return FPF_OK;
-  hipLaunchKernelGGL(triattn_stage_v, dim3((unsigned)cdiv(u1, 4)), dim3(256), 0, st, p);
+  if (p.v2) hipLaunchKernelGGL(triattn_stage_v, dim3((unsigned)cdiv(u1, 4)), dim3(256), 0, st, p);
   hipLaunchKernelGGL(triattn_stage_bias, dim3((unsigned)cdiv(u2, 4)), dim3(256), 0, st, p);
   return launched(err, errlen, "triattn_stage_v / triattn_stage_bias");
 }

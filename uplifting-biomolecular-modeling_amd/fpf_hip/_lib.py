@@ -11,7 +11,7 @@ import torch  # noqa: F401  (must precede the dlopen below: see the module docst
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfpf_hip.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 DT_BF16, DT_F32, DT_U8, DT_F32Z_BF16 = 1, 2, 3, 4
 TRIMUL_NOALLOC_SCRATCH_BYTES = 50331648          # include/fpf_hip.h FPF_TRIMUL_NOALLOC_SCRATCH_BYTES
 ERRORS = {1: "version", 2: "args", 3: "shape", 4: "dtype", 5: "align", 6: "workspace", 7: "launch"}
