@@ -849,8 +849,7 @@ __global__ void __launch_bounds__(256) triattn_epilogue_f32(const float* __restr
 }
 
 // dry = true: every check, nothing launched
-// Sv: the real keys / queries of a v_layout 2 call whose key axis is padded (S = Sv rounded up to 64); -1 = S.
-// Sv: the real keys / queries of a padded block-layout call (-1: S).  qmul > 0: a block-layout call whose q and k hold only the
+// Sv: the real keys / queries of a block-layout call whose key axis is padded (S = Sv rounded up to 64); -1: S.  qmul > 0: a block-layout call whose q and k hold only the
 // Sv real rows, q not yet multiplied by the scale -- the core multiplies q by qmul in registers and re-reads the last real key
 // row for the padding keys (the op face's in-place route); 0: q and k hold S rows, q already multiplied.
 static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_t errlen, bool dry = false, int64_t Sv = -1,
@@ -898,19 +897,19 @@ static int core_launch(const FpfTriattnArgs* a, hipStream_t st, char* err, size_
     if (p.v_t >= 2) {                  // the block layout (q times the scale; V^T keys permuted in 16-blocks, or V as key rows):
                                        // the DMA-staged core
       if (!p.bias_vec || p.S % TA_KT != 0 || p.S > 64 * TA_MAXW || p.vs[3] % 8 != 0)
-        return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
+        return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 / 3 needs an fp32 16-byte-aligned bias and S a multiple of 64 up to %d", 64 * TA_MAXW);
       if (p.bs[2] != p.S || p.bs[3] != 1)
-        return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 reads contiguous S x S bias planes in 32 x 32 register-order blocks (bias_stride[2] = S, [3] = 1)");
-      if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 takes q already multiplied by the scale (scale must be 1)");
+        return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 / 3 reads contiguous S x S bias planes in 32 x 32 register-order blocks (bias_stride[2] = S, [3] = 1)");
+      if (p.scale != 1.0f) return fail(err, errlen, FPF_E_ARGS, "v_layout 2 / 3 takes q already multiplied by the scale (scale must be 1)");
       if (!(p.qmul > 0.f) || !std::isfinite(p.qmul) || p.Sqk <= p.S - TA_KT || p.Sqk > p.S)
-        return fail(err, errlen, FPF_E_ARGS, "v_layout 2: q / k rows %lld of %lld, q factor %g", (long long)p.Sqk, (long long)p.S, (double)p.qmul);
+        return fail(err, errlen, FPF_E_ARGS, "v_layout 2 / 3: q / k rows %lld of %lld, q factor %g", (long long)p.Sqk, (long long)p.S, (double)p.qmul);
       if (p.mask && !a->keep)
-        return fail(err, errlen, FPF_E_ARGS, "v_layout 2 reads the mask as a keep-bit table (keep); the fused block builds it");
+        return fail(err, errlen, FPF_E_ARGS, "v_layout 2 / 3 reads the mask as a keep-bit table (keep); the fused block builds it");
       if (p.os[3] != TA_D || ((p.os[0] | p.os[1] | p.os[2]) & 7) || !aligned16(a->out))
-        return fail(err, errlen, FPF_E_ALIGN, "v_layout 2 writes out rows of %d contiguous bf16, 16-byte aligned", TA_D);
+        return fail(err, errlen, FPF_E_ALIGN, "v_layout 2 / 3 writes out rows of %d contiguous bf16, 16-byte aligned", TA_D);
       const size_t need = (size_t)redo_words(a->B, a->N, a->H, a->S) * 4;
       if (!a->workspace || a->workspace_bytes < need)
-        return fail(err, errlen, FPF_E_WORKSPACE, "v_layout 2: workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
+        return fail(err, errlen, FPF_E_WORKSPACE, "v_layout 2 / 3: workspace %zu < %zu bytes", (size_t)a->workspace_bytes, need);
       p.keep = a->keep;
       p.redo = static_cast<uint32_t*>(a->workspace);
       return pipe_core_launch(p, st, err, errlen, dry);
@@ -983,7 +982,8 @@ static bool rows32_ok(const void* p, const int64_t* st4) {     // rows of 32 con
   return aligned16(p) && ((st4[0] | st4[1] | st4[2] | st4[3]) & 7) == 0;
 }
 
-// the caller's q and k strides (and the staged V^T's) within the block-layout core's 32-bit in-item offsets
+// the caller's q, k and v strides (or, for V^T given transposed, the staged copy's) within the block-layout core's 32-bit
+// in-item offsets
 static bool op_in_place_fits(const FpfTriattnArgs* a) {
   const int64_t Sp = block_np(FPF_DT_BF16, a->S);
   if (a->v_layout == 0) return pipe_offsets_fit(Sp, a->q_stride, a->k_stride, a->v_stride, true);

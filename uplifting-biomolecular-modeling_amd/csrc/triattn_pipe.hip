@@ -1,4 +1,5 @@
-// Triangle attention: the fused block's core on the block's own operand layout (v_layout 2), and the keep-bit table it reads.
+// Triangle attention: the fused block's core on the block's own operand layout (v_layout 2; V as key rows: v_layout 3), and the
+// keep-bit table it reads.
 // Replaces the core stage of common/opt_core/opt_core/attn/pair_fused.py:1391 (core_attention) inside tri_attn_block (:1500):
 // o = softmax_j(q.k + bias, -inf at masked keys) v per (b, attention row i, head h), kernels/triattn/__init__.py:3-8; a row with
 // no kept key is the uniform mean of v.
@@ -948,9 +949,9 @@ int pipe_core_launch(const CoreParams& p, hipStream_t st, char* err, size_t errl
   const int64_t total = wide ? rows_heads * q8 : rows_heads * q4;
   if (cdiv(total, 8) * 8 > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
   if (p.bs[2] < 0 || !pipe_offsets_fit(p.S, p.qs, p.ks, p.vs, p.v_rows != 0) || p.B * p.N > 0x7fffffffLL)
-    return fail(err, errlen, FPF_E_SHAPE, "v_layout 2: q / bias / k / v in-item offsets must fit 31 bits");
+    return fail(err, errlen, FPF_E_SHAPE, "v_layout 2 / 3: q / bias / k / v in-item offsets must fit 31 bits");
   if (p.Sv <= 0 || p.Sv > p.S || (p.Sv < p.S && !p.keep))
-    return fail(err, errlen, FPF_E_ARGS, "v_layout 2: %lld real keys of %lld need a keep table masking the padding", (long long)p.Sv, (long long)p.S);
+    return fail(err, errlen, FPF_E_ARGS, "v_layout 2 / 3: %lld real keys of %lld need a keep table masking the padding", (long long)p.Sv, (long long)p.S);
   if (dry) return FPF_OK;
   // persistent grids: one fast workgroup per CU walking every nwg-th item of its XCD's range (two per CU for the 4-wave
   // split, whose LDS and registers fit twice), and at least 8 workgroups, so that every XCD's range has one (with fewer
