@@ -444,9 +444,11 @@ def test_block_layout_core_fallback_extreme_logits(N, masked, vrows):
     assert_bf16_close(got, ref, "block-layout core N=%d masked=%s vrows=%s, extreme query tiles" % (N, masked, vrows))
 
 
-@pytest.mark.parametrize("S_,layout,N,B", [(456, "contig", 7, 1), (800, "contig", 7, 1), (768, "endstrided", 7, 1),
-                                           (130, "endstrided", 7, 1), (720, "contig", 512, 1), (300, "endstrided", 5, 2)])
-def test_op_face_in_place_route_equals_the_block_core_on_restaged_operands(S_, layout, N, B):
+@pytest.mark.parametrize("S_,layout,N,B,bias_bf16", [(456, "contig", 7, 1, False), (800, "contig", 7, 1, False),
+                                                     (768, "endstrided", 7, 1, False), (130, "endstrided", 7, 1, False),
+                                                     (720, "contig", 512, 1, False), (300, "endstrided", 5, 2, False),
+                                                     (200, "contig", 6, 1, True)])
+def test_op_face_in_place_route_equals_the_block_core_on_restaged_operands(S_, layout, N, B, bias_bf16):
     """The op face's route onto the block-layout core reads q, k and v in place -- q times scale * log2(e) in registers, V's
     key rows through LDS transpose reads, the padding keys of the last tile re-reading the last real key row under the keep
     table's mask -- and restages only the bias.  Its output equals, bit for bit, the block-layout core with V^T in its key
@@ -454,13 +456,16 @@ def test_op_face_in_place_route_equals_the_block_core_on_restaged_operands(S_, l
     q2 = bf16(q * fp32(scale * log2(e))), k and V^T padded with zeros to Sp = S rounded up to 64 (V^T in the 16-block key
     order), the bias times log2(e) in register-order blocks, the keep table with the padding keys masked.  A random mask with a
     dead row; `endstrided`: q, k and v as transposed views of [B, S, H, N, D] storage (the ending node's layout).  N = 7 runs the
-    4-wave split, N = 512 at S = 720 (padded to 768) the 8-wave one; B = 2 runs two batch entries."""
+    4-wave split, N = 512 at S = 720 (padded to 768) the 8-wave one; B = 2 runs two batch entries; `bias_bf16` hands the
+    bias as bf16 (restaged as its fp32 value times log2(e))."""
     import ctypes
     from fpf_hip import _lib as L
     from fpf_hip.kernels import triattn as TA
     H, D = 4, 32
     Sp = -(-S_ // 64) * 64
     q, k, v, bias = _rand_op(B, N, H, S_, D, 31 + S_, torch.bfloat16)
+    if bias_bf16:
+        bias = bias.to(torch.bfloat16)
     g = torch.Generator().manual_seed(32 + S_)
     mask = torch.rand(B, N, 1, 1, S_, generator=g) > 0.2
     mask[0, 3] = False
