@@ -93,24 +93,46 @@ __global__ void __launch_bounds__(64 * AP_W) apb_fwd_kernel(const ApbParams p) {
   const int64_t ntile = cdiv(p.NK, AP_KT), per = cdiv(ntile, AP_W);
   const int64_t t0 = wave * per, t1 = std::min<int64_t>(ntile, t0 + per);
   const int64_t bplane = s * p.bs[0] + h * p.bs[1];       // bs[0] = 0: one plane shared by the samples
+  // a tile's K / V values (NKV per lane each), then its bias values (NB per lane): each group's loads are all issued before
+  // its first LDS store, so the tile waits for two memory latencies rather than one per element
+  constexpr int NKV = AP_KT * D / 64, NB = AP_Q * AP_KT / 64;
+  static_assert(AP_KT * D % 64 == 0 && AP_Q * AP_KT % 64 == 0, "whole rounds of 64 lanes");
   for (int64_t t = t0; t < t1; ++t) {
     const int64_t k0 = t * AP_KT;
-    for (int e = l; e < AP_KT * D; e += 64) {
-      const int kk = e / D, d = e - kk * D;
-      const int64_t j = k0 + kk;
-      const bool ok = j < p.NK;
-      sK[kk * D + d] = ok ? ldv(kp, s * p.ks[0] + j * p.ks[1] + h * p.ks[2] + d) : 0.f;
-      sV[kk * D + d] = ok ? ldv(vp, s * p.vs[0] + j * p.vs[1] + h * p.vs[2] + d) : 0.f;
-    }
-    for (int e = l; e < AP_Q * AP_KT; e += 64) {
-      const int qq = e / AP_KT, kk = e - qq * AP_KT;
-      const int64_t ii = qt * AP_Q + qq, j = k0 + kk;
-      float bv = 0.f;
-      if (ii < p.N && j < p.NK) {
-        const int64_t o = bplane + ii * p.bs[2] + j;
-        bv = p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[o]) : static_cast<const float*>(p.bias)[o];
+    {
+      float rk[NKV], rv[NKV];
+#pragma unroll
+      for (int r = 0; r < NKV; ++r) {
+        const int e = l + 64 * r, kk = e / D, d = e - kk * D;
+        const int64_t j = k0 + kk;
+        const bool ok = j < p.NK;
+        rk[r] = ok ? ldv(kp, s * p.ks[0] + j * p.ks[1] + h * p.ks[2] + d) : 0.f;
+        rv[r] = ok ? ldv(vp, s * p.vs[0] + j * p.vs[1] + h * p.vs[2] + d) : 0.f;
       }
-      sB[qq * (AP_KT + 1) + kk] = bv * AP_LOG2E;
+#pragma unroll
+      for (int r = 0; r < NKV; ++r) {
+        sK[l + 64 * r] = rk[r];
+        sV[l + 64 * r] = rv[r];
+      }
+    }
+    {
+      float rb[NB];
+#pragma unroll
+      for (int r = 0; r < NB; ++r) {
+        const int e = l + 64 * r, qq = e / AP_KT, kk = e - qq * AP_KT;
+        const int64_t ii = qt * AP_Q + qq, j = k0 + kk;
+        float bv = 0.f;
+        if (ii < p.N && j < p.NK) {
+          const int64_t o = bplane + ii * p.bs[2] + j;
+          bv = p.bias_bf16 ? bf2f(static_cast<const uint16_t*>(p.bias)[o]) : static_cast<const float*>(p.bias)[o];
+        }
+        rb[r] = bv;
+      }
+#pragma unroll
+      for (int r = 0; r < NB; ++r) {
+        const int e = l + 64 * r, qq = e / AP_KT, kk = e - qq * AP_KT;
+        sB[qq * (AP_KT + 1) + kk] = rb[r] * AP_LOG2E;
+      }
     }
     if (l < AP_KT) sKeep[l] = (k0 + l < p.NK && (dead || apb_keep(p, s, k0 + l))) ? 1.f : 0.f;
     apb_wave_sync();
