@@ -23,13 +23,16 @@ def _apb_inputs(seed, S_, N, NK, H, D, per_sample, dtype):
 
 @pytest.mark.parametrize("D", [16, 24, 32, 48, 64])
 @pytest.mark.parametrize("layout", ["rows", "shnd"])
-def test_apb_core_fp32(D, layout):
+@pytest.mark.parametrize("NK", [130, 128])
+def test_apb_core_fp32(D, layout, NK):
+    """fp32 against the fp64 statement; NK = 128 (16-byte aligned rows, a multiple of 4 keys) takes the kernel's 16-byte tile
+    loads, NK = 130 the 4-byte ones."""
     from fpf_hip.attn import apb_core as APB
-    S_, N, NK, H = 2, 77, 130, 3
+    S_, N, H = 2, 77, 3
     q, k, v, bias, gate = _apb_inputs(D, S_, N, NK, H, D, False, torch.float32)
     mask = (torch.arange(NK) % 5 != 3).to(torch.uint8).reshape(1, NK)
     ref = S.pair_bias_attention_op(q, k, v, bias, mask, gate, dtype=torch.float64).float()
-    print("[apb] fp32 D=%d layout=%s" % (D, layout), flush=True)
+    print("[apb] fp32 D=%d layout=%s NK=%d" % (D, layout, NK), flush=True)
     if layout == "rows":
         qd, kd, vd, gd = (t.reshape(-1, H * D).to(DEV) for t in (q, k, v, gate))
         out = APB.pair_bias_attention(qd, kd, vd, bias.to(DEV), mask.to(DEV), gate=gd, num_samples=S_, num_heads=H, layout="rows")
@@ -38,7 +41,7 @@ def test_apb_core_fp32(D, layout):
         qd, kd, vd = (t.permute(0, 2, 1, 3).to(DEV) for t in (q, k, v))          # [S, H, N, D] views of [S, N, H, D] storage
         out = APB.pair_bias_attention(qd, kd, vd, bias.to(DEV), mask.to(DEV), gate=gate.to(DEV), layout="shnd").reshape(S_, N, H, D)
     torch.cuda.synchronize()
-    assert_f32_close(out, ref, "apb fp32 D%d %s" % (D, layout))
+    assert_f32_close(out, ref, "apb fp32 D%d %s NK%d" % (D, layout, NK))
 
 
 def test_apb_core_bf16_per_sample_bias_and_dead_sample():

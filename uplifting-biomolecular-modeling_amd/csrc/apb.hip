@@ -12,6 +12,7 @@
 // W partial states are combined through LDS and the sigmoid gate applied on the way out.  A sample whose keys are all masked
 // attends uniformly to every key (logits 0), the convention of the reference faces.
 #include <algorithm>
+#include <type_traits>
 
 #include "fpf_common.h"
 
@@ -35,6 +36,7 @@ struct ApbParams {
   int64_t S, N, NK, H;
   float scale;
   int bias_bf16, mask_f32;
+  int vec;                       // fp32 K / V / bias in 16-byte aligned rows (NK a multiple of 4): the tiles load 16 bytes a lane
 };
 
 __device__ __forceinline__ float ldv(const float* p, int64_t o) { return p[o]; }
@@ -55,7 +57,7 @@ __device__ __forceinline__ void apb_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <typename T, int D, int AP_W>
+template <typename T, int D, int AP_W, bool VEC>
 __global__ void __launch_bounds__(64 * AP_W) apb_fwd_kernel(const ApbParams p) {
   // per-wave slots: K and V [AP_KT][D] (16-byte rows, read as broadcasts), bias [AP_Q][AP_KT + 1], keep [AP_KT]; reused
   // after the key loop for the partial states [AP_W][AP_Q][D + 2] (o, m, l) of the combine
@@ -99,6 +101,40 @@ __global__ void __launch_bounds__(64 * AP_W) apb_fwd_kernel(const ApbParams p) {
   static_assert(AP_KT * D % 64 == 0 && AP_Q * AP_KT % 64 == 0, "whole rounds of 64 lanes");
   for (int64_t t = t0; t < t1; ++t) {
     const int64_t k0 = t * AP_KT;
+    if constexpr (VEC) {
+      // K / V: key row kk as D / 4 16-byte pieces, D / 8 per lane; bias: 64 query rows x 8 pieces, 8 per lane
+      constexpr int NV4 = AP_KT * D / 4 / 64, NB4 = AP_Q * AP_KT / 4 / 64;
+      static_assert(AP_KT * D / 4 % 64 == 0, "whole rounds of 64 lanes");
+      const float* kf = reinterpret_cast<const float*>(kp);
+      const float* vf = reinterpret_cast<const float*>(vp);
+      const float* bf = static_cast<const float*>(p.bias);
+      f32x4 rk[NV4], rv[NV4], rb[NB4];
+#pragma unroll
+      for (int r = 0; r < NV4; ++r) {
+        const int e = l + 64 * r, kk = e / (D / 4), c4 = e - kk * (D / 4);
+        const int64_t j = k0 + kk;
+        const bool ok = j < p.NK;
+        rk[r] = ok ? *reinterpret_cast<const f32x4*>(kf + s * p.ks[0] + j * p.ks[1] + h * p.ks[2] + 4 * c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        rv[r] = ok ? *reinterpret_cast<const f32x4*>(vf + s * p.vs[0] + j * p.vs[1] + h * p.vs[2] + 4 * c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int r = 0; r < NB4; ++r) {
+        const int e = l + 64 * r, qq = e / (AP_KT / 4), c = e - qq * (AP_KT / 4);
+        const int64_t ii = qt * AP_Q + qq, j = k0 + 4 * c;
+        rb[r] = ii < p.N && j < p.NK ? *reinterpret_cast<const f32x4*>(bf + bplane + ii * p.bs[2] + j) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int r = 0; r < NV4; ++r) {
+        *reinterpret_cast<f32x4*>(sK + 4 * (l + 64 * r)) = rk[r];
+        *reinterpret_cast<f32x4*>(sV + 4 * (l + 64 * r)) = rv[r];
+      }
+#pragma unroll
+      for (int r = 0; r < NB4; ++r) {
+        const int e = l + 64 * r, qq = e / (AP_KT / 4), c = e - qq * (AP_KT / 4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sB[qq * (AP_KT + 1) + 4 * c + u] = rb[r][u] * AP_LOG2E;
+      }
+    } else {
     {
       float rk[NKV], rv[NKV];
 #pragma unroll
@@ -133,6 +169,7 @@ __global__ void __launch_bounds__(64 * AP_W) apb_fwd_kernel(const ApbParams p) {
         const int e = l + 64 * r, qq = e / AP_KT, kk = e - qq * AP_KT;
         sB[qq * (AP_KT + 1) + kk] = rb[r] * AP_LOG2E;
       }
+    }
     }
     if (l < AP_KT) sKeep[l] = (k0 + l < p.NK && (dead || apb_keep(p, s, k0 + l))) ? 1.f : 0.f;
     apb_wave_sync();
@@ -215,13 +252,24 @@ __global__ void __launch_bounds__(64 * AP_W) apb_fwd_kernel(const ApbParams p) {
   }
 }
 
+template <typename T, int DD>
+static void apb_launch_dd(const ApbParams& p, int64_t blocks, hipStream_t st) {
+  if constexpr (std::is_same<T, float>::value) {
+    if (p.vec) {
+      hipLaunchKernelGGL((apb_fwd_kernel<T, DD, ap_waves<DD>(), true>), dim3((unsigned)blocks), dim3(64 * ap_waves<DD>()), 0, st, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((apb_fwd_kernel<T, DD, ap_waves<DD>(), false>), dim3((unsigned)blocks), dim3(64 * ap_waves<DD>()), 0, st, p);
+}
+
 template <typename T>
 static int apb_launch_d(const ApbParams& p, int64_t D, hipStream_t st, char* err, size_t errlen) {
   const int64_t blocks = p.S * p.H * cdiv(p.N, AP_Q);
   if (blocks > 0x7fffffffLL) return fail(err, errlen, FPF_E_SHAPE, "grid too large");
 #define FPF_APB(DD)                                                                                   \
   if (D == DD) {                                                                                      \
-    hipLaunchKernelGGL((apb_fwd_kernel<T, DD, ap_waves<DD>()>), dim3((unsigned)blocks), dim3(64 * ap_waves<DD>()), 0, st, p); \
+    apb_launch_dd<T, DD>(p, blocks, st);                                                              \
     return launched(err, errlen, "apb_fwd_kernel");                                                   \
   }
   FPF_APB(16) FPF_APB(24) FPF_APB(32) FPF_APB(48) FPF_APB(64)
@@ -270,6 +318,9 @@ extern "C" int fpf_apb_fwd(const FpfApbArgs* a, void* stream, char* err, size_t 
   p.scale = a->scale;
   p.bias_bf16 = a->bias_dtype == FPF_DT_BF16;
   p.mask_f32 = a->mask_dtype == FPF_DT_F32;
+  const auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  p.vec = a->dtype == FPF_DT_F32 && !p.bias_bf16 && a->NK % 4 == 0 && a16(a->k) && a16(a->v) && a16(a->bias) &&
+          ((p.ks[0] | p.ks[1] | p.ks[2] | p.vs[0] | p.vs[1] | p.vs[2] | p.bs[0] | p.bs[1] | p.bs[2]) & 3) == 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   return a->dtype == FPF_DT_F32 ? apb_launch_d<float>(p, a->D, st, err, errlen) : apb_launch_d<uint16_t>(p, a->D, st, err, errlen);
 }
