@@ -349,3 +349,49 @@ def test_layer_no_host_sync_after_first_call():
             finally:
                 torch.cuda.set_sync_debug_mode("default")
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("N,masked", [(200, True), (768, False)])
+def test_pair_block_graph_replays_equal_eager(N, masked):
+    """The pair block captured into a HIP graph (torch.cuda.graph on a side stream, after one eager call there sized that
+    stream's shared scratch) replays the eager block's bits: three replays from the same z, with eager work and a
+    synchronisation between them, each bitwise equal to the eager block on the same input and finite -- the library records
+    no memset nodes and keeps no host-side state that a replay would skip.  N = 200 with a random mask, dead rows and masked
+    trailing keys runs the keep table, the masked core and its fallback check; N = 768 without a mask the metric's path."""
+    from fpf_hip import pairformer as PFM
+    g = torch.Generator().manual_seed(N + 17)
+    blk = PFM.PairBlock(PFM.random_params(seed=7), DEV, torch.bfloat16)
+    z0 = torch.randn(1, N, N, 128, generator=g).to(torch.bfloat16).to(DEV)
+    m = torch.ones(1, N, N)
+    if masked:
+        m = (torch.rand(1, N, N, generator=g) > 0.2).float()
+        m[:, 3:7, :] = 0                                  # dead rows
+        m[:, :, N - 9:] = 0                               # trailing keys masked in every row
+    mask = m.to(DEV)
+    print("[case] graph replay N=%d masked=%s" % (N, masked), flush=True)
+    eager, ze = [], z0.clone()
+    for _ in range(3):
+        PFM.pair_block(ze, mask, blk)
+        eager.append(ze.clone())
+    torch.cuda.synchronize()
+    zg = z0.clone()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        PFM.pair_block(zg, mask, blk)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        PFM.pair_block(zg, mask, blk)
+    torch.cuda.synchronize()
+    zg.copy_(z0)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(zg.float()).all(), "replay %d: non-finite" % i
+        assert torch.equal(zg, eager[i]), "replay %d differs from the eager block" % i
+        PFM.pair_block(z0.clone(), mask, blk)             # eager work between replays
+        torch.cuda.synchronize()
+    del graph
+    torch.cuda.synchronize()
