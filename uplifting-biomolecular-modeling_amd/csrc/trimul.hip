@@ -39,9 +39,12 @@ __device__ __forceinline__ int64_t tl_off(int64_t b, int64_t c, int64_t P, int64
 // ---------------------------------------------------------------------------------------------------------------- K1 (bf16)
 // Persistent: the four [128 x 128] projection weights live in LDS (139 KB) for the workgroup's lifetime; each wave walks
 // 32-column plane tiles (plane row P, columns Q0 .. Q0+31), prefetching the next tile's 32 z rows while it computes.
+// NT: planes larger than the 256 MiB last-level cache (2 x 151 MB at N = 768) are written with non-temporal stores, so they
+// do not displace z, which K3 reads again (trimul 10-20 us faster per direction at N = 768, the same bits); smaller planes
+// stay cacheable for the contraction (non-temporal at N = 512 made it 10-15 us slower).
 // ZF32: z is fp32 (the fp32-resident form); each tile's rows are read and rounded to bf16 at the start of its iteration.
 // NCB: the 32-channel blocks computed (4: the whole op; fewer: one block of the channels mode, from channel 32 cb0).
-template <bool ZF32, int NCB>
+template <bool ZF32, int NCB, bool NT>
 __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z, const float* __restrict__ mask,
                                                       const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
                                                       const uint16_t* __restrict__ w_ap, const uint16_t* __restrict__ w_ag,
@@ -62,6 +65,15 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z
   const uint32_t stride = gridDim.x * RT_WAVES;
   uint32_t t = blockIdx.x * RT_WAVES + wave;
   u32x4 raw[8];
+  auto put = [&](uint16_t* dst, const u32x4& lo, const u32x4& hi) {   // 16 + 16 channel values of one plane row block
+    if constexpr (NT) {
+      __builtin_nontemporal_store(lo, reinterpret_cast<u32x4*>(dst));
+      __builtin_nontemporal_store(hi, reinterpret_cast<u32x4*>(dst + 16));
+    } else {
+      *reinterpret_cast<u32x4*>(dst) = lo;
+      *reinterpret_cast<u32x4*>(dst + 16) = hi;
+    }
+  };
   auto fetch = [&](uint32_t tt) {
     const RtTile tl = rt_tile(tt, per_b, tpr);
     const int64_t b = tl.b, P = tl.r, Q = tl.c * 32 + n;
@@ -86,10 +98,8 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z
       for (int cb = 0; cb < NCB; ++cb) {
         const int64_t c = cb * 32 + n;
         const u32x4 zero = {0, 0, 0, 0};
-        *reinterpret_cast<u32x4*>(oa + c * 32) = zero;
-        *reinterpret_cast<u32x4*>(oa + c * 32 + 16) = zero;
-        *reinterpret_cast<u32x4*>(ob + c * 32) = zero;
-        *reinterpret_cast<u32x4*>(ob + c * 32 + 16) = zero;
+        put(oa + c * 32, zero, zero);
+        put(ob + c * 32, zero, zero);
       }
       continue;
     }
@@ -134,11 +144,9 @@ __global__ void __launch_bounds__(512) trimul_k1_bf16(const void* __restrict__ z
       const int64_t c = cb * 32 + n;
       u32x4 lo, hi;
       rt_pack16(va, lo, hi);
-      *reinterpret_cast<u32x4*>(oa + c * 32) = lo;
-      *reinterpret_cast<u32x4*>(oa + c * 32 + 16) = hi;
+      put(oa + c * 32, lo, hi);
       rt_pack16(vb, lo, hi);
-      *reinterpret_cast<u32x4*>(ob + c * 32) = lo;
-      *reinterpret_cast<u32x4*>(ob + c * 32 + 16) = hi;
+      put(ob + c * 32, lo, hi);
     }
   }
 }
@@ -899,8 +907,12 @@ static int bf16_planes(const FpfTrimulArgs* a, hipStream_t st, uint16_t* pa, uin
   if (ncb != 1 && ncb != 2 && ncb != 4) return fail(err, errlen, FPF_E_ARGS, "K1 writes 1, 2 or 4 channel blocks (got %d)", ncb);
   const unsigned k1_grid = (unsigned)std::min<int64_t>(num_cus(), cdiv(k1_tiles, RT_WAVES));
   const bool f = a->dtype == FPF_DT_F32Z_BF16;
-  auto kern = ncb == 4 ? (f ? trimul_k1_bf16<true, 4> : trimul_k1_bf16<false, 4>)
-                       : ncb == 2 ? (f ? trimul_k1_bf16<true, 2> : trimul_k1_bf16<false, 2>) : (f ? trimul_k1_bf16<true, 1> : trimul_k1_bf16<false, 1>);
+  const double plane_bytes = 2.0 * (double)B * (32 * ncb) * (double)Np * (double)Np * 2;      // A and B planes, bf16
+  const bool nt = plane_bytes > 256.0 * 1024 * 1024;                                           // above the last-level cache
+#define FPF_K1(Z, C) (nt ? trimul_k1_bf16<Z, C, true> : trimul_k1_bf16<Z, C, false>)
+  auto kern = ncb == 4 ? (f ? FPF_K1(true, 4) : FPF_K1(false, 4))
+                       : ncb == 2 ? (f ? FPF_K1(true, 2) : FPF_K1(false, 2)) : (f ? FPF_K1(true, 1) : FPF_K1(false, 1));
+#undef FPF_K1
   hipLaunchKernelGGL(kern, dim3(k1_grid), dim3(512), 0, st, a->z, a->mask, a->ln_in_w, a->ln_in_b, a->eps, (const uint16_t*)a->w_ap,
                      (const uint16_t*)a->w_ag, (const uint16_t*)a->w_bp, (const uint16_t*)a->w_bg, pa, pb, N, Np, B, a->outgoing, cb0);
   return launched(err, errlen, "trimul_k1_bf16");
