@@ -193,6 +193,38 @@ def test_pair_block_same_class(N):
     assert_same_class(zd.float(), ref, S.pair_block_autocast(z, mask, params), "pair block N=%d" % N)
 
 
+@pytest.mark.parametrize("N", [96, 160])
+def test_pair_block_batch2_same_class_and_entries_independent(N):
+    """Two batch entries with different masks (entry 0 padded by 6 residues on both axes, entry 1 a random pair mask with two
+    dead rows): the B = 2 pair block against the fp32 statements at SAME_CLASS, and each entry bitwise equal to a B = 1 block
+    on that entry alone (no kernel mixes entries, whatever the grid).  N = 96 runs the generic tri-att core, N = 160 the
+    block-layout core with its key axis padded to 192."""
+    from fpf_hip import pairformer as PFM
+    params = _bf16_weights(PFM.random_params(seed=N + 3))
+    g = torch.Generator().manual_seed(N + 5)
+    z = torch.randn(2, N, N, 128, generator=g).to(torch.bfloat16)
+    mask = torch.ones(2, N, N)
+    mask[0, N - 6:, :] = 0
+    mask[0, :, N - 6:] = 0
+    mask[1] = (torch.rand(N, N, generator=g) > 0.15).float()
+    mask[1, 7:9, :] = 0
+    blk = PFM.PairBlock(params, DEV, torch.bfloat16)
+    print("[case] pair block B=2 N=%d" % N, flush=True)
+    zd, md = z.to(DEV), mask.to(DEV)
+    PFM.pair_block(zd, md, blk)
+    singles = []
+    for e in range(2):
+        ze = z[e:e + 1].to(DEV)
+        PFM.pair_block(ze, md[e:e + 1].contiguous(), blk)
+        singles.append(ze)
+    torch.cuda.synchronize()
+    assert torch.isfinite(zd.float()).all()
+    for e in range(2):
+        assert torch.equal(zd[e:e + 1], singles[e]), "entry %d of the batch differs from the block on it alone" % e
+    ref = S.pair_block(z.float(), mask, params, dtype=torch.float32)
+    assert_same_class(zd.float(), ref, S.pair_block_autocast(z, mask, params), "pair block B=2 N=%d" % N)
+
+
 def test_pair_block_per_site_budget():
     """Where the block's error comes from, on the smoke's inputs (N = 48, 4 padded residues, seed-1 weights): each site alone,
     fed the same bf16 input (the fp32 chain's state rounded to bf16), its update against the fp32 statement of that site, next
