@@ -215,10 +215,11 @@ def test_trimul_chunked_bitwise_equals_whole(direction, B, N, chunk):
 
 
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
-@pytest.mark.parametrize("B,N,chunk", [(1, 403, 32), (1, 300, 96), (2, 130, 64), (1, 200, 20), (1, 256, 128)])
+@pytest.mark.parametrize("B,N,chunk", [(1, 403, 32), (1, 300, 96), (2, 130, 64), (1, 200, 20), (1, 256, 128), (1, 768, 32)])
 def test_trimul_channels_bitwise_equals_whole(direction, B, N, chunk):
     """Channels mode (chunk.py:542-552): the operand planes per block of chunk hidden channels (96: blocks of 64; 20: of 32), each block's products into the one full product plane, then the output stage over all rows.  Out of place,
-    in place and the bare update, each equal to the whole op bitwise."""
+    in place and the bare update, each equal to the whole op bitwise.  At N = 768 the whole op's K1 writes its planes (302 MB,
+    above the last-level cache) with non-temporal stores and the channels mode's 75 MB planes with ordinary ones."""
     from fpf_hip import pairformer as PFM
     from fpf_hip.kernels import trimul as TM
     blk = PFM.PairBlock(PFM.random_params(seed=4), DEV, torch.bfloat16)
